@@ -1,0 +1,131 @@
+"""ctypes binding of libcresso_hip.so (the C ABI declared in include/cresso_hip.h).
+
+The library is the only compute path of this package: there is no PyTorch or
+CPU fallback.  :func:`load` raises ``RuntimeError`` when the library is
+missing or was built for another ABI.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_NAME = "libcresso_hip.so"
+ABI_VERSION = 1
+
+F32, F64, F16, BF16 = 0, 1, 2, 3
+DTYPE_CODE = {torch.float32: F32, torch.float64: F64, torch.float16: F16, torch.bfloat16: BF16}
+
+# Order of the double fields of cresso_hyper (include/cresso_hip.h).
+HYPER_DOUBLES = (
+    "lr", "weight_decay", "energy_power", "dt", "impulse_friction", "contact_gain",
+    "restoring", "cubic", "metric_dt", "metric_friction", "metric_coupling",
+    "local_sharpness", "instant_metric_coupling", "instant_metric_power",
+    "root_channel_mix", "echo_mix", "transport_mix", "hash_decay",
+    "hash_impulse_decay", "hash_metric_coupling", "hash_drive_mix",
+    "direct_force_mix", "residual_feedback_mix", "reservoir_decay",
+    "refractory_decay", "refractory_gain", "confidence_decay", "confidence_gain",
+    "surprise_gain", "surprise_decay", "prediction_mix", "novelty_mix",
+    "surprise_brake", "target_update_rms", "min_gain", "max_gain", "drive_clip",
+    "spike_mix", "eps",
+)
+
+
+class Hyper(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in HYPER_DOUBLES] + [
+        ("warmup_steps", ctypes.c_int32),
+        ("maximize", ctypes.c_int32),
+    ]
+
+
+class ScalarDesc(ctypes.Structure):
+    _fields_ = [
+        ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p),
+        ("state", ctypes.c_void_p * 8),
+        ("shape", ctypes.c_int64 * 8),
+        ("numel", ctypes.c_int64),
+        ("ndim", ctypes.c_int32),
+        ("param_dtype", ctypes.c_int32),
+        ("grad_dtype", ctypes.c_int32),
+        ("step", ctypes.c_int32),
+    ]
+
+
+def hyper_from_group(group: dict) -> Hyper:
+    h = Hyper()
+    for n in HYPER_DOUBLES:
+        setattr(h, n, float(group[n]))
+    h.warmup_steps = int(group["warmup_steps"])
+    h.maximize = 1 if bool(group["maximize"]) else 0
+    return h
+
+
+_LOCK = threading.Lock()
+_LIB: Optional[ctypes.CDLL] = None
+_ERR: Optional[BaseException] = None
+
+
+def library_path() -> Path:
+    env = os.environ.get("CRESSO_HIP_LIBRARY")
+    if env:
+        return Path(env)
+    return Path(__file__).resolve().with_name(LIB_NAME)
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    c = ctypes
+    lib.cresso_hip_abi_version.restype = c.c_int32
+    lib.cresso_hip_abi_version.argtypes = []
+    lib.cresso_hip_last_error.restype = c.c_char_p
+    lib.cresso_hip_last_error.argtypes = []
+    lib.cresso_scalar_plan_create.restype = c.c_void_p
+    lib.cresso_scalar_plan_create.argtypes = [c.POINTER(ScalarDesc), c.c_int32, c.POINTER(Hyper)]
+    lib.cresso_scalar_plan_destroy.restype = None
+    lib.cresso_scalar_plan_destroy.argtypes = [c.c_void_p]
+    lib.cresso_scalar_plan_bytes.restype = c.c_size_t
+    lib.cresso_scalar_plan_bytes.argtypes = [c.c_void_p]
+    lib.cresso_scalar_plan_upload.restype = c.c_int32
+    lib.cresso_scalar_plan_upload.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p]
+    lib.cresso_scalar_plan_step.restype = c.c_int32
+    lib.cresso_scalar_plan_step.argtypes = [c.c_void_p, c.c_void_p, c.POINTER(c.c_void_p), c.POINTER(Hyper),
+                                            c.c_void_p]
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once per process; raise RuntimeError if it cannot be used."""
+    global _LIB, _ERR
+    with _LOCK:
+        if _LIB is not None:
+            return _LIB
+        if _ERR is not None:
+            raise RuntimeError(f"CRESSO5 CUDA ops failed to load: {_ERR}") from _ERR
+        path = library_path()
+        try:
+            if not path.exists():
+                raise FileNotFoundError(f"{path} not found; build it with `python -m cresso_amd.build`")
+            lib = ctypes.CDLL(str(path))
+            _declare(lib)
+            ver = int(lib.cresso_hip_abi_version())
+            if ver != ABI_VERSION:
+                raise RuntimeError(f"{path} has ABI version {ver}, expected {ABI_VERSION}")
+        except Exception as exc:  # remembered: later calls fail the same way
+            _ERR = exc
+            raise RuntimeError(f"CRESSO5 CUDA ops failed to load: {exc}") from exc
+        _LIB = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = (_LIB.cresso_hip_last_error() or b"").decode(errors="replace") if _LIB is not None else ""
+        raise RuntimeError(f"CRESSO5 {what} failed ({rc}): {msg}")
+
+
+def stream_handle(device: torch.device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,167 @@
+// Shared device/host helpers of the CRESSO5 gfx950 library.
+//
+// Conventions used by every kernel in this library:
+//  * wave64 (gfx950); block sizes are multiples of 64;
+//  * reductions are deterministic: per-thread fp32 partials, wave butterflies
+//    in a fixed lane order, then a fixed-order merge over waves/blocks in fp64;
+//    histogram-style scatter uses 64-bit fixed-point integer atomics (integer
+//    addition is associative, so the result does not depend on arrival order);
+//  * per-element transcendental math uses the hardware approximations
+//    (v_exp_f32 / v_log_f32 / v_rcp_f32 / v_sqrt_f32); per-tensor scalars use
+//    the accurate libm versions in the state dtype.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/cresso_hip.h"
+
+namespace cresso {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// dtype traits
+// ---------------------------------------------------------------------------
+template <typename T> struct dt;
+template <> struct dt<float> { static constexpr int code = CRESSO_F32; };
+template <> struct dt<double> { static constexpr int code = CRESSO_F64; };
+template <> struct dt<__half> { static constexpr int code = CRESSO_F16; };
+template <> struct dt<__hip_bfloat16> { static constexpr int code = CRESSO_BF16; };
+
+__device__ __forceinline__ float to_f(float v) { return v; }
+__device__ __forceinline__ float to_f(double v) { return (float)v; }
+__device__ __forceinline__ float to_f(__half v) { return __half2float(v); }
+__device__ __forceinline__ float to_f(__hip_bfloat16 v) { return __bfloat162float(v); }
+
+template <typename W, typename T> __device__ __forceinline__ W to_w(T v) { return (W)to_f(v); }
+template <> __device__ __forceinline__ double to_w<double, double>(double v) { return v; }
+
+// Round a work-dtype value to the storage dtype (round to nearest even).
+template <typename T> __device__ __forceinline__ T from_w(float v);
+template <> __device__ __forceinline__ float from_w<float>(float v) { return v; }
+template <> __device__ __forceinline__ double from_w<double>(float v) { return (double)v; }
+template <> __device__ __forceinline__ __half from_w<__half>(float v) { return __float2half_rn(v); }
+template <> __device__ __forceinline__ __hip_bfloat16 from_w<__hip_bfloat16>(float v) { return __float2bfloat16(v); }
+template <typename T> __device__ __forceinline__ T from_wd(double v) { return from_w<T>((float)v); }
+template <> __device__ __forceinline__ double from_wd<double>(double v) { return v; }
+
+// ---------------------------------------------------------------------------
+// fast per-element math (hardware approximations, ~1 ulp on their domain)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float flog2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fsqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+__device__ __forceinline__ float fexp(float x) { return fexp2(x * 1.4426950408889634f); }
+__device__ __forceinline__ float flog(float x) { return flog2(x) * 0.6931471805599453f; }
+// x^y for x > 0
+__device__ __forceinline__ float fpow(float x, float y) { return fexp2(y * flog2(x)); }
+// log(1 + x) for x >= 0 (absolute error ~1e-7; only ever averaged)
+__device__ __forceinline__ float flog1p(float x) { return flog2(1.0f + x) * 0.6931471805599453f; }
+// tanh with absolute error ~1e-7
+__device__ __forceinline__ float ftanh(float x) {
+    float e = fexp2(-2.8853900817779268f * fabsf(x));   // exp(-2|x|)
+    float r = (1.0f - e) * frcp(1.0f + e);
+    return copysignf(r, x);
+}
+__device__ __forceinline__ float fsign(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f); }
+__device__ __forceinline__ float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
+
+// double versions for the f64 work dtype (accurate libm)
+__device__ __forceinline__ double fexp(double x) { return exp(x); }
+__device__ __forceinline__ double flog(double x) { return log(x); }
+__device__ __forceinline__ double fpow(double x, double y) { return pow(x, y); }
+__device__ __forceinline__ double flog1p(double x) { return log1p(x); }
+__device__ __forceinline__ double ftanh(double x) { return tanh(x); }
+__device__ __forceinline__ double frcp(double x) { return 1.0 / x; }
+__device__ __forceinline__ double fsqrt(double x) { return sqrt(x); }
+__device__ __forceinline__ double fsign(double x) { return x > 0.0 ? 1.0 : (x < 0.0 ? -1.0 : 0.0); }
+__device__ __forceinline__ double clampf(double x, double lo, double hi) { return fmin(fmax(x, lo), hi); }
+
+// ---------------------------------------------------------------------------
+// wave / block reductions (deterministic)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+
+// Sum V values over the block; every thread receives the totals.
+// lds must hold (blockDim.x/64) * V doubles.  Two barriers.
+template <int V>
+__device__ __forceinline__ void block_sum(double (&v)[V], double* lds) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int nw = blockDim.x / kWave;
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = wave_sum(v[i]);
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) lds[wave * V + i] = v[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        double s = 0.0;
+        for (int w = 0; w < nw; ++w) s += lds[w * V + i];
+        v[i] = s;
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Coordinate hash (cresso_v5.py:495-516): int64 wrap, arithmetic shifts,
+// floor-mod.  `i` is the row-major linear index.
+// ---------------------------------------------------------------------------
+struct HashSalt {
+    uint64_t a, b, c, d;   // multiplier, offset, 2nd and 3rd multipliers
+};
+
+__host__ __device__ inline HashSalt hash_salt(int64_t salt) {
+    uint64_t s = (uint64_t)(salt + 1);
+    HashSalt h;
+    h.a = 1103515245ULL + 97ULL * s;
+    h.b = 12345ULL + 0x9E3779B1ULL * s;
+    h.c = 2246822519ULL + 1315423911ULL * s;
+    h.d = 3266489917ULL + 374761393ULL * s;
+    return h;
+}
+
+__device__ __forceinline__ uint64_t ashr64(uint64_t x, int k) { return (uint64_t)((int64_t)x >> k); }
+
+__device__ __forceinline__ int64_t hash_raw(uint64_t i, const HashSalt& s) {
+    uint64_t h = i * s.a + s.b;
+    h ^= ashr64(h, 16);
+    h *= s.c;
+    h ^= ashr64(h, 13);
+    h *= s.d;
+    h ^= ashr64(h, 16);
+    return (int64_t)h;
+}
+
+// bins > 0; mask = bins-1 when bins is a power of two (floor-mod == low bits
+// in two's complement), else -1 and a signed floor-mod is used.
+__device__ __forceinline__ int hash_bin(uint64_t i, const HashSalt& s, int64_t bins, int64_t mask) {
+    int64_t h = hash_raw(i, s);
+    if (mask >= 0) return (int)(h & mask);
+    int64_t r = h % bins;
+    if (r < 0) r += bins;
+    return (int)r;
+}
+
+}  // namespace cresso
+
+// error reporting shared by all host entry points (abi.cpp)
+namespace cresso {
+int32_t fail(int32_t code, const char* fmt, ...);
+int32_t hip_fail(hipError_t e, const char* what);
+}  // namespace cresso

@@ -1,0 +1,913 @@
+// Scalar (LoRA-thin / small tensor) route of CRESSO5 on gfx950.
+//
+// Math: the reference's PyTorch scalar step, cresso_v5.py:1505-1582 (its
+// fused scalar_update_2d_cuda, cresso_cuda_kernel.cu:3225-3605, mirrors it for
+// 2D tensors in 8 dense passes and 17 launches per tensor).
+//
+// ONE call updates every scalar-route tensor; one 1024-thread workgroup owns
+// one tensor.  The step's dependent global reductions become block
+// reductions:
+//   A: sum f^2                                -> force-RMS reservoir, scale s
+//   B: sum log1p((|f|/s+eps)^p), axis sums of the density
+//                                             -> metric oscillator, instant metric
+//   C: t = f / (s M I + eps); 13 moments of t  -> surprise, contact oscillator and,
+//                                                in closed form, every RMS of the
+//                                                drive shaping (root, shaped, core,
+//                                                residual)
+//   D: drive; sum drive^2                     -> drive-energy reservoir, gain
+//   E: param -= lr * cast(drive * gain)
+//
+// Two kernels:
+//  * scalar_resident_kernel: 2D tensors of <= 64 Ki elements whose rows map to
+//    lane groups (LoRA-thin (L,16)) or whose rows are exactly one block wide
+//    ((16,4096)); f, then t, then drive stay in VGPRs, so HBM traffic is the
+//    compulsory grad read + param read/write.  Axis sums use register partials,
+//    fixed-order wave butterflies and LDS, never float atomics.
+//  * scalar_stream_kernel: every other shape/size/dtype; re-reads the grad in
+//    each pass and keeps general-ndim axis sums as 64-bit fixed-point integers
+//    in a global scratch area (integer atomics: order-independent results).
+#include "common.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+namespace cresso {
+namespace {
+
+constexpr int SR_NT = 1024;                                  // threads per tensor
+constexpr int SR_SLOTS = 16;                                 // float4 slots per thread
+constexpr int64_t SR_RESIDENT_MAX = (int64_t)SR_NT * SR_SLOTS * 4;
+
+enum Layout : int32_t { L_NONE = 0, L_1D = 1, L_ROWGROUP = 2, L_COLBLOCK = 3, L_GENERIC = 4 };
+
+struct ScalarRec {
+    cresso_scalar_desc d;
+    int32_t layout;
+    int32_t group;          // ROWGROUP: lanes per row (power of two <= 64)
+    int64_t rows, cols;     // 2D geometry
+    int64_t stride[8];      // row-major strides (GENERIC)
+    int64_t axis_off[8];    // offset of each axis in the axis-sum array (GENERIC)
+    int64_t sum_dims;       // GENERIC: sum of dims
+    int64_t scratch_off;    // GENERIC: byte offset of the axis-sum scratch in the table
+    int32_t frac_bits;      // GENERIC: fixed-point fraction bits of the axis sums
+    int32_t resident;       // 1: scalar_resident_kernel
+};
+
+__device__ __forceinline__ float uni(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// ---- vector access -------------------------------------------------------
+template <typename T> struct V4;
+template <> struct V4<float> {
+    __device__ static void ld(const float* p, int64_t e, float* o) {
+        float4 v = *reinterpret_cast<const float4*>(p + e);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+    __device__ static void st(float* p, int64_t e, const float* v) {
+        *reinterpret_cast<float4*>(p + e) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+};
+template <typename T> struct V4h {
+    __device__ static void ld(const T* p, int64_t e, float* o) {
+        uint2 raw = *reinterpret_cast<const uint2*>(p + e);
+        const T* h = reinterpret_cast<const T*>(&raw);
+        o[0] = to_f(h[0]); o[1] = to_f(h[1]); o[2] = to_f(h[2]); o[3] = to_f(h[3]);
+    }
+    __device__ static void st(T* p, int64_t e, const float* v) {
+        uint2 raw;
+        T* h = reinterpret_cast<T*>(&raw);
+        h[0] = from_w<T>(v[0]); h[1] = from_w<T>(v[1]); h[2] = from_w<T>(v[2]); h[3] = from_w<T>(v[3]);
+        *reinterpret_cast<uint2*>(p + e) = raw;
+    }
+};
+template <> struct V4<__half> : V4h<__half> {};
+template <> struct V4<__hip_bfloat16> : V4h<__hip_bfloat16> {};
+
+// ---- shared scalar math (work dtype W) ------------------------------------
+template <typename W> __device__ __forceinline__ W reservoir(W old, W cur, double decay, int step) {
+    // cresso_v5.py:900-905: copy on the first step, else in-place EMA
+    if (step <= 1) return cur;
+    return old * (W)decay + (W)(1.0 - decay) * cur;
+}
+
+// rat = t/(1+|t|/clip), bnd = clip*tanh(t/clip), root = sign(t)*sqrt(min(|t|,clip^2)+eps)
+// (cresso_v5.py:1563-1566); rat and bnd share one reciprocal.
+template <typename W>
+__device__ __forceinline__ void shape3(W t, W iclip, W clip, W clip2, W eps, W& rat, W& bnd, W& root) {
+    const W at = t < 0 ? -t : t;
+    const W ex = fexp((W)-2 * at * iclip);
+    const W d1 = (W)1 + ex;
+    const W d2 = (W)1 + at * iclip;
+    const W inv = frcp(d1 * d2);
+    const W th = ((W)1 - ex) * d2 * inv;
+    bnd = (t < 0 ? -th : th) * clip;
+    rat = t * d1 * inv;
+    root = fsign(t) * fsqrt((at < clip2 ? at : clip2) + eps);
+}
+
+// Everything a drive evaluation needs after the pass-C reduction.
+template <typename W> struct DriveCoef {
+    W q1, cA, cB, cN, cD, cr, cb, co, ct, nscale;
+};
+
+// Scalar-state update between passes C and D: surprise, contact oscillator
+// (cresso_v5.py:1525-1547) and the drive-shaping coefficients in closed form
+// from the moments M (cresso_v5.py:1549-1576).
+template <typename W>
+__device__ DriveCoef<W> contact_and_coefs(const double* M, double dn, const cresso_hyper& h, int step, W q0, W& imp,
+                                          W& act, W& sur) {
+    const W eps = (W)h.eps;
+    sur = reservoir(sur, (W)sqrt((double)(W)(M[1] / dn) + (double)eps), h.surprise_decay, step);
+    const W port = (W)(M[0] / dn);
+    const W S = sur;
+    const W dt = (W)h.dt;
+    const W plast = (W)1 + (W)h.surprise_gain * S / ((W)1 + S);
+    const W brake = (W)1 / ((W)1 + (W)h.surprise_brake * S);
+    const W energy = (W)0.5 * (imp * imp + q0 * q0);
+    act = act * (W)0.985 + dt * (port * imp - energy);
+    const W fric = (W)h.impulse_friction + (W)h.contact_gain * (W)tanh((double)(act < 0 ? -act : act));
+    const W damp = (W)1 - dt * fric;
+    imp = imp * (damp > 0 ? damp : (W)0);
+    imp = imp + dt * (plast * brake * port - (W)h.restoring * q0 - (W)h.cubic * (q0 * q0 * q0));
+    W q1 = q0 + dt * imp;
+    q1 = q1 < (W)-8 ? (W)-8 : (q1 > (W)8 ? (W)8 : q1);
+
+    const W frms = (W)sqrt((double)((W)(M[3] / dn) + eps));
+    const W prms = (W)sqrt((double)(q1 * q1 + eps));
+    W align = (W)((double)q1 * M[2] / dn) / (frms * prms + eps);
+    align = align < (W)-1 ? (W)-1 : (align > (W)1 ? (W)1 : align);
+    W agate = (align + (W)1) * (W)0.5;
+    agate = agate < 0 ? (W)0 : (agate > 1 ? (W)1 : agate);
+    if (!(prms > (W)sqrt(h.eps))) agate = 0;
+    const double warm = h.warmup_steps == 0 ? 1.0 : 1.0 - exp(-(double)step / (double)(h.warmup_steps > 1 ? h.warmup_steps : 1));
+    const W mix = (W)(h.prediction_mix * warm) * agate / ((W)1 + S);
+    const W rms_rat = (W)sqrt((double)((W)(M[4] / dn) + eps));
+    const W rms_root = (W)sqrt((double)((W)(M[6] / dn) + eps));
+    const W kroot = rms_rat / (rms_root > eps ? rms_root : eps);
+    const W spike = (W)h.spike_mix / ((W)1 + S);
+    const W rmix = (W)h.root_channel_mix / ((W)1 + (W)0.5 * S);
+    const double ar = (double)(((W)1 - rmix) * ((W)1 - spike));
+    const double ab = (double)(((W)1 - rmix) * spike);
+    const double ao = (double)(rmix * kroot);
+    const double Srr = M[4], Sbb = M[5], Soo = M[6], Srb = M[7], Sro = M[8], Sbo = M[9];
+    const double Stt = M[3], Str = M[10], Stb = M[11], Sto = M[12];
+    const double sh2 = ar * ar * Srr + ab * ab * Sbb + ao * ao * Soo + 2.0 * (ar * ab * Srb + ar * ao * Sro + ab * ao * Sbo);
+    const W srms = (W)sqrt((double)((W)(sh2 / dn) + eps));
+    const W dmix = (W)h.direct_force_mix / ((W)1 + (W)0.35 * S);
+    const W kdir = srms / (frms > eps ? frms : eps);
+    const double cr = (1.0 - (double)dmix) * ar, cb = (1.0 - (double)dmix) * ab, co = (1.0 - (double)dmix) * ao;
+    const double ct = (double)(dmix * kdir);
+    const double core2 = cr * cr * Srr + cb * cb * Sbb + co * co * Soo + ct * ct * Stt +
+                         2.0 * (cr * cb * Srb + cr * co * Sro + cb * co * Sbo + ct * cr * Str + ct * cb * Stb + ct * co * Sto);
+    const W crms = (W)sqrt((double)((W)(core2 / dn) + eps));
+    const double delta = (double)q1 - (double)q0;
+    const double ee1 = fmax(M[1] - 2.0 * delta * M[0] + dn * delta * delta, 0.0);
+    const W erms = (W)sqrt((double)((W)(ee1 / dn) + eps));
+    const W resmix = (W)h.residual_feedback_mix / ((W)1 + S);
+    const W kres = crms / (erms > eps ? erms : eps);
+    DriveCoef<W> c;
+    c.q1 = q1;
+    c.cA = (W)1 - mix;
+    c.cB = mix * q1;
+    c.cN = (W)h.novelty_mix;
+    c.cD = resmix * kres;
+    c.cr = (W)cr; c.cb = (W)cb; c.co = (W)co; c.ct = (W)ct;
+    c.nscale = (W)1 / ((W)h.drive_clip * ((W)1 + S));
+    return c;
+}
+
+// ---------------------------------------------------------------------------
+// register-resident kernel (2D, <= 64 Ki elements, float4-aligned)
+// ---------------------------------------------------------------------------
+template <typename PT, typename GT, int LAYOUT>
+__global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec* __restrict__ recs,
+                                                                 int32_t* __restrict__ steps,
+                                                                 const void* const* __restrict__ grads, int32_t first,
+                                                                 cresso_hyper h) {
+    __shared__ double red[16 * SR_SLOTS];
+    __shared__ int s_step;
+    extern __shared__ __align__(16) unsigned char dyn[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int ri = first + blockIdx.x;
+    const ScalarRec& R = recs[ri];
+    const int64_t n = R.d.numel;
+    const int64_t rows = R.rows;
+    const int C0 = (int)R.cols;
+    const int G = R.group;
+    const float eps = (float)h.eps;
+    float* sp[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sp[i] = reinterpret_cast<float*>(R.d.state[i]);
+    float q0 = *sp[0], imp = *sp[1], mq = *sp[2], mp = *sp[3], fr = *sp[4], de = *sp[5], sur = *sp[6], act = *sp[7];
+    if (tid == 0) {
+        const int s = steps[ri] + 1;
+        steps[ri] = s;
+        s_step = s;
+    }
+    const GT* __restrict__ g = reinterpret_cast<const GT*>(grads[ri]);
+    PT* __restrict__ p = reinterpret_cast<PT*>(R.d.param);
+    const bool wd_on = h.weight_decay != 0.0;
+    const float wd = (float)h.weight_decay;
+
+    float x[SR_SLOTS * 4];
+    auto e0_of = [&](int k) -> int64_t { return ((int64_t)k * SR_NT + tid) * 4; };
+
+    // ---- pass A ----
+    float a_ff = 0.f;
+#pragma unroll
+    for (int k = 0; k < SR_SLOTS; ++k) {
+        const int64_t e0 = e0_of(k);
+        if (e0 < n) {
+            V4<GT>::ld(g, e0, &x[4 * k]);
+            if (h.maximize) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) x[4 * k + c] = -x[4 * k + c];
+            }
+            if (wd_on) {
+                float pv[4];
+                V4<PT>::ld(p, e0, pv);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) x[4 * k + c] = x[4 * k + c] + wd * pv[c];
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[4 * k + c] = 0.f;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) a_ff += x[4 * k + c] * x[4 * k + c];
+    }
+    __syncthreads();
+    const int step = s_step;
+    const double dn = (double)n;
+    {
+        double v[1] = {(double)a_ff};
+        block_sum<1>(v, red);
+        fr = reservoir(fr, sqrtf((float)(v[0] / dn) + eps), h.reservoir_decay, step);
+    }
+    const float scale = fmaxf(fr, eps);
+    const float inv_s = uni(1.0f / scale);
+
+    // ---- pass B ----
+    const float pw = uni((float)h.energy_power);
+    const float ipw = (float)fmax(h.instant_metric_power, 0.25);
+    const bool ip_one = ipw == 1.0f;
+    const float kappa = (float)(h.instant_metric_coupling / (2.0 * fmax(h.instant_metric_power, 0.25)));
+    float* rowfac = reinterpret_cast<float*>(dyn);                       // [rows]
+    double* colred = reinterpret_cast<double*>(dyn + ((sizeof(float) * rows + 15) & ~(size_t)15));  // [16][C0]
+    float colacc[4] = {0.f, 0.f, 0.f, 0.f};
+    float slotrow[SR_SLOTS];  // COLBLOCK: per-slot row partials
+    float a_L = 0.f, a_dens = 0.f;
+#pragma unroll
+    for (int k = 0; k < SR_SLOTS; ++k) {
+        const bool ok = e0_of(k) < n;
+        float rs = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float r = fabsf(x[4 * k + c]) * inv_s + eps;
+            const float L = flog1p(fpow(r, pw));
+            const float rl = fmaxf(fminf(r, 1.0e4f), eps);
+            const float dens = fminf(ip_one ? rl : fpow(rl, ipw), 1.0e6f);
+            if (ok) {
+                a_L += L;
+                a_dens += dens;
+                rs += dens;
+                colacc[c] += dens;
+            }
+            sched_fence();
+        }
+        if (LAYOUT == L_ROWGROUP) {
+            for (int m = 1; m < G; m <<= 1) rs += __shfl_xor(rs, m, 64);
+            const int64_t row = ((int64_t)k * SR_NT + tid) / G;
+            if (ok && (tid % G) == 0) rowfac[row] = rs;
+        } else {
+            slotrow[k] = rs;
+        }
+    }
+    double gmean;
+    {
+        double v[2] = {(double)a_L, (double)a_dens};
+        block_sum<2>(v, red);
+        const float dens_mean = (float)(v[0] / dn);
+        gmean = v[1] / dn;
+        // scalar metric oscillator (cresso_v5.py:1510-1518)
+        const float mport = dens_mean - tanhf(mq);
+        mp = mp * (float)fmax(0.0, 1.0 - h.metric_dt * h.metric_friction);
+        mp = mp + (float)h.metric_dt * (mport - mq);
+        mq = mq + (float)h.metric_dt * mp;
+        mq = clampf(mq, -3.0f, 3.0f);
+    }
+    const float metric = clampf(expf((float)h.metric_coupling * mq), 0.06f, 16.0f);
+    const float gden = (float)fmax(gmean, (double)eps);
+    float Ec[4];
+    if (LAYOUT == L_ROWGROUP) {
+        // column sums: butterfly over lanes sharing tid % G, then waves in order
+        float cs[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            cs[c] = colacc[c];
+            for (int m = G; m < 64; m <<= 1) cs[c] += __shfl_xor(cs[c], m, 64);
+        }
+        const int wave = tid >> 6;
+        if (lane < G) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) colred[wave * C0 + lane * 4 + c] = (double)cs[c];
+        }
+        __syncthreads();   // rowfac and colred complete
+        float* colfac = reinterpret_cast<float*>(colred + 16 * C0);
+        if (tid < C0) {
+            double s = 0.0;
+            for (int w = 0; w < SR_NT / 64; ++w) s += colred[w * C0 + tid];
+            const float cm = (float)(s / (double)rows);
+            colfac[tid] = expf(kappa * logf(fmaxf(cm / gden, eps)));
+        }
+        for (int64_t i = tid; i < rows; i += SR_NT) {
+            const float rm = rowfac[i] / (float)C0;
+            rowfac[i] = expf(kappa * logf(fmaxf(rm / gden, eps)));
+        }
+        __syncthreads();
+        const int cg = tid % G;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) Ec[c] = colfac[cg * 4 + c];
+    } else {
+        double v[SR_SLOTS];
+#pragma unroll
+        for (int k = 0; k < SR_SLOTS; ++k) v[k] = (double)slotrow[k];
+        block_sum<SR_SLOTS>(v, red);
+        if (tid < SR_SLOTS && tid < rows) {
+            const float rm = (float)(v[tid] / (double)C0);
+            rowfac[tid] = expf(kappa * logf(fmaxf(rm / gden, eps)));
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float cm = colacc[c] / (float)rows;
+            Ec[c] = expf(kappa * logf(fmaxf(cm / gden, eps)));
+        }
+        __syncthreads();
+    }
+
+    // ---- pass C ----
+    const float sM = uni(scale * metric);
+    const bool ls_on = h.local_sharpness != 0.0;
+    const float ls = (float)h.local_sharpness;
+    const float clip = uni((float)h.drive_clip);
+    const float iclip = uni(1.0f / clip);
+    const float clip2 = uni(clip * clip);
+    float m[13];
+#pragma unroll
+    for (int i = 0; i < 13; ++i) m[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < SR_SLOTS; ++k) {
+        const bool ok = e0_of(k) < n;
+        const int64_t row = LAYOUT == L_ROWGROUP ? ((int64_t)k * SR_NT + tid) / G : (int64_t)k;
+        const float Er = ok ? rowfac[row] : 1.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float f = x[4 * k + c];
+            float den = sM;
+            if (ls_on) {
+                const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
+                den = den * clampf(1.0f + ls * fsqrt(fminf(rel, 100.0f)), 1.0f, 8.0f);
+            }
+            const float inst = clampf(Er * Ec[c], 0.08f, 12.0f);
+            const float t = clampf(f * frcp(den * inst + eps), -1.0e4f, 1.0e4f);
+            x[4 * k + c] = t;
+            if (ok) {
+                float rat, bnd, root;
+                shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
+                const float e = t - q0;
+                m[0] += e; m[1] += e * e; m[2] += t; m[3] += t * t;
+                m[4] += rat * rat; m[5] += bnd * bnd; m[6] += root * root;
+                m[7] += rat * bnd; m[8] += rat * root; m[9] += bnd * root;
+                m[10] += t * rat; m[11] += t * bnd; m[12] += t * root;
+            }
+            sched_fence();
+        }
+    }
+    double M[13];
+#pragma unroll
+    for (int i = 0; i < 13; ++i) M[i] = (double)m[i];
+    block_sum<13>(M, red);
+    const DriveCoef<float> dc = contact_and_coefs<float>(M, dn, h, step, q0, imp, act, sur);
+
+    // ---- pass D ----
+    const float q1 = uni(dc.q1), cA = uni(dc.cA), cB = uni(dc.cB), cN = uni(dc.cN), cD = uni(dc.cD);
+    const float cr = uni(dc.cr), cb = uni(dc.cb), co = uni(dc.co), ct = uni(dc.ct), ns = uni(dc.nscale);
+    float a_dd = 0.f;
+#pragma unroll
+    for (int k = 0; k < SR_SLOTS; ++k) {
+        const bool ok = e0_of(k) < n;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float t = x[4 * k + c];
+            float rat, bnd, root;
+            shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
+            const float e = t - q1;
+            const float nov = ftanh(e * ns) * clip;
+            const float core = cr * rat + cb * bnd + co * root + ct * t;
+            const float drv = cA * core + cB + cN * nov + cD * e;
+            x[4 * k + c] = drv;
+            if (ok) a_dd += drv * drv;
+            sched_fence();
+        }
+    }
+    {
+        double v[1] = {(double)a_dd};
+        block_sum<1>(v, red);
+        de = reservoir(de, (float)(v[0] / dn), h.reservoir_decay, step);
+    }
+    const float gain = uni(clampf((float)h.target_update_rms / sqrtf(de + eps), (float)h.min_gain, (float)h.max_gain));
+
+    // ---- pass E ----
+    const float nlr = uni((float)(-h.lr));
+#pragma unroll
+    for (int k = 0; k < SR_SLOTS; ++k) {
+        const int64_t e0 = e0_of(k);
+        if (e0 < n) {
+            float pv[4];
+            V4<PT>::ld(p, e0, pv);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) pv[c] = pv[c] + nlr * to_f(from_w<PT>(x[4 * k + c] * gain));
+            V4<PT>::st(p, e0, pv);
+        }
+    }
+    if (tid == 0) {
+        *sp[0] = dc.q1; *sp[1] = imp; *sp[2] = mq; *sp[3] = mp; *sp[4] = fr; *sp[5] = de; *sp[6] = sur; *sp[7] = act;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// streaming kernel (any shape, any size; work dtype W)
+// ---------------------------------------------------------------------------
+template <typename W, typename T> __device__ __forceinline__ W ldw(const T* p, int64_t i) { return to_w<W>(p[i]); }
+
+template <typename W, typename PT, typename GT>
+__global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* __restrict__ recs, int32_t* __restrict__ steps,
+                                                              const void* const* __restrict__ grads, int32_t first,
+                                                              unsigned char* table, cresso_hyper h) {
+    __shared__ double red[16 * 13];
+    __shared__ int s_step;
+    const int tid = threadIdx.x;
+    const int ri = first + blockIdx.x;
+    const ScalarRec& R = recs[ri];
+    const int64_t n = R.d.numel;
+    const int nd = R.d.ndim;
+    const int layout = R.layout;
+    const W eps = (W)h.eps;
+    W* sp[8];
+    for (int i = 0; i < 8; ++i) sp[i] = reinterpret_cast<W*>(R.d.state[i]);
+    W q0 = *sp[0], imp = *sp[1], mq = *sp[2], mp = *sp[3], fr = *sp[4], de = *sp[5], sur = *sp[6], act = *sp[7];
+    if (tid == 0) {
+        const int s = steps[ri] + 1;
+        steps[ri] = s;
+        s_step = s;
+    }
+    const GT* __restrict__ g = reinterpret_cast<const GT*>(grads[ri]);
+    PT* __restrict__ p = reinterpret_cast<PT*>(R.d.param);
+    const bool wd_on = h.weight_decay != 0.0;
+    const W wd = (W)h.weight_decay;
+    const bool neg = h.maximize != 0;
+    auto force = [&](int64_t i) -> W {
+        W f = ldw<W>(g, i);
+        if (neg) f = -f;
+        if (wd_on) f = f + wd * ldw<W>(p, i);
+        return f;
+    };
+    unsigned long long* axis_fx = reinterpret_cast<unsigned long long*>(table + R.scratch_off);
+    float* axis_fac = reinterpret_cast<float*>(table + R.scratch_off + sizeof(unsigned long long) * R.sum_dims);
+    const double dn = (double)n;
+
+    // ---- pass A ----
+    W a = 0;
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W f = force(i);
+        a += f * f;
+    }
+    if (layout == L_GENERIC)
+        for (int64_t i = tid; i < R.sum_dims; i += SR_NT) axis_fx[i] = 0ull;
+    __syncthreads();
+    const int step = s_step;
+    {
+        double v[1] = {(double)a};
+        block_sum<1>(v, red);
+        fr = reservoir(fr, (W)sqrt((double)((W)(v[0] / dn) + eps)), h.reservoir_decay, step);
+    }
+    const W scale = fr > eps ? fr : eps;
+    const W inv_s = (W)1 / scale;
+
+    // ---- pass B ----
+    const W pw = (W)h.energy_power;
+    const W ipw = (W)fmax(h.instant_metric_power, 0.25);
+    const W kappa = nd > 0 ? (W)(h.instant_metric_coupling / ((double)nd * fmax(h.instant_metric_power, 0.25))) : (W)0;
+    const double fx_scale = ldexp(1.0, R.frac_bits);
+    auto density = [&](W f) -> W {
+        W rel = (f < 0 ? -f : f) * inv_s + eps;
+        rel = rel < (W)1e4 ? rel : (W)1e4;
+        rel = rel > eps ? rel : eps;
+        const W d = ipw == (W)1 ? rel : fpow(rel, ipw);
+        return d < (W)1e6 ? d : (W)1e6;
+    };
+    W aL = 0, aD = 0;
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W f = force(i);
+        const W r = (f < 0 ? -f : f) * inv_s + eps;
+        aL += flog1p(fpow(r, pw));
+        const W d = density(f);
+        aD += d;
+        if (layout == L_GENERIC) {
+            const unsigned long long v = (unsigned long long)llrint((double)d * fx_scale);
+            for (int ax = 0; ax < nd; ++ax) atomicAdd(&axis_fx[R.axis_off[ax] + (i / R.stride[ax]) % R.d.shape[ax]], v);
+        }
+    }
+    double gmean;
+    {
+        double v[2] = {(double)aL, (double)aD};
+        block_sum<2>(v, red);
+        const W dens_mean = (W)(v[0] / dn);
+        gmean = v[1] / dn;
+        const W mport = dens_mean - (W)tanh((double)mq);
+        mp = mp * (W)fmax(0.0, 1.0 - h.metric_dt * h.metric_friction);
+        mp = mp + (W)h.metric_dt * (mport - mq);
+        mq = mq + (W)h.metric_dt * mp;
+        mq = mq < (W)-3 ? (W)-3 : (mq > (W)3 ? (W)3 : mq);
+    }
+    W metric = (W)exp((double)((W)h.metric_coupling * mq));
+    metric = metric < (W)0.06 ? (W)0.06 : (metric > (W)16 ? (W)16 : metric);
+    const W gden = (W)fmax(gmean, (double)eps);
+    if (layout == L_GENERIC) {
+        for (int64_t i = tid; i < R.sum_dims; i += SR_NT) {
+            int ax = 0;
+            while (ax + 1 < nd && i >= R.axis_off[ax + 1]) ++ax;
+            const unsigned long long raw = __hip_atomic_load(&axis_fx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const W mean = (W)((double)(long long)raw / fx_scale / (dn / (double)R.d.shape[ax]));
+            const W r = mean / gden;
+            axis_fac[i] = (float)(kappa * flog(r > eps ? r : eps));
+        }
+        __syncthreads();
+    }
+    const W sM = scale * metric;
+    const bool ls_on = h.local_sharpness != 0.0;
+    const W ls = (W)h.local_sharpness;
+    auto tangent = [&](W f, int64_t i) -> W {
+        W den = sM;
+        if (ls_on) {
+            W rel = (f < 0 ? -f : f) * inv_s + eps;
+            rel = rel < (W)100 ? rel : (W)100;
+            W lm = (W)1 + ls * fsqrt(rel);
+            den = den * (lm < (W)1 ? (W)1 : (lm > (W)8 ? (W)8 : lm));
+        }
+        W inst = 1;
+        if (layout == L_1D) {
+            const W r = density(f) / gden;
+            inst = fexp(kappa * flog(r > eps ? r : eps));
+        } else if (layout == L_GENERIC) {
+            float ls_ = 0.f;
+            for (int ax = 0; ax < nd; ++ax) ls_ += axis_fac[R.axis_off[ax] + (i / R.stride[ax]) % R.d.shape[ax]];
+            inst = fexp((W)ls_);
+        }
+        if (layout != L_NONE) inst = inst < (W)0.08 ? (W)0.08 : (inst > (W)12 ? (W)12 : inst);
+        W t = f / (den * inst + eps);
+        return t < (W)-1e4 ? (W)-1e4 : (t > (W)1e4 ? (W)1e4 : t);
+    };
+    const W clip = (W)h.drive_clip, iclip = (W)1 / clip, clip2 = clip * clip;
+
+    // ---- pass C ----
+    W m[13];
+    for (int j = 0; j < 13; ++j) m[j] = 0;
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W t = tangent(force(i), i);
+        W rat, bnd, root;
+        shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
+        const W e = t - q0;
+        m[0] += e; m[1] += e * e; m[2] += t; m[3] += t * t;
+        m[4] += rat * rat; m[5] += bnd * bnd; m[6] += root * root;
+        m[7] += rat * bnd; m[8] += rat * root; m[9] += bnd * root;
+        m[10] += t * rat; m[11] += t * bnd; m[12] += t * root;
+    }
+    double M[13];
+    for (int j = 0; j < 13; ++j) M[j] = (double)m[j];
+    block_sum<13>(M, red);
+    const DriveCoef<W> dc = contact_and_coefs<W>(M, dn, h, step, q0, imp, act, sur);
+    auto drive = [&](W t) -> W {
+        W rat, bnd, root;
+        shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
+        const W e = t - dc.q1;
+        const W nov = ftanh(e * dc.nscale) * clip;
+        const W core = dc.cr * rat + dc.cb * bnd + dc.co * root + dc.ct * t;
+        return dc.cA * core + dc.cB + dc.cN * nov + dc.cD * e;
+    };
+
+    // ---- pass D ----
+    W add = 0;
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W d = drive(tangent(force(i), i));
+        add += d * d;
+    }
+    {
+        double v[1] = {(double)add};
+        block_sum<1>(v, red);
+        de = reservoir(de, (W)(v[0] / dn), h.reservoir_decay, step);
+    }
+    W gain = (W)h.target_update_rms / (W)sqrt((double)(de + eps));
+    gain = gain < (W)h.min_gain ? (W)h.min_gain : (gain > (W)h.max_gain ? (W)h.max_gain : gain);
+
+    // ---- pass E ---- (force is recomputed before any param store of this thread)
+    const W nlr = (W)(-h.lr);
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W d = drive(tangent(force(i), i));
+        const W u = to_w<W>(from_wd<PT>((double)(d * gain)));
+        p[i] = from_wd<PT>((double)(ldw<W>(p, i) + nlr * u));
+    }
+    if (tid == 0) {
+        *sp[0] = dc.q1; *sp[1] = imp; *sp[2] = mq; *sp[3] = mp; *sp[4] = fr; *sp[5] = de; *sp[6] = sur; *sp[7] = act;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+struct Variant {
+    int pt, gt, kind;   // kind: 0 stream, 1 resident ROWGROUP, 2 resident COLBLOCK
+    bool operator==(const Variant& o) const { return pt == o.pt && gt == o.gt && kind == o.kind; }
+};
+
+int dtype_bytes(int t) { return t == CRESSO_F64 ? 8 : (t == CRESSO_F32 ? 4 : 2); }
+
+// Fills r (except scratch_off) and returns the generic scratch bytes needed.
+int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec& r, Variant& v, size_t& lds,
+                  size_t& scratch) {
+    if (d.ndim < 0 || d.ndim > 8) return fail(CRESSO_E_INVALID, "scalar route: ndim %d outside 0..8", d.ndim);
+    int64_t n = 1;
+    for (int a = 0; a < d.ndim; ++a) {
+        if (d.shape[a] <= 0)
+            return fail(CRESSO_E_INVALID, "scalar route: shape[%d]=%lld must be positive", a, (long long)d.shape[a]);
+        n *= d.shape[a];
+    }
+    if (n != d.numel)
+        return fail(CRESSO_E_INVALID, "scalar route: numel %lld != product of shape %lld", (long long)d.numel, (long long)n);
+    if (!d.param || !d.grad) return fail(CRESSO_E_INVALID, "scalar route: null param or grad pointer");
+    for (int i = 0; i < 8; ++i)
+        if (!d.state[i]) return fail(CRESSO_E_INVALID, "scalar route: null state pointer %d", i);
+    auto okdt = [](int t) { return t == CRESSO_F32 || t == CRESSO_F16 || t == CRESSO_BF16 || t == CRESSO_F64; };
+    if (!okdt(d.param_dtype) || !okdt(d.grad_dtype)) return fail(CRESSO_E_INVALID, "scalar route: unknown dtype code");
+    if ((d.param_dtype == CRESSO_F64) != (d.grad_dtype == CRESSO_F64))
+        return fail(CRESSO_E_UNSUPPORTED, "scalar route: float64 params need float64 grads");
+    std::memset(&r, 0, sizeof(r));
+    r.d = d;
+    lds = 0;
+    scratch = 0;
+    const bool aligned = ((uintptr_t)d.param % (uintptr_t)(4 * dtype_bytes(d.param_dtype))) == 0 &&
+                         ((uintptr_t)d.grad % (uintptr_t)(4 * dtype_bytes(d.grad_dtype))) == 0;
+    const bool same = d.param_dtype == d.grad_dtype;
+    int kind = 0;
+    if (h.instant_metric_coupling == 0.0 || d.ndim == 0 || n <= 1) {
+        r.layout = L_NONE;
+    } else if (d.ndim == 1) {
+        r.layout = L_1D;
+    } else {
+        const int64_t C0 = d.ndim == 2 ? d.shape[1] : 0;
+        const bool res_ok = d.ndim == 2 && same && d.param_dtype != CRESSO_F64 && aligned && n <= SR_RESIDENT_MAX && C0 % 4 == 0;
+        if (res_ok && is_pow2(C0 / 4) && C0 / 4 <= 64) {
+            r.layout = L_ROWGROUP;
+            r.group = (int32_t)(C0 / 4);
+            r.rows = d.shape[0];
+            r.cols = C0;
+            kind = 1;
+            lds = ((sizeof(float) * (size_t)r.rows + 15) & ~(size_t)15) + sizeof(double) * 16 * (size_t)C0 + sizeof(float) * (size_t)C0;
+        } else if (res_ok && C0 == (int64_t)SR_NT * 4) {
+            r.layout = L_COLBLOCK;
+            r.rows = d.shape[0];
+            r.cols = C0;
+            kind = 2;
+            lds = sizeof(float) * SR_SLOTS;
+        } else {
+            int64_t sum = 0, maxcnt = 1, st = 1;
+            for (int a = d.ndim - 1; a >= 0; --a) {
+                r.stride[a] = st;
+                st *= d.shape[a];
+            }
+            for (int a = 0; a < d.ndim; ++a) {
+                r.axis_off[a] = sum;
+                sum += d.shape[a];
+                maxcnt = std::max<int64_t>(maxcnt, n / d.shape[a]);
+            }
+            r.layout = L_GENERIC;
+            r.sum_dims = sum;
+            // density <= 1e6 per element: every fixed-point axis sum stays below 2^62
+            r.frac_bits = (int32_t)std::floor(62.0 - std::log2(1.0e6 * (double)maxcnt));
+            scratch = (size_t)sum * (sizeof(unsigned long long) + sizeof(float));
+            scratch = (scratch + 255) & ~(size_t)255;
+        }
+    }
+    r.resident = kind != 0;
+    v = Variant{d.param_dtype, d.grad_dtype, kind};
+    return CRESSO_OK;
+}
+
+template <typename PT, typename GT>
+hipError_t launch_resident(int kind, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
+                           int32_t cnt, size_t lds, const cresso_hyper& h, hipStream_t s) {
+    if (kind == 1)
+        hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, L_ROWGROUP>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads,
+                           first, h);
+    else
+        hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, L_COLBLOCK>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads,
+                           first, h);
+    return hipGetLastError();
+}
+
+template <typename W, typename PT, typename GT>
+hipError_t launch_stream(const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first, int32_t cnt,
+                         unsigned char* table, const cresso_hyper& h, hipStream_t s) {
+    hipLaunchKernelGGL((scalar_stream_kernel<W, PT, GT>), dim3(cnt), dim3(SR_NT), 0, s, recs, steps, grads, first, table, h);
+    return hipGetLastError();
+}
+
+hipError_t dispatch(const Variant& v, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
+                    int32_t cnt, size_t lds, unsigned char* table, const cresso_hyper& h, hipStream_t s) {
+    if (v.kind != 0) {
+        if (v.pt == CRESSO_F32) return launch_resident<float, float>(v.kind, recs, steps, grads, first, cnt, lds, h, s);
+        if (v.pt == CRESSO_BF16) return launch_resident<__hip_bfloat16, __hip_bfloat16>(v.kind, recs, steps, grads, first, cnt, lds, h, s);
+        if (v.pt == CRESSO_F16) return launch_resident<__half, __half>(v.kind, recs, steps, grads, first, cnt, lds, h, s);
+        return hipErrorInvalidValue;
+    }
+#define CRESSO_SR_CASE(PC, GC, W, PT, GT) \
+    if (v.pt == PC && v.gt == GC) return launch_stream<W, PT, GT>(recs, steps, grads, first, cnt, table, h, s);
+    CRESSO_SR_CASE(CRESSO_F32, CRESSO_F32, float, float, float)
+    CRESSO_SR_CASE(CRESSO_BF16, CRESSO_BF16, float, __hip_bfloat16, __hip_bfloat16)
+    CRESSO_SR_CASE(CRESSO_F16, CRESSO_F16, float, __half, __half)
+    CRESSO_SR_CASE(CRESSO_F64, CRESSO_F64, double, double, double)
+    CRESSO_SR_CASE(CRESSO_BF16, CRESSO_F32, float, __hip_bfloat16, float)
+    CRESSO_SR_CASE(CRESSO_F16, CRESSO_F32, float, __half, float)
+    CRESSO_SR_CASE(CRESSO_F32, CRESSO_BF16, float, float, __hip_bfloat16)
+    CRESSO_SR_CASE(CRESSO_F32, CRESSO_F16, float, float, __half)
+#undef CRESSO_SR_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+}  // namespace cresso
+
+// Opaque plan: validated, grouped descriptor table plus pinned staging for
+// the per-step grad pointers (double-buffered, guarded by events).
+struct cresso_scalar_plan {
+    std::vector<cresso::ScalarRec> recs;     // grouped order
+    std::vector<int32_t> steps;               // grouped order
+    std::vector<int32_t> order;               // grouped index -> caller index
+    struct Group { cresso::Variant v; int32_t first, count; size_t lds; };
+    std::vector<Group> groups;
+    size_t steps_off = 0, grads_off = 0, total = 0;
+    bool no_instant = false;                  // instant_metric_coupling == 0 at planning time
+    const void** staging[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    int flip = 0;
+};
+
+namespace cresso {
+namespace {
+
+int32_t build_plan(const cresso_scalar_desc* descs, int32_t count, const cresso_hyper& h, cresso_scalar_plan& P) {
+    std::vector<ScalarRec> recs((size_t)count);
+    std::vector<Variant> var((size_t)count);
+    std::vector<size_t> lds((size_t)count), scr((size_t)count);
+    for (int32_t i = 0; i < count; ++i) {
+        int32_t rc = plan_desc(descs[i], h, recs[(size_t)i], var[(size_t)i], lds[(size_t)i], scr[(size_t)i]);
+        if (rc != CRESSO_OK) return rc;
+    }
+    std::vector<Variant> keys;
+    for (const Variant& v : var)
+        if (std::find(keys.begin(), keys.end(), v) == keys.end()) keys.push_back(v);
+    std::vector<int32_t> key((size_t)count);
+    for (int32_t i = 0; i < count; ++i)
+        key[(size_t)i] = (int32_t)(std::find(keys.begin(), keys.end(), var[(size_t)i]) - keys.begin());
+    P.order.resize((size_t)count);
+    for (int32_t i = 0; i < count; ++i) P.order[(size_t)i] = i;
+    std::stable_sort(P.order.begin(), P.order.end(), [&](int32_t a, int32_t b) { return key[(size_t)a] < key[(size_t)b]; });
+    const size_t recs_bytes = (sizeof(ScalarRec) * (size_t)count + 255) & ~(size_t)255;
+    P.steps_off = recs_bytes;
+    P.grads_off = P.steps_off + ((sizeof(int32_t) * (size_t)count + 255) & ~(size_t)255);
+    size_t off = P.grads_off + ((sizeof(void*) * (size_t)count + 255) & ~(size_t)255);
+    P.recs.resize((size_t)count);
+    P.steps.resize((size_t)count);
+    P.groups.clear();
+    for (int32_t j = 0; j < count; ++j) {
+        const int32_t i = P.order[(size_t)j];
+        P.recs[(size_t)j] = recs[(size_t)i];
+        P.recs[(size_t)j].scratch_off = (int64_t)off;
+        off += scr[(size_t)i];
+        P.steps[(size_t)j] = descs[i].step;
+        if (P.groups.empty() || !(P.groups.back().v == var[(size_t)i]))
+            P.groups.push_back({var[(size_t)i], j, 0, 0});
+        P.groups.back().count += 1;
+        P.groups.back().lds = std::max(P.groups.back().lds, lds[(size_t)i]);
+    }
+    P.total = off;
+    P.no_instant = h.instant_metric_coupling == 0.0;
+    return CRESSO_OK;
+}
+
+}  // namespace
+}  // namespace cresso
+
+using namespace cresso;
+
+extern "C" cresso_scalar_plan* cresso_scalar_plan_create(const cresso_scalar_desc* host_descs, int32_t count,
+                                                         const cresso_hyper* hyper) {
+    if (count <= 0 || !host_descs || !hyper) {
+        fail(CRESSO_E_INVALID, "scalar route: plan needs count > 0, descriptors and hyperparameters");
+        return nullptr;
+    }
+    if (!(hyper->drive_clip > 0.0)) {
+        fail(CRESSO_E_INVALID, "scalar route: drive_clip must be positive");
+        return nullptr;
+    }
+    cresso_scalar_plan* P = new cresso_scalar_plan();
+    if (build_plan(host_descs, count, *hyper, *P) != CRESSO_OK) {
+        delete P;
+        return nullptr;
+    }
+    for (int k = 0; k < 2; ++k) {
+        hipError_t e = hipHostMalloc((void**)&P->staging[k], sizeof(void*) * (size_t)count, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&P->ev[k], hipEventDisableTiming);
+        if (e != hipSuccess) {
+            hip_fail(e, "scalar route: plan staging");
+            cresso_scalar_plan_destroy(P);
+            return nullptr;
+        }
+    }
+    return P;
+}
+
+extern "C" void cresso_scalar_plan_destroy(cresso_scalar_plan* P) {
+    if (!P) return;
+    for (int k = 0; k < 2; ++k) {
+        if (P->ev[k]) {
+            (void)hipEventSynchronize(P->ev[k]);
+            (void)hipEventDestroy(P->ev[k]);
+        }
+        if (P->staging[k]) (void)hipHostFree(P->staging[k]);
+    }
+    delete P;
+}
+
+extern "C" size_t cresso_scalar_plan_bytes(const cresso_scalar_plan* P) { return P ? P->total : 0; }
+
+extern "C" int32_t cresso_scalar_plan_upload(cresso_scalar_plan* P, void* dev_table, size_t table_bytes, void* stream) {
+    if (!P || !dev_table) return fail(CRESSO_E_INVALID, "scalar route: null plan or table");
+    if (table_bytes < P->total)
+        return fail(CRESSO_E_INVALID, "scalar route: table of %zu bytes is smaller than the %zu bytes needed", table_bytes, P->total);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    unsigned char* table = reinterpret_cast<unsigned char*>(dev_table);
+    const size_t count = P->recs.size();
+    hipError_t e = hipMemcpyAsync(table, P->recs.data(), sizeof(ScalarRec) * count, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(table + P->steps_off, P->steps.data(), sizeof(int32_t) * count, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) {
+        std::vector<const void*> g(count);
+        for (size_t j = 0; j < count; ++j) g[j] = P->recs[j].d.grad;
+        e = hipMemcpyAsync(table + P->grads_off, g.data(), sizeof(void*) * count, hipMemcpyHostToDevice, s);
+    }
+    // pageable sources: make sure the copies have consumed them before returning
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "scalar route: table upload");
+}
+
+extern "C" int32_t cresso_scalar_plan_step(cresso_scalar_plan* P, void* dev_table, const void* const* grads,
+                                           const cresso_hyper* hyper, void* stream) {
+    if (!P || !dev_table || !hyper) return fail(CRESSO_E_INVALID, "scalar route: null argument");
+    const cresso_hyper& h = *hyper;
+    if (!(h.drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "scalar route: drive_clip must be positive");
+    if ((h.instant_metric_coupling == 0.0) != P->no_instant)
+        return fail(CRESSO_E_INVALID, "scalar route: instant_metric_coupling switched between zero and non-zero; re-plan");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    unsigned char* table = reinterpret_cast<unsigned char*>(dev_table);
+    const size_t count = P->recs.size();
+    if (grads) {
+        const int k = P->flip;
+        P->flip ^= 1;
+        hipError_t e = hipEventSynchronize(P->ev[k]);   // the copy issued two steps ago is done
+        if (e != hipSuccess) return hip_fail(e, "scalar route: staging wait");
+        for (size_t j = 0; j < count; ++j) {
+            const void* gp = grads[P->order[j]];
+            if (!gp) return fail(CRESSO_E_INVALID, "scalar route: null grad pointer for tensor %d", P->order[j]);
+            P->staging[k][j] = gp;
+        }
+        e = hipMemcpyAsync(table + P->grads_off, P->staging[k], sizeof(void*) * count, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipEventRecord(P->ev[k], s);
+        if (e != hipSuccess) return hip_fail(e, "scalar route: grad pointer upload");
+    }
+    const ScalarRec* drecs = reinterpret_cast<const ScalarRec*>(table);
+    int32_t* dsteps = reinterpret_cast<int32_t*>(table + P->steps_off);
+    const void* const* dgrads = reinterpret_cast<const void* const*>(table + P->grads_off);
+    for (const auto& G : P->groups) {
+        hipError_t e = dispatch(G.v, drecs, dsteps, dgrads, G.first, G.count, G.lds, table, h, s);
+        if (e != hipSuccess) return hip_fail(e, "scalar route: kernel launch");
+    }
+    return CRESSO_OK;
+}
