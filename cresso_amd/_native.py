@@ -57,6 +57,22 @@ class ScalarDesc(ctypes.Structure):
     ]
 
 
+class SpectralDesc(ctypes.Structure):
+    _fields_ = [
+        ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p),
+        ("param_dtype", ctypes.c_int32),
+        ("grad_dtype", ctypes.c_int32),
+        ("numel", ctypes.c_int64),
+    ] + [(k, ctypes.c_void_p) for k in (
+        "force_rms", "drive_energy", "surprise", "action", "omega", "q_cos", "q_sin", "p_cos", "p_sin",
+        "metric_cos", "metric_sin", "metric_p_cos", "metric_p_sin", "calcium_cos", "calcium_sin", "mode_confidence",
+        "hash_energy", "hash_impulse", "hash_refractory")] + [
+        ("step", ctypes.c_int32),
+        ("hard", ctypes.c_int32),
+    ]
+
+
 def hyper_from_group(group: dict) -> Hyper:
     h = Hyper()
     for n in HYPER_DOUBLES:
@@ -95,6 +111,18 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cresso_scalar_plan_step.restype = c.c_int32
     lib.cresso_scalar_plan_step.argtypes = [c.c_void_p, c.c_void_p, c.POINTER(c.c_void_p), c.POINTER(Hyper),
                                             c.c_void_p]
+    lib.cresso_spectral_plan_create.restype = c.c_void_p
+    lib.cresso_spectral_plan_create.argtypes = [c.POINTER(c.c_int64), c.c_int32, c.POINTER(c.c_int64), c.c_int32,
+                                                c.c_int32, c.c_int32]
+    lib.cresso_spectral_plan_destroy.restype = None
+    lib.cresso_spectral_plan_destroy.argtypes = [c.c_void_p]
+    lib.cresso_spectral_workspace_bytes.restype = c.c_size_t
+    lib.cresso_spectral_workspace_bytes.argtypes = [c.c_void_p]
+    lib.cresso_spectral_workspace_init.restype = c.c_int32
+    lib.cresso_spectral_workspace_init.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.POINTER(Hyper), c.c_void_p]
+    lib.cresso_spectral_step.restype = c.c_int32
+    lib.cresso_spectral_step.argtypes = [c.c_void_p, c.POINTER(SpectralDesc), c.c_void_p, c.c_size_t,
+                                         c.POINTER(Hyper), c.c_void_p]
 
 
 def load() -> ctypes.CDLL:

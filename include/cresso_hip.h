@@ -111,6 +111,58 @@ int32_t cresso_scalar_plan_upload(cresso_scalar_plan* plan, void* dev_table, siz
 int32_t cresso_scalar_plan_step(cresso_scalar_plan* plan, void* dev_table, const void* const* grads,
                                 const cresso_hyper* hyper, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Spectral / coordinate-hash route (large tensors).
+ *
+ * Replaces the reference's per-step op chain of cresso_v5.py:945-1353 as
+ * fused by cresso_cuda_kernel.cu (basis_axis_cache_cuda 842,
+ * basis_stats_with_cache_cuda 897, basis_project_with_cache_cuda 996,
+ * basis_reconstruct_with_cache_cuda 1148, hash_metric_update_log_cuda 1515,
+ * hash_impulse_update_gather_cuda 1593, instant_axis_metric_2d_cuda 1766,
+ * metric_update_cuda 1829, confidence_update_cuda 1869,
+ * contact_update_pair_cuda 1903, drive_update_cuda 2995; bindings
+ * cresso_cuda.cpp:170-196) with one call per tensor and step.
+ * ------------------------------------------------------------------------- */
+
+/* Opaque plan for one (shape, freqs, hash_bins, hash_tables): geometry,
+ * carrier bookkeeping and workspace layout.  freqs is the host copy of
+ * state["freqs"] (int64 [rank][ndim], cresso_v5.py:864-868).  NULL on error. */
+typedef struct cresso_spectral_plan cresso_spectral_plan;
+cresso_spectral_plan* cresso_spectral_plan_create(const int64_t* shape, int32_t ndim, const int64_t* freqs,
+                                                  int32_t rank, int32_t hash_bins, int32_t hash_tables);
+void cresso_spectral_plan_destroy(cresso_spectral_plan* plan);
+
+/* Device bytes of the plan's workspace: per-axis carrier tables, basis stats,
+ * cached coordinate-hash bins of every element (data independent), bin
+ * counts, the stored tangent field and per-step scratch.  Not optimizer
+ * state: it is rebuilt from the shape and freqs. */
+size_t cresso_spectral_workspace_bytes(const cresso_spectral_plan* plan);
+
+/* Build the workspace tables on the device (synchronizes `stream` once). */
+int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* plan, void* workspace, size_t workspace_bytes,
+                                       const cresso_hyper* hyper, void* stream);
+
+typedef struct cresso_spectral_desc {
+    void* param;              /* contiguous, param_dtype                    */
+    const void* grad;         /* contiguous, grad_dtype                     */
+    int32_t param_dtype;
+    int32_t grad_dtype;
+    int64_t numel;
+    /* state of cresso_v5.py:857-883, fp32, updated in place */
+    void *force_rms, *drive_energy, *surprise, *action;       /* 0-dim       */
+    const void* omega;                                         /* [rank]      */
+    void *q_cos, *q_sin, *p_cos, *p_sin;                       /* [rank]      */
+    void *metric_cos, *metric_sin, *metric_p_cos, *metric_p_sin;
+    void *calcium_cos, *calcium_sin, *mode_confidence;
+    void *hash_energy, *hash_impulse, *hash_refractory;       /* [T][B] or all NULL */
+    int32_t step;             /* state["step"] AFTER the increment          */
+    int32_t hard;             /* hard channel on (cresso_v5.py:981-983)     */
+} cresso_spectral_desc;
+
+/* One optimizer step of one tensor on the spectral route. */
+int32_t cresso_spectral_step(const cresso_spectral_plan* plan, const cresso_spectral_desc* desc, void* workspace,
+                             size_t workspace_bytes, const cresso_hyper* hyper, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

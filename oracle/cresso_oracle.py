@@ -191,8 +191,16 @@ def hash_counts_np(n: int, bins: int, salt: int) -> np.ndarray:
     return np.bincount(hash_index_np(n, bins, salt), minlength=bins).astype(np.int64)
 
 
-def hash_reduce_mean(x: Tensor, idx: Tensor, bins: int) -> Tensor:
-    """Bin mean by sequential fp32 scatter_add (cresso_v5.py:519-526)."""
+def hash_reduce_mean(x: Tensor, idx: Tensor, bins: int, accum: str = "native") -> Tensor:
+    """Bin mean by sequential scatter_add in x's dtype (cresso_v5.py:519-526).
+
+    accum="fp64" accumulates in float64 and rounds the means to x's dtype: the
+    tie-breaker for tensors whose bins hold so many elements that the
+    reference's own fp32 accumulation error (~sqrt(count) ulp, 3.8e-5
+    relative at 262144 elements per bin) exceeds the parity tolerance.
+    """
+    if accum == "fp64" and x.dtype != torch.float64:
+        return hash_reduce_mean(x.double(), idx, bins).to(x.dtype)
     fi = idx.reshape(-1)
     fx = x.reshape(-1)
     total = torch.zeros(int(bins), dtype=x.dtype).scatter_add_(0, fi, fx)
@@ -419,10 +427,13 @@ class OracleCRESSO5:
     (cresso_v5.py:857-898).
     """
 
-    def __init__(self, params: Sequence[Tensor], **kwargs):
+    def __init__(self, params: Sequence[Tensor], hash_accum: str = "native", **kwargs):
+        """hash_accum: "native" (the reference's fp32 scatter_add, default) or
+        "fp64" (the tie-breaker described at hash_reduce_mean)."""
         unknown = set(kwargs) - set(DEFAULTS) - {"cuda_ops"}
         if unknown:
             raise TypeError(f"unknown hyperparameters {sorted(unknown)}")
+        self.hash_accum = hash_accum
         self.h = dict(DEFAULTS)
         self.h.update({k: v for k, v in kwargs.items() if k != "cuda_ops"})
         self.params = list(params)
@@ -548,7 +559,7 @@ class OracleCRESSO5:
             for t in range(tables):
                 idx = hash_index(shape, bins, t)
                 hash_idx.append(idx)
-                cell = hash_reduce_mean(dsrc, idx, bins)
+                cell = hash_reduce_mean(dsrc, idx, bins, self.hash_accum)
                 e_t = st["hash_energy"][t]
                 if step <= 1:
                     e_t.copy_(cell.to(e_t.dtype))
@@ -598,7 +609,7 @@ class OracleCRESSO5:
         if hash_idx is not None and "hash_impulse" in st:
             acc: Optional[Tensor] = None
             for t, idx in enumerate(hash_idx):
-                cp = hash_reduce_mean(psrc, idx, bins).to(st["hash_impulse"].dtype)
+                cp = hash_reduce_mean(psrc, idx, bins, self.hash_accum).to(st["hash_impulse"].dtype)
                 ref_t = st["hash_refractory"][t]
                 imp_t = st["hash_impulse"][t]
                 ref_t.mul_(float(h["hash_decay"])).add_(cp.abs(), alpha=1.0 - float(h["hash_decay"]))
