@@ -1,12 +1,15 @@
 """Benchmark of the CRESSO5 hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|copy] [--no-cpu]
 
 Workloads:
   c2: one fp32 (4096,4096) parameter, spectral/hash route, rank 8, F=5, B=64, T=2;
       grads N(0,1e-3) with 1% of entries x50, fresh per step.
   c3: 840 LoRA-thin fp32 matrices alternating (4096,16)/(16,4096), scalar route,
       rank 4; per-tensor scale 10^U(-4,-1) times N(0,1e-2).
+  copy: calibration only -- torch's device copy of a 256 MiB fp32 buffer, the
+      plain copy kernel of known size that scales rocprofv3's FETCH_SIZE and
+      WRITE_SIZE counters to bytes.
 Inputs are resident in HBM before the timed region; each step's grads are
 pre-generated on the device (a pool of 4 grad sets cycled through), so the
 timed region holds only optimizer.step().
@@ -111,6 +114,26 @@ def time_gpu(workload, steps, warmup):
                 shapes=shapes, kwargs=kwargs)
 
 
+def copy_calibration(steps, warmup, nbytes=256 << 20):
+    """Plain device copy of a known size, for scaling the HBM byte counters."""
+    device = torch.device("cuda:0")
+    src = torch.randn(nbytes // 4, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    return dict(read_bytes=nbytes, write_bytes=nbytes, ms_per_copy=round(ms, 4),
+                gb_s=round(2 * nbytes / (ms * 1e-3) / 1e9, 1))
+
+
 def time_cpu(workload, sample_steps=2):
     """CPU oracle (port of the reference's cuda_ops='off' path) on this host's cores."""
     from oracle.cresso_oracle import OracleCRESSO5
@@ -155,7 +178,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["c2", "c3"], default=None)
+    ap.add_argument("--workload", choices=["c2", "c3", "copy"], default=None)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -168,6 +191,9 @@ def main():
     except Exception:
         spectral_ready = False
     workload = args.workload or ("c2" if spectral_ready else "c3")
+    if workload == "copy":
+        print(json.dumps({"calibration": "device copy", **copy_calibration(args.steps, args.warmup)}))
+        return
     res = time_gpu(workload, args.steps, args.warmup)
     nbytes, n = algorithmic_bytes(res["shapes"])
     ms = res["ms_per_step"]

@@ -79,12 +79,17 @@ struct Geom {
     int32_t R, K, T, B;
     int32_t ndim, ntrail;
     int64_t tdim[8];  // dims of the column group, row-major
-    int32_t PR, slabs, panels, nblk;
+    int32_t PR, slabs, panels, nblk;   // tiles of the field sweeps
+    int32_t nblk1;                     // blocks of the flat force-RMS sweep
+    int32_t KA;                        // alpha row width: 2*rmax+1 carriers (zero beyond K) + constant
+    int32_t RW;                        // row-table width: 2*rmax (zero beyond 2R)
+    int64_t chunk1;                    // elements per block of the flat sweep (multiple of 4)
+    double hs_row, hs_col;             // fixed-point scales of the axis density sums
     int32_t binbytes, bpb, one_d, pad;
 };
 
 struct Offs {
-    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, counts, bins, tbuf, part, hist, lt, imp, rowpart, colpart,
+    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, counts, bins, tbuf, part, hist, lt, imp, alpha, rowfx, colfx,
         rowfac, colfac, terms, ctrl, total;
 };
 
@@ -187,9 +192,10 @@ __global__ void ws_rowtab_kernel(Geom g, const AxisConst* __restrict__ axc, cons
             const int64_t dim = g.rows;
             group_carrier(axc + (size_t)r * g.ndim, kind, 1, &coord, &dim, a1, a2);
         }
-        rowtab[i * 2 * g.R + 2 * r] = a1;
-        rowtab[i * 2 * g.R + 2 * r + 1] = a2;
+        rowtab[i * g.RW + 2 * r] = a1;
+        rowtab[i * g.RW + 2 * r + 1] = a2;
     }
+    for (int j = 2 * g.R; j < g.RW; ++j) rowtab[i * g.RW + j] = 0.f;
 }
 
 __global__ void ws_coltab_kernel(Geom g, const AxisConst* __restrict__ axc, const ModeMeta* __restrict__ meta,
@@ -248,7 +254,7 @@ __global__ __launch_bounds__(SP_FIN_NT) void ws_stats_kernel(Geom g, const ModeM
         // row sums of this mode
         double v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         for (int64_t i = tid; i < g.rows; i += SP_FIN_NT) {
-            const double a1 = rowtab[i * 2 * g.R + 2 * r], a2 = rowtab[i * 2 * g.R + 2 * r + 1];
+            const double a1 = rowtab[i * g.RW + 2 * r], a2 = rowtab[i * g.RW + 2 * r + 1];
             v[0] += a1; v[1] += a2; v[2] += a1 * a1; v[3] += a1 * a2; v[4] += a2 * a2;
             v[5] = fmax(v[5], fabs(a1)); v[6] = fmax(v[6], fabs(a2));
         }
@@ -337,6 +343,24 @@ __device__ __forceinline__ int bin_of(uint64_t packed, int t, int bpb) {
 // ---------------------------------------------------------------------------
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f(p[i]); }
 
+// 4 consecutive elements at e (e multiple of 4, base aligned to 4 elements)
+template <typename T> struct Ld4;
+template <> struct Ld4<float> {
+    __device__ static void go(const float* p, int64_t e, float* o) {
+        const float4 v = *reinterpret_cast<const float4*>(p + e);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+};
+template <typename T> struct Ld4h {
+    __device__ static void go(const T* p, int64_t e, float* o) {
+        const uint2 raw = *reinterpret_cast<const uint2*>(p + e);
+        const T* h = reinterpret_cast<const T*>(&raw);
+        o[0] = to_f(h[0]); o[1] = to_f(h[1]); o[2] = to_f(h[2]); o[3] = to_f(h[3]);
+    }
+};
+template <> struct Ld4<__half> : Ld4h<__half> {};
+template <> struct Ld4<__hip_bfloat16> : Ld4h<__hip_bfloat16> {};
+
 struct Tile {
     int slab, panel;
     int64_t col, r0, r1;
@@ -353,64 +377,70 @@ __device__ __forceinline__ Tile tile_of(const Geom& g) {
     return t;
 }
 
-// Block partials, one value at a time: wave sums in a fixed lane order into
-// LDS [wave][V], then a fixed-order sum over the block's waves written as
-// this block's partial (value-major layout part[v][block]).
+// Wave sum of a float in a fixed lane order with DPP (quad xor 1, 2; row
+// rotate 4, 8; row broadcasts 15, 31): the total lands in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                        0xF, false));
+}
+__device__ __forceinline__ float wave_total(float v) {
+    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x124, 0xF>(v);  // row_ror:4
+    v = dpp_add<0x128, 0xF>(v);  // row_ror:8
+    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
+    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
+    return v;                    // lane 63 holds the sum
+}
+
+// Block partials, one value at a time: DPP wave totals into LDS [wave][V],
+// then a fixed-order sum over the block's waves, written value-major
+// part[v][block].
 struct Partials {
-    double* lds;
+    float* lds;
     int V;
     __device__ __forceinline__ void add(int idx, float x) {
-        const double w = wave_sum((double)x);
-        if ((threadIdx.x & 63) == 0) lds[(threadIdx.x >> 6) * V + idx] = w;
+        const float w = wave_total(x);
+        if ((threadIdx.x & 63) == 63) lds[(threadIdx.x >> 6) * V + idx] = w;
     }
     __device__ __forceinline__ void flush(double* part, int nblk) {
         __syncthreads();
         for (int v = threadIdx.x; v < V; v += SP_NT) {
             double s = 0.0;
-            for (int w = 0; w < SP_NT / 64; ++w) s += lds[w * V + v];
+            for (int w = 0; w < SP_NT / 64; ++w) s += (double)lds[w * V + v];
             part[(size_t)v * nblk + blockIdx.x] = s;
         }
     }
 };
 
-// column carriers of this lane's column
+// Non-negative float (already scaled by a power of two, < 2^62) to a 64-bit
+// fixed-point integer, truncating: two exact 32-bit conversions.
+__device__ __forceinline__ unsigned long long to_fixed_u(float x) {
+    const float hf = floorf(x * 2.3283064365386963e-10f);  // x / 2^32 (exact scaling)
+    const float lf = fmaf(-hf, 4294967296.0f, x);           // x - hi*2^32: exact, in [0, 2^32)
+    return ((unsigned long long)(unsigned)hf << 32) | (unsigned long long)(unsigned)lf;
+}
+__device__ __forceinline__ unsigned long long to_fixed_s(float x) {
+    const unsigned long long u = to_fixed_u(fabsf(x));
+    return x < 0.f ? (0ull - u) : u;
+}
+
 template <int KM>
 __device__ __forceinline__ void load_cols(const Geom& g, const float* __restrict__ coltab, const Tile& t, float (&b)[KM]) {
 #pragma unroll
     for (int k = 0; k < KM; ++k) b[k] = (k < g.K && t.colok) ? coltab[(size_t)k * g.cols + t.col] : 0.f;
 }
 
-// alpha[row][0..K) + const for reconstruction `which` of the rows of this panel
-__device__ void build_alpha(const Geom& g, const Tile& t, const float* __restrict__ rowtab,
-                            const ModeMeta* __restrict__ meta, const Ctrl* __restrict__ ctrl, int which, float* s_alpha) {
-    const int stride = g.K + 1;
-    for (int lr = threadIdx.x; lr < g.PR; lr += SP_NT) {
-        const int64_t i = t.r0 + lr;
-        float* al = s_alpha + (size_t)lr * stride;
-        for (int k = 0; k < stride; ++k) al[k] = 0.f;
-        if (i >= t.r1) continue;
-        al[g.K] = ctrl->rconst[which];
-        for (int r = 0; r < g.R; ++r) {
-            const float wc = ctrl->rc[which][r][0], ws = ctrl->rc[which][r][1];
-            const float a1 = rowtab[i * 2 * g.R + 2 * r], a2 = rowtab[i * 2 * g.R + 2 * r + 1];
-            const ModeMeta m = meta[r];
-            if (m.type == M_ADD) {
-                al[m.k1] += wc * a1 + ws * a2;
-                if (m.k2 >= 0) al[m.k2] += ws * a1 - wc * a2;
-            } else {  // product and zero modes (zero: a1 = 1, a2 = 0, k1 = k2 = 0)
-                al[m.k1] += wc * a1;
-                if (m.k2 >= 0) al[m.k2] += ws * a2;
-            }
-        }
-    }
-}
-
+// reconstruction at (row, lane column): alpha row (wave-uniform) against the
+// lane's column carriers
+// (alpha rows are zero beyond the K live carriers and the lane's b is zero
+// there too, so the loop has no guards and the row loads vectorize)
 template <int KM>
-__device__ __forceinline__ float recon(const float* al, const float (&b)[KM], int K) {
-    float v = al[K];
+__device__ __forceinline__ float recon(const float* __restrict__ al, const float (&b)[KM]) {
+    float v = al[KM];
 #pragma unroll
-    for (int k = 0; k < KM; ++k)
-        if (k < K) v += al[k] * b[k];
+    for (int k = 0; k < KM; ++k) v += al[k] * b[k];
     return v;
 }
 
@@ -443,8 +473,10 @@ __device__ __forceinline__ void proj_finish(const Geom& g, const ModeMeta* __res
     }
 }
 
-template <typename W> __device__ __forceinline__ void shape3f(float t, float iclip, float clip, float clip2, float eps,
-                                                              float& rat, float& bnd, float& root) {
+// rat = t/(1+|t|/clip), bnd = clip*tanh(t/clip), root = sign(t)*sqrt(min(|t|,clip^2)+eps)
+// (cresso_v5.py:1321-1324); rat and bnd share one reciprocal.
+__device__ __forceinline__ void shape3f(float t, float iclip, float clip, float clip2, float eps, float& rat, float& bnd,
+                                        float& root) {
     const float at = fabsf(t);
     const float ex = fexp2(-2.8853900817779268f * at * iclip);
     const float d1 = 1.0f + ex;
@@ -456,57 +488,107 @@ template <typename W> __device__ __forceinline__ void shape3f(float t, float icl
     root = fsign(t) * fsqrt(fminf(at, clip2) + eps);
 }
 
-// ---------------------------------------------------------------------------
-// S1: sum f^2
-// ---------------------------------------------------------------------------
-template <typename PT, typename GT>
-__global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
-                                                       double* __restrict__ part, cresso_hyper h) {
-    __shared__ double red[4 * 1];
-    const Tile t = tile_of(g);
-    const float wd = (float)h.weight_decay;
-    const bool wd_on = h.weight_decay != 0.0;
-    const float sg = h.maximize ? -1.f : 1.f;
-    float a = 0.f;
-    if (t.colok) {
-        for (int64_t i = t.r0; i < t.r1; ++i) {
-            const int64_t e = i * g.cols + t.col;
-            float f = sg * ld(grad, e);
-            if (wd_on) f = f + wd * ld(param, e);
-            a += f * f;
-        }
-    }
-    Partials P{red, 1};
-    P.add(0, a);
-    P.flush(part, g.nblk);
-}
-
-// fixed-order reduction of partial value `v` over all blocks (every thread gets it)
-__device__ double reduce_part(const double* part, int nblk, int v, double* red) {
-    double s[1] = {0.0};
-    for (int b = threadIdx.x; b < nblk; b += SP_FIN_NT) s[0] += part[(size_t)v * nblk + b];
-    block_sum<1>(s, red);
-    return s[0];
-}
-
 __device__ __forceinline__ float reservoir_f(float old, float cur, double decay, int step) {
     if (step <= 1) return cur;
     return old * (float)decay + (float)(1.0 - decay) * cur;
 }
 
+// All partial values of a sweep reduced over blocks in a fixed order; result
+// in out[v] (LDS), visible after return.  Each value owns TPV consecutive
+// threads (TPV = largest power of two with V*TPV <= block size, at most 64):
+// thread j of value v sums blocks j, j+TPV, ... (the group's loads coalesce),
+// eight independent accumulators deep, and one thread per value adds the TPV
+// sums in order.  No cross-lane traffic; the loads of a thread are all in
+// flight together.
+__device__ void reduce_all(const double* __restrict__ part, int nblk, int V, double* out) {
+    __shared__ double s_seg[SP_FIN_NT];
+    const int tid = threadIdx.x;
+    int tpv = 64;
+    while (tpv > 1 && tpv * V > SP_FIN_NT) tpv >>= 1;
+    const int v = tid / tpv, j = tid % tpv;
+    if (v < V) {
+        const double* __restrict__ p = part + (size_t)v * nblk;
+        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0, a4 = 0.0, a5 = 0.0, a6 = 0.0, a7 = 0.0;
+        int b = j;
+        const int step = tpv;
+        for (; b + 7 * step < nblk; b += 8 * step) {
+            a0 += p[b];
+            a1 += p[b + step];
+            a2 += p[b + 2 * step];
+            a3 += p[b + 3 * step];
+            a4 += p[b + 4 * step];
+            a5 += p[b + 5 * step];
+            a6 += p[b + 6 * step];
+            a7 += p[b + 7 * step];
+        }
+        for (; b < nblk; b += step) a0 += p[b];
+        s_seg[tid] = ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7));
+    }
+    __syncthreads();
+    if (tid < V) {
+        double sum = 0.0;
+        for (int k = 0; k < tpv; ++k) sum += s_seg[tid * tpv + k];
+        out[tid] = sum;
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// S1: sum f^2 over contiguous chunks (float4 loads when aligned)
+// ---------------------------------------------------------------------------
+template <typename PT, typename GT, bool V4>
+__global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
+                                                       double* __restrict__ part, cresso_hyper h) {
+    __shared__ float red[4];
+    const float wd = (float)h.weight_decay;
+    const bool wd_on = h.weight_decay != 0.0;
+    const int64_t beg = (int64_t)blockIdx.x * g.chunk1;
+    const int64_t end = beg + g.chunk1 < g.n ? beg + g.chunk1 : g.n;
+    const float sg = h.maximize ? -1.f : 1.f;
+    float a = 0.f;
+    const int64_t vend = beg + ((end - beg) & ~(int64_t)3);
+    if (V4) {
+        for (int64_t e = beg + 4 * (int64_t)threadIdx.x; e < vend; e += 4 * SP_NT) {
+            float f[4];
+            Ld4<GT>::go(grad, e, f);
+            if (wd_on) {
+                float pv[4];
+                Ld4<PT>::go(param, e, pv);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) f[c] = sg * f[c] + wd * pv[c];
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a += f[c] * f[c];
+        }
+    }
+    // scalar elements: the < 4 tail of a vectorized chunk, or the whole chunk
+    for (int64_t i = (V4 ? vend : beg) + threadIdx.x; i < end; i += SP_NT) {
+        float f = sg * ld(grad, i);
+        if (wd_on) f = f + wd * ld(param, i);
+        a += f * f;
+    }
+    Partials P{red, 1};
+    P.add(0, a);
+    P.flush(part, g.nblk1);
+}
+
 __global__ __launch_bounds__(SP_FIN_NT) void fin1_kernel(Geom g, const double* __restrict__ part, SpecState st,
-                                                         Ctrl* __restrict__ ctrl, int step, cresso_hyper h) {
-    __shared__ double red[16];
-    const double ff = reduce_part(part, g.nblk, 0, red);
+                                                         Ctrl* __restrict__ ctrl, unsigned long long* __restrict__ rowfx,
+                                                         unsigned long long* __restrict__ colfx, int step, cresso_hyper h) {
+    __shared__ double red[1];
+    reduce_all(part, g.nblk1, 1, red);
+    // clear the axis density sums for this step's sweep 2
+    for (int64_t i = threadIdx.x; i < g.rows; i += SP_FIN_NT) rowfx[i] = 0ull;
+    for (int64_t i = threadIdx.x; i < g.cols; i += SP_FIN_NT) colfx[i] = 0ull;
     if (threadIdx.x == 0) {
         const float eps = (float)h.eps;
-        const float now = sqrtf((float)(ff / (double)g.n) + eps);
+        const float now = sqrtf((float)(red[0] / (double)g.n) + eps);
         const float fr = reservoir_f(*st.force_rms, now, h.reservoir_decay, step);
         *st.force_rms = fr;
         const float s = fmaxf(fr, eps);
         ctrl->scale = s;
         ctrl->inv_s = 1.0f / s;
-        // fixed-point scale of the density histogram: ds = rel^p <= (1e4)^p, n elements at most per bin
+        // density histogram scale: ds = rel^p <= (1e4)^p, at most n elements per bin
         const double dsmax = pow(1.0e4, h.energy_power) + 1.0;
         ctrl->hs_ds = ldexp(1.0, (int)floor(62.0 - log2(dsmax * (double)g.n)));
     }
@@ -521,22 +603,18 @@ __global__ __launch_bounds__(SP_NT) void sweep2_kernel(Geom g, const GT* __restr
                                                        const ModeMeta* __restrict__ meta,
                                                        const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
                                                        double* __restrict__ part, unsigned long long* __restrict__ hist,
-                                                       float* __restrict__ rowpart, float* __restrict__ colpart,
-                                                       int hash_on, cresso_hyper h) {
+                                                       unsigned long long* __restrict__ rowfx,
+                                                       unsigned long long* __restrict__ colfx, int hash_on, int axes_on,
+                                                       cresso_hyper h) {
     extern __shared__ __align__(16) unsigned char dyn[];
-    __shared__ double red[4 * NV2];
+    __shared__ float red[4 * NV2];
     const Tile t = tile_of(g);
-    // LDS: histogram [T][B] u64, row carriers [PR][2R], wave row sums [4][PR]
+    // LDS: histogram [T][B] u64, wave row sums [4][PR]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
-    float* s_rows = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)g.T * g.B);
-    float* s_wrow = s_rows + (size_t)g.PR * 2 * g.R;
+    float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)g.T * g.B);
     const int TB = g.T * g.B;
     if (hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_hist[i] = 0ull;
-    for (int i = threadIdx.x; i < g.PR * 2 * g.R; i += SP_NT) {
-        const int64_t row = t.r0 + i / (2 * g.R);
-        s_rows[i] = row < t.r1 ? rowtab[row * 2 * g.R + i % (2 * g.R)] : 0.f;
-    }
     __syncthreads();
     float b[KM];
     load_cols<KM>(g, coltab, t, b);
@@ -548,7 +626,7 @@ __global__ __launch_bounds__(SP_NT) void sweep2_kernel(Geom g, const GT* __restr
     const float wd = (float)h.weight_decay;
     const bool wd_on = h.weight_decay != 0.0;
     const float sg = h.maximize ? -1.f : 1.f;
-    const double hs = ctrl->hs_ds;
+    const float hs = (float)ctrl->hs_ds;
     float Z1[RM], Z2[RM];
 #pragma unroll
     for (int r = 0; r < RM; ++r) Z1[r] = Z2[r] = 0.f;
@@ -556,13 +634,13 @@ __global__ __launch_bounds__(SP_NT) void sweep2_kernel(Geom g, const GT* __restr
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int64_t i = t.r0; i < t.r1; ++i) {
         const int lr = (int)(i - t.r0);
+        const float* __restrict__ ar = rowtab + i * g.RW;
         float dens = 0.f;
         if (t.colok) {
             const int64_t e = i * g.cols + t.col;
             float f = sg * ld(grad, e);
             if (wd_on) f = f + wd * ld(param, e);
-            const float r = fabsf(f) * inv_s + eps;
-            const float rel = fminf(r, 1.0e4f);
+            const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
             const float ds = fpow(rel, pw);
             const float L = flog1p(ds);
             const float rl = fmaxf(rel, eps);
@@ -570,30 +648,32 @@ __global__ __launch_bounds__(SP_NT) void sweep2_kernel(Geom g, const GT* __restr
             aL += L;
             aD += dens;
             colsum += dens;
-            const float* ar = s_rows + (size_t)lr * 2 * g.R;
 #pragma unroll
-            for (int q = 0; q < RM; ++q)
-                if (q < g.R) {
-                    Z1[q] += ar[2 * q] * L;
-                    Z2[q] += ar[2 * q + 1] * L;
-                }
+            for (int q = 0; q < RM; ++q) {
+                Z1[q] += ar[2 * q] * L;
+                Z2[q] += ar[2 * q + 1] * L;
+            }
             if (hash_on) {
                 const uint64_t pk = load_bins(bins, e, g.binbytes);
-                const unsigned long long v = (unsigned long long)llrint((double)ds * hs);
+                const unsigned long long v = to_fixed_u(ds * hs);
                 for (int tt = 0; tt < g.T; ++tt) atomicAdd(&s_hist[tt * g.B + bin_of(pk, tt, g.bpb)], v);
             }
         }
-        const float ws = wave_sum(dens);
-        if (lane == 0) s_wrow[wave * g.PR + lr] = ws;
+        if (axes_on) {
+            const float ws = wave_total(dens);
+            if (lane == 63) s_wrow[wave * g.PR + lr] = ws;
+        }
     }
     __syncthreads();
-    // row partials of this slab, column partials of this panel
-    for (int lr = threadIdx.x; lr < (int)(t.r1 - t.r0); lr += SP_NT) {
-        float s = 0.f;
-        for (int w = 0; w < SP_NT / 64; ++w) s += s_wrow[w * g.PR + lr];
-        rowpart[(size_t)t.slab * g.rows + t.r0 + lr] = s;
+    if (axes_on) {
+        // axis density sums: one fixed-point atomic per row of this slab and per column of this panel
+        for (int lr = threadIdx.x; lr < (int)(t.r1 - t.r0); lr += SP_NT) {
+            float s = 0.f;
+            for (int w = 0; w < SP_NT / 64; ++w) s += s_wrow[w * g.PR + lr];
+            atomicAdd(&rowfx[t.r0 + lr], to_fixed_u(s * (float)g.hs_row));
+        }
+        if (t.colok) atomicAdd(&colfx[t.col], to_fixed_u(colsum * (float)g.hs_col));
     }
-    if (t.colok) colpart[(size_t)t.panel * g.cols + t.col] = colsum;
     if (hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT)
             if (s_hist[i]) atomicAdd(&hist[i], s_hist[i]);
@@ -607,9 +687,11 @@ __global__ __launch_bounds__(SP_NT) void sweep2_kernel(Geom g, const GT* __restr
 // ---------------------------------------------------------------------------
 // F2: hash metric, metric oscillator, recon coefficients
 // ---------------------------------------------------------------------------
-__device__ void set_recon(const Geom& g, const ModeMeta* meta, const double* stats, Ctrl* ctrl, int which,
-                          const float* cc, const float* sc, const float* gates) {
-    // shrink * g_r * (cc_r Cn_r + sc_r Sn_r) summed over modes (cresso_v5.py:362-376)
+// Coefficients (wc, ws) per mode and the constant of
+//   shrink * sum_r g_r (cc_r Cn_r + sc_r Sn_r)  (cresso_v5.py:362-376)
+// with Cn = (Craw - mu_c) ic; a gate of exactly 0 drops the mode.
+__device__ void set_recon(const Geom& g, const double* stats, float (*rc)[2], float& rconst, const float* cc,
+                          const float* sc, const float* gates) {
     const double shrink = 1.0 / sqrt(fmax(1.0, 0.7 * log2((double)g.R + 1.0)));
     float cst = 0.f;
     for (int r = 0; r < g.R; ++r) {
@@ -622,41 +704,59 @@ __device__ void set_recon(const Geom& g, const ModeMeta* meta, const double* sta
             ws = (float)((double)ks * stats[4 * r + 3]);
             cst -= (float)((double)wc * stats[4 * r + 0] + (double)ws * stats[4 * r + 2]);
         }
-        ctrl->rc[which][r][0] = wc;
-        ctrl->rc[which][r][1] = ws;
+        rc[r][0] = wc;
+        rc[r][1] = ws;
     }
-    ctrl->rconst[which] = cst;
+    rconst = cst;
+}
+
+// alpha[row][k] = sum of the coefficients of reconstruction `w` that multiply
+// column carrier k at this row (zero for k >= K), alpha[row][KM] = constant.
+// One thread per row; reconstructions w0 .. w0+count-1.
+template <int RM>
+__global__ void alpha_kernel(Geom g, const ModeMeta* __restrict__ meta, const float* __restrict__ rowtab,
+                             const Ctrl* __restrict__ ctrl, int w0, int count, float* __restrict__ alpha) {
+    constexpr int KM = 2 * RM + 1;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= g.rows) return;
+    for (int w = w0; w < w0 + count; ++w) {
+        float al[KM + 1];
+#pragma unroll
+        for (int k = 0; k < KM; ++k) al[k] = 0.f;
+        al[KM] = ctrl->rconst[w];
+        for (int r = 0; r < g.R; ++r) {
+            const ModeMeta m = meta[r];
+            const float wc = ctrl->rc[w][r][0], ws = ctrl->rc[w][r][1];
+            const float a1 = rowtab[i * g.RW + 2 * r], a2 = rowtab[i * g.RW + 2 * r + 1];
+            // additive: C = a1 b1 - a2 b2, S = a2 b1 + a1 b2; product/constant: C = a1 b1, S = a2 b2
+            const float c1 = m.type == M_ADD ? wc * a1 + ws * a2 : wc * a1;
+            const float c2 = m.type == M_ADD ? ws * a1 - wc * a2 : ws * a2;
+#pragma unroll
+            for (int k = 0; k < KM; ++k) al[k] += (k == m.k1 ? c1 : 0.f) + (k == m.k2 ? c2 : 0.f);
+        }
+        float* dst = alpha + ((size_t)w * g.rows + i) * g.KA;
+#pragma unroll
+        for (int k = 0; k <= KM; ++k) dst[k] = al[k];
+    }
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 __global__ __launch_bounds__(SP_FIN_NT) void fin2_kernel(Geom g, const ModeMeta* __restrict__ meta,
                                                          const double* __restrict__ stats, const double* __restrict__ bounds,
-                                                         const double* __restrict__ part,
+                                                         const float* __restrict__ rowtab, const double* __restrict__ part,
                                                          unsigned long long* __restrict__ hist,
                                                          const unsigned long long* __restrict__ counts,
-                                                         float* __restrict__ lt, SpecState st, Ctrl* __restrict__ ctrl,
-                                                         int step, int hash_on, int hard, cresso_hyper h) {
+                                                         float* __restrict__ lt, float* __restrict__ alpha, SpecState st,
+                                                         Ctrl* __restrict__ ctrl, int step, int hash_on, int hard,
+                                                         cresso_hyper h) {
+    __shared__ double s_v[NV2];
     __shared__ double red[16];
-    __shared__ float s_port[2 * SP_MAXR];
     __shared__ float s_emean[SP_MAXT];
     const int tid = threadIdx.x;
     const float eps = (float)h.eps;
     const double n = (double)g.n;
-    const double sumL = reduce_part(part, g.nblk, 0, red);
-    const double sumD = reduce_part(part, g.nblk, 1, red);
-    for (int v = 0; v < 2 * g.R; ++v) {
-        const double x = reduce_part(part, g.nblk, 2 + v, red);
-        if (tid == 0) {
-            const int r = v / 2;
-            const double mu = stats[4 * r + 2 * (v & 1)], inv = stats[4 * r + 2 * (v & 1) + 1];
-            // d = L / max(mean L, eps) - 1; mean(d * Cn) = mean(L Cn)/m - mean(Cn)
-            const double m = fmax((double)(float)(sumL / n), (double)eps);
-            double pr = (x - mu * sumL) * inv / n / m;
-            if (meta[r].type == M_ZERO && (v & 1) == 0) pr -= 1.0;  // mean(Cn) = 1 for the constant mode
-            s_port[v] = (float)pr;
-        }
-    }
+    reduce_all(part, g.nblk, 2 + 2 * g.R, s_v);
     // hash energy per table (cresso_v5.py:1012-1056)
     if (hash_on) {
         const int TB = g.T * g.B;
@@ -680,121 +780,146 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin2_kernel(Geom g, const ModeMeta*
         for (int i = tid; i < TB; i += SP_FIN_NT) {
             const int tt = i / g.B;
             const float hm = fmaxf(st.hash_energy[i] / fmaxf(s_emean[tt], eps), eps);
-            const float hp = powf(hm, ex);
-            lt[i] = logf(fmaxf(clampf(hp, 0.08f, 12.0f), eps));
+            lt[i] = logf(fmaxf(clampf(powf(hm, ex), 0.08f, 12.0f), eps));
         }
+    }
+    // per-mode state staged in LDS by parallel threads; the recurrences run
+    // on one thread over LDS, results written back in parallel
+    __shared__ double s_st[SP_MAXR][6];
+    __shared__ float s_f[SP_MAXR][8];
+    __shared__ int s_type[SP_MAXR];
+    if (tid < g.R) {
+        const int r = tid;
+        for (int j = 0; j < 4; ++j) s_st[r][j] = stats[4 * r + j];
+        s_st[r][4] = bounds[2 * r];
+        s_st[r][5] = bounds[2 * r + 1];
+        s_f[r][0] = st.omega[r];
+        s_f[r][1] = st.metric_cos[r];
+        s_f[r][2] = st.metric_p_cos[r];
+        s_f[r][3] = st.metric_sin[r];
+        s_f[r][4] = st.metric_p_sin[r];
+        s_f[r][5] = st.q_cos[r];
+        s_f[r][6] = st.q_sin[r];
+        s_f[r][7] = st.conf[r];
+        s_type[r] = meta[r].type;
     }
     __syncthreads();
     if (tid == 0) {
+        // log-density projections: d = L/max(mean L, eps) - 1, mean(d Cn) = mean(L Cn)/m - mean(Cn)
+        const double sumL = s_v[0], sumD = s_v[1];
+        const double m = fmax((double)(float)(sumL / n), (double)eps);
+        double stt[4 * SP_MAXR];
+        for (int r = 0; r < g.R; ++r)
+            for (int j = 0; j < 4; ++j) stt[4 * r + j] = s_st[r][j];
+        float port[2 * SP_MAXR];
+        for (int v = 0; v < 2 * g.R; ++v) {
+            const int r = v / 2;
+            const double mu = s_st[r][2 * (v & 1)], inv = s_st[r][2 * (v & 1) + 1];
+            double pr = (s_v[2 + v] - mu * sumL) * inv / n / m;
+            if (s_type[r] == M_ZERO && (v & 1) == 0) pr -= 1.0;  // mean(Cn) = 1 for the constant mode
+            port[v] = (float)pr;
+        }
         // metric oscillator (cresso_v5.py:1064-1088)
         const float mdt = (float)h.metric_dt;
         const float damp = (float)fmax(0.0, 1.0 - h.metric_dt * h.metric_friction);
         float mcs[SP_MAXR], mss[SP_MAXR];
         for (int r = 0; r < g.R; ++r) {
-            const float om = st.omega[r];
+            const float om = s_f[r][0];
             const float o2 = om * om;
-            float mq = st.metric_cos[r], mp = st.metric_p_cos[r];
+            float mq = s_f[r][1], mp = s_f[r][2];
             mp = mp * damp;
-            mp = mp + mdt * (s_port[2 * r] - o2 * mq);
+            mp = mp + mdt * (port[2 * r] - o2 * mq);
             mq = clampf(mq + mdt * mp, -3.0f, 3.0f);
-            st.metric_cos[r] = mq; st.metric_p_cos[r] = mp; mcs[r] = mq;
-            mq = st.metric_sin[r]; mp = st.metric_p_sin[r];
+            s_f[r][1] = mq; s_f[r][2] = mp; mcs[r] = mq;
+            mq = s_f[r][3]; mp = s_f[r][4];
             mp = mp * damp;
-            mp = mp + mdt * (s_port[2 * r + 1] - o2 * mq);
+            mp = mp + mdt * (port[2 * r + 1] - o2 * mq);
             mq = clampf(mq + mdt * mp, -3.0f, 3.0f);
-            st.metric_sin[r] = mq; st.metric_p_sin[r] = mp; mss[r] = mq;
+            s_f[r][3] = mq; s_f[r][4] = mp; mss[r] = mq;
         }
-        set_recon(g, meta, stats, ctrl, 0, mcs, mss, nullptr);
+        set_recon(g, stt, ctrl->rc[0], ctrl->rconst[0], mcs, mss, nullptr);
         // prediction with the pre-contact state and gates
         float qc[SP_MAXR], qs[SP_MAXR], gt[SP_MAXR];
         double pmax = 0.0;
         const double shrink = 1.0 / sqrt(fmax(1.0, 0.7 * log2((double)g.R + 1.0)));
         for (int r = 0; r < g.R; ++r) {
-            qc[r] = st.q_cos[r];
-            qs[r] = st.q_sin[r];
-            gt[r] = sigmoidf_((float)h.confidence_gain * st.conf[r]);
-            pmax += shrink * gt[r] * (fabs((double)qc[r]) * bounds[2 * r] + fabs((double)qs[r]) * bounds[2 * r + 1]);
+            qc[r] = s_f[r][5];
+            qs[r] = s_f[r][6];
+            gt[r] = sigmoidf_((float)h.confidence_gain * s_f[r][7]);
+            pmax += shrink * gt[r] * (fabs((double)qc[r]) * s_st[r][4] + fabs((double)qs[r]) * s_st[r][5]);
         }
-        set_recon(g, meta, stats, ctrl, 1, qc, qs, gt);
+        set_recon(g, stt, ctrl->rc[1], ctrl->rconst[1], qc, qs, gt);
         // instant metric: mean density and coupling (cresso_v5.py:243-262)
-        const double gm = sumD / n;
-        ctrl->gden = (float)fmax(gm, (double)eps);
+        ctrl->gden = (float)fmax(sumD / n, (double)eps);
         const float icoup = hard ? (float)h.instant_metric_coupling : 0.0f;
         ctrl->kappa = (float)((double)icoup / ((double)g.ndim * fmax(h.instant_metric_power, 0.25)));
-        // fixed-point scale of the port histogram: |P| <= (1+tm)*1e4 + max|pred|
+        // fixed-point scale of the port histogram: |P| <= (1+tm)*1e4 + max|pred|, <= n elements per bin
         const double vmax = (1.0 + h.transport_mix) * 1.0e4 + pmax * 1.01 + 1.0;
-        double cmax = 1.0;
-        if (hash_on)
-            for (int i = 0; i < g.T * g.B; ++i) cmax = fmax(cmax, (double)counts[i]);
-        ctrl->hs_P = ldexp(1.0, (int)floor(62.0 - log2(vmax * cmax)));
+        ctrl->hs_P = ldexp(1.0, (int)floor(62.0 - log2(vmax * (double)g.n)));
+    }
+    __syncthreads();
+    if (tid < g.R) {
+        const int r = tid;
+        st.metric_cos[r] = s_f[r][1];
+        st.metric_p_cos[r] = s_f[r][2];
+        st.metric_sin[r] = s_f[r][3];
+        st.metric_p_sin[r] = s_f[r][4];
     }
 }
 
-// M1: instant-metric factors per row and per column (and axis terms for
-// ndim >= 3 column groups).  One block per 256 rows/cols.
-__global__ void marg_kernel(Geom g, const float* __restrict__ rowpart, const float* __restrict__ colpart,
-                            float* __restrict__ terms) {
+// M1: instant-metric factors (cresso_v5.py:243-262) from the fixed-point axis
+// density sums: rows always; columns directly for 2-D tensors.
+__global__ void marg_kernel(Geom g, const unsigned long long* __restrict__ rowfx,
+                            const unsigned long long* __restrict__ colfx, float* __restrict__ rowfac,
+                            float* __restrict__ colfac, const Ctrl* __restrict__ ctrl, float eps) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    {
-        // row and column density sums in fixed order
-        if (i < g.rows) {
-            float s = 0.f;
-            for (int sl = 0; sl < g.slabs; ++sl) s += rowpart[(size_t)sl * g.rows + i];
-            terms[i] = s;
-        } else if (i < g.rows + g.cols) {
-            const int64_t c = i - g.rows;
-            float s = 0.f;
-            for (int p = 0; p < g.panels; ++p) s += colpart[(size_t)p * g.cols + c];
-            terms[i] = s;
-        }
+    const float gden = ctrl->gden, kappa = ctrl->kappa;
+    if (i < g.rows) {
+        const float mean = (float)((double)rowfx[i] / g.hs_row / (double)g.cols);
+        rowfac[i] = expf(kappa * logf(fmaxf(mean / gden, eps)));
+    } else if (g.ntrail == 1 && i < g.rows + g.cols) {
+        const int64_t c = i - g.rows;
+        const float mean = (float)((double)colfx[c] / g.hs_col / (double)g.rows);
+        colfac[c] = expf(kappa * logf(fmaxf(mean / gden, eps)));
     }
 }
 
-__global__ __launch_bounds__(SP_FIN_NT) void marg_axes_kernel(Geom g, float* __restrict__ terms, float* __restrict__ rowfac,
-                                                              float* __restrict__ colfac, const Ctrl* __restrict__ ctrl,
-                                                              float eps) {
-    // terms[0..rows) = row sums, terms[rows..rows+cols) = column sums.  Axis
-    // marginal means (cresso_v5.py:253-259): axis 0 from rows, the column
-    // group's axes by summing the column sums that share a coordinate.
-    float* axis_terms = terms + g.rows + g.cols;   // [sum of trailing dims]
+// ndim >= 3: axis terms of the column group by summing the column sums that
+// share a coordinate (fixed order), then the per-column factor.
+__global__ __launch_bounds__(SP_FIN_NT) void marg_axes_kernel(Geom g, const unsigned long long* __restrict__ colfx,
+                                                              float* __restrict__ terms, float* __restrict__ colfac,
+                                                              const Ctrl* __restrict__ ctrl, float eps) {
     const float gden = ctrl->gden, kappa = ctrl->kappa;
     const double n = (double)g.n;
-    // trailing axes (ndim >= 3): fixed-order sums over the other trailing coords
     int64_t off = 0;
-    for (int a = 0; a < g.ntrail && !g.one_d; ++a) {
+    for (int a = 0; a < g.ntrail; ++a) {
         int64_t inner = 1;
         for (int b = a + 1; b < g.ntrail; ++b) inner *= g.tdim[b];
         const int64_t dim = g.tdim[a];
         const int64_t outer = g.cols / (dim * inner);
         for (int64_t k = threadIdx.x; k < dim; k += SP_FIN_NT) {
-            float s = 0.f;
+            double s = 0.0;
             for (int64_t o = 0; o < outer; ++o)
-                for (int64_t in = 0; in < inner; ++in) s += terms[g.rows + (o * dim + k) * inner + in];
-            const float mean = (float)((double)s / (n / (double)dim));
-            axis_terms[off + k] = kappa * logf(fmaxf(mean / gden, eps));
+                for (int64_t in = 0; in < inner; ++in) s += (double)colfx[(o * dim + k) * inner + in];
+            const float mean = (float)(s / g.hs_col / (n / (double)dim));
+            terms[off + k] = kappa * logf(fmaxf(mean / gden, eps));
         }
         off += dim;
     }
     __syncthreads();
-    if (!g.one_d) {
-        for (int64_t i = threadIdx.x; i < g.rows; i += SP_FIN_NT) {
-            const float mean = (float)((double)terms[i] / (double)g.cols);
-            rowfac[i] = expf(kappa * logf(fmaxf(mean / gden, eps)));
+    for (int64_t c = threadIdx.x; c < g.cols; c += SP_FIN_NT) {
+        float ls = 0.f;
+        int64_t rem = c, o2 = 0;
+        int64_t coord[8];
+        for (int a = g.ntrail - 1; a >= 0; --a) {
+            coord[a] = rem % g.tdim[a];
+            rem /= g.tdim[a];
         }
-        for (int64_t c = threadIdx.x; c < g.cols; c += SP_FIN_NT) {
-            float ls = 0.f;
-            int64_t rem = c, o2 = 0;
-            int64_t coord[8];
-            for (int a = g.ntrail - 1; a >= 0; --a) {
-                coord[a] = rem % g.tdim[a];
-                rem /= g.tdim[a];
-            }
-            for (int a = 0; a < g.ntrail; ++a) {
-                ls += axis_terms[o2 + coord[a]];
-                o2 += g.tdim[a];
-            }
-            colfac[c] = expf(ls);
+        for (int a = 0; a < g.ntrail; ++a) {
+            ls += terms[o2 + coord[a]];
+            o2 += g.tdim[a];
         }
+        colfac[c] = expf(ls);
     }
 }
 
@@ -806,31 +931,22 @@ __global__ __launch_bounds__(SP_NT) void sweep3_kernel(Geom g, const GT* __restr
                                                        const float* __restrict__ rowtab, const float* __restrict__ coltab,
                                                        const ModeMeta* __restrict__ meta,
                                                        const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
-                                                       const float* __restrict__ lt, const float* __restrict__ rowfac,
-                                                       const float* __restrict__ colfac, float* __restrict__ tbuf,
-                                                       double* __restrict__ part, unsigned long long* __restrict__ hist,
-                                                       int hash_on, int echo_on, cresso_hyper h) {
+                                                       const float* __restrict__ lt, const float* __restrict__ alpha,
+                                                       const float* __restrict__ rowfac, const float* __restrict__ colfac,
+                                                       float* __restrict__ tbuf, double* __restrict__ part,
+                                                       unsigned long long* __restrict__ hist, int hash_on, int echo_on,
+                                                       cresso_hyper h) {
     extern __shared__ __align__(16) unsigned char dyn[];
-    __shared__ double red[4 * NV3];
+    __shared__ float red[4 * NV3];
     const Tile t = tile_of(g);
     const int TB = g.T * g.B;
-    const int st_al = g.K + 1;
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
     float* s_lt = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
-    float* s_rows = s_lt + TB;
-    float* s_aM = s_rows + (size_t)g.PR * 2 * g.R;
-    float* s_aP = s_aM + (size_t)g.PR * st_al;
     if (hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) {
             s_hist[i] = 0ull;
             s_lt[i] = lt[i];
         }
-    for (int i = threadIdx.x; i < g.PR * 2 * g.R; i += SP_NT) {
-        const int64_t row = t.r0 + i / (2 * g.R);
-        s_rows[i] = row < t.r1 ? rowtab[row * 2 * g.R + i % (2 * g.R)] : 0.f;
-    }
-    build_alpha(g, t, rowtab, meta, ctrl, 0, s_aM);
-    build_alpha(g, t, rowtab, meta, ctrl, 1, s_aP);
     __syncthreads();
     float b[KM];
     load_cols<KM>(g, coltab, t, b);
@@ -848,8 +964,10 @@ __global__ __launch_bounds__(SP_NT) void sweep3_kernel(Geom g, const GT* __restr
     const float ec = inst_on && !g.one_d && t.colok ? colfac[t.col] : 1.0f;
     const float invT = 1.0f / (float)g.T;
     const float tm = (float)h.transport_mix;
-    const double hs = ctrl->hs_P;
+    const float hs = (float)ctrl->hs_P;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
+    const float* __restrict__ alM = alpha;
+    const float* __restrict__ alP = alpha + (size_t)g.rows * g.KA;
     float ZP1[RM], ZP2[RM], ZT1[RM], ZT2[RM];
 #pragma unroll
     for (int r = 0; r < RM; ++r) ZP1[r] = ZP2[r] = ZT1[r] = ZT2[r] = 0.f;
@@ -857,12 +975,11 @@ __global__ __launch_bounds__(SP_NT) void sweep3_kernel(Geom g, const GT* __restr
           m_bo = 0.f, m_tr = 0.f, m_tb = 0.f, m_to = 0.f;
     if (t.colok) {
         for (int64_t i = t.r0; i < t.r1; ++i) {
-            const int lr = (int)(i - t.r0);
             const int64_t e = i * g.cols + t.col;
             float f = sg * ld(grad, e);
             if (wd_on) f = f + wd * ld(param, e);
             // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
-            const float lm = clampf(recon<KM>(s_aM + (size_t)lr * st_al, b, g.K), -3.0f, 3.0f);
+            const float lm = clampf(recon<KM>(alM + i * g.KA, b), -3.0f, 3.0f);
             const float M = clampf(fexp(mcoup * lm), 0.06f, 16.0f);
             float den = scale * M;
             if (ls_on) {
@@ -889,7 +1006,7 @@ __global__ __launch_bounds__(SP_NT) void sweep3_kernel(Geom g, const GT* __restr
             }
             const float tv = clampf(f * frcp(den + eps), -1.0e4f, 1.0e4f);
             tbuf[e] = tv;
-            const float pred = recon<KM>(s_aP + (size_t)lr * st_al, b, g.K);
+            const float pred = recon<KM>(alP + i * g.KA, b);
             const float err = tv - pred;
             const float P = err + tm * tv;
             m_ee += err * err;
@@ -897,23 +1014,25 @@ __global__ __launch_bounds__(SP_NT) void sweep3_kernel(Geom g, const GT* __restr
             m_t += tv;
             m_tt += tv * tv;
             float rat, bnd, root;
-            shape3f<float>(tv, iclip, clip, clip2, eps, rat, bnd, root);
+            shape3f(tv, iclip, clip, clip2, eps, rat, bnd, root);
             m_rr += rat * rat; m_bb += bnd * bnd; m_oo += root * root;
             m_rb += rat * bnd; m_ro += rat * root; m_bo += bnd * root;
             m_tr += tv * rat; m_tb += tv * bnd; m_to += tv * root;
-            const float* ar = s_rows + (size_t)lr * 2 * g.R;
+            const float* __restrict__ ar = rowtab + i * g.RW;
 #pragma unroll
-            for (int q = 0; q < RM; ++q)
-                if (q < g.R) {
-                    ZP1[q] += ar[2 * q] * P;
-                    ZP2[q] += ar[2 * q + 1] * P;
-                    if (echo_on) {
-                        ZT1[q] += ar[2 * q] * tv;
-                        ZT2[q] += ar[2 * q + 1] * tv;
-                    }
+            for (int q = 0; q < RM; ++q) {
+                ZP1[q] += ar[2 * q] * P;
+                ZP2[q] += ar[2 * q + 1] * P;
+            }
+            if (echo_on) {
+#pragma unroll
+                for (int q = 0; q < RM; ++q) {
+                    ZT1[q] += ar[2 * q] * tv;
+                    ZT2[q] += ar[2 * q + 1] * tv;
                 }
+            }
             if (hash_on) {
-                const unsigned long long v = (unsigned long long)llrint((double)P * hs);
+                const unsigned long long v = to_fixed_s(P * hs);
                 for (int tt = 0; tt < g.T; ++tt) atomicAdd(&s_hist[tt * g.B + bin_of(pk, tt, g.bpb)], v);
             }
         }
@@ -971,21 +1090,18 @@ __device__ void contact_bank(float* q, float* p, const float* port, const float*
 }
 
 __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                         const double* __restrict__ stats, const double* __restrict__ part,
+                                                         const double* __restrict__ stats, const float* __restrict__ rowtab,
+                                                         const double* __restrict__ part,
                                                          unsigned long long* __restrict__ hist,
                                                          const unsigned long long* __restrict__ counts,
-                                                         float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
-                                                         int step, int hash_on, int hard, int echo_on, cresso_hyper h,
+                                                         float* __restrict__ imp_tab, float* __restrict__ alpha,
+                                                         SpecState st, Ctrl* __restrict__ ctrl, int step, int hash_on,
+                                                         int hard, int echo_on, cresso_hyper h,
                                                          double* __restrict__ moments) {
-    __shared__ double red[16];
-    __shared__ double s_m[15 + 4 * SP_MAXR];
+    __shared__ double s_m[NV3];
     const int tid = threadIdx.x;
     const double n = (double)g.n;
-    for (int v = 0; v < 15 + 4 * g.R; ++v) {
-        const double x = reduce_part(part, g.nblk, v, red);
-        if (tid == 0) s_m[v] = x;
-    }
-    __syncthreads();
+    reduce_all(part, g.nblk, 15 + 4 * g.R, s_m);
     const float eps = (float)h.eps;
     // hash refractory / impulse (cresso_v5.py:1140-1184)
     if (hash_on) {
@@ -994,50 +1110,77 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta*
             const double cnt = fmax((double)counts[i], 1.0);
             const float cp = (float)((double)(long long)hist[i] / ctrl->hs_P / cnt);
             hist[i] = 0ull;
-            float ref = st.hash_refractory[i] * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * fabsf(cp);
+            const float ref = st.hash_refractory[i] * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * fabsf(cp);
             const float gate = 1.0f / (1.0f + (float)h.refractory_gain * ref);
-            float im = st.hash_impulse[i] * (float)h.hash_impulse_decay + (float)(1.0 - h.hash_impulse_decay) * (cp * gate);
+            const float im = st.hash_impulse[i] * (float)h.hash_impulse_decay + (float)(1.0 - h.hash_impulse_decay) * (cp * gate);
             st.hash_refractory[i] = ref;
             st.hash_impulse[i] = im;
             imp_tab[i] = im;
         }
     }
+    __shared__ double s_st[SP_MAXR][4];
+    __shared__ float s_f[SP_MAXR][9];
+    __shared__ float s_sc[2];
+    if (tid < g.R) {
+        const int r = tid;
+        for (int j = 0; j < 4; ++j) s_st[r][j] = stats[4 * r + j];
+        s_f[r][0] = st.omega[r];
+        s_f[r][1] = st.q_cos[r];
+        s_f[r][2] = st.q_sin[r];
+        s_f[r][3] = st.p_cos[r];
+        s_f[r][4] = st.p_sin[r];
+        s_f[r][5] = st.calcium_cos[r];
+        s_f[r][6] = st.calcium_sin[r];
+        s_f[r][7] = st.conf[r];
+    }
+    if (tid == 0) {
+        s_sc[0] = *st.surprise;
+        s_sc[1] = *st.action;
+    }
+    __syncthreads();
     if (tid == 0) {
         const double sP = s_m[1], sT = s_m[2];
         // surprise reservoir (cresso_v5.py:1127-1129)
-        float sur = reservoir_f(*st.surprise, sqrtf((float)(s_m[0] / n) + eps), h.surprise_decay, step);
-        *st.surprise = sur;
+        const float sur = reservoir_f(s_sc[0], sqrtf((float)(s_m[0] / n) + eps), h.surprise_decay, step);
+        s_sc[0] = sur;
+        double stt[4 * SP_MAXR];
+        for (int r = 0; r < g.R; ++r)
+            for (int j = 0; j < 4; ++j) stt[4 * r + j] = s_st[r][j];
         // port and echo projections -> mean(x Cn)
         float pc[SP_MAXR], ps[SP_MAXR], ecs[SP_MAXR], ess[SP_MAXR];
         for (int r = 0; r < g.R; ++r) {
-            const double mc = stats[4 * r], ic = stats[4 * r + 1], ms = stats[4 * r + 2], is = stats[4 * r + 3];
+            const double mc = s_st[r][0], ic = s_st[r][1], ms = s_st[r][2], is = s_st[r][3];
             pc[r] = (float)((s_m[15 + 2 * r] - mc * sP) * ic / n);
             ps[r] = (float)((s_m[16 + 2 * r] - ms * sP) * is / n);
             ecs[r] = (float)((s_m[15 + 2 * g.R + 2 * r] - mc * sT) * ic / n);
             ess[r] = (float)((s_m[16 + 2 * g.R + 2 * r] - ms * sT) * is / n);
         }
+        float om[SP_MAXR], qc[SP_MAXR], qs[SP_MAXR], pcv[SP_MAXR], psv[SP_MAXR], cac[SP_MAXR], cas[SP_MAXR];
+        for (int r = 0; r < g.R; ++r) {
+            om[r] = s_f[r][0]; qc[r] = s_f[r][1]; qs[r] = s_f[r][2]; pcv[r] = s_f[r][3]; psv[r] = s_f[r][4];
+            cac[r] = s_f[r][5]; cas[r] = s_f[r][6];
+        }
         // confidence (cresso_v5.py:1199-1202) with the pre-contact q
         const float cd = (float)h.confidence_decay;
+        float gt[SP_MAXR];
         for (int r = 0; r < g.R; ++r) {
-            const float qc = st.q_cos[r], qs = st.q_sin[r];
             const float pe = sqrtf(pc[r] * pc[r] + ps[r] * ps[r] + eps);
-            const float sup = (pc[r] * qc + ps[r] * qs) / (pe * sqrtf(qc * qc + qs * qs + eps) + eps);
-            float c = st.conf[r] * cd + (float)(1.0 - h.confidence_decay) * clampf(sup, -1.0f, 1.0f);
-            st.conf[r] = clampf(c, -4.0f, 4.0f);
+            const float sup = (pc[r] * qc[r] + ps[r] * qs[r]) / (pe * sqrtf(qc[r] * qc[r] + qs[r] * qs[r] + eps) + eps);
+            const float c = s_f[r][7] * cd + (float)(1.0 - h.confidence_decay) * clampf(sup, -1.0f, 1.0f);
+            s_f[r][7] = clampf(c, -4.0f, 4.0f);
+            gt[r] = sigmoidf_((float)h.confidence_gain * s_f[r][7]);
         }
         // contact on the cos bank then the sin bank with the shared action
-        float action = *st.action;
-        contact_bank(st.q_cos, st.p_cos, pc, st.omega, st.calcium_cos, action, sur, g.R, h);
-        contact_bank(st.q_sin, st.p_sin, ps, st.omega, st.calcium_sin, action, sur, g.R, h);
-        *st.action = action;
-        float gt[SP_MAXR], qc[SP_MAXR], qs[SP_MAXR];
+        float action = s_sc[1];
+        contact_bank(qc, pcv, pc, om, cac, action, sur, g.R, h);
+        contact_bank(qs, psv, ps, om, cas, action, sur, g.R, h);
+        s_sc[1] = action;
         for (int r = 0; r < g.R; ++r) {
-            gt[r] = sigmoidf_((float)h.confidence_gain * st.conf[r]);
-            qc[r] = st.q_cos[r];
-            qs[r] = st.q_sin[r];
+            s_f[r][1] = qc[r]; s_f[r][2] = qs[r]; s_f[r][3] = pcv[r]; s_f[r][4] = psv[r];
+            s_f[r][5] = cac[r]; s_f[r][6] = cas[r];
         }
-        set_recon(g, meta, stats, ctrl, 2, qc, qs, gt);
-        if (echo_on) set_recon(g, meta, stats, ctrl, 3, ecs, ess, nullptr);
+        set_recon(g, stt, ctrl->rc[2], ctrl->rconst[2], qc, qs, gt);
+        if (echo_on) set_recon(g, stt, ctrl->rc[3], ctrl->rconst[3], ecs, ess, nullptr);
         // drive shaping coefficients that depend only on moments of t
         // (cresso_v5.py:1303-1337): shaped = ar rat + ab bnd + ao root,
         // core = (1-dmix) shaped + dmix t srms/max(frms,eps)
@@ -1065,6 +1208,21 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta*
         moments[1] = (double)srms;
         moments[2] = (double)frms;
     }
+    __syncthreads();
+    if (tid < g.R) {
+        const int r = tid;
+        st.q_cos[r] = s_f[r][1];
+        st.q_sin[r] = s_f[r][2];
+        st.p_cos[r] = s_f[r][3];
+        st.p_sin[r] = s_f[r][4];
+        st.calcium_cos[r] = s_f[r][5];
+        st.calcium_sin[r] = s_f[r][6];
+        st.conf[r] = s_f[r][7];
+    }
+    if (tid == 0) {
+        *st.surprise = s_sc[0];
+        *st.action = s_sc[1];
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1076,23 +1234,18 @@ __device__ __forceinline__ int pair_index(int a, int b) {  // a <= b < 6
 }
 
 template <int RM, int KM>
-__global__ __launch_bounds__(SP_NT) void sweep4_kernel(Geom g, const float* __restrict__ rowtab,
-                                                       const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
+__global__ __launch_bounds__(SP_NT) void sweep4_kernel(Geom g, const float* __restrict__ coltab,
                                                        const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
-                                                       const float* __restrict__ imp_tab, const float* __restrict__ tbuf,
-                                                       double* __restrict__ part, int hash_on, int echo_on, cresso_hyper h) {
+                                                       const float* __restrict__ imp_tab, const float* __restrict__ alpha,
+                                                       const float* __restrict__ tbuf, double* __restrict__ part,
+                                                       int hash_on, int echo_on, cresso_hyper h) {
     extern __shared__ __align__(16) unsigned char dyn[];
-    __shared__ double red[4 * NV4];
+    __shared__ float red[4 * NV4];
     const Tile t = tile_of(g);
     const int TB = g.T * g.B;
-    const int st_al = g.K + 1;
     float* s_imp = reinterpret_cast<float*>(dyn);
-    float* s_aQ = s_imp + TB;
-    float* s_aE = s_aQ + (size_t)g.PR * st_al;
     if (hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
-    build_alpha(g, t, rowtab, meta, ctrl, 2, s_aQ);
-    if (echo_on) build_alpha(g, t, rowtab, meta, ctrl, 3, s_aE);
     __syncthreads();
     float b[KM];
     load_cols<KM>(g, coltab, t, b);
@@ -1100,18 +1253,19 @@ __global__ __launch_bounds__(SP_NT) void sweep4_kernel(Geom g, const float* __re
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
     const float cr = ctrl->cr, cb = ctrl->cb, co = ctrl->co, ct = ctrl->ct, ns = ctrl->nscale;
     const float invT = 1.0f / (float)g.T;
+    const float* __restrict__ alQ = alpha + 2 * (size_t)g.rows * g.KA;
+    const float* __restrict__ alE = alQ + (size_t)g.rows * g.KA;
     float m[NV4];
 #pragma unroll
     for (int k = 0; k < NV4; ++k) m[k] = 0.f;
     if (t.colok) {
         for (int64_t i = t.r0; i < t.r1; ++i) {
-            const int lr = (int)(i - t.r0);
             const int64_t e = i * g.cols + t.col;
             const float tv = tbuf[e];
-            const float pred = recon<KM>(s_aQ + (size_t)lr * st_al, b, g.K);
+            const float pred = recon<KM>(alQ + i * g.KA, b);
             const float err = tv - pred;
             const float nov = ftanh(err * ns) * clip;
-            const float echo = echo_on ? recon<KM>(s_aE + (size_t)lr * st_al, b, g.K) : 0.f;
+            const float echo = echo_on ? recon<KM>(alE + i * g.KA, b) : 0.f;
             float hp = 0.f;
             if (hash_on) {
                 const uint64_t pk = load_bins(bins, e, g.binbytes);
@@ -1119,7 +1273,7 @@ __global__ __launch_bounds__(SP_NT) void sweep4_kernel(Geom g, const float* __re
                 hp = hp * invT;
             }
             float rat, bnd, root;
-            shape3f<float>(tv, iclip, clip, clip2, eps, rat, bnd, root);
+            shape3f(tv, iclip, clip, clip2, eps, rat, bnd, root);
             const float core = cr * rat + cb * bnd + co * root + ct * tv;
             const float Y[6] = {core, pred, nov, err, echo, hp};
 #pragma unroll
@@ -1138,15 +1292,9 @@ __global__ __launch_bounds__(SP_NT) void sweep4_kernel(Geom g, const float* __re
 __global__ __launch_bounds__(SP_FIN_NT) void fin4_kernel(Geom g, const double* __restrict__ part, SpecState st,
                                                          Ctrl* __restrict__ ctrl, int step, int hash_on, int hard,
                                                          int echo_on, cresso_hyper h, const double* __restrict__ moments) {
-    __shared__ double red[16];
     __shared__ double s_m[NV4];
-    const int tid = threadIdx.x;
-    for (int v = 0; v < NV4; ++v) {
-        const double x = reduce_part(part, g.nblk, v, red);
-        if (tid == 0) s_m[v] = x;
-    }
-    __syncthreads();
-    if (tid != 0) return;
+    reduce_all(part, g.nblk, NV4, s_m);
+    if (threadIdx.x != 0) return;
     const double n = (double)g.n;
     const float eps = (float)h.eps;
     auto G = [&](int a, int b) { return a <= b ? s_m[pair_index(a, b)] : s_m[pair_index(b, a)]; };
@@ -1194,22 +1342,17 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin4_kernel(Geom g, const double* _
 // S5: parameter update
 // ---------------------------------------------------------------------------
 template <int RM, int KM, typename PT>
-__global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ param, const float* __restrict__ rowtab,
-                                                       const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
+__global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ param, const float* __restrict__ coltab,
                                                        const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
-                                                       const float* __restrict__ imp_tab, const float* __restrict__ tbuf,
-                                                       int hash_on, int echo_on, cresso_hyper h) {
+                                                       const float* __restrict__ imp_tab, const float* __restrict__ alpha,
+                                                       const float* __restrict__ tbuf, int hash_on, int echo_on,
+                                                       cresso_hyper h) {
     extern __shared__ __align__(16) unsigned char dyn[];
     const Tile t = tile_of(g);
     const int TB = g.T * g.B;
-    const int st_al = g.K + 1;
     float* s_imp = reinterpret_cast<float*>(dyn);
-    float* s_aQ = s_imp + TB;
-    float* s_aE = s_aQ + (size_t)g.PR * st_al;
     if (hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
-    build_alpha(g, t, rowtab, meta, ctrl, 2, s_aQ);
-    if (echo_on) build_alpha(g, t, rowtab, meta, ctrl, 3, s_aE);
     __syncthreads();
     if (!t.colok) return;
     float b[KM];
@@ -1221,15 +1364,16 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
     const float gain = ctrl->gain;
     const float nlr = (float)(-h.lr);
     const float invT = 1.0f / (float)g.T;
+    const float* __restrict__ alQ = alpha + 2 * (size_t)g.rows * g.KA;
+    const float* __restrict__ alE = alQ + (size_t)g.rows * g.KA;
     for (int64_t i = t.r0; i < t.r1; ++i) {
-        const int lr = (int)(i - t.r0);
         const int64_t e = i * g.cols + t.col;
         const float tv = tbuf[e];
-        const float pred = recon<KM>(s_aQ + (size_t)lr * st_al, b, g.K);
+        const float pred = recon<KM>(alQ + i * g.KA, b);
         const float err = tv - pred;
         const float nov = ftanh(err * ns) * clip;
         float drive = d1 * pred + d2 * nov + d3 * err;
-        if (echo_on) drive += d4 * recon<KM>(s_aE + (size_t)lr * st_al, b, g.K);
+        if (echo_on) drive += d4 * recon<KM>(alE + i * g.KA, b);
         if (hash_on) {
             const uint64_t pk = load_bins(bins, e, g.binbytes);
             float hp = 0.f;
@@ -1237,7 +1381,7 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
             drive += d5 * (hp * invT);
         }
         float rat, bnd, root;
-        shape3f<float>(tv, iclip, clip, clip2, eps, rat, bnd, root);
+        shape3f(tv, iclip, clip, clip2, eps, rat, bnd, root);
         const float core = cr * rat + cb * bnd + co * root + ct * tv;
         drive += d0 * core;
         const float u = to_f(from_w<PT>(drive * gain));
@@ -1386,13 +1530,22 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     if (g.K > KM) return fail(CRESSO_E_INVALID, "spectral route: %d column carriers exceed %d", g.K, KM);
     if ((double)g.K * (double)g.cols * 4.0 > 2.0e9)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: column carrier table too large (%d x %lld)", g.K, (long long)g.cols);
-    // tiling: 256 columns per block, PR rows per block, ~2048 blocks
+    g.KA = 2 * P.rmax + 2;
+    g.RW = 2 * P.rmax;
+    // tiling: 256 columns per block, PR rows per block, ~1024 blocks
     g.slabs = (int32_t)((g.cols + SP_NT - 1) / SP_NT);
-    int64_t pr = std::max<int64_t>(8, (g.rows * g.slabs) / 2048);
+    int64_t pr = std::max<int64_t>(16, (g.rows * g.slabs) / 1024);
     pr = std::min<int64_t>(std::min<int64_t>(pr, 64), g.rows);
     g.PR = (int32_t)std::max<int64_t>(1, pr);
     g.panels = (int32_t)((g.rows + g.PR - 1) / g.PR);
     g.nblk = g.slabs * g.panels;
+    // flat force-RMS sweep: contiguous chunks (multiple of 4 elements) per block
+    g.nblk1 = (int32_t)std::max<int64_t>(1, std::min<int64_t>(1024, (g.n + 16383) / 16384));
+    g.chunk1 = (((g.n + g.nblk1 - 1) / g.nblk1) + 3) & ~(int64_t)3;
+    g.nblk1 = (int32_t)((g.n + g.chunk1 - 1) / g.chunk1);
+    // axis density sums: density <= 1e6 per element, sums below 2^62
+    g.hs_row = ldexp(1.0, (int)std::floor(62.0 - std::log2(1.0e6 * (double)g.cols)));
+    g.hs_col = ldexp(1.0, (int)std::floor(62.0 - std::log2(1.0e6 * (double)g.rows)));
     // workspace layout
     Offs& o = P.o;
     size_t off = 0;
@@ -1400,24 +1553,25 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.axc = take(sizeof(AxisConst) * P.axc.size());
     o.meta = take(sizeof(ModeMeta) * P.meta.size());
     o.csrc = take(sizeof(CarrierSrc) * P.csrc.size());
-    o.rowtab = take(sizeof(float) * (size_t)g.rows * 2 * g.R);
+    o.rowtab = take(sizeof(float) * (size_t)g.rows * g.RW);
     o.coltab = take(sizeof(float) * (size_t)g.K * g.cols);
     o.stats = take(sizeof(double) * 4 * g.R);
     o.bounds = take(sizeof(double) * 2 * g.R);
     o.counts = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
     o.bins = take((size_t)g.binbytes * (size_t)g.n);
     o.tbuf = take(sizeof(float) * (size_t)g.n);
-    o.part = take(sizeof(double) * (size_t)NVMAX * g.nblk);
+    o.part = take(sizeof(double) * (size_t)NVMAX * std::max(g.nblk, g.nblk1));
     o.hist = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
     o.lt = take(sizeof(float) * (size_t)g.T * g.B);
     o.imp = take(sizeof(float) * (size_t)g.T * g.B);
-    o.rowpart = take(sizeof(float) * (size_t)g.slabs * g.rows);
-    o.colpart = take(sizeof(float) * (size_t)g.panels * g.cols);
+    o.alpha = take(sizeof(float) * 4 * (size_t)g.rows * g.KA);
+    o.rowfx = take(sizeof(unsigned long long) * (size_t)g.rows);
+    o.colfx = take(sizeof(unsigned long long) * (size_t)g.cols);
     o.rowfac = take(sizeof(float) * (size_t)g.rows);
     o.colfac = take(sizeof(float) * (size_t)g.cols);
     int64_t sum_trail = 0;
     for (int a = 0; a < g.ntrail; ++a) sum_trail += g.tdim[a];
-    o.terms = take(sizeof(float) * (size_t)(g.rows + g.cols + sum_trail));
+    o.terms = take(sizeof(float) * (size_t)std::max<int64_t>(1, sum_trail));
     o.ctrl = take(sizeof(Ctrl) + 3 * sizeof(double));
     o.total = off;
     return CRESSO_OK;
@@ -1425,11 +1579,9 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
 
 template <typename T> T* at(void* ws, size_t off) { return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off); }
 
-size_t lds_sweep2(const Geom& g) { return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * ((size_t)g.PR * 2 * g.R + 4 * g.PR); }
-size_t lds_sweep3(const Geom& g) {
-    return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * ((size_t)g.T * g.B + (size_t)g.PR * 2 * g.R + 2 * (size_t)g.PR * (g.K + 1));
-}
-size_t lds_sweep45(const Geom& g) { return sizeof(float) * ((size_t)g.T * g.B + 2 * (size_t)g.PR * (g.K + 1)); }
+size_t lds_sweep2(const Geom& g) { return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * 4 * (size_t)g.PR; }
+size_t lds_sweep3(const Geom& g) { return (sizeof(unsigned long long) + sizeof(float)) * g.T * g.B; }
+size_t lds_sweep45(const Geom& g) { return sizeof(float) * (size_t)g.T * g.B; }
 
 template <int RM, typename PT, typename GT>
 int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws, const cresso_hyper& h,
@@ -1460,8 +1612,9 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     unsigned long long* hist = at<unsigned long long>(ws, o.hist);
     float* lt = at<float>(ws, o.lt);
     float* imp = at<float>(ws, o.imp);
-    float* rowpart = at<float>(ws, o.rowpart);
-    float* colpart = at<float>(ws, o.colpart);
+    float* alpha = at<float>(ws, o.alpha);
+    unsigned long long* rowfx = at<unsigned long long>(ws, o.rowfx);
+    unsigned long long* colfx = at<unsigned long long>(ws, o.colfx);
     float* rowfac = at<float>(ws, o.rowfac);
     float* colfac = at<float>(ws, o.colfac);
     float* terms = at<float>(ws, o.terms);
@@ -1471,28 +1624,38 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     const double* stats = at<double>(ws, o.stats);
     const double* bounds = at<double>(ws, o.bounds);
     const int step = d.step;
+    const int axes_on = (hard && h.instant_metric_coupling != 0.0 && !g.one_d) ? 1 : 0;
     const dim3 grid(g.nblk), blk(SP_NT);
-    hipLaunchKernelGGL((sweep1_kernel<PT, GT>), grid, blk, 0, s, g, grad, param, part, h);
-    hipLaunchKernelGGL(fin1_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, part, st, ctrl, step, h);
+    const bool v4 = ((uintptr_t)grad % (4 * sizeof(GT))) == 0 && ((uintptr_t)param % (4 * sizeof(PT))) == 0;
+    if (v4)
+        hipLaunchKernelGGL((sweep1_kernel<PT, GT, true>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, h);
+    else
+        hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, h);
+    hipLaunchKernelGGL(fin1_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, part, st, ctrl, rowfx, colfx, step, h);
     hipLaunchKernelGGL((sweep2_kernel<RM, KM, PT, GT>), grid, blk, lds_sweep2(g), s, g, grad, param, rowtab, coltab, meta,
-                       bins, ctrl, part, hist, rowpart, colpart, hash_on, h);
-    hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, bounds, part, hist, counts, lt, st, ctrl,
-                       step, hash_on, hard, h);
-    if (hard && h.instant_metric_coupling != 0.0 && !g.one_d) {
-        const int64_t cnt = g.rows + g.cols;
-        hipLaunchKernelGGL(marg_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s, g, rowpart, colpart, terms);
-        hipLaunchKernelGGL(marg_axes_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, terms, rowfac, colfac, ctrl, (float)h.eps);
+                       bins, ctrl, part, hist, rowfx, colfx, hash_on, axes_on, h);
+    hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, bounds, rowtab, part, hist, counts, lt,
+                       alpha, st, ctrl, step, hash_on, hard, h);
+    const dim3 rgrid((unsigned)((g.rows + 255) / 256)), rblk(256);
+    hipLaunchKernelGGL((alpha_kernel<RM>), rgrid, rblk, 0, s, g, meta, rowtab, (const Ctrl*)ctrl, 0, 2, alpha);
+    if (axes_on) {
+        const int64_t cnt = g.rows + (g.ntrail == 1 ? g.cols : 0);
+        hipLaunchKernelGGL(marg_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s, g, rowfx, colfx, rowfac,
+                           colfac, ctrl, (float)h.eps);
+        if (g.ntrail > 1)
+            hipLaunchKernelGGL(marg_axes_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, colfx, terms, colfac, ctrl, (float)h.eps);
     }
     hipLaunchKernelGGL((sweep3_kernel<RM, KM, PT, GT>), grid, blk, lds_sweep3(g), s, g, grad, param, rowtab, coltab, meta,
-                       bins, ctrl, lt, rowfac, colfac, tbuf, part, hist, hash_on, echo_on, h);
-    hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, part, hist, counts, imp, st, ctrl, step,
-                       hash_on, hard, echo_on, h, moments);
-    hipLaunchKernelGGL((sweep4_kernel<RM, KM>), grid, blk, lds_sweep45(g), s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf,
-                       part, hash_on, echo_on, h);
+                       bins, ctrl, lt, alpha, rowfac, colfac, tbuf, part, hist, hash_on, echo_on, h);
+    hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, rowtab, part, hist, counts, imp, alpha,
+                       st, ctrl, step, hash_on, hard, echo_on, h, moments);
+    hipLaunchKernelGGL((alpha_kernel<RM>), rgrid, rblk, 0, s, g, meta, rowtab, (const Ctrl*)ctrl, 2, echo_on ? 2 : 1, alpha);
+    hipLaunchKernelGGL((sweep4_kernel<RM, KM>), grid, blk, lds_sweep45(g), s, g, coltab, bins, ctrl, imp, alpha, tbuf, part,
+                       hash_on, echo_on, h);
     hipLaunchKernelGGL(fin4_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, part, st, ctrl, step, hash_on, hard, echo_on, h,
                        (const double*)moments);
-    hipLaunchKernelGGL((sweep5_kernel<RM, KM, PT>), grid, blk, lds_sweep45(g), s, g, param, rowtab, coltab, meta, bins, ctrl,
-                       imp, tbuf, hash_on, echo_on, h);
+    hipLaunchKernelGGL((sweep5_kernel<RM, KM, PT>), grid, blk, lds_sweep45(g), s, g, param, coltab, bins, ctrl, imp, alpha,
+                       tbuf, hash_on, echo_on, h);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: launch");
 }
