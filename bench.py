@@ -1,6 +1,7 @@
 """Benchmark of the CRESSO5 hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|copy] [--no-cpu]
+    python bench.py --rocprof-summary DIR [--calib DIR] [--launches N]
 
 Workloads:
   c2: one fp32 (4096,4096) parameter, spectral/hash route, rank 8, F=5, B=64, T=2;
@@ -13,6 +14,13 @@ Workloads:
 Inputs are resident in HBM before the timed region; each step's grads are
 pre-generated on the device (a pool of 4 grad sets cycled through), so the
 timed region holds only optimizer.step().
+
+The --rocprof-summary mode turns rocprofv3 CSV output (--output-format csv)
+in DIR into markdown tables: per-kernel durations from *kernel_stats.csv, and
+per-kernel counter means per dispatch from *counter_collection.csv, with the
+HBM byte counters scaled by the copy calibration in --calib (FETCH_SIZE and
+WRITE_SIZE of the known-size copy) and summed per launch of the hot path
+(--launches = optimizer steps the profiled run executed).
 
 Prints ONE JSON line.  `value` is the algorithmic HBM throughput of a step
 (grad read + param read + param write, 12 B per fp32 element) in GB/s.
@@ -68,6 +76,21 @@ def make_c2(device, pool=4, seed=0):
         grads.append([torch.where(mask, g * 50.0, g).to(device)])
     kwargs = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2)
     return params, grads, kwargs, [shape], None
+
+
+TRAFFIC_FILES = {"c2": "profiles/spectral_step_c2_hbm_traffic.md", "c3": "profiles/scalar_step_c3_hbm_traffic.md"}
+
+
+def measured_traffic(workload):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary of this workload (scaled by the copy calibration), or None."""
+    path = ROOT / TRAFFIC_FILES.get(workload, "-")
+    if not path.is_file():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("- scaled HBM bytes"):
+            return int(float(line.rsplit(":", 1)[1]))
+    return None
 
 
 def algorithmic_bytes(shapes, elem_bytes=4):
@@ -134,6 +157,126 @@ def copy_calibration(steps, warmup, nbytes=256 << 20):
                 gb_s=round(2 * nbytes / (ms * 1e-3) / 1e9, 1))
 
 
+# ---------------------------------------------------------------------------
+# rocprofv3 CSV summaries
+# ---------------------------------------------------------------------------
+_SETUP = ("ws_", "zero_u64")  # one-time workspace set-up kernels of the library
+
+
+def _hot(name: str) -> bool:
+    """A kernel of the library's per-step launch (not torch's, not set-up)."""
+    return "cresso::" in name and not _short_kernel(name).startswith(_SETUP)
+
+
+def _short_kernel(name: str) -> str:
+    import re
+    m = re.search(r"cresso::(?:\(anonymous namespace\)::)?(\w+)", name)
+    if m:
+        return m.group(1)
+    if "copyBuffer" in name:
+        return "__amd_rocclr_copyBuffer"
+    return name.split("(")[0][-60:]
+
+
+def _read_csv(path):
+    import csv
+    with open(path, newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def _counter_means(paths):
+    """{kernel: {counter: (mean value per dispatch, dispatches)}}; rows of one
+    dispatch (counter dimensions) are summed first."""
+    from collections import defaultdict
+    per = defaultdict(float)
+    names = {}
+    for path in paths:
+        for row in _read_csv(path):
+            key = (path, row["Dispatch_Id"], row["Counter_Name"])
+            per[key] += float(row["Counter_Value"])
+            names[(path, row["Dispatch_Id"])] = ("*" if _hot(row["Kernel_Name"]) else "") + \
+                _short_kernel(row["Kernel_Name"])
+    agg = defaultdict(lambda: defaultdict(list))
+    for (path, did, cn), v in per.items():
+        agg[names[(path, did)]][cn].append(v)
+    return {k: {cn: (sum(v) / len(v), len(v)) for cn, v in d.items()} for k, d in agg.items()}
+
+
+def _copy_reading(calib_dirs, counter):
+    """Median reading of `counter` over the 256 MiB copies of `bench.py --workload copy`."""
+    import glob
+    from collections import defaultdict
+    vals = defaultdict(float)
+    for d in calib_dirs:
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for row in _read_csv(path):
+                if row["Counter_Name"] == counter and "copyBuffer" in row["Kernel_Name"]:
+                    vals[(path, row["Dispatch_Id"])] += float(row["Counter_Value"])
+    if not vals:
+        return None
+    big = sorted(v for v in vals.values() if v >= 0.5 * max(vals.values()))
+    return big[len(big) // 2]
+
+
+def rocprof_summary(d, calib=None, launches=None):
+    import glob
+    out = []
+    for path in sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)):
+        rows = _read_csv(path)
+        out.append(f"### Kernel durations ({os.path.basename(path)})\n")
+        out.append("| kernel | calls | avg us | min us | max us | % |")
+        out.append("|---|---:|---:|---:|---:|---:|")
+        per_launch = 0.0
+        for r in rows:
+            k = _short_kernel(r["Name"])
+            avg = float(r["AverageNs"]) / 1e3
+            calls = int(r["Calls"])
+            out.append(f"| {k} | {calls} | {avg:.2f} | {float(r['MinNs'])/1e3:.2f} | {float(r['MaxNs'])/1e3:.2f} | "
+                       f"{float(r['Percentage']):.1f} |")
+            if launches and _hot(r["Name"]):
+                per_launch += float(r["TotalDurationNs"]) / 1e3 / launches
+        if launches:
+            out.append(f"\nkernel time per launch of the hot path (library kernels without one-time set-up, "
+                       f"{launches} launches): {per_launch:.2f} us\n")
+    cc = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if cc:
+        means = _counter_means(cc)
+        scale = {}
+        if calib:
+            for cn in ("FETCH_SIZE", "WRITE_SIZE"):
+                kib = _copy_reading(calib, cn)
+                if kib:
+                    nbytes = 256 << 20
+                    scale[cn] = nbytes / (kib * 1024.0)
+                    out.append(f"{cn} calibration: device copy of {nbytes} B reads {kib:.1f} KiB per dispatch "
+                               f"-> bytes = KiB x 1024 x {scale[cn]:.4f}")
+        counters = sorted({cn for d_ in means.values() for cn in d_})
+        out.append("\n### Counters, mean per dispatch (* = kernel of the per-step launch)\n")
+        out.append("| kernel | dispatches | " + " | ".join(counters) + " |")
+        out.append("|---|---:|" + "---:|" * len(counters))
+        totals = {cn: 0.0 for cn in counters}
+        for k, d_ in sorted(means.items(), key=lambda kv: kv[0]):
+            n = max(v[1] for v in d_.values())
+            out.append(f"| {k} | {n} | " + " | ".join(f"{d_[cn][0]:.5g}" if cn in d_ else "" for cn in counters) + " |")
+            if launches and k.startswith("*"):
+                for cn in counters:
+                    if cn in d_:
+                        totals[cn] += d_[cn][0] * d_[cn][1] / launches
+        if launches:
+            out.append(f"\nper launch of the hot path (* kernels, {launches} launches):")
+            tb = 0
+            for cn in counters:
+                line = f"- {cn}: {totals[cn]:.6g}"
+                if cn in scale:
+                    b = totals[cn] * 1024.0 * scale[cn]
+                    tb += b
+                    line += f" KiB -> {b:.0f} bytes"
+                out.append(line)
+            if tb:
+                out.append(f"- scaled HBM bytes (those counters above): {tb:.0f}")
+    print("\n".join(out))
+
+
 def time_cpu(workload, sample_steps=2):
     """CPU oracle (port of the reference's cuda_ops='off' path) on this host's cores."""
     from oracle.cresso_oracle import OracleCRESSO5
@@ -159,7 +302,7 @@ def time_cpu(workload, sample_steps=2):
         opt.step(grads[1 + k])
     dt = (time.perf_counter() - t0) / sample_steps / frac
     return dict(value=round(dt * 1e3, 3), unit="ms/step", cores=torch.get_num_threads(), kind="port",
-                sample=sample, cpu=platform.processor() or _cpu_model())
+                sample=sample, cpu=_cpu_model())
 
 
 def _cpu_model():
@@ -180,7 +323,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=["c2", "c3", "copy"], default=None)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--rocprof-summary", default=None, metavar="DIR")
+    ap.add_argument("--calib", default=None, nargs="+", metavar="DIR")
+    ap.add_argument("--launches", type=int, default=None)
     args = ap.parse_args()
+    if args.rocprof_summary:
+        rocprof_summary(args.rocprof_summary, args.calib, args.launches)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
               "(every GPU box here has one GPU)", file=sys.stderr)
@@ -217,7 +366,7 @@ def main():
                                 "c3": "C3: 840 LoRA-thin fp32 (4096,16)/(16,4096), scalar route, rank 4"}[workload],
                    "elements": n, "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(workload)},
     }
     if not args.no_cpu:
         out["cpu_baseline"] = time_cpu(workload)

@@ -95,6 +95,26 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Wave total of a double by DPP row operations (VALU only, no LDS round
+// trips); the total lands in lane 63, other lanes hold partial sums.  Each
+// step moves both 32-bit halves with the same DPP control; lanes without a
+// source receive +0.0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_add_d(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, ROW_MASK, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, ROW_MASK, 0xF, false);
+    return v + __hiloint2double(hi, lo);
+}
+__device__ __forceinline__ double wave_total_d(double v) {
+    v = dpp_add_d<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add_d<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add_d<0x124, 0xF>(v);  // row_ror:4
+    v = dpp_add_d<0x128, 0xF>(v);  // row_ror:8
+    v = dpp_add_d<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
+    v = dpp_add_d<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
 // Sum V values over the block; every thread receives the totals.
 // lds must hold (blockDim.x/64) * V doubles.  Two barriers.
 template <int V>
@@ -103,8 +123,8 @@ __device__ __forceinline__ void block_sum(double (&v)[V], double* lds) {
     const int wave = threadIdx.x / kWave;
     const int nw = blockDim.x / kWave;
 #pragma unroll
-    for (int i = 0; i < V; ++i) v[i] = wave_sum(v[i]);
-    if (lane == 0) {
+    for (int i = 0; i < V; ++i) v[i] = wave_total_d(v[i]);
+    if (lane == kWave - 1) {
 #pragma unroll
         for (int i = 0; i < V; ++i) lds[wave * V + i] = v[i];
     }

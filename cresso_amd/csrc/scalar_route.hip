@@ -20,9 +20,10 @@
 // Two kernels:
 //  * scalar_resident_kernel: 2D tensors of <= 64 Ki elements whose rows map to
 //    lane groups (LoRA-thin (L,16)) or whose rows are exactly one block wide
-//    ((16,4096)); f, then t, then drive stay in VGPRs, so HBM traffic is the
-//    compulsory grad read + param read/write.  Axis sums use register partials,
-//    fixed-order wave butterflies and LDS, never float atomics.
+//    ((16,4096)); f, then t, then drive stay on chip (half of each thread's
+//    64 elements in VGPRs, half in a 128 KiB LDS slot array), so HBM traffic is
+//    the compulsory grad read + param read/write.  Axis sums use register
+//    partials, fixed-order wave butterflies (DPP) and LDS, never float atomics.
 //  * scalar_stream_kernel: every other shape/size/dtype; re-reads the grad in
 //    each pass and keeps general-ndim axis sums as 64-bit fixed-point integers
 //    in a global scratch area (integer atomics: order-independent results).
@@ -38,6 +39,9 @@ namespace {
 
 constexpr int SR_NT = 1024;                                  // threads per tensor
 constexpr int SR_SLOTS = 16;                                 // float4 slots per thread
+constexpr int SR_VSLOTS = 8;                                 // slots held in VGPRs; the rest live in LDS
+constexpr size_t SR_XLDS = (size_t)(SR_SLOTS - SR_VSLOTS) * SR_NT * 16;  // LDS bytes of the LDS slots (128 KiB)
+constexpr size_t SR_LDS_MAX = 160 * 1024 - 4096;             // dynamic LDS budget of one workgroup (static LDS aside)
 constexpr int64_t SR_RESIDENT_MAX = (int64_t)SR_NT * SR_SLOTS * 4;
 
 enum Layout : int32_t { L_NONE = 0, L_1D = 1, L_ROWGROUP = 2, L_COLBLOCK = 3, L_GENERIC = 4 };
@@ -215,7 +219,29 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
     const bool wd_on = h.weight_decay != 0.0;
     const float wd = (float)h.weight_decay;
 
-    float x[SR_SLOTS * 4];
+    // per-thread element slots: the first SR_VSLOTS in VGPRs, the rest in LDS
+    // ([slot][thread] float4, conflict-free); k is a compile-time constant at
+    // every use, so the choice folds away
+    float xv[SR_VSLOTS * 4];
+    float4* __restrict__ xl = reinterpret_cast<float4*>(dyn);
+    unsigned char* const dyn2 = dyn + SR_XLDS;
+    auto ldx = [&](int k, float* v) {
+        if (k < SR_VSLOTS) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = xv[4 * k + c];
+        } else {
+            const float4 q = xl[(k - SR_VSLOTS) * SR_NT + tid];
+            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+        }
+    };
+    auto stx = [&](int k, const float* v) {
+        if (k < SR_VSLOTS) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) xv[4 * k + c] = v[c];
+        } else {
+            xl[(k - SR_VSLOTS) * SR_NT + tid] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    };
     auto e0_of = [&](int k) -> int64_t { return ((int64_t)k * SR_NT + tid) * 4; };
 
     // ---- pass A ----
@@ -223,24 +249,26 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
 #pragma unroll
     for (int k = 0; k < SR_SLOTS; ++k) {
         const int64_t e0 = e0_of(k);
+        float v[4];
         if (e0 < n) {
-            V4<GT>::ld(g, e0, &x[4 * k]);
+            V4<GT>::ld(g, e0, v);
             if (h.maximize) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) x[4 * k + c] = -x[4 * k + c];
+                for (int c = 0; c < 4; ++c) v[c] = -v[c];
             }
             if (wd_on) {
                 float pv[4];
                 V4<PT>::ld(p, e0, pv);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) x[4 * k + c] = x[4 * k + c] + wd * pv[c];
+                for (int c = 0; c < 4; ++c) v[c] = v[c] + wd * pv[c];
             }
         } else {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) x[4 * k + c] = 0.f;
+            for (int c = 0; c < 4; ++c) v[c] = 0.f;
         }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) a_ff += x[4 * k + c] * x[4 * k + c];
+        for (int c = 0; c < 4; ++c) a_ff += v[c] * v[c];
+        stx(k, v);
     }
     __syncthreads();
     const int step = s_step;
@@ -258,8 +286,8 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
     const float ipw = (float)fmax(h.instant_metric_power, 0.25);
     const bool ip_one = ipw == 1.0f;
     const float kappa = (float)(h.instant_metric_coupling / (2.0 * fmax(h.instant_metric_power, 0.25)));
-    float* rowfac = reinterpret_cast<float*>(dyn);                       // [rows]
-    double* colred = reinterpret_cast<double*>(dyn + ((sizeof(float) * rows + 15) & ~(size_t)15));  // [16][C0]
+    float* rowfac = reinterpret_cast<float*>(dyn2);                      // [rows]
+    double* colred = reinterpret_cast<double*>(dyn2 + ((sizeof(float) * rows + 15) & ~(size_t)15));  // [16][C0]
     float colacc[4] = {0.f, 0.f, 0.f, 0.f};
     float slotrow[SR_SLOTS];  // COLBLOCK: per-slot row partials
     float a_L = 0.f, a_dens = 0.f;
@@ -267,9 +295,11 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
     for (int k = 0; k < SR_SLOTS; ++k) {
         const bool ok = e0_of(k) < n;
         float rs = 0.f;
+        float xk[4];
+        ldx(k, xk);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const float r = fabsf(x[4 * k + c]) * inv_s + eps;
+            const float r = fabsf(xk[c]) * inv_s + eps;
             const float L = flog1p(fpow(r, pw));
             const float rl = fmaxf(fminf(r, 1.0e4f), eps);
             const float dens = fminf(ip_one ? rl : fpow(rl, ipw), 1.0e6f);
@@ -282,7 +312,11 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
             sched_fence();
         }
         if (LAYOUT == L_ROWGROUP) {
-            for (int m = 1; m < G; m <<= 1) rs += __shfl_xor(rs, m, 64);
+            // butterfly over the G lanes of a row: xor 1 and 2 by DPP quad
+            // permutes (same pairings as the lane shuffles), wider by shuffles
+            if (G >= 2) rs += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, rs), 0xB1, 0xF, 0xF, false));
+            if (G >= 4) rs += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, rs), 0x4E, 0xF, 0xF, false));
+            for (int m = 4; m < G; m <<= 1) rs += __shfl_xor(rs, m, 64);
             const int64_t row = ((int64_t)k * SR_NT + tid) / G;
             if (ok && (tid % G) == 0) rowfac[row] = rs;
         } else {
@@ -366,9 +400,11 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
         const bool ok = e0_of(k) < n;
         const int64_t row = LAYOUT == L_ROWGROUP ? ((int64_t)k * SR_NT + tid) / G : (int64_t)k;
         const float Er = ok ? rowfac[row] : 1.0f;
+        float xk[4];
+        ldx(k, xk);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const float f = x[4 * k + c];
+            const float f = xk[c];
             float den = sM;
             if (ls_on) {
                 const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
@@ -376,7 +412,7 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
             }
             const float inst = clampf(Er * Ec[c], 0.08f, 12.0f);
             const float t = clampf(f * frcp(den * inst + eps), -1.0e4f, 1.0e4f);
-            x[4 * k + c] = t;
+            xk[c] = t;
             if (ok) {
                 float rat, bnd, root;
                 shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
@@ -388,6 +424,7 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
             }
             sched_fence();
         }
+        stx(k, xk);
     }
     double M[13];
 #pragma unroll
@@ -402,19 +439,22 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
 #pragma unroll
     for (int k = 0; k < SR_SLOTS; ++k) {
         const bool ok = e0_of(k) < n;
+        float xk[4];
+        ldx(k, xk);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const float t = x[4 * k + c];
+            const float t = xk[c];
             float rat, bnd, root;
             shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
             const float e = t - q1;
             const float nov = ftanh(e * ns) * clip;
             const float core = cr * rat + cb * bnd + co * root + ct * t;
             const float drv = cA * core + cB + cN * nov + cD * e;
-            x[4 * k + c] = drv;
+            xk[c] = drv;
             if (ok) a_dd += drv * drv;
             sched_fence();
         }
+        stx(k, xk);
     }
     {
         double v[1] = {(double)a_dd};
@@ -429,10 +469,11 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
     for (int k = 0; k < SR_SLOTS; ++k) {
         const int64_t e0 = e0_of(k);
         if (e0 < n) {
-            float pv[4];
+            float pv[4], xk[4];
+            ldx(k, xk);
             V4<PT>::ld(p, e0, pv);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) pv[c] = pv[c] + nlr * to_f(from_w<PT>(x[4 * k + c] * gain));
+            for (int c = 0; c < 4; ++c) pv[c] = pv[c] + nlr * to_f(from_w<PT>(xk[c] * gain));
             V4<PT>::st(p, e0, pv);
         }
     }
@@ -674,19 +715,23 @@ int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec&
     } else {
         const int64_t C0 = d.ndim == 2 ? d.shape[1] : 0;
         const bool res_ok = d.ndim == 2 && same && d.param_dtype != CRESSO_F64 && aligned && n <= SR_RESIDENT_MAX && C0 % 4 == 0;
-        if (res_ok && is_pow2(C0 / 4) && C0 / 4 <= 64) {
+        // resident layouts: LDS slots first, then row factors / column partials
+        const size_t rg_lds = C0 > 0 ? SR_XLDS + ((sizeof(float) * (size_t)d.shape[0] + 15) & ~(size_t)15) +
+                                           sizeof(double) * 16 * (size_t)C0 + sizeof(float) * (size_t)C0
+                                     : 0;
+        if (res_ok && is_pow2(C0 / 4) && C0 / 4 <= 64 && rg_lds <= SR_LDS_MAX) {
             r.layout = L_ROWGROUP;
             r.group = (int32_t)(C0 / 4);
             r.rows = d.shape[0];
             r.cols = C0;
             kind = 1;
-            lds = ((sizeof(float) * (size_t)r.rows + 15) & ~(size_t)15) + sizeof(double) * 16 * (size_t)C0 + sizeof(float) * (size_t)C0;
+            lds = rg_lds;
         } else if (res_ok && C0 == (int64_t)SR_NT * 4) {
             r.layout = L_COLBLOCK;
             r.rows = d.shape[0];
             r.cols = C0;
             kind = 2;
-            lds = sizeof(float) * SR_SLOTS;
+            lds = SR_XLDS + sizeof(float) * SR_SLOTS;
         } else {
             int64_t sum = 0, maxcnt = 1, st = 1;
             for (int a = d.ndim - 1; a >= 0; --a) {
@@ -711,15 +756,31 @@ int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec&
     return CRESSO_OK;
 }
 
+// The resident kernels use more than 64 KiB of dynamic LDS: raise the
+// function's limit once (thread-safe static initialisation).
+template <typename PT, typename GT, int LAYOUT>
+hipError_t allow_resident_lds() {
+    static const hipError_t e =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&scalar_resident_kernel<PT, GT, LAYOUT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)SR_LDS_MAX);
+    return e;
+}
+
 template <typename PT, typename GT>
 hipError_t launch_resident(int kind, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
                            int32_t cnt, size_t lds, const cresso_hyper& h, hipStream_t s) {
-    if (kind == 1)
+    if (lds > SR_LDS_MAX) return hipErrorInvalidValue;
+    if (kind == 1) {
+        const hipError_t e = allow_resident_lds<PT, GT, L_ROWGROUP>();
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, L_ROWGROUP>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads,
                            first, h);
-    else
+    } else {
+        const hipError_t e = allow_resident_lds<PT, GT, L_COLBLOCK>();
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, L_COLBLOCK>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads,
                            first, h);
+    }
     return hipGetLastError();
 }
 
