@@ -310,20 +310,42 @@ __global__ __launch_bounds__(SP_FIN_NT) void ws_stats_kernel(Geom g, const ModeM
 }
 
 // Packed bins of every element (data independent; computed once per shape)
-// and exact bin counts via integer atomics.
-__global__ void ws_bins_kernel(Geom g, unsigned char* __restrict__ bins, unsigned long long* __restrict__ counts) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= g.n) return;
+// and exact bin counts: per-block u32 counts in LDS when the [T][B] table
+// fits (integer adds, so the totals do not depend on arrival order), merged
+// into the u64 totals with one global atomic per non-empty bin.
+constexpr int WS_BINS_LDS = 8192;  // u32 counters privatised per block
+__global__ __launch_bounds__(256) void ws_bins_kernel(Geom g, unsigned char* __restrict__ bins,
+                                                      unsigned long long* __restrict__ counts) {
+    __shared__ unsigned int s_cnt[WS_BINS_LDS];
+    const int TB = g.T * g.B;
+    const bool priv = TB <= WS_BINS_LDS;
+    if (priv)
+        for (int i = threadIdx.x; i < TB; i += blockDim.x) s_cnt[i] = 0u;
+    __syncthreads();
     const int64_t mask = (g.B & (g.B - 1)) == 0 ? (int64_t)g.B - 1 : -1;
-    uint64_t packed = 0;
-    for (int t = 0; t < g.T; ++t) {
-        const HashSalt s = hash_salt(t);
-        const int b = hash_bin((uint64_t)i, s, g.B, mask);
-        packed |= (uint64_t)b << (8 * g.bpb * t);
-        atomicAdd(&counts[(size_t)t * g.B + b], 1ull);
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
+        uint64_t packed = 0;
+        for (int t = 0; t < g.T; ++t) {
+            const HashSalt s = hash_salt(t);
+            const int b = hash_bin((uint64_t)i, s, g.B, mask);
+            packed |= (uint64_t)b << (8 * g.bpb * t);
+            if (priv)
+                atomicAdd(&s_cnt[t * g.B + b], 1u);
+            else
+                atomicAdd(&counts[(size_t)t * g.B + b], 1ull);
+        }
+        switch (g.binbytes) {
+            case 1: bins[i] = (unsigned char)packed; break;
+            case 2: reinterpret_cast<uint16_t*>(bins)[i] = (uint16_t)packed; break;
+            case 4: reinterpret_cast<uint32_t*>(bins)[i] = (uint32_t)packed; break;
+            default: reinterpret_cast<uint64_t*>(bins)[i] = packed; break;
+        }
     }
-    unsigned char* dst = bins + (size_t)i * g.binbytes;
-    for (int k = 0; k < g.binbytes; ++k) dst[k] = (unsigned char)(packed >> (8 * k));
+    __syncthreads();
+    if (priv)
+        for (int i = threadIdx.x; i < TB; i += blockDim.x)
+            if (s_cnt[i]) atomicAdd(&counts[i], (unsigned long long)s_cnt[i]);
 }
 
 __device__ __forceinline__ uint64_t load_bins(const unsigned char* __restrict__ bins, int64_t e, int binbytes) {
@@ -336,6 +358,39 @@ __device__ __forceinline__ uint64_t load_bins(const unsigned char* __restrict__ 
 }
 __device__ __forceinline__ int bin_of(uint64_t packed, int t, int bpb) {
     return (int)((packed >> (8 * bpb * t)) & (bpb == 1 ? 0xffull : 0xffffull));
+}
+
+// ---------------------------------------------------------------------------
+// workspace inspection (parity checks of what the sweeps consume)
+// ---------------------------------------------------------------------------
+// Bin of every element for every table, int32 [T][n].
+__global__ void ws_unpack_bins_kernel(Geom g, const unsigned char* __restrict__ bins, int32_t* __restrict__ out) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
+        const uint64_t pk = load_bins(bins, i, g.binbytes);
+        for (int t = 0; t < g.T; ++t) out[(size_t)t * g.n + i] = bin_of(pk, t, g.bpb);
+    }
+}
+
+// Normalized carriers C_r, S_r of mode r at every element, formed from the
+// row table, the column table and the closed-form stats exactly as the
+// sweeps' reconstruction coefficients combine them.
+__global__ void ws_basis_kernel(Geom g, const ModeMeta* __restrict__ meta, const float* __restrict__ rowtab,
+                                const float* __restrict__ coltab, const double* __restrict__ stats, int r,
+                                float* __restrict__ cout, float* __restrict__ sout) {
+    const ModeMeta m = meta[r];
+    const double muc = stats[4 * r], ic = stats[4 * r + 1], mus = stats[4 * r + 2], is = stats[4 * r + 3];
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
+        const int64_t row = i / g.cols, col = i - row * g.cols;
+        const float a1 = rowtab[row * g.RW + 2 * r], a2 = rowtab[row * g.RW + 2 * r + 1];
+        const float b1 = coltab[(size_t)m.k1 * g.cols + col];
+        const float b2 = m.k2 >= 0 ? coltab[(size_t)m.k2 * g.cols + col] : 0.f;
+        const float craw = m.type == M_ADD ? a1 * b1 - a2 * b2 : a1 * b1;
+        const float sraw = m.type == M_ADD ? a2 * b1 + a1 * b2 : a2 * b2;
+        cout[i] = (float)(((double)craw - muc) * ic);
+        sout[i] = (float)(((double)sraw - mus) * is);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1415,6 +1470,7 @@ struct cresso_spectral_plan {
     std::vector<int64_t> freqs;
     int64_t shape[8];
     int32_t rmax;
+    int32_t bins_off;   // hash_bins == 0: no bin tables (bins/counts hold a dummy single bin)
 };
 
 namespace cresso {
@@ -1448,6 +1504,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     g.R = rank;
     g.T = bins > 0 ? tables : 1;
     g.B = bins > 0 ? bins : 1;
+    P.bins_off = bins > 0 ? 0 : 1;
     g.bpb = g.B <= 256 ? 1 : 2;
     int bb = g.T * g.bpb;
     g.binbytes = bb <= 1 ? 1 : (bb <= 2 ? 2 : (bb <= 4 ? 4 : 8));
@@ -1715,7 +1772,8 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
     const int64_t TB = (int64_t)g.T * g.B;
     hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((TB + 255) / 256)), dim3(256), 0, s, at<unsigned long long>(ws, o.counts), TB);
     hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((TB + 255) / 256)), dim3(256), 0, s, at<unsigned long long>(ws, o.hist), TB);
-    hipLaunchKernelGGL(ws_bins_kernel, dim3((unsigned)((g.n + 255) / 256)), dim3(256), 0, s, g, at<unsigned char>(ws, o.bins),
+    const int64_t bins_blocks = std::max<int64_t>(1, std::min<int64_t>(2048, (g.n + 255) / 256));
+    hipLaunchKernelGGL(ws_bins_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g, at<unsigned char>(ws, o.bins),
                        at<unsigned long long>(ws, o.counts));
     e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -1749,4 +1807,37 @@ extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cre
     CRESSO_SP_CASE(CRESSO_F16, CRESSO_F16, __half, __half)
 #undef CRESSO_SP_CASE
     return fail(CRESSO_E_UNSUPPORTED, "spectral route: param/grad dtype pair (%d,%d) not supported by this build", pt, gt);
+}
+
+extern "C" int32_t cresso_spectral_workspace_bins(const cresso_spectral_plan* P, const void* ws, size_t ws_bytes,
+                                                  int32_t* bins_out, int64_t* counts_out, void* stream) {
+    if (!P || !ws || !bins_out || !counts_out) return fail(CRESSO_E_INVALID, "spectral route: null argument");
+    if (ws_bytes < P->o.total) return fail(CRESSO_E_INVALID, "spectral route: workspace too small");
+    const Geom& g = P->g;
+    if (P->bins_off) return fail(CRESSO_E_INVALID, "spectral route: plan has hash_bins = 0 (no bins)");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(4096, (g.n + 255) / 256));
+    hipLaunchKernelGGL(ws_unpack_bins_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g,
+                       at<unsigned char>(const_cast<void*>(ws), P->o.bins), bins_out);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(counts_out, at<unsigned long long>(const_cast<void*>(ws), P->o.counts),
+                           sizeof(int64_t) * (size_t)g.T * g.B, hipMemcpyDeviceToDevice, s);
+    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace bins");
+}
+
+extern "C" int32_t cresso_spectral_workspace_basis(const cresso_spectral_plan* P, const void* ws, size_t ws_bytes,
+                                                   int32_t mode, float* cos_out, float* sin_out, void* stream) {
+    if (!P || !ws || !cos_out || !sin_out) return fail(CRESSO_E_INVALID, "spectral route: null argument");
+    if (ws_bytes < P->o.total) return fail(CRESSO_E_INVALID, "spectral route: workspace too small");
+    const Geom& g = P->g;
+    if (mode < 0 || mode >= g.R) return fail(CRESSO_E_INVALID, "spectral route: mode %d outside 0..%d", mode, g.R - 1);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    void* w = const_cast<void*>(ws);
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(4096, (g.n + 255) / 256));
+    hipLaunchKernelGGL(ws_basis_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, at<ModeMeta>(w, P->o.meta),
+                       at<float>(w, P->o.rowtab), at<float>(w, P->o.coltab), at<double>(w, P->o.stats), mode, cos_out,
+                       sin_out);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace basis");
 }

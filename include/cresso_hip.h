@@ -163,6 +163,28 @@ typedef struct cresso_spectral_desc {
 int32_t cresso_spectral_step(const cresso_spectral_plan* plan, const cresso_spectral_desc* desc, void* workspace,
                              size_t workspace_bytes, const cresso_hyper* hyper, void* stream);
 
+/* Inspection of an initialised workspace, for parity checks (a step does not
+ * need these).
+ *
+ * cresso_spectral_workspace_bins: the coordinate-hash bin of every element
+ * for every table, exactly as the step consumes them, into bins_out (device
+ * int32 [hash_tables][numel]); the bin occupancy counts into counts_out
+ * (device int64 [hash_tables][hash_bins]).  Counterpart of the index/count
+ * half of hash_reduce_mean_cuda (cresso_cuda_kernel.cu:1222; bin function
+ * cresso_hash_index, cu:189-201) and of the reference's _hash_index_tensor
+ * (cresso_v5.py:495-516).  Fails on a plan with hash_bins = 0.
+ *
+ * cresso_spectral_workspace_basis: the normalized basis pair (C_r, S_r) of
+ * mode `mode` at every element, formed from the separable row/column tables
+ * and the closed-form stats as the step's reconstructions combine them
+ * (device fp32 [numel] each).  Counterpart of basis_axis_cache_cuda +
+ * basis_stats_with_cache_cuda (cu:842, 897) and of the reference's
+ * _basis_pair (cresso_v5.py:295-348). */
+int32_t cresso_spectral_workspace_bins(const cresso_spectral_plan* plan, const void* workspace, size_t workspace_bytes,
+                                       int32_t* bins_out, int64_t* counts_out, void* stream);
+int32_t cresso_spectral_workspace_basis(const cresso_spectral_plan* plan, const void* workspace, size_t workspace_bytes,
+                                        int32_t mode, float* cos_out, float* sin_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
