@@ -126,6 +126,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cresso_spectral_workspace_bins.restype = c.c_int32
     lib.cresso_spectral_workspace_bins.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_void_p,
                                                    c.c_void_p]
+    lib.cresso_spectral_workspace_gram.restype = c.c_int32
+    lib.cresso_spectral_workspace_gram.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_void_p]
     lib.cresso_spectral_workspace_basis.restype = c.c_int32
     lib.cresso_spectral_workspace_basis.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_int32, c.c_void_p,
                                                     c.c_void_p, c.c_void_p]

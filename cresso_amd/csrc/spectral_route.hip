@@ -85,12 +85,12 @@ struct Geom {
     int32_t RW;                        // row-table width: 2*rmax (zero beyond 2R)
     int64_t chunk1;                    // elements per block of the flat sweep (multiple of 4)
     double hs_row, hs_col;             // fixed-point scales of the axis density sums
-    int32_t binbytes, bpb, one_d, pad;
+    int32_t binbytes, bpb, one_d, nblkg;   // nblkg: blocks of the Gram pair-sum kernel
 };
 
 struct Offs {
-    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, counts, bins, tbuf, part, hist, lt, imp, alpha, rowfx, colfx,
-        rowfac, colfac, terms, ctrl, total;
+    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, bins, tbuf, part, hist, lt, imp, rowfx,
+        colfx, colfac, terms, ctrl, total;
 };
 
 // per-step device scalars (written by finalize kernels)
@@ -99,10 +99,12 @@ struct Ctrl {
     float gden, kappa;
     float rc[4][SP_MAXR][2];  // recon coefficients: 0 metric, 1 pred, 2 pred', 3 echo
     float rconst[4];
+    float wpred[2 * SP_MAXR]; // weights of the pre-contact prediction on the normalized carriers
     double hs_ds, hs_P;       // fixed-point scales of the histograms
-    float nscale, cr, cb, co, ct;
-    float dcore, dpred, dnov, derr, decho, dhp, gain;
-    float pad[3];
+    float nscale, srms;
+    // drive = k_rat rat + k_ths tanh(t/clip) + k_root root + k_t t + k_pred pred' + k_echo echo
+    //         + k_nov tanh(err' nscale) + k_hash hash_pred
+    float k_rat, k_ths, k_root, k_t, k_pred, k_echo, k_nov, k_hash, gain;
 };
 
 // state pointers of one tensor (kernel argument)
@@ -114,15 +116,10 @@ struct SpecState {
     float *hash_energy, *hash_impulse, *hash_refractory;
 };
 
-constexpr int NV1 = 1;
 constexpr int NV2 = 2 + 2 * SP_MAXR;            // sum L, sum dens, proj L (C,S)
 constexpr int NV3 = 15 + 4 * SP_MAXR;           // see sweep3
-constexpr int NV4 = 22;
+constexpr int NV4 = 3;                          // sum d^2, sum d hp, sum hp^2
 constexpr int NVMAX = NV3;
-
-__device__ __forceinline__ float uniform(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
-}
 
 // ---------------------------------------------------------------------------
 // workspace construction
@@ -219,6 +216,7 @@ __global__ void ws_coltab_kernel(Geom g, const AxisConst* __restrict__ axc, cons
         }
         coltab[(size_t)k * g.cols + c] = v;
     }
+    for (int k = g.K; k < g.KA - 1; ++k) coltab[(size_t)k * g.cols + c] = 0.f;
 }
 
 // block-wide max of two non-negative values; every thread receives them
@@ -306,6 +304,84 @@ __global__ __launch_bounds__(SP_FIN_NT) void ws_stats_kernel(Geom g, const ModeM
             }
         }
         __syncthreads();
+    }
+}
+
+// Gram matrix of the normalized basis, G[v][w] = mean over elements of
+// Xn_v Xn_w (v = 2r: C_r, v = 2r + 1: S_r), in closed form from the separable
+// tables: each raw carrier is a sum of at most two (row factor x column
+// carrier) terms, so sum_i X_v X_w is a combination of the row pair sums
+// sum_rows a_x a_y (x, y < 2R) and the column pair sums sum_cols b_k b_l
+// (k, l < K).  Pair sums are split over nblkg blocks (fixed-order partials).
+__global__ __launch_bounds__(256) void ws_pairsum_kernel(Geom g, const float* __restrict__ rowtab,
+                                                         const float* __restrict__ coltab, double* __restrict__ gpart) {
+    const int V = 2 * g.R, NA = V * V, NB = g.K * g.K;
+    const int nb = g.nblkg;
+    const int64_t r0 = g.rows * blockIdx.x / nb, r1 = g.rows * (blockIdx.x + 1) / nb;
+    const int64_t c0 = g.cols * blockIdx.x / nb, c1 = g.cols * (blockIdx.x + 1) / nb;
+    for (int p = threadIdx.x; p < NA + NB; p += blockDim.x) {
+        double s = 0.0;
+        if (p < NA) {
+            const int x = p / V, y = p - x * V;
+            for (int64_t i = r0; i < r1; ++i) s += (double)rowtab[i * g.RW + x] * (double)rowtab[i * g.RW + y];
+        } else {
+            const int q = p - NA, k = q / g.K, l = q - k * g.K;
+            for (int64_t c = c0; c < c1; ++c)
+                s += (double)coltab[(size_t)k * g.cols + c] * (double)coltab[(size_t)l * g.cols + c];
+        }
+        gpart[(size_t)blockIdx.x * (NA + NB) + p] = s;
+    }
+}
+
+// terms (sign, row factor x, column carrier k) of raw carrier v; returns the count
+__device__ int carrier_terms(const ModeMeta& m, int v, float* sg, int* x, int* k) {
+    const int r = v >> 1, c = v & 1;
+    int n = 0;
+    auto add = [&](float s_, int x_, int k_) {
+        if (k_ >= 0) { sg[n] = s_; x[n] = x_; k[n] = k_; ++n; }
+    };
+    if (m.type == M_ZERO) {
+        if (c == 0) add(1.f, 2 * r, m.k1);
+    } else if (m.type == M_ADD) {
+        if (c == 0) { add(1.f, 2 * r, m.k1); add(-1.f, 2 * r + 1, m.k2); }
+        else { add(1.f, 2 * r + 1, m.k1); add(1.f, 2 * r, m.k2); }
+    } else {
+        if (c == 0) add(1.f, 2 * r, m.k1);
+        else add(1.f, 2 * r + 1, m.k2);
+    }
+    return n;
+}
+
+__global__ __launch_bounds__(SP_FIN_NT) void ws_gram_kernel(Geom g, const ModeMeta* __restrict__ meta,
+                                                            const double* __restrict__ stats,
+                                                            const double* __restrict__ gpart, double* __restrict__ gram) {
+    const int V = 2 * g.R, NA = V * V, NB = g.K * g.K;
+    extern __shared__ double s_pair[];   // [NA + NB]
+    for (int p = threadIdx.x; p < NA + NB; p += SP_FIN_NT) {
+        double s = 0.0;
+        for (int b = 0; b < g.nblkg; ++b) s += gpart[(size_t)b * (NA + NB) + p];
+        s_pair[p] = s;
+    }
+    __syncthreads();
+    const double n = (double)g.n;
+    for (int p = threadIdx.x; p < V * V; p += SP_FIN_NT) {
+        const int v = p / V, w = p - v * V;
+        float sv[2], sw[2];
+        int xv[2], xw[2], kv[2], kw[2];
+        const int nv = carrier_terms(meta[v >> 1], v, sv, xv, kv);
+        const int nw = carrier_terms(meta[w >> 1], w, sw, xw, kw);
+        double sum = 0.0;
+        for (int i = 0; i < nv; ++i)
+            for (int j = 0; j < nw; ++j)
+                sum += (double)(sv[i] * sw[j]) * s_pair[xv[i] * V + xw[j]] * s_pair[NA + kv[i] * g.K + kw[j]];
+        // Xn = (X - mu) ic with mu the normalization shift and m the true mean
+        // of X (equal, except the constant carrier: mu = 0, m = 1):
+        // mean(Xn_v Xn_w) = ic_v ic_w (mean(X_v X_w) - mu_v m_w - mu_w m_v + mu_v mu_w)
+        const double muv = stats[4 * (v >> 1) + 2 * (v & 1)], icv = stats[4 * (v >> 1) + 2 * (v & 1) + 1];
+        const double muw = stats[4 * (w >> 1) + 2 * (w & 1)], icw = stats[4 * (w >> 1) + 2 * (w & 1) + 1];
+        const double mv = (meta[v >> 1].type == M_ZERO && (v & 1) == 0) ? 1.0 : muv;
+        const double mw = (meta[w >> 1].type == M_ZERO && (w & 1) == 0) ? 1.0 : muw;
+        gram[p] = icv * icw * (sum / n - muv * mw - muw * mv + muv * muw);
     }
 }
 
@@ -416,6 +492,24 @@ template <typename T> struct Ld4h {
 template <> struct Ld4<__half> : Ld4h<__half> {};
 template <> struct Ld4<__hip_bfloat16> : Ld4h<__hip_bfloat16> {};
 
+// 4 consecutive elements stored at e, rounded to the storage dtype
+template <typename T> struct St4;
+template <> struct St4<float> {
+    __device__ static void go(float* p, int64_t e, const float* v) {
+        *reinterpret_cast<float4*>(p + e) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+};
+template <typename T> struct St4h {
+    __device__ static void go(T* p, int64_t e, const float* v) {
+        uint2 raw;
+        T* q = reinterpret_cast<T*>(&raw);
+        q[0] = from_w<T>(v[0]); q[1] = from_w<T>(v[1]); q[2] = from_w<T>(v[2]); q[3] = from_w<T>(v[3]);
+        *reinterpret_cast<uint2*>(p + e) = raw;
+    }
+};
+template <> struct St4<__half> : St4h<__half> {};
+template <> struct St4<__hip_bfloat16> : St4h<__hip_bfloat16> {};
+
 struct Tile {
     int slab, panel;
     int64_t col, r0, r1;
@@ -481,56 +575,10 @@ __device__ __forceinline__ unsigned long long to_fixed_s(float x) {
     return x < 0.f ? (0ull - u) : u;
 }
 
-template <int KM>
-__device__ __forceinline__ void load_cols(const Geom& g, const float* __restrict__ coltab, const Tile& t, float (&b)[KM]) {
-#pragma unroll
-    for (int k = 0; k < KM; ++k) b[k] = (k < g.K && t.colok) ? coltab[(size_t)k * g.cols + t.col] : 0.f;
-}
-
-// reconstruction at (row, lane column): alpha row (wave-uniform) against the
-// lane's column carriers
-// (alpha rows are zero beyond the K live carriers and the lane's b is zero
-// there too, so the loop has no guards and the row loads vectorize)
-template <int KM>
-__device__ __forceinline__ float recon(const float* __restrict__ al, const float (&b)[KM]) {
-    float v = al[KM];
-#pragma unroll
-    for (int k = 0; k < KM; ++k) v += al[k] * b[k];
-    return v;
-}
-
-// lane contribution of a projection (Z1/Z2 accumulated over the lane's rows)
-// reduced mode by mode into partial slots base + 2r (C) and base + 2r + 1 (S)
-template <int RM, int KM>
-__device__ __forceinline__ void proj_finish(const Geom& g, const ModeMeta* __restrict__ meta, const float (&Z1)[RM],
-                                            const float (&Z2)[RM], const float (&b)[KM], Partials& P, int base) {
-#pragma unroll
-    for (int r = 0; r < RM; ++r) {
-        if (r < g.R) {
-            const ModeMeta m = meta[r];
-            float b1 = 0.f, b2 = 0.f;
-#pragma unroll
-            for (int k = 0; k < KM; ++k) {
-                if (k == m.k1) b1 = b[k];
-                if (k == m.k2) b2 = b[k];
-            }
-            float c, sn;
-            if (m.type == M_ADD) {
-                c = b1 * Z1[r] - b2 * Z2[r];
-                sn = b1 * Z2[r] + b2 * Z1[r];
-            } else {
-                c = b1 * Z1[r];
-                sn = b2 * Z2[r];
-            }
-            P.add(base + 2 * r, c);
-            P.add(base + 2 * r + 1, sn);
-        }
-    }
-}
-
-// rat = t/(1+|t|/clip), bnd = clip*tanh(t/clip), root = sign(t)*sqrt(min(|t|,clip^2)+eps)
-// (cresso_v5.py:1321-1324); rat and bnd share one reciprocal.
-__device__ __forceinline__ void shape3f(float t, float iclip, float clip, float clip2, float eps, float& rat, float& bnd,
+// rat = t/(1+|t|/clip), ths = tanh(t/clip) (bnd = clip ths),
+// root = sign(t)*sqrt(min(|t|,clip^2)+eps) (cresso_v5.py:1321-1324); rat and
+// ths share one reciprocal.
+__device__ __forceinline__ void shape3f(float t, float iclip, float clip2, float eps, float& rat, float& ths,
                                         float& root) {
     const float at = fabsf(t);
     const float ex = fexp2(-2.8853900817779268f * at * iclip);
@@ -538,7 +586,7 @@ __device__ __forceinline__ void shape3f(float t, float iclip, float clip, float 
     const float d2 = 1.0f + at * iclip;
     const float inv = frcp(d1 * d2);
     const float th = (1.0f - ex) * d2 * inv;
-    bnd = copysignf(th, t) * clip;
+    ths = copysignf(th, t);
     rat = t * d1 * inv;
     root = fsign(t) * fsqrt(fminf(at, clip2) + eps);
 }
@@ -650,29 +698,145 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin1_kernel(Geom g, const double* _
 }
 
 // ---------------------------------------------------------------------------
+// per-row data of a block's panel, staged in LDS by the block prologue
+// ---------------------------------------------------------------------------
+// Reconstruction coefficient of column carrier k at row `row` for the
+// coefficients (rc, rconst): sum over modes of the carrier factors times the
+// mode weights; k == KC is the constant.  Carriers k >= K get no mode and stay
+// zero.
+//   additive kinds: C = a1 b1 - a2 b2, S = a2 b1 + a1 b2
+//   product / constant: C = a1 b1, S = a2 b2
+template <int KC>
+__device__ __forceinline__ float alpha_coef(const Geom& g, const ModeMeta* __restrict__ meta,
+                                            const float* __restrict__ arow, const float (*rc)[2], float rconst, int k) {
+    if (k == KC) return rconst;
+    float al = 0.f;
+    for (int r = 0; r < g.R; ++r) {
+        const ModeMeta m = meta[r];
+        if (k != m.k1 && k != m.k2) continue;
+        const float wc = rc[r][0], ws = rc[r][1];
+        const float a1 = arow[2 * r], a2 = arow[2 * r + 1];
+        const float c1 = m.type == M_ADD ? wc * a1 + ws * a2 : wc * a1;
+        const float c2 = m.type == M_ADD ? ws * a1 - wc * a2 : ws * a2;
+        al += (k == m.k1 ? c1 : 0.f) + (k == m.k2 ? c2 : 0.f);
+    }
+    return al;
+}
+
+// Lane's column carriers (zero beyond K and for columns past the end).
+template <int KC>
+__device__ __forceinline__ void load_cols(const Geom& g, const float* __restrict__ coltab, const Tile& t, float (&b)[KC]) {
+#pragma unroll
+    for (int k = 0; k < KC; ++k) b[k] = t.colok ? coltab[(size_t)k * g.cols + t.col] : 0.f;
+}
+
+// reconstruction at (row, lane column): alpha row (uniform over the wave,
+// from LDS) against the lane's column carriers
+template <int KC>
+__device__ __forceinline__ float recon(const float* __restrict__ al, const float (&b)[KC]) {
+    float v = al[KC];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) v += al[k] * b[k];
+    return v;
+}
+
+// Lane contribution of a projection: Z[2q] = sum over the lane's rows of
+// a1_q(row) x, Z[2q+1] = the same with a2_q; combined with the lane's column
+// carriers into the raw C/S projections of every mode, partial slots
+// base + 2r (C) and base + 2r + 1 (S).
+template <int RM, int KC>
+__device__ __forceinline__ void proj_finish(const Geom& g, const ModeMeta* __restrict__ meta, const float (&Z)[2 * RM],
+                                            const float (&b)[KC], Partials& P, int base) {
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        if (r < g.R) {
+            const ModeMeta m = meta[r];
+            float b1 = 0.f, b2 = 0.f;
+#pragma unroll
+            for (int k = 0; k < KC; ++k) {
+                if (k == m.k1) b1 = b[k];
+                if (k == m.k2) b2 = b[k];
+            }
+            float c, sn;
+            if (m.type == M_ADD) {
+                c = b1 * Z[2 * r] - b2 * Z[2 * r + 1];
+                sn = b1 * Z[2 * r + 1] + b2 * Z[2 * r];
+            } else {
+                c = b1 * Z[2 * r];
+                sn = b2 * Z[2 * r + 1];
+            }
+            P.add(base + 2 * r, c);
+            P.add(base + 2 * r + 1, sn);
+        }
+    }
+}
+
+// Instant-metric factor of an axis marginal (cresso_v5.py:243-262):
+// exp(kappa * log(max(mean/gden, eps))), mean from a fixed-point sum.
+__device__ __forceinline__ float marg_factor(unsigned long long fx, double hs, double count, float gden, float kappa,
+                                             float eps) {
+    const float mean = (float)((double)fx / hs / count);
+    return expf(kappa * logf(fmaxf(mean / gden, eps)));
+}
+
+constexpr int SP_U = 8;  // rows whose loads are in flight together
+
+// Keeps the scheduler from interleaving the arithmetic of consecutive
+// elements (their loads are already in flight): bounds register pressure.
+__device__ __forceinline__ void elem_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Element addressing inside a block's panel: the element index of the panel's
+// first element (row r0, first column of the slab) is uniform, so each array
+// is addressed as (uniform base pointer) + (32-bit lane offset lr * cols +
+// lane); the planner keeps PR * cols below 2^29.
+__device__ __forceinline__ int64_t panel_base(const Geom& g, const Tile& t) { return t.r0 * g.cols + (int64_t)t.slab * SP_NT; }
+__device__ __forceinline__ uint32_t panel_off(const Geom& g, int lr) { return (uint32_t)lr * (uint32_t)g.cols + threadIdx.x; }
+__device__ __forceinline__ uint64_t load_bins_at(const unsigned char* __restrict__ bins, int64_t base, uint32_t off,
+                                                 int binbytes) {
+    switch (binbytes) {
+        case 1: return (bins + base)[off];
+        case 2: return (reinterpret_cast<const uint16_t*>(bins) + base)[off];
+        case 4: return (reinterpret_cast<const uint32_t*>(bins) + base)[off];
+        default: return (reinterpret_cast<const uint64_t*>(bins) + base)[off];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // S2: density field
 // ---------------------------------------------------------------------------
-template <int RM, int KM, typename PT, typename GT>
-__global__ __launch_bounds__(SP_NT) void sweep2_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
-                                                       const float* __restrict__ rowtab, const float* __restrict__ coltab,
-                                                       const ModeMeta* __restrict__ meta,
-                                                       const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
-                                                       double* __restrict__ part, unsigned long long* __restrict__ hist,
-                                                       unsigned long long* __restrict__ rowfx,
-                                                       unsigned long long* __restrict__ colfx, int hash_on, int axes_on,
-                                                       cresso_hyper h) {
+template <int RM, int KC, typename PT, typename GT>
+__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
+                                                          const float* __restrict__ rowtab, const float* __restrict__ coltab,
+                                                          const ModeMeta* __restrict__ meta,
+                                                          const unsigned char* __restrict__ bins,
+                                                          const Ctrl* __restrict__ ctrl, double* __restrict__ part,
+                                                          unsigned long long* __restrict__ hist,
+                                                          unsigned long long* __restrict__ rowfx,
+                                                          unsigned long long* __restrict__ colfx, int hash_on, int axes_on,
+                                                          cresso_hyper h) {
+    constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV2];
     const Tile t = tile_of(g);
-    // LDS: histogram [T][B] u64, wave row sums [4][PR]
-    unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
-    float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)g.T * g.B);
     const int TB = g.T * g.B;
+    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
+    const int nr = (int)(t.r1 - t.r0);
+    // LDS: histogram [T][B] u64 | row factors [PR][RW] | wave row sums [4][PR]
+    unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
+    float* s_row = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
+    float* s_wrow = s_row + (size_t)g.PR * RW;
     if (hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_hist[i] = 0ull;
+    for (int j = threadIdx.x; j < nr * RW; j += SP_NT) {
+        const int lr = j / RW, q = j - lr * RW;
+        s_row[j] = rowtab[(t.r0 + lr) * g.RW + q];
+    }
     __syncthreads();
-    float b[KM];
-    load_cols<KM>(g, coltab, t, b);
+    float b[KC];
+    load_cols<KC>(g, coltab, t, b);
+    const int64_t base = panel_base(g, t);
+    const GT* __restrict__ gb = grad + base;
+    const PT* __restrict__ pb = param + base;
     const float inv_s = ctrl->inv_s;
     const float eps = (float)h.eps;
     const float pw = (float)h.energy_power;
@@ -682,52 +846,69 @@ __global__ __launch_bounds__(SP_NT) void sweep2_kernel(Geom g, const GT* __restr
     const bool wd_on = h.weight_decay != 0.0;
     const float sg = h.maximize ? -1.f : 1.f;
     const float hs = (float)ctrl->hs_ds;
-    float Z1[RM], Z2[RM];
+    float Z[RW];
 #pragma unroll
-    for (int r = 0; r < RM; ++r) Z1[r] = Z2[r] = 0.f;
-    float aL = 0.f, aD = 0.f, colsum = 0.f;
+    for (int q = 0; q < RW; ++q) Z[q] = 0.f;
+    float aL = 0.f, aD = 0.f;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int64_t i = t.r0; i < t.r1; ++i) {
-        const int lr = (int)(i - t.r0);
-        const float* __restrict__ ar = rowtab + i * g.RW;
-        float dens = 0.f;
-        if (t.colok) {
-            const int64_t e = i * g.cols + t.col;
-            float f = sg * ld(grad, e);
-            if (wd_on) f = f + wd * ld(param, e);
-            const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
-            const float ds = fpow(rel, pw);
-            const float L = flog1p(ds);
-            const float rl = fmaxf(rel, eps);
-            dens = fminf(ip_one ? rl : fpow(rl, ipw), 1.0e6f);
-            aL += L;
-            aD += dens;
-            colsum += dens;
+    for (int i0 = 0; i0 < nr; i0 += SP_U) {
+        float gv[SP_U], pv[SP_U];
+        uint64_t bv[SP_U];
 #pragma unroll
-            for (int q = 0; q < RM; ++q) {
-                Z1[q] += ar[2 * q] * L;
-                Z2[q] += ar[2 * q + 1] * L;
-            }
-            if (hash_on) {
-                const uint64_t pk = load_bins(bins, e, g.binbytes);
-                const unsigned long long v = to_fixed_u(ds * hs);
-                for (int tt = 0; tt < g.T; ++tt) atomicAdd(&s_hist[tt * g.B + bin_of(pk, tt, g.bpb)], v);
+        for (int u = 0; u < SP_U; ++u) {
+            gv[u] = 0.f;
+            pv[u] = 0.f;
+            bv[u] = 0;
+            if (i0 + u < nr && t.colok) {
+                const uint32_t o = panel_off(g, i0 + u);
+                gv[u] = to_f(gb[o]);
+                if (wd_on) pv[u] = to_f(pb[o]);
+                if (hash_on) bv[u] = load_bins_at(bins, base, o, binbytes);
             }
         }
-        if (axes_on) {
-            const float ws = wave_total(dens);
-            if (lane == 63) s_wrow[wave * g.PR + lr] = ws;
+#pragma unroll
+        for (int u = 0; u < SP_U; ++u) {
+            const int lr = i0 + u;
+            if (lr >= nr) break;
+            float dens = 0.f;
+            if (t.colok) {
+                float f = sg * gv[u];
+                if (wd_on) f = f + wd * pv[u];
+                const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
+                const float ds = fpow(rel, pw);
+                const float L = flog1p(ds);
+                const float rl = fmaxf(rel, eps);
+                dens = fminf(ip_one ? rl : fpow(rl, ipw), 1.0e6f);
+                aL += L;
+                aD += dens;
+                const float* __restrict__ ar = s_row + lr * RW;
+#pragma unroll
+                for (int q = 0; q < RW; ++q) Z[q] += ar[q] * L;
+                if (hash_on) {
+                    const unsigned long long v = to_fixed_u(ds * hs);
+#pragma unroll
+                    for (int tt = 0; tt < SP_MAXT; ++tt) {
+                        if (tt >= T) break;
+                        atomicAdd(&s_hist[tt * B + bin_of(bv[u], tt, bpb)], v);
+                    }
+                }
+            }
+            if (axes_on) {
+                const float ws = wave_total(dens);
+                if (lane == 63) s_wrow[wave * g.PR + lr] = ws;
+            }
+            elem_fence();
         }
     }
     __syncthreads();
     if (axes_on) {
         // axis density sums: one fixed-point atomic per row of this slab and per column of this panel
-        for (int lr = threadIdx.x; lr < (int)(t.r1 - t.r0); lr += SP_NT) {
+        for (int lr = threadIdx.x; lr < nr; lr += SP_NT) {
             float s = 0.f;
             for (int w = 0; w < SP_NT / 64; ++w) s += s_wrow[w * g.PR + lr];
             atomicAdd(&rowfx[t.r0 + lr], to_fixed_u(s * (float)g.hs_row));
         }
-        if (t.colok) atomicAdd(&colfx[t.col], to_fixed_u(colsum * (float)g.hs_col));
+        if (t.colok) atomicAdd(&colfx[t.col], to_fixed_u(aD * (float)g.hs_col));
     }
     if (hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT)
@@ -735,76 +916,50 @@ __global__ __launch_bounds__(SP_NT) void sweep2_kernel(Geom g, const GT* __restr
     Partials P{red, 2 + 2 * g.R};
     P.add(0, aL);
     P.add(1, aD);
-    proj_finish<RM, KM>(g, meta, Z1, Z2, b, P, 2);
+    proj_finish<RM, KC>(g, meta, Z, b, P, 2);
     P.flush(part, g.nblk);
 }
 
 // ---------------------------------------------------------------------------
 // F2: hash metric, metric oscillator, recon coefficients
 // ---------------------------------------------------------------------------
-// Coefficients (wc, ws) per mode and the constant of
+// Mode weights (the coefficient of each normalized carrier) and the
+// coefficients (wc, ws) per mode and constant of
 //   shrink * sum_r g_r (cc_r Cn_r + sc_r Sn_r)  (cresso_v5.py:362-376)
 // with Cn = (Craw - mu_c) ic; a gate of exactly 0 drops the mode.
 __device__ void set_recon(const Geom& g, const double* stats, float (*rc)[2], float& rconst, const float* cc,
-                          const float* sc, const float* gates) {
+                          const float* sc, const float* gates, float* weights = nullptr) {
     const double shrink = 1.0 / sqrt(fmax(1.0, 0.7 * log2((double)g.R + 1.0)));
     float cst = 0.f;
     for (int r = 0; r < g.R; ++r) {
         const float gate = gates ? gates[r] : 1.0f;
-        float wc = 0.f, ws = 0.f;
+        float wc = 0.f, ws = 0.f, kc = 0.f, ks = 0.f;
         if (gate != 0.0f) {
-            const float kc = (float)((double)cc[r] * shrink) * gate;
-            const float ks = (float)((double)sc[r] * shrink) * gate;
+            kc = (float)((double)cc[r] * shrink) * gate;
+            ks = (float)((double)sc[r] * shrink) * gate;
             wc = (float)((double)kc * stats[4 * r + 1]);
             ws = (float)((double)ks * stats[4 * r + 3]);
             cst -= (float)((double)wc * stats[4 * r + 0] + (double)ws * stats[4 * r + 2]);
         }
         rc[r][0] = wc;
         rc[r][1] = ws;
+        if (weights) {
+            weights[2 * r] = kc;
+            weights[2 * r + 1] = ks;
+        }
     }
     rconst = cst;
-}
-
-// alpha[row][k] = sum of the coefficients of reconstruction `w` that multiply
-// column carrier k at this row (zero for k >= K), alpha[row][KM] = constant.
-// One thread per row; reconstructions w0 .. w0+count-1.
-template <int RM>
-__global__ void alpha_kernel(Geom g, const ModeMeta* __restrict__ meta, const float* __restrict__ rowtab,
-                             const Ctrl* __restrict__ ctrl, int w0, int count, float* __restrict__ alpha) {
-    constexpr int KM = 2 * RM + 1;
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= g.rows) return;
-    for (int w = w0; w < w0 + count; ++w) {
-        float al[KM + 1];
-#pragma unroll
-        for (int k = 0; k < KM; ++k) al[k] = 0.f;
-        al[KM] = ctrl->rconst[w];
-        for (int r = 0; r < g.R; ++r) {
-            const ModeMeta m = meta[r];
-            const float wc = ctrl->rc[w][r][0], ws = ctrl->rc[w][r][1];
-            const float a1 = rowtab[i * g.RW + 2 * r], a2 = rowtab[i * g.RW + 2 * r + 1];
-            // additive: C = a1 b1 - a2 b2, S = a2 b1 + a1 b2; product/constant: C = a1 b1, S = a2 b2
-            const float c1 = m.type == M_ADD ? wc * a1 + ws * a2 : wc * a1;
-            const float c2 = m.type == M_ADD ? ws * a1 - wc * a2 : ws * a2;
-#pragma unroll
-            for (int k = 0; k < KM; ++k) al[k] += (k == m.k1 ? c1 : 0.f) + (k == m.k2 ? c2 : 0.f);
-        }
-        float* dst = alpha + ((size_t)w * g.rows + i) * g.KA;
-#pragma unroll
-        for (int k = 0; k <= KM; ++k) dst[k] = al[k];
-    }
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 __global__ __launch_bounds__(SP_FIN_NT) void fin2_kernel(Geom g, const ModeMeta* __restrict__ meta,
                                                          const double* __restrict__ stats, const double* __restrict__ bounds,
-                                                         const float* __restrict__ rowtab, const double* __restrict__ part,
+                                                         const double* __restrict__ part,
                                                          unsigned long long* __restrict__ hist,
                                                          const unsigned long long* __restrict__ counts,
-                                                         float* __restrict__ lt, float* __restrict__ alpha, SpecState st,
-                                                         Ctrl* __restrict__ ctrl, int step, int hash_on, int hard,
-                                                         cresso_hyper h) {
+                                                         float* __restrict__ lt, SpecState st, Ctrl* __restrict__ ctrl,
+                                                         int step, int hash_on, int hard, cresso_hyper h) {
     __shared__ double s_v[NV2];
     __shared__ double red[16];
     __shared__ float s_emean[SP_MAXT];
@@ -903,7 +1058,7 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin2_kernel(Geom g, const ModeMeta*
             gt[r] = sigmoidf_((float)h.confidence_gain * s_f[r][7]);
             pmax += shrink * gt[r] * (fabs((double)qc[r]) * s_st[r][4] + fabs((double)qs[r]) * s_st[r][5]);
         }
-        set_recon(g, stt, ctrl->rc[1], ctrl->rconst[1], qc, qs, gt);
+        set_recon(g, stt, ctrl->rc[1], ctrl->rconst[1], qc, qs, gt, ctrl->wpred);
         // instant metric: mean density and coupling (cresso_v5.py:243-262)
         ctrl->gden = (float)fmax(sumD / n, (double)eps);
         const float icoup = hard ? (float)h.instant_metric_coupling : 0.0f;
@@ -919,23 +1074,6 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin2_kernel(Geom g, const ModeMeta*
         st.metric_p_cos[r] = s_f[r][2];
         st.metric_sin[r] = s_f[r][3];
         st.metric_p_sin[r] = s_f[r][4];
-    }
-}
-
-// M1: instant-metric factors (cresso_v5.py:243-262) from the fixed-point axis
-// density sums: rows always; columns directly for 2-D tensors.
-__global__ void marg_kernel(Geom g, const unsigned long long* __restrict__ rowfx,
-                            const unsigned long long* __restrict__ colfx, float* __restrict__ rowfac,
-                            float* __restrict__ colfac, const Ctrl* __restrict__ ctrl, float eps) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const float gden = ctrl->gden, kappa = ctrl->kappa;
-    if (i < g.rows) {
-        const float mean = (float)((double)rowfx[i] / g.hs_row / (double)g.cols);
-        rowfac[i] = expf(kappa * logf(fmaxf(mean / gden, eps)));
-    } else if (g.ntrail == 1 && i < g.rows + g.cols) {
-        const int64_t c = i - g.rows;
-        const float mean = (float)((double)colfx[c] / g.hs_col / (double)g.rows);
-        colfac[c] = expf(kappa * logf(fmaxf(mean / gden, eps)));
     }
 }
 
@@ -963,49 +1101,71 @@ __global__ __launch_bounds__(SP_FIN_NT) void marg_axes_kernel(Geom g, const unsi
     }
     __syncthreads();
     for (int64_t c = threadIdx.x; c < g.cols; c += SP_FIN_NT) {
-        float ls = 0.f;
-        int64_t rem = c, o2 = 0;
-        int64_t coord[8];
+        int64_t rem = c;
+        float acc = 0.f;
+        int64_t o2 = off;
         for (int a = g.ntrail - 1; a >= 0; --a) {
-            coord[a] = rem % g.tdim[a];
+            o2 -= g.tdim[a];
+            const int64_t k = rem % g.tdim[a];
             rem /= g.tdim[a];
+            acc += terms[o2 + k];
         }
-        for (int a = 0; a < g.ntrail; ++a) {
-            ls += terms[o2 + coord[a]];
-            o2 += g.tdim[a];
-        }
-        colfac[c] = expf(ls);
+        colfac[c] = expf(acc);
     }
 }
 
 // ---------------------------------------------------------------------------
-// S3: tangent force, prediction error, port projection / histograms, echo
+// S3: tangent force, prediction error, port projection / histograms, t projection
 // ---------------------------------------------------------------------------
-template <int RM, int KM, typename PT, typename GT>
-__global__ __launch_bounds__(SP_NT) void sweep3_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
-                                                       const float* __restrict__ rowtab, const float* __restrict__ coltab,
-                                                       const ModeMeta* __restrict__ meta,
-                                                       const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
-                                                       const float* __restrict__ lt, const float* __restrict__ alpha,
-                                                       const float* __restrict__ rowfac, const float* __restrict__ colfac,
-                                                       float* __restrict__ tbuf, double* __restrict__ part,
-                                                       unsigned long long* __restrict__ hist, int hash_on, int echo_on,
-                                                       cresso_hyper h) {
+template <int RM, int KC, typename PT, typename GT>
+__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
+                                                          const float* __restrict__ rowtab, const float* __restrict__ coltab,
+                                                          const ModeMeta* __restrict__ meta,
+                                                          const unsigned char* __restrict__ bins,
+                                                          const Ctrl* __restrict__ ctrl, const float* __restrict__ lt,
+                                                          const unsigned long long* __restrict__ rowfx,
+                                                          const unsigned long long* __restrict__ colfx,
+                                                          const float* __restrict__ colfac, float* __restrict__ tbuf,
+                                                          double* __restrict__ part, unsigned long long* __restrict__ hist,
+                                                          int hash_on, cresso_hyper h) {
+    constexpr int RW = 2 * RM, KA = KC + 1;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV3];
     const Tile t = tile_of(g);
     const int TB = g.T * g.B;
+    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
+    const int nr = (int)(t.r1 - t.r0);
+    // LDS: histogram [T][B] u64 | log hash metric [T][B] | alpha [PR][2][KA] | row factors [PR][RW] | row metric [PR]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
     float* s_lt = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
+    float* s_al = s_lt + TB;
+    float* s_row = s_al + (size_t)g.PR * 2 * KA;
+    float* s_rf = s_row + (size_t)g.PR * RW;
+    const float eps = (float)h.eps;
+    const float kappa = ctrl->kappa, gden = ctrl->gden;
+    const bool inst_on = kappa != 0.0f;
     if (hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) {
             s_hist[i] = 0ull;
             s_lt[i] = lt[i];
         }
+    for (int j = threadIdx.x; j < nr * 2 * KA; j += SP_NT) {
+        const int lr = j / (2 * KA), w = (j / KA) & 1, k = j % KA;
+        s_al[j] = alpha_coef<KC>(g, meta, rowtab + (t.r0 + lr) * g.RW, ctrl->rc[w], ctrl->rconst[w], k);
+    }
+    for (int j = threadIdx.x; j < nr * RW; j += SP_NT) {
+        const int lr = j / RW, q = j - lr * RW;
+        s_row[j] = rowtab[(t.r0 + lr) * g.RW + q];
+    }
+    for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
+        s_rf[lr] = (inst_on && !g.one_d) ? marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps) : 1.0f;
     __syncthreads();
-    float b[KM];
-    load_cols<KM>(g, coltab, t, b);
-    const float eps = (float)h.eps;
+    float b[KC];
+    load_cols<KC>(g, coltab, t, b);
+    const int64_t base = panel_base(g, t);
+    const GT* __restrict__ gb = grad + base;
+    const PT* __restrict__ pb = param + base;
+    float* __restrict__ tb = tbuf + base;
     const float inv_s = ctrl->inv_s, scale = ctrl->scale;
     const float mcoup = (float)h.metric_coupling;
     const float wd = (float)h.weight_decay;
@@ -1013,82 +1173,100 @@ __global__ __launch_bounds__(SP_NT) void sweep3_kernel(Geom g, const GT* __restr
     const float sg = h.maximize ? -1.f : 1.f;
     const bool ls_on = h.local_sharpness != 0.0;
     const float ls = (float)h.local_sharpness;
-    const float kappa = ctrl->kappa, gden = ctrl->gden;
-    const bool inst_on = kappa != 0.0f;
     const float ipw = (float)fmax(h.instant_metric_power, 0.25);
-    const float ec = inst_on && !g.one_d && t.colok ? colfac[t.col] : 1.0f;
-    const float invT = 1.0f / (float)g.T;
+    float ec = 1.0f;
+    if (inst_on && !g.one_d && t.colok)
+        ec = g.ntrail == 1 ? marg_factor(colfx[t.col], g.hs_col, (double)g.rows, gden, kappa, eps) : colfac[t.col];
+    const float invT = 1.0f / (float)T;
     const float tm = (float)h.transport_mix;
     const float hs = (float)ctrl->hs_P;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
-    const float* __restrict__ alM = alpha;
-    const float* __restrict__ alP = alpha + (size_t)g.rows * g.KA;
-    float ZP1[RM], ZP2[RM], ZT1[RM], ZT2[RM];
+    float ZP[RW], ZT[RW];
 #pragma unroll
-    for (int r = 0; r < RM; ++r) ZP1[r] = ZP2[r] = ZT1[r] = ZT2[r] = 0.f;
+    for (int q = 0; q < RW; ++q) ZP[q] = ZT[q] = 0.f;
     float m_ee = 0.f, m_P = 0.f, m_t = 0.f, m_tt = 0.f, m_rr = 0.f, m_bb = 0.f, m_oo = 0.f, m_rb = 0.f, m_ro = 0.f,
           m_bo = 0.f, m_tr = 0.f, m_tb = 0.f, m_to = 0.f;
     if (t.colok) {
-        for (int64_t i = t.r0; i < t.r1; ++i) {
-            const int64_t e = i * g.cols + t.col;
-            float f = sg * ld(grad, e);
-            if (wd_on) f = f + wd * ld(param, e);
-            // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
-            const float lm = clampf(recon<KM>(alM + i * g.KA, b), -3.0f, 3.0f);
-            const float M = clampf(fexp(mcoup * lm), 0.06f, 16.0f);
-            float den = scale * M;
-            if (ls_on) {
-                const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
-                den = den * clampf(1.0f + ls * fsqrt(fminf(rel, 100.0f)), 1.0f, 8.0f);
-            }
-            if (inst_on) {
-                float I;
-                if (g.one_d) {
-                    const float rel = fmaxf(fminf(fabsf(f) * inv_s + eps, 1.0e4f), eps);
-                    const float dens = fminf(ipw == 1.0f ? rel : fpow(rel, ipw), 1.0e6f);
-                    I = fexp(kappa * flog(fmaxf(dens / gden, eps)));
-                } else {
-                    I = rowfac[i] * ec;
-                }
-                den = den * clampf(I, 0.08f, 12.0f);
-            }
-            uint64_t pk = 0;
-            if (hash_on) {
-                pk = load_bins(bins, e, g.binbytes);
-                float ls_ = 0.f;
-                for (int tt = 0; tt < g.T; ++tt) ls_ += s_lt[tt * g.B + bin_of(pk, tt, g.bpb)];
-                den = den * clampf(fexp(ls_ * invT), 0.08f, 12.0f);
-            }
-            const float tv = clampf(f * frcp(den + eps), -1.0e4f, 1.0e4f);
-            tbuf[e] = tv;
-            const float pred = recon<KM>(alP + i * g.KA, b);
-            const float err = tv - pred;
-            const float P = err + tm * tv;
-            m_ee += err * err;
-            m_P += P;
-            m_t += tv;
-            m_tt += tv * tv;
-            float rat, bnd, root;
-            shape3f(tv, iclip, clip, clip2, eps, rat, bnd, root);
-            m_rr += rat * rat; m_bb += bnd * bnd; m_oo += root * root;
-            m_rb += rat * bnd; m_ro += rat * root; m_bo += bnd * root;
-            m_tr += tv * rat; m_tb += tv * bnd; m_to += tv * root;
-            const float* __restrict__ ar = rowtab + i * g.RW;
+        for (int i0 = 0; i0 < nr; i0 += SP_U) {
+            float gv[SP_U], pv[SP_U];
+            uint64_t bv[SP_U];
 #pragma unroll
-            for (int q = 0; q < RM; ++q) {
-                ZP1[q] += ar[2 * q] * P;
-                ZP2[q] += ar[2 * q + 1] * P;
-            }
-            if (echo_on) {
-#pragma unroll
-                for (int q = 0; q < RM; ++q) {
-                    ZT1[q] += ar[2 * q] * tv;
-                    ZT2[q] += ar[2 * q + 1] * tv;
+            for (int u = 0; u < SP_U; ++u) {
+                gv[u] = 0.f;
+                pv[u] = 0.f;
+                bv[u] = 0;
+                if (i0 + u < nr) {
+                    const uint32_t o = panel_off(g, i0 + u);
+                    gv[u] = to_f(gb[o]);
+                    if (wd_on) pv[u] = to_f(pb[o]);
+                    if (hash_on) bv[u] = load_bins_at(bins, base, o, binbytes);
                 }
             }
-            if (hash_on) {
-                const unsigned long long v = to_fixed_s(P * hs);
-                for (int tt = 0; tt < g.T; ++tt) atomicAdd(&s_hist[tt * g.B + bin_of(pk, tt, g.bpb)], v);
+#pragma unroll
+            for (int u = 0; u < SP_U; ++u) {
+                const int lr = i0 + u;
+                if (lr >= nr) break;
+                float f = sg * gv[u];
+                if (wd_on) f = f + wd * pv[u];
+                const float* __restrict__ al = s_al + lr * 2 * KA;
+                // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
+                const float lm = clampf(recon<KC>(al, b), -3.0f, 3.0f);
+                const float M = clampf(fexp(mcoup * lm), 0.06f, 16.0f);
+                float den = scale * M;
+                if (ls_on) {
+                    const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
+                    den = den * clampf(1.0f + ls * fsqrt(fminf(rel, 100.0f)), 1.0f, 8.0f);
+                }
+                if (inst_on) {
+                    float I;
+                    if (g.one_d) {
+                        const float rel = fmaxf(fminf(fabsf(f) * inv_s + eps, 1.0e4f), eps);
+                        const float dens = fminf(ipw == 1.0f ? rel : fpow(rel, ipw), 1.0e6f);
+                        I = fexp(kappa * flog(fmaxf(dens / gden, eps)));
+                    } else {
+                        I = s_rf[lr] * ec;
+                    }
+                    den = den * clampf(I, 0.08f, 12.0f);
+                }
+                if (hash_on) {
+                    float lsum = 0.f;
+#pragma unroll
+                    for (int tt = 0; tt < SP_MAXT; ++tt) {
+                        if (tt >= T) break;
+                        lsum += s_lt[tt * B + bin_of(bv[u], tt, bpb)];
+                    }
+                    den = den * clampf(fexp(lsum * invT), 0.08f, 12.0f);
+                }
+                const float tv = clampf(f * frcp(den + eps), -1.0e4f, 1.0e4f);
+                tb[panel_off(g, lr)] = tv;
+                const float pred = recon<KC>(al + KA, b);
+                const float err = tv - pred;
+                const float P = err + tm * tv;
+                m_ee += err * err;
+                m_P += P;
+                m_t += tv;
+                m_tt += tv * tv;
+                float rat, ths, root;
+                shape3f(tv, iclip, clip2, eps, rat, ths, root);
+                const float bnd = ths * clip;
+                m_rr += rat * rat; m_bb += bnd * bnd; m_oo += root * root;
+                m_rb += rat * bnd; m_ro += rat * root; m_bo += bnd * root;
+                m_tr += tv * rat; m_tb += tv * bnd; m_to += tv * root;
+                const float* __restrict__ ar = s_row + lr * RW;
+#pragma unroll
+                for (int q = 0; q < RW; ++q) {
+                    ZP[q] += ar[q] * P;
+                    ZT[q] += ar[q] * tv;
+                }
+                if (hash_on) {
+                    const unsigned long long v = to_fixed_s(P * hs);
+#pragma unroll
+                    for (int tt = 0; tt < SP_MAXT; ++tt) {
+                        if (tt >= T) break;
+                        atomicAdd(&s_hist[tt * B + bin_of(bv[u], tt, bpb)], v);
+                    }
+                }
+                elem_fence();
             }
         }
     }
@@ -1102,13 +1280,14 @@ __global__ __launch_bounds__(SP_NT) void sweep3_kernel(Geom g, const GT* __restr
     for (int k = 0; k < 13; ++k) P.add(k, mm[k]);
     P.add(13, 0.f);
     P.add(14, 0.f);
-    proj_finish<RM, KM>(g, meta, ZP1, ZP2, b, P, 15);
-    proj_finish<RM, KM>(g, meta, ZT1, ZT2, b, P, 15 + 2 * g.R);
+    proj_finish<RM, KC>(g, meta, ZP, b, P, 15);
+    proj_finish<RM, KC>(g, meta, ZT, b, P, 15 + 2 * g.R);
     P.flush(part, g.nblk);
 }
 
 // ---------------------------------------------------------------------------
-// F3: surprise, hash impulse, confidence, contact, core coefficients
+// F3: surprise, hash impulse, confidence, contact, and every drive-shaping
+// coefficient that does not need the hash prediction's rms
 // ---------------------------------------------------------------------------
 __device__ void contact_bank(float* q, float* p, const float* port, const float* omega, float* calcium, float& action,
                              float S, int R, const cresso_hyper& h) {
@@ -1144,19 +1323,31 @@ __device__ void contact_bank(float* q, float* p, const float* port, const float*
     }
 }
 
+// The drive (cresso_v5.py:1303-1353) is
+//   c0 core + c1 pred' + c2 nov + c3 err' + c4 echo + c5 hash
+// with core = cr rat + cb bnd + co root + ct t.  Every c except c5 depends on
+// rms values that are closed forms of this step's sweep-3 sums:
+//   * mean(core^2): a quadratic form in the 13 moments of t;
+//   * mean(pred'^2), mean(echo^2): u^T G u over the Gram matrix G of the
+//     normalized basis (pred' and echo are reconstructions with weights u);
+//   * mean(t pred') = sum_v u'_v mean(t Xn_v) (the t projection);
+//   * mean(err'^2) = mean(err^2) - 2 mean(err D) + mean(D^2), D = pred' - pred
+//     a reconstruction with weights du = u' - u, mean(err Xn_v) =
+//     mean(t Xn_v) - (G u)_v: small corrections to a directly summed term.
+// So sweep 4 can write the drive without c5; the hash term's rms comes from
+// sweep 4's sums and is added in sweep 5.
 __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                         const double* __restrict__ stats, const float* __restrict__ rowtab,
+                                                         const double* __restrict__ stats, const double* __restrict__ gram,
                                                          const double* __restrict__ part,
                                                          unsigned long long* __restrict__ hist,
                                                          const unsigned long long* __restrict__ counts,
-                                                         float* __restrict__ imp_tab, float* __restrict__ alpha,
-                                                         SpecState st, Ctrl* __restrict__ ctrl, int step, int hash_on,
-                                                         int hard, int echo_on, cresso_hyper h,
-                                                         double* __restrict__ moments) {
+                                                         float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
+                                                         int step, int hash_on, int hard, int echo_on, cresso_hyper h) {
     __shared__ double s_m[NV3];
     const int tid = threadIdx.x;
     const double n = (double)g.n;
-    reduce_all(part, g.nblk, 15 + 4 * g.R, s_m);
+    const int R = g.R, V = 2 * g.R;
+    reduce_all(part, g.nblk, 15 + 4 * R, s_m);
     const float eps = (float)h.eps;
     // hash refractory / impulse (cresso_v5.py:1140-1184)
     if (hash_on) {
@@ -1176,7 +1367,10 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta*
     __shared__ double s_st[SP_MAXR][4];
     __shared__ float s_f[SP_MAXR][9];
     __shared__ float s_sc[2];
-    if (tid < g.R) {
+    __shared__ double s_ec[2 * SP_MAXR];   // mean(t Xn_v)
+    __shared__ double s_u[3][2 * SP_MAXR]; // weights of pred, pred', echo
+    __shared__ double s_q[2 * SP_MAXR][5];
+    if (tid < R) {
         const int r = tid;
         for (int j = 0; j < 4; ++j) s_st[r][j] = stats[4 * r + j];
         s_f[r][0] = st.omega[r];
@@ -1187,6 +1381,12 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta*
         s_f[r][5] = st.calcium_cos[r];
         s_f[r][6] = st.calcium_sin[r];
         s_f[r][7] = st.conf[r];
+    }
+    if (tid < V) {
+        const int r = tid >> 1, c = tid & 1;
+        const double mu = stats[4 * r + 2 * c], ic = stats[4 * r + 2 * c + 1];
+        s_ec[tid] = (s_m[15 + 2 * R + tid] - mu * s_m[2]) * ic / n;
+        s_u[0][tid] = (double)ctrl->wpred[tid];
     }
     if (tid == 0) {
         s_sc[0] = *st.surprise;
@@ -1199,26 +1399,26 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta*
         const float sur = reservoir_f(s_sc[0], sqrtf((float)(s_m[0] / n) + eps), h.surprise_decay, step);
         s_sc[0] = sur;
         double stt[4 * SP_MAXR];
-        for (int r = 0; r < g.R; ++r)
+        for (int r = 0; r < R; ++r)
             for (int j = 0; j < 4; ++j) stt[4 * r + j] = s_st[r][j];
         // port and echo projections -> mean(x Cn)
         float pc[SP_MAXR], ps[SP_MAXR], ecs[SP_MAXR], ess[SP_MAXR];
-        for (int r = 0; r < g.R; ++r) {
+        for (int r = 0; r < R; ++r) {
             const double mc = s_st[r][0], ic = s_st[r][1], ms = s_st[r][2], is = s_st[r][3];
             pc[r] = (float)((s_m[15 + 2 * r] - mc * sP) * ic / n);
             ps[r] = (float)((s_m[16 + 2 * r] - ms * sP) * is / n);
-            ecs[r] = (float)((s_m[15 + 2 * g.R + 2 * r] - mc * sT) * ic / n);
-            ess[r] = (float)((s_m[16 + 2 * g.R + 2 * r] - ms * sT) * is / n);
+            ecs[r] = (float)((s_m[15 + 2 * R + 2 * r] - mc * sT) * ic / n);
+            ess[r] = (float)((s_m[16 + 2 * R + 2 * r] - ms * sT) * is / n);
         }
         float om[SP_MAXR], qc[SP_MAXR], qs[SP_MAXR], pcv[SP_MAXR], psv[SP_MAXR], cac[SP_MAXR], cas[SP_MAXR];
-        for (int r = 0; r < g.R; ++r) {
+        for (int r = 0; r < R; ++r) {
             om[r] = s_f[r][0]; qc[r] = s_f[r][1]; qs[r] = s_f[r][2]; pcv[r] = s_f[r][3]; psv[r] = s_f[r][4];
             cac[r] = s_f[r][5]; cas[r] = s_f[r][6];
         }
         // confidence (cresso_v5.py:1199-1202) with the pre-contact q
         const float cd = (float)h.confidence_decay;
         float gt[SP_MAXR];
-        for (int r = 0; r < g.R; ++r) {
+        for (int r = 0; r < R; ++r) {
             const float pe = sqrtf(pc[r] * pc[r] + ps[r] * ps[r] + eps);
             const float sup = (pc[r] * qc[r] + ps[r] * qs[r]) / (pe * sqrtf(qc[r] * qc[r] + qs[r] * qs[r] + eps) + eps);
             const float c = s_f[r][7] * cd + (float)(1.0 - h.confidence_decay) * clampf(sup, -1.0f, 1.0f);
@@ -1227,20 +1427,49 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta*
         }
         // contact on the cos bank then the sin bank with the shared action
         float action = s_sc[1];
-        contact_bank(qc, pcv, pc, om, cac, action, sur, g.R, h);
-        contact_bank(qs, psv, ps, om, cas, action, sur, g.R, h);
+        contact_bank(qc, pcv, pc, om, cac, action, sur, R, h);
+        contact_bank(qs, psv, ps, om, cas, action, sur, R, h);
         s_sc[1] = action;
-        for (int r = 0; r < g.R; ++r) {
+        for (int r = 0; r < R; ++r) {
             s_f[r][1] = qc[r]; s_f[r][2] = qs[r]; s_f[r][3] = pcv[r]; s_f[r][4] = psv[r];
             s_f[r][5] = cac[r]; s_f[r][6] = cas[r];
         }
-        set_recon(g, stt, ctrl->rc[2], ctrl->rconst[2], qc, qs, gt);
-        if (echo_on) set_recon(g, stt, ctrl->rc[3], ctrl->rconst[3], ecs, ess, nullptr);
-        // drive shaping coefficients that depend only on moments of t
-        // (cresso_v5.py:1303-1337): shaped = ar rat + ab bnd + ao root,
-        // core = (1-dmix) shaped + dmix t srms/max(frms,eps)
+        float wp[2 * SP_MAXR], we[2 * SP_MAXR];
+        set_recon(g, stt, ctrl->rc[2], ctrl->rconst[2], qc, qs, gt, wp);
+        for (int v = 0; v < V; ++v) we[v] = 0.f;
+        if (echo_on) set_recon(g, stt, ctrl->rc[3], ctrl->rconst[3], ecs, ess, nullptr, we);
+        for (int v = 0; v < V; ++v) {
+            s_u[1][v] = (double)wp[v];
+            s_u[2][v] = (double)we[v];
+        }
+    }
+    __syncthreads();
+    // Gram products, one thread per carrier v
+    if (tid < V) {
+        const int v = tid;
+        double gu = 0.0, gup = 0.0, gue = 0.0;
+        for (int w = 0; w < V; ++w) {
+            const double gvw = gram[v * V + w];
+            gu += gvw * s_u[0][w];
+            gup += gvw * s_u[1][w];
+            gue += gvw * s_u[2][w];
+        }
+        const double du = s_u[1][v] - s_u[0][v];
+        s_q[v][0] = s_u[1][v] * gup;            // -> mean(pred'^2)
+        s_q[v][1] = s_u[2][v] * gue;            // -> mean(echo^2)
+        s_q[v][2] = du * (gup - gu);            // -> mean(D^2)
+        s_q[v][3] = du * (s_ec[v] - gu);        // -> mean(err D)
+        s_q[v][4] = s_u[1][v] * s_ec[v];        // -> mean(t pred')
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double q[5] = {0, 0, 0, 0, 0};
+        for (int v = 0; v < V; ++v)
+            for (int j = 0; j < 5; ++j) q[j] += s_q[v][j];
+        const float S = s_sc[0];
+        // shaped / core coefficients from the moments of t (cresso_v5.py:1315-1337)
         const double Stt = s_m[3], Srr = s_m[4], Sbb = s_m[5], Soo = s_m[6], Srb = s_m[7], Sro = s_m[8], Sbo = s_m[9];
-        const float S = sur;
+        const double Str = s_m[10], Stb = s_m[11], Sto = s_m[12];
         const float frms = sqrtf((float)(Stt / n) + eps);
         const float rms_rat = sqrtf((float)(Srr / n) + eps);
         const float rms_root = sqrtf((float)(Soo / n) + eps);
@@ -1254,17 +1483,42 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta*
         const float srms = sqrtf((float)(sh2 / n) + eps);
         const float dmix = (float)h.direct_force_mix / (1.0f + 0.35f * S);
         const float kdir = srms / fmaxf(frms, eps);
-        ctrl->cr = (float)((1.0 - (double)dmix) * ar);
-        ctrl->cb = (float)((1.0 - (double)dmix) * ab);
-        ctrl->co = (float)((1.0 - (double)dmix) * ao);
-        ctrl->ct = dmix * kdir;
-        ctrl->nscale = 1.0f / ((float)h.drive_clip * (1.0f + S));
-        moments[0] = Stt;
-        moments[1] = (double)srms;
-        moments[2] = (double)frms;
+        const double cr = (1.0 - (double)dmix) * ar, cb = (1.0 - (double)dmix) * ab, co = (1.0 - (double)dmix) * ao;
+        const double ct = (double)(dmix * kdir);
+        const double core2 = cr * cr * Srr + cb * cb * Sbb + co * co * Soo + ct * ct * Stt +
+                             2.0 * (cr * cb * Srb + cr * co * Sro + cb * co * Sbo + ct * cr * Str + ct * cb * Stb + ct * co * Sto);
+        // alignment gate and prediction mix (cresso_v5.py:1303-1313)
+        const float prms = sqrtf((float)q[0] + eps);
+        const float align = clampf((float)q[4] / (frms * prms + eps), -1.0f, 1.0f);
+        float agate = clampf((align + 1.0f) * 0.5f, 0.0f, 1.0f);
+        if (!(prms > (float)sqrt(h.eps))) agate = 0.0f;
+        const double warm = h.warmup_steps == 0 ? 1.0 : 1.0 - exp(-(double)step / (double)(h.warmup_steps > 1 ? h.warmup_steps : 1));
+        const float mix = (float)(h.prediction_mix * warm) * agate * (1.0f / (1.0f + S));
+        // residual feedback: err' rms from the directly summed err rms and the Gram corrections
+        const float crms = sqrtf((float)(core2 / n) + eps);
+        const double ee = fmax(s_m[0] / n - 2.0 * q[3] + q[2], 0.0);
+        const float erms = sqrtf((float)ee + eps);
+        const float kres = crms / fmaxf(erms, eps);
+        const float resmix = (float)h.residual_feedback_mix / (1.0f + S);
+        float kecho = 0.f;
+        if (hard && echo_on) kecho = srms / fmaxf(sqrtf((float)q[1] + eps), eps);
+        const double c0 = 1.0 - (double)mix, c1 = mix, c2 = h.novelty_mix, c3 = (double)(resmix * kres);
+        const double c4 = hard ? h.echo_mix * (double)kecho : 0.0;
+        const float clip = (float)h.drive_clip;
+        // drive without the hash term:
+        //   c0 cr rat + c0 cb clip tanh + c0 co root + (c0 ct + c3) t + (c1 - c3) pred' + c4 echo + c2 clip tanh(err' ns)
+        ctrl->k_rat = (float)(c0 * cr);
+        ctrl->k_ths = (float)(c0 * cb * (double)clip);
+        ctrl->k_root = (float)(c0 * co);
+        ctrl->k_t = (float)(c0 * ct + c3);
+        ctrl->k_pred = (float)(c1 - c3);
+        ctrl->k_echo = (float)c4;
+        ctrl->k_nov = (float)(c2 * (double)clip);
+        ctrl->nscale = 1.0f / (clip * (1.0f + S));
+        ctrl->srms = srms;
     }
     __syncthreads();
-    if (tid < g.R) {
+    if (tid < R) {
         const int r = tid;
         st.q_cos[r] = s_f[r][1];
         st.q_sin[r] = s_f[r][2];
@@ -1281,167 +1535,172 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta*
 }
 
 // ---------------------------------------------------------------------------
-// S4: cross moments for the drive energy
+// S4: drive without the hash term, written over t; sums for the drive energy
 // ---------------------------------------------------------------------------
-// Y = {core, pred', nov, err', echo, hash}; sums of Y_a Y_b (a <= b) and t*pred'
-__device__ __forceinline__ int pair_index(int a, int b) {  // a <= b < 6
-    return a * 6 - (a * (a - 1)) / 2 + (b - a);
-}
-
-template <int RM, int KM>
-__global__ __launch_bounds__(SP_NT) void sweep4_kernel(Geom g, const float* __restrict__ coltab,
-                                                       const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
-                                                       const float* __restrict__ imp_tab, const float* __restrict__ alpha,
-                                                       const float* __restrict__ tbuf, double* __restrict__ part,
-                                                       int hash_on, int echo_on, cresso_hyper h) {
+template <int RM, int KC>
+__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(Geom g, const float* __restrict__ rowtab,
+                                                          const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
+                                                          const unsigned char* __restrict__ bins,
+                                                          const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
+                                                          float* __restrict__ tbuf, double* __restrict__ part, int hash_on,
+                                                          int echo_on, cresso_hyper h) {
+    constexpr int KA = KC + 1;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV4];
     const Tile t = tile_of(g);
     const int TB = g.T * g.B;
+    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
+    const int nr = (int)(t.r1 - t.r0);
+    // LDS: impulse table [T][B] | alpha [PR][2][KA] (pred', then k_pred pred' + k_echo echo)
     float* s_imp = reinterpret_cast<float*>(dyn);
+    float* s_al = s_imp + TB;
     if (hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
+    const float kp = ctrl->k_pred, ke = ctrl->k_echo;
+    for (int j = threadIdx.x; j < nr * KA; j += SP_NT) {
+        const int lr = j / KA, k = j - lr * KA;
+        const float* arow = rowtab + (t.r0 + lr) * g.RW;
+        const float ap = alpha_coef<KC>(g, meta, arow, ctrl->rc[2], ctrl->rconst[2], k);
+        const float ae = echo_on ? alpha_coef<KC>(g, meta, arow, ctrl->rc[3], ctrl->rconst[3], k) : 0.f;
+        s_al[lr * 2 * KA + k] = ap;
+        s_al[lr * 2 * KA + KA + k] = kp * ap + ke * ae;
+    }
     __syncthreads();
-    float b[KM];
-    load_cols<KM>(g, coltab, t, b);
+    float b[KC];
+    load_cols<KC>(g, coltab, t, b);
+    const int64_t base = panel_base(g, t);
+    float* __restrict__ tb = tbuf + base;
     const float eps = (float)h.eps;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
-    const float cr = ctrl->cr, cb = ctrl->cb, co = ctrl->co, ct = ctrl->ct, ns = ctrl->nscale;
-    const float invT = 1.0f / (float)g.T;
-    const float* __restrict__ alQ = alpha + 2 * (size_t)g.rows * g.KA;
-    const float* __restrict__ alE = alQ + (size_t)g.rows * g.KA;
-    float m[NV4];
-#pragma unroll
-    for (int k = 0; k < NV4; ++k) m[k] = 0.f;
+    const float k_rat = ctrl->k_rat, k_ths = ctrl->k_ths, k_root = ctrl->k_root, k_t = ctrl->k_t, k_nov = ctrl->k_nov;
+    const float ns = ctrl->nscale;
+    const float invT = 1.0f / (float)T;
+    float a_dd = 0.f, a_dh = 0.f, a_hh = 0.f;
     if (t.colok) {
-        for (int64_t i = t.r0; i < t.r1; ++i) {
-            const int64_t e = i * g.cols + t.col;
-            const float tv = tbuf[e];
-            const float pred = recon<KM>(alQ + i * g.KA, b);
-            const float err = tv - pred;
-            const float nov = ftanh(err * ns) * clip;
-            const float echo = echo_on ? recon<KM>(alE + i * g.KA, b) : 0.f;
-            float hp = 0.f;
-            if (hash_on) {
-                const uint64_t pk = load_bins(bins, e, g.binbytes);
-                for (int tt = 0; tt < g.T; ++tt) hp += s_imp[tt * g.B + bin_of(pk, tt, g.bpb)];
-                hp = hp * invT;
+        for (int i0 = 0; i0 < nr; i0 += SP_U) {
+            float tvs[SP_U];
+            uint64_t bv[SP_U];
+#pragma unroll
+            for (int u = 0; u < SP_U; ++u) {
+                tvs[u] = 0.f;
+                bv[u] = 0;
+                if (i0 + u < nr) {
+                    const uint32_t o = panel_off(g, i0 + u);
+                    tvs[u] = tb[o];
+                    if (hash_on) bv[u] = load_bins_at(bins, base, o, binbytes);
+                }
             }
-            float rat, bnd, root;
-            shape3f(tv, iclip, clip, clip2, eps, rat, bnd, root);
-            const float core = cr * rat + cb * bnd + co * root + ct * tv;
-            const float Y[6] = {core, pred, nov, err, echo, hp};
 #pragma unroll
-            for (int a = 0; a < 6; ++a)
+            for (int u = 0; u < SP_U; ++u) {
+                const int lr = i0 + u;
+                if (lr >= nr) break;
+                const float tv = tvs[u];
+                const float* __restrict__ al = s_al + lr * 2 * KA;
+                const float pred = recon<KC>(al, b);
+                const float mixed = recon<KC>(al + KA, b);
+                const float err = tv - pred;
+                const float nov = ftanh(err * ns);
+                float rat, ths, root;
+                shape3f(tv, iclip, clip2, eps, rat, ths, root);
+                const float d = k_rat * rat + k_ths * ths + k_root * root + k_t * tv + mixed + k_nov * nov;
+                tb[panel_off(g, lr)] = d;
+                a_dd += d * d;
+                if (hash_on) {
+                    float hp = 0.f;
 #pragma unroll
-                for (int c = a; c < 6; ++c) m[pair_index(a, c)] += Y[a] * Y[c];
-            m[21] += tv * pred;
+                    for (int tt = 0; tt < SP_MAXT; ++tt) {
+                        if (tt >= T) break;
+                        hp += s_imp[tt * B + bin_of(bv[u], tt, bpb)];
+                    }
+                    hp = hp * invT;
+                    a_dh += d * hp;
+                    a_hh += hp * hp;
+                }
+                elem_fence();
+            }
         }
     }
-    Partials P{red, NV4};
-#pragma unroll
-    for (int k = 0; k < NV4; ++k) P.add(k, m[k]);
+    Partials P{red, 3};
+    P.add(0, a_dd);
+    P.add(1, a_dh);
+    P.add(2, a_hh);
     P.flush(part, g.nblk);
 }
 
+// F4: hash-term coefficient, drive energy reservoir, gain.
+//   sum drive^2 = sum d^2 + 2 c5 sum d hp + c5^2 sum hp^2
 __global__ __launch_bounds__(SP_FIN_NT) void fin4_kernel(Geom g, const double* __restrict__ part, SpecState st,
                                                          Ctrl* __restrict__ ctrl, int step, int hash_on, int hard,
-                                                         int echo_on, cresso_hyper h, const double* __restrict__ moments) {
-    __shared__ double s_m[NV4];
-    reduce_all(part, g.nblk, NV4, s_m);
+                                                         cresso_hyper h) {
+    __shared__ double s_m[3];
+    reduce_all(part, g.nblk, 3, s_m);
     if (threadIdx.x != 0) return;
     const double n = (double)g.n;
     const float eps = (float)h.eps;
-    auto G = [&](int a, int b) { return a <= b ? s_m[pair_index(a, b)] : s_m[pair_index(b, a)]; };
-    const float S = *st.surprise;
-    const float frms = (float)moments[2];
-    const float srms = (float)moments[1];
-    // alignment gate and prediction mix (cresso_v5.py:1303-1313)
-    const float prms = sqrtf((float)(G(1, 1) / n) + eps);
-    const float align = clampf((float)(s_m[21] / n) / (frms * prms + eps), -1.0f, 1.0f);
-    float agate = clampf((align + 1.0f) * 0.5f, 0.0f, 1.0f);
-    if (!(prms > (float)sqrt(h.eps))) agate = 0.0f;
-    const double warm = h.warmup_steps == 0 ? 1.0 : 1.0 - exp(-(double)step / (double)(h.warmup_steps > 1 ? h.warmup_steps : 1));
-    const float mix = (float)(h.prediction_mix * warm) * agate * (1.0f / (1.0f + S));
-    const float crms = sqrtf((float)(G(0, 0) / n) + eps);
-    const float erms = sqrtf((float)(G(3, 3) / n) + eps);
-    const float kres = crms / fmaxf(erms, eps);
-    const float resmix = (float)h.residual_feedback_mix / (1.0f + S);
-    float kecho = 0.f, khp = 0.f;
-    if (hard && echo_on) kecho = srms / fmaxf(sqrtf((float)(G(4, 4) / n) + eps), eps);
-    if (hard && hash_on) khp = srms / fmaxf(sqrtf((float)(G(5, 5) / n) + eps), eps);
-    double c[6];
-    c[0] = 1.0 - (double)mix;
-    c[1] = mix;
-    c[2] = h.novelty_mix;
-    c[3] = (double)(resmix * kres);
-    c[4] = hard ? h.echo_mix * (double)kecho : 0.0;
-    c[5] = hard ? h.hash_drive_mix * (double)khp : 0.0;
-    double dd = 0.0;
-    for (int a = 0; a < 6; ++a)
-        for (int b = 0; b < 6; ++b) dd += c[a] * c[b] * G(a, b);
+    float khp = 0.f;
+    if (hard && hash_on) khp = ctrl->srms / fmaxf(sqrtf((float)(s_m[2] / n) + eps), eps);
+    const double c5 = hard ? h.hash_drive_mix * (double)khp : 0.0;
+    const double dd = s_m[0] + 2.0 * c5 * s_m[1] + c5 * c5 * s_m[2];
     const float de_now = (float)(fmax(dd, 0.0) / n);
     const float de = reservoir_f(*st.drive_energy, de_now, h.reservoir_decay, step);
     *st.drive_energy = de;
-    const float gain = clampf((float)h.target_update_rms / sqrtf(de + eps), (float)h.min_gain, (float)h.max_gain);
-    ctrl->dcore = (float)c[0];
-    ctrl->dpred = (float)c[1];
-    ctrl->dnov = (float)c[2];
-    ctrl->derr = (float)c[3];
-    ctrl->decho = (float)c[4];
-    ctrl->dhp = (float)c[5];
-    ctrl->gain = gain;
+    ctrl->k_hash = (float)c5;
+    ctrl->gain = clampf((float)h.target_update_rms / sqrtf(de + eps), (float)h.min_gain, (float)h.max_gain);
 }
 
 // ---------------------------------------------------------------------------
-// S5: parameter update
+// S5: parameter update, param -= lr * cast(drive * gain) (cresso_v5.py:1353)
 // ---------------------------------------------------------------------------
-template <int RM, int KM, typename PT>
-__global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ param, const float* __restrict__ coltab,
-                                                       const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
-                                                       const float* __restrict__ imp_tab, const float* __restrict__ alpha,
-                                                       const float* __restrict__ tbuf, int hash_on, int echo_on,
+template <typename PT>
+__device__ __forceinline__ void apply1(PT* __restrict__ param, int64_t e, float drive, float gain, float nlr) {
+    const float u = to_f(from_w<PT>(drive * gain));
+    param[e] = from_w<PT>(to_f(param[e]) + nlr * u);
+}
+
+template <typename PT, bool HASH, bool V4>
+__global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ param, const float* __restrict__ dbuf,
+                                                       const unsigned char* __restrict__ bins,
+                                                       const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
                                                        cresso_hyper h) {
     extern __shared__ __align__(16) unsigned char dyn[];
-    const Tile t = tile_of(g);
     const int TB = g.T * g.B;
+    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
     float* s_imp = reinterpret_cast<float*>(dyn);
-    if (hash_on)
+    if (HASH) {
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
-    __syncthreads();
-    if (!t.colok) return;
-    float b[KM];
-    load_cols<KM>(g, coltab, t, b);
-    const float eps = (float)h.eps;
-    const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
-    const float cr = ctrl->cr, cb = ctrl->cb, co = ctrl->co, ct = ctrl->ct, ns = ctrl->nscale;
-    const float d0 = ctrl->dcore, d1 = ctrl->dpred, d2 = ctrl->dnov, d3 = ctrl->derr, d4 = ctrl->decho, d5 = ctrl->dhp;
-    const float gain = ctrl->gain;
-    const float nlr = (float)(-h.lr);
-    const float invT = 1.0f / (float)g.T;
-    const float* __restrict__ alQ = alpha + 2 * (size_t)g.rows * g.KA;
-    const float* __restrict__ alE = alQ + (size_t)g.rows * g.KA;
-    for (int64_t i = t.r0; i < t.r1; ++i) {
-        const int64_t e = i * g.cols + t.col;
-        const float tv = tbuf[e];
-        const float pred = recon<KM>(alQ + i * g.KA, b);
-        const float err = tv - pred;
-        const float nov = ftanh(err * ns) * clip;
-        float drive = d1 * pred + d2 * nov + d3 * err;
-        if (echo_on) drive += d4 * recon<KM>(alE + i * g.KA, b);
-        if (hash_on) {
-            const uint64_t pk = load_bins(bins, e, g.binbytes);
-            float hp = 0.f;
-            for (int tt = 0; tt < g.T; ++tt) hp += s_imp[tt * g.B + bin_of(pk, tt, g.bpb)];
-            drive += d5 * (hp * invT);
-        }
-        float rat, bnd, root;
-        shape3f(tv, iclip, clip, clip2, eps, rat, bnd, root);
-        const float core = cr * rat + cb * bnd + co * root + ct * tv;
-        drive += d0 * core;
-        const float u = to_f(from_w<PT>(drive * gain));
-        param[e] = from_w<PT>(to_f(param[e]) + nlr * u);
+        __syncthreads();
     }
+    const float gain = ctrl->gain, kh = ctrl->k_hash * (1.0f / (float)T);
+    const float nlr = (float)(-h.lr);
+    const int64_t beg = (int64_t)blockIdx.x * g.chunk1;
+    const int64_t end = beg + g.chunk1 < g.n ? beg + g.chunk1 : g.n;
+    auto drive_at = [&](int64_t e, float d) -> float {
+        if (!HASH) return d;
+        const uint64_t pk = load_bins(bins, e, binbytes);
+        float hp = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < SP_MAXT; ++tt) {
+            if (tt >= T) break;
+            hp += s_imp[tt * B + bin_of(pk, tt, bpb)];
+        }
+        return d + kh * hp;
+    };
+    // chunks are multiples of 4 elements: float4 drive loads (param 4-element aligned)
+    const int64_t vend = V4 ? beg + ((end - beg) & ~(int64_t)3) : beg;
+    for (int64_t e = beg + 4 * (int64_t)threadIdx.x; e < vend; e += 4 * SP_NT) {
+        const float4 d4 = *reinterpret_cast<const float4*>(dbuf + e);
+        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+        float pv[4];
+        Ld4<PT>::go(param, e, pv);
+        float o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float u = to_f(from_w<PT>(drive_at(e + c, dv[c]) * gain));
+            o[c] = pv[c] + nlr * u;
+        }
+        St4<PT>::go(param, e, o);
+    }
+    for (int64_t e = vend + threadIdx.x; e < end; e += SP_NT) apply1(param, e, drive_at(e, dbuf[e]), gain, nlr);
 }
 
 // ---------------------------------------------------------------------------
@@ -1593,10 +1852,17 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     g.slabs = (int32_t)((g.cols + SP_NT - 1) / SP_NT);
     int64_t pr = std::max<int64_t>(16, (g.rows * g.slabs) / 1024);
     pr = std::min<int64_t>(std::min<int64_t>(pr, 64), g.rows);
+    // 32-bit element offsets inside a panel: PR * cols < 2^29
+    if (g.cols >= ((int64_t)1 << 29))
+        return fail(CRESSO_E_UNSUPPORTED, "spectral route: %lld elements per row exceed this build's panel limit",
+                    (long long)g.cols);
+    pr = std::min<int64_t>(pr, ((int64_t)1 << 29) / g.cols);
     g.PR = (int32_t)std::max<int64_t>(1, pr);
     g.panels = (int32_t)((g.rows + g.PR - 1) / g.PR);
     g.nblk = g.slabs * g.panels;
-    // flat force-RMS sweep: contiguous chunks (multiple of 4 elements) per block
+    // Gram pair sums: one block per ~1024 rows/columns of the longer axis, at most 256
+    g.nblkg = (int32_t)std::max<int64_t>(1, std::min<int64_t>(256, std::max(g.rows, g.cols) / 1024));
+    // flat force-RMS sweep and parameter update: contiguous chunks (multiple of 4 elements) per block
     g.nblk1 = (int32_t)std::max<int64_t>(1, std::min<int64_t>(1024, (g.n + 16383) / 16384));
     g.chunk1 = (((g.n + g.nblk1 - 1) / g.nblk1) + 3) & ~(int64_t)3;
     g.nblk1 = (int32_t)((g.n + g.chunk1 - 1) / g.chunk1);
@@ -1611,9 +1877,11 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.meta = take(sizeof(ModeMeta) * P.meta.size());
     o.csrc = take(sizeof(CarrierSrc) * P.csrc.size());
     o.rowtab = take(sizeof(float) * (size_t)g.rows * g.RW);
-    o.coltab = take(sizeof(float) * (size_t)g.K * g.cols);
+    o.coltab = take(sizeof(float) * (size_t)(g.KA - 1) * g.cols);   // 2*rmax+1 rows, zero beyond K
     o.stats = take(sizeof(double) * 4 * g.R);
     o.bounds = take(sizeof(double) * 2 * g.R);
+    o.gram = take(sizeof(double) * 4 * (size_t)g.R * g.R);
+    o.gpart = take(sizeof(double) * (size_t)g.nblkg * (4 * (size_t)g.R * g.R + (size_t)g.K * g.K));
     o.counts = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
     o.bins = take((size_t)g.binbytes * (size_t)g.n);
     o.tbuf = take(sizeof(float) * (size_t)g.n);
@@ -1621,29 +1889,34 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.hist = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
     o.lt = take(sizeof(float) * (size_t)g.T * g.B);
     o.imp = take(sizeof(float) * (size_t)g.T * g.B);
-    o.alpha = take(sizeof(float) * 4 * (size_t)g.rows * g.KA);
     o.rowfx = take(sizeof(unsigned long long) * (size_t)g.rows);
     o.colfx = take(sizeof(unsigned long long) * (size_t)g.cols);
-    o.rowfac = take(sizeof(float) * (size_t)g.rows);
     o.colfac = take(sizeof(float) * (size_t)g.cols);
     int64_t sum_trail = 0;
     for (int a = 0; a < g.ntrail; ++a) sum_trail += g.tdim[a];
     o.terms = take(sizeof(float) * (size_t)std::max<int64_t>(1, sum_trail));
-    o.ctrl = take(sizeof(Ctrl) + 3 * sizeof(double));
+    o.ctrl = take(sizeof(Ctrl));
     o.total = off;
     return CRESSO_OK;
 }
 
 template <typename T> T* at(void* ws, size_t off) { return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off); }
 
-size_t lds_sweep2(const Geom& g) { return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * 4 * (size_t)g.PR; }
-size_t lds_sweep3(const Geom& g) { return (sizeof(unsigned long long) + sizeof(float)) * g.T * g.B; }
-size_t lds_sweep45(const Geom& g) { return sizeof(float) * (size_t)g.T * g.B; }
+template <int RM> size_t lds_sweep2(const Geom& g) {
+    return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * (size_t)g.PR * (2 * RM + 4);
+}
+template <int RM, int KC> size_t lds_sweep3(const Geom& g) {
+    return (sizeof(unsigned long long) + sizeof(float)) * g.T * g.B +
+           sizeof(float) * (size_t)g.PR * (2 * (KC + 1) + 2 * RM + 1);
+}
+template <int KC> size_t lds_sweep4(const Geom& g) {
+    return sizeof(float) * ((size_t)g.T * g.B + (size_t)g.PR * 2 * (KC + 1));
+}
+constexpr size_t SP_LDS_MAX = 64 * 1024;
 
-template <int RM, typename PT, typename GT>
+template <int RM, int KC, typename PT, typename GT>
 int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws, const cresso_hyper& h,
                  hipStream_t s) {
-    constexpr int KM = 2 * RM + 1;
     const Geom& g = P.g;
     const Offs& o = P.o;
     SpecState st;
@@ -1669,19 +1942,21 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     unsigned long long* hist = at<unsigned long long>(ws, o.hist);
     float* lt = at<float>(ws, o.lt);
     float* imp = at<float>(ws, o.imp);
-    float* alpha = at<float>(ws, o.alpha);
     unsigned long long* rowfx = at<unsigned long long>(ws, o.rowfx);
     unsigned long long* colfx = at<unsigned long long>(ws, o.colfx);
-    float* rowfac = at<float>(ws, o.rowfac);
     float* colfac = at<float>(ws, o.colfac);
     float* terms = at<float>(ws, o.terms);
     float* tbuf = at<float>(ws, o.tbuf);
     Ctrl* ctrl = at<Ctrl>(ws, o.ctrl);
-    double* moments = reinterpret_cast<double*>(ctrl + 1);
     const double* stats = at<double>(ws, o.stats);
     const double* bounds = at<double>(ws, o.bounds);
+    const double* gram = at<double>(ws, o.gram);
     const int step = d.step;
     const int axes_on = (hard && h.instant_metric_coupling != 0.0 && !g.one_d) ? 1 : 0;
+    const size_t l2 = lds_sweep2<RM>(g), l3 = lds_sweep3<RM, KC>(g), l4 = lds_sweep4<KC>(g);
+    if (l2 > SP_LDS_MAX || l3 > SP_LDS_MAX || l4 > SP_LDS_MAX)
+        return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_tables x hash_bins = %d needs %zu bytes of LDS per block",
+                    g.T * g.B, std::max(l2, std::max(l3, l4)));
     const dim3 grid(g.nblk), blk(SP_NT);
     const bool v4 = ((uintptr_t)grad % (4 * sizeof(GT))) == 0 && ((uintptr_t)param % (4 * sizeof(PT))) == 0;
     if (v4)
@@ -1689,30 +1964,29 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     else
         hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, h);
     hipLaunchKernelGGL(fin1_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, part, st, ctrl, rowfx, colfx, step, h);
-    hipLaunchKernelGGL((sweep2_kernel<RM, KM, PT, GT>), grid, blk, lds_sweep2(g), s, g, grad, param, rowtab, coltab, meta,
-                       bins, ctrl, part, hist, rowfx, colfx, hash_on, axes_on, h);
-    hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, bounds, rowtab, part, hist, counts, lt,
-                       alpha, st, ctrl, step, hash_on, hard, h);
-    const dim3 rgrid((unsigned)((g.rows + 255) / 256)), rblk(256);
-    hipLaunchKernelGGL((alpha_kernel<RM>), rgrid, rblk, 0, s, g, meta, rowtab, (const Ctrl*)ctrl, 0, 2, alpha);
-    if (axes_on) {
-        const int64_t cnt = g.rows + (g.ntrail == 1 ? g.cols : 0);
-        hipLaunchKernelGGL(marg_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s, g, rowfx, colfx, rowfac,
-                           colfac, ctrl, (float)h.eps);
-        if (g.ntrail > 1)
-            hipLaunchKernelGGL(marg_axes_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, colfx, terms, colfac, ctrl, (float)h.eps);
-    }
-    hipLaunchKernelGGL((sweep3_kernel<RM, KM, PT, GT>), grid, blk, lds_sweep3(g), s, g, grad, param, rowtab, coltab, meta,
-                       bins, ctrl, lt, alpha, rowfac, colfac, tbuf, part, hist, hash_on, echo_on, h);
-    hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, rowtab, part, hist, counts, imp, alpha,
-                       st, ctrl, step, hash_on, hard, echo_on, h, moments);
-    hipLaunchKernelGGL((alpha_kernel<RM>), rgrid, rblk, 0, s, g, meta, rowtab, (const Ctrl*)ctrl, 2, echo_on ? 2 : 1, alpha);
-    hipLaunchKernelGGL((sweep4_kernel<RM, KM>), grid, blk, lds_sweep45(g), s, g, coltab, bins, ctrl, imp, alpha, tbuf, part,
+    hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins, ctrl,
+                       part, hist, rowfx, colfx, hash_on, axes_on, h);
+    hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, bounds, part, hist, counts, lt, st,
+                       ctrl, step, hash_on, hard, h);
+    if (axes_on && g.ntrail > 1)
+        hipLaunchKernelGGL(marg_axes_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, colfx, terms, colfac, ctrl, (float)h.eps);
+    hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins, ctrl,
+                       lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
+    hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, gram, part, hist, counts, imp, st, ctrl,
+                       step, hash_on, hard, echo_on, h);
+    hipLaunchKernelGGL((sweep4_kernel<RM, KC>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
                        hash_on, echo_on, h);
-    hipLaunchKernelGGL(fin4_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, part, st, ctrl, step, hash_on, hard, echo_on, h,
-                       (const double*)moments);
-    hipLaunchKernelGGL((sweep5_kernel<RM, KM, PT>), grid, blk, lds_sweep45(g), s, g, param, coltab, bins, ctrl, imp, alpha,
-                       tbuf, hash_on, echo_on, h);
+    hipLaunchKernelGGL(fin4_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, part, st, ctrl, step, hash_on, hard, h);
+    const size_t l5 = hash_on ? sizeof(float) * (size_t)g.T * g.B : 0;
+    const bool pv4 = ((uintptr_t)param % (4 * sizeof(PT))) == 0;
+    if (hash_on && pv4)
+        hipLaunchKernelGGL((sweep5_kernel<PT, true, true>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, h);
+    else if (hash_on)
+        hipLaunchKernelGGL((sweep5_kernel<PT, true, false>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, h);
+    else if (pv4)
+        hipLaunchKernelGGL((sweep5_kernel<PT, false, true>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, h);
+    else
+        hipLaunchKernelGGL((sweep5_kernel<PT, false, false>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, h);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: launch");
 }
@@ -1769,6 +2043,11 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
                        at<CarrierSrc>(ws, o.csrc), at<float>(ws, o.coltab));
     hipLaunchKernelGGL(ws_stats_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, at<float>(ws, o.rowtab),
                        at<float>(ws, o.coltab), at<double>(ws, o.stats), at<double>(ws, o.bounds));
+    hipLaunchKernelGGL(ws_pairsum_kernel, dim3((unsigned)g.nblkg), dim3(256), 0, s, g, at<float>(ws, o.rowtab),
+                       at<float>(ws, o.coltab), at<double>(ws, o.gpart));
+    const size_t gram_lds = sizeof(double) * (4 * (size_t)g.R * g.R + (size_t)g.K * g.K);
+    hipLaunchKernelGGL(ws_gram_kernel, dim3(1), dim3(SP_FIN_NT), gram_lds, s, g, meta, at<double>(ws, o.stats),
+                       at<double>(ws, o.gpart), at<double>(ws, o.gram));
     const int64_t TB = (int64_t)g.T * g.B;
     hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((TB + 255) / 256)), dim3(256), 0, s, at<unsigned long long>(ws, o.counts), TB);
     hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((TB + 255) / 256)), dim3(256), 0, s, at<unsigned long long>(ws, o.hist), TB);
@@ -1798,14 +2077,23 @@ extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cre
     if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "spectral route: drive_clip must be positive");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int pt = d->param_dtype, gt = d->grad_dtype;
-    const bool r8 = P->rmax == 8;
-#define CRESSO_SP_CASE(PC, GC, PTy, GTy)                                                          \
-    if (pt == PC && gt == GC)                                                                      \
-        return r8 ? run_step<8, PTy, GTy>(*P, *d, ws, *hyper, s) : run_step<16, PTy, GTy>(*P, *d, ws, *hyper, s);
+    // carrier-count variant: (modes, column carriers) fixed at compile time
+    const int R = g.R, K = g.K;
+    const int var = (R <= 4 && K <= 9) ? 0 : (R <= 8 && K <= 11) ? 1 : (R <= 8) ? 2 : 3;
+#define CRESSO_SP_RUN(PTy, GTy)                                                  \
+    switch (var) {                                                               \
+        case 0: return run_step<4, 9, PTy, GTy>(*P, *d, ws, *hyper, s);          \
+        case 1: return run_step<8, 11, PTy, GTy>(*P, *d, ws, *hyper, s);         \
+        case 2: return run_step<8, 17, PTy, GTy>(*P, *d, ws, *hyper, s);         \
+        default: return run_step<16, 33, PTy, GTy>(*P, *d, ws, *hyper, s);       \
+    }
+#define CRESSO_SP_CASE(PC, GC, PTy, GTy) \
+    if (pt == PC && gt == GC) { CRESSO_SP_RUN(PTy, GTy) }
     CRESSO_SP_CASE(CRESSO_F32, CRESSO_F32, float, float)
     CRESSO_SP_CASE(CRESSO_BF16, CRESSO_BF16, __hip_bfloat16, __hip_bfloat16)
     CRESSO_SP_CASE(CRESSO_F16, CRESSO_F16, __half, __half)
 #undef CRESSO_SP_CASE
+#undef CRESSO_SP_RUN
     return fail(CRESSO_E_UNSUPPORTED, "spectral route: param/grad dtype pair (%d,%d) not supported by this build", pt, gt);
 }
 
@@ -1840,4 +2128,14 @@ extern "C" int32_t cresso_spectral_workspace_basis(const cresso_spectral_plan* P
                        sin_out);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace basis");
+}
+
+extern "C" int32_t cresso_spectral_workspace_gram(const cresso_spectral_plan* P, const void* ws, size_t ws_bytes,
+                                                  double* gram_out, void* stream) {
+    if (!P || !ws || !gram_out) return fail(CRESSO_E_INVALID, "spectral route: null argument");
+    if (ws_bytes < P->o.total) return fail(CRESSO_E_INVALID, "spectral route: workspace too small");
+    const size_t V = 2 * (size_t)P->g.R;
+    hipError_t e = hipMemcpyAsync(gram_out, at<double>(const_cast<void*>(ws), P->o.gram), sizeof(double) * V * V,
+                                  hipMemcpyDeviceToDevice, reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace gram");
 }

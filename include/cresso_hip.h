@@ -185,6 +185,14 @@ int32_t cresso_spectral_workspace_bins(const cresso_spectral_plan* plan, const v
 int32_t cresso_spectral_workspace_basis(const cresso_spectral_plan* plan, const void* workspace, size_t workspace_bytes,
                                         int32_t mode, float* cos_out, float* sin_out, void* stream);
 
+/* Gram matrix of the normalized basis that the step's closed-form drive
+ * statistics use: G[v][w] = mean over elements of Xn_v Xn_w with v = 2r for
+ * C_r and v = 2r+1 for S_r, into gram_out (device fp64 [2*rank][2*rank]).
+ * The reference evaluates the same quantities element by element
+ * (cresso_v5.py:1303-1353; drive_update_cuda, cresso_cuda_kernel.cu:2995). */
+int32_t cresso_spectral_workspace_gram(const cresso_spectral_plan* plan, const void* workspace, size_t workspace_bytes,
+                                       double* gram_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -175,3 +175,40 @@ def _raw_rms(shape, rank, fmax, r, cos):
                     w = w * torch.exp(-0.5 * ((u - mu) / sig) ** 2)
         v = w * (torch.cos(ph) if cos else torch.sin(ph))
     return float((v - v.mean()).pow(2).mean().sqrt())
+
+
+GRAM_CASES = [((17, 19), 8, 5), ((64, 48), 8, 5), ((2048,), 8, 5), ((6, 10, 12), 16, 7), ((8, 6, 3, 3), 16, 7),
+              ((300, 257), 4, 3)]
+
+
+@pytest.mark.parametrize("case", GRAM_CASES, ids=["x".join(map(str, c[0])) + f"_r{c[1]}" for c in GRAM_CASES])
+def test_workspace_gram_matches_dense_basis(case):
+    """The closed-form Gram matrix (pair sums of the separable tables) against
+    the dense fp64 product of the carriers the same workspace forms."""
+    from cresso_amd import _native
+
+    shape, rank, fmax = case
+    announce(f"workspace gram {shape} r{rank}")
+    lib, ws = _workspace(shape, rank, fmax, 64, 2)
+    n = int(np.prod(shape))
+    stream = torch.cuda.current_stream().cuda_stream
+    X = torch.empty((2 * rank, n), dtype=torch.float32, device="cuda")
+    for r in range(rank):
+        _native.check(lib.cresso_spectral_workspace_basis(ws.plan, ctypes.c_void_p(ws.buf.data_ptr()),
+                                                          ctypes.c_size_t(ws.buf.numel()), r,
+                                                          ctypes.c_void_p(X[2 * r].data_ptr()),
+                                                          ctypes.c_void_p(X[2 * r + 1].data_ptr()),
+                                                          ctypes.c_void_p(stream)), "workspace basis")
+    G = torch.empty((2 * rank, 2 * rank), dtype=torch.float64, device="cuda")
+    _native.check(lib.cresso_spectral_workspace_gram(ws.plan, ctypes.c_void_p(ws.buf.data_ptr()),
+                                                     ctypes.c_size_t(ws.buf.numel()), ctypes.c_void_p(G.data_ptr()),
+                                                     ctypes.c_void_p(stream)), "workspace gram")
+    torch.cuda.synchronize()
+    Xd = X.double().cpu()
+    dense = (Xd @ Xd.T / n).numpy()
+    got = G.cpu().numpy()
+    scale = np.sqrt(np.outer(np.diag(dense), np.diag(dense))) + 1e-30
+    # the dense side is built from fp32-rounded carriers: agreement to ~1e-6 of the entry scale
+    assert np.abs(got - dense).max() <= 2e-6 * max(1.0, scale.max()), np.abs(got - dense).max()
+    assert np.allclose(np.diag(got), np.diag(dense), rtol=2e-6, atol=1e-9)
+    np.testing.assert_allclose(got, got.T, rtol=0, atol=1e-12)
