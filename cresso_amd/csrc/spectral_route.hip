@@ -49,7 +49,8 @@ namespace {
 constexpr int SP_NT = 256;
 constexpr int SP_MAXR = 16;
 constexpr int SP_MAXT = 8;
-constexpr int SP_FIN_NT = 1024;
+constexpr int SP_FIN_NT = 1024;  // workspace set-up kernels
+constexpr int SP_FN_NT = 512;    // per-step finalize kernels (room for fp64 accumulators)
 
 enum ModeType : int32_t { M_ZERO = 0, M_ADD = 1, M_PROD = 2 };
 
@@ -89,7 +90,7 @@ struct Geom {
 };
 
 struct Offs {
-    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, bins, tbuf, part, hist, lt, imp, rowfx,
+    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, bins, tbuf, part, sums, hist, lt, imp, rowfx,
         colfx, colfac, terms, ctrl, total;
 };
 
@@ -549,16 +550,19 @@ __device__ __forceinline__ float wave_total(float v) {
 struct Partials {
     float* lds;
     int V;
+    int VS;   // row stride of the block-major partials (the consumer's fixed width; zero padded)
     __device__ __forceinline__ void add(int idx, float x) {
         const float w = wave_total(x);
         if ((threadIdx.x & 63) == 63) lds[(threadIdx.x >> 6) * V + idx] = w;
     }
-    __device__ __forceinline__ void flush(double* part, int nblk) {
+    // block-major: part[block][VS], slots V..VS-1 zero
+    __device__ __forceinline__ void flush(double* part) {
         __syncthreads();
-        for (int v = threadIdx.x; v < V; v += SP_NT) {
+        for (int v = threadIdx.x; v < VS; v += SP_NT) {
             double s = 0.0;
-            for (int w = 0; w < SP_NT / 64; ++w) s += (double)lds[w * V + v];
-            part[(size_t)v * nblk + blockIdx.x] = s;
+            if (v < V)
+                for (int w = 0; w < SP_NT / 64; ++w) s += (double)lds[w * V + v];
+            part[(size_t)blockIdx.x * VS + v] = s;
         }
     }
 };
@@ -596,43 +600,58 @@ __device__ __forceinline__ float reservoir_f(float old, float cur, double decay,
     return old * (float)decay + (float)(1.0 - decay) * cur;
 }
 
-// All partial values of a sweep reduced over blocks in a fixed order; result
-// in out[v] (LDS), visible after return.  Each value owns TPV consecutive
-// threads (TPV = largest power of two with V*TPV <= block size, at most 64):
-// thread j of value v sums blocks j, j+TPV, ... (the group's loads coalesce),
-// eight independent accumulators deep, and one thread per value adds the TPV
-// sums in order.  No cross-lane traffic; the loads of a thread are all in
-// flight together.
-__device__ void reduce_all(const double* __restrict__ part, int nblk, int V, double* out) {
-    __shared__ double s_seg[SP_FIN_NT];
-    const int tid = threadIdx.x;
-    int tpv = 64;
-    while (tpv > 1 && tpv * V > SP_FIN_NT) tpv >>= 1;
-    const int v = tid / tpv, j = tid % tpv;
-    if (v < V) {
-        const double* __restrict__ p = part + (size_t)v * nblk;
-        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0, a4 = 0.0, a5 = 0.0, a6 = 0.0, a7 = 0.0;
-        int b = j;
-        const int step = tpv;
-        for (; b + 7 * step < nblk; b += 8 * step) {
-            a0 += p[b];
-            a1 += p[b + step];
-            a2 += p[b + 2 * step];
-            a3 += p[b + 3 * step];
-            a4 += p[b + 4 * step];
-            a5 += p[b + 5 * step];
-            a6 += p[b + 6 * step];
-            a7 += p[b + 7 * step];
+// All partial values of a sweep (block-major part[block][V]) reduced in a
+// fixed order into out[v] (LDS), visible after return: thread j accumulates
+// blocks j, j + NT, ... in fp64 (its loads all in flight), each wave reduces
+// every value with DPP in fixed lane order, and the wave totals are added in
+// wave order.
+template <int VMAX>
+__device__ void reduce_bm(const double* __restrict__ part, int nblk, int V, double* out) {
+    __shared__ double s_w[SP_FN_NT / 64][VMAX];
+    double acc[VMAX];
+#pragma unroll
+    for (int v = 0; v < VMAX; ++v) acc[v] = 0.0;
+    // rows have the fixed width VMAX (zero padded): unconditional loads, all in flight
+    for (int b = threadIdx.x; b < nblk; b += SP_FN_NT) {
+        const double* __restrict__ p = part + (size_t)b * VMAX;
+#pragma unroll
+        for (int v = 0; v < VMAX; ++v) acc[v] += p[v];
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int v = 0; v < VMAX; ++v) {
+        if (v < V) {
+            const double w = wave_total_d(acc[v]);
+            if (lane == 63) s_w[wave][v] = w;
         }
-        for (; b < nblk; b += step) a0 += p[b];
-        s_seg[tid] = ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7));
     }
     __syncthreads();
-    if (tid < V) {
-        double sum = 0.0;
-        for (int k = 0; k < tpv; ++k) sum += s_seg[tid * tpv + k];
-        out[tid] = sum;
+    for (int v = threadIdx.x; v < V; v += SP_FN_NT) {
+        double s = 0.0;
+        for (int w = 0; w < SP_FN_NT / 64; ++w) s += s_w[w][v];
+        out[v] = s;
     }
+    __syncthreads();
+}
+
+// Cross-block merge of a sweep's partials spread over many CUs: block v sums
+// value v of every block (thread j: blocks j, j + 256, ... in order; then a
+// fixed-order DPP wave tree and the four wave totals in order) into sums[v].
+__global__ __launch_bounds__(256) void part_reduce_kernel(const double* __restrict__ part, int nblk, int VS,
+                                                          double* __restrict__ sums) {
+    __shared__ double s_w[4];
+    const int v = blockIdx.x;
+    double a = 0.0;
+    for (int b = threadIdx.x; b < nblk; b += 256) a += part[(size_t)b * VS + v];
+    a = wave_total_d(a);
+    if ((threadIdx.x & 63) == 63) s_w[threadIdx.x >> 6] = a;
+    __syncthreads();
+    if (threadIdx.x == 0) sums[v] = ((s_w[0] + s_w[1]) + s_w[2]) + s_w[3];
+}
+
+// The merged sums of a sweep into LDS (all loads in flight).
+__device__ void load_sums(const double* __restrict__ sums, int V, double* out) {
+    for (int v = threadIdx.x; v < V; v += blockDim.x) out[v] = sums[v];
     __syncthreads();
 }
 
@@ -670,19 +689,19 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restr
         if (wd_on) f = f + wd * ld(param, i);
         a += f * f;
     }
-    Partials P{red, 1};
+    Partials P{red, 1, 1};
     P.add(0, a);
-    P.flush(part, g.nblk1);
+    P.flush(part);
 }
 
-__global__ __launch_bounds__(SP_FIN_NT) void fin1_kernel(Geom g, const double* __restrict__ part, SpecState st,
+__global__ __launch_bounds__(SP_FN_NT) void fin1_kernel(Geom g, const double* __restrict__ part, SpecState st,
                                                          Ctrl* __restrict__ ctrl, unsigned long long* __restrict__ rowfx,
                                                          unsigned long long* __restrict__ colfx, int step, cresso_hyper h) {
     __shared__ double red[1];
-    reduce_all(part, g.nblk1, 1, red);
+    reduce_bm<1>(part, g.nblk1, 1, red);
     // clear the axis density sums for this step's sweep 2
-    for (int64_t i = threadIdx.x; i < g.rows; i += SP_FIN_NT) rowfx[i] = 0ull;
-    for (int64_t i = threadIdx.x; i < g.cols; i += SP_FIN_NT) colfx[i] = 0ull;
+    for (int64_t i = threadIdx.x; i < g.rows; i += SP_FN_NT) rowfx[i] = 0ull;
+    for (int64_t i = threadIdx.x; i < g.cols; i += SP_FN_NT) colfx[i] = 0ull;
     if (threadIdx.x == 0) {
         const float eps = (float)h.eps;
         const float now = sqrtf((float)(red[0] / (double)g.n) + eps);
@@ -698,46 +717,48 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin1_kernel(Geom g, const double* _
 }
 
 // ---------------------------------------------------------------------------
-// per-row data of a block's panel, staged in LDS by the block prologue
+// reconstruction weights of a lane's column
 // ---------------------------------------------------------------------------
-// Reconstruction coefficient of column carrier k at row `row` for the
-// coefficients (rc, rconst): sum over modes of the carrier factors times the
-// mode weights; k == KC is the constant.  Carriers k >= K get no mode and stay
-// zero.
-//   additive kinds: C = a1 b1 - a2 b2, S = a2 b1 + a1 b2
-//   product / constant: C = a1 b1, S = a2 b2
-template <int KC>
-__device__ __forceinline__ float alpha_coef(const Geom& g, const ModeMeta* __restrict__ meta,
-                                            const float* __restrict__ arow, const float (*rc)[2], float rconst, int k) {
-    if (k == KC) return rconst;
-    float al = 0.f;
-    for (int r = 0; r < g.R; ++r) {
-        const ModeMeta m = meta[r];
-        if (k != m.k1 && k != m.k2) continue;
-        const float wc = rc[r][0], ws = rc[r][1];
-        const float a1 = arow[2 * r], a2 = arow[2 * r + 1];
-        const float c1 = m.type == M_ADD ? wc * a1 + ws * a2 : wc * a1;
-        const float c2 = m.type == M_ADD ? ws * a1 - wc * a2 : ws * a2;
-        al += (k == m.k1 ? c1 : 0.f) + (k == m.k2 ? c2 : 0.f);
+// A reconstruction sum_r (wc_r Craw_r + ws_r Sraw_r) + const equals
+// sum_x a_x(row) gam_x(col) + const with the row factors a_{2r} = a1_r,
+// a_{2r+1} = a2_r of the row table and, per column,
+//   additive kinds:     gam_{2r} = wc b_k1 + ws b_k2, gam_{2r+1} = ws b_k1 - wc b_k2
+//   product / constant: gam_{2r} = wc b_k1,           gam_{2r+1} = ws b_k2
+// (C = a1 b1 - a2 b2, S = a2 b1 + a1 b2, resp. C = a1 b1, S = a2 b2).
+// The sweeps read the row factors of the row all lanes share as scalars.
+template <int RM, int KC>
+__device__ __forceinline__ void recon_weights(const Geom& g, const ModeMeta* __restrict__ meta, const float (&b)[KC],
+                                              const float (*rc)[2], float (&gam)[2 * RM]) {
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        float g1 = 0.f, g2 = 0.f;
+        if (r < g.R) {
+            const ModeMeta m = meta[r];
+            float b1 = 0.f, b2 = 0.f;
+#pragma unroll
+            for (int k = 0; k < KC; ++k) {
+                if (k == m.k1) b1 = b[k];
+                if (k == m.k2) b2 = b[k];
+            }
+            const float wc = rc[r][0], ws = rc[r][1];
+            if (m.type == M_ADD) {
+                g1 = wc * b1 + ws * b2;
+                g2 = ws * b1 - wc * b2;
+            } else {
+                g1 = wc * b1;
+                g2 = ws * b2;
+            }
+        }
+        gam[2 * r] = g1;
+        gam[2 * r + 1] = g2;
     }
-    return al;
 }
 
-// Lane's column carriers (zero beyond K and for columns past the end).
+// Lane's column carriers (the table has 2*rmax+1 rows, zero beyond K).
 template <int KC>
 __device__ __forceinline__ void load_cols(const Geom& g, const float* __restrict__ coltab, const Tile& t, float (&b)[KC]) {
 #pragma unroll
     for (int k = 0; k < KC; ++k) b[k] = t.colok ? coltab[(size_t)k * g.cols + t.col] : 0.f;
-}
-
-// reconstruction at (row, lane column): alpha row (uniform over the wave,
-// from LDS) against the lane's column carriers
-template <int KC>
-__device__ __forceinline__ float recon(const float* __restrict__ al, const float (&b)[KC]) {
-    float v = al[KC];
-#pragma unroll
-    for (int k = 0; k < KC; ++k) v += al[k] * b[k];
-    return v;
 }
 
 // Lane contribution of a projection: Z[2q] = sum over the lane's rows of
@@ -801,49 +822,67 @@ __device__ __forceinline__ uint64_t load_bins_at(const unsigned char* __restrict
     }
 }
 
+// Sweep variants: MODE 1 is the common large-matrix case with every option
+// fixed at compile time (2-D tensor, instant metric on, two hash tables of at
+// most 256 bins, no weight decay, no local sharpness); MODE 0 handles every
+// other combination with runtime flags.
+struct SweepFlags {
+    bool hash_on, axes_on, wd_on, ls_on;
+    int T, bpb, binbytes;
+};
+template <int MODE>
+__device__ __forceinline__ SweepFlags sweep_flags(const Geom& g, int hash_arg, int axes_arg, const cresso_hyper& h) {
+    SweepFlags f;
+    if (MODE == 1) {
+        f.hash_on = true; f.axes_on = true; f.wd_on = false; f.ls_on = false;
+        f.T = 2; f.bpb = 1; f.binbytes = 2;
+    } else {
+        f.hash_on = hash_arg != 0; f.axes_on = axes_arg != 0;
+        f.wd_on = h.weight_decay != 0.0; f.ls_on = h.local_sharpness != 0.0;
+        f.T = g.T; f.bpb = g.bpb; f.binbytes = g.binbytes;
+    }
+    return f;
+}
+// whether a tensor's step can use MODE 1 (host side)
+inline bool fast_mode(const Geom& g, int hash_on, int axes_on, const cresso_hyper& h) {
+    return hash_on && axes_on && g.T == 2 && g.bpb == 1 && g.binbytes == 2 && !g.one_d && h.weight_decay == 0.0 &&
+           h.local_sharpness == 0.0;
+}
+
 // ---------------------------------------------------------------------------
 // S2: density field
 // ---------------------------------------------------------------------------
-template <int RM, int KC, typename PT, typename GT>
-__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
-                                                          const float* __restrict__ rowtab, const float* __restrict__ coltab,
-                                                          const ModeMeta* __restrict__ meta,
-                                                          const unsigned char* __restrict__ bins,
-                                                          const Ctrl* __restrict__ ctrl, double* __restrict__ part,
-                                                          unsigned long long* __restrict__ hist,
-                                                          unsigned long long* __restrict__ rowfx,
-                                                          unsigned long long* __restrict__ colfx, int hash_on, int axes_on,
-                                                          cresso_hyper h) {
+template <int RM, int KC, typename PT, typename GT, int MODE>
+__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
+    Geom g, const GT* __restrict__ grad, const PT* __restrict__ param, const float* __restrict__ rowtab,
+    const float* __restrict__ coltab, const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins,
+    const Ctrl* __restrict__ ctrl, double* __restrict__ part, unsigned long long* __restrict__ hist,
+    unsigned long long* __restrict__ rowfx, unsigned long long* __restrict__ colfx, int hash_arg, int axes_arg,
+    cresso_hyper h) {
     constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV2];
+    const SweepFlags F = sweep_flags<MODE>(g, hash_arg, axes_arg, h);
     const Tile t = tile_of(g);
-    const int TB = g.T * g.B;
-    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
+    const int B = g.B;
+    const int TB = F.T * B;
     const int nr = (int)(t.r1 - t.r0);
-    // LDS: histogram [T][B] u64 | row factors [PR][RW] | wave row sums [4][PR]
+    // LDS: histogram [T][B] u64 | wave row sums [4][PR]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
-    float* s_row = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
-    float* s_wrow = s_row + (size_t)g.PR * RW;
-    if (hash_on)
+    float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
+    if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_hist[i] = 0ull;
-    for (int j = threadIdx.x; j < nr * RW; j += SP_NT) {
-        const int lr = j / RW, q = j - lr * RW;
-        s_row[j] = rowtab[(t.r0 + lr) * g.RW + q];
-    }
     __syncthreads();
-    float b[KC];
-    load_cols<KC>(g, coltab, t, b);
     const int64_t base = panel_base(g, t);
     const GT* __restrict__ gb = grad + base;
     const PT* __restrict__ pb = param + base;
+    const float* __restrict__ rt = rowtab + t.r0 * g.RW;
     const float inv_s = ctrl->inv_s;
     const float eps = (float)h.eps;
     const float pw = (float)h.energy_power;
     const float ipw = (float)fmax(h.instant_metric_power, 0.25);
     const bool ip_one = ipw == 1.0f;
     const float wd = (float)h.weight_decay;
-    const bool wd_on = h.weight_decay != 0.0;
     const float sg = h.maximize ? -1.f : 1.f;
     const float hs = (float)ctrl->hs_ds;
     float Z[RW];
@@ -862,8 +901,8 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(Geom g,
             if (i0 + u < nr && t.colok) {
                 const uint32_t o = panel_off(g, i0 + u);
                 gv[u] = to_f(gb[o]);
-                if (wd_on) pv[u] = to_f(pb[o]);
-                if (hash_on) bv[u] = load_bins_at(bins, base, o, binbytes);
+                if (F.wd_on) pv[u] = to_f(pb[o]);
+                if (F.hash_on) bv[u] = load_bins_at(bins, base, o, F.binbytes);
             }
         }
 #pragma unroll
@@ -873,7 +912,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(Geom g,
             float dens = 0.f;
             if (t.colok) {
                 float f = sg * gv[u];
-                if (wd_on) f = f + wd * pv[u];
+                if (F.wd_on) f = f + wd * pv[u];
                 const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
                 const float ds = fpow(rel, pw);
                 const float L = flog1p(ds);
@@ -881,27 +920,27 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(Geom g,
                 dens = fminf(ip_one ? rl : fpow(rl, ipw), 1.0e6f);
                 aL += L;
                 aD += dens;
-                const float* __restrict__ ar = s_row + lr * RW;
+                const float* __restrict__ ar = rt + lr * g.RW;
 #pragma unroll
                 for (int q = 0; q < RW; ++q) Z[q] += ar[q] * L;
-                if (hash_on) {
+                if (F.hash_on) {
                     const unsigned long long v = to_fixed_u(ds * hs);
 #pragma unroll
                     for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= T) break;
-                        atomicAdd(&s_hist[tt * B + bin_of(bv[u], tt, bpb)], v);
+                        if (tt >= F.T) break;
+                        atomicAdd(&s_hist[tt * B + bin_of(bv[u], tt, F.bpb)], v);
                     }
                 }
             }
-            if (axes_on) {
+            if (F.axes_on) {
                 const float ws = wave_total(dens);
                 if (lane == 63) s_wrow[wave * g.PR + lr] = ws;
             }
-            elem_fence();
+            if (MODE == 0) elem_fence();
         }
     }
     __syncthreads();
-    if (axes_on) {
+    if (F.axes_on) {
         // axis density sums: one fixed-point atomic per row of this slab and per column of this panel
         for (int lr = threadIdx.x; lr < nr; lr += SP_NT) {
             float s = 0.f;
@@ -910,67 +949,108 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(Geom g,
         }
         if (t.colok) atomicAdd(&colfx[t.col], to_fixed_u(aD * (float)g.hs_col));
     }
-    if (hash_on)
+    if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT)
             if (s_hist[i]) atomicAdd(&hist[i], s_hist[i]);
-    Partials P{red, 2 + 2 * g.R};
+    float b[KC];
+    load_cols<KC>(g, coltab, t, b);
+    Partials P{red, 2 + 2 * g.R, NV2};
     P.add(0, aL);
     P.add(1, aD);
     proj_finish<RM, KC>(g, meta, Z, b, P, 2);
-    P.flush(part, g.nblk);
+    P.flush(part);
 }
 
 // ---------------------------------------------------------------------------
-// F2: hash metric, metric oscillator, recon coefficients
+// finalize helpers: one wave, one lane per mode
 // ---------------------------------------------------------------------------
 // Mode weights (the coefficient of each normalized carrier) and the
-// coefficients (wc, ws) per mode and constant of
+// coefficients (wc, ws) of the raw carriers and the constant of
 //   shrink * sum_r g_r (cc_r Cn_r + sc_r Sn_r)  (cresso_v5.py:362-376)
-// with Cn = (Craw - mu_c) ic; a gate of exactly 0 drops the mode.
-__device__ void set_recon(const Geom& g, const double* stats, float (*rc)[2], float& rconst, const float* cc,
-                          const float* sc, const float* gates, float* weights = nullptr) {
+// with Cn = (Craw - mu_c) ic; a gate of exactly 0 drops the mode.  Lane r of
+// the calling wave handles mode r; the constant is summed in mode order.
+__device__ void set_recon_lanes(const Geom& g, const double* __restrict__ stats, float (*rc)[2], float* rconst,
+                                float cc, float sc, float gate, float* s_tmp, float* weights = nullptr) {
+    const int r = threadIdx.x & 63;
     const double shrink = 1.0 / sqrt(fmax(1.0, 0.7 * log2((double)g.R + 1.0)));
-    float cst = 0.f;
-    for (int r = 0; r < g.R; ++r) {
-        const float gate = gates ? gates[r] : 1.0f;
-        float wc = 0.f, ws = 0.f, kc = 0.f, ks = 0.f;
+    float kc = 0.f, ks = 0.f, wc = 0.f, ws = 0.f, cterm = 0.f;
+    if (r < g.R) {
         if (gate != 0.0f) {
-            kc = (float)((double)cc[r] * shrink) * gate;
-            ks = (float)((double)sc[r] * shrink) * gate;
+            kc = (float)((double)cc * shrink) * gate;
+            ks = (float)((double)sc * shrink) * gate;
             wc = (float)((double)kc * stats[4 * r + 1]);
             ws = (float)((double)ks * stats[4 * r + 3]);
-            cst -= (float)((double)wc * stats[4 * r + 0] + (double)ws * stats[4 * r + 2]);
+            cterm = (float)((double)wc * stats[4 * r + 0] + (double)ws * stats[4 * r + 2]);
         }
         rc[r][0] = wc;
         rc[r][1] = ws;
+        s_tmp[r] = cterm;
         if (weights) {
             weights[2 * r] = kc;
             weights[2 * r + 1] = ks;
         }
     }
-    rconst = cst;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    if (r == 0) {
+        float cst = 0.f;
+        for (int q = 0; q < g.R; ++q) cst -= s_tmp[q];
+        *rconst = cst;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+}
+
+// Sum over the R lanes of wave 0 in lane order (fp64).
+__device__ double lanes_sum(double v, int R, double* s_tmp) {
+    const int r = threadIdx.x & 63;
+    if (r < R) s_tmp[r] = v;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    double s = 0.0;
+    for (int q = 0; q < R; ++q) s += s_tmp[q];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    return s;
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-__global__ __launch_bounds__(SP_FIN_NT) void fin2_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                         const double* __restrict__ stats, const double* __restrict__ bounds,
-                                                         const double* __restrict__ part,
-                                                         unsigned long long* __restrict__ hist,
-                                                         const unsigned long long* __restrict__ counts,
-                                                         float* __restrict__ lt, SpecState st, Ctrl* __restrict__ ctrl,
-                                                         int step, int hash_on, int hard, cresso_hyper h) {
+// ---------------------------------------------------------------------------
+// F2: hash metric, metric oscillator, recon coefficients
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(Geom g, const ModeMeta* __restrict__ meta,
+                                                        const double* __restrict__ stats, const double* __restrict__ bounds,
+                                                        const double* __restrict__ part,
+                                                        unsigned long long* __restrict__ hist,
+                                                        const unsigned long long* __restrict__ counts,
+                                                        float* __restrict__ lt, SpecState st, Ctrl* __restrict__ ctrl,
+                                                        int step, int hash_on, int hard, cresso_hyper h) {
     __shared__ double s_v[NV2];
-    __shared__ double red[16];
+    __shared__ double red[SP_FN_NT / 64];
     __shared__ float s_emean[SP_MAXT];
+    __shared__ float s_tmpf[64];
+    __shared__ double s_tmpd[64];
     const int tid = threadIdx.x;
     const float eps = (float)h.eps;
     const double n = (double)g.n;
-    reduce_all(part, g.nblk, 2 + 2 * g.R, s_v);
+    __shared__ double s_stats[4 * SP_MAXR], s_bounds[2 * SP_MAXR];
+    __shared__ float s_mode[SP_MAXR][9];
+    __shared__ int s_zero[SP_MAXR];
+    for (int i = tid; i < 4 * g.R; i += SP_FN_NT) s_stats[i] = stats[i];
+    for (int i = tid; i < 2 * g.R; i += SP_FN_NT) s_bounds[i] = bounds[i];
+    for (int i = tid; i < 9 * g.R; i += SP_FN_NT) {
+        const int r = i / 9, j = i - 9 * r;
+        const float* src[8] = {st.omega, st.metric_cos, st.metric_p_cos, st.metric_sin, st.metric_p_sin, st.q_cos,
+                               st.q_sin, st.conf};
+        if (j < 8) s_mode[r][j] = src[j][r];
+        else s_zero[r] = meta[r].type == M_ZERO;
+    }
+    load_sums(part, 2 + 2 * g.R, s_v);
     // hash energy per table (cresso_v5.py:1012-1056)
     if (hash_on) {
         const int TB = g.T * g.B;
-        for (int i = tid; i < TB; i += SP_FIN_NT) {
+        for (int i = tid; i < TB; i += SP_FN_NT) {
             const double cnt = (double)counts[i];
             const float cell = (float)((double)(long long)hist[i] / ctrl->hs_ds / fmax(cnt, 1.0));
             hist[i] = 0ull;
@@ -981,99 +1061,78 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin2_kernel(Geom g, const ModeMeta*
         __syncthreads();
         for (int tt = 0; tt < g.T; ++tt) {
             double s[1] = {0.0};
-            for (int b = tid; b < g.B; b += SP_FIN_NT) s[0] += (double)st.hash_energy[tt * g.B + b];
+            for (int b = tid; b < g.B; b += SP_FN_NT) s[0] += (double)st.hash_energy[tt * g.B + b];
             block_sum<1>(s, red);
             if (tid == 0) s_emean[tt] = (float)(s[0] / (double)g.B);
         }
         __syncthreads();
         const float ex = (float)(h.hash_metric_coupling / fmax(0.25, h.energy_power));
-        for (int i = tid; i < TB; i += SP_FIN_NT) {
+        for (int i = tid; i < TB; i += SP_FN_NT) {
             const int tt = i / g.B;
             const float hm = fmaxf(st.hash_energy[i] / fmaxf(s_emean[tt], eps), eps);
             lt[i] = logf(fmaxf(clampf(powf(hm, ex), 0.08f, 12.0f), eps));
         }
     }
-    // per-mode state staged in LDS by parallel threads; the recurrences run
-    // on one thread over LDS, results written back in parallel
-    __shared__ double s_st[SP_MAXR][6];
-    __shared__ float s_f[SP_MAXR][8];
-    __shared__ int s_type[SP_MAXR];
-    if (tid < g.R) {
+    if (tid < 64) {
+        // lane r: mode r
         const int r = tid;
-        for (int j = 0; j < 4; ++j) s_st[r][j] = stats[4 * r + j];
-        s_st[r][4] = bounds[2 * r];
-        s_st[r][5] = bounds[2 * r + 1];
-        s_f[r][0] = st.omega[r];
-        s_f[r][1] = st.metric_cos[r];
-        s_f[r][2] = st.metric_p_cos[r];
-        s_f[r][3] = st.metric_sin[r];
-        s_f[r][4] = st.metric_p_sin[r];
-        s_f[r][5] = st.q_cos[r];
-        s_f[r][6] = st.q_sin[r];
-        s_f[r][7] = st.conf[r];
-        s_type[r] = meta[r].type;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        // log-density projections: d = L/max(mean L, eps) - 1, mean(d Cn) = mean(L Cn)/m - mean(Cn)
+        const bool on = r < g.R;
         const double sumL = s_v[0], sumD = s_v[1];
+        // log-density projections: d = L/max(mean L, eps) - 1, mean(d Cn) = mean(L Cn)/m - mean(Cn)
         const double m = fmax((double)(float)(sumL / n), (double)eps);
-        double stt[4 * SP_MAXR];
-        for (int r = 0; r < g.R; ++r)
-            for (int j = 0; j < 4; ++j) stt[4 * r + j] = s_st[r][j];
-        float port[2 * SP_MAXR];
-        for (int v = 0; v < 2 * g.R; ++v) {
-            const int r = v / 2;
-            const double mu = s_st[r][2 * (v & 1)], inv = s_st[r][2 * (v & 1) + 1];
-            double pr = (s_v[2 + v] - mu * sumL) * inv / n / m;
-            if (s_type[r] == M_ZERO && (v & 1) == 0) pr -= 1.0;  // mean(Cn) = 1 for the constant mode
-            port[v] = (float)pr;
+        float pcos = 0.f, psin = 0.f;
+        if (on) {
+            const double prc = (s_v[2 + 2 * r] - s_stats[4 * r] * sumL) * s_stats[4 * r + 1] / n / m -
+                               (s_zero[r] ? 1.0 : 0.0);   // mean(Cn) = 1 for the constant mode
+            const double prs = (s_v[3 + 2 * r] - s_stats[4 * r + 2] * sumL) * s_stats[4 * r + 3] / n / m;
+            pcos = (float)prc;
+            psin = (float)prs;
         }
         // metric oscillator (cresso_v5.py:1064-1088)
         const float mdt = (float)h.metric_dt;
         const float damp = (float)fmax(0.0, 1.0 - h.metric_dt * h.metric_friction);
-        float mcs[SP_MAXR], mss[SP_MAXR];
-        for (int r = 0; r < g.R; ++r) {
-            const float om = s_f[r][0];
+        float mqc = 0.f, mqs = 0.f;
+        if (on) {
+            const float om = s_mode[r][0];
             const float o2 = om * om;
-            float mq = s_f[r][1], mp = s_f[r][2];
+            float mq = s_mode[r][1], mp = s_mode[r][2];
             mp = mp * damp;
-            mp = mp + mdt * (port[2 * r] - o2 * mq);
+            mp = mp + mdt * (pcos - o2 * mq);
             mq = clampf(mq + mdt * mp, -3.0f, 3.0f);
-            s_f[r][1] = mq; s_f[r][2] = mp; mcs[r] = mq;
-            mq = s_f[r][3]; mp = s_f[r][4];
+            st.metric_cos[r] = mq;
+            st.metric_p_cos[r] = mp;
+            mqc = mq;
+            mq = s_mode[r][3];
+            mp = s_mode[r][4];
             mp = mp * damp;
-            mp = mp + mdt * (port[2 * r + 1] - o2 * mq);
+            mp = mp + mdt * (psin - o2 * mq);
             mq = clampf(mq + mdt * mp, -3.0f, 3.0f);
-            s_f[r][3] = mq; s_f[r][4] = mp; mss[r] = mq;
+            st.metric_sin[r] = mq;
+            st.metric_p_sin[r] = mp;
+            mqs = mq;
         }
-        set_recon(g, stt, ctrl->rc[0], ctrl->rconst[0], mcs, mss, nullptr);
+        set_recon_lanes(g, s_stats, ctrl->rc[0], &ctrl->rconst[0], mqc, mqs, 1.0f, s_tmpf);
         // prediction with the pre-contact state and gates
-        float qc[SP_MAXR], qs[SP_MAXR], gt[SP_MAXR];
-        double pmax = 0.0;
+        float qc = 0.f, qs = 0.f, gt = 0.f;
+        double pm = 0.0;
         const double shrink = 1.0 / sqrt(fmax(1.0, 0.7 * log2((double)g.R + 1.0)));
-        for (int r = 0; r < g.R; ++r) {
-            qc[r] = s_f[r][5];
-            qs[r] = s_f[r][6];
-            gt[r] = sigmoidf_((float)h.confidence_gain * s_f[r][7]);
-            pmax += shrink * gt[r] * (fabs((double)qc[r]) * s_st[r][4] + fabs((double)qs[r]) * s_st[r][5]);
+        if (on) {
+            qc = s_mode[r][5];
+            qs = s_mode[r][6];
+            gt = sigmoidf_((float)h.confidence_gain * s_mode[r][7]);
+            pm = shrink * gt * (fabs((double)qc) * s_bounds[2 * r] + fabs((double)qs) * s_bounds[2 * r + 1]);
         }
-        set_recon(g, stt, ctrl->rc[1], ctrl->rconst[1], qc, qs, gt, ctrl->wpred);
-        // instant metric: mean density and coupling (cresso_v5.py:243-262)
-        ctrl->gden = (float)fmax(sumD / n, (double)eps);
-        const float icoup = hard ? (float)h.instant_metric_coupling : 0.0f;
-        ctrl->kappa = (float)((double)icoup / ((double)g.ndim * fmax(h.instant_metric_power, 0.25)));
-        // fixed-point scale of the port histogram: |P| <= (1+tm)*1e4 + max|pred|, <= n elements per bin
-        const double vmax = (1.0 + h.transport_mix) * 1.0e4 + pmax * 1.01 + 1.0;
-        ctrl->hs_P = ldexp(1.0, (int)floor(62.0 - log2(vmax * (double)g.n)));
-    }
-    __syncthreads();
-    if (tid < g.R) {
-        const int r = tid;
-        st.metric_cos[r] = s_f[r][1];
-        st.metric_p_cos[r] = s_f[r][2];
-        st.metric_sin[r] = s_f[r][3];
-        st.metric_p_sin[r] = s_f[r][4];
+        set_recon_lanes(g, s_stats, ctrl->rc[1], &ctrl->rconst[1], qc, qs, gt, s_tmpf, ctrl->wpred);
+        const double pmax = lanes_sum(pm, g.R, s_tmpd);
+        if (r == 0) {
+            // instant metric: mean density and coupling (cresso_v5.py:243-262)
+            ctrl->gden = (float)fmax(sumD / n, (double)eps);
+            const float icoup = hard ? (float)h.instant_metric_coupling : 0.0f;
+            ctrl->kappa = (float)((double)icoup / ((double)g.ndim * fmax(h.instant_metric_power, 0.25)));
+            // fixed-point scale of the port histogram: |P| <= (1+tm)*1e4 + max|pred|, <= n elements per bin
+            const double vmax = (1.0 + h.transport_mix) * 1.0e4 + pmax * 1.01 + 1.0;
+            ctrl->hs_P = ldexp(1.0, (int)floor(62.0 - log2(vmax * (double)g.n)));
+        }
     }
 }
 
@@ -1117,67 +1176,60 @@ __global__ __launch_bounds__(SP_FIN_NT) void marg_axes_kernel(Geom g, const unsi
 // ---------------------------------------------------------------------------
 // S3: tangent force, prediction error, port projection / histograms, t projection
 // ---------------------------------------------------------------------------
-template <int RM, int KC, typename PT, typename GT>
-__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
-                                                          const float* __restrict__ rowtab, const float* __restrict__ coltab,
-                                                          const ModeMeta* __restrict__ meta,
-                                                          const unsigned char* __restrict__ bins,
-                                                          const Ctrl* __restrict__ ctrl, const float* __restrict__ lt,
-                                                          const unsigned long long* __restrict__ rowfx,
-                                                          const unsigned long long* __restrict__ colfx,
-                                                          const float* __restrict__ colfac, float* __restrict__ tbuf,
-                                                          double* __restrict__ part, unsigned long long* __restrict__ hist,
-                                                          int hash_on, cresso_hyper h) {
-    constexpr int RW = 2 * RM, KA = KC + 1;
+template <int RM, int KC, typename PT, typename GT, int MODE>
+__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
+    Geom g, const GT* __restrict__ grad, const PT* __restrict__ param, const float* __restrict__ rowtab,
+    const float* __restrict__ coltab, const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins,
+    const Ctrl* __restrict__ ctrl, const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx,
+    const unsigned long long* __restrict__ colfx, const float* __restrict__ colfac, float* __restrict__ tbuf,
+    double* __restrict__ part, unsigned long long* __restrict__ hist, int hash_arg, cresso_hyper h) {
+    constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV3];
+    const SweepFlags F = sweep_flags<MODE>(g, hash_arg, 1, h);
     const Tile t = tile_of(g);
-    const int TB = g.T * g.B;
-    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
+    const int B = g.B;
+    const int TB = F.T * B;
     const int nr = (int)(t.r1 - t.r0);
-    // LDS: histogram [T][B] u64 | log hash metric [T][B] | alpha [PR][2][KA] | row factors [PR][RW] | row metric [PR]
+    // LDS: histogram [T][B] u64 | log hash metric [T][B] | row metric factor [PR]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
     float* s_lt = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
-    float* s_al = s_lt + TB;
-    float* s_row = s_al + (size_t)g.PR * 2 * KA;
-    float* s_rf = s_row + (size_t)g.PR * RW;
+    float* s_rf = s_lt + TB;
     const float eps = (float)h.eps;
     const float kappa = ctrl->kappa, gden = ctrl->gden;
-    const bool inst_on = kappa != 0.0f;
-    if (hash_on)
+    const bool inst_on = MODE == 1 ? true : kappa != 0.0f;
+    if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) {
             s_hist[i] = 0ull;
             s_lt[i] = lt[i];
         }
-    for (int j = threadIdx.x; j < nr * 2 * KA; j += SP_NT) {
-        const int lr = j / (2 * KA), w = (j / KA) & 1, k = j % KA;
-        s_al[j] = alpha_coef<KC>(g, meta, rowtab + (t.r0 + lr) * g.RW, ctrl->rc[w], ctrl->rconst[w], k);
-    }
-    for (int j = threadIdx.x; j < nr * RW; j += SP_NT) {
-        const int lr = j / RW, q = j - lr * RW;
-        s_row[j] = rowtab[(t.r0 + lr) * g.RW + q];
-    }
     for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
         s_rf[lr] = (inst_on && !g.one_d) ? marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps) : 1.0f;
+    // per-lane reconstruction weights of the metric field and the prediction
+    float gM[RW], gP[RW];
+    {
+        float b[KC];
+        load_cols<KC>(g, coltab, t, b);
+        recon_weights<RM, KC>(g, meta, b, ctrl->rc[0], gM);
+        recon_weights<RM, KC>(g, meta, b, ctrl->rc[1], gP);
+    }
+    const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
     __syncthreads();
-    float b[KC];
-    load_cols<KC>(g, coltab, t, b);
     const int64_t base = panel_base(g, t);
     const GT* __restrict__ gb = grad + base;
     const PT* __restrict__ pb = param + base;
     float* __restrict__ tb = tbuf + base;
+    const float* __restrict__ rt = rowtab + t.r0 * g.RW;
     const float inv_s = ctrl->inv_s, scale = ctrl->scale;
     const float mcoup = (float)h.metric_coupling;
     const float wd = (float)h.weight_decay;
-    const bool wd_on = h.weight_decay != 0.0;
     const float sg = h.maximize ? -1.f : 1.f;
-    const bool ls_on = h.local_sharpness != 0.0;
     const float ls = (float)h.local_sharpness;
     const float ipw = (float)fmax(h.instant_metric_power, 0.25);
     float ec = 1.0f;
     if (inst_on && !g.one_d && t.colok)
         ec = g.ntrail == 1 ? marg_factor(colfx[t.col], g.hs_col, (double)g.rows, gden, kappa, eps) : colfac[t.col];
-    const float invT = 1.0f / (float)T;
+    const float invT = 1.0f / (float)F.T;
     const float tm = (float)h.transport_mix;
     const float hs = (float)ctrl->hs_P;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
@@ -1198,8 +1250,8 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(Geom g,
                 if (i0 + u < nr) {
                     const uint32_t o = panel_off(g, i0 + u);
                     gv[u] = to_f(gb[o]);
-                    if (wd_on) pv[u] = to_f(pb[o]);
-                    if (hash_on) bv[u] = load_bins_at(bins, base, o, binbytes);
+                    if (F.wd_on) pv[u] = to_f(pb[o]);
+                    if (F.hash_on) bv[u] = load_bins_at(bins, base, o, F.binbytes);
                 }
             }
 #pragma unroll
@@ -1207,19 +1259,22 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(Geom g,
                 const int lr = i0 + u;
                 if (lr >= nr) break;
                 float f = sg * gv[u];
-                if (wd_on) f = f + wd * pv[u];
-                const float* __restrict__ al = s_al + lr * 2 * KA;
+                if (F.wd_on) f = f + wd * pv[u];
+                const float* __restrict__ ar = rt + lr * g.RW;
                 // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
-                const float lm = clampf(recon<KC>(al, b), -3.0f, 3.0f);
+                float lm = cM;
+#pragma unroll
+                for (int q = 0; q < RW; ++q) lm += ar[q] * gM[q];
+                lm = clampf(lm, -3.0f, 3.0f);
                 const float M = clampf(fexp(mcoup * lm), 0.06f, 16.0f);
                 float den = scale * M;
-                if (ls_on) {
+                if (F.ls_on) {
                     const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
                     den = den * clampf(1.0f + ls * fsqrt(fminf(rel, 100.0f)), 1.0f, 8.0f);
                 }
                 if (inst_on) {
                     float I;
-                    if (g.one_d) {
+                    if (MODE == 0 && g.one_d) {
                         const float rel = fmaxf(fminf(fabsf(f) * inv_s + eps, 1.0e4f), eps);
                         const float dens = fminf(ipw == 1.0f ? rel : fpow(rel, ipw), 1.0e6f);
                         I = fexp(kappa * flog(fmaxf(dens / gden, eps)));
@@ -1228,18 +1283,20 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(Geom g,
                     }
                     den = den * clampf(I, 0.08f, 12.0f);
                 }
-                if (hash_on) {
+                if (F.hash_on) {
                     float lsum = 0.f;
 #pragma unroll
                     for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= T) break;
-                        lsum += s_lt[tt * B + bin_of(bv[u], tt, bpb)];
+                        if (tt >= F.T) break;
+                        lsum += s_lt[tt * B + bin_of(bv[u], tt, F.bpb)];
                     }
                     den = den * clampf(fexp(lsum * invT), 0.08f, 12.0f);
                 }
                 const float tv = clampf(f * frcp(den + eps), -1.0e4f, 1.0e4f);
                 tb[panel_off(g, lr)] = tv;
-                const float pred = recon<KC>(al + KA, b);
+                float pred = cP;
+#pragma unroll
+                for (int q = 0; q < RW; ++q) pred += ar[q] * gP[q];
                 const float err = tv - pred;
                 const float P = err + tm * tv;
                 m_ee += err * err;
@@ -1252,18 +1309,17 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(Geom g,
                 m_rr += rat * rat; m_bb += bnd * bnd; m_oo += root * root;
                 m_rb += rat * bnd; m_ro += rat * root; m_bo += bnd * root;
                 m_tr += tv * rat; m_tb += tv * bnd; m_to += tv * root;
-                const float* __restrict__ ar = s_row + lr * RW;
 #pragma unroll
                 for (int q = 0; q < RW; ++q) {
                     ZP[q] += ar[q] * P;
                     ZT[q] += ar[q] * tv;
                 }
-                if (hash_on) {
+                if (F.hash_on) {
                     const unsigned long long v = to_fixed_s(P * hs);
 #pragma unroll
                     for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= T) break;
-                        atomicAdd(&s_hist[tt * B + bin_of(bv[u], tt, bpb)], v);
+                        if (tt >= F.T) break;
+                        atomicAdd(&s_hist[tt * B + bin_of(bv[u], tt, F.bpb)], v);
                     }
                 }
                 elem_fence();
@@ -1271,10 +1327,12 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(Geom g,
         }
     }
     __syncthreads();
-    if (hash_on)
+    if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT)
             if (s_hist[i]) atomicAdd(&hist[i], s_hist[i]);
-    Partials P{red, 15 + 4 * g.R};
+    float b[KC];
+    load_cols<KC>(g, coltab, t, b);
+    Partials P{red, 15 + 4 * g.R, NV3};
     const float mm[13] = {m_ee, m_P, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
 #pragma unroll
     for (int k = 0; k < 13; ++k) P.add(k, mm[k]);
@@ -1282,44 +1340,48 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(Geom g,
     P.add(14, 0.f);
     proj_finish<RM, KC>(g, meta, ZP, b, P, 15);
     proj_finish<RM, KC>(g, meta, ZT, b, P, 15 + 2 * g.R);
-    P.flush(part, g.nblk);
+    P.flush(part);
 }
 
 // ---------------------------------------------------------------------------
 // F3: surprise, hash impulse, confidence, contact, and every drive-shaping
 // coefficient that does not need the hash prediction's rms
 // ---------------------------------------------------------------------------
-__device__ void contact_bank(float* q, float* p, const float* port, const float* omega, float* calcium, float& action,
-                             float S, int R, const cresso_hyper& h) {
-    // cresso_v5.py:914-943
+// Contact oscillator of one bank (cresso_v5.py:914-943), lane r = mode r; the
+// energy and power sums over modes are summed in mode order.
+__device__ void contact_bank_lanes(float& q, float& p, float port, float omega, float& calcium, float& action, float S,
+                                   int R, const cresso_hyper& h, double* s_tmp) {
+    const int r = threadIdx.x & 63;
+    const bool on = r < R;
     const float dt = (float)h.dt;
     const float rd = (float)h.refractory_decay;
     const float plast = 1.0f + (float)h.surprise_gain * S / (1.0f + S);
     const float brake = 1.0f / (1.0f + (float)h.surprise_brake * S);
-    float gp[SP_MAXR];
+    float gp = 0.f;
     double e1 = 0.0, e2 = 0.0, pw = 0.0;
-    for (int r = 0; r < R; ++r) {
-        calcium[r] = calcium[r] * rd + (float)(1.0 - h.refractory_decay) * fabsf(port[r]);
-        const float gate = 1.0f / (1.0f + (float)h.refractory_gain * calcium[r]);
-        gp[r] = port[r] * gate * plast * brake;
-        e1 += (double)(p[r] * p[r]);
-        const float oq = omega[r] * q[r];
-        e2 += (double)(oq * oq);
-        pw += (double)(gp[r] * p[r]);
+    if (on) {
+        calcium = calcium * rd + (float)(1.0 - h.refractory_decay) * fabsf(port);
+        const float gate = 1.0f / (1.0f + (float)h.refractory_gain * calcium);
+        gp = port * gate * plast * brake;
+        e1 = (double)(p * p);
+        const float oq = omega * q;
+        e2 = (double)(oq * oq);
+        pw = (double)(gp * p);
     }
+    const double E1 = lanes_sum(e1, R, s_tmp), E2 = lanes_sum(e2, R, s_tmp), PW = lanes_sum(pw, R, s_tmp);
     if (R > 0) {
-        const float energy = 0.5f * ((float)(e1 / R) + (float)(e2 / R));
-        const float power = (float)(pw / R);
+        const float energy = 0.5f * ((float)(E1 / R) + (float)(E2 / R));
+        const float power = (float)(PW / R);
         action = action * 0.985f + dt * (power - energy);
     }
     const float fric = (float)h.impulse_friction + (float)h.contact_gain * tanhf(fabsf(action));
     const float damp = fmaxf(1.0f - dt * fric, 0.0f);
-    for (int r = 0; r < R; ++r) {
-        float pr = p[r] * damp;
-        const float qq = q[r];
-        pr = pr + dt * (gp[r] - (float)h.restoring * (omega[r] * omega[r]) * qq - (float)h.cubic * (qq * qq * qq));
-        p[r] = pr;
-        q[r] = clampf(qq + dt * pr, -8.0f, 8.0f);
+    if (on) {
+        float pr = p * damp;
+        const float qq = q;
+        pr = pr + dt * (gp - (float)h.restoring * (omega * omega) * qq - (float)h.cubic * (qq * qq * qq));
+        p = pr;
+        q = clampf(qq + dt * pr, -8.0f, 8.0f);
     }
 }
 
@@ -1336,23 +1398,46 @@ __device__ void contact_bank(float* q, float* p, const float* port, const float*
 //     mean(t Xn_v) - (G u)_v: small corrections to a directly summed term.
 // So sweep 4 can write the drive without c5; the hash term's rms comes from
 // sweep 4's sums and is added in sweep 5.
-__global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                         const double* __restrict__ stats, const double* __restrict__ gram,
-                                                         const double* __restrict__ part,
-                                                         unsigned long long* __restrict__ hist,
-                                                         const unsigned long long* __restrict__ counts,
-                                                         float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
-                                                         int step, int hash_on, int hard, int echo_on, cresso_hyper h) {
+__global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* __restrict__ meta,
+                                                        const double* __restrict__ stats, const double* __restrict__ gram,
+                                                        const double* __restrict__ part,
+                                                        unsigned long long* __restrict__ hist,
+                                                        const unsigned long long* __restrict__ counts,
+                                                        float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
+                                                        int step, int hash_on, int hard, int echo_on, cresso_hyper h) {
     __shared__ double s_m[NV3];
+    __shared__ double s_ec[2 * SP_MAXR];    // mean(t Xn_v)
+    __shared__ double s_u[3][2 * SP_MAXR];  // weights of pred, pred', echo
+    __shared__ float s_wp[2 * SP_MAXR], s_we[2 * SP_MAXR];
+    __shared__ float s_tmpf[64];
+    __shared__ double s_tmpd[64];
     const int tid = threadIdx.x;
     const double n = (double)g.n;
     const int R = g.R, V = 2 * g.R;
-    reduce_all(part, g.nblk, 15 + 4 * R, s_m);
+    // everything the mode lanes read, staged in LDS by all threads (global
+    // loads in flight together instead of one round trip per use)
+    __shared__ double s_gram[4 * SP_MAXR * SP_MAXR];
+    __shared__ double s_stats[4 * SP_MAXR];
+    __shared__ float s_mode[SP_MAXR][9];
+    __shared__ float s_scal[2];
+    for (int i = tid; i < V * V; i += SP_FN_NT) s_gram[i] = gram[i];
+    for (int i = tid; i < 4 * R; i += SP_FN_NT) s_stats[i] = stats[i];
+    for (int i = tid; i < 9 * R; i += SP_FN_NT) {
+        const int r = i / 9, j = i - 9 * r;
+        const float* src[8] = {st.omega, st.q_cos, st.q_sin, st.p_cos, st.p_sin, st.calcium_cos, st.calcium_sin, st.conf};
+        s_mode[r][j] = j < 8 ? src[j][r] : 0.f;
+    }
+    for (int i = tid; i < V; i += SP_FN_NT) s_u[0][i] = (double)ctrl->wpred[i];
+    if (tid == 0) {
+        s_scal[0] = *st.surprise;
+        s_scal[1] = *st.action;
+    }
+    load_sums(part, 15 + 4 * R, s_m);
     const float eps = (float)h.eps;
     // hash refractory / impulse (cresso_v5.py:1140-1184)
     if (hash_on) {
         const int TB = g.T * g.B;
-        for (int i = tid; i < TB; i += SP_FIN_NT) {
+        for (int i = tid; i < TB; i += SP_FN_NT) {
             const double cnt = fmax((double)counts[i], 1.0);
             const float cp = (float)((double)(long long)hist[i] / ctrl->hs_P / cnt);
             hist[i] = 0ull;
@@ -1364,217 +1449,177 @@ __global__ __launch_bounds__(SP_FIN_NT) void fin3_kernel(Geom g, const ModeMeta*
             imp_tab[i] = im;
         }
     }
-    __shared__ double s_st[SP_MAXR][4];
-    __shared__ float s_f[SP_MAXR][9];
-    __shared__ float s_sc[2];
-    __shared__ double s_ec[2 * SP_MAXR];   // mean(t Xn_v)
-    __shared__ double s_u[3][2 * SP_MAXR]; // weights of pred, pred', echo
-    __shared__ double s_q[2 * SP_MAXR][5];
-    if (tid < R) {
+    if (tid < 64) {
         const int r = tid;
-        for (int j = 0; j < 4; ++j) s_st[r][j] = stats[4 * r + j];
-        s_f[r][0] = st.omega[r];
-        s_f[r][1] = st.q_cos[r];
-        s_f[r][2] = st.q_sin[r];
-        s_f[r][3] = st.p_cos[r];
-        s_f[r][4] = st.p_sin[r];
-        s_f[r][5] = st.calcium_cos[r];
-        s_f[r][6] = st.calcium_sin[r];
-        s_f[r][7] = st.conf[r];
-    }
-    if (tid < V) {
-        const int r = tid >> 1, c = tid & 1;
-        const double mu = stats[4 * r + 2 * c], ic = stats[4 * r + 2 * c + 1];
-        s_ec[tid] = (s_m[15 + 2 * R + tid] - mu * s_m[2]) * ic / n;
-        s_u[0][tid] = (double)ctrl->wpred[tid];
-    }
-    if (tid == 0) {
-        s_sc[0] = *st.surprise;
-        s_sc[1] = *st.action;
-    }
-    __syncthreads();
-    if (tid == 0) {
+        const bool on = r < R;
         const double sP = s_m[1], sT = s_m[2];
         // surprise reservoir (cresso_v5.py:1127-1129)
-        const float sur = reservoir_f(s_sc[0], sqrtf((float)(s_m[0] / n) + eps), h.surprise_decay, step);
-        s_sc[0] = sur;
-        double stt[4 * SP_MAXR];
-        for (int r = 0; r < R; ++r)
-            for (int j = 0; j < 4; ++j) stt[4 * r + j] = s_st[r][j];
-        // port and echo projections -> mean(x Cn)
-        float pc[SP_MAXR], ps[SP_MAXR], ecs[SP_MAXR], ess[SP_MAXR];
-        for (int r = 0; r < R; ++r) {
-            const double mc = s_st[r][0], ic = s_st[r][1], ms = s_st[r][2], is = s_st[r][3];
-            pc[r] = (float)((s_m[15 + 2 * r] - mc * sP) * ic / n);
-            ps[r] = (float)((s_m[16 + 2 * r] - ms * sP) * is / n);
-            ecs[r] = (float)((s_m[15 + 2 * R + 2 * r] - mc * sT) * ic / n);
-            ess[r] = (float)((s_m[16 + 2 * R + 2 * r] - ms * sT) * is / n);
+        const float sur = reservoir_f(s_scal[0], sqrtf((float)(s_m[0] / n) + eps), h.surprise_decay, step);
+        // port and echo projections -> mean(x Cn); t projections in fp64
+        float pc = 0.f, ps = 0.f, ecs = 0.f, ess = 0.f;
+        if (on) {
+            const double mc = s_stats[4 * r], ic = s_stats[4 * r + 1], ms = s_stats[4 * r + 2], is = s_stats[4 * r + 3];
+            pc = (float)((s_m[15 + 2 * r] - mc * sP) * ic / n);
+            ps = (float)((s_m[16 + 2 * r] - ms * sP) * is / n);
+            const double ecd = (s_m[15 + 2 * R + 2 * r] - mc * sT) * ic / n;
+            const double esd = (s_m[16 + 2 * R + 2 * r] - ms * sT) * is / n;
+            ecs = (float)ecd;
+            ess = (float)esd;
+            s_ec[2 * r] = ecd;
+            s_ec[2 * r + 1] = esd;
         }
-        float om[SP_MAXR], qc[SP_MAXR], qs[SP_MAXR], pcv[SP_MAXR], psv[SP_MAXR], cac[SP_MAXR], cas[SP_MAXR];
-        for (int r = 0; r < R; ++r) {
-            om[r] = s_f[r][0]; qc[r] = s_f[r][1]; qs[r] = s_f[r][2]; pcv[r] = s_f[r][3]; psv[r] = s_f[r][4];
-            cac[r] = s_f[r][5]; cas[r] = s_f[r][6];
+        float om = 0.f, qc = 0.f, qs = 0.f, pcv = 0.f, psv = 0.f, cac = 0.f, cas = 0.f, conf = 0.f;
+        if (on) {
+            om = s_mode[r][0]; qc = s_mode[r][1]; qs = s_mode[r][2]; pcv = s_mode[r][3]; psv = s_mode[r][4];
+            cac = s_mode[r][5]; cas = s_mode[r][6]; conf = s_mode[r][7];
         }
         // confidence (cresso_v5.py:1199-1202) with the pre-contact q
-        const float cd = (float)h.confidence_decay;
-        float gt[SP_MAXR];
-        for (int r = 0; r < R; ++r) {
-            const float pe = sqrtf(pc[r] * pc[r] + ps[r] * ps[r] + eps);
-            const float sup = (pc[r] * qc[r] + ps[r] * qs[r]) / (pe * sqrtf(qc[r] * qc[r] + qs[r] * qs[r] + eps) + eps);
-            const float c = s_f[r][7] * cd + (float)(1.0 - h.confidence_decay) * clampf(sup, -1.0f, 1.0f);
-            s_f[r][7] = clampf(c, -4.0f, 4.0f);
-            gt[r] = sigmoidf_((float)h.confidence_gain * s_f[r][7]);
+        float gt = 0.f;
+        if (on) {
+            const float pe = sqrtf(pc * pc + ps * ps + eps);
+            const float sup = (pc * qc + ps * qs) / (pe * sqrtf(qc * qc + qs * qs + eps) + eps);
+            const float c = conf * (float)h.confidence_decay + (float)(1.0 - h.confidence_decay) * clampf(sup, -1.0f, 1.0f);
+            conf = clampf(c, -4.0f, 4.0f);
+            gt = sigmoidf_((float)h.confidence_gain * conf);
         }
         // contact on the cos bank then the sin bank with the shared action
-        float action = s_sc[1];
-        contact_bank(qc, pcv, pc, om, cac, action, sur, R, h);
-        contact_bank(qs, psv, ps, om, cas, action, sur, R, h);
-        s_sc[1] = action;
-        for (int r = 0; r < R; ++r) {
-            s_f[r][1] = qc[r]; s_f[r][2] = qs[r]; s_f[r][3] = pcv[r]; s_f[r][4] = psv[r];
-            s_f[r][5] = cac[r]; s_f[r][6] = cas[r];
+        float action = s_scal[1];
+        contact_bank_lanes(qc, pcv, pc, om, cac, action, sur, R, h, s_tmpd);
+        contact_bank_lanes(qs, psv, ps, om, cas, action, sur, R, h, s_tmpd);
+        set_recon_lanes(g, s_stats, ctrl->rc[2], &ctrl->rconst[2], qc, qs, gt, s_tmpf, s_wp);
+        if (echo_on) set_recon_lanes(g, s_stats, ctrl->rc[3], &ctrl->rconst[3], ecs, ess, 1.0f, s_tmpf, s_we);
+        if (on) {
+            st.q_cos[r] = qc; st.q_sin[r] = qs; st.p_cos[r] = pcv; st.p_sin[r] = psv;
+            st.calcium_cos[r] = cac; st.calcium_sin[r] = cas; st.conf[r] = conf;
+            s_u[1][2 * r] = (double)s_wp[2 * r];
+            s_u[1][2 * r + 1] = (double)s_wp[2 * r + 1];
+            s_u[2][2 * r] = echo_on ? (double)s_we[2 * r] : 0.0;
+            s_u[2][2 * r + 1] = echo_on ? (double)s_we[2 * r + 1] : 0.0;
         }
-        float wp[2 * SP_MAXR], we[2 * SP_MAXR];
-        set_recon(g, stt, ctrl->rc[2], ctrl->rconst[2], qc, qs, gt, wp);
-        for (int v = 0; v < V; ++v) we[v] = 0.f;
-        if (echo_on) set_recon(g, stt, ctrl->rc[3], ctrl->rconst[3], ecs, ess, nullptr, we);
-        for (int v = 0; v < V; ++v) {
-            s_u[1][v] = (double)wp[v];
-            s_u[2][v] = (double)we[v];
+        if (r == 0) {
+            *st.surprise = sur;
+            *st.action = action;
         }
-    }
-    __syncthreads();
-    // Gram products, one thread per carrier v
-    if (tid < V) {
-        const int v = tid;
-        double gu = 0.0, gup = 0.0, gue = 0.0;
-        for (int w = 0; w < V; ++w) {
-            const double gvw = gram[v * V + w];
-            gu += gvw * s_u[0][w];
-            gup += gvw * s_u[1][w];
-            gue += gvw * s_u[2][w];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        // Gram products, lane v = carrier v (v < 2R <= 32)
+        double q0 = 0.0, q1 = 0.0, q2 = 0.0, q3 = 0.0, q4 = 0.0;
+        if (r < V) {
+            const int v = r;
+            double gu = 0.0, gup = 0.0, gue = 0.0;
+            for (int w = 0; w < V; ++w) {
+                const double gvw = s_gram[v * V + w];
+                gu += gvw * s_u[0][w];
+                gup += gvw * s_u[1][w];
+                gue += gvw * s_u[2][w];
+            }
+            const double du = s_u[1][v] - s_u[0][v];
+            q0 = s_u[1][v] * gup;        // -> mean(pred'^2)
+            q1 = s_u[2][v] * gue;        // -> mean(echo^2)
+            q2 = du * (gup - gu);        // -> mean(D^2)
+            q3 = du * (s_ec[v] - gu);    // -> mean(err D)
+            q4 = s_u[1][v] * s_ec[v];    // -> mean(t pred')
         }
-        const double du = s_u[1][v] - s_u[0][v];
-        s_q[v][0] = s_u[1][v] * gup;            // -> mean(pred'^2)
-        s_q[v][1] = s_u[2][v] * gue;            // -> mean(echo^2)
-        s_q[v][2] = du * (gup - gu);            // -> mean(D^2)
-        s_q[v][3] = du * (s_ec[v] - gu);        // -> mean(err D)
-        s_q[v][4] = s_u[1][v] * s_ec[v];        // -> mean(t pred')
-    }
-    __syncthreads();
-    if (tid == 0) {
-        double q[5] = {0, 0, 0, 0, 0};
-        for (int v = 0; v < V; ++v)
-            for (int j = 0; j < 5; ++j) q[j] += s_q[v][j];
-        const float S = s_sc[0];
-        // shaped / core coefficients from the moments of t (cresso_v5.py:1315-1337)
-        const double Stt = s_m[3], Srr = s_m[4], Sbb = s_m[5], Soo = s_m[6], Srb = s_m[7], Sro = s_m[8], Sbo = s_m[9];
-        const double Str = s_m[10], Stb = s_m[11], Sto = s_m[12];
-        const float frms = sqrtf((float)(Stt / n) + eps);
-        const float rms_rat = sqrtf((float)(Srr / n) + eps);
-        const float rms_root = sqrtf((float)(Soo / n) + eps);
-        const float kroot = rms_rat / fmaxf(rms_root, eps);
-        const float spike = (float)h.spike_mix / (1.0f + S);
-        const float rmix = (hard ? (float)h.root_channel_mix : 0.0f) / (1.0f + 0.5f * S);
-        const double ar = (double)((1.0f - rmix) * (1.0f - spike));
-        const double ab = (double)((1.0f - rmix) * spike);
-        const double ao = (double)(rmix * kroot);
-        const double sh2 = ar * ar * Srr + ab * ab * Sbb + ao * ao * Soo + 2.0 * (ar * ab * Srb + ar * ao * Sro + ab * ao * Sbo);
-        const float srms = sqrtf((float)(sh2 / n) + eps);
-        const float dmix = (float)h.direct_force_mix / (1.0f + 0.35f * S);
-        const float kdir = srms / fmaxf(frms, eps);
-        const double cr = (1.0 - (double)dmix) * ar, cb = (1.0 - (double)dmix) * ab, co = (1.0 - (double)dmix) * ao;
-        const double ct = (double)(dmix * kdir);
-        const double core2 = cr * cr * Srr + cb * cb * Sbb + co * co * Soo + ct * ct * Stt +
-                             2.0 * (cr * cb * Srb + cr * co * Sro + cb * co * Sbo + ct * cr * Str + ct * cb * Stb + ct * co * Sto);
-        // alignment gate and prediction mix (cresso_v5.py:1303-1313)
-        const float prms = sqrtf((float)q[0] + eps);
-        const float align = clampf((float)q[4] / (frms * prms + eps), -1.0f, 1.0f);
-        float agate = clampf((align + 1.0f) * 0.5f, 0.0f, 1.0f);
-        if (!(prms > (float)sqrt(h.eps))) agate = 0.0f;
-        const double warm = h.warmup_steps == 0 ? 1.0 : 1.0 - exp(-(double)step / (double)(h.warmup_steps > 1 ? h.warmup_steps : 1));
-        const float mix = (float)(h.prediction_mix * warm) * agate * (1.0f / (1.0f + S));
-        // residual feedback: err' rms from the directly summed err rms and the Gram corrections
-        const float crms = sqrtf((float)(core2 / n) + eps);
-        const double ee = fmax(s_m[0] / n - 2.0 * q[3] + q[2], 0.0);
-        const float erms = sqrtf((float)ee + eps);
-        const float kres = crms / fmaxf(erms, eps);
-        const float resmix = (float)h.residual_feedback_mix / (1.0f + S);
-        float kecho = 0.f;
-        if (hard && echo_on) kecho = srms / fmaxf(sqrtf((float)q[1] + eps), eps);
-        const double c0 = 1.0 - (double)mix, c1 = mix, c2 = h.novelty_mix, c3 = (double)(resmix * kres);
-        const double c4 = hard ? h.echo_mix * (double)kecho : 0.0;
-        const float clip = (float)h.drive_clip;
-        // drive without the hash term:
-        //   c0 cr rat + c0 cb clip tanh + c0 co root + (c0 ct + c3) t + (c1 - c3) pred' + c4 echo + c2 clip tanh(err' ns)
-        ctrl->k_rat = (float)(c0 * cr);
-        ctrl->k_ths = (float)(c0 * cb * (double)clip);
-        ctrl->k_root = (float)(c0 * co);
-        ctrl->k_t = (float)(c0 * ct + c3);
-        ctrl->k_pred = (float)(c1 - c3);
-        ctrl->k_echo = (float)c4;
-        ctrl->k_nov = (float)(c2 * (double)clip);
-        ctrl->nscale = 1.0f / (clip * (1.0f + S));
-        ctrl->srms = srms;
-    }
-    __syncthreads();
-    if (tid < R) {
-        const int r = tid;
-        st.q_cos[r] = s_f[r][1];
-        st.q_sin[r] = s_f[r][2];
-        st.p_cos[r] = s_f[r][3];
-        st.p_sin[r] = s_f[r][4];
-        st.calcium_cos[r] = s_f[r][5];
-        st.calcium_sin[r] = s_f[r][6];
-        st.conf[r] = s_f[r][7];
-    }
-    if (tid == 0) {
-        *st.surprise = s_sc[0];
-        *st.action = s_sc[1];
+        const double Q0 = lanes_sum(q0, V, s_tmpd), Q1 = lanes_sum(q1, V, s_tmpd), Q2 = lanes_sum(q2, V, s_tmpd);
+        const double Q3 = lanes_sum(q3, V, s_tmpd), Q4 = lanes_sum(q4, V, s_tmpd);
+        if (r == 0) {
+            const float S = sur;
+            // shaped / core coefficients from the moments of t (cresso_v5.py:1315-1337)
+            const double Stt = s_m[3], Srr = s_m[4], Sbb = s_m[5], Soo = s_m[6], Srb = s_m[7], Sro = s_m[8], Sbo = s_m[9];
+            const double Str = s_m[10], Stb = s_m[11], Sto = s_m[12];
+            const float frms = sqrtf((float)(Stt / n) + eps);
+            const float rms_rat = sqrtf((float)(Srr / n) + eps);
+            const float rms_root = sqrtf((float)(Soo / n) + eps);
+            const float kroot = rms_rat / fmaxf(rms_root, eps);
+            const float spike = (float)h.spike_mix / (1.0f + S);
+            const float rmix = (hard ? (float)h.root_channel_mix : 0.0f) / (1.0f + 0.5f * S);
+            const double ar = (double)((1.0f - rmix) * (1.0f - spike));
+            const double ab = (double)((1.0f - rmix) * spike);
+            const double ao = (double)(rmix * kroot);
+            const double sh2 = ar * ar * Srr + ab * ab * Sbb + ao * ao * Soo + 2.0 * (ar * ab * Srb + ar * ao * Sro + ab * ao * Sbo);
+            const float srms = sqrtf((float)(sh2 / n) + eps);
+            const float dmix = (float)h.direct_force_mix / (1.0f + 0.35f * S);
+            const float kdir = srms / fmaxf(frms, eps);
+            const double cr = (1.0 - (double)dmix) * ar, cb = (1.0 - (double)dmix) * ab, co = (1.0 - (double)dmix) * ao;
+            const double ct = (double)(dmix * kdir);
+            const double core2 = cr * cr * Srr + cb * cb * Sbb + co * co * Soo + ct * ct * Stt +
+                                 2.0 * (cr * cb * Srb + cr * co * Sro + cb * co * Sbo + ct * cr * Str + ct * cb * Stb + ct * co * Sto);
+            // alignment gate and prediction mix (cresso_v5.py:1303-1313)
+            const float prms = sqrtf((float)Q0 + eps);
+            const float align = clampf((float)Q4 / (frms * prms + eps), -1.0f, 1.0f);
+            float agate = clampf((align + 1.0f) * 0.5f, 0.0f, 1.0f);
+            if (!(prms > (float)sqrt(h.eps))) agate = 0.0f;
+            const double warm = h.warmup_steps == 0 ? 1.0 : 1.0 - exp(-(double)step / (double)(h.warmup_steps > 1 ? h.warmup_steps : 1));
+            const float mix = (float)(h.prediction_mix * warm) * agate * (1.0f / (1.0f + S));
+            // residual feedback: err' rms from the directly summed err rms and the Gram corrections
+            const float crms = sqrtf((float)(core2 / n) + eps);
+            const double ee = fmax(s_m[0] / n - 2.0 * Q3 + Q2, 0.0);
+            const float erms = sqrtf((float)ee + eps);
+            const float kres = crms / fmaxf(erms, eps);
+            const float resmix = (float)h.residual_feedback_mix / (1.0f + S);
+            float kecho = 0.f;
+            if (hard && echo_on) kecho = srms / fmaxf(sqrtf((float)Q1 + eps), eps);
+            const double c0 = 1.0 - (double)mix, c1 = mix, c2 = h.novelty_mix, c3 = (double)(resmix * kres);
+            const double c4 = hard ? h.echo_mix * (double)kecho : 0.0;
+            const float clip = (float)h.drive_clip;
+            // drive without the hash term:
+            //   c0 cr rat + c0 cb clip tanh + c0 co root + (c0 ct + c3) t + (c1 - c3) pred' + c4 echo + c2 clip tanh(err' ns)
+            ctrl->k_rat = (float)(c0 * cr);
+            ctrl->k_ths = (float)(c0 * cb * (double)clip);
+            ctrl->k_root = (float)(c0 * co);
+            ctrl->k_t = (float)(c0 * ct + c3);
+            ctrl->k_pred = (float)(c1 - c3);
+            ctrl->k_echo = (float)c4;
+            ctrl->k_nov = (float)(c2 * (double)clip);
+            ctrl->nscale = 1.0f / (clip * (1.0f + S));
+            ctrl->srms = srms;
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
 // S4: drive without the hash term, written over t; sums for the drive energy
 // ---------------------------------------------------------------------------
-template <int RM, int KC>
-__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(Geom g, const float* __restrict__ rowtab,
-                                                          const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
-                                                          const unsigned char* __restrict__ bins,
-                                                          const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
-                                                          float* __restrict__ tbuf, double* __restrict__ part, int hash_on,
-                                                          int echo_on, cresso_hyper h) {
-    constexpr int KA = KC + 1;
+template <int RM, int KC, int MODE>
+__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
+    Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
+    const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
+    float* __restrict__ tbuf, double* __restrict__ part, int hash_arg, int echo_on, cresso_hyper h) {
+    constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV4];
+    const SweepFlags F = sweep_flags<MODE>(g, hash_arg, 1, h);
     const Tile t = tile_of(g);
-    const int TB = g.T * g.B;
-    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
+    const int B = g.B;
+    const int TB = F.T * B;
     const int nr = (int)(t.r1 - t.r0);
-    // LDS: impulse table [T][B] | alpha [PR][2][KA] (pred', then k_pred pred' + k_echo echo)
+    // LDS: impulse table [T][B]
     float* s_imp = reinterpret_cast<float*>(dyn);
-    float* s_al = s_imp + TB;
-    if (hash_on)
+    if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
+    // per-lane weights of pred' and of k_pred pred' + k_echo echo
+    float gQ[RW], gX[RW];
     const float kp = ctrl->k_pred, ke = ctrl->k_echo;
-    for (int j = threadIdx.x; j < nr * KA; j += SP_NT) {
-        const int lr = j / KA, k = j - lr * KA;
-        const float* arow = rowtab + (t.r0 + lr) * g.RW;
-        const float ap = alpha_coef<KC>(g, meta, arow, ctrl->rc[2], ctrl->rconst[2], k);
-        const float ae = echo_on ? alpha_coef<KC>(g, meta, arow, ctrl->rc[3], ctrl->rconst[3], k) : 0.f;
-        s_al[lr * 2 * KA + k] = ap;
-        s_al[lr * 2 * KA + KA + k] = kp * ap + ke * ae;
+    {
+        float b[KC];
+        load_cols<KC>(g, coltab, t, b);
+        recon_weights<RM, KC>(g, meta, b, ctrl->rc[2], gQ);
+        float gE[RW];
+        recon_weights<RM, KC>(g, meta, b, ctrl->rc[3], gE);
+#pragma unroll
+        for (int q = 0; q < RW; ++q) gX[q] = kp * gQ[q] + (echo_on ? ke * gE[q] : 0.f);
     }
+    const float cQ = ctrl->rconst[2];
+    const float cX = kp * ctrl->rconst[2] + (echo_on ? ke * ctrl->rconst[3] : 0.f);
     __syncthreads();
-    float b[KC];
-    load_cols<KC>(g, coltab, t, b);
     const int64_t base = panel_base(g, t);
     float* __restrict__ tb = tbuf + base;
+    const float* __restrict__ rt = rowtab + t.r0 * g.RW;
     const float eps = (float)h.eps;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
     const float k_rat = ctrl->k_rat, k_ths = ctrl->k_ths, k_root = ctrl->k_root, k_t = ctrl->k_t, k_nov = ctrl->k_nov;
     const float ns = ctrl->nscale;
-    const float invT = 1.0f / (float)T;
+    const float invT = 1.0f / (float)F.T;
     float a_dd = 0.f, a_dh = 0.f, a_hh = 0.f;
     if (t.colok) {
         for (int i0 = 0; i0 < nr; i0 += SP_U) {
@@ -1587,7 +1632,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(Geom g,
                 if (i0 + u < nr) {
                     const uint32_t o = panel_off(g, i0 + u);
                     tvs[u] = tb[o];
-                    if (hash_on) bv[u] = load_bins_at(bins, base, o, binbytes);
+                    if (F.hash_on) bv[u] = load_bins_at(bins, base, o, F.binbytes);
                 }
             }
 #pragma unroll
@@ -1595,9 +1640,13 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(Geom g,
                 const int lr = i0 + u;
                 if (lr >= nr) break;
                 const float tv = tvs[u];
-                const float* __restrict__ al = s_al + lr * 2 * KA;
-                const float pred = recon<KC>(al, b);
-                const float mixed = recon<KC>(al + KA, b);
+                const float* __restrict__ ar = rt + lr * g.RW;
+                float pred = cQ, mixed = cX;
+#pragma unroll
+                for (int q = 0; q < RW; ++q) {
+                    pred += ar[q] * gQ[q];
+                    mixed += ar[q] * gX[q];
+                }
                 const float err = tv - pred;
                 const float nov = ftanh(err * ns);
                 float rat, ths, root;
@@ -1605,12 +1654,12 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(Geom g,
                 const float d = k_rat * rat + k_ths * ths + k_root * root + k_t * tv + mixed + k_nov * nov;
                 tb[panel_off(g, lr)] = d;
                 a_dd += d * d;
-                if (hash_on) {
+                if (F.hash_on) {
                     float hp = 0.f;
 #pragma unroll
                     for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= T) break;
-                        hp += s_imp[tt * B + bin_of(bv[u], tt, bpb)];
+                        if (tt >= F.T) break;
+                        hp += s_imp[tt * B + bin_of(bv[u], tt, F.bpb)];
                     }
                     hp = hp * invT;
                     a_dh += d * hp;
@@ -1620,20 +1669,20 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(Geom g,
             }
         }
     }
-    Partials P{red, 3};
+    Partials P{red, 3, NV4};
     P.add(0, a_dd);
     P.add(1, a_dh);
     P.add(2, a_hh);
-    P.flush(part, g.nblk);
+    P.flush(part);
 }
 
 // F4: hash-term coefficient, drive energy reservoir, gain.
 //   sum drive^2 = sum d^2 + 2 c5 sum d hp + c5^2 sum hp^2
-__global__ __launch_bounds__(SP_FIN_NT) void fin4_kernel(Geom g, const double* __restrict__ part, SpecState st,
-                                                         Ctrl* __restrict__ ctrl, int step, int hash_on, int hard,
-                                                         cresso_hyper h) {
-    __shared__ double s_m[3];
-    reduce_all(part, g.nblk, 3, s_m);
+__global__ __launch_bounds__(SP_FN_NT) void fin4_kernel(Geom g, const double* __restrict__ part, SpecState st,
+                                                        Ctrl* __restrict__ ctrl, int step, int hash_on, int hard,
+                                                        cresso_hyper h) {
+    __shared__ double s_m[NV4];
+    reduce_bm<NV4>(part, g.nblk, 3, s_m);
     if (threadIdx.x != 0) return;
     const double n = (double)g.n;
     const float eps = (float)h.eps;
@@ -1886,6 +1935,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.bins = take((size_t)g.binbytes * (size_t)g.n);
     o.tbuf = take(sizeof(float) * (size_t)g.n);
     o.part = take(sizeof(double) * (size_t)NVMAX * std::max(g.nblk, g.nblk1));
+    o.sums = take(sizeof(double) * (size_t)NVMAX);
     o.hist = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
     o.lt = take(sizeof(float) * (size_t)g.T * g.B);
     o.imp = take(sizeof(float) * (size_t)g.T * g.B);
@@ -1902,16 +1952,13 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
 
 template <typename T> T* at(void* ws, size_t off) { return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off); }
 
-template <int RM> size_t lds_sweep2(const Geom& g) {
-    return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * (size_t)g.PR * (2 * RM + 4);
+size_t lds_sweep2(const Geom& g) {
+    return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * 4 * (size_t)g.PR;
 }
-template <int RM, int KC> size_t lds_sweep3(const Geom& g) {
-    return (sizeof(unsigned long long) + sizeof(float)) * g.T * g.B +
-           sizeof(float) * (size_t)g.PR * (2 * (KC + 1) + 2 * RM + 1);
+size_t lds_sweep3(const Geom& g) {
+    return (sizeof(unsigned long long) + sizeof(float)) * g.T * g.B + sizeof(float) * (size_t)g.PR;
 }
-template <int KC> size_t lds_sweep4(const Geom& g) {
-    return sizeof(float) * ((size_t)g.T * g.B + (size_t)g.PR * 2 * (KC + 1));
-}
+size_t lds_sweep4(const Geom& g) { return sizeof(float) * (size_t)g.T * g.B; }
 constexpr size_t SP_LDS_MAX = 64 * 1024;
 
 template <int RM, int KC, typename PT, typename GT>
@@ -1939,6 +1986,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     const unsigned char* bins = at<unsigned char>(ws, o.bins);
     const unsigned long long* counts = at<unsigned long long>(ws, o.counts);
     double* part = at<double>(ws, o.part);
+    double* sums = at<double>(ws, o.sums);
     unsigned long long* hist = at<unsigned long long>(ws, o.hist);
     float* lt = at<float>(ws, o.lt);
     float* imp = at<float>(ws, o.imp);
@@ -1953,7 +2001,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     const double* gram = at<double>(ws, o.gram);
     const int step = d.step;
     const int axes_on = (hard && h.instant_metric_coupling != 0.0 && !g.one_d) ? 1 : 0;
-    const size_t l2 = lds_sweep2<RM>(g), l3 = lds_sweep3<RM, KC>(g), l4 = lds_sweep4<KC>(g);
+    const size_t l2 = lds_sweep2(g), l3 = lds_sweep3(g), l4 = lds_sweep4(g);
     if (l2 > SP_LDS_MAX || l3 > SP_LDS_MAX || l4 > SP_LDS_MAX)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_tables x hash_bins = %d needs %zu bytes of LDS per block",
                     g.T * g.B, std::max(l2, std::max(l3, l4)));
@@ -1963,20 +2011,35 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
         hipLaunchKernelGGL((sweep1_kernel<PT, GT, true>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, h);
     else
         hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, h);
-    hipLaunchKernelGGL(fin1_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, part, st, ctrl, rowfx, colfx, step, h);
-    hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins, ctrl,
-                       part, hist, rowfx, colfx, hash_on, axes_on, h);
-    hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, bounds, part, hist, counts, lt, st,
+    hipLaunchKernelGGL(fin1_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, rowfx, colfx, step, h);
+    const bool fast = fast_mode(g, hash_on, axes_on, h);
+    if (fast)
+        hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
+                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, h);
+    else
+        hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 0>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
+                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, h);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2), dim3(256), 0, s, part, g.nblk, NV2, sums);
+    hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st,
                        ctrl, step, hash_on, hard, h);
     if (axes_on && g.ntrail > 1)
         hipLaunchKernelGGL(marg_axes_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, colfx, terms, colfac, ctrl, (float)h.eps);
-    hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins, ctrl,
-                       lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
-    hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, stats, gram, part, hist, counts, imp, st, ctrl,
+    if (fast)
+        hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 1>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
+                           ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
+    else
+        hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 0>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
+                           ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3), dim3(256), 0, s, part, g.nblk, NV3, sums);
+    hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
                        step, hash_on, hard, echo_on, h);
-    hipLaunchKernelGGL((sweep4_kernel<RM, KC>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
-                       hash_on, echo_on, h);
-    hipLaunchKernelGGL(fin4_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, part, st, ctrl, step, hash_on, hard, h);
+    if (fast)
+        hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
+                           hash_on, echo_on, h);
+    else
+        hipLaunchKernelGGL((sweep4_kernel<RM, KC, 0>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
+                           hash_on, echo_on, h);
+    hipLaunchKernelGGL(fin4_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, step, hash_on, hard, h);
     const size_t l5 = hash_on ? sizeof(float) * (size_t)g.T * g.B : 0;
     const bool pv4 = ((uintptr_t)param % (4 * sizeof(PT))) == 0;
     if (hash_on && pv4)
