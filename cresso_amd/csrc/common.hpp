@@ -49,6 +49,46 @@ template <typename T> __device__ __forceinline__ T from_wd(double v) { return fr
 template <> __device__ __forceinline__ double from_wd<double>(double v) { return v; }
 
 // ---------------------------------------------------------------------------
+// global-memory views of caller pointers: the address-space cast lets the
+// compiler emit global_load / global_store (no flat aperture handling, no LDS
+// counter waits) for pointers that arrive through generic pointer tables
+// ---------------------------------------------------------------------------
+#define CRESSO_GLOBAL __attribute__((address_space(1)))
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f32x4 gload4(const float* p) { return *(const CRESSO_GLOBAL f32x4*)p; }
+__device__ __forceinline__ void gstore4(float* p, f32x4 v) { *(CRESSO_GLOBAL f32x4*)p = v; }
+__device__ __forceinline__ u32x2 gload2u(const void* p) { return *(const CRESSO_GLOBAL u32x2*)p; }
+__device__ __forceinline__ void gstore2u(void* p, u32x2 v) { *(CRESSO_GLOBAL u32x2*)p = v; }
+
+// Buffer view of one array: a resource descriptor (base, size in bytes) in
+// SGPRs, addressed by a per-lane byte offset (one VGPR shared by every access
+// of a pass) plus a uniform byte offset in an SGPR, so a thread's strided
+// accesses need no address registers of their own.  Accesses at or beyond
+// `bytes` read 0 and store nothing.  Word 3 is the gfx9-family raw-buffer
+// format (32-bit data).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+// Stores take the whole offset in the VGPR and a literal 0 soffset: after a
+// store of more than 8 bytes whose soffset is an SGPR, the compiler does not
+// wait before the next VALU overwrites the store's data registers, and on
+// gfx950 the last lanes of each 16-lane pass then store the new values.
+__device__ __forceinline__ void bstore4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff + soff, 0, 0);
+}
+__device__ __forceinline__ u32x2 bload2u(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+}
+__device__ __forceinline__ void bstore2u(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, u32x2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, voff + soff, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
 // fast per-element math (hardware approximations, ~1 ulp on their domain)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -69,6 +109,34 @@ __device__ __forceinline__ float ftanh(float x) {
 }
 __device__ __forceinline__ float fsign(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f); }
 __device__ __forceinline__ float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
+// clamp to [lo, hi] (lo <= hi) in one instruction: the median of three
+__device__ __forceinline__ float med3f(float x, float lo, float hi) { return __builtin_amdgcn_fmed3f(x, lo, hi); }
+// |m| with the sign of s (one bitfield insert)
+__device__ __forceinline__ float with_sign(float m, float s) { return copysignf(m, s); }
+
+// Unsigned parts of the drive shaping of t (cresso_v5.py:1321-1324, scalar
+// route 1563-1566) from at = |t|:
+//   rat  = t/(1+|t|/clip)           -> |rat|  = at/(1+at/clip)
+//   tanh(t/clip)                    -> |tanh| = (1-e)/(1+e), e = exp(-2 at/clip)
+//   root = sign(t) sqrt(min(|t|,clip^2)+eps) -> |root| (0 when t == 0)
+// All three carry the sign of t, so every product of two of them, or of one
+// with t, equals the product of their magnitudes.  k2 = -2 log2(e) / clip.
+struct Shape3A {
+    float rat, th, root;
+};
+__device__ __forceinline__ Shape3A shape3a(float at, float k2, float iclip, float clip2, float eps) {
+    Shape3A s;
+    const float ex = fexp2(k2 * at);
+    const float d1 = 1.0f + ex;
+    const float d2 = fmaf(at, iclip, 1.0f);
+    const float inv = frcp(d1 * d2);
+    const float u = d2 * inv;   // 1/d1
+    s.th = fmaf(-ex, u, u);     // (1-e)/(1+e)
+    s.rat = at * (d1 * inv);    // at/d2
+    const float r = fsqrt(fminf(at, clip2) + eps);
+    s.root = at > 0.0f ? r : 0.0f;
+    return s;
+}
 
 // double versions for the f64 work dtype (accurate libm)
 __device__ __forceinline__ double fexp(double x) { return exp(x); }

@@ -63,21 +63,67 @@ __device__ __forceinline__ float uni(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+// Read of a value that every thread of the block reads at the same address
+// (a 0-dim state tensor): a scalar load through the constant address space.
+// Each value is read once, before this kernel writes it back at its end.
+__device__ __forceinline__ float ld_uniform(const float* p) {
+    return *(const __attribute__((address_space(4))) float*)p;
+}
+// Pins four values in VGPRs at this point of the program: work that depends on
+// them cannot be hoisted above it, so each slot's arithmetic stays in its own
+// region (without this, IR passes move the cheap per-element math of all 16
+// slots ahead of the transcendental chains and the kernel spills).
+__device__ __forceinline__ void pin4(float* v) {
+    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+}
+// The same for an accumulator at the end of a slot: the slot's contributions
+// are complete here (otherwise they may be sunk to the end of the pass, with
+// every slot's inputs kept alive until then).
+__device__ __forceinline__ void pin1(float& v) { asm volatile("" : "+v"(v)); }
 
 // ---- vector access -------------------------------------------------------
 template <typename T> struct V4;
 template <> struct V4<float> {
+    // buffer forms: 4 consecutive elements at byte offset voff + soff
+    __device__ static void bld(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float* o) {
+        const f32x4 v = bload4(r, voff, soff);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+    __device__ static void bst(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const float* v) {
+        f32x4 w;
+        w.x = v[0]; w.y = v[1]; w.z = v[2]; w.w = v[3];
+        bstore4(r, voff, soff, w);
+    }
     __device__ static void ld(const float* p, int64_t e, float* o) {
-        float4 v = *reinterpret_cast<const float4*>(p + e);
+        const f32x4 v = gload4(p + e);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
     }
     __device__ static void st(float* p, int64_t e, const float* v) {
-        *reinterpret_cast<float4*>(p + e) = make_float4(v[0], v[1], v[2], v[3]);
+        f32x4 w;
+        w.x = v[0]; w.y = v[1]; w.z = v[2]; w.w = v[3];
+        gstore4(p + e, w);
     }
 };
 template <typename T> struct V4h {
+    __device__ static void bld(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float* o) {
+        const u32x2 q = bload2u(r, voff, soff);
+        uint2 raw;
+        raw.x = q.x; raw.y = q.y;
+        const T* h = reinterpret_cast<const T*>(&raw);
+        o[0] = to_f(h[0]); o[1] = to_f(h[1]); o[2] = to_f(h[2]); o[3] = to_f(h[3]);
+    }
+    __device__ static void bst(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const float* v) {
+        uint2 raw;
+        T* h = reinterpret_cast<T*>(&raw);
+        h[0] = from_w<T>(v[0]); h[1] = from_w<T>(v[1]); h[2] = from_w<T>(v[2]); h[3] = from_w<T>(v[3]);
+        u32x2 q;
+        q.x = raw.x; q.y = raw.y;
+        bstore2u(r, voff, soff, q);
+    }
     __device__ static void ld(const T* p, int64_t e, float* o) {
-        uint2 raw = *reinterpret_cast<const uint2*>(p + e);
+        const u32x2 r = gload2u(p + e);
+        uint2 raw;
+        raw.x = r.x; raw.y = r.y;
         const T* h = reinterpret_cast<const T*>(&raw);
         o[0] = to_f(h[0]); o[1] = to_f(h[1]); o[2] = to_f(h[2]); o[3] = to_f(h[3]);
     }
@@ -85,11 +131,26 @@ template <typename T> struct V4h {
         uint2 raw;
         T* h = reinterpret_cast<T*>(&raw);
         h[0] = from_w<T>(v[0]); h[1] = from_w<T>(v[1]); h[2] = from_w<T>(v[2]); h[3] = from_w<T>(v[3]);
-        *reinterpret_cast<uint2*>(p + e) = raw;
+        u32x2 r;
+        r.x = raw.x; r.y = raw.y;
+        gstore2u(p + e, r);
     }
 };
 template <> struct V4<__half> : V4h<__half> {};
 template <> struct V4<__hip_bfloat16> : V4h<__hip_bfloat16> {};
+
+// Sum over aligned groups of G lanes (G a power of two <= 64), pairing lanes
+// xor 1, 2, 4, ... in that order: xor 1 and 2 by DPP quad permutes, wider by
+// shuffles (only when a group spans more than 4 lanes).
+__device__ __forceinline__ float lanes_group_sum(float v, int G) {
+    float o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += G > 1 ? o : 0.0f;
+    o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += G > 2 ? o : 0.0f;
+    if (G > 4)
+        for (int m = 4; m < G; m <<= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
 
 // ---- shared scalar math (work dtype W) ------------------------------------
 template <typename W> __device__ __forceinline__ W reservoir(W old, W cur, double decay, int step) {
@@ -187,7 +248,14 @@ __device__ DriveCoef<W> contact_and_coefs(const double* M, double dn, const cres
 // ---------------------------------------------------------------------------
 // register-resident kernel (2D, <= 64 Ki elements, float4-aligned)
 // ---------------------------------------------------------------------------
-template <typename PT, typename GT, int LAYOUT>
+// FAST: numel is exactly SR_NT*SR_SLOTS*4 (65536, e.g. (4096,16) and
+// (16,4096)), so every slot of every thread is valid with no guard at all and
+// the loads of a pass are all in flight together, and the options that add
+// per-element work are off (weight decay, local sharpness, an instant-metric
+// power other than 1).  The drive shaping then
+// runs on |t| (shape3a): the moments need no signs, and the drive takes the
+// sign of t once.
+template <typename PT, typename GT, int LAYOUT, bool FAST>
 __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec* __restrict__ recs,
                                                                  int32_t* __restrict__ steps,
                                                                  const void* const* __restrict__ grads, int32_t first,
@@ -203,12 +271,15 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
     const int64_t n = R.d.numel;
     const int64_t rows = R.rows;
     const int C0 = (int)R.cols;
-    const int G = R.group;
+    const int G = R.group;                        // ROWGROUP: a power of two <= 64
+    const int lgG = G > 0 ? __builtin_ctz(G) : 0;
     const float eps = (float)h.eps;
     float* sp[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) sp[i] = reinterpret_cast<float*>(R.d.state[i]);
-    float q0 = *sp[0], imp = *sp[1], mq = *sp[2], mp = *sp[3], fr = *sp[4], de = *sp[5], sur = *sp[6], act = *sp[7];
+    // uniform state: scalar loads into SGPRs (issued together, no VGPRs held)
+    float q0 = ld_uniform(sp[0]), imp = ld_uniform(sp[1]), mq = ld_uniform(sp[2]), mp = ld_uniform(sp[3]);
+    float fr = ld_uniform(sp[4]), de = ld_uniform(sp[5]), sur = ld_uniform(sp[6]), act = ld_uniform(sp[7]);
     if (tid == 0) {
         const int s = steps[ri] + 1;
         steps[ri] = s;
@@ -244,12 +315,26 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
     };
     auto e0_of = [&](int k) -> int64_t { return ((int64_t)k * SR_NT + tid) * 4; };
 
+    // FAST: buffer views of grad and param (byte offsets fit in 32 bits)
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, FAST ? (uint32_t)(n * (int64_t)sizeof(GT)) : 0u);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p, FAST ? (uint32_t)(n * (int64_t)sizeof(PT)) : 0u);
+    const uint32_t vog = (uint32_t)(tid * 4 * sizeof(GT)), vop = (uint32_t)(tid * 4 * sizeof(PT));
+
     // ---- pass A ----
     float a_ff = 0.f;
 #pragma unroll
     for (int k = 0; k < SR_SLOTS; ++k) {
         const int64_t e0 = e0_of(k);
         float v[4];
+        if constexpr (FAST) {
+            // the raw grad is kept: maximize (force = -grad) enters pass C as
+            // the sign of the denominator, the only place the force's sign is used
+            V4<GT>::bld(rg, vog, (uint32_t)(k * SR_NT * 4 * sizeof(GT)), v);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a_ff = fmaf(v[c], v[c], a_ff);
+            stx(k, v);
+            continue;
+        }
         if (e0 < n) {
             V4<GT>::ld(g, e0, v);
             if (h.maximize) {
@@ -293,41 +378,70 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
     float a_L = 0.f, a_dens = 0.f;
 #pragma unroll
     for (int k = 0; k < SR_SLOTS; ++k) {
-        const bool ok = e0_of(k) < n;
+        const bool ok = FAST || e0_of(k) < n;
         float rs = 0.f;
-        float xk[4];
-        ldx(k, xk);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float r = fabsf(xk[c]) * inv_s + eps;
-            const float L = flog1p(fpow(r, pw));
-            const float rl = fmaxf(fminf(r, 1.0e4f), eps);
-            const float dens = fminf(ip_one ? rl : fpow(rl, ipw), 1.0e6f);
+        if constexpr (FAST) {
+            // a_L sums log2(1 + r^p) (scaled by ln 2 after the block sum);
+            // r >= eps, so the instant density is min(r, 1e4)
             if (ok) {
-                a_L += L;
-                a_dens += dens;
-                rs += dens;
-                colacc[c] += dens;
+                float xk[4];
+                ldx(k, xk);
+                pin4(xk);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float r = fmaf(fabsf(xk[c]), inv_s, eps);
+                    a_L += flog2(1.0f + fexp2(pw * flog2(r)));
+                    const float dens = fminf(r, 1.0e4f);
+                    rs += dens;
+                    colacc[c] += dens;
+                    sched_fence();
+                }
+                pin1(a_L);
+                a_dens += rs;
             }
-            sched_fence();
+        } else {
+            float xk[4];
+            ldx(k, xk);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float r = fabsf(xk[c]) * inv_s + eps;
+                const float L = flog1p(fpow(r, pw));
+                const float rl = fmaxf(fminf(r, 1.0e4f), eps);
+                const float dens = fminf(ip_one ? rl : fpow(rl, ipw), 1.0e6f);
+                if (ok) {
+                    a_L += L;
+                    a_dens += dens;
+                    rs += dens;
+                    colacc[c] += dens;
+                }
+                sched_fence();
+            }
         }
         if (LAYOUT == L_ROWGROUP) {
-            // butterfly over the G lanes of a row: xor 1 and 2 by DPP quad
-            // permutes (same pairings as the lane shuffles), wider by shuffles
-            if (G >= 2) rs += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, rs), 0xB1, 0xF, 0xF, false));
-            if (G >= 4) rs += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, rs), 0x4E, 0xF, 0xF, false));
-            for (int m = 4; m < G; m <<= 1) rs += __shfl_xor(rs, m, 64);
-            const int64_t row = ((int64_t)k * SR_NT + tid) / G;
-            if (ok && (tid % G) == 0) rowfac[row] = rs;
+            rs = lanes_group_sum(rs, G);
+            const int row = (k * SR_NT + tid) >> lgG;
+            if (ok && (tid & (G - 1)) == 0) rowfac[row] = rs;
+        } else if (FAST) {
+            // the row of slot k is the whole block: its wave totals now (fp64,
+            // DPP), summed over the waves after the pass
+            const double w = wave_total_d((double)rs);
+            if (lane == 63) red[(tid >> 6) * SR_SLOTS + k] = w;
         } else {
             slotrow[k] = rs;
         }
+    }
+    double rowsum = 0.0;   // FAST COLBLOCK: density sum of row tid (threads < SR_SLOTS)
+    if (FAST && LAYOUT == L_COLBLOCK) {
+        __syncthreads();
+        if (tid < SR_SLOTS)
+            for (int w = 0; w < SR_NT / 64; ++w) rowsum += red[w * SR_SLOTS + tid];
+        __syncthreads();   // red is reused by the next block sum
     }
     double gmean;
     {
         double v[2] = {(double)a_L, (double)a_dens};
         block_sum<2>(v, red);
-        const float dens_mean = (float)(v[0] / dn);
+        const float dens_mean = (float)((FAST ? v[0] * 0.6931471805599453 : v[0]) / dn);
         gmean = v[1] / dn;
         // scalar metric oscillator (cresso_v5.py:1510-1518)
         const float mport = dens_mean - tanhf(mq);
@@ -365,16 +479,19 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
             rowfac[i] = expf(kappa * logf(fmaxf(rm / gden, eps)));
         }
         __syncthreads();
-        const int cg = tid % G;
+        const int cg = tid & (G - 1);
 #pragma unroll
         for (int c = 0; c < 4; ++c) Ec[c] = colfac[cg * 4 + c];
     } else {
-        double v[SR_SLOTS];
+        if (!FAST) {
+            double v[SR_SLOTS];
 #pragma unroll
-        for (int k = 0; k < SR_SLOTS; ++k) v[k] = (double)slotrow[k];
-        block_sum<SR_SLOTS>(v, red);
+            for (int k = 0; k < SR_SLOTS; ++k) v[k] = (double)slotrow[k];
+            block_sum<SR_SLOTS>(v, red);
+            if (tid < SR_SLOTS) rowsum = v[tid];
+        }
         if (tid < SR_SLOTS && tid < rows) {
-            const float rm = (float)(v[tid] / (double)C0);
+            const float rm = (float)(rowsum / (double)C0);
             rowfac[tid] = expf(kappa * logf(fmaxf(rm / gden, eps)));
         }
 #pragma unroll
@@ -392,13 +509,42 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
     const float clip = uni((float)h.drive_clip);
     const float iclip = uni(1.0f / clip);
     const float clip2 = uni(clip * clip);
+    const float k2 = uni(-2.8853900817779268f * iclip);   // -2 log2(e) / clip
+    // FAST keeps the raw grad: f / den = grad / (sign * den) with sign = -1 under maximize
+    const float sMs = uni(h.maximize ? -sM : sM), epss = uni(h.maximize ? -eps : eps);
     float m[13];
 #pragma unroll
     for (int i = 0; i < 13; ++i) m[i] = 0.f;
 #pragma unroll
     for (int k = 0; k < SR_SLOTS; ++k) {
-        const bool ok = e0_of(k) < n;
-        const int64_t row = LAYOUT == L_ROWGROUP ? ((int64_t)k * SR_NT + tid) / G : (int64_t)k;
+        const bool ok = FAST || e0_of(k) < n;
+        const int row = LAYOUT == L_ROWGROUP ? (k * SR_NT + tid) >> lgG : k;
+        if constexpr (FAST) {
+            if (ok) {
+                const float Er = rowfac[row];
+                float xk[4];
+                ldx(k, xk);
+                pin4(xk);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float inst = med3f(Er * Ec[c], 0.08f, 12.0f);
+                    const float t = med3f(xk[c] * frcp(fmaf(sMs, inst, epss)), -1.0e4f, 1.0e4f);
+                    xk[c] = t;
+                    const float at = fabsf(t);
+                    const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+                    const float e = t - q0;
+                    m[0] += e; m[1] = fmaf(e, e, m[1]); m[2] += t; m[3] = fmaf(t, t, m[3]);
+                    m[4] = fmaf(z.rat, z.rat, m[4]); m[5] = fmaf(z.th, z.th, m[5]); m[6] = fmaf(z.root, z.root, m[6]);
+                    m[7] = fmaf(z.rat, z.th, m[7]); m[8] = fmaf(z.rat, z.root, m[8]); m[9] = fmaf(z.th, z.root, m[9]);
+                    m[10] = fmaf(at, z.rat, m[10]); m[11] = fmaf(at, z.th, m[11]); m[12] = fmaf(at, z.root, m[12]);
+                    sched_fence();
+                }
+#pragma unroll
+                for (int i = 0; i < 13; ++i) pin1(m[i]);
+                stx(k, xk);
+            }
+            continue;
+        }
         const float Er = ok ? rowfac[row] : 1.0f;
         float xk[4];
         ldx(k, xk);
@@ -430,15 +576,54 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
 #pragma unroll
     for (int i = 0; i < 13; ++i) M[i] = (double)m[i];
     block_sum<13>(M, red);
+    if (FAST) {
+        // the FAST sums hold |tanh| where the moments need bnd = clip tanh
+        const double dc_ = (double)clip;
+        M[5] *= dc_ * dc_;
+        M[7] *= dc_;
+        M[9] *= dc_;
+        M[11] *= dc_;
+    }
     const DriveCoef<float> dc = contact_and_coefs<float>(M, dn, h, step, q0, imp, act, sur);
 
     // ---- pass D ----
     const float q1 = uni(dc.q1), cA = uni(dc.cA), cB = uni(dc.cB), cN = uni(dc.cN), cD = uni(dc.cD);
     const float cr = uni(dc.cr), cb = uni(dc.cb), co = uni(dc.co), ct = uni(dc.ct), ns = uni(dc.nscale);
+    // FAST coefficients: cA folded into the core weights, clip into the tanh weights
+    const float kr = uni(cA * cr), kb = uni(cA * (cb * clip)), ko = uni(cA * co), kt = uni(cA * ct);
+    const float kN = uni(cN * clip), k2n = uni(-2.8853900817779268f * ns);
     float a_dd = 0.f;
 #pragma unroll
     for (int k = 0; k < SR_SLOTS; ++k) {
-        const bool ok = e0_of(k) < n;
+        const bool ok = FAST || e0_of(k) < n;
+        if constexpr (FAST) {
+            // drive = sign(t) (kr|rat| + kb|tanh| + ko|root| + kt|t|) + kB + kN tanh(e ns) + kD e
+            if (ok) {
+                float xk[4];
+                ldx(k, xk);
+                pin4(xk);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float t = xk[c];
+                    const float at = fabsf(t);
+                    const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+                    const float cm = fmaf(kt, at, fmaf(ko, z.root, fmaf(kb, z.th, kr * z.rat)));
+                    const float core = __builtin_bit_cast(
+                        float, __builtin_bit_cast(uint32_t, cm) ^ (__builtin_bit_cast(uint32_t, t) & 0x80000000u));
+                    const float e = t - q1;
+                    const float ex = fexp2(k2n * fabsf(e));
+                    const float ri = frcp(1.0f + ex);
+                    const float nov = with_sign(fmaf(-ex, ri, ri), e);
+                    const float drv = fmaf(kN, nov, fmaf(cD, e, core + cB));
+                    xk[c] = drv;
+                    a_dd = fmaf(drv, drv, a_dd);
+                    sched_fence();
+                }
+                pin1(a_dd);
+                stx(k, xk);
+            }
+            continue;
+        }
         float xk[4];
         ldx(k, xk);
 #pragma unroll
@@ -465,8 +650,37 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
 
     // ---- pass E ----
     const float nlr = uni((float)(-h.lr));
+    if constexpr (FAST) {
+        // groups of 4 slots; the param loads of group j+1 are issued before
+        // group j is updated (two groups of loads in flight, bounded registers)
+        constexpr int GS = 4, NG = SR_SLOTS / GS;
+        float pv[2][GS][4];
+        auto issue = [&](int j) {
+#pragma unroll
+            for (int i = 0; i < GS; ++i)
+                V4<PT>::bld(rp, vop, (uint32_t)((j * GS + i) * SR_NT * 4 * sizeof(PT)), pv[j & 1][i]);
+        };
+        issue(0);
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            if (j + 1 < NG) issue(j + 1);
+            sched_fence();
+#pragma unroll
+            for (int i = 0; i < GS; ++i) {
+                const int k = j * GS + i;
+                float xk[4];
+                ldx(k, xk);
+                float* pp = pv[j & 1][i];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) pp[c] = pp[c] + nlr * to_f(from_w<PT>(xk[c] * gain));
+                V4<PT>::bst(rp, vop, (uint32_t)(k * SR_NT * 4 * sizeof(PT)), pp);
+            }
+            sched_fence();
+        }
+    }
 #pragma unroll
     for (int k = 0; k < SR_SLOTS; ++k) {
+        if (FAST) break;
         const int64_t e0 = e0_of(k);
         if (e0 < n) {
             float pv[4], xk[4];
@@ -676,8 +890,14 @@ bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 struct Variant {
     int pt, gt, kind;   // kind: 0 stream, 1 resident ROWGROUP, 2 resident COLBLOCK
-    bool operator==(const Variant& o) const { return pt == o.pt && gt == o.gt && kind == o.kind; }
+    bool full;          // resident with numel == SR_RESIDENT_MAX: eligible for the FAST kernel
+    bool operator==(const Variant& o) const { return pt == o.pt && gt == o.gt && kind == o.kind && full == o.full; }
 };
+
+// The FAST resident kernel skips the per-element work of these options.
+bool fast_hyper(const cresso_hyper& h) {
+    return h.weight_decay == 0.0 && h.local_sharpness == 0.0 && (float)fmax(h.instant_metric_power, 0.25) == 1.0f;
+}
 
 int dtype_bytes(int t) { return t == CRESSO_F64 ? 8 : (t == CRESSO_F32 ? 4 : 2); }
 
@@ -752,36 +972,39 @@ int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec&
         }
     }
     r.resident = kind != 0;
-    v = Variant{d.param_dtype, d.grad_dtype, kind};
+    v = Variant{d.param_dtype, d.grad_dtype, kind, kind != 0 && n == SR_RESIDENT_MAX};
     return CRESSO_OK;
 }
 
 // The resident kernels use more than 64 KiB of dynamic LDS: raise the
 // function's limit once (thread-safe static initialisation).
-template <typename PT, typename GT, int LAYOUT>
+template <typename PT, typename GT, int LAYOUT, bool FAST>
 hipError_t allow_resident_lds() {
     static const hipError_t e =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&scalar_resident_kernel<PT, GT, LAYOUT>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&scalar_resident_kernel<PT, GT, LAYOUT, FAST>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)SR_LDS_MAX);
     return e;
 }
 
-template <typename PT, typename GT>
-hipError_t launch_resident(int kind, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
-                           int32_t cnt, size_t lds, const cresso_hyper& h, hipStream_t s) {
-    if (lds > SR_LDS_MAX) return hipErrorInvalidValue;
-    if (kind == 1) {
-        const hipError_t e = allow_resident_lds<PT, GT, L_ROWGROUP>();
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, L_ROWGROUP>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads,
-                           first, h);
-    } else {
-        const hipError_t e = allow_resident_lds<PT, GT, L_COLBLOCK>();
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, L_COLBLOCK>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads,
-                           first, h);
-    }
+template <typename PT, typename GT, int LAYOUT, bool FAST>
+hipError_t launch_resident_v(const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first, int32_t cnt,
+                             size_t lds, const cresso_hyper& h, hipStream_t s) {
+    const hipError_t e = allow_resident_lds<PT, GT, LAYOUT, FAST>();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, LAYOUT, FAST>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads,
+                       first, h);
     return hipGetLastError();
+}
+
+template <typename PT, typename GT>
+hipError_t launch_resident(int kind, bool fast, const ScalarRec* recs, int32_t* steps, const void* const* grads,
+                           int32_t first, int32_t cnt, size_t lds, const cresso_hyper& h, hipStream_t s) {
+    if (lds > SR_LDS_MAX) return hipErrorInvalidValue;
+    if (kind == 1)
+        return fast ? launch_resident_v<PT, GT, L_ROWGROUP, true>(recs, steps, grads, first, cnt, lds, h, s)
+                    : launch_resident_v<PT, GT, L_ROWGROUP, false>(recs, steps, grads, first, cnt, lds, h, s);
+    return fast ? launch_resident_v<PT, GT, L_COLBLOCK, true>(recs, steps, grads, first, cnt, lds, h, s)
+                : launch_resident_v<PT, GT, L_COLBLOCK, false>(recs, steps, grads, first, cnt, lds, h, s);
 }
 
 template <typename W, typename PT, typename GT>
@@ -794,9 +1017,11 @@ hipError_t launch_stream(const ScalarRec* recs, int32_t* steps, const void* cons
 hipError_t dispatch(const Variant& v, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
                     int32_t cnt, size_t lds, unsigned char* table, const cresso_hyper& h, hipStream_t s) {
     if (v.kind != 0) {
-        if (v.pt == CRESSO_F32) return launch_resident<float, float>(v.kind, recs, steps, grads, first, cnt, lds, h, s);
-        if (v.pt == CRESSO_BF16) return launch_resident<__hip_bfloat16, __hip_bfloat16>(v.kind, recs, steps, grads, first, cnt, lds, h, s);
-        if (v.pt == CRESSO_F16) return launch_resident<__half, __half>(v.kind, recs, steps, grads, first, cnt, lds, h, s);
+        const bool fast = v.full && fast_hyper(h);
+        if (v.pt == CRESSO_F32) return launch_resident<float, float>(v.kind, fast, recs, steps, grads, first, cnt, lds, h, s);
+        if (v.pt == CRESSO_BF16)
+            return launch_resident<__hip_bfloat16, __hip_bfloat16>(v.kind, fast, recs, steps, grads, first, cnt, lds, h, s);
+        if (v.pt == CRESSO_F16) return launch_resident<__half, __half>(v.kind, fast, recs, steps, grads, first, cnt, lds, h, s);
         return hipErrorInvalidValue;
     }
 #define CRESSO_SR_CASE(PC, GC, W, PT, GT) \

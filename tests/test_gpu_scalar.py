@@ -10,7 +10,11 @@ pytestmark = [pytest.mark.gpu, needs_gpu]
 SCALAR_KW = dict(lr=2e-3, rank=4, hash_bins=64, hash_tables=2)
 
 
-@pytest.mark.parametrize("shape", [(4096, 16), (16, 4096), (128, 16), (16, 300), (64, 16), (1024, 64), (256, 4)])
+# (4096,16), (16,4096), (1024,64): every thread holds 16 float4 slots (the fast
+# resident kernel); (1024,16), (2048,8), (8,4096): the fast kernel with 4, 4
+# and 8 slots; (128,16), (64,16), (256,4): the general resident kernel
+@pytest.mark.parametrize("shape", [(4096, 16), (16, 4096), (128, 16), (16, 300), (64, 16), (1024, 64), (256, 4),
+                                   (1024, 16), (2048, 8), (8, 4096)])
 def test_scalar_2d_matches_oracle(shape):
     announce(f"scalar 2d {shape}")
     res = run_pair([shape], torch.float32, SCALAR_KW, steps=4, seed=1)
@@ -31,6 +35,47 @@ def test_scalar_options_maximize_local_sharpness_no_warmup():
     kw = dict(SCALAR_KW, maximize=True, local_sharpness=0.3, warmup_steps=0, instant_metric_power=1.5)
     res = run_pair([(4096, 16), (16, 4096), (300,)], torch.float32, kw, steps=3, seed=3)
     compare(*res)
+
+
+def test_scalar_maximize_fast_kernel():
+    # maximize alone keeps the fast resident kernel (the force is -grad)
+    announce("scalar maximize fast")
+    kw = dict(SCALAR_KW, maximize=True, warmup_steps=0)
+    res = run_pair([(4096, 16), (16, 4096), (1024, 16)], torch.float32, kw, steps=3, seed=10)
+    compare(*res)
+
+
+def test_scalar_exact_zero_gradients():
+    # rows and single entries of exactly zero grad: t == 0 there, where the
+    # root channel sign(t) sqrt(min(|t|, clip^2) + eps) is 0, not sqrt(eps)
+    announce("scalar exact zeros")
+    import cresso_amd
+    from oracle.cresso_oracle import OracleCRESSO5
+    import numpy as np
+
+    gen = torch.Generator().manual_seed(11)
+    shapes = [(4096, 16), (16, 4096), (128, 16)]
+    p0 = [0.05 * torch.randn(s, generator=gen) for s in shapes]
+    gs = []
+    for _ in range(3):
+        step = []
+        for s in shapes:
+            g = 1e-2 * torch.randn(s, generator=gen)
+            g[::3] = 0.0
+            g[torch.rand(s, generator=gen) < 0.2] = 0.0
+            step.append(g)
+        gs.append(step)
+    hp = [torch.nn.Parameter(p.clone().cuda()) for p in p0]
+    op = [p.clone() for p in p0]
+    hopt = cresso_amd.CRESSO5(hp, cuda_ops="required", **SCALAR_KW)
+    oopt = OracleCRESSO5(op, **SCALAR_KW)
+    for step in gs:
+        for p, g in zip(hp, step):
+            p.grad = g.cuda()
+        hopt.step()
+        oopt.step(step)
+    torch.cuda.synchronize()
+    compare(hp, hopt, op, oopt)
 
 
 def test_scalar_tiny_gradients_eps_dominated():
