@@ -81,12 +81,36 @@ __device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff,
 __device__ __forceinline__ void bstore4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, f32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff + soff, 0, 0);
 }
+__device__ __forceinline__ float bload1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t bload1u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+__device__ __forceinline__ void bstore1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff + soff, 0, 0);
+}
 __device__ __forceinline__ u32x2 bload2u(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
 }
 __device__ __forceinline__ void bstore2u(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, u32x2 v) {
     __builtin_amdgcn_raw_buffer_store_b64(v, r, voff + soff, 0, 0);
 }
+
+// ---------------------------------------------------------------------------
+// Program-order pins.  sched_barrier only orders the machine scheduler; IR
+// passes still hoist cheap per-element math of many elements ahead of the
+// transcendental chains, or sink accumulations to the end of a loop with
+// every element's inputs kept alive, and the kernel spills.  An empty asm that
+// reads and writes a value fixes the point where it is materialized:
+//  * pin4 on a slot's inputs: nothing that depends on them moves above it;
+//  * pin1 on an accumulator at the end of a slot or row: its contributions
+//    are complete there.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void pin4(float* v) {
+    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+}
+__device__ __forceinline__ void pin1(float& v) { asm volatile("" : "+v"(v)); }
 
 // ---------------------------------------------------------------------------
 // fast per-element math (hardware approximations, ~1 ulp on their domain)
@@ -113,6 +137,16 @@ __device__ __forceinline__ float clampf(float x, float lo, float hi) { return fm
 __device__ __forceinline__ float med3f(float x, float lo, float hi) { return __builtin_amdgcn_fmed3f(x, lo, hi); }
 // |m| with the sign of s (one bitfield insert)
 __device__ __forceinline__ float with_sign(float m, float s) { return copysignf(m, s); }
+// m times the sign of s (+-1; m unchanged for s = +0): flips the sign bit
+__device__ __forceinline__ float xorsign(float m, float s) {
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, m) ^ (__builtin_bit_cast(uint32_t, s) & 0x80000000u));
+}
+// tanh(c x) given k2 = -2 log2(e) c (c > 0): exp(-2c|x|) by one exp2
+__device__ __forceinline__ float ftanh_k(float x, float k2) {
+    const float ex = fexp2(k2 * fabsf(x));
+    const float r = frcp(1.0f + ex);
+    return copysignf(fmaf(-ex, r, r), x);
+}
 
 // Unsigned parts of the drive shaping of t (cresso_v5.py:1321-1324, scalar
 // route 1563-1566) from at = |t|:

@@ -69,17 +69,7 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 __device__ __forceinline__ float ld_uniform(const float* p) {
     return *(const __attribute__((address_space(4))) float*)p;
 }
-// Pins four values in VGPRs at this point of the program: work that depends on
-// them cannot be hoisted above it, so each slot's arithmetic stays in its own
-// region (without this, IR passes move the cheap per-element math of all 16
-// slots ahead of the transcendental chains and the kernel spills).
-__device__ __forceinline__ void pin4(float* v) {
-    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
-}
-// The same for an accumulator at the end of a slot: the slot's contributions
-// are complete here (otherwise they may be sunk to the end of the pass, with
-// every slot's inputs kept alive until then).
-__device__ __forceinline__ void pin1(float& v) { asm volatile("" : "+v"(v)); }
+
 
 // ---- vector access -------------------------------------------------------
 template <typename T> struct V4;
@@ -608,8 +598,7 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
                     const float at = fabsf(t);
                     const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
                     const float cm = fmaf(kt, at, fmaf(ko, z.root, fmaf(kb, z.th, kr * z.rat)));
-                    const float core = __builtin_bit_cast(
-                        float, __builtin_bit_cast(uint32_t, cm) ^ (__builtin_bit_cast(uint32_t, t) & 0x80000000u));
+                    const float core = xorsign(cm, t);
                     const float e = t - q1;
                     const float ex = fexp2(k2n * fabsf(e));
                     const float ri = frcp(1.0f + ex);

@@ -118,7 +118,7 @@ struct SpecState {
 };
 
 constexpr int NV2 = 2 + 2 * SP_MAXR;            // sum L, sum dens, proj L (C,S)
-constexpr int NV3 = 15 + 4 * SP_MAXR;           // see sweep3
+constexpr int NV3 = 15 + 2 * SP_MAXR;           // see sweep3
 constexpr int NV4 = 3;                          // sum d^2, sum d hp, sum hp^2
 constexpr int NVMAX = NV3;
 
@@ -579,22 +579,6 @@ __device__ __forceinline__ unsigned long long to_fixed_s(float x) {
     return x < 0.f ? (0ull - u) : u;
 }
 
-// rat = t/(1+|t|/clip), ths = tanh(t/clip) (bnd = clip ths),
-// root = sign(t)*sqrt(min(|t|,clip^2)+eps) (cresso_v5.py:1321-1324); rat and
-// ths share one reciprocal.
-__device__ __forceinline__ void shape3f(float t, float iclip, float clip2, float eps, float& rat, float& ths,
-                                        float& root) {
-    const float at = fabsf(t);
-    const float ex = fexp2(-2.8853900817779268f * at * iclip);
-    const float d1 = 1.0f + ex;
-    const float d2 = 1.0f + at * iclip;
-    const float inv = frcp(d1 * d2);
-    const float th = (1.0f - ex) * d2 * inv;
-    ths = copysignf(th, t);
-    rat = t * d1 * inv;
-    root = fsign(t) * fsqrt(fminf(at, clip2) + eps);
-}
-
 __device__ __forceinline__ float reservoir_f(float old, float cur, double decay, int step) {
     if (step <= 1) return cur;
     return old * (float)decay + (float)(1.0 - decay) * cur;
@@ -761,6 +745,50 @@ __device__ __forceinline__ void load_cols(const Geom& g, const float* __restrict
     for (int k = 0; k < KC; ++k) b[k] = t.colok ? coltab[(size_t)k * g.cols + t.col] : 0.f;
 }
 
+// Row coefficients of two reconstructions in the column-carrier form
+//   recon(row, col) = c + sum_k alpha_k(row) b_k(col)
+// (b_k: the lane's column carriers, b_0 = 1), for the block's nr rows: the
+// per-lane form sum_q a_q(row) gamma_q(col) has 2R terms, this one K.  Set
+// j's mode coefficients are w0[j] rc0[j] + w1[j] rc1[j] (rc1 may be null).
+// Out: s_al[lr][j][k], row stride 2 * KCP (KCP = KC rounded up to 4).
+template <int KC> constexpr int kcp() { return (KC + 3) & ~3; }
+// byte offset of sweep 3's row coefficients in its dynamic LDS
+__host__ __device__ inline size_t lds_al_off(const Geom& g) {
+    const size_t head = (sizeof(unsigned long long) + sizeof(float)) * (size_t)g.T * g.B + sizeof(float) * (size_t)g.PR;
+    return (head + 15) & ~(size_t)15;
+}
+template <int RM, int KC>
+__device__ void alpha_rows(const Geom& g, const ModeMeta* __restrict__ meta, const float* __restrict__ rt, int nr,
+                           const float (*const rc0[2])[2], const float w0[2], const float (*const rc1[2])[2],
+                           const float w1[2], float* __restrict__ s_al) {
+    constexpr int KP = kcp<KC>();
+    for (int e = threadIdx.x; e < nr * 2 * KP; e += blockDim.x) {
+        const int lr = e / (2 * KP), rem = e - lr * 2 * KP, j = rem / KP, k = rem - j * KP;
+        const float* __restrict__ ar = rt + lr * g.RW;
+        float a = 0.f;
+        if (k < KC) {
+            for (int r = 0; r < g.R; ++r) {
+                const ModeMeta m = meta[r];
+                if (m.k1 != k && m.k2 != k) continue;
+                float wc = w0[j] * rc0[j][r][0], ws = w0[j] * rc0[j][r][1];
+                if (rc1[j]) {
+                    wc += w1[j] * rc1[j][r][0];
+                    ws += w1[j] * rc1[j][r][1];
+                }
+                const float a1 = ar[2 * r], a2 = ar[2 * r + 1];
+                if (m.type == M_ADD) {   // coefficient of a1: wc b1 + ws b2; of a2: ws b1 - wc b2
+                    if (m.k1 == k) a += wc * a1 + ws * a2;
+                    if (m.k2 == k) a += ws * a1 - wc * a2;
+                } else {                 // a1 wc b1 + a2 ws b2
+                    if (m.k1 == k) a += wc * a1;
+                    if (m.k2 == k) a += ws * a2;
+                }
+            }
+        }
+        s_al[e] = a;
+    }
+}
+
 // Lane contribution of a projection: Z[2q] = sum over the lane's rows of
 // a1_q(row) x, Z[2q+1] = the same with a2_q; combined with the lane's column
 // carriers into the raw C/S projections of every mode, partial slots
@@ -822,6 +850,102 @@ __device__ __forceinline__ uint64_t load_bins_at(const unsigned char* __restrict
     }
 }
 
+// Panel arrays of a full tile as buffer views: one descriptor per array (the
+// panel's first element as base), the lane's column as the VGPR offset and the
+// row as a uniform SGPR offset, so the row loop needs no address arithmetic.
+// Byte sizes stay below 2^31 (the planner keeps PR * cols below 2^29).
+struct PanelBuf {
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t lane;   // byte offset of the lane's column
+    uint32_t row;    // bytes per row
+};
+template <typename T>
+__device__ __forceinline__ PanelBuf panel_buf(const T* panel0, const Geom& g, int nr) {
+    PanelBuf b;
+    b.r = make_rsrc(panel0, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(T)));
+    b.lane = (uint32_t)(threadIdx.x * sizeof(T));
+    b.row = (uint32_t)(g.cols * sizeof(T));
+    return b;
+}
+template <typename T> __device__ __forceinline__ float ldb_lane(const PanelBuf& b, int lr);
+template <> __device__ __forceinline__ float ldb_lane<float>(const PanelBuf& b, int lr) {
+    return bload1(b.r, b.lane, (uint32_t)lr * b.row);
+}
+template <> __device__ __forceinline__ float ldb_lane<__half>(const PanelBuf& b, int lr) {
+    return to_f(__builtin_bit_cast(__half, (unsigned short)bload1u16(b.r, b.lane, (uint32_t)lr * b.row)));
+}
+template <> __device__ __forceinline__ float ldb_lane<__hip_bfloat16>(const PanelBuf& b, int lr) {
+    return to_f(__builtin_bit_cast(__hip_bfloat16, (unsigned short)bload1u16(b.r, b.lane, (uint32_t)lr * b.row)));
+}
+__device__ __forceinline__ uint32_t ldb_bins16(const PanelBuf& b, int lr) {
+    return bload1u16(b.r, b.lane, (uint32_t)lr * b.row);
+}
+__device__ __forceinline__ void stb_lane(const PanelBuf& b, int lr, float v) {
+    bstore1(b.r, b.lane, (uint32_t)lr * b.row, v);
+}
+
+// Rows of a full panel in batches of U: the loads of batch i+1 are issued
+// before batch i is processed (two register sets, no copies).  nr is a
+// multiple of 2U.  load(lr, x, b) loads row lr's lane values, body(lr, x, b)
+// processes them.
+// The same with a per-batch body: batch(i0, x[U], b[U]) processes rows i0..i0+U-1.
+template <int U, typename Load, typename Batch>
+__device__ __forceinline__ void pipelined_batches(int nr, Load&& load, Batch&& batch) {
+    float xa[U], xb[U];
+    uint32_t ba[U], bb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load(u, xa[u], ba[u]);
+    for (int i0 = 0; i0 < nr; i0 += 2 * U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) load(i0 + U + u, xb[u], bb[u]);
+        batch(i0, xa, ba);
+        if (i0 + 2 * U < nr) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) load(i0 + 2 * U + u, xa[u], ba[u]);
+        }
+        batch(i0 + U, xb, bb);
+    }
+}
+template <int U, typename Load, typename Body>
+__device__ __forceinline__ void pipelined_rows(int nr, Load&& load, Body&& body) {
+    pipelined_batches<U>(nr, load, [&](int i0, const float* x, const uint32_t* b) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) body(i0 + u, x[u], b[u]);
+    });
+}
+
+// Sums of 8 per-lane values (rows i0..i0+7 of the lane's column) over the 16
+// lanes of each DPP row: lane l returns row (l & 7)'s partial (lanes l and
+// l ^ 8 hold the same sum).  Lanes pair xor 1, 2, 4 while the values halve
+// (each lane keeps the rows of its own bit and receives them from its
+// partner), then xor 8: 25 instructions instead of 8 full wave reductions.
+// DPP row_ror:n reads lane (l - n) mod 16, so xor 4 is ror 4 for lanes with
+// bit 2 set and ror 12 for the others.
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float rows8_lanesum16(const float (&v)[8]) {
+    const int l = threadIdx.x & 63;
+    const bool b0 = (l & 1) != 0, b1 = (l & 2) != 0, b2 = (l & 4) != 0;
+    float w4[4], w2[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float keep = b0 ? v[2 * j + 1] : v[2 * j], give = b0 ? v[2 * j] : v[2 * j + 1];
+        w4[j] = keep + dpp_mov<0xB1>(give);   // quad_perm [1,0,3,2]: xor 1
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float keep = b1 ? w4[2 * j + 1] : w4[2 * j], give = b1 ? w4[2 * j] : w4[2 * j + 1];
+        w2[j] = keep + dpp_mov<0x4E>(give);   // quad_perm [2,3,0,1]: xor 2
+    }
+    const float keep = b2 ? w2[1] : w2[0], give = b2 ? w2[0] : w2[1];
+    const float from_below = dpp_mov<0x124>(give);   // row_ror:4  -> lane l - 4
+    const float from_above = dpp_mov<0x12C>(give);   // row_ror:12 -> lane l + 4
+    float w1 = keep + (b2 ? from_below : from_above);
+    w1 += dpp_mov<0x128>(w1);                        // row_ror:8: xor 8
+    return w1;
+}
+
 // Sweep variants: MODE 1 is the common large-matrix case with every option
 // fixed at compile time (2-D tensor, instant metric on, two hash tables of at
 // most 256 bins, no weight decay, no local sharpness); MODE 0 handles every
@@ -844,9 +968,12 @@ __device__ __forceinline__ SweepFlags sweep_flags(const Geom& g, int hash_arg, i
     return f;
 }
 // whether a tensor's step can use MODE 1 (host side)
+// (MODE 1 also needs full tiles: every row of every panel and every lane's
+// column valid, and panels of a multiple of 2 SP_U rows for the row pipeline.)
 inline bool fast_mode(const Geom& g, int hash_on, int axes_on, const cresso_hyper& h) {
     return hash_on && axes_on && g.T == 2 && g.bpb == 1 && g.binbytes == 2 && !g.one_d && h.weight_decay == 0.0 &&
-           h.local_sharpness == 0.0;
+           h.local_sharpness == 0.0 && (float)fmax(h.instant_metric_power, 0.25) == 1.0f && g.rows % g.PR == 0 &&
+           g.cols % SP_NT == 0 && g.PR % (2 * SP_U) == 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -867,11 +994,18 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     const int B = g.B;
     const int TB = F.T * B;
     const int nr = (int)(t.r1 - t.r0);
-    // LDS: histogram [T][B] u64 | wave row sums [4][PR]
+    // LDS: histogram [T][B] u64 | row-sum partials [16][PR] (MODE 0: [4 waves][PR];
+    // MODE 1: [4 waves][4 DPP rows][PR]) | MODE 1 row factors [PR][RW]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
     float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
+    float* s_ar = s_wrow + 16 * g.PR;
     if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_hist[i] = 0ull;
+    if (MODE == 1)
+        for (int e = threadIdx.x; e < nr * RW; e += SP_NT) {
+            const int lr = e / RW, q = e - lr * RW;
+            s_ar[e] = rowtab[(t.r0 + lr) * g.RW + q];
+        }
     __syncthreads();
     const int64_t base = panel_base(g, t);
     const GT* __restrict__ gb = grad + base;
@@ -890,6 +1024,44 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     for (int q = 0; q < RW; ++q) Z[q] = 0.f;
     float aL = 0.f, aD = 0.f;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // Sums of log(1 + ds) are kept in log2 units (fin2 scales them by ln 2).
+    if constexpr (MODE == 1) {
+        // full tile: rel >= eps and instant-metric power 1, so the density is rel
+        const PanelBuf gbv = panel_buf(gb, g, nr);
+        const PanelBuf bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
+        pipelined_batches<SP_U>(
+            nr,
+            [&](int lr, float& x, uint32_t& b) {
+                x = ldb_lane<GT>(gbv, lr);
+                b = ldb_bins16(bnv, lr);
+            },
+            [&](int i0, const float* x, const uint32_t* bv) {
+                float dn[SP_U];
+#pragma unroll
+                for (int u = 0; u < SP_U; ++u) {
+                    const float rel = fminf(fmaf(fabsf(x[u]), inv_s, eps), 1.0e4f);
+                    const float ds = fexp2(pw * flog2(rel));
+                    const float L = flog2(1.0f + ds);
+                    dn[u] = rel;
+                    aL += L;
+                    aD += rel;
+                    const float* __restrict__ ar = s_ar + (i0 + u) * RW;
+#pragma unroll
+                    for (int q = 0; q < RW; ++q) Z[q] = fmaf(ar[q], L, Z[q]);
+                    const unsigned long long v = to_fixed_u(ds * hs);
+                    atomicAdd(&s_hist[bin_of(bv[u], 0, 1)], v);
+                    atomicAdd(&s_hist[B + bin_of(bv[u], 1, 1)], v);
+#pragma unroll
+                    for (int q = 0; q < RW; ++q) pin1(Z[q]);
+                    pin1(aL);
+                    pin1(aD);
+                    pin1(dn[u]);
+                    elem_fence();
+                }
+                const float rs = rows8_lanesum16(dn);
+                if ((lane & 8) == 0) s_wrow[((wave << 2) + (lane >> 4)) * g.PR + i0 + (lane & 7)] = rs;
+            });
+    } else
     for (int i0 = 0; i0 < nr; i0 += SP_U) {
         float gv[SP_U], pv[SP_U];
         uint64_t bv[SP_U];
@@ -915,7 +1087,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
                 if (F.wd_on) f = f + wd * pv[u];
                 const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
                 const float ds = fpow(rel, pw);
-                const float L = flog1p(ds);
+                const float L = flog2(1.0f + ds);
                 const float rl = fmaxf(rel, eps);
                 dens = fminf(ip_one ? rl : fpow(rl, ipw), 1.0e6f);
                 aL += L;
@@ -944,7 +1116,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
         // axis density sums: one fixed-point atomic per row of this slab and per column of this panel
         for (int lr = threadIdx.x; lr < nr; lr += SP_NT) {
             float s = 0.f;
-            for (int w = 0; w < SP_NT / 64; ++w) s += s_wrow[w * g.PR + lr];
+            for (int w = 0; w < (MODE == 1 ? 16 : SP_NT / 64); ++w) s += s_wrow[w * g.PR + lr];
             atomicAdd(&rowfx[t.r0 + lr], to_fixed_u(s * (float)g.hs_row));
         }
         if (t.colok) atomicAdd(&colfx[t.col], to_fixed_u(aD * (float)g.hs_col));
@@ -1047,6 +1219,9 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(Geom g, const ModeMeta* 
         else s_zero[r] = meta[r].type == M_ZERO;
     }
     load_sums(part, 2 + 2 * g.R, s_v);
+    // sweep 2 sums log(1 + ds) in log2 units
+    if (tid < 2 + 2 * g.R && tid != 1) s_v[tid] *= 0.6931471805599453;
+    __syncthreads();
     // hash energy per table (cresso_v5.py:1012-1056)
     if (hash_on) {
         const int TB = g.T * g.B;
@@ -1192,6 +1367,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     const int TB = F.T * B;
     const int nr = (int)(t.r1 - t.r0);
     // LDS: histogram [T][B] u64 | log hash metric [T][B] | row metric factor [PR]
+    //      | row reconstruction coefficients [PR][2][KP] (16-byte aligned) | row factors [PR][RW]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
     float* s_lt = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
     float* s_rf = s_lt + TB;
@@ -1205,13 +1381,24 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
         }
     for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
         s_rf[lr] = (inst_on && !g.one_d) ? marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps) : 1.0f;
-    // per-lane reconstruction weights of the metric field and the prediction
-    float gM[RW], gP[RW];
+    // the lane's column carriers and the rows' coefficients of the metric
+    // field (set 0) and the prediction (set 1)
+    constexpr int KP = kcp<KC>();
+    float bc[KC];
+    load_cols<KC>(g, coltab, t, bc);
+    float* s_al = reinterpret_cast<float*>(dyn + lds_al_off(g));
+    // the rows' factors a_q of the t projection, staged with the coefficients
+    // (uniform LDS reads in the loop instead of scalar loads of every row)
+    float* s_ar = s_al + 2 * KP * g.PR;
+    for (int e = threadIdx.x; e < nr * RW; e += SP_NT) {
+        const int lr = e / RW, q = e - lr * RW;
+        s_ar[e] = rowtab[(t.r0 + lr) * g.RW + q];
+    }
     {
-        float b[KC];
-        load_cols<KC>(g, coltab, t, b);
-        recon_weights<RM, KC>(g, meta, b, ctrl->rc[0], gM);
-        recon_weights<RM, KC>(g, meta, b, ctrl->rc[1], gP);
+        const float (*const r0[2])[2] = {ctrl->rc[0], ctrl->rc[1]};
+        const float (*const r1[2])[2] = {nullptr, nullptr};
+        const float w0[2] = {1.f, 1.f}, w1[2] = {0.f, 0.f};
+        alpha_rows<RM, KC>(g, meta, rowtab + t.r0 * g.RW, nr, r0, w0, r1, w1, s_al);
     }
     const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
     __syncthreads();
@@ -1219,7 +1406,6 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     const GT* __restrict__ gb = grad + base;
     const PT* __restrict__ pb = param + base;
     float* __restrict__ tb = tbuf + base;
-    const float* __restrict__ rt = rowtab + t.r0 * g.RW;
     const float inv_s = ctrl->inv_s, scale = ctrl->scale;
     const float mcoup = (float)h.metric_coupling;
     const float wd = (float)h.weight_decay;
@@ -1233,12 +1419,107 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     const float tm = (float)h.transport_mix;
     const float hs = (float)ctrl->hs_P;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
-    float ZP[RW], ZT[RW];
+    const float k2 = -2.8853900817779268f * iclip;   // -2 log2(e) / clip
+    // Only t is projected: the port P = (1 + tm) t - pred projects to
+    // (1 + tm) mean(t Xn) - G u_pred, formed in fin3 from the Gram matrix.
+    float ZT[RW];
 #pragma unroll
-    for (int q = 0; q < RW; ++q) ZP[q] = ZT[q] = 0.f;
-    float m_ee = 0.f, m_P = 0.f, m_t = 0.f, m_tt = 0.f, m_rr = 0.f, m_bb = 0.f, m_oo = 0.f, m_rb = 0.f, m_ro = 0.f,
+    for (int q = 0; q < RW; ++q) ZT[q] = 0.f;
+    float m_ee = 0.f, m_t = 0.f, m_tt = 0.f, m_rr = 0.f, m_bb = 0.f, m_oo = 0.f, m_rb = 0.f, m_ro = 0.f,
           m_bo = 0.f, m_tr = 0.f, m_tb = 0.f, m_to = 0.f;
-    if (t.colok) {
+    // MODE 1 panel views (full tile)
+    PanelBuf gbv, bnv, tbv;
+    if (MODE == 1) {
+        gbv = panel_buf(gb, g, nr);
+        bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
+        tbv = panel_buf(tb, g, nr);
+    }
+    // one row of the lane's column: f -> t (stored), moments, projection, histogram
+    auto row = [&](int lr, float gval, float pval, uint64_t bval) {
+                float f = sg * gval;
+                if (F.wd_on) f = f + wd * pval;
+                const float* __restrict__ ar = s_ar + lr * RW;
+                // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
+                const float* __restrict__ al = s_al + lr * (2 * KP);
+                float lm = cM;
+#pragma unroll
+                for (int k = 0; k < KC; ++k) lm = fmaf(al[k], bc[k], lm);
+                lm = med3f(lm, -3.0f, 3.0f);
+                const float M = med3f(fexp(mcoup * lm), 0.06f, 16.0f);
+                float den = scale * M;
+                if (F.ls_on) {
+                    const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
+                    den = den * clampf(1.0f + ls * fsqrt(fminf(rel, 100.0f)), 1.0f, 8.0f);
+                }
+                if (inst_on) {
+                    float I;
+                    if (MODE == 0 && g.one_d) {
+                        const float rel = fmaxf(fminf(fabsf(f) * inv_s + eps, 1.0e4f), eps);
+                        const float dens = fminf(ipw == 1.0f ? rel : fpow(rel, ipw), 1.0e6f);
+                        I = fexp(kappa * flog(fmaxf(dens / gden, eps)));
+                    } else {
+                        I = s_rf[lr] * ec;
+                    }
+                    den = den * med3f(I, 0.08f, 12.0f);
+                }
+                if (F.hash_on) {
+                    float lsum = 0.f;
+#pragma unroll
+                    for (int tt = 0; tt < SP_MAXT; ++tt) {
+                        if (tt >= F.T) break;
+                        lsum += s_lt[tt * B + bin_of(bval, tt, F.bpb)];
+                    }
+                    den = den * med3f(fexp(lsum * invT), 0.08f, 12.0f);
+                }
+                const float tv = med3f(f * frcp(den + eps), -1.0e4f, 1.0e4f);
+                if (MODE == 1)
+                    stb_lane(tbv, lr, tv);
+                else
+                    tb[panel_off(g, lr)] = tv;
+                float pred = cP;
+#pragma unroll
+                for (int k = 0; k < KC; ++k) pred = fmaf(al[KP + k], bc[k], pred);
+                const float err = tv - pred;
+                const float P = err + tm * tv;
+                m_ee += err * err;
+                m_t += tv;
+                m_tt += tv * tv;
+                // |rat|, |tanh|, |root| share the sign of t: the moments take
+                // magnitudes, and fin3 scales the tanh ones by clip (bnd = clip tanh)
+                const float at = fabsf(tv);
+                const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+                m_rr = fmaf(z.rat, z.rat, m_rr); m_bb = fmaf(z.th, z.th, m_bb); m_oo = fmaf(z.root, z.root, m_oo);
+                m_rb = fmaf(z.rat, z.th, m_rb); m_ro = fmaf(z.rat, z.root, m_ro); m_bo = fmaf(z.th, z.root, m_bo);
+                m_tr = fmaf(at, z.rat, m_tr); m_tb = fmaf(at, z.th, m_tb); m_to = fmaf(at, z.root, m_to);
+#pragma unroll
+                for (int q = 0; q < RW; ++q) ZT[q] += ar[q] * tv;
+                if (F.hash_on) {
+                    const unsigned long long v = to_fixed_s(P * hs);
+#pragma unroll
+                    for (int tt = 0; tt < SP_MAXT; ++tt) {
+                        if (tt >= F.T) break;
+                        atomicAdd(&s_hist[tt * B + bin_of(bval, tt, F.bpb)], v);
+                    }
+                }
+                if (MODE == 1) {
+                    // this row's contributions are complete here
+#pragma unroll
+                    for (int q = 0; q < RW; ++q) pin1(ZT[q]);
+                    pin1(m_ee); pin1(m_t); pin1(m_tt); pin1(m_rr); pin1(m_bb); pin1(m_oo);
+                    pin1(m_rb); pin1(m_ro); pin1(m_bo); pin1(m_tr); pin1(m_tb); pin1(m_to);
+                }
+                elem_fence();
+    };
+    if constexpr (MODE == 1) {
+        // full tile: no guards, next rows' loads in flight during these rows
+        pipelined_rows<SP_U>(
+            nr,
+            [&](int lr, float& x, uint32_t& b) {
+                x = ldb_lane<GT>(gbv, lr);
+                b = ldb_bins16(bnv, lr);
+            },
+            [&](int lr, float x, uint32_t b) { row(lr, x, 0.f, b); });
+    } else if (t.colok) {
         for (int i0 = 0; i0 < nr; i0 += SP_U) {
             float gv[SP_U], pv[SP_U];
             uint64_t bv[SP_U];
@@ -1256,73 +1537,8 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
             }
 #pragma unroll
             for (int u = 0; u < SP_U; ++u) {
-                const int lr = i0 + u;
-                if (lr >= nr) break;
-                float f = sg * gv[u];
-                if (F.wd_on) f = f + wd * pv[u];
-                const float* __restrict__ ar = rt + lr * g.RW;
-                // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
-                float lm = cM;
-#pragma unroll
-                for (int q = 0; q < RW; ++q) lm += ar[q] * gM[q];
-                lm = clampf(lm, -3.0f, 3.0f);
-                const float M = clampf(fexp(mcoup * lm), 0.06f, 16.0f);
-                float den = scale * M;
-                if (F.ls_on) {
-                    const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
-                    den = den * clampf(1.0f + ls * fsqrt(fminf(rel, 100.0f)), 1.0f, 8.0f);
-                }
-                if (inst_on) {
-                    float I;
-                    if (MODE == 0 && g.one_d) {
-                        const float rel = fmaxf(fminf(fabsf(f) * inv_s + eps, 1.0e4f), eps);
-                        const float dens = fminf(ipw == 1.0f ? rel : fpow(rel, ipw), 1.0e6f);
-                        I = fexp(kappa * flog(fmaxf(dens / gden, eps)));
-                    } else {
-                        I = s_rf[lr] * ec;
-                    }
-                    den = den * clampf(I, 0.08f, 12.0f);
-                }
-                if (F.hash_on) {
-                    float lsum = 0.f;
-#pragma unroll
-                    for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= F.T) break;
-                        lsum += s_lt[tt * B + bin_of(bv[u], tt, F.bpb)];
-                    }
-                    den = den * clampf(fexp(lsum * invT), 0.08f, 12.0f);
-                }
-                const float tv = clampf(f * frcp(den + eps), -1.0e4f, 1.0e4f);
-                tb[panel_off(g, lr)] = tv;
-                float pred = cP;
-#pragma unroll
-                for (int q = 0; q < RW; ++q) pred += ar[q] * gP[q];
-                const float err = tv - pred;
-                const float P = err + tm * tv;
-                m_ee += err * err;
-                m_P += P;
-                m_t += tv;
-                m_tt += tv * tv;
-                float rat, ths, root;
-                shape3f(tv, iclip, clip2, eps, rat, ths, root);
-                const float bnd = ths * clip;
-                m_rr += rat * rat; m_bb += bnd * bnd; m_oo += root * root;
-                m_rb += rat * bnd; m_ro += rat * root; m_bo += bnd * root;
-                m_tr += tv * rat; m_tb += tv * bnd; m_to += tv * root;
-#pragma unroll
-                for (int q = 0; q < RW; ++q) {
-                    ZP[q] += ar[q] * P;
-                    ZT[q] += ar[q] * tv;
-                }
-                if (F.hash_on) {
-                    const unsigned long long v = to_fixed_s(P * hs);
-#pragma unroll
-                    for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= F.T) break;
-                        atomicAdd(&s_hist[tt * B + bin_of(bv[u], tt, F.bpb)], v);
-                    }
-                }
-                elem_fence();
+                if (i0 + u >= nr) break;
+                row(i0 + u, gv[u], pv[u], bv[u]);
             }
         }
     }
@@ -1330,16 +1546,13 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT)
             if (s_hist[i]) atomicAdd(&hist[i], s_hist[i]);
-    float b[KC];
-    load_cols<KC>(g, coltab, t, b);
-    Partials P{red, 15 + 4 * g.R, NV3};
-    const float mm[13] = {m_ee, m_P, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
+    Partials P{red, 15 + 2 * g.R, NV3};
+    const float mm[13] = {m_ee, 0.f, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
 #pragma unroll
     for (int k = 0; k < 13; ++k) P.add(k, mm[k]);
     P.add(13, 0.f);
     P.add(14, 0.f);
-    proj_finish<RM, KC>(g, meta, ZP, b, P, 15);
-    proj_finish<RM, KC>(g, meta, ZT, b, P, 15 + 2 * g.R);
+    proj_finish<RM, KC>(g, meta, ZT, bc, P, 15);
     P.flush(part);
 }
 
@@ -1432,7 +1645,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
         s_scal[0] = *st.surprise;
         s_scal[1] = *st.action;
     }
-    load_sums(part, 15 + 4 * R, s_m);
+    load_sums(part, 15 + 2 * R, s_m);
     const float eps = (float)h.eps;
     // hash refractory / impulse (cresso_v5.py:1140-1184)
     if (hash_on) {
@@ -1449,24 +1662,38 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
             imp_tab[i] = im;
         }
     }
+    __shared__ double s_gu[2 * SP_MAXR];     // G u_pred: mean(pred Xn_v)
     if (tid < 64) {
         const int r = tid;
         const bool on = r < R;
-        const double sP = s_m[1], sT = s_m[2];
+        const double sT = s_m[2];
         // surprise reservoir (cresso_v5.py:1127-1129)
         const float sur = reservoir_f(s_scal[0], sqrtf((float)(s_m[0] / n) + eps), h.surprise_decay, step);
-        // port and echo projections -> mean(x Cn); t projections in fp64
-        float pc = 0.f, ps = 0.f, ecs = 0.f, ess = 0.f;
+        // t projections mean(t Xn) in fp64
+        float ecs = 0.f, ess = 0.f;
         if (on) {
             const double mc = s_stats[4 * r], ic = s_stats[4 * r + 1], ms = s_stats[4 * r + 2], is = s_stats[4 * r + 3];
-            pc = (float)((s_m[15 + 2 * r] - mc * sP) * ic / n);
-            ps = (float)((s_m[16 + 2 * r] - ms * sP) * is / n);
-            const double ecd = (s_m[15 + 2 * R + 2 * r] - mc * sT) * ic / n;
-            const double esd = (s_m[16 + 2 * R + 2 * r] - ms * sT) * is / n;
+            const double ecd = (s_m[15 + 2 * r] - mc * sT) * ic / n;
+            const double esd = (s_m[16 + 2 * r] - ms * sT) * is / n;
             ecs = (float)ecd;
             ess = (float)esd;
             s_ec[2 * r] = ecd;
             s_ec[2 * r + 1] = esd;
+        }
+        // mean(pred Xn_v) = (G u_pred)_v, lane v = carrier v
+        if (r < V) {
+            double gu = 0.0;
+            for (int w = 0; w < V; ++w) gu += s_gram[r * V + w] * s_u[0][w];
+            s_gu[r] = gu;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        // port projections (cresso_v5.py:1136): P = err + tm t = (1 + tm) t - pred
+        float pc = 0.f, ps = 0.f;
+        if (on) {
+            const double k1 = 1.0 + (double)(float)h.transport_mix;
+            pc = (float)(k1 * s_ec[2 * r] - s_gu[2 * r]);
+            ps = (float)(k1 * s_ec[2 * r + 1] - s_gu[2 * r + 1]);
         }
         float om = 0.f, qc = 0.f, qs = 0.f, pcv = 0.f, psv = 0.f, cac = 0.f, cas = 0.f, conf = 0.f;
         if (on) {
@@ -1506,10 +1733,10 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
         double q0 = 0.0, q1 = 0.0, q2 = 0.0, q3 = 0.0, q4 = 0.0;
         if (r < V) {
             const int v = r;
-            double gu = 0.0, gup = 0.0, gue = 0.0;
+            const double gu = s_gu[v];
+            double gup = 0.0, gue = 0.0;
             for (int w = 0; w < V; ++w) {
                 const double gvw = s_gram[v * V + w];
-                gu += gvw * s_u[0][w];
                 gup += gvw * s_u[1][w];
                 gue += gvw * s_u[2][w];
             }
@@ -1525,8 +1752,11 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
         if (r == 0) {
             const float S = sur;
             // shaped / core coefficients from the moments of t (cresso_v5.py:1315-1337)
-            const double Stt = s_m[3], Srr = s_m[4], Sbb = s_m[5], Soo = s_m[6], Srb = s_m[7], Sro = s_m[8], Sbo = s_m[9];
-            const double Str = s_m[10], Stb = s_m[11], Sto = s_m[12];
+            // sweep 3 sums |tanh| where the moments use bnd = clip tanh
+            const double cl = (double)(float)h.drive_clip;
+            const double Stt = s_m[3], Srr = s_m[4], Sbb = s_m[5] * cl * cl, Soo = s_m[6], Srb = s_m[7] * cl;
+            const double Sro = s_m[8], Sbo = s_m[9] * cl;
+            const double Str = s_m[10], Stb = s_m[11] * cl, Sto = s_m[12];
             const float frms = sqrtf((float)(Stt / n) + eps);
             const float rms_rat = sqrtf((float)(Srr / n) + eps);
             const float rms_root = sqrtf((float)(Soo / n) + eps);
@@ -1585,7 +1815,6 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
     const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
     float* __restrict__ tbuf, double* __restrict__ part, int hash_arg, int echo_on, cresso_hyper h) {
-    constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV4];
     const SweepFlags F = sweep_flags<MODE>(g, hash_arg, 1, h);
@@ -1593,35 +1822,84 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
     const int B = g.B;
     const int TB = F.T * B;
     const int nr = (int)(t.r1 - t.r0);
-    // LDS: impulse table [T][B]
+    // LDS: impulse table [T][B] | row coefficients [PR][2][KP] of pred' (set 0)
+    // and of k_pred pred' + k_echo echo (set 1), 16-byte aligned
+    constexpr int KP = kcp<KC>();
     float* s_imp = reinterpret_cast<float*>(dyn);
+    float* s_al = reinterpret_cast<float*>(dyn + ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15));
     if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
-    // per-lane weights of pred' and of k_pred pred' + k_echo echo
-    float gQ[RW], gX[RW];
     const float kp = ctrl->k_pred, ke = ctrl->k_echo;
+    float bc[KC];
+    load_cols<KC>(g, coltab, t, bc);
     {
-        float b[KC];
-        load_cols<KC>(g, coltab, t, b);
-        recon_weights<RM, KC>(g, meta, b, ctrl->rc[2], gQ);
-        float gE[RW];
-        recon_weights<RM, KC>(g, meta, b, ctrl->rc[3], gE);
-#pragma unroll
-        for (int q = 0; q < RW; ++q) gX[q] = kp * gQ[q] + (echo_on ? ke * gE[q] : 0.f);
+        const float (*const r0[2])[2] = {ctrl->rc[2], ctrl->rc[2]};
+        const float (*const r1[2])[2] = {nullptr, echo_on ? ctrl->rc[3] : nullptr};
+        const float w0[2] = {1.f, kp}, w1[2] = {0.f, ke};
+        alpha_rows<RM, KC>(g, meta, rowtab + t.r0 * g.RW, nr, r0, w0, r1, w1, s_al);
     }
     const float cQ = ctrl->rconst[2];
     const float cX = kp * ctrl->rconst[2] + (echo_on ? ke * ctrl->rconst[3] : 0.f);
     __syncthreads();
     const int64_t base = panel_base(g, t);
     float* __restrict__ tb = tbuf + base;
-    const float* __restrict__ rt = rowtab + t.r0 * g.RW;
     const float eps = (float)h.eps;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
     const float k_rat = ctrl->k_rat, k_ths = ctrl->k_ths, k_root = ctrl->k_root, k_t = ctrl->k_t, k_nov = ctrl->k_nov;
-    const float ns = ctrl->nscale;
+    const float k2 = -2.8853900817779268f * iclip;            // -2 log2(e) / clip
+    const float k2n = -2.8853900817779268f * ctrl->nscale;    // tanh(err' nscale)
     const float invT = 1.0f / (float)F.T;
     float a_dd = 0.f, a_dh = 0.f, a_hh = 0.f;
-    if (t.colok) {
+    PanelBuf tbv, bnv;
+    if (MODE == 1) {
+        tbv = panel_buf(tb, g, nr);
+        bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
+    }
+    // one row of the lane's column: t -> drive without the hash term (stored over t)
+    auto row = [&](int lr, float tv, uint64_t bval) {
+        const float* __restrict__ al = s_al + lr * (2 * KP);
+        float pred = cQ, mixed = cX;
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+            pred = fmaf(al[k], bc[k], pred);
+            mixed = fmaf(al[KP + k], bc[k], mixed);
+        }
+        const float err = tv - pred;
+        const float nov = ftanh_k(err, k2n);
+        const float at = fabsf(tv);
+        const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+        const float core = xorsign(fmaf(k_t, at, fmaf(k_root, z.root, fmaf(k_ths, z.th, k_rat * z.rat))), tv);
+        const float d = fmaf(k_nov, nov, core + mixed);
+        if (MODE == 1)
+            stb_lane(tbv, lr, d);
+        else
+            tb[panel_off(g, lr)] = d;
+        a_dd = fmaf(d, d, a_dd);
+        if (F.hash_on) {
+            float hp = 0.f;
+#pragma unroll
+            for (int tt = 0; tt < SP_MAXT; ++tt) {
+                if (tt >= F.T) break;
+                hp += s_imp[tt * B + bin_of(bval, tt, F.bpb)];
+            }
+            hp = hp * invT;
+            a_dh = fmaf(d, hp, a_dh);
+            a_hh = fmaf(hp, hp, a_hh);
+        }
+        if (MODE == 1) {
+            pin1(a_dd); pin1(a_dh); pin1(a_hh);
+        }
+        elem_fence();
+    };
+    if constexpr (MODE == 1) {
+        pipelined_rows<SP_U>(
+            nr,
+            [&](int lr, float& x, uint32_t& b) {
+                x = ldb_lane<float>(tbv, lr);
+                b = ldb_bins16(bnv, lr);
+            },
+            [&](int lr, float x, uint32_t b) { row(lr, x, b); });
+    } else if (t.colok) {
         for (int i0 = 0; i0 < nr; i0 += SP_U) {
             float tvs[SP_U];
             uint64_t bv[SP_U];
@@ -1637,35 +1915,8 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
             }
 #pragma unroll
             for (int u = 0; u < SP_U; ++u) {
-                const int lr = i0 + u;
-                if (lr >= nr) break;
-                const float tv = tvs[u];
-                const float* __restrict__ ar = rt + lr * g.RW;
-                float pred = cQ, mixed = cX;
-#pragma unroll
-                for (int q = 0; q < RW; ++q) {
-                    pred += ar[q] * gQ[q];
-                    mixed += ar[q] * gX[q];
-                }
-                const float err = tv - pred;
-                const float nov = ftanh(err * ns);
-                float rat, ths, root;
-                shape3f(tv, iclip, clip2, eps, rat, ths, root);
-                const float d = k_rat * rat + k_ths * ths + k_root * root + k_t * tv + mixed + k_nov * nov;
-                tb[panel_off(g, lr)] = d;
-                a_dd += d * d;
-                if (F.hash_on) {
-                    float hp = 0.f;
-#pragma unroll
-                    for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= F.T) break;
-                        hp += s_imp[tt * B + bin_of(bv[u], tt, F.bpb)];
-                    }
-                    hp = hp * invT;
-                    a_dh += d * hp;
-                    a_hh += hp * hp;
-                }
-                elem_fence();
+                if (i0 + u >= nr) break;
+                row(i0 + u, tvs[u], bv[u]);
             }
         }
     }
@@ -1952,13 +2203,15 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
 
 template <typename T> T* at(void* ws, size_t off) { return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off); }
 
-size_t lds_sweep2(const Geom& g) {
-    return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * 4 * (size_t)g.PR;
+size_t lds_sweep2(const Geom& g, int rw) {
+    return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * (16 + (size_t)rw) * g.PR;
 }
-size_t lds_sweep3(const Geom& g) {
-    return (sizeof(unsigned long long) + sizeof(float)) * g.T * g.B + sizeof(float) * (size_t)g.PR;
+size_t lds_sweep3(const Geom& g, int kp, int rw) {
+    return lds_al_off(g) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
 }
-size_t lds_sweep4(const Geom& g) { return sizeof(float) * (size_t)g.T * g.B; }
+size_t lds_sweep4(const Geom& g, int kp) {
+    return ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15) + sizeof(float) * 2 * (size_t)kp * g.PR;
+}
 constexpr size_t SP_LDS_MAX = 64 * 1024;
 
 template <int RM, int KC, typename PT, typename GT>
@@ -2001,7 +2254,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     const double* gram = at<double>(ws, o.gram);
     const int step = d.step;
     const int axes_on = (hard && h.instant_metric_coupling != 0.0 && !g.one_d) ? 1 : 0;
-    const size_t l2 = lds_sweep2(g), l3 = lds_sweep3(g), l4 = lds_sweep4(g);
+    const size_t l2 = lds_sweep2(g, 2 * RM), l3 = lds_sweep3(g, kcp<KC>(), 2 * RM), l4 = lds_sweep4(g, kcp<KC>());
     if (l2 > SP_LDS_MAX || l3 > SP_LDS_MAX || l4 > SP_LDS_MAX)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_tables x hash_bins = %d needs %zu bytes of LDS per block",
                     g.T * g.B, std::max(l2, std::max(l3, l4)));
