@@ -51,6 +51,11 @@ constexpr int SP_MAXR = 16;
 constexpr int SP_MAXT = 8;
 constexpr int SP_FIN_NT = 1024;  // workspace set-up kernels
 constexpr int SP_FN_NT = 512;    // per-step finalize kernels (room for fp64 accumulators)
+// Fast-path histograms keep SP_NHIST interleaved copies ([bin][copy], copy =
+// lane & 3): lanes of one wave then collide on an address only when both the
+// bin and the copy match.  The copies are summed (integers: any order) before
+// the block's global atomics.  LDS is sized for the copies in every mode.
+constexpr int SP_NHIST = 4;
 
 enum ModeType : int32_t { M_ZERO = 0, M_ADD = 1, M_PROD = 2 };
 
@@ -754,7 +759,8 @@ __device__ __forceinline__ void load_cols(const Geom& g, const float* __restrict
 template <int KC> constexpr int kcp() { return (KC + 3) & ~3; }
 // byte offset of sweep 3's row coefficients in its dynamic LDS
 __host__ __device__ inline size_t lds_al_off(const Geom& g) {
-    const size_t head = (sizeof(unsigned long long) + sizeof(float)) * (size_t)g.T * g.B + sizeof(float) * (size_t)g.PR;
+    const size_t head = (sizeof(unsigned long long) * SP_NHIST + sizeof(float)) * (size_t)g.T * g.B +
+                        sizeof(float) * (size_t)g.PR;
     return (head + 15) & ~(size_t)15;
 }
 template <int RM, int KC>
@@ -969,11 +975,11 @@ __device__ __forceinline__ SweepFlags sweep_flags(const Geom& g, int hash_arg, i
 }
 // whether a tensor's step can use MODE 1 (host side)
 // (MODE 1 also needs full tiles: every row of every panel and every lane's
-// column valid, and panels of a multiple of 2 SP_U rows for the row pipeline.)
+// column valid, and panels of a multiple of 4 SP_U rows for the row pipelines.)
 inline bool fast_mode(const Geom& g, int hash_on, int axes_on, const cresso_hyper& h) {
     return hash_on && axes_on && g.T == 2 && g.bpb == 1 && g.binbytes == 2 && !g.one_d && h.weight_decay == 0.0 &&
            h.local_sharpness == 0.0 && (float)fmax(h.instant_metric_power, 0.25) == 1.0f && g.rows % g.PR == 0 &&
-           g.cols % SP_NT == 0 && g.PR % (2 * SP_U) == 0;
+           g.cols % SP_NT == 0 && g.PR % (4 * SP_U) == 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -997,10 +1003,11 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     // LDS: histogram [T][B] u64 | row-sum partials [16][PR] (MODE 0: [4 waves][PR];
     // MODE 1: [4 waves][4 DPP rows][PR]) | MODE 1 row factors [PR][RW]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
-    float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
+    float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
+    constexpr int NH = MODE == 1 ? SP_NHIST : 1;   // histogram copies in use
     float* s_ar = s_wrow + 16 * g.PR;
     if (F.hash_on)
-        for (int i = threadIdx.x; i < TB; i += SP_NT) s_hist[i] = 0ull;
+        for (int i = threadIdx.x; i < NH * TB; i += SP_NT) s_hist[i] = 0ull;
     if (MODE == 1)
         for (int e = threadIdx.x; e < nr * RW; e += SP_NT) {
             const int lr = e / RW, q = e - lr * RW;
@@ -1029,37 +1036,43 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
         // full tile: rel >= eps and instant-metric power 1, so the density is rel
         const PanelBuf gbv = panel_buf(gb, g, nr);
         const PanelBuf bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
-        pipelined_batches<SP_U>(
+        constexpr int U = SP_U;
+        const int hc = threadIdx.x & (SP_NHIST - 1);
+        pipelined_batches<U>(
             nr,
             [&](int lr, float& x, uint32_t& b) {
                 x = ldb_lane<GT>(gbv, lr);
                 b = ldb_bins16(bnv, lr);
             },
             [&](int i0, const float* x, const uint32_t* bv) {
-                float dn[SP_U];
 #pragma unroll
-                for (int u = 0; u < SP_U; ++u) {
-                    const float rel = fminf(fmaf(fabsf(x[u]), inv_s, eps), 1.0e4f);
-                    const float ds = fexp2(pw * flog2(rel));
-                    const float L = flog2(1.0f + ds);
-                    dn[u] = rel;
-                    aL += L;
-                    aD += rel;
-                    const float* __restrict__ ar = s_ar + (i0 + u) * RW;
+                for (int h8 = 0; h8 < U / 8; ++h8) {
+                    float dn[8];
 #pragma unroll
-                    for (int q = 0; q < RW; ++q) Z[q] = fmaf(ar[q], L, Z[q]);
-                    const unsigned long long v = to_fixed_u(ds * hs);
-                    atomicAdd(&s_hist[bin_of(bv[u], 0, 1)], v);
-                    atomicAdd(&s_hist[B + bin_of(bv[u], 1, 1)], v);
+                    for (int v8 = 0; v8 < 8; ++v8) {
+                        const int u = 8 * h8 + v8;
+                        const float rel = fminf(fmaf(fabsf(x[u]), inv_s, eps), 1.0e4f);
+                        const float ds = fexp2(pw * flog2(rel));
+                        const float L = flog2(1.0f + ds);
+                        dn[v8] = rel;
+                        aL += L;
+                        aD += rel;
+                        const float* __restrict__ ar = s_ar + (i0 + u) * RW;
 #pragma unroll
-                    for (int q = 0; q < RW; ++q) pin1(Z[q]);
-                    pin1(aL);
-                    pin1(aD);
-                    pin1(dn[u]);
-                    elem_fence();
+                        for (int q = 0; q < RW; ++q) Z[q] = fmaf(ar[q], L, Z[q]);
+                        const unsigned long long v = to_fixed_u(ds * hs);
+                        atomicAdd(&s_hist[bin_of(bv[u], 0, 1) * NH + hc], v);
+                        atomicAdd(&s_hist[(B + bin_of(bv[u], 1, 1)) * NH + hc], v);
+#pragma unroll
+                        for (int q = 0; q < RW; ++q) pin1(Z[q]);
+                        pin1(aL);
+                        pin1(aD);
+                        pin1(dn[v8]);
+                        elem_fence();
+                    }
+                    const float rs = rows8_lanesum16(dn);
+                    if ((lane & 8) == 0) s_wrow[((wave << 2) + (lane >> 4)) * g.PR + i0 + 8 * h8 + (lane & 7)] = rs;
                 }
-                const float rs = rows8_lanesum16(dn);
-                if ((lane & 8) == 0) s_wrow[((wave << 2) + (lane >> 4)) * g.PR + i0 + (lane & 7)] = rs;
             });
     } else
     for (int i0 = 0; i0 < nr; i0 += SP_U) {
@@ -1122,8 +1135,12 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
         if (t.colok) atomicAdd(&colfx[t.col], to_fixed_u(aD * (float)g.hs_col));
     }
     if (F.hash_on)
-        for (int i = threadIdx.x; i < TB; i += SP_NT)
-            if (s_hist[i]) atomicAdd(&hist[i], s_hist[i]);
+        for (int i = threadIdx.x; i < TB; i += SP_NT) {
+            unsigned long long v = 0ull;
+#pragma unroll
+            for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
+            if (v) atomicAdd(&hist[i], v);
+        }
     float b[KC];
     load_cols<KC>(g, coltab, t, b);
     Partials P{red, 2 + 2 * g.R, NV2};
@@ -1369,15 +1386,18 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     // LDS: histogram [T][B] u64 | log hash metric [T][B] | row metric factor [PR]
     //      | row reconstruction coefficients [PR][2][KP] (16-byte aligned) | row factors [PR][RW]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
-    float* s_lt = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * (size_t)TB);
+    float* s_lt = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
+    constexpr int NH = MODE == 1 ? SP_NHIST : 1;   // histogram copies in use
+    const int hc = MODE == 1 ? (int)(threadIdx.x & (SP_NHIST - 1)) : 0;
     float* s_rf = s_lt + TB;
     const float eps = (float)h.eps;
     const float kappa = ctrl->kappa, gden = ctrl->gden;
     const bool inst_on = MODE == 1 ? true : kappa != 0.0f;
     if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) {
-            s_hist[i] = 0ull;
             s_lt[i] = lt[i];
+#pragma unroll
+            for (int c = 0; c < NH; ++c) s_hist[i * NH + c] = 0ull;
         }
     for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
         s_rf[lr] = (inst_on && !g.one_d) ? marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps) : 1.0f;
@@ -1498,7 +1518,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
 #pragma unroll
                     for (int tt = 0; tt < SP_MAXT; ++tt) {
                         if (tt >= F.T) break;
-                        atomicAdd(&s_hist[tt * B + bin_of(bval, tt, F.bpb)], v);
+                        atomicAdd(&s_hist[(tt * B + bin_of(bval, tt, F.bpb)) * NH + hc], v);
                     }
                 }
                 if (MODE == 1) {
@@ -1544,8 +1564,12 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     }
     __syncthreads();
     if (F.hash_on)
-        for (int i = threadIdx.x; i < TB; i += SP_NT)
-            if (s_hist[i]) atomicAdd(&hist[i], s_hist[i]);
+        for (int i = threadIdx.x; i < TB; i += SP_NT) {
+            unsigned long long v = 0ull;
+#pragma unroll
+            for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
+            if (v) atomicAdd(&hist[i], v);
+        }
     Partials P{red, 15 + 2 * g.R, NV3};
     const float mm[13] = {m_ee, 0.f, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
 #pragma unroll
@@ -2204,7 +2228,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
 template <typename T> T* at(void* ws, size_t off) { return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off); }
 
 size_t lds_sweep2(const Geom& g, int rw) {
-    return sizeof(unsigned long long) * g.T * g.B + sizeof(float) * (16 + (size_t)rw) * g.PR;
+    return sizeof(unsigned long long) * SP_NHIST * g.T * g.B + sizeof(float) * (16 + (size_t)rw) * g.PR;
 }
 size_t lds_sweep3(const Geom& g, int kp, int rw) {
     return lds_al_off(g) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
