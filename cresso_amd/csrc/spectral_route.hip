@@ -755,6 +755,10 @@ __device__ __forceinline__ void load_cols(const Geom& g, const float* __restrict
 // (b_k: the lane's column carriers, b_0 = 1), for the block's nr rows: the
 // per-lane form sum_q a_q(row) gamma_q(col) has 2R terms, this one K.  Set
 // j's mode coefficients are w0[j] rc0[j] + w1[j] rc1[j] (rc1 may be null).
+// The block's row factors arrive staged in LDS (s_rows[lr][q], q < 2 RM).
+// Loops of dependent reads per entry (global or LDS) cost microseconds per
+// block at the start of a sweep, so the computation is a small dense product
+// with independent reads.  Ends with a barrier.
 // Out: s_al[lr][j][k], row stride 2 * KCP (KCP = KC rounded up to 4).
 template <int KC> constexpr int kcp() { return (KC + 3) & ~3; }
 // byte offset of sweep 3's row coefficients in its dynamic LDS
@@ -764,34 +768,64 @@ __host__ __device__ inline size_t lds_al_off(const Geom& g) {
     return (head + 15) & ~(size_t)15;
 }
 template <int RM, int KC>
-__device__ void alpha_rows(const Geom& g, const ModeMeta* __restrict__ meta, const float* __restrict__ rt, int nr,
+__device__ void alpha_rows(const Geom& g, const ModeMeta* __restrict__ meta, const float* __restrict__ s_rows, int nr,
                            const float (*const rc0[2])[2], const float w0[2], const float (*const rc1[2])[2],
                            const float w1[2], float* __restrict__ s_al) {
+    // alpha = rows x Cm^T: Cm[j][k][q] is the coefficient of the row factor
+    // a_q (q = 2r + c: component c of mode r) in alpha_k of set j.  Every Cm
+    // entry is built by its own thread from the mode table; each (row, set)
+    // pair is then 2 RM x KP branch-free FMAs on values held in registers.
     constexpr int KP = kcp<KC>();
-    for (int e = threadIdx.x; e < nr * 2 * KP; e += blockDim.x) {
-        const int lr = e / (2 * KP), rem = e - lr * 2 * KP, j = rem / KP, k = rem - j * KP;
-        const float* __restrict__ ar = rt + lr * g.RW;
-        float a = 0.f;
-        if (k < KC) {
-            for (int r = 0; r < g.R; ++r) {
-                const ModeMeta m = meta[r];
-                if (m.k1 != k && m.k2 != k) continue;
-                float wc = w0[j] * rc0[j][r][0], ws = w0[j] * rc0[j][r][1];
-                if (rc1[j]) {
-                    wc += w1[j] * rc1[j][r][0];
-                    ws += w1[j] * rc1[j][r][1];
-                }
-                const float a1 = ar[2 * r], a2 = ar[2 * r + 1];
-                if (m.type == M_ADD) {   // coefficient of a1: wc b1 + ws b2; of a2: ws b1 - wc b2
-                    if (m.k1 == k) a += wc * a1 + ws * a2;
-                    if (m.k2 == k) a += ws * a1 - wc * a2;
-                } else {                 // a1 wc b1 + a2 ws b2
-                    if (m.k1 == k) a += wc * a1;
-                    if (m.k2 == k) a += ws * a2;
-                }
+    constexpr int RW = 2 * RM;
+    __shared__ __align__(16) float s_cm[2][KP][RW];
+    for (int e = threadIdx.x; e < 2 * KP * RW; e += blockDim.x) {
+        const int j = e / (KP * RW), rem = e - j * (KP * RW), k = rem / RW, q = rem - k * RW;
+        const int r = q >> 1, c = q & 1;
+        float v = 0.f;
+        if (r < g.R && k < KC) {
+            const ModeMeta m = meta[r];
+            float wc = w0[j] * rc0[j][r][0], ws = w0[j] * rc0[j][r][1];
+            if (rc1[j]) {
+                wc += w1[j] * rc1[j][r][0];
+                ws += w1[j] * rc1[j][r][1];
+            }
+            if (m.type == M_ADD) {   // alpha_k1 += wc a1 + ws a2, alpha_k2 += ws a1 - wc a2
+                if (m.k1 == k) v += c == 0 ? wc : ws;
+                if (m.k2 == k) v += c == 0 ? ws : -wc;
+            } else {                 // alpha_k1 += wc a1, alpha_k2 += ws a2
+                if (m.k1 == k && c == 0) v += wc;
+                if (m.k2 == k && c == 1) v += ws;
             }
         }
-        s_al[e] = a;
+        s_cm[j][k][q] = v;
+    }
+    __syncthreads();   // Cm and the caller's staged rows are complete
+    for (int p = threadIdx.x; p < 2 * nr; p += blockDim.x) {
+        const int lr = p >> 1, j = p & 1;
+        float row[RW];
+#pragma unroll
+        for (int q = 0; q < RW; ++q) row[q] = s_rows[lr * RW + q];
+        float* __restrict__ out = s_al + lr * (2 * KP) + j * KP;
+#pragma unroll
+        for (int k = 0; k < KP; ++k) {
+            float a = 0.f;
+#pragma unroll
+            for (int q = 0; q < RW; ++q) a = fmaf(s_cm[j][k][q], row[q], a);
+            out[k] = a;
+        }
+    }
+    __syncthreads();
+}
+
+// The block's rows of the row-factor table into LDS: s_rows[lr][q], q < 2 RM
+// (the table's rows have g.RW >= 2 RM entries).  No barrier.
+template <int RM>
+__device__ __forceinline__ void stage_rows(const Geom& g, const float* __restrict__ rowtab, int64_t r0, int nr,
+                                           float* __restrict__ s_rows) {
+    constexpr int RW = 2 * RM;
+    for (int e = threadIdx.x; e < nr * RW; e += blockDim.x) {
+        const int lr = e / RW, q = e - lr * RW;
+        s_rows[e] = rowtab[(r0 + lr) * g.RW + q];
     }
 }
 
@@ -895,12 +929,13 @@ __device__ __forceinline__ void stb_lane(const PanelBuf& b, int lr, float v) {
 // multiple of 2U.  load(lr, x, b) loads row lr's lane values, body(lr, x, b)
 // processes them.
 // The same with a per-batch body: batch(i0, x[U], b[U]) processes rows i0..i0+U-1.
+// xa/ba hold the first batch, loaded by the caller (at the top of the kernel,
+// so that its latency overlaps the block's set-up).
 template <int U, typename Load, typename Batch>
-__device__ __forceinline__ void pipelined_batches(int nr, Load&& load, Batch&& batch) {
-    float xa[U], xb[U];
-    uint32_t ba[U], bb[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) load(u, xa[u], ba[u]);
+__device__ __forceinline__ void pipelined_batches(int nr, Load&& load, Batch&& batch, float (&xa)[U],
+                                                  uint32_t (&ba)[U]) {
+    float xb[U];
+    uint32_t bb[U];
     for (int i0 = 0; i0 < nr; i0 += 2 * U) {
 #pragma unroll
         for (int u = 0; u < U; ++u) load(i0 + U + u, xb[u], bb[u]);
@@ -913,11 +948,14 @@ __device__ __forceinline__ void pipelined_batches(int nr, Load&& load, Batch&& b
     }
 }
 template <int U, typename Load, typename Body>
-__device__ __forceinline__ void pipelined_rows(int nr, Load&& load, Body&& body) {
-    pipelined_batches<U>(nr, load, [&](int i0, const float* x, const uint32_t* b) {
+__device__ __forceinline__ void pipelined_rows(int nr, Load&& load, Body&& body, float (&xa)[U], uint32_t (&ba)[U]) {
+    pipelined_batches<U>(
+        nr, load,
+        [&](int i0, const float* x, const uint32_t* b) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) body(i0 + u, x[u], b[u]);
-    });
+            for (int u = 0; u < U; ++u) body(i0 + u, x[u], b[u]);
+        },
+        xa, ba);
 }
 
 // Sums of 8 per-lane values (rows i0..i0+7 of the lane's column) over the 16
@@ -1000,6 +1038,21 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     const int B = g.B;
     const int TB = F.T * B;
     const int nr = (int)(t.r1 - t.r0);
+    const int64_t base = panel_base(g, t);
+    const GT* __restrict__ gb = grad + base;
+    // MODE 1: the first batch's loads go out before the set-up below
+    PanelBuf gbv, bnv;
+    float x0[SP_U];
+    uint32_t b0[SP_U];
+    if constexpr (MODE == 1) {
+        gbv = panel_buf(gb, g, nr);
+        bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
+#pragma unroll
+        for (int u = 0; u < SP_U; ++u) {
+            x0[u] = ldb_lane<GT>(gbv, u);
+            b0[u] = ldb_bins16(bnv, u);
+        }
+    }
     // LDS: histogram [T][B] u64 | row-sum partials [16][PR] (MODE 0: [4 waves][PR];
     // MODE 1: [4 waves][4 DPP rows][PR]) | MODE 1 row factors [PR][RW]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
@@ -1008,14 +1061,8 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     float* s_ar = s_wrow + 16 * g.PR;
     if (F.hash_on)
         for (int i = threadIdx.x; i < NH * TB; i += SP_NT) s_hist[i] = 0ull;
-    if (MODE == 1)
-        for (int e = threadIdx.x; e < nr * RW; e += SP_NT) {
-            const int lr = e / RW, q = e - lr * RW;
-            s_ar[e] = rowtab[(t.r0 + lr) * g.RW + q];
-        }
+    if (MODE == 1) stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
     __syncthreads();
-    const int64_t base = panel_base(g, t);
-    const GT* __restrict__ gb = grad + base;
     const PT* __restrict__ pb = param + base;
     const float* __restrict__ rt = rowtab + t.r0 * g.RW;
     const float inv_s = ctrl->inv_s;
@@ -1034,8 +1081,6 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     // Sums of log(1 + ds) are kept in log2 units (fin2 scales them by ln 2).
     if constexpr (MODE == 1) {
         // full tile: rel >= eps and instant-metric power 1, so the density is rel
-        const PanelBuf gbv = panel_buf(gb, g, nr);
-        const PanelBuf bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
         constexpr int U = SP_U;
         const int hc = threadIdx.x & (SP_NHIST - 1);
         pipelined_batches<U>(
@@ -1073,7 +1118,8 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
                     const float rs = rows8_lanesum16(dn);
                     if ((lane & 8) == 0) s_wrow[((wave << 2) + (lane >> 4)) * g.PR + i0 + 8 * h8 + (lane & 7)] = rs;
                 }
-            });
+            },
+            x0, b0);
     } else
     for (int i0 = 0; i0 < nr; i0 += SP_U) {
         float gv[SP_U], pv[SP_U];
@@ -1383,6 +1429,23 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     const int B = g.B;
     const int TB = F.T * B;
     const int nr = (int)(t.r1 - t.r0);
+    const int64_t base = panel_base(g, t);
+    const GT* __restrict__ gb = grad + base;
+    float* __restrict__ tb = tbuf + base;
+    // MODE 1: the first batch's loads go out before the set-up below
+    PanelBuf gbv, bnv, tbv;
+    float x0[SP_U];
+    uint32_t b0[SP_U];
+    if constexpr (MODE == 1) {
+        gbv = panel_buf(gb, g, nr);
+        bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
+        tbv = panel_buf(tb, g, nr);
+#pragma unroll
+        for (int u = 0; u < SP_U; ++u) {
+            x0[u] = ldb_lane<GT>(gbv, u);
+            b0[u] = ldb_bins16(bnv, u);
+        }
+    }
     // LDS: histogram [T][B] u64 | log hash metric [T][B] | row metric factor [PR]
     //      | row reconstruction coefficients [PR][2][KP] (16-byte aligned) | row factors [PR][RW]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
@@ -1410,22 +1473,16 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     // the rows' factors a_q of the t projection, staged with the coefficients
     // (uniform LDS reads in the loop instead of scalar loads of every row)
     float* s_ar = s_al + 2 * KP * g.PR;
-    for (int e = threadIdx.x; e < nr * RW; e += SP_NT) {
-        const int lr = e / RW, q = e - lr * RW;
-        s_ar[e] = rowtab[(t.r0 + lr) * g.RW + q];
-    }
+    stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
     {
         const float (*const r0[2])[2] = {ctrl->rc[0], ctrl->rc[1]};
         const float (*const r1[2])[2] = {nullptr, nullptr};
         const float w0[2] = {1.f, 1.f}, w1[2] = {0.f, 0.f};
-        alpha_rows<RM, KC>(g, meta, rowtab + t.r0 * g.RW, nr, r0, w0, r1, w1, s_al);
+        alpha_rows<RM, KC>(g, meta, s_ar, nr, r0, w0, r1, w1, s_al);
     }
     const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
     __syncthreads();
-    const int64_t base = panel_base(g, t);
-    const GT* __restrict__ gb = grad + base;
     const PT* __restrict__ pb = param + base;
-    float* __restrict__ tb = tbuf + base;
     const float inv_s = ctrl->inv_s, scale = ctrl->scale;
     const float mcoup = (float)h.metric_coupling;
     const float wd = (float)h.weight_decay;
@@ -1448,12 +1505,6 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     float m_ee = 0.f, m_t = 0.f, m_tt = 0.f, m_rr = 0.f, m_bb = 0.f, m_oo = 0.f, m_rb = 0.f, m_ro = 0.f,
           m_bo = 0.f, m_tr = 0.f, m_tb = 0.f, m_to = 0.f;
     // MODE 1 panel views (full tile)
-    PanelBuf gbv, bnv, tbv;
-    if (MODE == 1) {
-        gbv = panel_buf(gb, g, nr);
-        bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
-        tbv = panel_buf(tb, g, nr);
-    }
     // one row of the lane's column: f -> t (stored), moments, projection, histogram
     auto row = [&](int lr, float gval, float pval, uint64_t bval) {
                 float f = sg * gval;
@@ -1538,7 +1589,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
                 x = ldb_lane<GT>(gbv, lr);
                 b = ldb_bins16(bnv, lr);
             },
-            [&](int lr, float x, uint32_t b) { row(lr, x, 0.f, b); });
+            [&](int lr, float x, uint32_t b) { row(lr, x, 0.f, b); }, x0, b0);
     } else if (t.colok) {
         for (int i0 = 0; i0 < nr; i0 += SP_U) {
             float gv[SP_U], pv[SP_U];
@@ -1847,10 +1898,12 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
     const int TB = F.T * B;
     const int nr = (int)(t.r1 - t.r0);
     // LDS: impulse table [T][B] | row coefficients [PR][2][KP] of pred' (set 0)
-    // and of k_pred pred' + k_echo echo (set 1), 16-byte aligned
+    // and of k_pred pred' + k_echo echo (set 1), 16-byte aligned | row factors [PR][2 RM]
     constexpr int KP = kcp<KC>();
     float* s_imp = reinterpret_cast<float*>(dyn);
     float* s_al = reinterpret_cast<float*>(dyn + ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15));
+    float* s_rows = s_al + 2 * KP * g.PR;   // the block's row factors [PR][2 RM]
+    stage_rows<RM>(g, rowtab, t.r0, nr, s_rows);
     if (F.hash_on)
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
     const float kp = ctrl->k_pred, ke = ctrl->k_echo;
@@ -1860,7 +1913,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
         const float (*const r0[2])[2] = {ctrl->rc[2], ctrl->rc[2]};
         const float (*const r1[2])[2] = {nullptr, echo_on ? ctrl->rc[3] : nullptr};
         const float w0[2] = {1.f, kp}, w1[2] = {0.f, ke};
-        alpha_rows<RM, KC>(g, meta, rowtab + t.r0 * g.RW, nr, r0, w0, r1, w1, s_al);
+        alpha_rows<RM, KC>(g, meta, s_rows, nr, r0, w0, r1, w1, s_al);
     }
     const float cQ = ctrl->rconst[2];
     const float cX = kp * ctrl->rconst[2] + (echo_on ? ke * ctrl->rconst[3] : 0.f);
@@ -1916,13 +1969,20 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
         elem_fence();
     };
     if constexpr (MODE == 1) {
+        float x0[SP_U];
+        uint32_t b0[SP_U];
+#pragma unroll
+        for (int u = 0; u < SP_U; ++u) {
+            x0[u] = ldb_lane<float>(tbv, u);
+            b0[u] = ldb_bins16(bnv, u);
+        }
         pipelined_rows<SP_U>(
             nr,
             [&](int lr, float& x, uint32_t& b) {
                 x = ldb_lane<float>(tbv, lr);
                 b = ldb_bins16(bnv, lr);
             },
-            [&](int lr, float x, uint32_t b) { row(lr, x, b); });
+            [&](int lr, float x, uint32_t b) { row(lr, x, b); }, x0, b0);
     } else if (t.colok) {
         for (int i0 = 0; i0 < nr; i0 += SP_U) {
             float tvs[SP_U];
@@ -1943,6 +2003,141 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
                 row(i0 + u, tvs[u], bv[u]);
             }
         }
+    }
+    Partials P{red, 3, NV4};
+    P.add(0, a_dd);
+    P.add(1, a_dh);
+    P.add(2, a_hh);
+    P.flush(part);
+}
+
+// ---------------------------------------------------------------------------
+// S4 on the matrix cores (MODE 1 tiles).  Each wave owns 64 columns of the
+// panel as 4 x 4 tiles of 16 x 16 elements.  A reconstruction of a tile is
+// 3 MFMAs (v_mfma_f32_16x16x4f32, the K = KC carriers in chunks of 4):
+//   A[i][k] = alpha_{4kc+k}(row i)   lane l supplies i = l % 16, k = l / 16
+//   B[k][j] = b_{4kc+k}(col j)       lane l supplies j = l % 16, k = l / 16
+//   D[i][j]                          lane l, register r: i = 4 (l / 16) + r, j = l % 16
+// so lane l processes rows 4 (l/16) + r of column l % 16 of each tile, and the
+// elementwise drive math is unchanged.  The loads of the next tile are in
+// flight while a tile is processed.
+// ---------------------------------------------------------------------------
+typedef float f32x4m __attribute__((ext_vector_type(4)));
+template <int RM, int KC>
+__global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
+    Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
+    const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
+    float* __restrict__ tbuf, double* __restrict__ part, int echo_on, cresso_hyper h) {
+    static_assert(KC <= 12, "three K-chunks of four carriers");
+    extern __shared__ __align__(16) unsigned char dyn[];
+    __shared__ float red[4 * NV4];
+    const Tile t = tile_of(g);
+    const int B = g.B;
+    const int TB = 2 * B;
+    const int nr = g.PR;
+    constexpr int KP = kcp<KC>();
+    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int li = l & 15, lg = l >> 4;
+    const int64_t base = panel_base(g, t);
+    float* __restrict__ tb = tbuf + base;
+    const uint32_t cols = (uint32_t)g.cols;
+    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tb, (uint32_t)((int64_t)nr * g.cols * 4));
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(reinterpret_cast<const uint16_t*>(bins) + base, (uint32_t)((int64_t)nr * g.cols * 2));
+    const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
+    const uint32_t vt = lane_el * 4u, vb = lane_el * 2u;
+    // tile (tr, tc), lane element r: panel element (16 tr + 4 lg + r, 64 wv + 16 tc + li)
+    auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
+    // A row of tiles (4 tiles x 4 elements) is in flight while the previous row
+    // is processed; the first row's loads go out before the block's set-up, so
+    // that memory is busy during it.
+    float xa[16], xb[16];
+    uint32_t ba[16], bb[16];
+    auto load_row = [&](int tr, float* x, uint32_t* b) {
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t o = tile_off(tr, tc, r);
+                x[4 * tc + r] = bload1(rt, vt, o * 4u);
+                b[4 * tc + r] = bload1u16(rb, vb, o * 2u);
+            }
+    };
+    load_row(0, xa, ba);
+    float* s_imp = reinterpret_cast<float*>(dyn);
+    float* s_al = reinterpret_cast<float*>(dyn + ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15));
+    float* s_rows = s_al + 2 * KP * g.PR;   // the block's row factors [PR][2 RM]
+    stage_rows<RM>(g, rowtab, t.r0, nr, s_rows);
+    // B operands: carriers 4 kc + lg of the lane's column in each column tile
+    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
+    float bq[4][3];
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+        for (int kc = 0; kc < 3; ++kc) {
+            const int k = 4 * kc + lg;
+            bq[tc][kc] = k < KC ? coltab[(size_t)k * g.cols + colw + 16 * tc + li] : 0.f;
+        }
+    for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
+    const float kp = ctrl->k_pred, ke = ctrl->k_echo;
+    {
+        const float (*const r0[2])[2] = {ctrl->rc[2], ctrl->rc[2]};
+        const float (*const r1[2])[2] = {nullptr, echo_on ? ctrl->rc[3] : nullptr};
+        const float w0[2] = {1.f, kp}, w1[2] = {0.f, ke};
+        alpha_rows<RM, KC>(g, meta, s_rows, nr, r0, w0, r1, w1, s_al);
+    }
+    const float cQ = ctrl->rconst[2];
+    const float cX = kp * ctrl->rconst[2] + (echo_on ? ke * ctrl->rconst[3] : 0.f);
+    __syncthreads();
+    const float eps = (float)h.eps;
+    const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
+    const float k_rat = ctrl->k_rat, k_ths = ctrl->k_ths, k_root = ctrl->k_root, k_t = ctrl->k_t, k_nov = ctrl->k_nov;
+    const float k2 = -2.8853900817779268f * iclip;
+    const float k2n = -2.8853900817779268f * ctrl->nscale;
+    float a_dd = 0.f, a_dh = 0.f, a_hh = 0.f;
+    auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const float* aP, const float* aX) {
+        f32x4m pred = {cQ, cQ, cQ, cQ}, mixed = {cX, cX, cX, cX};
+#pragma unroll
+        for (int kc = 0; kc < 3; ++kc) {
+            pred = __builtin_amdgcn_mfma_f32_16x16x4f32(aP[kc], bq[tc][kc], pred, 0, 0, 0);
+            mixed = __builtin_amdgcn_mfma_f32_16x16x4f32(aX[kc], bq[tc][kc], mixed, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float tv = x[r];
+            const float err = tv - pred[r];
+            const float nov = ftanh_k(err, k2n);
+            const float at = fabsf(tv);
+            const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+            const float core = xorsign(fmaf(k_t, at, fmaf(k_root, z.root, fmaf(k_ths, z.th, k_rat * z.rat))), tv);
+            const float d = fmaf(k_nov, nov, core + mixed[r]);
+            bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
+            a_dd = fmaf(d, d, a_dd);
+            const float hp = (s_imp[b[r] & 0xffu] + s_imp[B + (b[r] >> 8)]) * 0.5f;
+            a_dh = fmaf(d, hp, a_dh);
+            a_hh = fmaf(hp, hp, a_hh);
+        }
+        pin1(a_dd); pin1(a_dh); pin1(a_hh);
+        elem_fence();
+    };
+    auto row_tiles = [&](int tr, const float* x, const uint32_t* b) {
+        // A operands of this row of tiles: alpha_{4 kc + lg}(row 16 tr + li)
+        const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
+        float aP[3], aX[3];
+#pragma unroll
+        for (int kc = 0; kc < 3; ++kc) {
+            aP[kc] = alr[4 * kc];
+            aX[kc] = alr[KP + 4 * kc];
+        }
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) tile(tr, tc, x + 4 * tc, b + 4 * tc, aP, aX);
+    };
+    const int ntr = nr / 16;   // even: PR is a multiple of 32 on this path
+    for (int tr = 0; tr < ntr; tr += 2) {
+        load_row(tr + 1, xb, bb);
+        row_tiles(tr, xa, ba);
+        if (tr + 2 < ntr) load_row(tr + 2, xa, ba);
+        row_tiles(tr + 1, xb, bb);
     }
     Partials P{red, 3, NV4};
     P.add(0, a_dd);
@@ -2233,8 +2428,8 @@ size_t lds_sweep2(const Geom& g, int rw) {
 size_t lds_sweep3(const Geom& g, int kp, int rw) {
     return lds_al_off(g) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
 }
-size_t lds_sweep4(const Geom& g, int kp) {
-    return ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15) + sizeof(float) * 2 * (size_t)kp * g.PR;
+size_t lds_sweep4(const Geom& g, int kp, int rw) {
+    return ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
 }
 constexpr size_t SP_LDS_MAX = 64 * 1024;
 
@@ -2278,7 +2473,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     const double* gram = at<double>(ws, o.gram);
     const int step = d.step;
     const int axes_on = (hard && h.instant_metric_coupling != 0.0 && !g.one_d) ? 1 : 0;
-    const size_t l2 = lds_sweep2(g, 2 * RM), l3 = lds_sweep3(g, kcp<KC>(), 2 * RM), l4 = lds_sweep4(g, kcp<KC>());
+    const size_t l2 = lds_sweep2(g, 2 * RM), l3 = lds_sweep3(g, kcp<KC>(), 2 * RM), l4 = lds_sweep4(g, kcp<KC>(), 2 * RM);
     if (l2 > SP_LDS_MAX || l3 > SP_LDS_MAX || l4 > SP_LDS_MAX)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_tables x hash_bins = %d needs %zu bytes of LDS per block",
                     g.T * g.B, std::max(l2, std::max(l3, l4)));
@@ -2310,12 +2505,20 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3), dim3(256), 0, s, part, g.nblk, NV3, sums);
     hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
                        step, hash_on, hard, echo_on, h);
+    if constexpr (KC <= 12) {
+        if (fast) {
+            hipLaunchKernelGGL((sweep4m_kernel<RM, KC>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf,
+                               part, echo_on, h);
+            goto swept4;
+        }
+    }
     if (fast)
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
                            hash_on, echo_on, h);
     else
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 0>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
                            hash_on, echo_on, h);
+swept4:
     hipLaunchKernelGGL(fin4_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, step, hash_on, hard, h);
     const size_t l5 = hash_on ? sizeof(float) * (size_t)g.T * g.B : 0;
     const bool pv4 = ((uintptr_t)param % (4 * sizeof(PT))) == 0;
