@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 LIB_NAME = "libcresso_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, F64, F16, BF16 = 0, 1, 2, 3
 DTYPE_CODE = {torch.float32: F32, torch.float64: F64, torch.float16: F16, torch.bfloat16: BF16}
@@ -32,7 +32,7 @@ HYPER_DOUBLES = (
     "refractory_decay", "refractory_gain", "confidence_decay", "confidence_gain",
     "surprise_gain", "surprise_decay", "prediction_mix", "novelty_mix",
     "surprise_brake", "target_update_rms", "min_gain", "max_gain", "drive_clip",
-    "spike_mix", "eps",
+    "spike_mix", "eps", "micro_decay", "micro_impulse_decay", "micro_drive_mix",
 )
 
 
@@ -54,7 +54,11 @@ class ScalarDesc(ctypes.Structure):
         ("param_dtype", ctypes.c_int32),
         ("grad_dtype", ctypes.c_int32),
         ("step", ctypes.c_int32),
+        ("route", ctypes.c_int32),
     ]
+
+
+ROUTE_SCALAR, ROUTE_MICRO = 0, 1
 
 
 class SpectralDesc(ctypes.Structure):

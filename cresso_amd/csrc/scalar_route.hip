@@ -17,7 +17,7 @@
 //   D: drive; sum drive^2                     -> drive-energy reservoir, gain
 //   E: param -= lr * cast(drive * gain)
 //
-// Two kernels:
+// Three kernels:
 //  * scalar_resident_kernel: 2D tensors of <= 64 Ki elements whose rows map to
 //    lane groups (LoRA-thin (L,16)) or whose rows are exactly one block wide
 //    ((16,4096)); f, then t, then drive stay on chip (half of each thread's
@@ -27,6 +27,8 @@
 //  * scalar_stream_kernel: every other shape/size/dtype; re-reads the grad in
 //    each pass and keeps general-ndim axis sums as 64-bit fixed-point integers
 //    in a global scratch area (integer atomics: order-independent results).
+//  * micro_kernel: the dense micro-field route (descriptor route 1) of
+//    cresso_v5.py:1355-1432, same plan, table and launch grouping.
 #include "common.hpp"
 
 #include <algorithm>
@@ -873,12 +875,260 @@ __global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* _
 }
 
 // ---------------------------------------------------------------------------
+// micro-field kernel: the dense per-coordinate route of small tensors
+// (micro_field_max_size > 0), cresso_v5.py:1355-1432 (PyTorch-only in the
+// reference).  One workgroup per tensor, five streaming passes:
+//   A: sum f^2                          -> force-RMS reservoir, scale s
+//   B: energy field e <- EMA of rel^p (written back), sum e; instant density,
+//      its sum and its per-axis sums    -> metric normaliser, instant metric
+//   C: t; refractory and impulse fields (written back); sums of err^2, rat^2,
+//      rat*bnd, bnd^2, pred^2, t^2      -> surprise reservoir, shaped-force
+//                                          RMS and the three RMS normalisers
+//   D: drive; sum drive^2               -> drive-energy reservoir, gain
+//   E: param -= lr * cast(drive * gain)
+// Per-axis density sums are 64-bit fixed-point integers (order-independent,
+// so the result does not depend on atomic order) in LDS when they fit, else
+// in the tensor's table scratch; the fixed-point scale comes from an upper
+// bound of the largest density, sqrt(sum f^2) >= max |f|.
+// ---------------------------------------------------------------------------
+constexpr int64_t MF_LDS_AXES = 4096;   // axis-sum entries held in LDS
+
+template <typename W, typename PT, typename GT>
+__global__ __launch_bounds__(SR_NT) void micro_kernel(const ScalarRec* __restrict__ recs, int32_t* __restrict__ steps,
+                                                      const void* const* __restrict__ grads, int32_t first,
+                                                      unsigned char* table, cresso_hyper h) {
+    __shared__ double red[16 * 6];
+    __shared__ unsigned long long s_ax[MF_LDS_AXES];
+    __shared__ int s_step;
+    const int tid = threadIdx.x;
+    const int ri = first + blockIdx.x;
+    const ScalarRec& R = recs[ri];
+    const int64_t n = R.d.numel;
+    const int nd = R.d.ndim;
+    const int layout = R.layout;
+    const W eps = (W)h.eps;
+    W* __restrict__ en = reinterpret_cast<W*>(R.d.state[0]);   // micro_energy
+    W* __restrict__ im = reinterpret_cast<W*>(R.d.state[1]);   // micro_impulse
+    W* __restrict__ rf = reinterpret_cast<W*>(R.d.state[2]);   // micro_refractory
+    W* const st_fr = reinterpret_cast<W*>(R.d.state[3]);
+    W* const st_de = reinterpret_cast<W*>(R.d.state[4]);
+    W* const st_su = reinterpret_cast<W*>(R.d.state[5]);
+    W fr = *st_fr, de = *st_de, sur = *st_su;
+    if (tid == 0) {
+        const int s = steps[ri] + 1;
+        steps[ri] = s;
+        s_step = s;
+    }
+    const GT* __restrict__ g = reinterpret_cast<const GT*>(grads[ri]);
+    PT* __restrict__ p = reinterpret_cast<PT*>(R.d.param);
+    const bool wd_on = h.weight_decay != 0.0;
+    const W wd = (W)h.weight_decay;
+    const bool neg = h.maximize != 0;
+    auto force = [&](int64_t i) -> W {
+        W f = ldw<W>(g, i);
+        if (neg) f = -f;
+        if (wd_on) f = f + wd * ldw<W>(p, i);
+        return f;
+    };
+    unsigned long long* ax = R.sum_dims <= MF_LDS_AXES ? s_ax : reinterpret_cast<unsigned long long*>(table + R.scratch_off);
+    const double dn = (double)n;
+
+    // ---- pass A ----
+    W a = 0;
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W f = force(i);
+        a += f * f;
+    }
+    if (layout == L_GENERIC) {
+        for (int64_t k = tid; k < R.sum_dims; k += SR_NT) ax[k] = 0ull;
+        __threadfence();   // zeros reach L2 before any wave's atomics
+    }
+    __syncthreads();
+    const int step = s_step;
+    double sumsq;
+    {
+        double v[1] = {(double)a};
+        block_sum<1>(v, red);
+        sumsq = v[0];
+        fr = reservoir(fr, (W)sqrt((double)((W)(v[0] / dn) + eps)), h.reservoir_decay, step);
+    }
+    const W scale = fr > eps ? fr : eps;
+
+    // ---- pass B ----
+    const W pw = (W)h.energy_power;
+    const W md = (W)h.micro_decay, md1 = (W)(1.0 - h.micro_decay);
+    const double ipw_d = fmax(h.instant_metric_power, 0.25);
+    const W ipw = (W)ipw_d;
+    // cresso_v5.py:1390-1392: the instant-metric coupling is capped at 0.35
+    const W kappa = nd > 0 ? (W)(fmin(0.35, h.instant_metric_coupling) / ((double)nd * ipw_d)) : (W)0;
+    auto rel_of = [&](W f) -> W {
+        const W r = (f < 0 ? -f : f) / scale + eps;
+        return r < (W)1e4 ? r : (W)1e4;
+    };
+    auto density = [&](W rel) -> W {   // cresso_v5.py:243-262
+        const W r = rel > eps ? rel : eps;
+        const W d = ipw == (W)1 ? r : fpow(r, ipw);
+        return d < (W)1e6 ? d : (W)1e6;
+    };
+    int64_t maxcnt = 1;
+    for (int k = 0; k < nd; ++k) maxcnt = n / R.d.shape[k] > maxcnt ? n / R.d.shape[k] : maxcnt;
+    double fx_scale = 1.0;
+    if (layout == L_GENERIC) {
+        // every |f| <= sqrt(sum f^2), so every density <= dens_b: the fixed-point
+        // axis sums stay below 2^62
+        double rb = sqrt(sumsq) / (double)scale + (double)eps;
+        rb = fmax(fmin(rb, 1e4), (double)eps);
+        const double dens_b = fmin(pow(rb, ipw_d), 1e6) * (1.0 + 1e-6);
+        const double lg = log2(fmax(dens_b, 1e-300) * (double)maxcnt);
+        int fb = isfinite(lg) ? (int)floor(62.0 - lg) : 0;
+        fb = fb < 0 ? 0 : (fb > 900 ? 900 : fb);
+        fx_scale = ldexp(1.0, fb);
+    }
+    W aE = 0, aD = 0;
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W rel = rel_of(force(i));
+        const W src = pw == (W)1 ? rel : fpow(rel, pw);
+        const W e = step <= 1 ? src : en[i] * md + md1 * src;
+        en[i] = e;
+        aE += e;
+        if (layout != L_NONE) {
+            const W d = density(rel);
+            aD += d;
+            if (layout == L_GENERIC) {
+                const unsigned long long v = (unsigned long long)llrint((double)d * fx_scale);
+                for (int k = 0; k < nd; ++k) atomicAdd(&ax[R.axis_off[k] + (i / R.stride[k]) % R.d.shape[k]], v);
+            }
+        }
+    }
+    if (layout == L_GENERIC) __threadfence();
+    W emean, gden;
+    {
+        double v[2] = {(double)aE, (double)aD};
+        block_sum<2>(v, red);
+        emean = (W)(v[0] / dn);
+        emean = emean > eps ? emean : eps;
+        gden = (W)(v[1] / dn);
+        gden = gden > eps ? gden : eps;
+    }
+    // per-axis log factors kappa * log(max(marginal mean / mean, eps)), in
+    // place; agent-scope atomic accesses keep the table-scratch case off the L1
+    double* axf = reinterpret_cast<double*>(ax);
+    if (layout == L_GENERIC) {
+        for (int64_t k = tid; k < R.sum_dims; k += SR_NT) {
+            int a_ = 0;
+            while (a_ + 1 < nd && k >= R.axis_off[a_ + 1]) ++a_;
+            const unsigned long long raw = __hip_atomic_load(&ax[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const W mean = (W)((double)(long long)raw / fx_scale / (dn / (double)R.d.shape[a_]));
+            const W r = mean / gden;
+            __hip_atomic_store(&axf[k], (double)(kappa * flog(r > eps ? r : eps)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __threadfence();
+        __syncthreads();
+    }
+    const bool metric_on = h.hash_metric_coupling != 0.0;
+    const W mpow = (W)(h.hash_metric_coupling / fmax(0.25, h.energy_power));
+    auto tangent = [&](W f, int64_t i) -> W {
+        W metric = 1;
+        if (metric_on) {
+            metric = fpow(en[i] / emean, mpow);
+            metric = metric < (W)0.08 ? (W)0.08 : (metric > (W)12 ? (W)12 : metric);
+        }
+        W inst = 1;
+        if (layout == L_1D) {
+            const W r = density(rel_of(f)) / gden;
+            inst = fexp(kappa * flog(r > eps ? r : eps));
+        } else if (layout == L_GENERIC) {
+            W s = 0;
+            for (int k = 0; k < nd; ++k)
+                s += (W)__hip_atomic_load(&axf[R.axis_off[k] + (i / R.stride[k]) % R.d.shape[k]], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+            inst = fexp(s);
+        }
+        if (layout != L_NONE) inst = inst < (W)0.08 ? (W)0.08 : (inst > (W)12 ? (W)12 : inst);
+        const W t = f / (scale * metric * inst + eps);
+        return t < (W)-1e4 ? (W)-1e4 : (t > (W)1e4 ? (W)1e4 : t);
+    };
+    const W clip = (W)h.drive_clip, iclip = (W)1 / clip, clip2 = clip * clip;
+
+    // ---- pass C ----
+    const W rd = (W)h.refractory_decay, rd1 = (W)(1.0 - h.refractory_decay), rg = (W)h.refractory_gain;
+    const W idk = (W)h.micro_impulse_decay, idk1 = (W)(1.0 - h.micro_impulse_decay);
+    W m[6] = {0, 0, 0, 0, 0, 0};
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W t = tangent(force(i), i);
+        const W r = rf[i] * rd + rd1 * (t < 0 ? -t : t);
+        rf[i] = r;
+        const W gate = (W)1 / ((W)1 + rg * r);
+        const W pr = im[i] * idk + idk1 * (t * gate);
+        im[i] = pr;
+        const W err = t - pr;
+        W rat, bnd, root;
+        shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
+        m[0] += err * err; m[1] += rat * rat; m[2] += rat * bnd;
+        m[3] += bnd * bnd; m[4] += pr * pr; m[5] += t * t;
+    }
+    double M[6];
+    for (int j = 0; j < 6; ++j) M[j] = (double)m[j];
+    block_sum<6>(M, red);
+    // cresso_v5.py:1406-1425 with every mean(x^2) taken from the sums above;
+    // mean(shaped^2) expands over rat^2, rat*bnd and bnd^2.
+    const W sur_now = (W)sqrt((double)((W)(M[0] / dn) + eps));
+    sur = reservoir(sur, sur_now, h.surprise_decay, step);
+    const W spike = (W)h.spike_mix / ((W)1 + sur);
+    const W a1 = (W)1 - spike;
+    const W ssq = (W)(((double)(a1 * a1) * M[1] + 2.0 * (double)(a1 * spike) * M[2] + (double)(spike * spike) * M[3]) / dn);
+    const W target = (W)sqrt((double)(ssq + eps));
+    const W rms_p = (W)sqrt((double)((W)(M[4] / dn) + eps));
+    const W rms_t = (W)sqrt((double)((W)(M[5] / dn) + eps));
+    const W kp = target / (rms_p > eps ? rms_p : eps);
+    const W kt = target / (rms_t > eps ? rms_t : eps);
+    const W ke = target / (sur_now > eps ? sur_now : eps);
+    const W dmix = (W)h.direct_force_mix / ((W)1 + (W)0.35 * sur);
+    const W mmix = (W)h.micro_drive_mix / ((W)1 + (W)0.25 * sur);
+    const W rmix = (W)h.residual_feedback_mix / ((W)1 + sur);
+    W cw = (W)1 - dmix - (W)0.5 * mmix;
+    cw = cw < (W)0 ? (W)0 : (cw > (W)1 ? (W)1 : cw);
+    const W cR = cw * a1, cBn = cw * spike, cT = dmix * kt, cP = mmix * kp, cE = rmix * ke;
+    auto drive = [&](W t, W pr) -> W {
+        W rat, bnd, root;
+        shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
+        return cR * rat + cBn * bnd + cT * t + cP * pr + cE * (t - pr);
+    };
+
+    // ---- pass D ----
+    W add = 0;
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W d = drive(tangent(force(i), i), im[i]);
+        add += d * d;
+    }
+    {
+        double v[1] = {(double)add};
+        block_sum<1>(v, red);
+        de = reservoir(de, (W)(v[0] / dn), h.reservoir_decay, step);
+    }
+    W gain = (W)h.target_update_rms / (W)sqrt((double)(de + eps));
+    gain = gain < (W)h.min_gain ? (W)h.min_gain : (gain > (W)h.max_gain ? (W)h.max_gain : gain);
+
+    // ---- pass E ---- (force is recomputed before any param store of this thread)
+    const W nlr = (W)(-h.lr);
+    for (int64_t i = tid; i < n; i += SR_NT) {
+        const W d = drive(tangent(force(i), i), im[i]);
+        const W u = to_w<W>(from_wd<PT>((double)(d * gain)));
+        p[i] = from_wd<PT>((double)(ldw<W>(p, i) + nlr * u));
+    }
+    if (tid == 0) {
+        *st_fr = fr; *st_de = de; *st_su = sur;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 struct Variant {
-    int pt, gt, kind;   // kind: 0 stream, 1 resident ROWGROUP, 2 resident COLBLOCK
+    int pt, gt, kind;   // kind: 0 stream, 1 resident ROWGROUP, 2 resident COLBLOCK, 3 micro field
     bool full;          // resident with numel == SR_RESIDENT_MAX: eligible for the FAST kernel
     bool operator==(const Variant& o) const { return pt == o.pt && gt == o.gt && kind == o.kind && full == o.full; }
 };
@@ -903,8 +1153,11 @@ int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec&
     if (n != d.numel)
         return fail(CRESSO_E_INVALID, "scalar route: numel %lld != product of shape %lld", (long long)d.numel, (long long)n);
     if (!d.param || !d.grad) return fail(CRESSO_E_INVALID, "scalar route: null param or grad pointer");
-    for (int i = 0; i < 8; ++i)
+    if (d.route != 0 && d.route != 1) return fail(CRESSO_E_INVALID, "scalar route: unknown route %d", d.route);
+    const int nstate = d.route == 1 ? 7 : 8;
+    for (int i = 0; i < nstate; ++i)
         if (!d.state[i]) return fail(CRESSO_E_INVALID, "scalar route: null state pointer %d", i);
+    if (d.route == 1 && d.ndim == 0) return fail(CRESSO_E_INVALID, "micro route: 0-dim tensors use the scalar route");
     auto okdt = [](int t) { return t == CRESSO_F32 || t == CRESSO_F16 || t == CRESSO_BF16 || t == CRESSO_F64; };
     if (!okdt(d.param_dtype) || !okdt(d.grad_dtype)) return fail(CRESSO_E_INVALID, "scalar route: unknown dtype code");
     if ((d.param_dtype == CRESSO_F64) != (d.grad_dtype == CRESSO_F64))
@@ -916,6 +1169,29 @@ int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec&
     const bool aligned = ((uintptr_t)d.param % (uintptr_t)(4 * dtype_bytes(d.param_dtype))) == 0 &&
                          ((uintptr_t)d.grad % (uintptr_t)(4 * dtype_bytes(d.grad_dtype))) == 0;
     const bool same = d.param_dtype == d.grad_dtype;
+    if (d.route == 1) {
+        // micro field: streaming kernel; axis sums in LDS up to MF_LDS_AXES entries
+        if (h.instant_metric_coupling == 0.0 || n <= 1) {
+            r.layout = L_NONE;
+        } else if (d.ndim == 1) {
+            r.layout = L_1D;
+        } else {
+            int64_t sum = 0, st = 1;
+            for (int a = d.ndim - 1; a >= 0; --a) {
+                r.stride[a] = st;
+                st *= d.shape[a];
+            }
+            for (int a = 0; a < d.ndim; ++a) {
+                r.axis_off[a] = sum;
+                sum += d.shape[a];
+            }
+            r.layout = L_GENERIC;
+            r.sum_dims = sum;
+            if (sum > MF_LDS_AXES) scratch = ((size_t)sum * sizeof(unsigned long long) + 255) & ~(size_t)255;
+        }
+        v = Variant{d.param_dtype, d.grad_dtype, 3, false};
+        return CRESSO_OK;
+    }
     int kind = 0;
     if (h.instant_metric_coupling == 0.0 || d.ndim == 0 || n <= 1) {
         r.layout = L_NONE;
@@ -997,15 +1273,19 @@ hipError_t launch_resident(int kind, bool fast, const ScalarRec* recs, int32_t* 
 }
 
 template <typename W, typename PT, typename GT>
-hipError_t launch_stream(const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first, int32_t cnt,
-                         unsigned char* table, const cresso_hyper& h, hipStream_t s) {
-    hipLaunchKernelGGL((scalar_stream_kernel<W, PT, GT>), dim3(cnt), dim3(SR_NT), 0, s, recs, steps, grads, first, table, h);
+hipError_t launch_stream(bool micro, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
+                         int32_t cnt, unsigned char* table, const cresso_hyper& h, hipStream_t s) {
+    if (micro)
+        hipLaunchKernelGGL((micro_kernel<W, PT, GT>), dim3(cnt), dim3(SR_NT), 0, s, recs, steps, grads, first, table, h);
+    else
+        hipLaunchKernelGGL((scalar_stream_kernel<W, PT, GT>), dim3(cnt), dim3(SR_NT), 0, s, recs, steps, grads, first,
+                           table, h);
     return hipGetLastError();
 }
 
 hipError_t dispatch(const Variant& v, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
                     int32_t cnt, size_t lds, unsigned char* table, const cresso_hyper& h, hipStream_t s) {
-    if (v.kind != 0) {
+    if (v.kind == 1 || v.kind == 2) {
         const bool fast = v.full && fast_hyper(h);
         if (v.pt == CRESSO_F32) return launch_resident<float, float>(v.kind, fast, recs, steps, grads, first, cnt, lds, h, s);
         if (v.pt == CRESSO_BF16)
@@ -1014,7 +1294,7 @@ hipError_t dispatch(const Variant& v, const ScalarRec* recs, int32_t* steps, con
         return hipErrorInvalidValue;
     }
 #define CRESSO_SR_CASE(PC, GC, W, PT, GT) \
-    if (v.pt == PC && v.gt == GC) return launch_stream<W, PT, GT>(recs, steps, grads, first, cnt, table, h, s);
+    if (v.pt == PC && v.gt == GC) return launch_stream<W, PT, GT>(v.kind == 3, recs, steps, grads, first, cnt, table, h, s);
     CRESSO_SR_CASE(CRESSO_F32, CRESSO_F32, float, float, float)
     CRESSO_SR_CASE(CRESSO_BF16, CRESSO_BF16, float, __hip_bfloat16, __hip_bfloat16)
     CRESSO_SR_CASE(CRESSO_F16, CRESSO_F16, float, __half, __half)

@@ -43,6 +43,8 @@ _INT_NONNEG = (("rank", "rank must be non-negative"), ("max_frequency", "max_fre
                ("hash_bins", "hash_bins must be non-negative"))
 
 _SCALAR_KEYS = ("q", "impulse", "metric_q", "metric_impulse", "force_rms", "drive_energy", "surprise", "action")
+# state order of a micro-route descriptor (route 1): dense fields, then the scalars
+_MICRO_KEYS = ("micro_energy", "micro_impulse", "micro_refractory", "force_rms", "drive_energy", "surprise", "action")
 _SPECTRAL_VEC_KEYS = ("q_cos", "q_sin", "p_cos", "p_sin", "metric_cos", "metric_sin", "metric_p_cos", "metric_p_sin",
                       "calcium_cos", "calcium_sin", "mode_confidence")
 
@@ -100,7 +102,8 @@ def theoretical_state_elements(shape: Sequence[int], rank: int, spectral: bool =
 
 
 class _ScalarBatch:
-    """Cached plan of the scalar-route tensors of one param group on one device."""
+    """Cached plan of the scalar-route and micro-route tensors of one param
+    group on one device (one library plan; micro tensors carry route 1)."""
 
     def __init__(self, params: List[Tensor], states: List[dict], group: dict, device: torch.device):
         lib = _native.load()
@@ -116,8 +119,10 @@ class _ScalarBatch:
             g = p.grad
             d.param = p.data_ptr()
             d.grad = g.data_ptr()
-            for j, k in enumerate(_SCALAR_KEYS):
+            micro = "micro_energy" in st
+            for j, k in enumerate(_MICRO_KEYS if micro else _SCALAR_KEYS):
                 d.state[j] = st[k].data_ptr()
+            d.route = _native.ROUTE_MICRO if micro else _native.ROUTE_SCALAR
             for a, s in enumerate(p.shape):
                 d.shape[a] = int(s)
             d.numel = p.numel()
@@ -262,6 +267,16 @@ class CRESSO5(Optimizer):
             st[k] = torch.zeros((), device=param.device, dtype=dtype)
         return st
 
+    def _init_micro(self, param: Tensor) -> dict:
+        """cresso_v5.py:893-898: common scalars plus three dense fields."""
+        st = self.state[param]
+        dtype = _state_dtype(param.dtype)
+        self._init_common(st, param.device, dtype)
+        st["micro_energy"] = torch.ones_like(param.detach(), dtype=dtype, memory_format=torch.contiguous_format)
+        st["micro_impulse"] = torch.zeros_like(param.detach(), dtype=dtype, memory_format=torch.contiguous_format)
+        st["micro_refractory"] = torch.zeros_like(param.detach(), dtype=dtype, memory_format=torch.contiguous_format)
+        return st
+
     def _init_spectral(self, param: Tensor, group: dict) -> dict:
         st = self.state[param]
         dtype = _state_dtype(param.dtype)
@@ -332,8 +347,13 @@ class CRESSO5(Optimizer):
                 raise RuntimeError("CRESSO5 needs contiguous parameters and gradients of the parameter's shape")
             route = self._route(p, group)
             if route == "micro":
-                raise NotImplementedError("CRESSO5 micro-field route (micro_field_max_size > 0) is not implemented "
-                                          "in the MI355X build")
+                st = self.state[p]
+                if len(st) == 0:
+                    st = self._init_micro(p)
+                else:
+                    self._check_micro_state(p, st)
+                scalar_ps.append(p)
+                continue
             if route == "spectral":
                 other = True
                 self._spectral(p, grad, group)
@@ -341,6 +361,8 @@ class CRESSO5(Optimizer):
             st = self.state[p]
             if len(st) == 0:
                 st = self._init_scalar(p)
+            elif "q" not in st:
+                raise RuntimeError("CRESSO5 scalar route: the parameter's state belongs to another route")
             elif st["q"].dtype != _state_dtype(p.dtype):
                 raise RuntimeError("CRESSO5 scalar state has dtype %s, expected %s" % (st["q"].dtype, _state_dtype(p.dtype)))
             scalar_ps.append(p)
@@ -357,6 +379,20 @@ class CRESSO5(Optimizer):
             batch = _ScalarBatch(scalar_ps, [self.state[p] for p in scalar_ps], group, scalar_ps[0].device)
             self._batches[(gi, "scalar")] = batch
         batch.run(group, [p.grad.data_ptr() for p in scalar_ps])
+
+    @staticmethod
+    def _check_micro_state(p: Tensor, st: dict) -> None:
+        want = _state_dtype(p.dtype)
+        for k in _MICRO_KEYS:
+            if k not in st:
+                raise RuntimeError(f"CRESSO5 micro route: state {k!r} is missing (the state belongs to another route)")
+            v = st[k]
+            if v.dtype != want or v.device != p.device:
+                raise RuntimeError(f"CRESSO5 micro route: state {k!r} is {v.dtype} on {v.device}, expected {want} on "
+                                   f"{p.device}")
+        for k in _MICRO_KEYS[:3]:
+            if st[k].shape != p.shape or not st[k].is_contiguous():
+                raise RuntimeError(f"CRESSO5 micro route: state {k!r} must be contiguous with the parameter's shape")
 
     def _spectral(self, param: Tensor, grad: Tensor, group: dict) -> None:
         if self._spectral_engine is None:

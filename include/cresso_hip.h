@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define CRESSO_HIP_ABI_VERSION 1
+#define CRESSO_HIP_ABI_VERSION 2
 
 /* error codes */
 #define CRESSO_OK 0
@@ -50,6 +50,7 @@ typedef struct cresso_hyper {
     double surprise_gain, surprise_decay, prediction_mix, novelty_mix;
     double surprise_brake, target_update_rms, min_gain, max_gain, drive_clip;
     double spike_mix, eps;
+    double micro_decay, micro_impulse_decay, micro_drive_mix;
     int32_t warmup_steps;
     int32_t maximize;     /* non-zero: the force is -grad (cresso_v5.py:835-836) */
 } cresso_hyper;
@@ -67,21 +68,28 @@ const char* cresso_hip_last_error(void);
  * Replaces scalar_update_2d_cuda (cresso_cuda_kernel.cu:3225-3605; binding
  * cresso_cuda.cpp:190, called at cresso_v5.py:1457-1500) and also covers the
  * ndim != 2 tensors that the reference sends to its PyTorch scalar path
- * (cresso_v5.py:1505-1582).  One launch updates `count` tensors: each
- * descriptor names a param, its grad and the 8 scalar states of
- * cresso_v5.py:885-891 + 857-862 (q, impulse, metric_q, metric_impulse,
- * force_rms, drive_energy, surprise, action), all updated in place.
+ * (cresso_v5.py:1505-1582), and the dense micro-field route of small tensors
+ * (micro_field_max_size > 0; PyTorch-only in the reference,
+ * cresso_v5.py:1355-1432).  One launch updates `count` tensors: each
+ * descriptor names a param, its grad and its states, all updated in place:
+ *   route 0 (scalar): the 8 scalar states of cresso_v5.py:885-891 + 857-862
+ *     (q, impulse, metric_q, metric_impulse, force_rms, drive_energy,
+ *     surprise, action);
+ *   route 1 (micro): micro_energy, micro_impulse, micro_refractory (dense,
+ *     the param's shape, cresso_v5.py:893-898), then force_rms, drive_energy,
+ *     surprise, action (0-dim); state[7] is unused.
  * ------------------------------------------------------------------------- */
 typedef struct cresso_scalar_desc {
     void* param;          /* contiguous, param_dtype                          */
     const void* grad;     /* contiguous, grad_dtype, same shape                */
-    void* state[8];       /* 0-dim state tensors, state dtype (f32, f64 for f64 params) */
+    void* state[8];       /* state tensors, state dtype (f32, f64 for f64 params) */
     int64_t shape[8];
     int64_t numel;
     int32_t ndim;         /* 0..8                                              */
     int32_t param_dtype;
     int32_t grad_dtype;
     int32_t step;         /* optimizer step BEFORE this call (state["step"])  */
+    int32_t route;        /* 0 scalar, 1 micro field                          */
 } cresso_scalar_desc;
 
 /* Opaque, host-side plan of one scalar-route batch: the descriptors
@@ -102,7 +110,8 @@ size_t cresso_scalar_plan_bytes(const cresso_scalar_plan* plan);
 int32_t cresso_scalar_plan_upload(cresso_scalar_plan* plan, void* dev_table, size_t table_bytes, void* stream);
 
 /* One optimizer step of every tensor of the plan: the fused scalar step of
- * cresso_v5.py:1434-1582 per tensor, param and the 8 states updated in place,
+ * cresso_v5.py:1434-1582 (route 0) or the micro-field step of
+ * cresso_v5.py:1355-1432 (route 1) per tensor, param and states updated in place,
  * each tensor's step counter advanced on the device (state["step"] += 1).
  *   grads : NULL to reuse the grad pointers already in the table, else a host
  *           array of `count` device pointers in descriptor order (autograd
