@@ -584,6 +584,16 @@ __device__ __forceinline__ unsigned long long to_fixed_s(float x) {
     return x < 0.f ? (0ull - u) : u;
 }
 
+// Any float x with |x| < 2^62 (already scaled by a power of two) to the
+// 64-bit two's complement integer floor(x): exact in double, the high word is
+// floor(x / 2^32) and the low word the remainder in [0, 2^32).
+__device__ __forceinline__ unsigned long long to_fixed_floor(float x) {
+    const double d = (double)x;
+    const double hi = floor(d * 2.3283064365386963e-10);
+    const double lo = fmin(fma(-hi, 4294967296.0, d), 4294967295.0);
+    return ((unsigned long long)(unsigned)(int)hi << 32) | (unsigned long long)(unsigned)lo;
+}
+
 __device__ __forceinline__ float reservoir_f(float old, float cur, double decay, int step) {
     if (step <= 1) return cur;
     return old * (float)decay + (float)(1.0 - decay) * cur;
@@ -1632,6 +1642,250 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// S3 on the matrix cores (MODE 1 tiles, RM <= 8, KC <= 12).  The element math
+// is sweep3_kernel's; the contractions run as v_mfma_f32_16x16x4f32 on 16 x 16
+// tiles, each wave owning 64 columns of the panel as 4 tile columns:
+//   metric and prediction fields: 3 + 3 MFMAs per tile (column-carrier form,
+//     A = the rows' alpha coefficients, B = the columns' carriers);
+//   t projection Z_q(col) = sum_rows a_q(row) t(row, col): 4 MFMAs per tile,
+//     A[q][k] = a_q(row 4k + r), B[k][col] = t(row 4k + r, col) for the
+//     tile's element r of each lane, accumulated over the panel in D[q][col].
+// Layouts (lane l, li = l % 16, lg = l / 16): A[i][k] from lane (i = li,
+// k = lg), B[k][j] from lane (j = li, k = lg), D[i][j] in lane (j = li),
+// register r: i = 4 lg + r.  Lane l processes rows 4 lg + r of column li of
+// each tile.  The loads of the next row of tiles are in flight while a row is
+// processed.
+// ---------------------------------------------------------------------------
+typedef float f32x4m __attribute__((ext_vector_type(4)));
+constexpr int SP_BQS = SP_NT + 16;   // row stride of sweep3m's LDS carrier table
+template <typename GT> __device__ __forceinline__ float ldg_el(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff);
+template <> __device__ __forceinline__ float ldg_el<float>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return bload1(r, voff, soff);
+}
+template <> __device__ __forceinline__ float ldg_el<__half>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return to_f(__builtin_bit_cast(__half, (unsigned short)bload1u16(r, voff, soff)));
+}
+template <>
+__device__ __forceinline__ float ldg_el<__hip_bfloat16>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return to_f(__builtin_bit_cast(__hip_bfloat16, (unsigned short)bload1u16(r, voff, soff)));
+}
+
+// Sum over each 16-lane DPP row (every lane of the row gets its row's total,
+// in a fixed order).
+__device__ __forceinline__ float row16_total(float v) {
+    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x124, 0xF>(v);  // row_ror:4
+    v = dpp_add<0x128, 0xF>(v);  // row_ror:8
+    return v;
+}
+
+template <int RM, int KC, typename GT>
+__global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
+    Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
+    const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
+    const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx, const unsigned long long* __restrict__ colfx,
+    const float* __restrict__ colfac, float* __restrict__ tbuf, double* __restrict__ part,
+    unsigned long long* __restrict__ hist, cresso_hyper h) {
+    static_assert(RM <= 8 && KC <= 12, "16 projection rows, three K-chunks of four carriers");
+    constexpr int RW = 2 * RM;
+    constexpr int KP = kcp<KC>();
+    extern __shared__ __align__(16) unsigned char dyn[];
+    __shared__ float red[4 * NV3];
+    const Tile t = tile_of(g);
+    const int B = g.B;
+    const int TB = 2 * B;
+    const int nr = g.PR;
+    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int li = l & 15, lg = l >> 4;
+    const int64_t base = panel_base(g, t);
+    const uint32_t cols = (uint32_t)g.cols;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(grad + base, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(GT)));
+    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tbuf + base, (uint32_t)((int64_t)nr * g.cols * 4));
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(reinterpret_cast<const uint16_t*>(bins) + base, (uint32_t)((int64_t)nr * g.cols * 2));
+    const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
+    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vt = lane_el * 4u, vb = lane_el * 2u;
+    // tile (tr, tc), lane element r: panel element (16 tr + 4 lg + r, 64 wv + 16 tc + li)
+    auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
+    // one register set, refilled tile by tile: the loads of tile (tr + 1, tc)
+    // go out as soon as tile (tr, tc) is done, three tiles ahead of their use
+    float xv[16];
+    uint32_t bv[16];
+    auto load_tile = [&](int tr, int tc) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t o = tile_off(tr, tc, r);
+            xv[4 * tc + r] = ldg_el<GT>(rg, vg, o * (uint32_t)sizeof(GT));
+            bv[4 * tc + r] = bload1u16(rb, vb, o * 2u);
+        }
+    };
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) load_tile(0, tc);
+    // LDS as sweep3_kernel: histogram copies [TB][NH] u64 | log hash metric [TB]
+    //      | row metric factor [PR] | (16-aligned) alpha [PR][2][KP] | row factors [PR][RW]
+    constexpr int NH = SP_NHIST;
+    const int hc = (int)(threadIdx.x & (SP_NHIST - 1));
+    unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
+    float* s_lt = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
+    float* s_rf = s_lt + TB;
+    float* s_al = reinterpret_cast<float*>(dyn + lds_al_off(g));
+    float* s_ar = s_al + 2 * KP * g.PR;
+    const float eps = (float)h.eps;
+    const float kappa = ctrl->kappa, gden = ctrl->gden;
+    for (int i = threadIdx.x; i < TB; i += SP_NT) {
+        s_lt[i] = lt[i];
+#pragma unroll
+        for (int c = 0; c < NH; ++c) s_hist[i * NH + c] = 0ull;
+    }
+    for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
+        s_rf[lr] = marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps);
+    stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
+    // the block's column carriers (B operands of the reconstructions) and
+    // column instant-metric factors, in LDS: [KP][SP_BQS] (rows padded so that
+    // the 4 lane groups of a wave read distinct banks) | [SP_NT]
+    float* s_bq = s_ar + RW * g.PR;
+    float* s_ec = s_bq + KP * SP_BQS;
+    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
+    {
+        const int64_t c = (int64_t)t.slab * SP_NT + threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < KP; ++k) s_bq[k * SP_BQS + threadIdx.x] = k < KC ? coltab[(size_t)k * g.cols + c] : 0.f;
+        s_ec[threadIdx.x] = g.ntrail == 1 ? marg_factor(colfx[c], g.hs_col, (double)g.rows, gden, kappa, eps) : colfac[c];
+    }
+    const float* __restrict__ bql = s_bq + lg * SP_BQS + 64 * wv + li;   // + 4 kc SP_BQS + 16 tc
+    const float* __restrict__ ecl = s_ec + 64 * wv + li;                  // + 16 tc
+    {
+        const float (*const r0[2])[2] = {ctrl->rc[0], ctrl->rc[1]};
+        const float (*const r1[2])[2] = {nullptr, nullptr};
+        const float w0[2] = {1.f, 1.f}, w1[2] = {0.f, 0.f};
+        alpha_rows<RM, KC>(g, meta, s_ar, nr, r0, w0, r1, w1, s_al);   // ends with a barrier
+    }
+    const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
+    const float scale = ctrl->scale;
+    const float mcoup = (float)h.metric_coupling;
+    const float sg = h.maximize ? -1.f : 1.f;
+    const float tm = (float)h.transport_mix;
+    const float hs = (float)ctrl->hs_P;
+    const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
+    const float k2 = -2.8853900817779268f * iclip;   // -2 log2(e) / clip
+    f32x4m zacc[4];
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) zacc[tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
+    float m_ee = 0.f, m_t = 0.f, m_tt = 0.f, m_rr = 0.f, m_bb = 0.f, m_oo = 0.f, m_rb = 0.f, m_ro = 0.f,
+          m_bo = 0.f, m_tr = 0.f, m_tb = 0.f, m_to = 0.f;
+    auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const float* aM, const float* aQ) {
+        f32x4m lm = {cM, cM, cM, cM}, pred = {cP, cP, cP, cP};
+#pragma unroll
+        for (int kc = 0; kc < 3; ++kc) {
+            const float bq = bql[4 * kc * SP_BQS + 16 * tc];
+            lm = __builtin_amdgcn_mfma_f32_16x16x4f32(aM[kc], bq, lm, 0, 0, 0);
+            pred = __builtin_amdgcn_mfma_f32_16x16x4f32(aQ[kc], bq, pred, 0, 0, 0);
+        }
+        const float ec = ecl[16 * tc];
+        float tvs[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float f = sg * x[r];
+            // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
+            const float M = med3f(fexp(mcoup * med3f(lm[r], -3.0f, 3.0f)), 0.06f, 16.0f);
+            float den = scale * M;
+            den = den * med3f(s_rf[16 * tr + 4 * lg + r] * ec, 0.08f, 12.0f);
+            const float lsum = s_lt[b[r] & 0xffu] + s_lt[B + (b[r] >> 8)];
+            den = den * med3f(fexp(lsum * 0.5f), 0.08f, 12.0f);
+            const float tv = med3f(f * frcp(den + eps), -1.0e4f, 1.0e4f);
+            bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
+            tvs[r] = tv;
+            const float err = tv - pred[r];
+            const float P = err + tm * tv;
+            m_ee += err * err;
+            m_t += tv;
+            m_tt += tv * tv;
+            const float at = fabsf(tv);
+            const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+            m_rr = fmaf(z.rat, z.rat, m_rr); m_bb = fmaf(z.th, z.th, m_bb); m_oo = fmaf(z.root, z.root, m_oo);
+            m_rb = fmaf(z.rat, z.th, m_rb); m_ro = fmaf(z.rat, z.root, m_ro); m_bo = fmaf(z.th, z.root, m_bo);
+            m_tr = fmaf(at, z.rat, m_tr); m_tb = fmaf(at, z.th, m_tb); m_to = fmaf(at, z.root, m_to);
+            const unsigned long long v = to_fixed_floor(P * hs);
+            atomicAdd(&s_hist[(b[r] & 0xffu) * NH + hc], v);
+            atomicAdd(&s_hist[(B + (b[r] >> 8)) * NH + hc], v);
+        }
+        // A of the projection: a_li(row 16 tr + 4 lg + r)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float aJ = li < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (li < RW ? li : 0)] : 0.f;
+            zacc[tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJ, tvs[r], zacc[tc], 0, 0, 0);
+        }
+        pin1(m_ee); pin1(m_t); pin1(m_tt); pin1(m_rr); pin1(m_bb); pin1(m_oo);
+        pin1(m_rb); pin1(m_ro); pin1(m_bo); pin1(m_tr); pin1(m_tb); pin1(m_to);
+        elem_fence();
+    };
+    const int ntr = nr / 16;
+    for (int tr = 0; tr < ntr; ++tr) {
+        // A operands of this row of tiles' fields: alpha_{4 kc + lg}(row 16 tr + li)
+        const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
+        float aM[3], aQ[3];
+#pragma unroll
+        for (int kc = 0; kc < 3; ++kc) {
+            aM[kc] = alr[4 * kc];
+            aQ[kc] = alr[KP + 4 * kc];
+        }
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) {
+            tile(tr, tc, xv + 4 * tc, bv + 4 * tc, aM, aQ);
+            if (tr + 1 < ntr) load_tile(tr + 1, tc);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < TB; i += SP_NT) {
+        unsigned long long v = 0ull;
+#pragma unroll
+        for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
+        if (v) atomicAdd(&hist[i], v);
+    }
+    Partials P{red, 15 + 2 * g.R, NV3};
+    const float mm[13] = {m_ee, 0.f, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
+#pragma unroll
+    for (int k = 0; k < 13; ++k) P.add(k, mm[k]);
+    P.add(13, 0.f);
+    P.add(14, 0.f);
+    // projection: lane group lg holds Z_{4 lg + j}(col), j < 4, i.e. both
+    // components of modes 2 lg and 2 lg + 1, for its 4 columns; each mode's raw
+    // C/S (proj_finish's form) is summed over the columns, then over the 16
+    // lanes of the group, into slots 15 + 4 lg + j.
+    float cs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const int r = 2 * lg + half;
+        if (r < g.R) {
+            const ModeMeta m = meta[r];
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) {
+                const int64_t c = colw + 16 * tc + li;
+                // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
+                const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
+                const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
+                const float z1 = zacc[tc][2 * half], z2 = zacc[tc][2 * half + 1];
+                if (m.type == M_ADD) {
+                    cs[2 * half] += b1 * z1 - b2 * z2;
+                    cs[2 * half + 1] += b1 * z2 + b2 * z1;
+                } else {
+                    cs[2 * half] += b1 * z1;
+                    cs[2 * half + 1] += b2 * z2;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float s = row16_total(cs[j]);
+        const int slot = 4 * lg + j;
+        if (li == 15 && slot < 2 * g.R) red[wv * P.V + 15 + slot] = s;
+    }
+    P.flush(part);
+}
+
+// ---------------------------------------------------------------------------
 // F3: surprise, hash impulse, confidence, contact, and every drive-shaping
 // coefficient that does not need the hash prediction's rms
 // ---------------------------------------------------------------------------
@@ -2022,7 +2276,6 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
 // elementwise drive math is unchanged.  The loads of the next tile are in
 // flight while a tile is processed.
 // ---------------------------------------------------------------------------
-typedef float f32x4m __attribute__((ext_vector_type(4)));
 template <int RM, int KC>
 __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
@@ -2428,6 +2681,7 @@ size_t lds_sweep2(const Geom& g, int rw) {
 size_t lds_sweep3(const Geom& g, int kp, int rw) {
     return lds_al_off(g) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
 }
+size_t lds_sweep3m(const Geom& g, int kp, int rw) { return lds_sweep3(g, kp, rw) + sizeof(float) * ((size_t)kp * SP_BQS + SP_NT); }
 size_t lds_sweep4(const Geom& g, int kp, int rw) {
     return ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
 }
@@ -2496,12 +2750,21 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
                        ctrl, step, hash_on, hard, h);
     if (axes_on && g.ntrail > 1)
         hipLaunchKernelGGL(marg_axes_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, colfx, terms, colfac, ctrl, (float)h.eps);
+    if constexpr (RM <= 8 && KC <= 12) {
+        const size_t l3m = lds_sweep3m(g, kcp<KC>(), 2 * RM);
+        if (fast && l3m <= SP_LDS_MAX) {
+            hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl, lt,
+                               rowfx, colfx, colfac, tbuf, part, hist, h);
+            goto swept3;
+        }
+    }
     if (fast)
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 1>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
     else
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 0>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
+swept3:
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3), dim3(256), 0, s, part, g.nblk, NV3, sums);
     hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
                        step, hash_on, hard, echo_on, h);
