@@ -1774,14 +1774,28 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
     for (int tc = 0; tc < 4; ++tc) zacc[tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
     float m_ee = 0.f, m_t = 0.f, m_tt = 0.f, m_rr = 0.f, m_bb = 0.f, m_oo = 0.f, m_rb = 0.f, m_ro = 0.f,
           m_bo = 0.f, m_tr = 0.f, m_tb = 0.f, m_to = 0.f;
-    auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const float* aM, const float* aQ) {
-        f32x4m lm = {cM, cM, cM, cM}, pred = {cP, cP, cP, cP};
+    // metric and prediction fields of tile column tc of the current row of tiles
+    float aM[3], aQ[3];
+    auto recon = [&](int tc, f32x4m& lm, f32x4m& pred) {
+        lm = f32x4m{cM, cM, cM, cM};
+        pred = f32x4m{cP, cP, cP, cP};
 #pragma unroll
         for (int kc = 0; kc < 3; ++kc) {
             const float bq = bql[4 * kc * SP_BQS + 16 * tc];
             lm = __builtin_amdgcn_mfma_f32_16x16x4f32(aM[kc], bq, lm, 0, 0, 0);
             pred = __builtin_amdgcn_mfma_f32_16x16x4f32(aQ[kc], bq, pred, 0, 0, 0);
         }
+    };
+    // A operands of row of tiles tr: alpha_{4 kc + lg}(row 16 tr + li) of both fields
+    auto row_alpha = [&](int tr) {
+        const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
+#pragma unroll
+        for (int kc = 0; kc < 3; ++kc) {
+            aM[kc] = alr[4 * kc];
+            aQ[kc] = alr[KP + 4 * kc];
+        }
+    };
+    auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const f32x4m& lm, const f32x4m& pred) {
         const float ec = ecl[16 * tc];
         float tvs[4];
 #pragma unroll
@@ -1821,19 +1835,25 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
         elem_fence();
     };
     const int ntr = nr / 16;
+    f32x4m lmA, prA, lmB, prB;
+    row_alpha(0);
+    recon(0, lmA, prA);
     for (int tr = 0; tr < ntr; ++tr) {
-        // A operands of this row of tiles' fields: alpha_{4 kc + lg}(row 16 tr + li)
-        const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
-        float aM[3], aQ[3];
-#pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
-            aM[kc] = alr[4 * kc];
-            aQ[kc] = alr[KP + 4 * kc];
-        }
+        // the fields of tile (tr, tc + 1), or of (tr + 1, 0), go to the matrix
+        // cores before tile (tr, tc)'s element math, which reads the fields
+        // issued one tile earlier
 #pragma unroll
         for (int tc = 0; tc < 4; ++tc) {
-            tile(tr, tc, xv + 4 * tc, bv + 4 * tc, aM, aQ);
+            if (tc < 3) {
+                recon(tc + 1, lmB, prB);
+            } else if (tr + 1 < ntr) {
+                row_alpha(tr + 1);
+                recon(0, lmB, prB);
+            }
+            tile(tr, tc, xv + 4 * tc, bv + 4 * tc, lmA, prA);
             if (tr + 1 < ntr) load_tile(tr + 1, tc);
+            lmA = lmB;
+            prA = prB;
         }
     }
     __syncthreads();
