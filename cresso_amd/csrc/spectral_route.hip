@@ -1246,17 +1246,14 @@ __device__ void set_recon_lanes(const Geom& g, const double* __restrict__ stats,
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
 }
 
-// Sum over the R lanes of wave 0 in lane order (fp64).
-__device__ double lanes_sum(double v, int R, double* s_tmp) {
+// Sum over lanes 0..R-1 of a fully active wave (fp64), in the fixed order of
+// the DPP wave reduction, returned to every lane.
+__device__ double lanes_sum(double v, int R) {
     const int r = threadIdx.x & 63;
-    if (r < R) s_tmp[r] = v;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    double s = 0.0;
-    for (int q = 0; q < R; ++q) s += s_tmp[q];
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    return s;
+    const double t = wave_total_d(r < R ? v : 0.0);
+    const int lo = __builtin_amdgcn_readlane(__double2loint(t), 63);
+    const int hi = __builtin_amdgcn_readlane(__double2hiint(t), 63);
+    return __hiloint2double(hi, lo);
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -1275,7 +1272,6 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(Geom g, const ModeMeta* 
     __shared__ double red[SP_FN_NT / 64];
     __shared__ float s_emean[SP_MAXT];
     __shared__ float s_tmpf[64];
-    __shared__ double s_tmpd[64];
     const int tid = threadIdx.x;
     const float eps = (float)h.eps;
     const double n = (double)g.n;
@@ -1371,7 +1367,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(Geom g, const ModeMeta* 
             pm = shrink * gt * (fabs((double)qc) * s_bounds[2 * r] + fabs((double)qs) * s_bounds[2 * r + 1]);
         }
         set_recon_lanes(g, s_stats, ctrl->rc[1], &ctrl->rconst[1], qc, qs, gt, s_tmpf, ctrl->wpred);
-        const double pmax = lanes_sum(pm, g.R, s_tmpd);
+        const double pmax = lanes_sum(pm, g.R);
         if (r == 0) {
             // instant metric: mean density and coupling (cresso_v5.py:243-262)
             ctrl->gden = (float)fmax(sumD / n, (double)eps);
@@ -1912,7 +1908,7 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
 // Contact oscillator of one bank (cresso_v5.py:914-943), lane r = mode r; the
 // energy and power sums over modes are summed in mode order.
 __device__ void contact_bank_lanes(float& q, float& p, float port, float omega, float& calcium, float& action, float S,
-                                   int R, const cresso_hyper& h, double* s_tmp) {
+                                   int R, const cresso_hyper& h) {
     const int r = threadIdx.x & 63;
     const bool on = r < R;
     const float dt = (float)h.dt;
@@ -1930,7 +1926,7 @@ __device__ void contact_bank_lanes(float& q, float& p, float port, float omega, 
         e2 = (double)(oq * oq);
         pw = (double)(gp * p);
     }
-    const double E1 = lanes_sum(e1, R, s_tmp), E2 = lanes_sum(e2, R, s_tmp), PW = lanes_sum(pw, R, s_tmp);
+    const double E1 = lanes_sum(e1, R), E2 = lanes_sum(e2, R), PW = lanes_sum(pw, R);
     if (R > 0) {
         const float energy = 0.5f * ((float)(E1 / R) + (float)(E2 / R));
         const float power = (float)(PW / R);
@@ -1972,7 +1968,6 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
     __shared__ double s_u[3][2 * SP_MAXR];  // weights of pred, pred', echo
     __shared__ float s_wp[2 * SP_MAXR], s_we[2 * SP_MAXR];
     __shared__ float s_tmpf[64];
-    __shared__ double s_tmpd[64];
     const int tid = threadIdx.x;
     const double n = (double)g.n;
     const int R = g.R, V = 2 * g.R;
@@ -2060,8 +2055,8 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
         }
         // contact on the cos bank then the sin bank with the shared action
         float action = s_scal[1];
-        contact_bank_lanes(qc, pcv, pc, om, cac, action, sur, R, h, s_tmpd);
-        contact_bank_lanes(qs, psv, ps, om, cas, action, sur, R, h, s_tmpd);
+        contact_bank_lanes(qc, pcv, pc, om, cac, action, sur, R, h);
+        contact_bank_lanes(qs, psv, ps, om, cas, action, sur, R, h);
         set_recon_lanes(g, s_stats, ctrl->rc[2], &ctrl->rconst[2], qc, qs, gt, s_tmpf, s_wp);
         if (echo_on) set_recon_lanes(g, s_stats, ctrl->rc[3], &ctrl->rconst[3], ecs, ess, 1.0f, s_tmpf, s_we);
         if (on) {
@@ -2096,8 +2091,8 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
             q3 = du * (s_ec[v] - gu);    // -> mean(err D)
             q4 = s_u[1][v] * s_ec[v];    // -> mean(t pred')
         }
-        const double Q0 = lanes_sum(q0, V, s_tmpd), Q1 = lanes_sum(q1, V, s_tmpd), Q2 = lanes_sum(q2, V, s_tmpd);
-        const double Q3 = lanes_sum(q3, V, s_tmpd), Q4 = lanes_sum(q4, V, s_tmpd);
+        const double Q0 = lanes_sum(q0, V), Q1 = lanes_sum(q1, V), Q2 = lanes_sum(q2, V);
+        const double Q3 = lanes_sum(q3, V), Q4 = lanes_sum(q4, V);
         if (r == 0) {
             const float S = sur;
             // shaped / core coefficients from the moments of t (cresso_v5.py:1315-1337)
