@@ -20,7 +20,8 @@
 //   Z1_r = sum_rows a1_r x, Z2_r = sum_rows a2_r x over the lane's column,
 //   combined with the lane's b values at the end; reconstruction is
 //   out = alpha_0(row) + sum_k alpha_k(row) b_k(col) with alpha built per row
-//   panel in LDS from the mode coefficients.
+//   panel in LDS from the mode coefficients.  On the fast path (MODE 1) sweeps
+//   3 and 4 run both as 16x16x4 fp32 MFMA tiles.
 // * Step = 5 sweeps over the field, each followed by a one-block finalize
 //   (deterministic fixed-order fp64 reductions of per-block partials) that
 //   runs the rank-level recurrences and writes the next sweep's coefficients:
@@ -28,12 +29,13 @@
 //     S2 density: hash histograms (64-bit fixed point, integer atomics),
 //        log-density projection, axis density sums -> F2 hash metric tables,
 //        metric oscillator, recon coefficients; M1 instant-metric factors
-//     S3 tangent t (stored), surprise, port projection, port histograms,
-//        echo projection, 13 moments of t -> F3 surprise, hash impulse,
-//        confidence, contact oscillator, core coefficients
-//     S4 the 22 cross moments of {core, pred, nov, err, echo, hash} that give
-//        every remaining RMS and the drive energy in closed form -> F4 gain
-//     S5 param -= lr * cast(drive * gain)
+//     S3 tangent t (stored), t projection, port histograms, 13 moments of t
+//        -> F3 surprise, port projection (1 + tm) mean(t Xn) - G u_pred from
+//        the basis Gram matrix G, hash impulse, confidence, contact
+//        oscillator, drive coefficients (every RMS in closed form)
+//     S4 drive without the hash term (written over t); sum d^2, sum d h,
+//        sum h^2 -> F4 drive energy, gain
+//     S5 param -= lr * cast((d + c5 h) * gain)
 #include "common.hpp"
 
 #include <algorithm>
