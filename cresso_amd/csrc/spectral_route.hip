@@ -34,8 +34,10 @@
 //        the basis Gram matrix G, hash impulse, confidence, contact
 //        oscillator, drive coefficients (every RMS in closed form)
 //     S4 drive without the hash term (written over t); sum d^2, sum d h,
-//        sum h^2 -> F4 drive energy, gain
-//     S5 param -= lr * cast((d + c5 h) * gain)
+//        sum h^2 -> F4 drive energy, gain.  Fast path: F3 already has the
+//        hash term's RMS in closed form (bin co-occurrence counts), so S4
+//        writes the full drive and sums drive^2
+//     S5 param -= lr * cast((d + c5 h) * gain), resp. cast(drive * gain)
 #include "common.hpp"
 
 #include <algorithm>
@@ -97,7 +99,7 @@ struct Geom {
 };
 
 struct Offs {
-    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, bins, tbuf, part, sums, hist, lt, imp, rowfx,
+    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins, tbuf, part, sums, hist, lt, imp, rowfx,
         colfx, colfac, terms, ctrl, total;
 };
 
@@ -430,6 +432,37 @@ __global__ __launch_bounds__(256) void ws_bins_kernel(Geom g, unsigned char* __r
     if (priv)
         for (int i = threadIdx.x; i < TB; i += blockDim.x)
             if (s_cnt[i]) atomicAdd(&counts[i], (unsigned long long)s_cnt[i]);
+}
+
+// Co-occurrence counts of the two tables' bins, cooc[b0][b1] = #{i : bin0(i) =
+// b0, bin1(i) = b1} (data independent, once per shape).  With them the hash
+// prediction's sum of squares is a closed form over the impulse tables:
+//   sum_i ((imp0[b0] + imp1[b1]) / 2)^2
+//     = (sum_b cnt0 imp0^2 + sum_b cnt1 imp1^2 + 2 sum_{b0,b1} cooc imp0 imp1) / 4.
+// Used when there are two tables of one-byte bins (the sweeps' fast path).
+__host__ __device__ inline bool cooc_closed(const Geom& g) { return g.T == 2 && g.bpb == 1 && g.binbytes == 2; }
+constexpr int WS_COOC_LDS = 16384;  // u32 counters privatised per block (B <= 128)
+__global__ __launch_bounds__(256) void ws_cooc_kernel(Geom g, const uint16_t* __restrict__ bins,
+                                                      unsigned long long* __restrict__ cooc) {
+    __shared__ unsigned int s_cnt[WS_COOC_LDS];
+    const int BB = g.B * g.B;
+    const bool priv = BB <= WS_COOC_LDS;
+    if (priv)
+        for (int i = threadIdx.x; i < BB; i += blockDim.x) s_cnt[i] = 0u;
+    __syncthreads();
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
+        const unsigned v = bins[i];
+        const int k = (int)(v & 0xffu) * g.B + (int)(v >> 8);
+        if (priv)
+            atomicAdd(&s_cnt[k], 1u);
+        else
+            atomicAdd(&cooc[k], 1ull);
+    }
+    __syncthreads();
+    if (priv)
+        for (int i = threadIdx.x; i < BB; i += blockDim.x)
+            if (s_cnt[i]) atomicAdd(&cooc[i], (unsigned long long)s_cnt[i]);
 }
 
 __device__ __forceinline__ uint64_t load_bins(const unsigned char* __restrict__ bins, int64_t e, int binbytes) {
@@ -1964,7 +1997,8 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
                                                         unsigned long long* __restrict__ hist,
                                                         const unsigned long long* __restrict__ counts,
                                                         float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
-                                                        int step, int hash_on, int hard, int echo_on, cresso_hyper h) {
+                                                        const unsigned long long* __restrict__ cooc, int step, int hash_on,
+                                                        int hard, int echo_on, int c5_closed, cresso_hyper h) {
     __shared__ double s_m[NV3];
     __shared__ double s_ec[2 * SP_MAXR];    // mean(t Xn_v)
     __shared__ double s_u[3][2 * SP_MAXR];  // weights of pred, pred', echo
@@ -1979,6 +2013,9 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
     __shared__ double s_stats[4 * SP_MAXR];
     __shared__ float s_mode[SP_MAXR][9];
     __shared__ float s_scal[2];
+    __shared__ float s_impv[2 * 256];
+    __shared__ double s_hhw[SP_FN_NT / 64];
+    __shared__ float s_srms;
     for (int i = tid; i < V * V; i += SP_FN_NT) s_gram[i] = gram[i];
     for (int i = tid; i < 4 * R; i += SP_FN_NT) s_stats[i] = stats[i];
     for (int i = tid; i < 9 * R; i += SP_FN_NT) {
@@ -2006,8 +2043,10 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
             st.hash_refractory[i] = ref;
             st.hash_impulse[i] = im;
             imp_tab[i] = im;
+            if (c5_closed) s_impv[i] = im;
         }
     }
+    if (c5_closed) __syncthreads();   // s_impv complete
     __shared__ double s_gu[2 * SP_MAXR];     // G u_pred: mean(pred Xn_v)
     if (tid < 64) {
         const int r = tid;
@@ -2149,6 +2188,30 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
             ctrl->k_nov = (float)(c2 * (double)clip);
             ctrl->nscale = 1.0f / (clip * (1.0f + S));
             ctrl->srms = srms;
+            s_srms = srms;
+        }
+    } else if (c5_closed) {
+        // waves 1.. (while wave 0 runs the mode lanes): the hash prediction's
+        // sum of squares over the field, sum_i ((imp0[b0] + imp1[b1]) / 2)^2,
+        // in closed form from the bin and co-occurrence counts
+        const int B = g.B;
+        const int t1 = tid - 64, n1 = SP_FN_NT - 64;
+        double a = 0.0;
+        for (int k = t1; k < B * B; k += n1)
+            a += (double)cooc[k] * (2.0 * (double)s_impv[k / B] * (double)s_impv[B + k % B]);
+        for (int k = t1; k < 2 * B; k += n1) a += (double)counts[k] * ((double)s_impv[k] * (double)s_impv[k]);
+        const double w = wave_total_d(a);
+        if ((tid & 63) == 63) s_hhw[(tid >> 6) - 1] = w;
+    }
+    if (c5_closed) {
+        __syncthreads();
+        if (tid == 0) {
+            double hh = 0.0;
+            for (int w = 0; w < SP_FN_NT / 64 - 1; ++w) hh += s_hhw[w];
+            hh *= 0.25;
+            // the hash term's coefficient as fin4_kernel forms it, from sum hp^2
+            const float khp = s_srms / fmaxf(sqrtf((float)(hh / n) + eps), eps);
+            ctrl->k_hash = (float)(hard ? h.hash_drive_mix * (double)khp : 0.0);
         }
     }
 }
@@ -2291,7 +2354,9 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
 //   D[i][j]                          lane l, register r: i = 4 (l / 16) + r, j = l % 16
 // so lane l processes rows 4 (l/16) + r of column l % 16 of each tile, and the
 // elementwise drive math is unchanged.  The loads of the next tile are in
-// flight while a tile is processed.
+// flight while a tile is processed.  The hash term's coefficient c5 is known
+// here (fin3 forms the hash prediction's RMS from the co-occurrence counts),
+// so the full drive is written and sum drive^2 is summed directly.
 // ---------------------------------------------------------------------------
 template <int RM, int KC>
 __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
@@ -2364,7 +2429,8 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
     const float k_rat = ctrl->k_rat, k_ths = ctrl->k_ths, k_root = ctrl->k_root, k_t = ctrl->k_t, k_nov = ctrl->k_nov;
     const float k2 = -2.8853900817779268f * iclip;
     const float k2n = -2.8853900817779268f * ctrl->nscale;
-    float a_dd = 0.f, a_dh = 0.f, a_hh = 0.f;
+    const float c5 = ctrl->k_hash;   // set by fin3 (closed-form hash-term RMS)
+    float a_dd = 0.f;
     auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const float* aP, const float* aX) {
         f32x4m pred = {cQ, cQ, cQ, cQ}, mixed = {cX, cX, cX, cX};
 #pragma unroll
@@ -2380,14 +2446,12 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
             const float at = fabsf(tv);
             const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
             const float core = xorsign(fmaf(k_t, at, fmaf(k_root, z.root, fmaf(k_ths, z.th, k_rat * z.rat))), tv);
-            const float d = fmaf(k_nov, nov, core + mixed[r]);
+            const float hp = (s_imp[b[r] & 0xffu] + s_imp[B + (b[r] >> 8)]) * 0.5f;
+            const float d = fmaf(c5, hp, fmaf(k_nov, nov, core + mixed[r]));
             bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
             a_dd = fmaf(d, d, a_dd);
-            const float hp = (s_imp[b[r] & 0xffu] + s_imp[B + (b[r] >> 8)]) * 0.5f;
-            a_dh = fmaf(d, hp, a_dh);
-            a_hh = fmaf(hp, hp, a_hh);
         }
-        pin1(a_dd); pin1(a_dh); pin1(a_hh);
+        pin1(a_dd);
         elem_fence();
     };
     auto row_tiles = [&](int tr, const float* x, const uint32_t* b) {
@@ -2411,8 +2475,8 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
     }
     Partials P{red, 3, NV4};
     P.add(0, a_dd);
-    P.add(1, a_dh);
-    P.add(2, a_hh);
+    P.add(1, 0.f);
+    P.add(2, 0.f);
     P.flush(part);
 }
 
@@ -2420,16 +2484,23 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
 //   sum drive^2 = sum d^2 + 2 c5 sum d hp + c5^2 sum hp^2
 __global__ __launch_bounds__(SP_FN_NT) void fin4_kernel(Geom g, const double* __restrict__ part, SpecState st,
                                                         Ctrl* __restrict__ ctrl, int step, int hash_on, int hard,
-                                                        cresso_hyper h) {
+                                                        int c5_closed, cresso_hyper h) {
     __shared__ double s_m[NV4];
     reduce_bm<NV4>(part, g.nblk, 3, s_m);
     if (threadIdx.x != 0) return;
     const double n = (double)g.n;
     const float eps = (float)h.eps;
-    float khp = 0.f;
-    if (hard && hash_on) khp = ctrl->srms / fmaxf(sqrtf((float)(s_m[2] / n) + eps), eps);
-    const double c5 = hard ? h.hash_drive_mix * (double)khp : 0.0;
-    const double dd = s_m[0] + 2.0 * c5 * s_m[1] + c5 * c5 * s_m[2];
+    double c5, dd;
+    if (c5_closed) {
+        // sweep 4 summed the full drive (the hash term's coefficient came from fin3)
+        c5 = (double)ctrl->k_hash;
+        dd = s_m[0];
+    } else {
+        float khp = 0.f;
+        if (hard && hash_on) khp = ctrl->srms / fmaxf(sqrtf((float)(s_m[2] / n) + eps), eps);
+        c5 = hard ? h.hash_drive_mix * (double)khp : 0.0;
+        dd = s_m[0] + 2.0 * c5 * s_m[1] + c5 * c5 * s_m[2];
+    }
     const float de_now = (float)(fmax(dd, 0.0) / n);
     const float de = reservoir_f(*st.drive_energy, de_now, h.reservoir_decay, step);
     *st.drive_energy = de;
@@ -2672,6 +2743,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.gram = take(sizeof(double) * 4 * (size_t)g.R * g.R);
     o.gpart = take(sizeof(double) * (size_t)g.nblkg * (4 * (size_t)g.R * g.R + (size_t)g.K * g.K));
     o.counts = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
+    o.cooc = take(cooc_closed(g) ? sizeof(unsigned long long) * (size_t)g.B * g.B : 0);
     o.bins = take((size_t)g.binbytes * (size_t)g.n);
     o.tbuf = take(sizeof(float) * (size_t)g.n);
     o.part = take(sizeof(double) * (size_t)NVMAX * std::max(g.nblk, g.nblk1));
@@ -2731,6 +2803,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     double* part = at<double>(ws, o.part);
     double* sums = at<double>(ws, o.sums);
     unsigned long long* hist = at<unsigned long long>(ws, o.hist);
+    const unsigned long long* cooc = at<unsigned long long>(ws, o.cooc);
     float* lt = at<float>(ws, o.lt);
     float* imp = at<float>(ws, o.imp);
     unsigned long long* rowfx = at<unsigned long long>(ws, o.rowfx);
@@ -2782,11 +2855,14 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 0>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
 swept3:
+    // sweep4m writes the full drive: fin3 then forms the hash term's RMS from
+    // the co-occurrence counts, and sweep 5 needs no bins
+    const int c5c = (KC <= 12 && fast && cooc_closed(g)) ? 1 : 0;
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3), dim3(256), 0, s, part, g.nblk, NV3, sums);
     hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
-                       step, hash_on, hard, echo_on, h);
+                       cooc, step, hash_on, hard, echo_on, c5c, h);
     if constexpr (KC <= 12) {
-        if (fast) {
+        if (c5c) {
             hipLaunchKernelGGL((sweep4m_kernel<RM, KC>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf,
                                part, echo_on, h);
             goto swept4;
@@ -2799,12 +2875,13 @@ swept3:
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 0>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
                            hash_on, echo_on, h);
 swept4:
-    hipLaunchKernelGGL(fin4_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, step, hash_on, hard, h);
-    const size_t l5 = hash_on ? sizeof(float) * (size_t)g.T * g.B : 0;
+    hipLaunchKernelGGL(fin4_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, step, hash_on, hard, c5c, h);
+    const bool hash5 = hash_on && !c5c;   // sweep 5 adds the hash term itself
+    const size_t l5 = hash5 ? sizeof(float) * (size_t)g.T * g.B : 0;
     const bool pv4 = ((uintptr_t)param % (4 * sizeof(PT))) == 0;
-    if (hash_on && pv4)
+    if (hash5 && pv4)
         hipLaunchKernelGGL((sweep5_kernel<PT, true, true>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, h);
-    else if (hash_on)
+    else if (hash5)
         hipLaunchKernelGGL((sweep5_kernel<PT, true, false>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, h);
     else if (pv4)
         hipLaunchKernelGGL((sweep5_kernel<PT, false, true>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, h);
@@ -2877,6 +2954,13 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
     const int64_t bins_blocks = std::max<int64_t>(1, std::min<int64_t>(2048, (g.n + 255) / 256));
     hipLaunchKernelGGL(ws_bins_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g, at<unsigned char>(ws, o.bins),
                        at<unsigned long long>(ws, o.counts));
+    if (cooc_closed(g)) {
+        const int64_t BB = (int64_t)g.B * g.B;
+        hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((BB + 255) / 256)), dim3(256), 0, s,
+                           at<unsigned long long>(ws, o.cooc), BB);
+        hipLaunchKernelGGL(ws_cooc_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g,
+                           at<const uint16_t>(ws, o.bins), at<unsigned long long>(ws, o.cooc));
+    }
     e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace init");

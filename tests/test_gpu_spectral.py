@@ -96,3 +96,36 @@ def test_spectral_deterministic():
     assert torch.equal(outs[0][0], outs[1][0])
     for k in outs[0][1]:
         assert torch.equal(outs[0][1][k], outs[1][1][k]), k
+
+
+# The matrix-core fast path (2-D, two tables of <= 256 bins, panel tiles of 32+
+# rows: at least 8 Mi elements) at other ranks and bin counts than the C2 case:
+# rank 4 with 128 bins (co-occurrence counts at the LDS limit), rank 8 with 256
+# bins (co-occurrence counts by global atomics) and maximize.
+FAST_CASES = [
+    ("r4_b128", (2048, 4096), dict(lr=2e-3, rank=4, max_frequency=3, hash_bins=128, hash_tables=2)),
+    ("r8_b256_max", (2048, 4096), dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=256, hash_tables=2, maximize=True)),
+]
+
+
+@pytest.mark.parametrize("case", FAST_CASES, ids=[c[0] for c in FAST_CASES])
+def test_spectral_fast_path_variants(case):
+    name, shape, kw = case
+    announce(f"spectral fast path {name} {shape}")
+    import cresso_amd
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    gen = torch.Generator().manual_seed(15)
+    p0 = 0.02 * torch.randn(shape, generator=gen)
+    hp = torch.nn.Parameter(p0.clone().cuda())
+    hopt = cresso_amd.CRESSO5([hp], cuda_ops="required", **kw)
+    op = p0.clone()
+    oopt = OracleCRESSO5([op], hash_accum="fp64", **kw)
+    for _ in range(3):
+        g = 1e-3 * torch.randn(shape, generator=gen)
+        g = torch.where(torch.rand(shape, generator=gen) < 0.01, g * 50.0, g)
+        hp.grad = g.cuda()
+        hopt.step()
+        oopt.step([g])
+    torch.cuda.synchronize()
+    compare([hp], hopt, [op], oopt)
