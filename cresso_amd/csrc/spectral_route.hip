@@ -1241,6 +1241,201 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     P.flush(part);
 }
 
+// Helpers of the matrix-core sweeps.
+typedef float f32x4m __attribute__((ext_vector_type(4)));
+constexpr int SP_BQS = SP_NT + 16;   // row stride of sweep3m's LDS carrier table
+template <typename GT> __device__ __forceinline__ float ldg_el(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff);
+template <> __device__ __forceinline__ float ldg_el<float>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return bload1(r, voff, soff);
+}
+template <> __device__ __forceinline__ float ldg_el<__half>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return to_f(__builtin_bit_cast(__half, (unsigned short)bload1u16(r, voff, soff)));
+}
+template <>
+__device__ __forceinline__ float ldg_el<__hip_bfloat16>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return to_f(__builtin_bit_cast(__hip_bfloat16, (unsigned short)bload1u16(r, voff, soff)));
+}
+
+// Sum over each 16-lane DPP row (every lane of the row gets its row's total,
+// in a fixed order).
+__device__ __forceinline__ float row16_total(float v) {
+    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x124, 0xF>(v);  // row_ror:4
+    v = dpp_add<0x128, 0xF>(v);  // row_ror:8
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// S2 on the matrix cores (MODE 1 tiles, RM <= 8): sweep2_kernel's element
+// math in sweep3m_kernel's tile layout (lane l: rows 4 lg + r of column li of
+// each 16 x 16 tile, 4 tile columns per wave).  The log-density projection
+// Z_q(col) = sum_rows a_q(row) L(row, col) is 4 MFMAs per tile (A = the rows'
+// factors, B = L).  Row density sums: the lane's 4 tile columns are added in
+// registers, then each 16-lane row group sums its columns with DPP; column
+// sums stay per lane and tile column until the end.
+// ---------------------------------------------------------------------------
+template <int RM, int KC, typename GT>
+__global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
+    Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
+    const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
+    double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ rowfx,
+    unsigned long long* __restrict__ colfx, cresso_hyper h) {
+    static_assert(RM <= 8, "16 projection rows");
+    constexpr int RW = 2 * RM;
+    extern __shared__ __align__(16) unsigned char dyn[];
+    __shared__ float red[4 * NV2];
+    const Tile t = tile_of(g);
+    const int B = g.B;
+    const int TB = 2 * B;
+    const int nr = g.PR;
+    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int li = l & 15, lg = l >> 4;
+    const int64_t base = panel_base(g, t);
+    const uint32_t cols = (uint32_t)g.cols;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(grad + base, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(GT)));
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(reinterpret_cast<const uint16_t*>(bins) + base, (uint32_t)((int64_t)nr * g.cols * 2));
+    const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
+    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vb = lane_el * 2u;
+    auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
+    // one register set, refilled tile by tile (loads three tiles ahead of use)
+    float xv[16];
+    uint32_t bv[16];
+    auto load_tile = [&](int tr, int tc) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t o = tile_off(tr, tc, r);
+            xv[4 * tc + r] = ldg_el<GT>(rg, vg, o * (uint32_t)sizeof(GT));
+            bv[4 * tc + r] = bload1u16(rb, vb, o * 2u);
+        }
+    };
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) load_tile(0, tc);
+    // LDS: histogram copies [TB][NH] u64 | row-sum partials [4 waves][PR] | row factors [PR][RW]
+    constexpr int NH = SP_NHIST;
+    const int hc = (int)(threadIdx.x & (SP_NHIST - 1));
+    unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
+    float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
+    float* s_ar = s_wrow + 16 * g.PR;
+    for (int i = threadIdx.x; i < NH * TB; i += SP_NT) s_hist[i] = 0ull;
+    stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
+    __syncthreads();
+    const float inv_s = ctrl->inv_s;
+    const float eps = (float)h.eps;
+    const float pw = (float)h.energy_power;
+    const float sg = h.maximize ? -1.f : 1.f;
+    const float hs = (float)ctrl->hs_ds;
+    f32x4m zacc[4];
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) zacc[tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
+    float aL = 0.f;
+    float cD[4] = {0.f, 0.f, 0.f, 0.f};   // column density sums of the lane's 4 tile columns
+    // Sums of log(1 + ds) are kept in log2 units (fin2 scales them by ln 2).
+    const int ntr = nr / 16;
+    for (int tr = 0; tr < ntr; ++tr) {
+        float rs[4] = {0.f, 0.f, 0.f, 0.f};   // this row of tiles' density, per lane row
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) {
+            const float* x = xv + 4 * tc;
+            const uint32_t* b = bv + 4 * tc;
+            float Ls[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                // full tile: rel >= eps and instant-metric power 1, so the density is rel
+                const float rel = fminf(fmaf(fabsf(sg * x[r]), inv_s, eps), 1.0e4f);
+                const float ds = fexp2(pw * flog2(rel));
+                const float L = flog2(1.0f + ds);
+                Ls[r] = L;
+                aL += L;
+                rs[r] += rel;
+                cD[tc] += rel;
+                const unsigned long long v = to_fixed_u(ds * hs);
+                atomicAdd(&s_hist[(b[r] & 0xffu) * NH + hc], v);
+                atomicAdd(&s_hist[(B + (b[r] >> 8)) * NH + hc], v);
+            }
+            // A of the projection: a_li(row 16 tr + 4 lg + r)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float aJ = li < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (li < RW ? li : 0)] : 0.f;
+                zacc[tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJ, Ls[r], zacc[tc], 0, 0, 0);
+            }
+            if (tr + 1 < ntr) load_tile(tr + 1, tc);
+            pin1(aL);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pin1(rs[r]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) pin1(cD[c]);
+            elem_fence();
+        }
+        // rows 16 tr + 4 lg + r: the 16 columns of the lane group, lane li = r writes
+        float rt[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rt[r] = row16_total(rs[r]);
+        if (li < 4) s_wrow[wv * g.PR + 16 * tr + 4 * lg + li] = li == 0 ? rt[0] : (li == 1 ? rt[1] : (li == 2 ? rt[2] : rt[3]));
+    }
+    __syncthreads();
+    // axis density sums: one fixed-point atomic per row of this slab and per column of this panel
+    for (int lr = threadIdx.x; lr < nr; lr += SP_NT) {
+        float sr = 0.f;
+        for (int w = 0; w < SP_NT / 64; ++w) sr += s_wrow[w * g.PR + lr];
+        atomicAdd(&rowfx[t.r0 + lr], to_fixed_u(sr * (float)g.hs_row));
+    }
+    float aD = 0.f;
+    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) {
+        // the column's 4 lane groups, in a fixed order
+        float c = cD[tc];
+        c += __shfl_xor(c, 16, 64);
+        c += __shfl_xor(c, 32, 64);
+        if (lg == 0) atomicAdd(&colfx[colw + 16 * tc + li], to_fixed_u(c * (float)g.hs_col));
+        aD += cD[tc];
+    }
+    for (int i = threadIdx.x; i < TB; i += SP_NT) {
+        unsigned long long v = 0ull;
+#pragma unroll
+        for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
+        if (v) atomicAdd(&hist[i], v);
+    }
+    Partials P{red, 2 + 2 * g.R, NV2};
+    P.add(0, aL);
+    P.add(1, aD);
+    // projection: lane group lg holds Z_{4 lg + j}(col), both components of
+    // modes 2 lg and 2 lg + 1, for its 4 columns (proj_finish's form), summed
+    // over the columns and the group's 16 lanes into slots 2 + 4 lg + j
+    float cs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const int r = 2 * lg + half;
+        if (r < g.R) {
+            const ModeMeta m = meta[r];
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) {
+                const int64_t c = colw + 16 * tc + li;
+                // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
+                const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
+                const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
+                const float z1 = zacc[tc][2 * half], z2 = zacc[tc][2 * half + 1];
+                if (m.type == M_ADD) {
+                    cs[2 * half] += b1 * z1 - b2 * z2;
+                    cs[2 * half + 1] += b1 * z2 + b2 * z1;
+                } else {
+                    cs[2 * half] += b1 * z1;
+                    cs[2 * half + 1] += b2 * z2;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float sm = row16_total(cs[j]);
+        const int slot = 4 * lg + j;
+        if (li == 15 && slot < 2 * g.R) red[wv * P.V + 2 + slot] = sm;
+    }
+    P.flush(part);
+}
+
 // ---------------------------------------------------------------------------
 // finalize helpers: one wave, one lane per mode
 // ---------------------------------------------------------------------------
@@ -1687,29 +1882,6 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
 // each tile.  The loads of the next row of tiles are in flight while a row is
 // processed.
 // ---------------------------------------------------------------------------
-typedef float f32x4m __attribute__((ext_vector_type(4)));
-constexpr int SP_BQS = SP_NT + 16;   // row stride of sweep3m's LDS carrier table
-template <typename GT> __device__ __forceinline__ float ldg_el(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff);
-template <> __device__ __forceinline__ float ldg_el<float>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return bload1(r, voff, soff);
-}
-template <> __device__ __forceinline__ float ldg_el<__half>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return to_f(__builtin_bit_cast(__half, (unsigned short)bload1u16(r, voff, soff)));
-}
-template <>
-__device__ __forceinline__ float ldg_el<__hip_bfloat16>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return to_f(__builtin_bit_cast(__hip_bfloat16, (unsigned short)bload1u16(r, voff, soff)));
-}
-
-// Sum over each 16-lane DPP row (every lane of the row gets its row's total,
-// in a fixed order).
-__device__ __forceinline__ float row16_total(float v) {
-    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-    v = dpp_add<0x124, 0xF>(v);  // row_ror:4
-    v = dpp_add<0x128, 0xF>(v);  // row_ror:8
-    return v;
-}
 
 template <int RM, int KC, typename GT>
 __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
@@ -2829,12 +3001,20 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
         hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, h);
     hipLaunchKernelGGL(fin1_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, rowfx, colfx, step, h);
     const bool fast = fast_mode(g, hash_on, axes_on, h);
+    if constexpr (RM <= 8) {
+        if (fast) {
+            hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl, part,
+                               hist, rowfx, colfx, h);
+            goto swept2;
+        }
+    }
     if (fast)
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, h);
     else
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 0>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, h);
+swept2:
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2), dim3(256), 0, s, part, g.nblk, NV2, sums);
     hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st,
                        ctrl, step, hash_on, hard, h);
