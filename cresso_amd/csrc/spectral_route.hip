@@ -586,23 +586,23 @@ __device__ __forceinline__ float wave_total(float v) {
 
 // Block partials, one value at a time: DPP wave totals into LDS [wave][V],
 // then a fixed-order sum over the block's waves, written value-major
-// part[v][block].
+// part[v][block] (consumers read each value's blocks contiguously).
 struct Partials {
     float* lds;
     int V;
-    int VS;   // row stride of the block-major partials (the consumer's fixed width; zero padded)
+    int VS;   // values written (the consumer's fixed width; slots V..VS-1 zero)
     __device__ __forceinline__ void add(int idx, float x) {
         const float w = wave_total(x);
         if ((threadIdx.x & 63) == 63) lds[(threadIdx.x >> 6) * V + idx] = w;
     }
-    // block-major: part[block][VS], slots V..VS-1 zero
+    // value-major: part[v][gridDim.x], slots V..VS-1 zero
     __device__ __forceinline__ void flush(double* part) {
         __syncthreads();
         for (int v = threadIdx.x; v < VS; v += SP_NT) {
             double s = 0.0;
             if (v < V)
                 for (int w = 0; w < SP_NT / 64; ++w) s += (double)lds[w * V + v];
-            part[(size_t)blockIdx.x * VS + v] = s;
+            part[(size_t)v * gridDim.x + blockIdx.x] = s;
         }
     }
 };
@@ -634,22 +634,21 @@ __device__ __forceinline__ float reservoir_f(float old, float cur, double decay,
     return old * (float)decay + (float)(1.0 - decay) * cur;
 }
 
-// All partial values of a sweep (block-major part[block][V]) reduced in a
+// All partial values of a sweep (value-major part[v][nblk]) reduced in a
 // fixed order into out[v] (LDS), visible after return: thread j accumulates
-// blocks j, j + NT, ... in fp64 (its loads all in flight), each wave reduces
-// every value with DPP in fixed lane order, and the wave totals are added in
-// wave order.
+// blocks j, j + NT, ... of every value in fp64 (coalesced loads, all in
+// flight), each wave reduces every value with DPP in fixed lane order, and the
+// wave totals are added in wave order.
 template <int VMAX>
 __device__ void reduce_bm(const double* __restrict__ part, int nblk, int V, double* out) {
     __shared__ double s_w[SP_FN_NT / 64][VMAX];
     double acc[VMAX];
 #pragma unroll
     for (int v = 0; v < VMAX; ++v) acc[v] = 0.0;
-    // rows have the fixed width VMAX (zero padded): unconditional loads, all in flight
     for (int b = threadIdx.x; b < nblk; b += SP_FN_NT) {
-        const double* __restrict__ p = part + (size_t)b * VMAX;
 #pragma unroll
-        for (int v = 0; v < VMAX; ++v) acc[v] += p[v];
+        for (int v = 0; v < VMAX; ++v)
+            if (v < V) acc[v] += part[(size_t)v * nblk + b];
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -675,8 +674,9 @@ __global__ __launch_bounds__(256) void part_reduce_kernel(const double* __restri
                                                           double* __restrict__ sums) {
     __shared__ double s_w[4];
     const int v = blockIdx.x;
+    (void)VS;
     double a = 0.0;
-    for (int b = threadIdx.x; b < nblk; b += 256) a += part[(size_t)b * VS + v];
+    for (int b = threadIdx.x; b < nblk; b += 256) a += part[(size_t)v * nblk + b];
     a = wave_total_d(a);
     if ((threadIdx.x & 63) == 63) s_w[threadIdx.x >> 6] = a;
     __syncthreads();
