@@ -248,12 +248,9 @@ __device__ DriveCoef<W> contact_and_coefs(const double* M, double dn, const cres
 // runs on |t| (shape3a): the moments need no signs, and the drive takes the
 // sign of t once.
 template <typename PT, typename GT, int LAYOUT, bool FAST>
-__global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec* __restrict__ recs,
-                                                                 int32_t* __restrict__ steps,
-                                                                 const void* const* __restrict__ grads, int32_t first,
-                                                                 cresso_hyper h) {
-    __shared__ double red[16 * SR_SLOTS];
-    __shared__ int s_step;
+__device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs, int32_t* __restrict__ steps,
+                                              const void* const* __restrict__ grads, int32_t first,
+                                              const cresso_hyper& h, double* __restrict__ red, int& s_step) {
     extern __shared__ __align__(16) unsigned char dyn[];
 
     const int tid = threadIdx.x;
@@ -685,6 +682,21 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
     if (tid == 0) {
         *sp[0] = dc.q1; *sp[1] = imp; *sp[2] = mq; *sp[3] = mp; *sp[4] = fr; *sp[5] = de; *sp[6] = sur; *sp[7] = act;
     }
+}
+
+// Both resident layouts in one launch (the layout is uniform per workgroup),
+// so the plan's resident tensors fill the CUs in one sequence of rounds.
+template <typename PT, typename GT, bool FAST>
+__global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec* __restrict__ recs,
+                                                                 int32_t* __restrict__ steps,
+                                                                 const void* const* __restrict__ grads, int32_t first,
+                                                                 cresso_hyper h) {
+    __shared__ double red[16 * SR_SLOTS];
+    __shared__ int s_step;
+    if (recs[first + blockIdx.x].layout == L_ROWGROUP)
+        resident_body<PT, GT, L_ROWGROUP, FAST>(recs, steps, grads, first, h, red, s_step);
+    else
+        resident_body<PT, GT, L_COLBLOCK, FAST>(recs, steps, grads, first, h, red, s_step);
 }
 
 // ---------------------------------------------------------------------------
@@ -1128,7 +1140,7 @@ __global__ __launch_bounds__(SR_NT) void micro_kernel(const ScalarRec* __restric
 bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 struct Variant {
-    int pt, gt, kind;   // kind: 0 stream, 1 resident ROWGROUP, 2 resident COLBLOCK, 3 micro field
+    int pt, gt, kind;   // kind: 0 stream, 1 resident (row-group or column-block layout), 3 micro field
     bool full;          // resident with numel == SR_RESIDENT_MAX: eligible for the FAST kernel
     bool operator==(const Variant& o) const { return pt == o.pt && gt == o.gt && kind == o.kind && full == o.full; }
 };
@@ -1215,7 +1227,7 @@ int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec&
             r.layout = L_COLBLOCK;
             r.rows = d.shape[0];
             r.cols = C0;
-            kind = 2;
+            kind = 1;
             lds = SR_XLDS + sizeof(float) * SR_SLOTS;
         } else {
             int64_t sum = 0, maxcnt = 1, st = 1;
@@ -1243,33 +1255,29 @@ int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec&
 
 // The resident kernels use more than 64 KiB of dynamic LDS: raise the
 // function's limit once (thread-safe static initialisation).
-template <typename PT, typename GT, int LAYOUT, bool FAST>
+template <typename PT, typename GT, bool FAST>
 hipError_t allow_resident_lds() {
     static const hipError_t e =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&scalar_resident_kernel<PT, GT, LAYOUT, FAST>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&scalar_resident_kernel<PT, GT, FAST>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)SR_LDS_MAX);
     return e;
 }
 
-template <typename PT, typename GT, int LAYOUT, bool FAST>
+template <typename PT, typename GT, bool FAST>
 hipError_t launch_resident_v(const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first, int32_t cnt,
                              size_t lds, const cresso_hyper& h, hipStream_t s) {
-    const hipError_t e = allow_resident_lds<PT, GT, LAYOUT, FAST>();
+    const hipError_t e = allow_resident_lds<PT, GT, FAST>();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, LAYOUT, FAST>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads,
-                       first, h);
+    hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, FAST>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads, first, h);
     return hipGetLastError();
 }
 
 template <typename PT, typename GT>
-hipError_t launch_resident(int kind, bool fast, const ScalarRec* recs, int32_t* steps, const void* const* grads,
-                           int32_t first, int32_t cnt, size_t lds, const cresso_hyper& h, hipStream_t s) {
+hipError_t launch_resident(bool fast, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
+                           int32_t cnt, size_t lds, const cresso_hyper& h, hipStream_t s) {
     if (lds > SR_LDS_MAX) return hipErrorInvalidValue;
-    if (kind == 1)
-        return fast ? launch_resident_v<PT, GT, L_ROWGROUP, true>(recs, steps, grads, first, cnt, lds, h, s)
-                    : launch_resident_v<PT, GT, L_ROWGROUP, false>(recs, steps, grads, first, cnt, lds, h, s);
-    return fast ? launch_resident_v<PT, GT, L_COLBLOCK, true>(recs, steps, grads, first, cnt, lds, h, s)
-                : launch_resident_v<PT, GT, L_COLBLOCK, false>(recs, steps, grads, first, cnt, lds, h, s);
+    return fast ? launch_resident_v<PT, GT, true>(recs, steps, grads, first, cnt, lds, h, s)
+                : launch_resident_v<PT, GT, false>(recs, steps, grads, first, cnt, lds, h, s);
 }
 
 template <typename W, typename PT, typename GT>
@@ -1285,12 +1293,12 @@ hipError_t launch_stream(bool micro, const ScalarRec* recs, int32_t* steps, cons
 
 hipError_t dispatch(const Variant& v, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
                     int32_t cnt, size_t lds, unsigned char* table, const cresso_hyper& h, hipStream_t s) {
-    if (v.kind == 1 || v.kind == 2) {
+    if (v.kind == 1) {
         const bool fast = v.full && fast_hyper(h);
-        if (v.pt == CRESSO_F32) return launch_resident<float, float>(v.kind, fast, recs, steps, grads, first, cnt, lds, h, s);
+        if (v.pt == CRESSO_F32) return launch_resident<float, float>(fast, recs, steps, grads, first, cnt, lds, h, s);
         if (v.pt == CRESSO_BF16)
-            return launch_resident<__hip_bfloat16, __hip_bfloat16>(v.kind, fast, recs, steps, grads, first, cnt, lds, h, s);
-        if (v.pt == CRESSO_F16) return launch_resident<__half, __half>(v.kind, fast, recs, steps, grads, first, cnt, lds, h, s);
+            return launch_resident<__hip_bfloat16, __hip_bfloat16>(fast, recs, steps, grads, first, cnt, lds, h, s);
+        if (v.pt == CRESSO_F16) return launch_resident<__half, __half>(fast, recs, steps, grads, first, cnt, lds, h, s);
         return hipErrorInvalidValue;
     }
 #define CRESSO_SR_CASE(PC, GC, W, PT, GT) \
