@@ -161,6 +161,24 @@ def load() -> ctypes.CDLL:
         return lib
 
 
+_HB = None
+_HB_TRIED = False
+
+
+def host_batch():
+    """The C++ host bookkeeping helper (cresso_amd/_hostbatch*.so), or None
+    when it is not built (the Python loops then do the same work)."""
+    global _HB, _HB_TRIED
+    if not _HB_TRIED:
+        _HB_TRIED = True
+        try:
+            from . import _hostbatch as hb  # type: ignore[attr-defined]
+            _HB = hb
+        except ImportError:
+            _HB = None
+    return _HB
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = (_LIB.cresso_hip_last_error() or b"").decode(errors="replace") if _LIB is not None else ""

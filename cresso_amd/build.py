@@ -31,7 +31,37 @@ def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
+HOST_SRC = CSRC / "host_batch.cpp"
+
+
+def host_ext_path() -> Path:
+    import sysconfig
+
+    return HERE / ("_hostbatch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def host_cmd() -> list:
+    """g++ line of the host bookkeeping extension (a torch C++ extension, CPU only)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension as ce
+
+    inc = [f"-I{d}" for d in ce.include_paths()] + [f"-I{sysconfig.get_paths()['include']}"]
+    libdir = ce.library_paths()[0]
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    tmp = host_ext_path().with_suffix(".tmp")
+    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-w", str(HOST_SRC), "-o", str(tmp), *inc,
+            "-DTORCH_EXTENSION_NAME=_hostbatch", "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+            f"-L{libdir}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", f"-Wl,-rpath,{libdir}"]
+
+
 def build(verbose: bool = False, jobs: int = 8) -> Path:
+    # the host extension (slowest compile: torch headers) starts first, in parallel
+    hcmd = host_cmd()
+    if verbose:
+        print(" ".join(hcmd), flush=True)
+    hproc = subprocess.Popen(hcmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
     srcs = sources()
     objdir = HERE / "_build"
     objdir.mkdir(exist_ok=True)
@@ -59,6 +89,10 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     if out.returncode != 0:
         raise RuntimeError("link failed:\n" + out.stdout.decode(errors="replace"))
     os.replace(tmp, LIB)
+    hout, _ = hproc.communicate()
+    if hproc.returncode != 0:
+        raise RuntimeError("g++ failed on host_batch.cpp:\n" + hout.decode(errors="replace"))
+    os.replace(host_ext_path().with_suffix(".tmp"), host_ext_path())
     return LIB
 
 

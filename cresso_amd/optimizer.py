@@ -143,6 +143,15 @@ class _ScalarBatch:
                                                     ctypes.c_size_t(self.table.numel()), ctypes.c_void_p(stream)),
                       "scalar route upload")
         self.gptr_type = ctypes.c_void_p * len(params)
+        # steady-state host bookkeeping in C++ when the helper is built
+        self.gbuf = self.gptr_type()
+        self.guard = None
+        hb = _native.host_batch()
+        if hb is not None:
+            try:
+                self.guard = hb.BatchGuard(list(params))
+            except (ValueError, RuntimeError):
+                self.guard = None
 
     @staticmethod
     def key_of(group: dict):
@@ -152,15 +161,29 @@ class _ScalarBatch:
         return (len(params) == len(self.params) and all(a is b for a, b in zip(params, self.params))
                 and [p.data_ptr() for p in params] == self.pptrs and self.key_of(group) == self.hyper_key)
 
-    def run(self, group: dict, gptrs: List[int]) -> None:
+    def run(self, group: dict, gptrs: Optional[List[int]]) -> None:
+        """One step; gptrs None: the grad pointers are already in self.gbuf."""
         hyper = _native.hyper_from_group(group)
-        arr = self.gptr_type(*gptrs)
+        arr = self.gbuf if gptrs is None else self.gptr_type(*gptrs)
         stream = _native.stream_handle(self.device)
         _native.check(self.lib.cresso_scalar_plan_step(self.plan, ctypes.c_void_p(self.table.data_ptr()), arr,
                                                        ctypes.byref(hyper), ctypes.c_void_p(stream)),
                       "scalar route step")
-        for st in self.states:
-            st["step"] += 1
+        if self.guard is not None:
+            self.guard.bump(self.states)
+        else:
+            for st in self.states:
+                st["step"] += 1
+
+    def fast_step(self, group: dict) -> bool:
+        """Steady state in C++: same params and storage, fresh grads of the
+        planned dtype; False (nothing launched) when anything changed."""
+        if self.guard is None or self.key_of(group) != self.hyper_key:
+            return False
+        if not self.guard.gather(group["params"], ctypes.addressof(self.gbuf)):
+            return False
+        self.run(group, None)
+        return True
 
     def __del__(self):
         plan = getattr(self, "plan", None)
@@ -313,6 +336,8 @@ class CRESSO5(Optimizer):
         batch = self._batches.get((gi, "scalar"))
         if batch is None or self._group_other.get(gi, True):
             return False
+        if batch.guard is not None:
+            return batch.fast_step(group)
         try:
             gptrs = [p.grad.data_ptr() for p in batch.params]
         except (AttributeError, RuntimeError):
