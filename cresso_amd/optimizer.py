@@ -112,6 +112,7 @@ class _ScalarBatch:
         self.states = states
         self.device = device
         self.pptrs = [p.data_ptr() for p in params]
+        self.gdtypes = [p.grad.dtype for p in params]   # the plan's descriptors fix the grad dtype
         self.hyper_key = self.key_of(group)
         descs = (_native.ScalarDesc * len(params))()
         for i, (p, st) in enumerate(zip(params, states)):
@@ -159,7 +160,8 @@ class _ScalarBatch:
 
     def matches(self, params: List[Tensor], group: dict) -> bool:
         return (len(params) == len(self.params) and all(a is b for a, b in zip(params, self.params))
-                and [p.data_ptr() for p in params] == self.pptrs and self.key_of(group) == self.hyper_key)
+                and [p.data_ptr() for p in params] == self.pptrs and self.key_of(group) == self.hyper_key
+                and [p.grad.dtype for p in params] == self.gdtypes)
 
     def run(self, group: dict, gptrs: Optional[List[int]]) -> None:
         """One step; gptrs None: the grad pointers are already in self.gbuf."""

@@ -211,3 +211,25 @@ def test_hash_bigint_brute_force_on_small_n():
                 h = wrap(h * (3266489917 + 374761393 * s))
                 h = wrap(h ^ (h >> 16))
                 assert got[i] == h % bins
+
+
+def test_host_batch_guard_cpu_behaviour():
+    # the C++ steady-state helper is built with the library; on CPU tensors it
+    # refuses the fast path, and bump() advances every state["step"]
+    import ctypes
+
+    hb = _native.host_batch()
+    assert hb is not None, "cresso_amd/_hostbatch extension not built"
+    ps = [torch.nn.Parameter(torch.zeros(4, 4)) for _ in range(3)]
+    for p in ps:
+        p.grad = torch.zeros(4, 4)
+    guard = hb.BatchGuard(ps)
+    buf = (ctypes.c_void_p * 3)()
+    assert guard.gather(ps, ctypes.addressof(buf)) is False      # CPU grads: no fast path
+    assert guard.gather(ps[:2], ctypes.addressof(buf)) is False  # different group
+    states = [{"step": 0}, {"step": 7}, {"step": 2}]
+    guard.bump(states)
+    assert [s["step"] for s in states] == [1, 8, 3]
+    ps[0].grad = None
+    with pytest.raises(ValueError):
+        hb.BatchGuard(ps)

@@ -163,3 +163,37 @@ def test_scalar_state_dict_roundtrip_resumes_identically():
     torch.cuda.synchronize()
     for a, b in zip(ps, ps2):
         assert torch.equal(a, b)
+
+
+def test_scalar_steady_state_replans_on_changes():
+    # the steady-state path (C++ guard) must notice a grad dtype change, a
+    # replaced parameter storage and a hyperparameter change, and re-plan
+    announce("scalar steady-state changes")
+    import cresso_amd
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    gen = torch.Generator().manual_seed(12)
+    shapes = [(4096, 16), (16, 4096), (128, 16)]
+    p0 = [0.02 * torch.randn(s, generator=gen) for s in shapes]
+    hp = [torch.nn.Parameter(p.clone().cuda()) for p in p0]
+    for p in hp:
+        p.grad_dtype = None   # allow grads of another dtype
+    op = [p.clone() for p in p0]
+    hopt = cresso_amd.CRESSO5(hp, cuda_ops="required", **SCALAR_KW)
+    oopt = OracleCRESSO5(op, **SCALAR_KW)
+    for k in range(6):
+        gs = [1e-2 * torch.randn(s, generator=gen) for s in shapes]
+        if k == 2:      # bf16 grads on fp32 params
+            gs = [g.to(torch.bfloat16) for g in gs]
+        if k == 3:      # new storage for one parameter (same values)
+            hp[1].data = hp[1].data.clone()
+        if k == 4:      # learning-rate change
+            for grp in hopt.param_groups:
+                grp["lr"] = 1e-3
+            oopt.h["lr"] = 1e-3
+        for p, g in zip(hp, gs):
+            p.grad = g.cuda()
+        hopt.step()
+        oopt.step(gs)
+    torch.cuda.synchronize()
+    compare(hp, hopt, op, oopt)
