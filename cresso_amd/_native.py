@@ -130,6 +130,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cresso_spectral_workspace_bins.restype = c.c_int32
     lib.cresso_spectral_workspace_bins.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_void_p,
                                                    c.c_void_p]
+    lib.cresso_spectral_workspace_project.restype = c.c_int32
+    lib.cresso_spectral_workspace_project.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_void_p,
+                                                      c.c_void_p]
+    lib.cresso_spectral_workspace_reconstruct.restype = c.c_int32
+    lib.cresso_spectral_workspace_reconstruct.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_void_p,
+                                                          c.c_void_p, c.c_void_p, c.c_void_p]
     lib.cresso_spectral_workspace_gram.restype = c.c_int32
     lib.cresso_spectral_workspace_gram.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_void_p]
     lib.cresso_spectral_workspace_basis.restype = c.c_int32

@@ -510,6 +510,81 @@ __global__ void ws_basis_kernel(Geom g, const ModeMeta* __restrict__ meta, const
     }
 }
 
+// Unit entry points of the basis algebra (cresso_v5.py:351-376) on the
+// workspace's separable tables, for parity checks and callers that want the
+// reference's project/reconstruct: the normalized carriers of
+// ws_basis_kernel, evaluated per element.
+__device__ __forceinline__ void carrier_pair_n(const Geom& g, const ModeMeta& m, const float* __restrict__ rowtab,
+                                               const float* __restrict__ coltab, const double* __restrict__ stats,
+                                               int r, int64_t row, int64_t col, float& cn, float& sn) {
+    const float a1 = rowtab[row * g.RW + 2 * r], a2 = rowtab[row * g.RW + 2 * r + 1];
+    const float b1 = coltab[(size_t)m.k1 * g.cols + col];
+    const float b2 = m.k2 >= 0 ? coltab[(size_t)m.k2 * g.cols + col] : 0.f;
+    const float craw = m.type == M_ADD ? a1 * b1 - a2 * b2 : a1 * b1;
+    const float sraw = m.type == M_ADD ? a2 * b1 + a1 * b2 : a2 * b2;
+    cn = (float)(((double)craw - stats[4 * r]) * stats[4 * r + 1]);
+    sn = (float)(((double)sraw - stats[4 * r + 2]) * stats[4 * r + 3]);
+}
+
+// sum_i x_i C_r(i), sum_i x_i S_r(i) (fp32 products, fp64 sums), value-major
+// block partials part[2r + c][block]
+__global__ __launch_bounds__(256) void ws_project_kernel(Geom g, const ModeMeta* __restrict__ meta,
+                                                         const float* __restrict__ rowtab,
+                                                         const float* __restrict__ coltab,
+                                                         const double* __restrict__ stats, const float* __restrict__ x,
+                                                         double* __restrict__ part) {
+    __shared__ double lds[4 * 2 * SP_MAXR];
+    double acc[2 * SP_MAXR];
+#pragma unroll
+    for (int v = 0; v < 2 * SP_MAXR; ++v) acc[v] = 0.0;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
+        const int64_t row = i / g.cols, col = i - row * g.cols;
+        const float xv = x[i];
+#pragma unroll
+        for (int r = 0; r < SP_MAXR; ++r) {
+            if (r < g.R) {
+                float cn, sn;
+                carrier_pair_n(g, meta[r], rowtab, coltab, stats, r, row, col, cn, sn);
+                acc[2 * r] += (double)(xv * cn);
+                acc[2 * r + 1] += (double)(xv * sn);
+            }
+        }
+    }
+    block_sum<2 * SP_MAXR>(acc, lds);
+    for (int v = threadIdx.x; v < 2 * g.R; v += blockDim.x) part[(size_t)v * gridDim.x + blockIdx.x] = acc[v];
+}
+
+__global__ void ws_mean_kernel(const double* __restrict__ sums, int V, double inv_n, double* __restrict__ out) {
+    const int v = threadIdx.x;
+    if (v < V) out[v] = sums[v] * inv_n;
+}
+
+// shrink * sum_r g_r (cc_r C_r + sc_r S_r) in mode order, a gate of exactly 0
+// skipping the mode (fp32 accumulation like the reference's add_(alpha))
+__global__ __launch_bounds__(256) void ws_reconstruct_kernel(Geom g, const ModeMeta* __restrict__ meta,
+                                                             const float* __restrict__ rowtab,
+                                                             const float* __restrict__ coltab,
+                                                             const double* __restrict__ stats,
+                                                             const float* __restrict__ cc, const float* __restrict__ sc,
+                                                             const float* __restrict__ gates, double shrink,
+                                                             float* __restrict__ out) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
+        const int64_t row = i / g.cols, col = i - row * g.cols;
+        float o = 0.f;
+        for (int r = 0; r < g.R; ++r) {
+            const double gr = gates ? (double)gates[r] : 1.0;
+            if (gr == 0.0) continue;
+            float cn, sn;
+            carrier_pair_n(g, meta[r], rowtab, coltab, stats, r, row, col, cn, sn);
+            o = o + (float)((double)cc[r] * shrink * gr) * cn;
+            o = o + (float)((double)sc[r] * shrink * gr) * sn;
+        }
+        out[i] = o;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // sweep helpers
 // ---------------------------------------------------------------------------
@@ -3215,6 +3290,43 @@ extern "C" int32_t cresso_spectral_workspace_basis(const cresso_spectral_plan* P
                        sin_out);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace basis");
+}
+
+extern "C" int32_t cresso_spectral_workspace_project(const cresso_spectral_plan* P, void* ws, size_t ws_bytes,
+                                                     const float* x, double* out, void* stream) {
+    if (!P || !ws || !x || !out) return fail(CRESSO_E_INVALID, "spectral route: null argument");
+    if (ws_bytes < P->o.total) return fail(CRESSO_E_INVALID, "spectral route: workspace too small");
+    const Geom& g = P->g;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // the step's partial and sum regions are the scratch (stream order keeps
+    // this call and the steps apart)
+    const int64_t blocks = std::max<int64_t>(
+        1, std::min<int64_t>(std::min<int64_t>(1024, std::max(g.nblk, g.nblk1)), (g.n + 255) / 256));
+    double* part = at<double>(ws, P->o.part);
+    double* sums = at<double>(ws, P->o.sums);
+    hipLaunchKernelGGL(ws_project_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, at<ModeMeta>(ws, P->o.meta),
+                       at<float>(ws, P->o.rowtab), at<float>(ws, P->o.coltab), at<double>(ws, P->o.stats), x, part);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3((unsigned)(2 * g.R)), dim3(256), 0, s, part, (int)blocks, 2 * g.R, sums);
+    hipLaunchKernelGGL(ws_mean_kernel, dim3(1), dim3(64), 0, s, sums, 2 * g.R, 1.0 / (double)g.n, out);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace project");
+}
+
+extern "C" int32_t cresso_spectral_workspace_reconstruct(const cresso_spectral_plan* P, const void* ws, size_t ws_bytes,
+                                                         const float* cc, const float* sc, const float* gates,
+                                                         float* out, void* stream) {
+    if (!P || !ws || !cc || !sc || !out) return fail(CRESSO_E_INVALID, "spectral route: null argument");
+    if (ws_bytes < P->o.total) return fail(CRESSO_E_INVALID, "spectral route: workspace too small");
+    const Geom& g = P->g;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    void* w = const_cast<void*>(ws);
+    const double shrink = 1.0 / std::sqrt(std::max(1.0, 0.7 * std::log2((double)g.R + 1.0)));
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(4096, (g.n + 255) / 256));
+    hipLaunchKernelGGL(ws_reconstruct_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, at<ModeMeta>(w, P->o.meta),
+                       at<float>(w, P->o.rowtab), at<float>(w, P->o.coltab), at<double>(w, P->o.stats), cc, sc, gates,
+                       shrink, out);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace reconstruct");
 }
 
 extern "C" int32_t cresso_spectral_workspace_gram(const cresso_spectral_plan* P, const void* ws, size_t ws_bytes,

@@ -202,6 +202,24 @@ int32_t cresso_spectral_workspace_basis(const cresso_spectral_plan* plan, const 
 int32_t cresso_spectral_workspace_gram(const cresso_spectral_plan* plan, const void* workspace, size_t workspace_bytes,
                                        double* gram_out, void* stream);
 
+/* Projection of a field on the normalized basis, out[2r] = mean(x C_r),
+ * out[2r+1] = mean(x S_r) (device fp32 x [numel] -> device fp64 out [2*rank];
+ * fp32 products, fp64 sums): the reference's _project / basis_project
+ * (cresso_v5.py:351-359; basis_project_with_cache_cuda, cu:996-1084).
+ * Uses the workspace's per-step scratch, so it is stream-ordered with steps. */
+int32_t cresso_spectral_workspace_project(const cresso_spectral_plan* plan, void* workspace, size_t workspace_bytes,
+                                          const float* x, double* out, void* stream);
+
+/* Reconstruction out = shrink * sum_r g_r (cc[r] C_r + sc[r] S_r), shrink =
+ * 1/sqrt(max(1, 0.7 log2(rank+1))), a gate of exactly 0 skipping mode r
+ * (gates may be NULL: all 1), accumulated in fp32 in mode order (device fp32
+ * cc, sc, gates [rank] -> device fp32 out [numel]): the reference's
+ * _reconstruct (cresso_v5.py:362-376; basis_reconstruct_with_cache_cuda,
+ * cu:1148-1210). */
+int32_t cresso_spectral_workspace_reconstruct(const cresso_spectral_plan* plan, const void* workspace,
+                                              size_t workspace_bytes, const float* cc, const float* sc,
+                                              const float* gates, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
