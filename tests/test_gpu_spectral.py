@@ -30,6 +30,10 @@ CASES = [
     ("mixed_group", [(256, 300), (4096, 16), (64, 65), (1500,)], dict(rank=8, hash_bins=64, hash_tables=2), 3,
      1e-3, 0.02),
     ("no_hash_b0", [(96, 80)], dict(rank=8, hash_bins=0), 3, 1e-3, 0.02),
+    # the matrix-core fast path with 32-row panels and few blocks (1024 rows)
+    ("fast_1024x768", [(1024, 768)], dict(rank=8, hash_bins=64, hash_tables=2), 3, 1e-3, 0.02),
+    ("fast_1024x512_r4_b32", [(1024, 512)], dict(rank=4, max_frequency=3, hash_bins=32, hash_tables=2), 3, 1e-3,
+     0.02),
 ]
 
 
