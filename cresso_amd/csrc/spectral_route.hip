@@ -779,7 +779,29 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restr
     float a = 0.f;
     const int64_t vend = beg + ((end - beg) & ~(int64_t)3);
     if (V4) {
-        for (int64_t e = beg + 4 * (int64_t)threadIdx.x; e < vend; e += 4 * SP_NT) {
+        // four float4 loads per thread in flight per iteration, then the rest one by one
+        constexpr int UN = 4;
+        const int64_t st = 4 * (int64_t)SP_NT;
+        int64_t e = beg + 4 * (int64_t)threadIdx.x;
+        for (; e + (UN - 1) * st < vend; e += UN * st) {
+            float f[UN][4];
+#pragma unroll
+            for (int u = 0; u < UN; ++u) Ld4<GT>::go(grad, e + u * st, f[u]);
+            if (wd_on) {
+                float pv[UN][4];
+#pragma unroll
+                for (int u = 0; u < UN; ++u) Ld4<PT>::go(param, e + u * st, pv[u]);
+#pragma unroll
+                for (int u = 0; u < UN; ++u)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) f[u][c] = sg * f[u][c] + wd * pv[u][c];
+            }
+#pragma unroll
+            for (int u = 0; u < UN; ++u)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) a += f[u][c] * f[u][c];
+        }
+        for (; e < vend; e += st) {
             float f[4];
             Ld4<GT>::go(grad, e, f);
             if (wd_on) {
@@ -2794,11 +2816,8 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
     };
     // chunks are multiples of 4 elements: float4 drive loads (param 4-element aligned)
     const int64_t vend = V4 ? beg + ((end - beg) & ~(int64_t)3) : beg;
-    for (int64_t e = beg + 4 * (int64_t)threadIdx.x; e < vend; e += 4 * SP_NT) {
-        const float4 d4 = *reinterpret_cast<const float4*>(dbuf + e);
+    auto apply4 = [&](int64_t e, const float4& d4, const float* pv) {
         const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-        float pv[4];
-        Ld4<PT>::go(param, e, pv);
         float o[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -2806,6 +2825,24 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
             o[c] = pv[c] + nlr * u;
         }
         St4<PT>::go(param, e, o);
+    };
+    // two float4 of drive and param per thread in flight per iteration, then the rest
+    const int64_t st = 4 * (int64_t)SP_NT;
+    int64_t e = beg + 4 * (int64_t)threadIdx.x;
+    for (; e + st < vend; e += 2 * st) {
+        const float4 d0 = *reinterpret_cast<const float4*>(dbuf + e);
+        const float4 d1 = *reinterpret_cast<const float4*>(dbuf + e + st);
+        float p0[4], p1[4];
+        Ld4<PT>::go(param, e, p0);
+        Ld4<PT>::go(param, e + st, p1);
+        apply4(e, d0, p0);
+        apply4(e + st, d1, p1);
+    }
+    for (; e < vend; e += st) {
+        const float4 d4 = *reinterpret_cast<const float4*>(dbuf + e);
+        float pv[4];
+        Ld4<PT>::go(param, e, pv);
+        apply4(e, d4, pv);
     }
     for (int64_t e = vend + threadIdx.x; e < end; e += SP_NT) apply1(param, e, drive_at(e, dbuf[e]), gain, nlr);
 }
