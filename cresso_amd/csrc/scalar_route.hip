@@ -46,7 +46,7 @@ constexpr size_t SR_XLDS = (size_t)(SR_SLOTS - SR_VSLOTS) * SR_NT * 16;  // LDS 
 constexpr size_t SR_LDS_MAX = 160 * 1024 - 4096;             // dynamic LDS budget of one workgroup (static LDS aside)
 constexpr int64_t SR_RESIDENT_MAX = (int64_t)SR_NT * SR_SLOTS * 4;
 
-enum Layout : int32_t { L_NONE = 0, L_1D = 1, L_ROWGROUP = 2, L_COLBLOCK = 3, L_GENERIC = 4 };
+enum Layout : int32_t { L_NONE = 0, L_1D = 1, L_ROWGROUP = 2, L_COLBLOCK = 3, L_GENERIC = 4, L_2D = 5 };
 
 struct ScalarRec {
     cresso_scalar_desc d;
@@ -141,6 +141,14 @@ __device__ __forceinline__ float lanes_group_sum(float v, int G) {
     v += G > 2 ? o : 0.0f;
     if (G > 4)
         for (int m = 4; m < G; m <<= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// The same group sum in the work dtype (fp64 work pairs lanes by shuffles).
+template <typename W> __device__ __forceinline__ W lanes_group_sum_w(W v, int G);
+template <> __device__ __forceinline__ float lanes_group_sum_w<float>(float v, int G) { return lanes_group_sum(v, G); }
+template <> __device__ __forceinline__ double lanes_group_sum_w<double>(double v, int G) {
+    for (int m = 1; m < G; m <<= 1) v += __shfl_xor(v, m, 64);
     return v;
 }
 
@@ -737,8 +745,21 @@ __global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* _
         return f;
     };
     unsigned long long* axis_fx = reinterpret_cast<unsigned long long*>(table + R.scratch_off);
-    float* axis_fac = reinterpret_cast<float*>(table + R.scratch_off + sizeof(unsigned long long) * R.sum_dims);
+    W* axis_fac = reinterpret_cast<W*>(table + R.scratch_off + sizeof(unsigned long long) * R.sum_dims);
     const double dn = (double)n;
+    const bool axes = layout == L_GENERIC || layout == L_2D;
+    // L_2D: (row, col) of element i = tid + k NT advanced without divisions
+    const uint32_t C2 = layout == L_2D ? (uint32_t)R.cols : 1u, R2 = layout == L_2D ? (uint32_t)R.rows : 1u;
+    const uint32_t dC = (uint32_t)SR_NT % C2, dR = (uint32_t)SR_NT / C2;
+    const uint32_t row0 = (uint32_t)tid / C2, col0 = (uint32_t)tid % C2;
+    auto advance = [&](uint32_t& row, uint32_t& col) {
+        col += dC;
+        row += dR;
+        if (col >= C2) {
+            col -= C2;
+            ++row;
+        }
+    };
 
     // ---- pass A ----
     W a = 0;
@@ -746,7 +767,7 @@ __global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* _
         const W f = force(i);
         a += f * f;
     }
-    if (layout == L_GENERIC)
+    if (axes)
         for (int64_t i = tid; i < R.sum_dims; i += SR_NT) axis_fx[i] = 0ull;
     __syncthreads();
     const int step = s_step;
@@ -771,16 +792,45 @@ __global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* _
         return d < (W)1e6 ? d : (W)1e6;
     };
     W aL = 0, aD = 0;
-    for (int64_t i = tid; i < n; i += SR_NT) {
-        const W f = force(i);
-        const W r = (f < 0 ? -f : f) * inv_s + eps;
-        aL += flog1p(fpow(r, pw));
-        const W d = density(f);
-        aD += d;
-        if (layout == L_GENERIC) {
-            const unsigned long long v = (unsigned long long)llrint((double)d * fx_scale);
-            for (int ax = 0; ax < nd; ++ax) atomicAdd(&axis_fx[R.axis_off[ax] + (i / R.stride[ax]) % R.d.shape[ax]], v);
+    // L_2D axis sums, pre-aggregated where lanes share a row or a column:
+    //   rows: a wave lies in one row when cols % 64 == 0 (wave total); aligned
+    //     groups of cols lanes hold one row when cols divides 64 (group total);
+    //   cols: a thread's column is fixed when cols divides NT (one register);
+    // each partial goes to the fixed-point sums once (integer atomics: the
+    // result does not depend on arrival order).
+    const int lane = tid & 63;
+    const int rowmode = layout != L_2D ? 0 : (C2 % 64u == 0 ? 1 : ((64u % C2 == 0) ? 2 : 0));
+    const bool colreg = layout == L_2D && (uint32_t)SR_NT % C2 == 0;
+    double colacc = 0;
+    {
+        uint32_t row = row0, col = col0;
+        for (int64_t i = tid; i < n; i += SR_NT) {
+            const W f = force(i);
+            const W r = (f < 0 ? -f : f) * inv_s + eps;
+            aL += flog1p(fpow(r, pw));
+            const W d = density(f);
+            aD += d;
+            if (layout == L_GENERIC) {
+                const unsigned long long v = (unsigned long long)llrint((double)d * fx_scale);
+                for (int ax = 0; ax < nd; ++ax) atomicAdd(&axis_fx[R.axis_off[ax] + (i / R.stride[ax]) % R.d.shape[ax]], v);
+            } else if (layout == L_2D) {
+                if (rowmode == 1) {
+                    const W w = lanes_group_sum_w<W>(d, 64);   // the wave's (one row's) sum, in every lane
+                    if (lane == 0) atomicAdd(&axis_fx[row], (unsigned long long)llrint((double)w * fx_scale));
+                } else if (rowmode == 2) {
+                    const W w = lanes_group_sum_w<W>(d, (int)C2);
+                    if ((uint32_t)lane % C2 == 0) atomicAdd(&axis_fx[row], (unsigned long long)llrint((double)w * fx_scale));
+                } else {
+                    atomicAdd(&axis_fx[row], (unsigned long long)llrint((double)d * fx_scale));
+                }
+                if (colreg)
+                    colacc += (double)d;
+                else
+                    atomicAdd(&axis_fx[R2 + col], (unsigned long long)llrint((double)d * fx_scale));
+            }
+            advance(row, col);
         }
+        if (colreg && tid < n) atomicAdd(&axis_fx[R2 + col0], (unsigned long long)llrint(colacc * fx_scale));
     }
     double gmean;
     {
@@ -797,21 +847,21 @@ __global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* _
     W metric = (W)exp((double)((W)h.metric_coupling * mq));
     metric = metric < (W)0.06 ? (W)0.06 : (metric > (W)16 ? (W)16 : metric);
     const W gden = (W)fmax(gmean, (double)eps);
-    if (layout == L_GENERIC) {
+    if (axes) {
         for (int64_t i = tid; i < R.sum_dims; i += SR_NT) {
             int ax = 0;
             while (ax + 1 < nd && i >= R.axis_off[ax + 1]) ++ax;
             const unsigned long long raw = __hip_atomic_load(&axis_fx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const W mean = (W)((double)(long long)raw / fx_scale / (dn / (double)R.d.shape[ax]));
             const W r = mean / gden;
-            axis_fac[i] = (float)(kappa * flog(r > eps ? r : eps));
+            axis_fac[i] = kappa * flog(r > eps ? r : eps);
         }
         __syncthreads();
     }
     const W sM = scale * metric;
     const bool ls_on = h.local_sharpness != 0.0;
     const W ls = (W)h.local_sharpness;
-    auto tangent = [&](W f, int64_t i) -> W {
+    auto tangent = [&](W f, int64_t i, uint32_t row, uint32_t col) -> W {
         W den = sM;
         if (ls_on) {
             W rel = (f < 0 ? -f : f) * inv_s + eps;
@@ -824,9 +874,11 @@ __global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* _
             const W r = density(f) / gden;
             inst = fexp(kappa * flog(r > eps ? r : eps));
         } else if (layout == L_GENERIC) {
-            float ls_ = 0.f;
+            W ls_ = 0;
             for (int ax = 0; ax < nd; ++ax) ls_ += axis_fac[R.axis_off[ax] + (i / R.stride[ax]) % R.d.shape[ax]];
-            inst = fexp((W)ls_);
+            inst = fexp(ls_);
+        } else if (layout == L_2D) {
+            inst = fexp(axis_fac[row] + axis_fac[R2 + col]);
         }
         if (layout != L_NONE) inst = inst < (W)0.08 ? (W)0.08 : (inst > (W)12 ? (W)12 : inst);
         W t = f / (den * inst + eps);
@@ -837,8 +889,9 @@ __global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* _
     // ---- pass C ----
     W m[13];
     for (int j = 0; j < 13; ++j) m[j] = 0;
-    for (int64_t i = tid; i < n; i += SR_NT) {
-        const W t = tangent(force(i), i);
+    uint32_t row = row0, col = col0;
+    for (int64_t i = tid; i < n; i += SR_NT, advance(row, col)) {
+        const W t = tangent(force(i), i, row, col);
         W rat, bnd, root;
         shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
         const W e = t - q0;
@@ -862,8 +915,10 @@ __global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* _
 
     // ---- pass D ----
     W add = 0;
-    for (int64_t i = tid; i < n; i += SR_NT) {
-        const W d = drive(tangent(force(i), i));
+    row = row0;
+    col = col0;
+    for (int64_t i = tid; i < n; i += SR_NT, advance(row, col)) {
+        const W d = drive(tangent(force(i), i, row, col));
         add += d * d;
     }
     {
@@ -876,8 +931,10 @@ __global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* _
 
     // ---- pass E ---- (force is recomputed before any param store of this thread)
     const W nlr = (W)(-h.lr);
-    for (int64_t i = tid; i < n; i += SR_NT) {
-        const W d = drive(tangent(force(i), i));
+    row = row0;
+    col = col0;
+    for (int64_t i = tid; i < n; i += SR_NT, advance(row, col)) {
+        const W d = drive(tangent(force(i), i, row, col));
         const W u = to_w<W>(from_wd<PT>((double)(d * gain)));
         p[i] = from_wd<PT>((double)(ldw<W>(p, i) + nlr * u));
     }
@@ -1240,11 +1297,15 @@ int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec&
                 sum += d.shape[a];
                 maxcnt = std::max<int64_t>(maxcnt, n / d.shape[a]);
             }
-            r.layout = L_GENERIC;
+            // 2-D: row/column coordinates advanced incrementally and the axis
+            // sums pre-aggregated per wave, lane group or thread (L_2D)
+            r.layout = d.ndim == 2 && n < ((int64_t)1 << 31) ? L_2D : L_GENERIC;
+            r.rows = d.shape[0];
+            r.cols = d.ndim == 2 ? d.shape[1] : 0;
             r.sum_dims = sum;
             // density <= 1e6 per element: every fixed-point axis sum stays below 2^62
             r.frac_bits = (int32_t)std::floor(62.0 - std::log2(1.0e6 * (double)maxcnt));
-            scratch = (size_t)sum * (sizeof(unsigned long long) + sizeof(float));
+            scratch = (size_t)sum * (sizeof(unsigned long long) + sizeof(double));   // fixed-point sums, factors in W
             scratch = (scratch + 255) & ~(size_t)255;
         }
     }

@@ -48,7 +48,7 @@ def run_pair(shapes, dtype, kwargs, steps, seed=0, grad_std=1e-2, param_std=0.05
 
 def compare(hp, hopt, op, oopt, param_tol=F32_TOL, state_tol=F32_TOL, skip_keys=()):
     for i, (a, b) in enumerate(zip(hp, op)):
-        np.testing.assert_allclose(a.detach().float().cpu().numpy(), b.float().numpy(), **param_tol,
+        np.testing.assert_allclose(a.detach().double().cpu().numpy(), b.double().numpy(), **param_tol,
                                    err_msg=f"param {i} shape {tuple(b.shape)}")
         sa = hopt.state[a]
         sb = oopt.state[i]

@@ -21,6 +21,28 @@ def test_scalar_2d_matches_oracle(shape):
     compare(*res)
 
 
+# 2-D tensors beyond the resident limit (streaming kernel, row/column axis sums):
+# (8192,64) and (64,8192): one row per wave; (8192,16): rows in groups of 16
+# lanes; (16,8192): a wave inside one row; (1000,60) and (3000,33): neither,
+# per-element row and column sums
+@pytest.mark.parametrize("shape", [(8192, 16), (16, 8192), (8192, 64), (64, 8192), (1000, 60), (3000, 33)])
+def test_scalar_streaming_2d_matches_oracle(shape):
+    announce(f"scalar streaming 2d {shape}")
+    res = run_pair([shape], torch.float32, SCALAR_KW, steps=3, seed=3)
+    compare(*res)
+
+
+def test_scalar_streaming_2d_options_and_dtypes():
+    announce("scalar streaming 2d options")
+    kw = dict(SCALAR_KW, maximize=True, weight_decay=0.01, instant_metric_power=0.7, local_sharpness=0.3)
+    compare(*run_pair([(8192, 16), (2000, 48)], torch.float32, kw, steps=3, seed=4))
+    announce("scalar streaming 2d bf16 / f64")
+    res = run_pair([(8192, 16), (40, 1000)], torch.bfloat16, SCALAR_KW, steps=3, seed=5)
+    compare(*res, param_tol=BF16_PARAM_TOL, state_tol=dict(rtol=1e-2, atol=1e-3))
+    res = run_pair([(8192, 16), (40, 1000)], torch.float64, SCALAR_KW, steps=3, seed=6)
+    compare(*res, param_tol=dict(rtol=1e-9, atol=1e-12), state_tol=dict(rtol=1e-9, atol=1e-12))
+
+
 def test_scalar_mixed_batch_one_launch_per_variant():
     # resident row-group, resident column-block, streaming 1D / 3D / 0-d /
     # odd 2D / large thin 2D, all in one optimizer group
