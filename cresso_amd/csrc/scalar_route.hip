@@ -59,6 +59,8 @@ struct ScalarRec {
     int64_t scratch_off;    // GENERIC: byte offset of the axis-sum scratch in the table
     int32_t frac_bits;      // GENERIC: fixed-point fraction bits of the axis sums
     int32_t resident;       // 1: scalar_resident_kernel
+    int64_t ctl_off;        // wide form: byte offset of the tensor's StreamCtl in the table
+    int32_t blk0, nblk;     // wide form: first block (within its group's launches) and block count
 };
 
 __device__ __forceinline__ float uni(float v) {
@@ -708,239 +710,626 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
 }
 
 // ---------------------------------------------------------------------------
-// streaming kernel (any shape, any size; work dtype W)
+// streaming passes (any shape, any size; work dtype W)
 // ---------------------------------------------------------------------------
+// The five passes of the scalar step over a range of elements, and the
+// per-tensor finishes between them, in two launch forms:
+//   - scalar_stream_kernel: one workgroup per tensor runs every pass over the
+//     whole tensor, with block reductions between the passes;
+//   - the wide form (tensors of SR_WIDE_MIN elements or more): each pass is
+//     one launch over chunks of SR_WIDE_CH elements of every tensor of the
+//     group, writing block partials; a finish kernel (one workgroup per
+//     tensor) reduces them in block order and carries the tensor's values
+//     (StreamCtl, in the plan table) to the next pass.  Nine launches per
+//     step, but a large tensor uses the whole GPU instead of one CU.
+// Axis sums of the instant metric are 64-bit fixed-point integer atomics, so
+// both forms get the same sums whatever the arrival order.
+template <typename W> struct StreamCtl {
+    W q0, imp, mq, mp, fr, de, sur, act;   // state scalars, advanced by the finishes
+    W scale, inv_s, sM, gden, gain;
+    DriveCoef<W> dc;
+    int32_t step;
+};
+constexpr int SR_WIDE_NT = 256;              // threads per block of the wide form
+constexpr int64_t SR_WIDE_CH = 8192;         // elements per block of the wide form
+constexpr int64_t SR_WIDE_MIN = 131072;      // non-resident tensors this large use the wide form
+constexpr size_t SR_CTL_BYTES = 256;         // table bytes of one StreamCtl
+static_assert(sizeof(StreamCtl<double>) <= SR_CTL_BYTES, "StreamCtl slot");
+
 template <typename W, typename T> __device__ __forceinline__ W ldw(const T* p, int64_t i) { return to_w<W>(p[i]); }
 
-template <typename W, typename PT, typename GT>
-__global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* __restrict__ recs, int32_t* __restrict__ steps,
-                                                              const void* const* __restrict__ grads, int32_t first,
-                                                              unsigned char* table, cresso_hyper h) {
-    __shared__ double red[16 * 13];
-    __shared__ int s_step;
-    const int tid = threadIdx.x;
-    const int ri = first + blockIdx.x;
-    const ScalarRec& R = recs[ri];
-    const int64_t n = R.d.numel;
-    const int nd = R.d.ndim;
-    const int layout = R.layout;
-    const W eps = (W)h.eps;
-    W* sp[8];
-    for (int i = 0; i < 8; ++i) sp[i] = reinterpret_cast<W*>(R.d.state[i]);
-    W q0 = *sp[0], imp = *sp[1], mq = *sp[2], mp = *sp[3], fr = *sp[4], de = *sp[5], sur = *sp[6], act = *sp[7];
-    if (tid == 0) {
-        const int s = steps[ri] + 1;
-        steps[ri] = s;
-        s_step = s;
-    }
-    const GT* __restrict__ g = reinterpret_cast<const GT*>(grads[ri]);
-    PT* __restrict__ p = reinterpret_cast<PT*>(R.d.param);
-    const bool wd_on = h.weight_decay != 0.0;
-    const W wd = (W)h.weight_decay;
-    const bool neg = h.maximize != 0;
-    auto force = [&](int64_t i) -> W {
-        W f = ldw<W>(g, i);
-        if (neg) f = -f;
-        if (wd_on) f = f + wd * ldw<W>(p, i);
-        return f;
-    };
-    unsigned long long* axis_fx = reinterpret_cast<unsigned long long*>(table + R.scratch_off);
-    W* axis_fac = reinterpret_cast<W*>(table + R.scratch_off + sizeof(unsigned long long) * R.sum_dims);
-    const double dn = (double)n;
-    const bool axes = layout == L_GENERIC || layout == L_2D;
-    // L_2D: (row, col) of element i = tid + k NT advanced without divisions
-    const uint32_t C2 = layout == L_2D ? (uint32_t)R.cols : 1u, R2 = layout == L_2D ? (uint32_t)R.rows : 1u;
-    const uint32_t dC = (uint32_t)SR_NT % C2, dR = (uint32_t)SR_NT / C2;
-    const uint32_t row0 = (uint32_t)tid / C2, col0 = (uint32_t)tid % C2;
-    auto advance = [&](uint32_t& row, uint32_t& col) {
+// Row and column of a linear index in an L_2D tensor, advanced by a fixed
+// stride without divisions.
+struct Walk2D {
+    uint32_t row, col, dR, dC, C;
+    __device__ __forceinline__ void next() {
         col += dC;
         row += dR;
-        if (col >= C2) {
-            col -= C2;
+        if (col >= C) {
+            col -= C;
             ++row;
         }
-    };
-
-    // ---- pass A ----
-    W a = 0;
-    for (int64_t i = tid; i < n; i += SR_NT) {
-        const W f = force(i);
-        a += f * f;
     }
-    if (axes)
-        for (int64_t i = tid; i < R.sum_dims; i += SR_NT) axis_fx[i] = 0ull;
-    __syncthreads();
-    const int step = s_step;
-    {
-        double v[1] = {(double)a};
-        block_sum<1>(v, red);
-        fr = reservoir(fr, (W)sqrt((double)((W)(v[0] / dn) + eps)), h.reservoir_decay, step);
-    }
-    const W scale = fr > eps ? fr : eps;
-    const W inv_s = (W)1 / scale;
+};
 
-    // ---- pass B ----
-    const W pw = (W)h.energy_power;
-    const W ipw = (W)fmax(h.instant_metric_power, 0.25);
-    const W kappa = nd > 0 ? (W)(h.instant_metric_coupling / ((double)nd * fmax(h.instant_metric_power, 0.25))) : (W)0;
-    const double fx_scale = ldexp(1.0, R.frac_bits);
-    auto density = [&](W f) -> W {
+template <typename W, typename PT, typename GT> struct Stream {
+    const ScalarRec& R;
+    const cresso_hyper& h;
+    const GT* __restrict__ g;
+    PT* __restrict__ p;
+    int64_t n;
+    double dn;
+    int nd, layout;
+    bool wd_on, neg, ls_on, axes;
+    W eps, wd, pw, ipw, kappa, ls, clip, iclip, clip2;
+    uint32_t C2, R2;   // L_2D cols and rows (1 otherwise)
+    bool mulfac;       // axis factors stored as exp(kappa log r) and multiplied
+    double fx_scale;
+    unsigned long long* axis_fx;
+    W* axis_fac;
+
+    __device__ Stream(const ScalarRec& r, const cresso_hyper& hy, const void* grad, unsigned char* table) : R(r), h(hy) {
+        g = reinterpret_cast<const GT*>(grad);
+        p = reinterpret_cast<PT*>(R.d.param);
+        n = R.d.numel;
+        dn = (double)n;
+        nd = R.d.ndim;
+        layout = R.layout;
+        wd_on = h.weight_decay != 0.0;
+        neg = h.maximize != 0;
+        ls_on = h.local_sharpness != 0.0;
+        axes = layout == L_GENERIC || layout == L_2D;
+        eps = (W)h.eps;
+        wd = (W)h.weight_decay;
+        pw = (W)h.energy_power;
+        ipw = (W)fmax(h.instant_metric_power, 0.25);
+        kappa = nd > 0 ? (W)(h.instant_metric_coupling / ((double)nd * fmax(h.instant_metric_power, 0.25))) : (W)0;
+        ls = (W)h.local_sharpness;
+        clip = (W)h.drive_clip;
+        iclip = (W)1 / clip;
+        clip2 = clip * clip;
+        C2 = layout == L_2D ? (uint32_t)R.cols : 1u;
+        R2 = layout == L_2D ? (uint32_t)R.rows : 1u;
+        // r = axis mean / global mean lies in [eps, 1e6 / eps], so the product of
+        // the nd factors r^kappa stays within exp(+-kappa nd log(1e6 / eps)): when
+        // that is inside the work dtype's range, the factors are stored as powers
+        // and multiplied (no exp per element); otherwise as logs, summed, exp'd
+        mulfac = (double)kappa * (double)nd * log(1.0e6 / fmin(h.eps, 0.5)) < (sizeof(W) == 8 ? 600.0 : 80.0);
+        fx_scale = ldexp(1.0, R.frac_bits);
+        axis_fx = reinterpret_cast<unsigned long long*>(table + R.scratch_off);
+        axis_fac = reinterpret_cast<W*>(table + R.scratch_off + sizeof(unsigned long long) * R.sum_dims);
+    }
+
+    __device__ W* st(int k) const { return reinterpret_cast<W*>(R.d.state[k]); }
+    __device__ void load_state(StreamCtl<W>& c) const {
+        c.q0 = *st(0); c.imp = *st(1); c.mq = *st(2); c.mp = *st(3);
+        c.fr = *st(4); c.de = *st(5); c.sur = *st(6); c.act = *st(7);
+    }
+    __device__ void store_state(const StreamCtl<W>& c) const {
+        *st(0) = c.dc.q1; *st(1) = c.imp; *st(2) = c.mq; *st(3) = c.mp;
+        *st(4) = c.fr; *st(5) = c.de; *st(6) = c.sur; *st(7) = c.act;
+    }
+
+    // force from the grad and the element's param value pv (read only under weight decay)
+    __device__ unsigned long long fx(W v) const { return (unsigned long long)llrint((double)v * fx_scale); }
+    __device__ W force(int64_t i, W pv) const {
+        W f = ldw<W>(g, i);
+        if (neg) f = -f;
+        if (wd_on) f = f + wd * pv;
+        return f;
+    }
+    static constexpr int U = sizeof(W) == 8 ? 2 : 8;   // elements per thread whose loads are in flight together
+
+    // The element's axis factors: L_2D the row's and the column's; GENERIC
+    // their product (mulfac) or sum in fa, the identity in fb.
+    __device__ void axis_load(int64_t i, const Walk2D& w, W& fa, W& fb) const {
+        if (layout == L_2D) {
+            fa = axis_fac[w.row];
+            fb = axis_fac[R2 + w.col];
+        } else if (layout == L_GENERIC) {
+            W acc = mulfac ? (W)1 : (W)0;
+            for (int ax = 0; ax < nd; ++ax) {
+                const W v = axis_fac[R.axis_off[ax] + (i / R.stride[ax]) % R.d.shape[ax]];
+                acc = mulfac ? acc * v : acc + v;
+            }
+            fa = acc;
+            fb = mulfac ? (W)1 : (W)0;
+        }
+    }
+
+    // fn(f, pv, fa, fb) for elements i = i0 + tid + k S < i1 in order; the
+    // loads of U elements (grad; param when PV or under weight decay; axis
+    // factors when AX) are issued before any of them is used.
+    template <bool PV, bool AX, typename F>
+    __device__ void each(int64_t i0, int64_t i1, int tid, int S, F&& fn) const {
+        Walk2D w = walk(i0 + tid, S);
+        for (int64_t ib = i0 + tid; ib < i1; ib += (int64_t)U * S) {
+            W f[U], pv[U], fa[U], fb[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t i = ib + (int64_t)u * S;
+                pv[u] = 0;
+                f[u] = 0;
+                fa[u] = 0;
+                fb[u] = 0;
+                if (i < i1) {
+                    if (PV || wd_on) pv[u] = ldw<W>(p, i);
+                    f[u] = force(i, pv[u]);
+                    if (AX) axis_load(i, w, fa[u], fb[u]);
+                }
+                w.next();
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (ib + (int64_t)u * S < i1) fn(f[u], pv[u], fa[u], fb[u]);
+        }
+    }
+    // Same over whole waves: every lane of a wave makes the same calls
+    // fn(i, ok, f, w), with ok false (and f = 0) past i1.
+    template <typename F>
+    __device__ void each_wave(int64_t i0, int64_t i1, int tid, int S, F&& fn) const {
+        const int lane = tid & 63;
+        Walk2D w = walk(i0 + tid, S);
+        for (int64_t wb = i0 + (tid - lane); wb < i1; wb += (int64_t)U * S) {
+            W f[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t i = wb + (int64_t)u * S + lane;
+                f[u] = 0;
+                if (i < i1) f[u] = force(i, wd_on ? ldw<W>(p, i) : (W)0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t iw = wb + (int64_t)u * S;
+                if (iw < i1) fn(iw + lane, iw + lane < i1, f[u], w);
+                w.next();
+            }
+        }
+    }
+    __device__ W density(W f, W inv_s) const {
         W rel = (f < 0 ? -f : f) * inv_s + eps;
         rel = rel < (W)1e4 ? rel : (W)1e4;
         rel = rel > eps ? rel : eps;
         const W d = ipw == (W)1 ? rel : fpow(rel, ipw);
         return d < (W)1e6 ? d : (W)1e6;
-    };
-    W aL = 0, aD = 0;
-    // L_2D axis sums, pre-aggregated where lanes share a row or a column:
-    //   rows: a wave lies in one row when cols % 64 == 0 (wave total); aligned
-    //     groups of cols lanes hold one row when cols divides 64 (group total);
-    //   cols: a thread's column is fixed when cols divides NT (one register);
-    // each partial goes to the fixed-point sums once (integer atomics: the
-    // result does not depend on arrival order).
-    const int lane = tid & 63;
-    const int rowmode = layout != L_2D ? 0 : (C2 % 64u == 0 ? 1 : ((64u % C2 == 0) ? 2 : 0));
-    const bool colreg = layout == L_2D && (uint32_t)SR_NT % C2 == 0;
-    double colacc = 0;
-    {
-        uint32_t row = row0, col = col0;
-        for (int64_t i = tid; i < n; i += SR_NT) {
-            const W f = force(i);
-            const W r = (f < 0 ? -f : f) * inv_s + eps;
-            aL += flog1p(fpow(r, pw));
-            const W d = density(f);
-            aD += d;
-            if (layout == L_GENERIC) {
-                const unsigned long long v = (unsigned long long)llrint((double)d * fx_scale);
-                for (int ax = 0; ax < nd; ++ax) atomicAdd(&axis_fx[R.axis_off[ax] + (i / R.stride[ax]) % R.d.shape[ax]], v);
-            } else if (layout == L_2D) {
-                if (rowmode == 1) {
-                    const W w = lanes_group_sum_w<W>(d, 64);   // the wave's (one row's) sum, in every lane
-                    if (lane == 0) atomicAdd(&axis_fx[row], (unsigned long long)llrint((double)w * fx_scale));
-                } else if (rowmode == 2) {
-                    const W w = lanes_group_sum_w<W>(d, (int)C2);
-                    if ((uint32_t)lane % C2 == 0) atomicAdd(&axis_fx[row], (unsigned long long)llrint((double)w * fx_scale));
-                } else {
-                    atomicAdd(&axis_fx[row], (unsigned long long)llrint((double)d * fx_scale));
-                }
-                if (colreg)
-                    colacc += (double)d;
-                else
-                    atomicAdd(&axis_fx[R2 + col], (unsigned long long)llrint((double)d * fx_scale));
-            }
-            advance(row, col);
+    }
+    // the walk of elements i, i + S, ... (L_2D only; n < 2^31 there)
+    __device__ Walk2D walk(int64_t i, int S) const {
+        Walk2D w{0u, 0u, 0u, 0u, C2};
+        if (layout == L_2D) {
+            w.row = (uint32_t)i / C2;
+            w.col = (uint32_t)i % C2;
+            w.dR = (uint32_t)S / C2;
+            w.dC = (uint32_t)S % C2;
         }
-        if (colreg && tid < n) atomicAdd(&axis_fx[R2 + col0], (unsigned long long)llrint(colacc * fx_scale));
+        return w;
     }
-    double gmean;
-    {
-        double v[2] = {(double)aL, (double)aD};
-        block_sum<2>(v, red);
-        const W dens_mean = (W)(v[0] / dn);
-        gmean = v[1] / dn;
-        const W mport = dens_mean - (W)tanh((double)mq);
-        mp = mp * (W)fmax(0.0, 1.0 - h.metric_dt * h.metric_friction);
-        mp = mp + (W)h.metric_dt * (mport - mq);
-        mq = mq + (W)h.metric_dt * mp;
-        mq = mq < (W)-3 ? (W)-3 : (mq > (W)3 ? (W)3 : mq);
-    }
-    W metric = (W)exp((double)((W)h.metric_coupling * mq));
-    metric = metric < (W)0.06 ? (W)0.06 : (metric > (W)16 ? (W)16 : metric);
-    const W gden = (W)fmax(gmean, (double)eps);
-    if (axes) {
-        for (int64_t i = tid; i < R.sum_dims; i += SR_NT) {
-            int ax = 0;
-            while (ax + 1 < nd && i >= R.axis_off[ax + 1]) ++ax;
-            const unsigned long long raw = __hip_atomic_load(&axis_fx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const W mean = (W)((double)(long long)raw / fx_scale / (dn / (double)R.d.shape[ax]));
-            const W r = mean / gden;
-            axis_fac[i] = kappa * flog(r > eps ? r : eps);
-        }
-        __syncthreads();
-    }
-    const W sM = scale * metric;
-    const bool ls_on = h.local_sharpness != 0.0;
-    const W ls = (W)h.local_sharpness;
-    auto tangent = [&](W f, int64_t i, uint32_t row, uint32_t col) -> W {
-        W den = sM;
+    // fa, fb: the element's axis factors from axis_load
+    __device__ W tangent(const StreamCtl<W>& c, W f, W fa, W fb) const {
+        W den = c.sM;
         if (ls_on) {
-            W rel = (f < 0 ? -f : f) * inv_s + eps;
+            W rel = (f < 0 ? -f : f) * c.inv_s + eps;
             rel = rel < (W)100 ? rel : (W)100;
             W lm = (W)1 + ls * fsqrt(rel);
             den = den * (lm < (W)1 ? (W)1 : (lm > (W)8 ? (W)8 : lm));
         }
         W inst = 1;
         if (layout == L_1D) {
-            const W r = density(f) / gden;
+            const W r = density(f, c.inv_s) / c.gden;
             inst = fexp(kappa * flog(r > eps ? r : eps));
-        } else if (layout == L_GENERIC) {
-            W ls_ = 0;
-            for (int ax = 0; ax < nd; ++ax) ls_ += axis_fac[R.axis_off[ax] + (i / R.stride[ax]) % R.d.shape[ax]];
-            inst = fexp(ls_);
-        } else if (layout == L_2D) {
-            inst = fexp(axis_fac[row] + axis_fac[R2 + col]);
+        } else if (layout == L_GENERIC || layout == L_2D) {
+            inst = mulfac ? fa * fb : fexp(fa + fb);
         }
         if (layout != L_NONE) inst = inst < (W)0.08 ? (W)0.08 : (inst > (W)12 ? (W)12 : inst);
-        W t = f / (den * inst + eps);
+        W t = f * frcp(den * inst + eps);
         return t < (W)-1e4 ? (W)-1e4 : (t > (W)1e4 ? (W)1e4 : t);
-    };
-    const W clip = (W)h.drive_clip, iclip = (W)1 / clip, clip2 = clip * clip;
-
-    // ---- pass C ----
-    W m[13];
-    for (int j = 0; j < 13; ++j) m[j] = 0;
-    uint32_t row = row0, col = col0;
-    for (int64_t i = tid; i < n; i += SR_NT, advance(row, col)) {
-        const W t = tangent(force(i), i, row, col);
+    }
+    __device__ W drive(const StreamCtl<W>& c, W t) const {
         W rat, bnd, root;
         shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
-        const W e = t - q0;
-        m[0] += e; m[1] += e * e; m[2] += t; m[3] += t * t;
-        m[4] += rat * rat; m[5] += bnd * bnd; m[6] += root * root;
-        m[7] += rat * bnd; m[8] += rat * root; m[9] += bnd * root;
-        m[10] += t * rat; m[11] += t * bnd; m[12] += t * root;
+        const W e = t - c.dc.q1;
+        const W nov = ftanh(e * c.dc.nscale) * clip;
+        const W core = c.dc.cr * rat + c.dc.cb * bnd + c.dc.co * root + c.dc.ct * t;
+        return c.dc.cA * core + c.dc.cB + c.dc.cN * nov + c.dc.cD * e;
     }
-    double M[13];
-    for (int j = 0; j < 13; ++j) M[j] = (double)m[j];
-    block_sum<13>(M, red);
-    const DriveCoef<W> dc = contact_and_coefs<W>(M, dn, h, step, q0, imp, act, sur);
-    auto drive = [&](W t) -> W {
-        W rat, bnd, root;
-        shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
-        const W e = t - dc.q1;
-        const W nov = ftanh(e * dc.nscale) * clip;
-        const W core = dc.cr * rat + dc.cb * bnd + dc.co * root + dc.ct * t;
-        return dc.cA * core + dc.cB + dc.cN * nov + dc.cD * e;
-    };
 
-    // ---- pass D ----
-    W add = 0;
-    row = row0;
-    col = col0;
-    for (int64_t i = tid; i < n; i += SR_NT, advance(row, col)) {
-        const W d = drive(tangent(force(i), i, row, col));
-        add += d * d;
+    // ---- passes over elements i0 + tid + k S < i1 (the whole block calls them) ----
+    __device__ W passA(int64_t i0, int64_t i1, int tid, int S) const {
+        W a = 0;
+        each<false, false>(i0, i1, tid, S, [&](W f, W, W, W) { a += f * f; });
+        return a;
     }
-    {
-        double v[1] = {(double)add};
-        block_sum<1>(v, red);
-        de = reservoir(de, (W)(v[0] / dn), h.reservoir_decay, step);
+    // Energy and instant density sums, and the axis sums (64-bit fixed-point
+    // atomics).  L_2D sums are first reduced across the lanes that share a row
+    // or a column, so each partial meets the atomics once:
+    //   rows: cols % 64 == 0: a wave lies in one row (wave total); cols divides
+    //     64: aligned groups of cols lanes (group total); otherwise a segmented
+    //     sum over the wave's runs of equal rows (rows grow with the lane);
+    //   cols: cols divides S: a thread's column is fixed (one register, reduced
+    //     over the lanes l, l + cols, ... at the end); cols < 64: lanes l,
+    //     l + cols, ... of each wave; otherwise one atomic per element.
+    // Callers keep i0 and S multiples of 64 (S also of cols when cols divides
+    // 64), and every lane of a wave runs the same iterations (lanes past i1 add
+    // nothing), so the wave-wide reductions always see whole waves.
+    // lds: S doubles (column partials of colmode 1).
+    __device__ void passB(const StreamCtl<W>& c, int64_t i0, int64_t i1, int tid, int S, W& aL, W& aD,
+                          double* lds) const {
+        const int lane = tid & 63;
+        const bool l2d = layout == L_2D;
+        const int rowmode = !l2d ? 0 : (C2 % 64u == 0 ? 1 : (64u % C2 == 0 ? 2 : 3));
+        const int colmode = !l2d ? 0 : ((uint32_t)S % C2 == 0 ? 1 : (C2 < 64u ? 2 : 3));
+        W colacc = 0;
+        const uint32_t col0 = walk(i0 + tid, S).col;
+        each_wave(i0, i1, tid, S, [&](int64_t i, bool ok, W f, const Walk2D& w) {
+            W d = 0;
+            if (ok) {
+                const W r = (f < 0 ? -f : f) * c.inv_s + eps;
+                aL += flog1p(fpow(r, pw));
+                d = density(f, c.inv_s);
+                aD += d;
+                if (layout == L_GENERIC)
+                    for (int ax = 0; ax < nd; ++ax) atomicAdd(&axis_fx[R.axis_off[ax] + (i / R.stride[ax]) % R.d.shape[ax]], fx(d));
+            }
+            if (!l2d) return;
+            if (rowmode == 1) {
+                const W s = lanes_group_sum_w<W>(d, 64);   // the wave's (one row's) sum, in every lane
+                if (lane == 0) atomicAdd(&axis_fx[w.row], fx(s));
+            } else if (rowmode == 2) {
+                const W s = lanes_group_sum_w<W>(d, (int)C2);
+                if (ok && (uint32_t)lane % C2 == 0) atomicAdd(&axis_fx[w.row], fx(s));
+            } else {
+                // suffix sums within runs of equal keys; a run's first lane holds its total
+                const uint32_t key = ok ? w.row : 0xFFFFFFFFu;
+                W s = d;
+                for (int off = 1; off < 64; off <<= 1) {
+                    const W o = __shfl_down(s, off, 64);
+                    const uint32_t ko = __shfl_down(key, off, 64);
+                    if (lane + off < 64 && ko == key) s += o;
+                }
+                const uint32_t kp = __shfl_up(key, 1, 64);
+                if (ok && (lane == 0 || kp != key)) atomicAdd(&axis_fx[w.row], fx(s));
+            }
+            if (colmode == 1) {
+                colacc += d;
+            } else if (colmode == 2) {
+                W s = d;
+                for (uint32_t off = C2; off < 64u; off += C2) {
+                    const W o = __shfl(d, lane + (int)off, 64);
+                    if ((uint32_t)lane + off < 64u) s += o;
+                }
+                if (ok && (uint32_t)lane < C2) atomicAdd(&axis_fx[R2 + w.col], fx(s));
+            } else if (ok) {
+                atomicAdd(&axis_fx[R2 + w.col], fx(d));
+            }
+        });
+        if (colmode == 1) {
+            // threads of one column: tid = col, col + cols, ... (col0 = tid % cols);
+            // summed in thread order through LDS, one atomic per column
+            lds[tid] = (double)colacc;   // zero for threads without elements
+            __syncthreads();
+            if ((uint32_t)tid < C2) {
+                double s = 0.0;
+                for (int k = tid; k < S; k += (int)C2) s += lds[k];
+                atomicAdd(&axis_fx[R2 + col0], (unsigned long long)llrint(s * fx_scale));
+            }
+            __syncthreads();
+        }
     }
-    W gain = (W)h.target_update_rms / (W)sqrt((double)(de + eps));
-    gain = gain < (W)h.min_gain ? (W)h.min_gain : (gain > (W)h.max_gain ? (W)h.max_gain : gain);
+    // Wide form, L_2D with more than 256 columns: block k of nblk takes tiles
+    // k, k + nblk, ... of 32 rows x 256 columns.  Thread t owns column c0 + t
+    // of a tile, so its column sum is one register and each row's sum is a
+    // block reduction: one atomic per tile column and per tile row.
+    // lds: 128 doubles.
+    __device__ void passB_tiles(const StreamCtl<W>& c, int64_t k, int64_t nblk, int tid, W& aL, W& aD, double* lds) const {
+        const int lane = tid & 63, wave = tid >> 6;
+        const uint32_t ncs = (C2 + 255u) / 256u, nrs = (R2 + 31u) / 32u;
+        const int64_t ntiles = (int64_t)ncs * nrs;
+        for (int64_t t = k; t < ntiles; t += nblk) {
+            const uint32_t r0 = (uint32_t)(t / ncs) * 32u, col = (uint32_t)(t % ncs) * 256u + (uint32_t)tid;
+            const bool cok = col < C2;
+            const uint32_t nr = R2 - r0 < 32u ? R2 - r0 : 32u;
+            W colsum = 0;
+            for (uint32_t rb = 0; rb < nr; rb += U) {
+                W f[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t r = rb + (uint32_t)u;
+                    f[u] = 0;
+                    if (cok && r < nr) {
+                        const int64_t i = (int64_t)(r0 + r) * C2 + col;
+                        f[u] = force(i, wd_on ? ldw<W>(p, i) : (W)0);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t r = rb + (uint32_t)u;
+                    if (r < nr) {   // uniform over the block
+                        W d = 0;
+                        if (cok) {
+                            const W fv = f[u];
+                            const W rr = (fv < 0 ? -fv : fv) * c.inv_s + eps;
+                            aL += flog1p(fpow(rr, pw));
+                            d = density(fv, c.inv_s);
+                            aD += d;
+                        }
+                        colsum += d;
+                        const W ws = lanes_group_sum_w<W>(d, 64);   // this wave's part of row r0 + r
+                        if (lane == 0) lds[wave * 32 + (int)r] = (double)ws;
+                    }
+                }
+            }
+            if (cok) atomicAdd(&axis_fx[R2 + col], fx(colsum));
+            __syncthreads();
+            if ((uint32_t)tid < nr) {
+                const double s = lds[tid] + lds[32 + tid] + lds[64 + tid] + lds[96 + tid];
+                atomicAdd(&axis_fx[r0 + (uint32_t)tid], (unsigned long long)llrint(s * fx_scale));
+            }
+            __syncthreads();
+        }
+    }
+    __device__ void passC(const StreamCtl<W>& c, int64_t i0, int64_t i1, int tid, int S, W (&m)[13]) const {
+        for (int j = 0; j < 13; ++j) m[j] = 0;
+        each<false, true>(i0, i1, tid, S, [&](W f, W, W fa, W fb) {
+            const W t = tangent(c, f, fa, fb);
+            W rat, bnd, root;
+            shape3(t, iclip, clip, clip2, eps, rat, bnd, root);
+            const W e = t - c.q0;
+            m[0] += e; m[1] += e * e; m[2] += t; m[3] += t * t;
+            m[4] += rat * rat; m[5] += bnd * bnd; m[6] += root * root;
+            m[7] += rat * bnd; m[8] += rat * root; m[9] += bnd * root;
+            m[10] += t * rat; m[11] += t * bnd; m[12] += t * root;
+        });
+    }
+    __device__ W passD(const StreamCtl<W>& c, int64_t i0, int64_t i1, int tid, int S) const {
+        W add = 0;
+        each<false, true>(i0, i1, tid, S, [&](W f, W, W fa, W fb) {
+            const W d = drive(c, tangent(c, f, fa, fb));
+            add += d * d;
+        });
+        return add;
+    }
+    // param -= lr * cast(drive * gain); each element's grad and param are read
+    // before this thread stores that element
+    __device__ void passE(const StreamCtl<W>& c, int64_t i0, int64_t i1, int tid, int S) const {
+        const W nlr = (W)(-h.lr);
+        int64_t i = i0 + tid;
+        each<true, true>(i0, i1, tid, S, [&](W f, W pv, W fa, W fb) {
+            const W d = drive(c, tangent(c, f, fa, fb));
+            const W u = to_w<W>(from_wd<PT>((double)(d * c.gain)));
+            p[i] = from_wd<PT>((double)(pv + nlr * u));
+            i += S;
+        });
+    }
 
-    // ---- pass E ---- (force is recomputed before any param store of this thread)
-    const W nlr = (W)(-h.lr);
-    row = row0;
-    col = col0;
-    for (int64_t i = tid; i < n; i += SR_NT, advance(row, col)) {
-        const W d = drive(tangent(force(i), i, row, col));
-        const W u = to_w<W>(from_wd<PT>((double)(d * gain)));
-        p[i] = from_wd<PT>((double)(ldw<W>(p, i) + nlr * u));
+    // ---- finishes on the tensor's totals (every thread, identical results) ----
+    __device__ void finA(StreamCtl<W>& c, double sff) const {
+        c.fr = reservoir(c.fr, (W)sqrt((double)((W)(sff / dn) + eps)), h.reservoir_decay, c.step);
+        c.scale = c.fr > eps ? c.fr : eps;
+        c.inv_s = (W)1 / c.scale;
     }
+    // scalar metric oscillator (cresso_v5.py:1510-1518) and the density normaliser
+    __device__ void finB(StreamCtl<W>& c, double sL, double sD) const {
+        const W dens_mean = (W)(sL / dn);
+        const W mport = dens_mean - (W)tanh((double)c.mq);
+        c.mp = c.mp * (W)fmax(0.0, 1.0 - h.metric_dt * h.metric_friction);
+        c.mp = c.mp + (W)h.metric_dt * (mport - c.mq);
+        c.mq = c.mq + (W)h.metric_dt * c.mp;
+        c.mq = c.mq < (W)-3 ? (W)-3 : (c.mq > (W)3 ? (W)3 : c.mq);
+        W metric = (W)exp((double)((W)h.metric_coupling * c.mq));
+        metric = metric < (W)0.06 ? (W)0.06 : (metric > (W)16 ? (W)16 : metric);
+        c.sM = c.scale * metric;
+        c.gden = (W)fmax(sD / dn, (double)eps);
+    }
+    // kappa log(max(axis mean / gden, eps)) of axis entries a0 + tid + k S < a1
+    __device__ void axis_factors(const StreamCtl<W>& c, int64_t a0, int64_t a1, int tid, int S) const {
+        for (int64_t i = a0 + tid; i < a1; i += S) {
+            int ax = 0;
+            while (ax + 1 < nd && i >= R.axis_off[ax + 1]) ++ax;
+            const unsigned long long raw = __hip_atomic_load(&axis_fx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const W mean = (W)((double)(long long)raw / fx_scale / (dn / (double)R.d.shape[ax]));
+            const W r = mean / c.gden;
+            const W lf = kappa * flog(r > eps ? r : eps);
+            axis_fac[i] = mulfac ? fexp(lf) : lf;
+        }
+    }
+    __device__ void finC(StreamCtl<W>& c, const double* M) const {
+        c.dc = contact_and_coefs<W>(M, dn, h, c.step, c.q0, c.imp, c.act, c.sur);
+    }
+    __device__ void finD(StreamCtl<W>& c, double sdd) const {
+        c.de = reservoir(c.de, (W)(sdd / dn), h.reservoir_decay, c.step);
+        W gain = (W)h.target_update_rms / (W)sqrt((double)(c.de + eps));
+        c.gain = gain < (W)h.min_gain ? (W)h.min_gain : (gain > (W)h.max_gain ? (W)h.max_gain : gain);
+    }
+};
+
+template <typename W, typename PT, typename GT>
+__global__ __launch_bounds__(SR_NT) void scalar_stream_kernel(const ScalarRec* __restrict__ recs, int32_t* __restrict__ steps,
+                                                              const void* const* __restrict__ grads, int32_t first,
+                                                              unsigned char* table, cresso_hyper h) {
+    __shared__ double red[SR_NT];   // block sums (16 x 13) and pass B's column partials
+    __shared__ int s_step;
+    const int tid = threadIdx.x;
+    const int ri = first + blockIdx.x;
+    const Stream<W, PT, GT> S(recs[ri], h, grads[ri], table);
+    const int64_t n = S.n;
+    StreamCtl<W> c;
+    S.load_state(c);
     if (tid == 0) {
-        *sp[0] = dc.q1; *sp[1] = imp; *sp[2] = mq; *sp[3] = mp; *sp[4] = fr; *sp[5] = de; *sp[6] = sur; *sp[7] = act;
+        const int s = steps[ri] + 1;
+        steps[ri] = s;
+        s_step = s;
     }
+    // ---- pass A ----
+    const W a = S.passA(0, n, tid, SR_NT);
+    if (S.axes)
+        for (int64_t i = tid; i < S.R.sum_dims; i += SR_NT) S.axis_fx[i] = 0ull;
+    __syncthreads();
+    c.step = s_step;
+    {
+        double v[1] = {(double)a};
+        block_sum<1>(v, red);
+        S.finA(c, v[0]);
+    }
+    // ---- pass B ----
+    {
+        W aL = 0, aD = 0;
+        S.passB(c, 0, n, tid, SR_NT, aL, aD, red);
+        double v[2] = {(double)aL, (double)aD};
+        block_sum<2>(v, red);
+        S.finB(c, v[0], v[1]);
+    }
+    if (S.axes) {
+        S.axis_factors(c, 0, S.R.sum_dims, tid, SR_NT);
+        __syncthreads();
+    }
+    // ---- pass C ----
+    {
+        W m[13];
+        S.passC(c, 0, n, tid, SR_NT, m);
+        double M[13];
+        for (int j = 0; j < 13; ++j) M[j] = (double)m[j];
+        block_sum<13>(M, red);
+        S.finC(c, M);
+    }
+    // ---- pass D ----
+    {
+        double v[1] = {(double)S.passD(c, 0, n, tid, SR_NT)};
+        block_sum<1>(v, red);
+        S.finD(c, v[0]);
+    }
+    // ---- pass E ----
+    S.passE(c, 0, n, tid, SR_NT);
+    if (tid == 0) S.store_state(c);
+}
+
+// Wide form: block k of a tensor's nblk blocks owns axis entries
+// [axis_slice(k), axis_slice(k + 1)) (zeroed in pass A, turned into factors by
+// scalar_wide_axes).
+__device__ __forceinline__ int64_t axis_slice(const ScalarRec& R, int64_t k) {
+    const int64_t per = (R.sum_dims + R.nblk - 1) / R.nblk;
+    const int64_t a = k * per;
+    return a < R.sum_dims ? a : R.sum_dims;
+}
+
+// Wide form, pass PH (0..4 = A..E) over one chunk per block.  bmap[b] is the
+// tensor of block b; the tensor's chunks are its blocks blk0 .. blk0+nblk-1.
+// Block partials: part[b * 16 + v].
+template <typename W, typename PT, typename GT, int PH>
+__global__ __launch_bounds__(SR_WIDE_NT) void scalar_wide_pass(const ScalarRec* __restrict__ recs,
+                                                               const int32_t* __restrict__ bmap,
+                                                               const void* const* __restrict__ grads, unsigned char* table,
+                                                               double* __restrict__ part, cresso_hyper h) {
+    __shared__ double red[SR_WIDE_NT];   // block sums (4 x 13) and pass B's column or row partials
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x;
+    const int ri = bmap[b];
+    const ScalarRec& R = recs[ri];
+    const Stream<W, PT, GT> S(R, h, grads[ri], table);
+    const int64_t i0 = (int64_t)(b - R.blk0) * SR_WIDE_CH;
+    const int64_t i1 = S.n < i0 + SR_WIDE_CH ? S.n : i0 + SR_WIDE_CH;
+    double* out = part + (size_t)b * 16;
+    if constexpr (PH == 0) {
+        if (S.axes) {
+            // this block's slice of the axis sums starts at zero (pass B adds to them)
+            const int64_t a0 = axis_slice(R, b - R.blk0), a1 = axis_slice(R, b - R.blk0 + 1);
+            for (int64_t a = a0 + tid; a < a1; a += SR_WIDE_NT) S.axis_fx[a] = 0ull;
+        }
+        double v[1] = {(double)S.passA(i0, i1, tid, SR_WIDE_NT)};
+        block_sum<1>(v, red);
+        if (tid == 0) out[0] = v[0];
+        return;
+    } else {
+        const StreamCtl<W> c = *reinterpret_cast<const StreamCtl<W>*>(table + R.ctl_off);
+        if constexpr (PH == 1) {
+            W aL = 0, aD = 0;
+            if (S.layout == L_2D && S.C2 > 256u)
+                S.passB_tiles(c, b - R.blk0, R.nblk, tid, aL, aD, red);
+            else
+                S.passB(c, i0, i1, tid, SR_WIDE_NT, aL, aD, red);
+            __syncthreads();   // red is reused by the block sum
+            double v[2] = {(double)aL, (double)aD};
+            block_sum<2>(v, red);
+            if (tid == 0) {
+                out[0] = v[0];
+                out[1] = v[1];
+            }
+        } else if constexpr (PH == 2) {
+            W m[13];
+            S.passC(c, i0, i1, tid, SR_WIDE_NT, m);
+            double M[13];
+            for (int j = 0; j < 13; ++j) M[j] = (double)m[j];
+            block_sum<13>(M, red);
+            if (tid == 0)
+                for (int j = 0; j < 13; ++j) out[j] = M[j];
+        } else if constexpr (PH == 3) {
+            double v[1] = {(double)S.passD(c, i0, i1, tid, SR_WIDE_NT)};
+            block_sum<1>(v, red);
+            if (tid == 0) out[0] = v[0];
+        } else {
+            S.passE(c, i0, i1, tid, SR_WIDE_NT);
+        }
+    }
+}
+
+// Wide form, finish after pass PH (0..3): one workgroup per tensor sums the
+// tensor's block partials in block order and advances its StreamCtl.
+template <typename W, typename PT, typename GT, int PH>
+__global__ __launch_bounds__(SR_WIDE_NT) void scalar_wide_fin(const ScalarRec* __restrict__ recs, int32_t* __restrict__ steps,
+                                                              const void* const* __restrict__ grads, int32_t first,
+                                                              unsigned char* table, const double* __restrict__ part,
+                                                              cresso_hyper h) {
+    constexpr int V = PH == 1 ? 2 : (PH == 2 ? 13 : 1);
+    __shared__ double red[(SR_WIDE_NT / 64) * V];
+    __shared__ int s_step;
+    const int tid = threadIdx.x;
+    const int ri = first + blockIdx.x;
+    const ScalarRec& R = recs[ri];
+    const Stream<W, PT, GT> S(R, h, grads[ri], table);
+    StreamCtl<W>* cp = reinterpret_cast<StreamCtl<W>*>(table + R.ctl_off);
+    StreamCtl<W> c;
+    if (PH == 0) {
+        S.load_state(c);
+        if (tid == 0) {
+            const int s = steps[ri] + 1;
+            steps[ri] = s;
+            s_step = s;
+        }
+    } else {
+        c = *cp;
+    }
+    double v[V];
+    for (int j = 0; j < V; ++j) v[j] = 0.0;
+    for (int b = tid; b < R.nblk; b += SR_WIDE_NT)
+        for (int j = 0; j < V; ++j) v[j] += part[(size_t)(R.blk0 + b) * 16 + j];
+    block_sum<V>(v, red);   // its barriers also publish s_step
+    if (PH == 0) {
+        c.step = s_step;
+        S.finA(c, v[0]);
+    } else if (PH == 1) {
+        S.finB(c, v[0], v[1]);
+    } else if (PH == 2) {
+        S.finC(c, v);
+    } else {
+        S.finD(c, v[0]);
+        if (tid == 0) S.store_state(c);
+    }
+    if (tid == 0) *cp = c;
+}
+
+// Wide form, after finish B: block k of each tensor turns its slice of the
+// fixed-point axis sums into factors.
+template <typename W, typename PT, typename GT>
+__global__ __launch_bounds__(SR_WIDE_NT) void scalar_wide_axes(const ScalarRec* __restrict__ recs,
+                                                               const int32_t* __restrict__ bmap,
+                                                               const void* const* __restrict__ grads, unsigned char* table,
+                                                               cresso_hyper h) {
+    const int b = blockIdx.x;
+    const int ri = bmap[b];
+    const ScalarRec& R = recs[ri];
+    if (R.layout != L_GENERIC && R.layout != L_2D) return;
+    const Stream<W, PT, GT> S(R, h, grads[ri], table);
+    const StreamCtl<W> c = *reinterpret_cast<const StreamCtl<W>*>(table + R.ctl_off);
+    S.axis_factors(c, axis_slice(R, b - R.blk0), axis_slice(R, b - R.blk0 + 1), threadIdx.x, SR_WIDE_NT);
 }
 
 // ---------------------------------------------------------------------------
@@ -1197,7 +1586,7 @@ __global__ __launch_bounds__(SR_NT) void micro_kernel(const ScalarRec* __restric
 bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 struct Variant {
-    int pt, gt, kind;   // kind: 0 stream, 1 resident (row-group or column-block layout), 3 micro field
+    int pt, gt, kind;   // kind: 0 stream, 1 resident (row-group or column-block layout), 2 wide stream, 3 micro field
     bool full;          // resident with numel == SR_RESIDENT_MAX: eligible for the FAST kernel
     bool operator==(const Variant& o) const { return pt == o.pt && gt == o.gt && kind == o.kind && full == o.full; }
 };
@@ -1309,8 +1698,9 @@ int32_t plan_desc(const cresso_scalar_desc& d, const cresso_hyper& h, ScalarRec&
             scratch = (scratch + 255) & ~(size_t)255;
         }
     }
-    r.resident = kind != 0;
-    v = Variant{d.param_dtype, d.grad_dtype, kind, kind != 0 && n == SR_RESIDENT_MAX};
+    if (kind == 0 && n >= SR_WIDE_MIN) kind = 2;
+    r.resident = kind == 1;
+    v = Variant{d.param_dtype, d.grad_dtype, kind, kind == 1 && n == SR_RESIDENT_MAX};
     return CRESSO_OK;
 }
 
@@ -1352,8 +1742,36 @@ hipError_t launch_stream(bool micro, const ScalarRec* recs, int32_t* steps, cons
     return hipGetLastError();
 }
 
+// The wide form's ten launches: pass A, finish A, pass B, finish B, axis
+// factors, pass C, finish C, pass D, finish D, pass E.
+template <typename W, typename PT, typename GT>
+hipError_t launch_wide(const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first, int32_t cnt,
+                       int32_t nblocks, const int32_t* bmap, unsigned char* table, double* part, const cresso_hyper& h,
+                       hipStream_t s) {
+    const dim3 pb(SR_WIDE_NT);
+    hipLaunchKernelGGL((scalar_wide_pass<W, PT, GT, 0>), dim3(nblocks), pb, 0, s, recs, bmap, grads, table, part, h);
+    hipLaunchKernelGGL((scalar_wide_fin<W, PT, GT, 0>), dim3(cnt), pb, 0, s, recs, steps, grads, first, table, part, h);
+    hipLaunchKernelGGL((scalar_wide_pass<W, PT, GT, 1>), dim3(nblocks), pb, 0, s, recs, bmap, grads, table, part, h);
+    hipLaunchKernelGGL((scalar_wide_fin<W, PT, GT, 1>), dim3(cnt), pb, 0, s, recs, steps, grads, first, table, part, h);
+    hipLaunchKernelGGL((scalar_wide_axes<W, PT, GT>), dim3(nblocks), pb, 0, s, recs, bmap, grads, table, h);
+    hipLaunchKernelGGL((scalar_wide_pass<W, PT, GT, 2>), dim3(nblocks), pb, 0, s, recs, bmap, grads, table, part, h);
+    hipLaunchKernelGGL((scalar_wide_fin<W, PT, GT, 2>), dim3(cnt), pb, 0, s, recs, steps, grads, first, table, part, h);
+    hipLaunchKernelGGL((scalar_wide_pass<W, PT, GT, 3>), dim3(nblocks), pb, 0, s, recs, bmap, grads, table, part, h);
+    hipLaunchKernelGGL((scalar_wide_fin<W, PT, GT, 3>), dim3(cnt), pb, 0, s, recs, steps, grads, first, table, part, h);
+    hipLaunchKernelGGL((scalar_wide_pass<W, PT, GT, 4>), dim3(nblocks), pb, 0, s, recs, bmap, grads, table, part, h);
+    return hipGetLastError();
+}
+
+// Launch geometry of a wide group: its block count and block map (in the table).
+struct WideGeom {
+    int32_t nblocks;
+    const int32_t* bmap;
+    double* part;
+};
+
 hipError_t dispatch(const Variant& v, const ScalarRec* recs, int32_t* steps, const void* const* grads, int32_t first,
-                    int32_t cnt, size_t lds, unsigned char* table, const cresso_hyper& h, hipStream_t s) {
+                    int32_t cnt, size_t lds, unsigned char* table, const WideGeom& wg, const cresso_hyper& h,
+                    hipStream_t s) {
     if (v.kind == 1) {
         const bool fast = v.full && fast_hyper(h);
         if (v.pt == CRESSO_F32) return launch_resident<float, float>(fast, recs, steps, grads, first, cnt, lds, h, s);
@@ -1362,8 +1780,10 @@ hipError_t dispatch(const Variant& v, const ScalarRec* recs, int32_t* steps, con
         if (v.pt == CRESSO_F16) return launch_resident<__half, __half>(fast, recs, steps, grads, first, cnt, lds, h, s);
         return hipErrorInvalidValue;
     }
-#define CRESSO_SR_CASE(PC, GC, W, PT, GT) \
-    if (v.pt == PC && v.gt == GC) return launch_stream<W, PT, GT>(v.kind == 3, recs, steps, grads, first, cnt, table, h, s);
+#define CRESSO_SR_CASE(PC, GC, W, PT, GT)                                                                            \
+    if (v.pt == PC && v.gt == GC)                                                                                    \
+        return v.kind == 2 ? launch_wide<W, PT, GT>(recs, steps, grads, first, cnt, wg.nblocks, wg.bmap, table, wg.part, h, s) \
+                           : launch_stream<W, PT, GT>(v.kind == 3, recs, steps, grads, first, cnt, table, h, s);
     CRESSO_SR_CASE(CRESSO_F32, CRESSO_F32, float, float, float)
     CRESSO_SR_CASE(CRESSO_BF16, CRESSO_BF16, float, __hip_bfloat16, __hip_bfloat16)
     CRESSO_SR_CASE(CRESSO_F16, CRESSO_F16, float, __half, __half)
@@ -1385,9 +1805,16 @@ struct cresso_scalar_plan {
     std::vector<cresso::ScalarRec> recs;     // grouped order
     std::vector<int32_t> steps;               // grouped order
     std::vector<int32_t> order;               // grouped index -> caller index
-    struct Group { cresso::Variant v; int32_t first, count; size_t lds; };
+    struct Group {
+        cresso::Variant v;
+        int32_t first, count;
+        size_t lds;
+        int32_t nblocks;   // wide form: blocks per pass launch
+        size_t map_off;    // wide form: table offset of the block map
+    };
     std::vector<Group> groups;
-    size_t steps_off = 0, grads_off = 0, total = 0;
+    std::vector<int32_t> bmap;                // wide form: block -> tensor, every wide group in turn
+    size_t steps_off = 0, grads_off = 0, bmap_off = 0, part_off = 0, total = 0;
     bool no_instant = false;                  // instant_metric_coupling == 0 at planning time
     const void** staging[2] = {nullptr, nullptr};
     hipEvent_t ev[2] = {nullptr, nullptr};
@@ -1421,17 +1848,41 @@ int32_t build_plan(const cresso_scalar_desc* descs, int32_t count, const cresso_
     P.recs.resize((size_t)count);
     P.steps.resize((size_t)count);
     P.groups.clear();
+    P.bmap.clear();
+    int32_t max_blocks = 0;
     for (int32_t j = 0; j < count; ++j) {
         const int32_t i = P.order[(size_t)j];
-        P.recs[(size_t)j] = recs[(size_t)i];
-        P.recs[(size_t)j].scratch_off = (int64_t)off;
+        ScalarRec& r = P.recs[(size_t)j];
+        r = recs[(size_t)i];
+        r.scratch_off = (int64_t)off;
         off += scr[(size_t)i];
         P.steps[(size_t)j] = descs[i].step;
         if (P.groups.empty() || !(P.groups.back().v == var[(size_t)i]))
-            P.groups.push_back({var[(size_t)i], j, 0, 0});
-        P.groups.back().count += 1;
-        P.groups.back().lds = std::max(P.groups.back().lds, lds[(size_t)i]);
+            P.groups.push_back({var[(size_t)i], j, 0, 0, 0, 0});
+        auto& G = P.groups.back();
+        G.count += 1;
+        G.lds = std::max(G.lds, lds[(size_t)i]);
+        if (G.v.kind == 2) {
+            r.ctl_off = (int64_t)off;
+            off += SR_CTL_BYTES;
+            const int64_t nb = (r.d.numel + SR_WIDE_CH - 1) / SR_WIDE_CH;
+            if (nb > (int64_t)INT32_MAX - G.nblocks)
+                return fail(CRESSO_E_UNSUPPORTED, "scalar route: wide group of more than 2^31 blocks");
+            if (G.nblocks == 0) G.map_off = sizeof(int32_t) * P.bmap.size();   // relative until placed below
+            r.blk0 = G.nblocks;
+            r.nblk = (int32_t)nb;
+            G.nblocks += (int32_t)nb;
+            P.bmap.insert(P.bmap.end(), (size_t)nb, j);
+            max_blocks = std::max(max_blocks, G.nblocks);
+        }
     }
+    // block maps, then one partials area shared by the wide groups (they run in turn)
+    P.bmap_off = off;
+    off += (sizeof(int32_t) * P.bmap.size() + 255) & ~(size_t)255;
+    for (auto& G : P.groups)
+        if (G.v.kind == 2) G.map_off += P.bmap_off;
+    P.part_off = off;
+    off += sizeof(double) * 16 * (size_t)max_blocks;
     P.total = off;
     P.no_instant = h.instant_metric_coupling == 0.0;
     return CRESSO_OK;
@@ -1497,6 +1948,8 @@ extern "C" int32_t cresso_scalar_plan_upload(cresso_scalar_plan* P, void* dev_ta
         for (size_t j = 0; j < count; ++j) g[j] = P->recs[j].d.grad;
         e = hipMemcpyAsync(table + P->grads_off, g.data(), sizeof(void*) * count, hipMemcpyHostToDevice, s);
     }
+    if (e == hipSuccess && !P->bmap.empty())
+        e = hipMemcpyAsync(table + P->bmap_off, P->bmap.data(), sizeof(int32_t) * P->bmap.size(), hipMemcpyHostToDevice, s);
     // pageable sources: make sure the copies have consumed them before returning
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "scalar route: table upload");
@@ -1530,7 +1983,9 @@ extern "C" int32_t cresso_scalar_plan_step(cresso_scalar_plan* P, void* dev_tabl
     int32_t* dsteps = reinterpret_cast<int32_t*>(table + P->steps_off);
     const void* const* dgrads = reinterpret_cast<const void* const*>(table + P->grads_off);
     for (const auto& G : P->groups) {
-        hipError_t e = dispatch(G.v, drecs, dsteps, dgrads, G.first, G.count, G.lds, table, h, s);
+        const WideGeom wg{G.nblocks, reinterpret_cast<const int32_t*>(table + G.map_off),
+                          reinterpret_cast<double*>(table + P->part_off)};
+        hipError_t e = dispatch(G.v, drecs, dsteps, dgrads, G.first, G.count, G.lds, table, wg, h, s);
         if (e != hipSuccess) return hip_fail(e, "scalar route: kernel launch");
     }
     return CRESSO_OK;

@@ -21,11 +21,12 @@ def test_scalar_2d_matches_oracle(shape):
     compare(*res)
 
 
-# 2-D tensors beyond the resident limit (streaming kernel, row/column axis sums):
-# (8192,64) and (64,8192): one row per wave; (8192,16): rows in groups of 16
-# lanes; (16,8192): a wave inside one row; (1000,60) and (3000,33): neither,
-# per-element row and column sums
-@pytest.mark.parametrize("shape", [(8192, 16), (16, 8192), (8192, 64), (64, 8192), (1000, 60), (3000, 33)])
+# 2-D tensors beyond the resident limit, row/column axis sums.  128 Ki elements
+# and more: the wide form (chunks over the whole GPU); below: one workgroup per
+# tensor.  (8192,64) and (64,8192): one row per wave; (8192,16): rows in groups
+# of 16 lanes; (16,8192): a wave inside one row; (1000,60), (3000,33) and
+# (5000,33): neither, per-element row and column sums
+@pytest.mark.parametrize("shape", [(8192, 16), (16, 8192), (8192, 64), (64, 8192), (1000, 60), (3000, 33), (5000, 33)])
 def test_scalar_streaming_2d_matches_oracle(shape):
     announce(f"scalar streaming 2d {shape}")
     res = run_pair([shape], torch.float32, SCALAR_KW, steps=3, seed=3)
@@ -36,11 +37,27 @@ def test_scalar_streaming_2d_options_and_dtypes():
     announce("scalar streaming 2d options")
     kw = dict(SCALAR_KW, maximize=True, weight_decay=0.01, instant_metric_power=0.7, local_sharpness=0.3)
     compare(*run_pair([(8192, 16), (2000, 48)], torch.float32, kw, steps=3, seed=4))
+    # a coupling this strong can push a product of axis factors past fp32's
+    # range, so the factors are kept as logs (summed, then one exp)
+    announce("scalar streaming 2d strong coupling")
+    kw = dict(SCALAR_KW, instant_metric_coupling=6.0)
+    compare(*run_pair([(8192, 16), (3000, 33), (16, 8192), (64, 48, 50)], torch.float32, kw, steps=3, seed=13))
     announce("scalar streaming 2d bf16 / f64")
     res = run_pair([(8192, 16), (40, 1000)], torch.bfloat16, SCALAR_KW, steps=3, seed=5)
     compare(*res, param_tol=BF16_PARAM_TOL, state_tol=dict(rtol=1e-2, atol=1e-3))
-    res = run_pair([(8192, 16), (40, 1000)], torch.float64, SCALAR_KW, steps=3, seed=6)
+    # f64 params are never resident: (1024,64), (64,1024) and (4096,16) take the
+    # one-workgroup kernel's wave, lane-group and per-thread column sums
+    res = run_pair([(8192, 16), (40, 1000), (1024, 64), (64, 1024), (4096, 16)], torch.float64, SCALAR_KW, steps=3,
+                   seed=6)
     compare(*res, param_tol=dict(rtol=1e-9, atol=1e-12), state_tol=dict(rtol=1e-9, atol=1e-12))
+
+
+def test_scalar_wide_form_1d_and_3d():
+    # large 1-D (instant metric from the element's own density) and 3-D
+    # (per-axis sums) tensors in the wide form, next to a resident tensor
+    announce("scalar wide 1d / 3d")
+    shapes = [(300000,), (64, 48, 50), (4096, 16), (2, 70000)]
+    compare(*run_pair(shapes, torch.float32, dict(SCALAR_KW, weight_decay=0.01), steps=3, seed=12))
 
 
 def test_scalar_mixed_batch_one_launch_per_variant():
