@@ -716,11 +716,12 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
 // per-tensor finishes between them, in two launch forms:
 //   - scalar_stream_kernel: one workgroup per tensor runs every pass over the
 //     whole tensor, with block reductions between the passes;
-//   - the wide form (tensors of SR_WIDE_MIN elements or more): each pass is
+//   - the wide form (tensors of more than 64 Ki elements, or of 16 Ki and
+//     more when the plan holds fewer than 256 of those): each pass is
 //     one launch over chunks of SR_WIDE_CH elements of every tensor of the
 //     group, writing block partials; a finish kernel (one workgroup per
 //     tensor) reduces them in block order and carries the tensor's values
-//     (StreamCtl, in the plan table) to the next pass.  Nine launches per
+//     (StreamCtl, in the plan table) to the next pass.  Ten launches per
 //     step, but a large tensor uses the whole GPU instead of one CU.
 // Axis sums of the instant metric are 64-bit fixed-point integer atomics, so
 // both forms get the same sums whatever the arrival order.
@@ -732,7 +733,9 @@ template <typename W> struct StreamCtl {
 };
 constexpr int SR_WIDE_NT = 256;              // threads per block of the wide form
 constexpr int64_t SR_WIDE_CH = 8192;         // elements per block of the wide form
-constexpr int64_t SR_WIDE_MIN = 131072;      // non-resident tensors this large use the wide form
+constexpr int64_t SR_WIDE_MIN = SR_RESIDENT_MAX + 1;   // non-resident tensors this large use the wide form
+constexpr int64_t SR_WIDE_MID = 16384;       // ... and from this size when fewer than SR_WIDE_FILL of them
+constexpr int32_t SR_WIDE_FILL = 256;        //     (one workgroup per tensor would leave CUs idle)
 constexpr size_t SR_CTL_BYTES = 256;         // table bytes of one StreamCtl
 static_assert(sizeof(StreamCtl<double>) <= SR_CTL_BYTES, "StreamCtl slot");
 
@@ -1832,6 +1835,14 @@ int32_t build_plan(const cresso_scalar_desc* descs, int32_t count, const cresso_
         int32_t rc = plan_desc(descs[i], h, recs[(size_t)i], var[(size_t)i], lds[(size_t)i], scr[(size_t)i]);
         if (rc != CRESSO_OK) return rc;
     }
+    // Mid-size streaming tensors (SR_WIDE_MID .. SR_RESIDENT_MAX elements) take
+    // the wide form too when they are too few to fill the GPU one workgroup each.
+    int32_t mid = 0;
+    for (int32_t i = 0; i < count; ++i)
+        mid += var[(size_t)i].kind == 0 && descs[i].numel >= SR_WIDE_MID;
+    if (mid > 0 && mid < SR_WIDE_FILL)
+        for (int32_t i = 0; i < count; ++i)
+            if (var[(size_t)i].kind == 0 && descs[i].numel >= SR_WIDE_MID) var[(size_t)i].kind = 2;
     std::vector<Variant> keys;
     for (const Variant& v : var)
         if (std::find(keys.begin(), keys.end(), v) == keys.end()) keys.push_back(v);

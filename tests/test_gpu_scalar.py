@@ -21,9 +21,9 @@ def test_scalar_2d_matches_oracle(shape):
     compare(*res)
 
 
-# 2-D tensors beyond the resident limit, row/column axis sums.  128 Ki elements
-# and more: the wide form (chunks over the whole GPU); below: one workgroup per
-# tensor.  (8192,64) and (64,8192): one row per wave; (8192,16): rows in groups
+# 2-D tensors beyond the resident limit, row/column axis sums.  More than 64 Ki
+# elements, or 16 Ki when a plan has fewer than 256 such tensors: the wide form
+# (chunks over the whole GPU); otherwise one workgroup per tensor.  (8192,64) and (64,8192): one row per wave; (8192,16): rows in groups
 # of 16 lanes; (16,8192): a wave inside one row; (1000,60), (3000,33) and
 # (5000,33): neither, per-element row and column sums
 @pytest.mark.parametrize("shape", [(8192, 16), (16, 8192), (8192, 64), (64, 8192), (1000, 60), (3000, 33), (5000, 33)])
@@ -45,10 +45,11 @@ def test_scalar_streaming_2d_options_and_dtypes():
     announce("scalar streaming 2d bf16 / f64")
     res = run_pair([(8192, 16), (40, 1000)], torch.bfloat16, SCALAR_KW, steps=3, seed=5)
     compare(*res, param_tol=BF16_PARAM_TOL, state_tol=dict(rtol=1e-2, atol=1e-3))
-    # f64 params are never resident: (1024,64), (64,1024) and (4096,16) take the
-    # one-workgroup kernel's wave, lane-group and per-thread column sums
-    res = run_pair([(8192, 16), (40, 1000), (1024, 64), (64, 1024), (4096, 16)], torch.float64, SCALAR_KW, steps=3,
-                   seed=6)
+    # f64 params are never resident: (256,32), (16,512) and (512,16) take the
+    # one-workgroup kernel's wave, lane-group and per-thread column sums; the
+    # others the wide form
+    res = run_pair([(8192, 16), (40, 1000), (1024, 64), (256, 32), (16, 512), (512, 16)], torch.float64, SCALAR_KW,
+                   steps=3, seed=6)
     compare(*res, param_tol=dict(rtol=1e-9, atol=1e-12), state_tol=dict(rtol=1e-9, atol=1e-12))
 
 
@@ -146,7 +147,9 @@ def test_scalar_deterministic_and_state_identity():
     import cresso_amd
 
     announce("scalar determinism")
-    shapes = [(4096, 16) if i % 2 == 0 else (16, 4096) for i in range(64)] + [(33, 7), (5, 6, 7)]
+    # resident, one-workgroup streaming and wide-form tensors
+    shapes = [(4096, 16) if i % 2 == 0 else (16, 4096) for i in range(64)] + [(33, 7), (5, 6, 7), (8192, 16),
+                                                                              (16, 8192), (3000, 33)]
     gen = torch.Generator().manual_seed(8)
     p0 = [0.02 * torch.randn(s, generator=gen) for s in shapes]
     g = [1e-3 * torch.randn(s, generator=gen) for s in shapes]
