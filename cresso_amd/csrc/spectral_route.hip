@@ -767,10 +767,23 @@ __device__ void load_sums(const double* __restrict__ sums, int V, double* out) {
 // ---------------------------------------------------------------------------
 // S1: sum f^2 over contiguous chunks (float4 loads when aligned)
 // ---------------------------------------------------------------------------
+// Each block also clears its slice of the axis density sums (rows, then
+// columns) for this step's sweep 2.
 template <typename PT, typename GT, bool V4>
 __global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
-                                                       double* __restrict__ part, cresso_hyper h) {
+                                                       double* __restrict__ part, unsigned long long* __restrict__ rowfx,
+                                                       unsigned long long* __restrict__ colfx, cresso_hyper h) {
     __shared__ float red[4];
+    {
+        const int64_t na = g.rows + g.cols, per = (na + g.nblk1 - 1) / g.nblk1;
+        const int64_t a0 = (int64_t)blockIdx.x * per, a1 = a0 + per < na ? a0 + per : na;
+        for (int64_t i = a0 + threadIdx.x; i < a1; i += SP_NT) {
+            if (i < g.rows)
+                rowfx[i] = 0ull;
+            else
+                colfx[i - g.rows] = 0ull;
+        }
+    }
     const float wd = (float)h.weight_decay;
     const bool wd_on = h.weight_decay != 0.0;
     const int64_t beg = (int64_t)blockIdx.x * g.chunk1;
@@ -826,13 +839,9 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restr
 }
 
 __global__ __launch_bounds__(SP_FN_NT) void fin1_kernel(Geom g, const double* __restrict__ part, SpecState st,
-                                                         Ctrl* __restrict__ ctrl, unsigned long long* __restrict__ rowfx,
-                                                         unsigned long long* __restrict__ colfx, int step, cresso_hyper h) {
+                                                         Ctrl* __restrict__ ctrl, int step, cresso_hyper h) {
     __shared__ double red[1];
     reduce_bm<1>(part, g.nblk1, 1, red);
-    // clear the axis density sums for this step's sweep 2
-    for (int64_t i = threadIdx.x; i < g.rows; i += SP_FN_NT) rowfx[i] = 0ull;
-    for (int64_t i = threadIdx.x; i < g.cols; i += SP_FN_NT) colfx[i] = 0ull;
     if (threadIdx.x == 0) {
         const float eps = (float)h.eps;
         const float now = sqrtf((float)(red[0] / (double)g.n) + eps);
@@ -1707,41 +1716,61 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(Geom g, const ModeMeta* 
     }
 }
 
-// ndim >= 3: axis terms of the column group by summing the column sums that
-// share a coordinate (fixed order), then the per-column factor.
-__global__ __launch_bounds__(SP_FIN_NT) void marg_axes_kernel(Geom g, const unsigned long long* __restrict__ colfx,
-                                                              float* __restrict__ terms, float* __restrict__ colfac,
-                                                              const Ctrl* __restrict__ ctrl, float eps) {
-    const float gden = ctrl->gden, kappa = ctrl->kappa;
-    const double n = (double)g.n;
-    int64_t off = 0;
-    for (int a = 0; a < g.ntrail; ++a) {
-        int64_t inner = 1;
-        for (int b = a + 1; b < g.ntrail; ++b) inner *= g.tdim[b];
-        const int64_t dim = g.tdim[a];
-        const int64_t outer = g.cols / (dim * inner);
-        for (int64_t k = threadIdx.x; k < dim; k += SP_FIN_NT) {
-            double s = 0.0;
-            for (int64_t o = 0; o < outer; ++o)
-                for (int64_t in = 0; in < inner; ++in) s += (double)colfx[(o * dim + k) * inner + in];
-            const float mean = (float)(s / g.hs_col / (n / (double)dim));
-            terms[off + k] = kappa * logf(fmaxf(mean / gden, eps));
-        }
-        off += dim;
+// ndim >= 3: the factor of each column of the column group (the trailing
+// axes) is the product over those axes of (axis mean / global mean)^kappa.
+// marg_terms_kernel: one block per coordinate k of trailing axis a sums the
+// column sums that share it (64-bit integers: exact in any order) into the
+// axis term kappa log(max(mean / gden, eps)).
+constexpr int SP_MARG_NT = 256;
+__global__ __launch_bounds__(SP_MARG_NT) void marg_terms_kernel(Geom g, const unsigned long long* __restrict__ colfx,
+                                                                float* __restrict__ terms, const Ctrl* __restrict__ ctrl,
+                                                                float eps) {
+    __shared__ unsigned long long red[SP_MARG_NT];
+    // block -> (axis a, coordinate k); the axis terms are laid out axis after axis
+    int64_t k = blockIdx.x, off = 0;
+    int a = 0;
+    while (a + 1 < g.ntrail && k >= g.tdim[a]) {
+        k -= g.tdim[a];
+        off += g.tdim[a];
+        ++a;
     }
+    int64_t inner = 1;
+    for (int b = a + 1; b < g.ntrail; ++b) inner *= g.tdim[b];
+    const int64_t dim = g.tdim[a];
+    const int64_t m = g.cols / dim;   // columns sharing coordinate k: outer x inner
+    unsigned long long s = 0ull;
+    for (int64_t j = threadIdx.x; j < m; j += SP_MARG_NT) {
+        const int64_t o = j / inner, in = j - o * inner;
+        s += colfx[(o * dim + k) * inner + in];
+    }
+    red[threadIdx.x] = s;
     __syncthreads();
-    for (int64_t c = threadIdx.x; c < g.cols; c += SP_FIN_NT) {
-        int64_t rem = c;
-        float acc = 0.f;
-        int64_t o2 = off;
-        for (int a = g.ntrail - 1; a >= 0; --a) {
-            o2 -= g.tdim[a];
-            const int64_t k = rem % g.tdim[a];
-            rem /= g.tdim[a];
-            acc += terms[o2 + k];
-        }
-        colfac[c] = expf(acc);
+    for (int w = SP_MARG_NT / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
     }
+    if (threadIdx.x == 0) {
+        const float mean = (float)((double)red[0] / g.hs_col / ((double)g.n / (double)dim));
+        terms[off + k] = ctrl->kappa * logf(fmaxf(mean / ctrl->gden, eps));
+    }
+}
+
+// marg_fac_kernel: one thread per column, exp of the sum of its axis terms.
+__global__ __launch_bounds__(SP_MARG_NT) void marg_fac_kernel(Geom g, const float* __restrict__ terms,
+                                                              float* __restrict__ colfac) {
+    const int64_t c = (int64_t)blockIdx.x * SP_MARG_NT + threadIdx.x;
+    if (c >= g.cols) return;
+    int64_t off = 0;
+    for (int a = 0; a < g.ntrail; ++a) off += g.tdim[a];
+    int64_t rem = c;
+    float acc = 0.f;
+    for (int a = g.ntrail - 1; a >= 0; --a) {
+        off -= g.tdim[a];
+        const int64_t k = rem % g.tdim[a];
+        rem /= g.tdim[a];
+        acc += terms[off + k];
+    }
+    colfac[c] = expf(acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -3111,10 +3140,10 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     const dim3 grid(g.nblk), blk(SP_NT);
     const bool v4 = ((uintptr_t)grad % (4 * sizeof(GT))) == 0 && ((uintptr_t)param % (4 * sizeof(PT))) == 0;
     if (v4)
-        hipLaunchKernelGGL((sweep1_kernel<PT, GT, true>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, h);
+        hipLaunchKernelGGL((sweep1_kernel<PT, GT, true>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, rowfx, colfx, h);
     else
-        hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, h);
-    hipLaunchKernelGGL(fin1_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, rowfx, colfx, step, h);
+        hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, rowfx, colfx, h);
+    hipLaunchKernelGGL(fin1_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, step, h);
     const bool fast = fast_mode(g, hash_on, axes_on, h);
     if constexpr (RM <= 8) {
         if (fast) {
@@ -3133,8 +3162,14 @@ swept2:
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2), dim3(256), 0, s, part, g.nblk, NV2, sums);
     hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st,
                        ctrl, step, hash_on, hard, h);
-    if (axes_on && g.ntrail > 1)
-        hipLaunchKernelGGL(marg_axes_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, colfx, terms, colfac, ctrl, (float)h.eps);
+    if (axes_on && g.ntrail > 1) {
+        int64_t nterms = 0;
+        for (int a = 0; a < g.ntrail; ++a) nterms += g.tdim[a];
+        hipLaunchKernelGGL(marg_terms_kernel, dim3((unsigned)nterms), dim3(SP_MARG_NT), 0, s, g, colfx, terms, ctrl,
+                           (float)h.eps);
+        hipLaunchKernelGGL(marg_fac_kernel, dim3((unsigned)((g.cols + SP_MARG_NT - 1) / SP_MARG_NT)), dim3(SP_MARG_NT), 0,
+                           s, g, terms, colfac);
+    }
     if constexpr (RM <= 8 && KC <= 12) {
         const size_t l3m = lds_sweep3m(g, kcp<KC>(), 2 * RM);
         if (fast && l3m <= SP_LDS_MAX) {
