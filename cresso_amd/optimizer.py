@@ -354,6 +354,7 @@ class CRESSO5(Optimizer):
             return
         mode = str(group.get("cuda_ops", "auto"))
         scalar_ps: List[Tensor] = []
+        spectral_items = []
         other = False
         for p in group["params"]:
             if p.grad is None or not torch.is_floating_point(p):
@@ -383,7 +384,10 @@ class CRESSO5(Optimizer):
                 continue
             if route == "spectral":
                 other = True
-                self._spectral(p, grad, group)
+                st = self.state[p]
+                if len(st) == 0:
+                    st = self._init_spectral(p, group)
+                spectral_items.append((p, grad, st))
                 continue
             st = self.state[p]
             if len(st) == 0:
@@ -393,6 +397,8 @@ class CRESSO5(Optimizer):
             elif st["q"].dtype != _state_dtype(p.dtype):
                 raise RuntimeError("CRESSO5 scalar state has dtype %s, expected %s" % (st["q"].dtype, _state_dtype(p.dtype)))
             scalar_ps.append(p)
+        if spectral_items:
+            self._spectral_step(spectral_items, group)
         self._group_other[gi] = other
         if not scalar_ps:
             self._batches.pop((gi, "scalar"), None)
@@ -421,14 +427,12 @@ class CRESSO5(Optimizer):
             if st[k].shape != p.shape or not st[k].is_contiguous():
                 raise RuntimeError(f"CRESSO5 micro route: state {k!r} must be contiguous with the parameter's shape")
 
-    def _spectral(self, param: Tensor, grad: Tensor, group: dict) -> None:
+    def _spectral_step(self, items, group: dict) -> None:
+        """Every spectral tensor of the group: (param, grad, state) each."""
         if self._spectral_engine is None:
             from .spectral import SpectralEngine
             self._spectral_engine = SpectralEngine()
-        st = self.state[param]
-        if len(st) == 0:
-            st = self._init_spectral(param, group)
-        self._spectral_engine.step(param, grad, st, group)
+        self._spectral_engine.step_many(items, group)
 
     # ------------------------------------------------------------- checkpoints
     def load_state_dict(self, state_dict: dict) -> None:

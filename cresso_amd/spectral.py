@@ -2,15 +2,23 @@
 
 The library keeps no state of its own: plans live here, keyed by
 (device, shape, freqs, hash_bins, hash_tables), together with their device
-workspace (carrier tables, cached coordinate-hash bins, scratch).  Tensors of
-the same shape share one workspace; they run one after another on the same
-stream, so the per-step scratch in it is never used concurrently.
+workspace (carrier tables, cached coordinate-hash bins, scratch).
+
+A step of several spectral tensors (`step_many`) spreads them over up to
+LANES side streams (default priority), so that one tensor's small finish
+kernels and partly filled sweeps overlap with another's work.  Every lane
+has its own workspace per shape: tensors that share a workspace run one
+after another on that lane's stream, so its per-step scratch is never used
+concurrently.  The side streams wait for the caller's stream before the
+first launch and the caller's stream waits for all of them after the last,
+so the step is ordered like any other work on the caller's stream.  A
+single spectral tensor runs on the caller's stream directly.
 """
 
 from __future__ import annotations
 
 import ctypes
-from typing import Dict, Tuple
+from typing import Dict, List, Sequence, Tuple
 
 import torch
 
@@ -50,10 +58,12 @@ class _Workspace:
 
 class SpectralEngine:
     READY = True
+    LANES = 4   # side streams of a multi-tensor step
 
     def __init__(self):
         self.lib = _native.load()
-        self.ws: Dict[tuple, _Workspace] = {}
+        self.ws: Dict[tuple, _Workspace] = {}   # (plan key, lane) -> workspace
+        self.side: Dict[torch.device, List[torch.cuda.Stream]] = {}
         self.freq_cache: Dict[int, Tuple[int, ...]] = {}
 
     def reset(self) -> None:
@@ -69,7 +79,16 @@ class SpectralEngine:
             self.freq_cache[key] = got
         return got[1]
 
-    def step(self, param: torch.Tensor, grad: torch.Tensor, st: dict, group: dict) -> None:
+    def _workspace(self, key: tuple, lane: int, rank: int, group: dict) -> _Workspace:
+        ws = self.ws.get((key, lane))
+        if ws is None:
+            device, shape, freqs, bins, tables = key
+            ws = _Workspace(self.lib, shape, freqs, rank, bins, tables, group, device)
+            self.ws[(key, lane)] = ws
+        return ws
+
+    def _prepare(self, param: torch.Tensor, grad: torch.Tensor, st: dict, group: dict):
+        """Validate one tensor's state and build its descriptor; -> (key, rank, desc)."""
         if param.dtype not in (torch.float32, torch.bfloat16, torch.float16) or grad.dtype != param.dtype:
             raise RuntimeError(f"CRESSO5 spectral route on MI355X supports fp32/bf16/fp16 params with grads of the "
                                f"same dtype (got {param.dtype} / {grad.dtype})")
@@ -81,11 +100,6 @@ class SpectralEngine:
         bins, tables = int(group["hash_bins"]), int(group["hash_tables"])
         shape = tuple(int(d) for d in param.shape)
         key = (param.device, shape, freqs, bins, tables)
-        ws = self.ws.get(key)
-        if ws is None:
-            ws = _Workspace(self.lib, shape, freqs, rank, bins, tables, group, param.device)
-            self.ws[key] = ws
-        st["step"] += 1
         cut = int(group["thin_matrix_hard_cutoff"])
         thin = param.ndim == 2 and cut > 0 and min(shape) <= cut
         hard = param.numel() >= int(group["hard_channel_min_size"]) and not thin
@@ -110,10 +124,61 @@ class SpectralEngine:
             d.hash_energy = st["hash_energy"].data_ptr()
             d.hash_impulse = st["hash_impulse"].data_ptr()
             d.hash_refractory = st["hash_refractory"].data_ptr()
-        d.step = int(st["step"])
+        d.step = int(st["step"]) + 1
         d.hard = 1 if hard else 0
-        hyper = _native.hyper_from_group(group)
-        stream = _native.stream_handle(param.device)
+        return key, rank, d
+
+    def _launch(self, ws: _Workspace, d, hyper, stream: int) -> None:
         _native.check(self.lib.cresso_spectral_step(ws.plan, ctypes.byref(d), ctypes.c_void_p(ws.buf.data_ptr()),
                                                     ctypes.c_size_t(ws.buf.numel()), ctypes.byref(hyper),
                                                     ctypes.c_void_p(stream)), "spectral route step")
+
+    def step(self, param: torch.Tensor, grad: torch.Tensor, st: dict, group: dict) -> None:
+        """One tensor on the caller's stream."""
+        key, rank, d = self._prepare(param, grad, st, group)
+        ws = self._workspace(key, 0, rank, group)
+        st["step"] += 1
+        self._launch(ws, d, _native.hyper_from_group(group), _native.stream_handle(param.device))
+
+    def _streams(self, device: torch.device, n: int) -> List[torch.cuda.Stream]:
+        have = self.side.setdefault(device, [])
+        while len(have) < n:
+            have.append(torch.cuda.Stream(device=device))   # default priority
+        return have[:n]
+
+    def step_many(self, items: Sequence[Tuple[torch.Tensor, torch.Tensor, dict]], group: dict) -> None:
+        """Every spectral tensor of a param group: (param, grad, state) each."""
+        if len(items) == 1:
+            self.step(*items[0], group)
+            return
+        by_dev: Dict[torch.device, list] = {}
+        for it in items:
+            by_dev.setdefault(it[0].device, []).append(it)
+        hyper = _native.hyper_from_group(group)
+        for device, its in by_dev.items():
+            # descriptors and workspaces first: a workspace created now is
+            # initialised on the caller's stream, before the lanes fork from it
+            prepared = [self._prepare(p, g, st, group) for p, g, st in its]
+            count: Dict[tuple, int] = {}
+            for key, _, _ in prepared:
+                count[key] = count.get(key, 0) + 1
+            nl = min(self.LANES, len(its))
+            seen: Dict[tuple, int] = {}
+            base: Dict[tuple, int] = {}
+            plan = []
+            for (key, rank, d), (_, _, st) in zip(prepared, its):
+                if key not in base:
+                    base[key] = len(base) % nl   # spreads the shapes over the lanes
+                j = seen.get(key, 0)
+                seen[key] = j + 1
+                lane = (base[key] + j % min(nl, count[key])) % nl
+                plan.append((self._workspace(key, lane, rank, group), d, lane, st))
+            cur = torch.cuda.current_stream(device)
+            side = self._streams(device, nl)
+            for s in side:
+                s.wait_stream(cur)
+            for ws, d, lane, st in plan:
+                st["step"] += 1
+                self._launch(ws, d, hyper, int(side[lane].cuda_stream))
+            for s in side:
+                cur.wait_stream(s)

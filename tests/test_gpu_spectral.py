@@ -133,3 +133,38 @@ def test_spectral_fast_path_variants(case):
         oopt.step([g])
     torch.cuda.synchronize()
     compare([hp], hopt, [op], oopt)
+
+
+def test_spectral_many_tensors_on_side_streams():
+    # several tensors of one shape and single tensors of other shapes in one
+    # group: the step spreads them over side streams, each lane with its own
+    # workspace per shape; parity with the oracle, and bit-identical to the
+    # same step run on one stream
+    import cresso_amd
+    from cresso_amd import spectral
+
+    shapes = [(256, 256)] * 5 + [(512, 128)] * 2 + [(2048,)] + [(64, 48)] * 3
+    kw = dict(rank=8, hash_bins=64, hash_tables=2)
+    announce(f"spectral lanes {len(shapes)} tensors")
+    compare(*run_pair(shapes, torch.float32, kw, steps=3, seed=41, grad_std=1e-3, param_std=0.02))
+
+    gen = torch.Generator().manual_seed(42)
+    p0 = [0.02 * torch.randn(s, generator=gen) for s in shapes]
+    gs = [[1e-3 * torch.randn(s, generator=gen) for s in shapes] for _ in range(3)]
+    outs = []
+    old = spectral.SpectralEngine.LANES
+    try:
+        for lanes in (1, 4):
+            spectral.SpectralEngine.LANES = lanes
+            ps = [torch.nn.Parameter(p.clone().cuda()) for p in p0]
+            opt = cresso_amd.CRESSO5(ps, cuda_ops="required", **kw)
+            for step in gs:
+                for p, g in zip(ps, step):
+                    p.grad = g.cuda()
+                opt.step()
+            torch.cuda.synchronize()
+            outs.append([p.detach().cpu() for p in ps] + [opt.state[p]["q_cos"].cpu() for p in ps])
+    finally:
+        spectral.SpectralEngine.LANES = old
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
