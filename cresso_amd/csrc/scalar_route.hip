@@ -1822,6 +1822,9 @@ struct cresso_scalar_plan {
     const void** staging[2] = {nullptr, nullptr};
     hipEvent_t ev[2] = {nullptr, nullptr};
     int flip = 0;
+    // grad pointers the table holds (grouped order), to skip an unchanged upload
+    std::vector<const void*> table_grads;
+    const void* table_ptr = nullptr;
 };
 
 namespace cresso {
@@ -1963,6 +1966,11 @@ extern "C" int32_t cresso_scalar_plan_upload(cresso_scalar_plan* P, void* dev_ta
         e = hipMemcpyAsync(table + P->bmap_off, P->bmap.data(), sizeof(int32_t) * P->bmap.size(), hipMemcpyHostToDevice, s);
     // pageable sources: make sure the copies have consumed them before returning
     if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess) {
+        P->table_grads.resize(count);
+        for (size_t j = 0; j < count; ++j) P->table_grads[j] = P->recs[j].d.grad;
+        P->table_ptr = dev_table;
+    }
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "scalar route: table upload");
 }
 
@@ -1977,18 +1985,28 @@ extern "C" int32_t cresso_scalar_plan_step(cresso_scalar_plan* P, void* dev_tabl
     unsigned char* table = reinterpret_cast<unsigned char*>(dev_table);
     const size_t count = P->recs.size();
     if (grads) {
-        const int k = P->flip;
-        P->flip ^= 1;
-        hipError_t e = hipEventSynchronize(P->ev[k]);   // the copy issued two steps ago is done
-        if (e != hipSuccess) return hip_fail(e, "scalar route: staging wait");
-        for (size_t j = 0; j < count; ++j) {
-            const void* gp = grads[P->order[j]];
-            if (!gp) return fail(CRESSO_E_INVALID, "scalar route: null grad pointer for tensor %d", P->order[j]);
-            P->staging[k][j] = gp;
+        // the table already holds these pointers (same grads as the last
+        // upload, as when the caching allocator hands the same blocks back):
+        // no copy
+        bool same = P->table_ptr == dev_table && P->table_grads.size() == count;
+        for (size_t j = 0; same && j < count; ++j) same = grads[P->order[j]] == P->table_grads[j];
+        if (!same) {
+            const int k = P->flip;
+            P->flip ^= 1;
+            hipError_t e = hipEventSynchronize(P->ev[k]);   // the copy issued two steps ago is done
+            if (e != hipSuccess) return hip_fail(e, "scalar route: staging wait");
+            for (size_t j = 0; j < count; ++j) {
+                const void* gp = grads[P->order[j]];
+                if (!gp) return fail(CRESSO_E_INVALID, "scalar route: null grad pointer for tensor %d", P->order[j]);
+                P->staging[k][j] = gp;
+            }
+            P->table_ptr = nullptr;   // unknown until the copy is queued
+            e = hipMemcpyAsync(table + P->grads_off, P->staging[k], sizeof(void*) * count, hipMemcpyHostToDevice, s);
+            if (e == hipSuccess) e = hipEventRecord(P->ev[k], s);
+            if (e != hipSuccess) return hip_fail(e, "scalar route: grad pointer upload");
+            P->table_grads.assign(P->staging[k], P->staging[k] + count);
+            P->table_ptr = dev_table;
         }
-        e = hipMemcpyAsync(table + P->grads_off, P->staging[k], sizeof(void*) * count, hipMemcpyHostToDevice, s);
-        if (e == hipSuccess) e = hipEventRecord(P->ev[k], s);
-        if (e != hipSuccess) return hip_fail(e, "scalar route: grad pointer upload");
     }
     const ScalarRec* drecs = reinterpret_cast<const ScalarRec*>(table);
     int32_t* dsteps = reinterpret_cast<int32_t*>(table + P->steps_off);
