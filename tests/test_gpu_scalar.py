@@ -61,6 +61,37 @@ def test_scalar_wide_form_1d_and_3d():
     compare(*run_pair(shapes, torch.float32, dict(SCALAR_KW, weight_decay=0.01), steps=3, seed=12))
 
 
+def test_scalar_wide_form_no_instant_metric_and_bf16_grads():
+    # instant_metric_coupling = 0 (no axis sums) in the wide form; then bf16
+    # grads on fp32 params (never resident), wide and one-workgroup tensors
+    import cresso_amd
+    from oracle.cresso_oracle import OracleCRESSO5
+    import numpy as np
+
+    announce("scalar wide no instant metric")
+    kw = dict(SCALAR_KW, instant_metric_coupling=0.0)
+    compare(*run_pair([(8192, 16), (16, 8192), (3000, 33)], torch.float32, kw, steps=3, seed=14))
+
+    announce("scalar wide bf16 grads on fp32 params")
+    gen = torch.Generator().manual_seed(15)
+    shapes = [(8192, 16), (16, 8192), (120, 30)]
+    p0 = [0.02 * torch.randn(s, generator=gen) for s in shapes]
+    gs = [[(1e-2 * torch.randn(s, generator=gen)).to(torch.bfloat16) for s in shapes] for _ in range(3)]
+    hp = [torch.nn.Parameter(p.clone().cuda()) for p in p0]
+    for p in hp:
+        p.grad_dtype = None   # allow grads of another dtype
+    op = [p.clone() for p in p0]
+    hopt = cresso_amd.CRESSO5(hp, cuda_ops="required", **SCALAR_KW)
+    oopt = OracleCRESSO5(op, **SCALAR_KW)
+    for step in gs:
+        for p, g in zip(hp, step):
+            p.grad = g.cuda()
+        hopt.step()
+        oopt.step(step)
+    torch.cuda.synchronize()
+    compare(hp, hopt, op, oopt)
+
+
 def test_scalar_mixed_batch_one_launch_per_variant():
     # resident row-group, resident column-block, streaming 1D / 3D / 0-d /
     # odd 2D / large thin 2D, all in one optimizer group
