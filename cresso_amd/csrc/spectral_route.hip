@@ -115,6 +115,7 @@ struct Ctrl {
     // drive = k_rat rat + k_ths tanh(t/clip) + k_root root + k_t t + k_pred pred' + k_echo echo
     //         + k_nov tanh(err' nscale) + k_hash hash_pred
     float k_rat, k_ths, k_root, k_t, k_pred, k_echo, k_nov, k_hash, gain;
+    float de_prev;            // drive_energy before this step (sweep 5 updates the state)
 };
 
 // state pointers of one tensor (kernel argument)
@@ -2297,6 +2298,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
                                                         float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
                                                         const unsigned long long* __restrict__ cooc, int step, int hash_on,
                                                         int hard, int echo_on, int c5_closed, cresso_hyper h) {
+    if (threadIdx.x == 0) ctrl->de_prev = *st.drive_energy;   // every block of sweep 5 reads the old value
     __shared__ double s_m[NV3];
     __shared__ double s_ec[2 * SP_MAXR];    // mean(t Xn_v)
     __shared__ double s_u[3][2 * SP_MAXR];  // weights of pred, pred', echo
@@ -2507,7 +2509,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
             double hh = 0.0;
             for (int w = 0; w < SP_FN_NT / 64 - 1; ++w) hh += s_hhw[w];
             hh *= 0.25;
-            // the hash term's coefficient as fin4_kernel forms it, from sum hp^2
+            // the hash term's coefficient as fin4_values forms it, from sum hp^2
             const float khp = s_srms / fmaxf(sqrtf((float)(hh / n) + eps), eps);
             ctrl->k_hash = (float)(hard ? h.hash_drive_mix * (double)khp : 0.0);
         }
@@ -2778,32 +2780,51 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
     P.flush(part);
 }
 
-// F4: hash-term coefficient, drive energy reservoir, gain.
+// F4, in every block of sweep 5: sweep 4's block partials summed in a fixed
+// order (so every block gets the same values), then the hash-term
+// coefficient, the drive-energy reservoir and the gain.  Block 0 stores the
+// new drive energy; the reservoir starts from ctrl->de_prev (stashed by fin3),
+// so no block reads a value another block of this launch wrote.
 //   sum drive^2 = sum d^2 + 2 c5 sum d hp + c5^2 sum hp^2
-__global__ __launch_bounds__(SP_FN_NT) void fin4_kernel(Geom g, const double* __restrict__ part, SpecState st,
-                                                        Ctrl* __restrict__ ctrl, int step, int hash_on, int hard,
-                                                        int c5_closed, cresso_hyper h) {
-    __shared__ double s_m[NV4];
-    reduce_bm<NV4>(part, g.nblk, 3, s_m);
-    if (threadIdx.x != 0) return;
+__device__ void fin4_values(const Geom& g, const double* __restrict__ part, const Ctrl* __restrict__ ctrl,
+                            float* __restrict__ de_state, int step, int hash_on, int hard, int c5_closed,
+                            const cresso_hyper& h, float& gain, float& c5f) {
+    __shared__ double s_w[SP_NT / 64][NV4];
+    double acc[NV4] = {0.0, 0.0, 0.0};
+    for (int b = threadIdx.x; b < g.nblk; b += SP_NT)
+#pragma unroll
+        for (int v = 0; v < NV4; ++v) acc[v] += part[(size_t)v * g.nblk + b];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int v = 0; v < NV4; ++v) {
+        const double w = wave_total_d(acc[v]);
+        if (lane == 63) s_w[wave][v] = w;
+    }
+    __syncthreads();
+    double m[NV4];
+#pragma unroll
+    for (int v = 0; v < NV4; ++v) {
+        m[v] = 0.0;
+        for (int w = 0; w < SP_NT / 64; ++w) m[v] += s_w[w][v];
+    }
     const double n = (double)g.n;
     const float eps = (float)h.eps;
     double c5, dd;
     if (c5_closed) {
         // sweep 4 summed the full drive (the hash term's coefficient came from fin3)
         c5 = (double)ctrl->k_hash;
-        dd = s_m[0];
+        dd = m[0];
     } else {
         float khp = 0.f;
-        if (hard && hash_on) khp = ctrl->srms / fmaxf(sqrtf((float)(s_m[2] / n) + eps), eps);
+        if (hard && hash_on) khp = ctrl->srms / fmaxf(sqrtf((float)(m[2] / n) + eps), eps);
         c5 = hard ? h.hash_drive_mix * (double)khp : 0.0;
-        dd = s_m[0] + 2.0 * c5 * s_m[1] + c5 * c5 * s_m[2];
+        dd = m[0] + 2.0 * c5 * m[1] + c5 * c5 * m[2];
     }
     const float de_now = (float)(fmax(dd, 0.0) / n);
-    const float de = reservoir_f(*st.drive_energy, de_now, h.reservoir_decay, step);
-    *st.drive_energy = de;
-    ctrl->k_hash = (float)c5;
-    ctrl->gain = clampf((float)h.target_update_rms / sqrtf(de + eps), (float)h.min_gain, (float)h.max_gain);
+    const float de = reservoir_f(ctrl->de_prev, de_now, h.reservoir_decay, step);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *de_state = de;
+    c5f = (float)c5;
+    gain = clampf((float)h.target_update_rms / sqrtf(de + eps), (float)h.min_gain, (float)h.max_gain);
 }
 
 // ---------------------------------------------------------------------------
@@ -2819,8 +2840,11 @@ template <typename PT, bool HASH, bool V4>
 __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ param, const float* __restrict__ dbuf,
                                                        const unsigned char* __restrict__ bins,
                                                        const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
-                                                       cresso_hyper h) {
+                                                       const double* __restrict__ part, float* __restrict__ de_state,
+                                                       int step, int hash_on, int hard, int c5_closed, cresso_hyper h) {
     extern __shared__ __align__(16) unsigned char dyn[];
+    float gain, c5;
+    fin4_values(g, part, ctrl, de_state, step, hash_on, hard, c5_closed, h, gain, c5);
     const int TB = g.T * g.B;
     const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
     float* s_imp = reinterpret_cast<float*>(dyn);
@@ -2828,7 +2852,7 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
         __syncthreads();
     }
-    const float gain = ctrl->gain, kh = ctrl->k_hash * (1.0f / (float)T);
+    const float kh = c5 * (1.0f / (float)T);
     const float nlr = (float)(-h.lr);
     const int64_t beg = (int64_t)blockIdx.x * g.chunk1;
     const int64_t end = beg + g.chunk1 < g.n ? beg + g.chunk1 : g.n;
@@ -3205,18 +3229,21 @@ swept3:
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 0>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
                            hash_on, echo_on, h);
 swept4:
-    hipLaunchKernelGGL(fin4_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, step, hash_on, hard, c5c, h);
     const bool hash5 = hash_on && !c5c;   // sweep 5 adds the hash term itself
     const size_t l5 = hash5 ? sizeof(float) * (size_t)g.T * g.B : 0;
     const bool pv4 = ((uintptr_t)param % (4 * sizeof(PT))) == 0;
     if (hash5 && pv4)
-        hipLaunchKernelGGL((sweep5_kernel<PT, true, true>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, h);
+        hipLaunchKernelGGL((sweep5_kernel<PT, true, true>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, part,
+                           st.drive_energy, step, hash_on, hard, c5c, h);
     else if (hash5)
-        hipLaunchKernelGGL((sweep5_kernel<PT, true, false>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, h);
+        hipLaunchKernelGGL((sweep5_kernel<PT, true, false>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, part,
+                           st.drive_energy, step, hash_on, hard, c5c, h);
     else if (pv4)
-        hipLaunchKernelGGL((sweep5_kernel<PT, false, true>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, h);
+        hipLaunchKernelGGL((sweep5_kernel<PT, false, true>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, part,
+                           st.drive_energy, step, hash_on, hard, c5c, h);
     else
-        hipLaunchKernelGGL((sweep5_kernel<PT, false, false>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, h);
+        hipLaunchKernelGGL((sweep5_kernel<PT, false, false>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, part,
+                           st.drive_energy, step, hash_on, hard, c5c, h);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: launch");
 }
