@@ -283,6 +283,22 @@ def rocprof_summary(dirs, calib=None, launches=None):
                 out.append(line)
             if tb:
                 out.append(f"- scaled HBM bytes (those counters above): {tb:.0f}")
+        if "SQ_INSTS_VALU" in counters:
+            # issue-time floor of each kernel's vector work on the whole chip:
+            # a wave64 VALU op holds a 16-lane SIMD 4 cycles (transcendentals
+            # 16), an fp32 16x16x4 MFMA 32 cycles; 1024 SIMDs at 2.4 GHz
+            out.append("\n### VALU and MFMA issue time per dispatch (1024 SIMDs, 2.4 GHz)\n")
+            out.append("| kernel | VALU instr | transcendental % | VALU issue us | MFMA instr | MFMA busy us |")
+            out.append("|---|---:|---:|---:|---:|---:|")
+            for k, d_ in sorted(means.items(), key=lambda kv: kv[0]):
+                if "SQ_INSTS_VALU" not in d_:
+                    continue
+                iv = d_["SQ_INSTS_VALU"][0]
+                tr = d_.get("SQ_INSTS_VALU_TRANS_F32", (0.0, 0))[0]
+                mf = d_.get("SQ_INSTS_MFMA", (0.0, 0))[0]
+                t_v = (iv - mf + 3.0 * tr) * 4 / 1024 / 2.4e9 * 1e6
+                t_m = mf * 32 / 1024 / 2.4e9 * 1e6
+                out.append(f"| {k} | {iv:.4g} | {100 * tr / max(iv, 1):.1f} | {t_v:.1f} | {mf:.4g} | {t_m:.1f} |")
     print("\n".join(out))
 
 
