@@ -28,6 +28,29 @@ _VEC_KEYS = ("q_cos", "q_sin", "p_cos", "p_sin", "metric_cos", "metric_sin", "me
              "calcium_cos", "calcium_sin", "mode_confidence")
 
 
+def assign_lanes(keys: Sequence[tuple], lanes: int) -> List[int]:
+    """Lane of each tensor of a multi-tensor step, given its plan key.
+
+    The m tensors of one key take min(lanes, m) distinct lanes, round robin
+    from a start lane that moves on with every new key (so single tensors of
+    different shapes spread over the lanes).  Each (key, lane) pair is one
+    workspace, used by its tensors one after another on that lane's stream.
+    """
+    count: Dict[tuple, int] = {}
+    for k in keys:
+        count[k] = count.get(k, 0) + 1
+    seen: Dict[tuple, int] = {}
+    base: Dict[tuple, int] = {}
+    out = []
+    for k in keys:
+        if k not in base:
+            base[k] = len(base) % lanes
+        j = seen.get(k, 0)
+        seen[k] = j + 1
+        out.append((base[k] + j % min(lanes, count[k])) % lanes)
+    return out
+
+
 class _Workspace:
     def __init__(self, lib, shape, freqs_host: Tuple[int, ...], rank: int, bins: int, tables: int, group: dict,
                  device: torch.device):
@@ -159,20 +182,10 @@ class SpectralEngine:
             # descriptors and workspaces first: a workspace created now is
             # initialised on the caller's stream, before the lanes fork from it
             prepared = [self._prepare(p, g, st, group) for p, g, st in its]
-            count: Dict[tuple, int] = {}
-            for key, _, _ in prepared:
-                count[key] = count.get(key, 0) + 1
             nl = min(self.LANES, len(its))
-            seen: Dict[tuple, int] = {}
-            base: Dict[tuple, int] = {}
-            plan = []
-            for (key, rank, d), (_, _, st) in zip(prepared, its):
-                if key not in base:
-                    base[key] = len(base) % nl   # spreads the shapes over the lanes
-                j = seen.get(key, 0)
-                seen[key] = j + 1
-                lane = (base[key] + j % min(nl, count[key])) % nl
-                plan.append((self._workspace(key, lane, rank, group), d, lane, st))
+            lanes = assign_lanes([key for key, _, _ in prepared], nl)
+            plan = [(self._workspace(key, lane, rank, group), d, lane, st)
+                    for (key, rank, d), (_, _, st), lane in zip(prepared, its, lanes)]
             cur = torch.cuda.current_stream(device)
             side = self._streams(device, nl)
             for s in side:

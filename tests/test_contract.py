@@ -233,3 +233,21 @@ def test_host_batch_guard_cpu_behaviour():
     ps[0].grad = None
     with pytest.raises(ValueError):
         hb.BatchGuard(ps)
+
+
+def test_spectral_lane_assignment():
+    # the multi-tensor spectral step: m tensors of one shape use min(4, m)
+    # distinct lanes (one workspace each), shapes spread over the lanes
+    from cresso_amd.spectral import assign_lanes
+
+    keys = ["a"] * 6 + ["b"] + ["c"] * 2 + ["d"]
+    lanes = assign_lanes(keys, 4)
+    assert len(lanes) == len(keys) and all(0 <= x < 4 for x in lanes)
+    by = {}
+    for k, x in zip(keys, lanes):
+        by.setdefault(k, []).append(x)
+    assert len(set(by["a"])) == 4 and len(set(by["c"])) == 2
+    assert by["a"][:4] == [0, 1, 2, 3] and by["a"][4:] == [0, 1]   # round robin
+    assert by["b"] == [1] and by["c"] == [2, 3] and by["d"] == [3]  # start lane moves with each new key
+    assert assign_lanes(["x", "y"], 1) == [0, 0]
+    assert assign_lanes([], 4) == []
