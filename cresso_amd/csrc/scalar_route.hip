@@ -1819,9 +1819,15 @@ struct cresso_scalar_plan {
     std::vector<int32_t> bmap;                // wide form: block -> tensor, every wide group in turn
     size_t steps_off = 0, grads_off = 0, bmap_off = 0, part_off = 0, total = 0;
     bool no_instant = false;                  // instant_metric_coupling == 0 at planning time
+    // per-step grad pointers in pinned, device-mapped, coherent host memory:
+    // the kernels read them there (no copy to the table, whose separate
+    // small transfer stalled the stream for tens of µs); double-buffered, ev[k]
+    // recorded after the last kernels that read staging[k]
     const void** staging[2] = {nullptr, nullptr};
+    const void* const* dstaging[2] = {nullptr, nullptr};
     hipEvent_t ev[2] = {nullptr, nullptr};
     int flip = 0;
+    int cur = -1;   // staging buffer the last step's kernels read (-1: the table)
     // grad pointers the table holds (grouped order), to skip an unchanged upload
     std::vector<const void*> table_grads;
     const void* table_ptr = nullptr;
@@ -1923,7 +1929,9 @@ extern "C" cresso_scalar_plan* cresso_scalar_plan_create(const cresso_scalar_des
         return nullptr;
     }
     for (int k = 0; k < 2; ++k) {
-        hipError_t e = hipHostMalloc((void**)&P->staging[k], sizeof(void*) * (size_t)count, hipHostMallocDefault);
+        hipError_t e = hipHostMalloc((void**)&P->staging[k], sizeof(void*) * (size_t)count,
+                                     hipHostMallocMapped | hipHostMallocCoherent);
+        if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&P->dstaging[k], (void*)P->staging[k], 0);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&P->ev[k], hipEventDisableTiming);
         if (e != hipSuccess) {
             hip_fail(e, "scalar route: plan staging");
@@ -1970,6 +1978,7 @@ extern "C" int32_t cresso_scalar_plan_upload(cresso_scalar_plan* P, void* dev_ta
         P->table_grads.resize(count);
         for (size_t j = 0; j < count; ++j) P->table_grads[j] = P->recs[j].d.grad;
         P->table_ptr = dev_table;
+        P->cur = -1;
     }
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "scalar route: table upload");
 }
@@ -1984,38 +1993,39 @@ extern "C" int32_t cresso_scalar_plan_step(cresso_scalar_plan* P, void* dev_tabl
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     unsigned char* table = reinterpret_cast<unsigned char*>(dev_table);
     const size_t count = P->recs.size();
+    int ks = P->cur;   // grads == NULL: the pointers of the previous call
     if (grads) {
-        // the table already holds these pointers (same grads as the last
-        // upload, as when the caching allocator hands the same blocks back):
-        // no copy
+        // the table holds these pointers (those of the upload, as when the
+        // caching allocator hands the same grad blocks back): read them there
         bool same = P->table_ptr == dev_table && P->table_grads.size() == count;
         for (size_t j = 0; same && j < count; ++j) same = grads[P->order[j]] == P->table_grads[j];
+        ks = -1;
         if (!same) {
             const int k = P->flip;
             P->flip ^= 1;
-            hipError_t e = hipEventSynchronize(P->ev[k]);   // the copy issued two steps ago is done
+            hipError_t e = hipEventSynchronize(P->ev[k]);   // the kernels that last read staging[k] are done
             if (e != hipSuccess) return hip_fail(e, "scalar route: staging wait");
             for (size_t j = 0; j < count; ++j) {
                 const void* gp = grads[P->order[j]];
                 if (!gp) return fail(CRESSO_E_INVALID, "scalar route: null grad pointer for tensor %d", P->order[j]);
                 P->staging[k][j] = gp;
             }
-            P->table_ptr = nullptr;   // unknown until the copy is queued
-            e = hipMemcpyAsync(table + P->grads_off, P->staging[k], sizeof(void*) * count, hipMemcpyHostToDevice, s);
-            if (e == hipSuccess) e = hipEventRecord(P->ev[k], s);
-            if (e != hipSuccess) return hip_fail(e, "scalar route: grad pointer upload");
-            P->table_grads.assign(P->staging[k], P->staging[k] + count);
-            P->table_ptr = dev_table;
+            ks = k;
         }
     }
+    P->cur = ks;
     const ScalarRec* drecs = reinterpret_cast<const ScalarRec*>(table);
     int32_t* dsteps = reinterpret_cast<int32_t*>(table + P->steps_off);
-    const void* const* dgrads = reinterpret_cast<const void* const*>(table + P->grads_off);
+    const void* const* dgrads = ks >= 0 ? P->dstaging[ks] : reinterpret_cast<const void* const*>(table + P->grads_off);
     for (const auto& G : P->groups) {
         const WideGeom wg{G.nblocks, reinterpret_cast<const int32_t*>(table + G.map_off),
                           reinterpret_cast<double*>(table + P->part_off)};
         hipError_t e = dispatch(G.v, drecs, dsteps, dgrads, G.first, G.count, G.lds, table, wg, h, s);
         if (e != hipSuccess) return hip_fail(e, "scalar route: kernel launch");
+    }
+    if (ks >= 0) {
+        const hipError_t e = hipEventRecord(P->ev[ks], s);
+        if (e != hipSuccess) return hip_fail(e, "scalar route: staging event");
     }
     return CRESSO_OK;
 }

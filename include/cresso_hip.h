@@ -113,9 +113,11 @@ int32_t cresso_scalar_plan_upload(cresso_scalar_plan* plan, void* dev_table, siz
  * cresso_v5.py:1434-1582 (route 0) or the micro-field step of
  * cresso_v5.py:1355-1432 (route 1) per tensor, param and states updated in place,
  * each tensor's step counter advanced on the device (state["step"] += 1).
- *   grads : NULL to reuse the grad pointers already in the table, else a host
+ *   grads : NULL to reuse the previous call's grad pointers, else a host
  *           array of `count` device pointers in descriptor order (autograd
- *           gives fresh grad tensors each step); uploaded from pinned staging
+ *           gives fresh grad tensors each step).  Copied (host side) into one
+ *           of two pinned, device-mapped staging buffers that the kernels read
+ *           directly; a call waits only for the kernels of two calls ago.
  *   hyper : current hyperparameters (lr may change between steps) */
 int32_t cresso_scalar_plan_step(cresso_scalar_plan* plan, void* dev_table, const void* const* grads,
                                 const cresso_hyper* hyper, void* stream);
