@@ -99,8 +99,8 @@ struct Geom {
 };
 
 struct Offs {
-    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins, tbuf, part, sums, hist, lt, imp, rowfx,
-        colfx, colfac, terms, ctrl, total;
+    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins, tbuf, part, part1, sums, hist, lt,
+        imp, rowfx, colfx, colfac, terms, ctrl, total;
 };
 
 // per-step device scalars (written by finalize kernels)
@@ -116,6 +116,7 @@ struct Ctrl {
     //         + k_nov tanh(err' nscale) + k_hash hash_pred
     float k_rat, k_ths, k_root, k_t, k_pred, k_echo, k_nov, k_hash, gain;
     float de_prev;            // drive_energy before this step (sweep 5 updates the state)
+    float fr_prev;            // force_rms before this step (sweep 2 updates the state)
 };
 
 // state pointers of one tensor (kernel argument)
@@ -773,8 +774,10 @@ __device__ void load_sums(const double* __restrict__ sums, int V, double* out) {
 template <typename PT, typename GT, bool V4>
 __global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
                                                        double* __restrict__ part, unsigned long long* __restrict__ rowfx,
-                                                       unsigned long long* __restrict__ colfx, cresso_hyper h) {
+                                                       unsigned long long* __restrict__ colfx, Ctrl* __restrict__ ctrl,
+                                                       const float* __restrict__ fr_state, cresso_hyper h) {
     __shared__ float red[4];
+    if (blockIdx.x == 0 && threadIdx.x == 0) ctrl->fr_prev = *fr_state;   // every block of sweep 2 reads the old value
     {
         const int64_t na = g.rows + g.cols, per = (na + g.nblk1 - 1) / g.nblk1;
         const int64_t a0 = (int64_t)blockIdx.x * per, a1 = a0 + per < na ? a0 + per : na;
@@ -839,22 +842,42 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restr
     P.flush(part);
 }
 
-__global__ __launch_bounds__(SP_FN_NT) void fin1_kernel(Geom g, const double* __restrict__ part, SpecState st,
-                                                         Ctrl* __restrict__ ctrl, int step, cresso_hyper h) {
-    __shared__ double red[1];
-    reduce_bm<1>(part, g.nblk1, 1, red);
-    if (threadIdx.x == 0) {
-        const float eps = (float)h.eps;
-        const float now = sqrtf((float)(red[0] / (double)g.n) + eps);
-        const float fr = reservoir_f(*st.force_rms, now, h.reservoir_decay, step);
-        *st.force_rms = fr;
-        const float s = fmaxf(fr, eps);
-        ctrl->scale = s;
-        ctrl->inv_s = 1.0f / s;
-        // density histogram scale: ds = rel^p <= (1e4)^p, at most n elements per bin
-        const double dsmax = pow(1.0e4, h.energy_power) + 1.0;
-        ctrl->hs_ds = ldexp(1.0, (int)floor(62.0 - log2(dsmax * (double)g.n)));
+// F1, in every block of sweep 2: sweep 1's block partials summed in a fixed
+// order (so every block gets the same values), then the force-RMS reservoir,
+// the scale and the density histogram's fixed-point scale.  Block 0 stores the
+// new force RMS and the values later kernels read from ctrl; the reservoir
+// starts from ctrl->fr_prev (stashed by sweep 1), so no block reads a value
+// another block of this launch writes.
+struct F1Values {
+    float inv_s;
+    double hs_ds;
+};
+__device__ F1Values fin1_values(const Geom& g, const double* __restrict__ part1, Ctrl* __restrict__ ctrl,
+                                float* __restrict__ fr_state, int step, const cresso_hyper& h) {
+    __shared__ double s_w[SP_NT / 64];
+    double a = 0.0;
+    for (int b = threadIdx.x; b < g.nblk1; b += SP_NT) a += part1[b];
+    const double w = wave_total_d(a);
+    if ((threadIdx.x & 63) == 63) s_w[threadIdx.x >> 6] = w;
+    __syncthreads();
+    double sum = 0.0;
+    for (int i = 0; i < SP_NT / 64; ++i) sum += s_w[i];
+    const float eps = (float)h.eps;
+    const float now = sqrtf((float)(sum / (double)g.n) + eps);
+    const float fr = reservoir_f(ctrl->fr_prev, now, h.reservoir_decay, step);
+    const float sc = fmaxf(fr, eps);
+    F1Values v;
+    v.inv_s = 1.0f / sc;
+    // density histogram scale: ds = rel^p <= (1e4)^p, at most n elements per bin
+    const double dsmax = pow(1.0e4, h.energy_power) + 1.0;
+    v.hs_ds = ldexp(1.0, (int)floor(62.0 - log2(dsmax * (double)g.n)));
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *fr_state = fr;
+        ctrl->scale = sc;
+        ctrl->inv_s = v.inv_s;
+        ctrl->hs_ds = v.hs_ds;
     }
+    return v;
 }
 
 // ---------------------------------------------------------------------------
@@ -1179,9 +1202,9 @@ template <int RM, int KC, typename PT, typename GT, int MODE>
 __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     Geom g, const GT* __restrict__ grad, const PT* __restrict__ param, const float* __restrict__ rowtab,
     const float* __restrict__ coltab, const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins,
-    const Ctrl* __restrict__ ctrl, double* __restrict__ part, unsigned long long* __restrict__ hist,
+    Ctrl* __restrict__ ctrl, double* __restrict__ part, unsigned long long* __restrict__ hist,
     unsigned long long* __restrict__ rowfx, unsigned long long* __restrict__ colfx, int hash_arg, int axes_arg,
-    cresso_hyper h) {
+    const double* __restrict__ part1, float* __restrict__ fr_state, int step, cresso_hyper h) {
     constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV2];
@@ -1217,14 +1240,15 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     __syncthreads();
     const PT* __restrict__ pb = param + base;
     const float* __restrict__ rt = rowtab + t.r0 * g.RW;
-    const float inv_s = ctrl->inv_s;
+    const F1Values f1 = fin1_values(g, part1, ctrl, fr_state, step, h);
+    const float inv_s = f1.inv_s;
     const float eps = (float)h.eps;
     const float pw = (float)h.energy_power;
     const float ipw = (float)fmax(h.instant_metric_power, 0.25);
     const bool ip_one = ipw == 1.0f;
     const float wd = (float)h.weight_decay;
     const float sg = h.maximize ? -1.f : 1.f;
-    const float hs = (float)ctrl->hs_ds;
+    const float hs = (float)f1.hs_ds;
     float Z[RW];
 #pragma unroll
     for (int q = 0; q < RW; ++q) Z[q] = 0.f;
@@ -1385,9 +1409,10 @@ __device__ __forceinline__ float row16_total(float v) {
 template <int RM, int KC, typename GT>
 __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
     Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
-    const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
+    const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl,
     double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ rowfx,
-    unsigned long long* __restrict__ colfx, cresso_hyper h) {
+    unsigned long long* __restrict__ colfx, const double* __restrict__ part1, float* __restrict__ fr_state, int step,
+    cresso_hyper h) {
     static_assert(RM <= 8, "16 projection rows");
     constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
@@ -1428,11 +1453,12 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
     for (int i = threadIdx.x; i < NH * TB; i += SP_NT) s_hist[i] = 0ull;
     stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
     __syncthreads();
-    const float inv_s = ctrl->inv_s;
+    const F1Values f1 = fin1_values(g, part1, ctrl, fr_state, step, h);
+    const float inv_s = f1.inv_s;
     const float eps = (float)h.eps;
     const float pw = (float)h.energy_power;
     const float sg = h.maximize ? -1.f : 1.f;
-    const float hs = (float)ctrl->hs_ds;
+    const float hs = (float)f1.hs_ds;
     f32x4m zacc[4];
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc) zacc[tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
@@ -3087,6 +3113,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.bins = take((size_t)g.binbytes * (size_t)g.n);
     o.tbuf = take(sizeof(float) * (size_t)g.n);
     o.part = take(sizeof(double) * (size_t)NVMAX * std::max(g.nblk, g.nblk1));
+    o.part1 = take(sizeof(double) * (size_t)g.nblk1);   // sweep 1's partials, read by every block of sweep 2
     o.sums = take(sizeof(double) * (size_t)NVMAX);
     o.hist = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
     o.lt = take(sizeof(float) * (size_t)g.T * g.B);
@@ -3155,6 +3182,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     const double* stats = at<double>(ws, o.stats);
     const double* bounds = at<double>(ws, o.bounds);
     const double* gram = at<double>(ws, o.gram);
+    double* part1 = at<double>(ws, o.part1);
     const int step = d.step;
     const int axes_on = (hard && h.instant_metric_coupling != 0.0 && !g.one_d) ? 1 : 0;
     const size_t l2 = lds_sweep2(g, 2 * RM), l3 = lds_sweep3(g, kcp<KC>(), 2 * RM), l4 = lds_sweep4(g, kcp<KC>(), 2 * RM);
@@ -3164,24 +3192,25 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     const dim3 grid(g.nblk), blk(SP_NT);
     const bool v4 = ((uintptr_t)grad % (4 * sizeof(GT))) == 0 && ((uintptr_t)param % (4 * sizeof(PT))) == 0;
     if (v4)
-        hipLaunchKernelGGL((sweep1_kernel<PT, GT, true>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, rowfx, colfx, h);
+        hipLaunchKernelGGL((sweep1_kernel<PT, GT, true>), dim3(g.nblk1), blk, 0, s, g, grad, param, part1, rowfx, colfx,
+                           ctrl, st.force_rms, h);
     else
-        hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part, rowfx, colfx, h);
-    hipLaunchKernelGGL(fin1_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, part, st, ctrl, step, h);
+        hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part1, rowfx, colfx,
+                           ctrl, st.force_rms, h);
     const bool fast = fast_mode(g, hash_on, axes_on, h);
     if constexpr (RM <= 8) {
         if (fast) {
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl, part,
-                               hist, rowfx, colfx, h);
+                               hist, rowfx, colfx, part1, st.force_rms, step, h);
             goto swept2;
         }
     }
     if (fast)
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, h);
+                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, h);
     else
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 0>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, h);
+                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, h);
 swept2:
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2), dim3(256), 0, s, part, g.nblk, NV2, sums);
     hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st,
