@@ -777,7 +777,12 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restr
                                                        unsigned long long* __restrict__ colfx, Ctrl* __restrict__ ctrl,
                                                        const float* __restrict__ fr_state, cresso_hyper h) {
     __shared__ float red[4];
-    if (blockIdx.x == 0 && threadIdx.x == 0) ctrl->fr_prev = *fr_state;   // every block of sweep 2 reads the old value
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        ctrl->fr_prev = *fr_state;   // every block of sweep 2 reads the old value
+        // density histogram scale: ds = rel^p <= (1e4)^p, at most n elements per bin
+        const double dsmax = pow(1.0e4, h.energy_power) + 1.0;
+        ctrl->hs_ds = ldexp(1.0, (int)floor(62.0 - log2(dsmax * (double)g.n)));
+    }
     {
         const int64_t na = g.rows + g.cols, per = (na + g.nblk1 - 1) / g.nblk1;
         const int64_t a0 = (int64_t)blockIdx.x * per, a1 = a0 + per < na ? a0 + per : na;
@@ -843,11 +848,11 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restr
 }
 
 // F1, in every block of sweep 2: sweep 1's block partials summed in a fixed
-// order (so every block gets the same values), then the force-RMS reservoir,
-// the scale and the density histogram's fixed-point scale.  Block 0 stores the
-// new force RMS and the values later kernels read from ctrl; the reservoir
-// starts from ctrl->fr_prev (stashed by sweep 1), so no block reads a value
-// another block of this launch writes.
+// order (so every block gets the same values), then the force-RMS reservoir
+// and the scale.  Block 0 stores the new force RMS and the values later
+// kernels read from ctrl; the reservoir starts from ctrl->fr_prev (stashed by
+// sweep 1, with the histogram scale hs_ds), so no block reads a value another
+// block of this launch writes.
 struct F1Values {
     float inv_s;
     double hs_ds;
@@ -868,14 +873,11 @@ __device__ F1Values fin1_values(const Geom& g, const double* __restrict__ part1,
     const float sc = fmaxf(fr, eps);
     F1Values v;
     v.inv_s = 1.0f / sc;
-    // density histogram scale: ds = rel^p <= (1e4)^p, at most n elements per bin
-    const double dsmax = pow(1.0e4, h.energy_power) + 1.0;
-    v.hs_ds = ldexp(1.0, (int)floor(62.0 - log2(dsmax * (double)g.n)));
+    v.hs_ds = ctrl->hs_ds;   // set by sweep 1
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         *fr_state = fr;
         ctrl->scale = sc;
         ctrl->inv_s = v.inv_s;
-        ctrl->hs_ds = v.hs_ds;
     }
     return v;
 }
