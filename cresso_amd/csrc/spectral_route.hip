@@ -2871,6 +2871,23 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
                                                        const double* __restrict__ part, float* __restrict__ de_state,
                                                        int step, int hash_on, int hard, int c5_closed, cresso_hyper h) {
     extern __shared__ __align__(16) unsigned char dyn[];
+    const int64_t beg = (int64_t)blockIdx.x * g.chunk1;
+    const int64_t end = beg + g.chunk1 < g.n ? beg + g.chunk1 : g.n;
+    // chunks are multiples of 4 elements: float4 drive loads (param 4-element aligned)
+    const int64_t vend = V4 ? beg + ((end - beg) & ~(int64_t)3) : beg;
+    const int64_t st = 4 * (int64_t)SP_NT;
+    int64_t e = beg + 4 * (int64_t)threadIdx.x;
+    // the first two float4 of drive and param go out before the gain is known
+    // (their loads stay in flight through the finish's reduction)
+    const bool pre = e + st < vend;
+    float4 d0 = make_float4(0.f, 0.f, 0.f, 0.f), d1 = d0;
+    float p0[4] = {0.f, 0.f, 0.f, 0.f}, p1[4] = {0.f, 0.f, 0.f, 0.f};
+    if (pre) {
+        d0 = *reinterpret_cast<const float4*>(dbuf + e);
+        d1 = *reinterpret_cast<const float4*>(dbuf + e + st);
+        Ld4<PT>::go(param, e, p0);
+        Ld4<PT>::go(param, e + st, p1);
+    }
     float gain, c5;
     fin4_values(g, part, ctrl, de_state, step, hash_on, hard, c5_closed, h, gain, c5);
     const int TB = g.T * g.B;
@@ -2882,8 +2899,6 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
     }
     const float kh = c5 * (1.0f / (float)T);
     const float nlr = (float)(-h.lr);
-    const int64_t beg = (int64_t)blockIdx.x * g.chunk1;
-    const int64_t end = beg + g.chunk1 < g.n ? beg + g.chunk1 : g.n;
     auto drive_at = [&](int64_t e, float d) -> float {
         if (!HASH) return d;
         const uint64_t pk = load_bins(bins, e, binbytes);
@@ -2895,8 +2910,6 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
         }
         return d + kh * hp;
     };
-    // chunks are multiples of 4 elements: float4 drive loads (param 4-element aligned)
-    const int64_t vend = V4 ? beg + ((end - beg) & ~(int64_t)3) : beg;
     auto apply4 = [&](int64_t e, const float4& d4, const float* pv) {
         const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
         float o[4];
@@ -2908,16 +2921,19 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
         St4<PT>::go(param, e, o);
     };
     // two float4 of drive and param per thread in flight per iteration, then the rest
-    const int64_t st = 4 * (int64_t)SP_NT;
-    int64_t e = beg + 4 * (int64_t)threadIdx.x;
-    for (; e + st < vend; e += 2 * st) {
-        const float4 d0 = *reinterpret_cast<const float4*>(dbuf + e);
-        const float4 d1 = *reinterpret_cast<const float4*>(dbuf + e + st);
-        float p0[4], p1[4];
-        Ld4<PT>::go(param, e, p0);
-        Ld4<PT>::go(param, e + st, p1);
+    if (pre) {
         apply4(e, d0, p0);
         apply4(e + st, d1, p1);
+        e += 2 * st;
+    }
+    for (; e + st < vend; e += 2 * st) {
+        const float4 da = *reinterpret_cast<const float4*>(dbuf + e);
+        const float4 db = *reinterpret_cast<const float4*>(dbuf + e + st);
+        float pa[4], pb[4];
+        Ld4<PT>::go(param, e, pa);
+        Ld4<PT>::go(param, e + st, pb);
+        apply4(e, da, pa);
+        apply4(e + st, db, pb);
     }
     for (; e < vend; e += st) {
         const float4 d4 = *reinterpret_cast<const float4*>(dbuf + e);
