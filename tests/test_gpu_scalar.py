@@ -270,3 +270,39 @@ def test_scalar_steady_state_replans_on_changes():
         oopt.step(gs)
     torch.cuda.synchronize()
     compare(hp, hopt, op, oopt)
+
+
+def test_scalar_plan_step_null_grads_reuse_the_previous_pointers():
+    # C ABI: grads == NULL reuses the previous call's grad pointers, here the
+    # staged ones of a step whose grads differ from the plan's upload
+    import ctypes
+
+    import cresso_amd
+    from cresso_amd import _native
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    announce("scalar plan step with NULL grads")
+    gen = torch.Generator().manual_seed(16)
+    shapes = [(4096, 16), (16, 4096), (33, 7)]
+    p0 = [0.02 * torch.randn(s, generator=gen) for s in shapes]
+    g1 = [1e-2 * torch.randn(s, generator=gen) for s in shapes]
+    g2 = [1e-2 * torch.randn(s, generator=gen) for s in shapes]
+    hp = [torch.nn.Parameter(p.clone().cuda()) for p in p0]
+    op = [p.clone() for p in p0]
+    hopt = cresso_amd.CRESSO5(hp, cuda_ops="required", **SCALAR_KW)
+    oopt = OracleCRESSO5(op, **SCALAR_KW)
+    for gs in (g1, g2):
+        for p, g in zip(hp, gs):
+            p.grad = g.cuda()
+        hopt.step()
+        oopt.step(gs)
+    batch = next(b for k, b in hopt._batches.items() if k[1] == "scalar")
+    hyper = _native.hyper_from_group(hopt.param_groups[0])
+    rc = batch.lib.cresso_scalar_plan_step(batch.plan, ctypes.c_void_p(batch.table.data_ptr()), None,
+                                           ctypes.byref(hyper), ctypes.c_void_p(_native.stream_handle(hp[0].device)))
+    _native.check(rc, "scalar plan step (NULL grads)")
+    for st in batch.states:
+        st["step"] += 1
+    oopt.step(g2)
+    torch.cuda.synchronize()
+    compare(hp, hopt, op, oopt)
