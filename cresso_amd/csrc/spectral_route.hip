@@ -41,9 +41,11 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <tuple>
 #include <vector>
 
@@ -2971,6 +2973,7 @@ struct cresso_spectral_plan {
     int64_t shape[8];
     int32_t rmax;
     int32_t bins_off;   // hash_bins == 0: no bin tables (bins/counts hold a dummy single bin)
+    uint64_t serial;    // unique per created plan (never reused): names the tables a workspace holds
 };
 
 namespace cresso {
@@ -3311,11 +3314,13 @@ extern "C" cresso_spectral_plan* cresso_spectral_plan_create(const int64_t* shap
         fail(CRESSO_E_INVALID, "spectral route: null shape or freqs");
         return nullptr;
     }
+    static std::atomic<uint64_t> next_serial{1};
     cresso_spectral_plan* P = new cresso_spectral_plan();
     if (plan_spectral(shape, ndim, freqs, rank, hash_bins, hash_tables, *P) != CRESSO_OK) {
         delete P;
         return nullptr;
     }
+    P->serial = next_serial.fetch_add(1);
     return P;
 }
 
@@ -3406,6 +3411,57 @@ extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cre
 #undef CRESSO_SP_CASE
 #undef CRESSO_SP_RUN
     return fail(CRESSO_E_UNSUPPORTED, "spectral route: param/grad dtype pair (%d,%d) not supported by this build", pt, gt);
+}
+
+// ---------------------------------------------------------------------------
+// cresso_spectral_step_noalloc: the step above with its workspace (carrier
+// tables, bins, tangent field and per-step scratch) in a static device array,
+// for callers that cannot allocate.  Each GPU the library runs on holds its
+// own copy of `scratch` until the process ends.  The array keeps the last
+// call's contents: a call whose plan differs from the one whose tables the
+// device's copy holds first rebuilds the tables (and clears the histogram
+// and count regions) exactly as cresso_spectral_workspace_init does.  Calls
+// that overlap on one GPU (two streams, or two host threads) share the array
+// and race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[CRESSO_SPECTRAL_NOALLOC_MAX_BYTES];
+
+namespace {
+constexpr int kNoallocMaxDev = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kNoallocMaxDev];       // device address of `scratch` per device (hipGetSymbolAddress)
+uint64_t g_noalloc_plan[kNoallocMaxDev];   // serial of the plan whose tables that copy holds (0: none)
+}  // namespace
+
+extern "C" int32_t cresso_spectral_step_noalloc(const cresso_spectral_plan* P, const cresso_spectral_desc* d,
+                                                const cresso_hyper* hyper, void* stream) {
+    if (!P || !d || !hyper) return fail(CRESSO_E_INVALID, "spectral route (no-alloc): null argument");
+    const size_t need = P->o.total;
+    if (need > (size_t)CRESSO_SPECTRAL_NOALLOC_MAX_BYTES)
+        return fail(CRESSO_E_INVALID,
+                    "spectral route (no-alloc): this plan needs %zu bytes of workspace, above the %zu-byte static "
+                    "scratch; use cresso_spectral_step with a caller-allocated workspace",
+                    need, (size_t)CRESSO_SPECTRAL_NOALLOC_MAX_BYTES);
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "spectral route (no-alloc): hipGetDevice");
+    if (dev < 0 || dev >= kNoallocMaxDev)
+        return fail(CRESSO_E_UNSUPPORTED, "spectral route (no-alloc): device %d outside 0..%d", dev, kNoallocMaxDev - 1);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return hip_fail(e, "spectral route (no-alloc): hipGetSymbolAddress(scratch)");
+        g_noalloc_ptr[dev] = ptr;
+    }
+    void* ws = g_noalloc_ptr[dev];
+    if (g_noalloc_plan[dev] != P->serial) {
+        g_noalloc_plan[dev] = 0;   // tables unknown until the rebuild below succeeds
+        const int32_t rc = cresso_spectral_workspace_init(P, ws, need, hyper, stream);
+        if (rc != CRESSO_OK) return rc;
+        g_noalloc_plan[dev] = P->serial;
+    }
+    return cresso_spectral_step(P, d, ws, need, hyper, stream);
 }
 
 extern "C" int32_t cresso_spectral_workspace_bins(const cresso_spectral_plan* P, const void* ws, size_t ws_bytes,

@@ -174,6 +174,26 @@ typedef struct cresso_spectral_desc {
 int32_t cresso_spectral_step(const cresso_spectral_plan* plan, const cresso_spectral_desc* desc, void* workspace,
                              size_t workspace_bytes, const cresso_hyper* hyper, void* stream);
 
+/* cresso_spectral_step without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ *
+ * The workspace lives in a static device array of
+ * CRESSO_SPECTRAL_NOALLOC_MAX_BYTES bytes that every GPU the library runs on
+ * holds until the process ends; the call allocates and frees nothing.  A plan
+ * whose cresso_spectral_workspace_bytes() exceeds that size is rejected with
+ * CRESSO_E_INVALID (at T = 2 tables of <= 256 bins the limit admits about
+ * 5 M elements, e.g. a 2048 x 2048 tensor).  The array keeps the last call's
+ * contents: when the plan differs from the one of the device's previous
+ * no-alloc call, the call first rebuilds the plan's tables in it (as
+ * cresso_spectral_workspace_init does, including its one synchronization of
+ * `stream`).  All calls on one GPU share the array: calls that overlap (two
+ * streams or two host threads) race.  Results are identical to
+ * cresso_spectral_step's. */
+#define CRESSO_SPECTRAL_NOALLOC_MAX_BYTES (32u << 20)
+int32_t cresso_spectral_step_noalloc(const cresso_spectral_plan* plan, const cresso_spectral_desc* desc,
+                                     const cresso_hyper* hyper, void* stream);
+
 /* Inspection of an initialised workspace, for parity checks (a step does not
  * need these).
  *
