@@ -31,8 +31,13 @@ Prints ONE JSON line.  `value` is the algorithmic HBM throughput of a step
 `roofline.achieved` is the same algorithmic bytes over one step's mean
 duration in the timed region: one pair of HIP events on the launch stream
 around the K steps (an event pair around every step would add its own cost,
-7-15 us a step, so the timed region holds none); `cpu_baseline` times the CPU oracle (a port of the reference's
-cuda_ops="off" path) on the host cores over a bounded sample.
+7-15 us a step, so the timed region holds none).  `roofline.traffic` is the
+HBM bytes per step from the committed rocprofv3 counter summary, reported only
+when that summary was measured on the current kernel sources (a digest of
+cresso_amd/csrc/ recorded in it).  `cpu_baseline` times the CPU oracle (a port
+of the reference's cuda_ops="off" path) on the host cores, and `parity`
+compares a fresh GPU optimizer with it after the same steps on the timed
+leg's own inputs (cpu_and_parity).
 """
 
 from __future__ import annotations
@@ -83,19 +88,89 @@ def make_c2(device, pool=4, seed=0):
     return params, grads, kwargs, [shape], None
 
 
+def make_c1(device, pool=10, seed=0):
+    """C1 (the reference's CPU-runnable case): one fp32 (2048,2048) param, p0 = 0.02 randn, then
+    a fresh grad 1e-3 randn per step from the same generator (seed 0); rank 8, F = 5, B = 64, T = 2."""
+    gen = torch.Generator().manual_seed(seed)
+    shape = (2048, 2048)
+    params = [torch.nn.Parameter((0.02 * torch.randn(shape, generator=gen)).to(device))]
+    grads = [[(1e-3 * torch.randn(shape, generator=gen)).to(device)] for _ in range(pool)]
+    kwargs = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2)
+    return params, grads, kwargs, [shape], None
+
+
+C4_SHAPES = [(32000, 2048), (2048, 2048), (5632, 2048), (2048, 5632), (2048,)]
+
+
+def c4_layer_shapes(layers=22):
+    """The full C4 set: embedding, then per layer q,k,v,o, gate, up, down and two RMSNorm weights."""
+    out = [(32000, 2048)]
+    for _ in range(layers):
+        out += [(2048, 2048)] * 4 + [(5632, 2048)] * 2 + [(2048, 5632)] + [(2048,)] * 2
+    return out
+
+
+def make_c4(device, pool=2, seed=0, shapes=None):
+    """C4: fp32 tensors, grads N(0, sigma) with sigma = 10^U(-5,-2) per tensor; p0 = 0.02 randn.
+    shapes=None is the full 1.2 B-element set; C4_SHAPES is one tensor of each distinct shape."""
+    shapes = c4_layer_shapes() if shapes is None else shapes
+    gen = torch.Generator().manual_seed(seed)
+    sig = (10.0 ** (torch.rand(len(shapes), generator=gen, dtype=torch.float64) * 3.0 - 5.0)).tolist()
+    params = [torch.nn.Parameter((0.02 * torch.randn(s, generator=gen)).to(device)) for s in shapes]
+    grads = [[(sc * torch.randn(s, generator=gen)).to(device) for s, sc in zip(shapes, sig)] for _ in range(pool)]
+    kwargs = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2)
+    return params, grads, kwargs, shapes, sig
+
+
+C5_SHAPES = [(8192, 8192), (512, 256, 3, 3), (256, 256, 3, 3), (64, 512, 512)]
+C5_DTYPES = [torch.bfloat16, torch.float32, torch.float32, torch.float32]
+
+
+def make_c5(device, pool=2, seed=0):
+    """C5: bf16 (8192,8192) with bf16 grads, fp32 conv and 3-D tensors; grads N(0, 1e-3) in the
+    parameter dtype (drawn in fp32, then cast); p0 = 0.02 randn.  rank 16, F = 7, B = 256, T = 4."""
+    gen = torch.Generator().manual_seed(seed)
+    params = [torch.nn.Parameter((0.02 * torch.randn(s, generator=gen)).to(dt).to(device))
+              for s, dt in zip(C5_SHAPES, C5_DTYPES)]
+    grads = [[(1e-3 * torch.randn(s, generator=gen)).to(dt).to(device) for s, dt in zip(C5_SHAPES, C5_DTYPES)]
+             for _ in range(pool)]
+    kwargs = dict(lr=2e-3, rank=16, max_frequency=7, hash_bins=256, hash_tables=4)
+    return params, grads, kwargs, C5_SHAPES, None
+
+
 TRAFFIC_FILES = {"c2": "profiles/spectral_step_c2_hbm_traffic.md", "c3": "profiles/scalar_step_c3_hbm_traffic.md"}
+SOURCE_GLOBS = ("cresso_amd/csrc/*.hip", "cresso_amd/csrc/*.hpp", "cresso_amd/csrc/*.cpp")
+
+
+def source_digest():
+    """Digest of the library's kernel sources: a traffic figure measured on other sources is stale."""
+    import hashlib
+    h = hashlib.sha256()
+    for pat in SOURCE_GLOBS:
+        for path in sorted(ROOT.glob(pat)):
+            h.update(path.name.encode())
+            h.update(path.read_bytes())
+    return h.hexdigest()[:16]
 
 
 def measured_traffic(workload):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary of this workload (scaled by the copy calibration), or None."""
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of
+    this workload (scaled by the copy calibration) -> (bytes or None, note).  The summary
+    records the digest of the kernel sources it was measured on; a figure measured on other
+    sources is not reported."""
     path = ROOT / TRAFFIC_FILES.get(workload, "-")
     if not path.is_file():
-        return None
+        return None, "no profile"
+    nbytes, digest = None, None
     for line in path.read_text().splitlines():
         if line.startswith("- scaled HBM bytes"):
-            return int(float(line.rsplit(":", 1)[1]))
-    return None
+            nbytes = int(float(line.rsplit(":", 1)[1]))
+        if line.startswith("- kernel source digest:"):
+            digest = line.rsplit(":", 1)[1].strip()
+    cur = source_digest()
+    if digest != cur:
+        return None, f"{TRAFFIC_FILES[workload]} was measured on kernel sources {digest}, these are {cur}"
+    return nbytes, f"{TRAFFIC_FILES[workload]} (rocprofv3 FETCH_SIZE + WRITE_SIZE, kernel sources {cur})"
 
 
 def algorithmic_bytes(shapes, elem_bytes=4):
@@ -107,8 +182,7 @@ def time_gpu(workload, steps, warmup):
     import cresso_amd
 
     device = torch.device("cuda:0")
-    maker = make_c2 if workload == "c2" else make_c3
-    params, grads, kwargs, shapes, _ = maker(device)
+    params, grads, kwargs, shapes, _ = MAKERS[workload](device)
     opt = cresso_amd.CRESSO5(params, cuda_ops="required", **kwargs)
     pool = len(grads)
 
@@ -281,6 +355,7 @@ def rocprof_summary(dirs, calib=None, launches=None):
                 out.append(line)
             if tb:
                 out.append(f"- scaled HBM bytes (those counters above): {tb:.0f}")
+                out.append(f"- kernel source digest: {source_digest()}")
         if "SQ_INSTS_VALU" in counters:
             # issue-time floor of each kernel's vector work on the whole chip:
             # a wave64 VALU op holds a 16-lane SIMD 4 cycles (transcendentals
@@ -300,32 +375,106 @@ def rocprof_summary(dirs, calib=None, launches=None):
     print("\n".join(out))
 
 
-def time_cpu(workload, sample_steps=2):
-    """CPU oracle (port of the reference's cuda_ops='off' path) on this host's cores."""
-    from oracle.cresso_oracle import OracleCRESSO5
+MAKERS = {"c2": make_c2, "c3": make_c3}
+
+
+def cpu_and_parity(workload, steps=4):
+    """The CPU baseline and the in-run parity check, on identical inputs.
+
+    The CPU oracle (a port of the reference's cuda_ops="off" path) and a fresh
+    GPU optimizer both take `steps` steps from the timed leg's own seeded
+    inputs (seed 0: the same params and grad pool, cycled the same way).  The
+    first CPU step (state set-up) is untimed; the others give the median and
+    mean.  Then params, every state tensor and the last step's update
+    dp = p_after - p_before are compared; for the spectral route the
+    workspace's hash bins and bin counts are compared with the oracle's
+    integer restatement, bit for bit."""
+    import numpy as np
+    import cresso_amd
+    from oracle.cresso_oracle import OracleCRESSO5, hash_index_np
 
     torch.set_num_threads(os.cpu_count() or 1)
-    maker = make_c2 if workload == "c2" else make_c3
-    params, grads, kwargs, shapes, _ = maker(torch.device("cpu"), pool=sample_steps + 1, seed=1)
-    ps = [p.detach().clone() for p in params]
-    opt = OracleCRESSO5(ps, **kwargs)
-    if workload == "c3":
-        # bounded sample: every 8th tensor (105 of 840), scaled to the full step
-        idx = list(range(0, len(ps), 8))
-        opt = OracleCRESSO5([ps[i] for i in idx], **kwargs)
-        grads = [[g[i] for i in idx] for g in grads]
-        frac = len(idx) / len(ps)
-        sample = f"{len(idx)} of 840 tensors, {sample_steps} timed steps after 1 warm-up, scaled x{1/frac:.1f}"
-    else:
-        frac = 1.0
-        sample = f"full (4096,4096) tensor, {sample_steps} timed steps after 1 warm-up"
-    opt.step(grads[0])
-    t0 = time.perf_counter()
-    for k in range(sample_steps):
-        opt.step(grads[1 + k])
-    dt = (time.perf_counter() - t0) / sample_steps / frac
-    return dict(value=round(dt * 1e3, 3), unit="ms/step", cores=torch.get_num_threads(), kind="port",
-                sample=sample, cpu=_cpu_model())
+    params, grads, kwargs, shapes, _ = MAKERS[workload](torch.device("cpu"))
+    pool = len(grads)
+    # the reference's sequential fp32 scatter_add carries ~1e-5 relative error
+    # of its own at 262144 elements per bin: fp64 bin sums break the tie
+    accum = "fp64" if workload == "c2" else "native"
+    cpu_ps = [p.detach().clone() for p in params]
+    oracle = OracleCRESSO5(cpu_ps, hash_accum=accum, **kwargs)
+    dev = torch.device("cuda:0")
+    gpu_ps = [torch.nn.Parameter(p.detach().clone().to(dev)) for p in params]
+    gopt = cresso_amd.CRESSO5(gpu_ps, cuda_ops="required", **kwargs)
+    gdev = [[g.to(dev) for g in gs] for gs in grads]
+    times = []
+    for k in range(steps):
+        last = k == steps - 1
+        if last:
+            torch.cuda.synchronize()
+            before_g = [p.detach().double().cpu() for p in gpu_ps]
+            before_o = [p.double() for p in cpu_ps]
+        t0 = time.perf_counter()
+        oracle.step(grads[k % pool])
+        if k:
+            times.append(time.perf_counter() - t0)
+        for p, g in zip(gpu_ps, gdev[k % pool]):
+            p.grad = g
+        gopt.step()
+    torch.cuda.synchronize()
+    # parity
+    p_err, p_ok, dp_err, s_err, s_ok = 0.0, True, 0.0, 0.0, True
+    for i, (a, b) in enumerate(zip(gpu_ps, cpu_ps)):
+        got, exp = a.detach().double().cpu(), b.double()
+        d = (got - exp).abs()
+        p_err = max(p_err, float(d.max()))
+        p_ok = p_ok and bool((d <= 1e-6 + 1e-5 * exp.abs()).all())
+        dg, de = got - before_g[i], exp - before_o[i]
+        scale = float(de.pow(2).mean().sqrt())
+        dp_err = max(dp_err, float(((dg - de).abs() / (de.abs() + scale + 1e-30)).max()))
+        sa, sb = gopt.state[a], oracle.state[i]
+        for key, v in sb.items():
+            if not torch.is_tensor(v) or key == "freqs":
+                s_ok = s_ok and (key not in sa or (sa[key] == v if not torch.is_tensor(v)
+                                                   else bool(torch.equal(sa[key].cpu(), v))))
+                continue
+            gv, ev = sa[key].double().cpu(), v.double()
+            dd = (gv - ev).abs()
+            s_err = max(s_err, float((dd / (ev.abs() + 1e-6)).max()))
+            s_ok = s_ok and bool((dd <= 1e-6 + 1e-5 * ev.abs()).all())
+    parity = {"steps": steps, "inputs": "identical to the timed leg's (seed 0, same grad pool)",
+              "oracle_hash_accum": accum, "tolerance": "rtol 1e-5, atol 1e-6 (fp32)",
+              "param_max_abs_err": float(f"{p_err:.3e}"), "params_within_tol": p_ok,
+              "state_max_rel_err": float(f"{s_err:.3e}"), "states_within_tol": s_ok,
+              "update_max_err_of_scale": float(f"{dp_err:.3e}")}
+    if workload == "c2":
+        eng = gopt._spectral_engine
+        ws = next(iter(eng.ws.values()))
+        n = gpu_ps[0].numel()
+        T, B = kwargs["hash_tables"], kwargs["hash_bins"]
+        bins = torch.empty(T, n, dtype=torch.int32, device=dev)
+        counts = torch.empty(T, B, dtype=torch.int64, device=dev)
+        import ctypes
+        from cresso_amd import _native
+        _native.check(eng.lib.cresso_spectral_workspace_bins(
+            ws.plan, ctypes.c_void_p(ws.buf.data_ptr()), ctypes.c_size_t(ws.buf.numel()),
+            ctypes.c_void_p(bins.data_ptr()), ctypes.c_void_p(counts.data_ptr()),
+            ctypes.c_void_p(_native.stream_handle(dev))), "workspace bins")
+        torch.cuda.synchronize()
+        bins_ok, counts_ok = True, True
+        for t in range(T):
+            ref = hash_index_np(n, B, t)
+            bins_ok = bins_ok and bool(np.array_equal(bins[t].cpu().numpy(), ref))
+            counts_ok = counts_ok and bool(np.array_equal(counts[t].cpu().numpy(), np.bincount(ref, minlength=B)))
+        parity["bins_bit_exact"] = bins_ok
+        parity["counts_bit_exact"] = counts_ok
+    parity["ok"] = bool(p_ok and s_ok and parity.get("bins_bit_exact", True) and parity.get("counts_bit_exact", True))
+    times.sort()
+    med = times[len(times) // 2] if len(times) % 2 else 0.5 * (times[len(times) // 2 - 1] + times[len(times) // 2])
+    what = "the full (4096,4096) tensor" if workload == "c2" else "all 840 tensors"
+    cpu = dict(value=round(med * 1e3, 3), unit="ms/step", median_ms=round(med * 1e3, 3),
+               mean_ms=round(sum(times) / len(times) * 1e3, 3), cores=torch.get_num_threads(), kind="port",
+               sample=f"{what}, {len(times)} timed steps after 1 untimed set-up step, on the timed leg's inputs",
+               cpu=_cpu_model(), os_cpu_count=os.cpu_count())
+    return cpu, parity
 
 
 def _cpu_model():
@@ -347,6 +496,7 @@ def measure(workload, args):
     """Time one workload on the GPU (and its CPU baseline); one record."""
     res = time_gpu(workload, args.steps, args.warmup)
     nbytes, n = algorithmic_bytes(res["shapes"])
+    traffic, traffic_note = measured_traffic(workload)
     ms = res["ms_per_step"]
     achieved = nbytes / (ms * 1e-3) / 1e9   # the launch = one step; its mean duration over the timed region
     rec = {
@@ -356,12 +506,12 @@ def measure(workload, args):
         "ms_per_step": round(ms, 4),
         "config": {"workload": WORKLOAD_NAMES[workload], "elements": n, "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(workload),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_note,
                      "launch": "one optimizer step (the library's kernel sequence); mean over the timed region, "
                                "HIP events on the launch stream"},
     }
     if not args.no_cpu:
-        rec["cpu_baseline"] = time_cpu(workload)
+        rec["cpu_baseline"], rec["parity"] = cpu_and_parity(workload)
     return rec
 
 
@@ -407,6 +557,7 @@ def main():
     }
     if "cpu_baseline" in first:
         out["cpu_baseline"] = first["cpu_baseline"]
+        out["parity"] = first["parity"]
     if len(recs) > 1:
         # the metric names both headline configs: the second rides along with
         # the same fields (value = algorithmic GB/s, ms_per_step, roofline, CPU)

@@ -141,6 +141,22 @@ def _declare(lib: ctypes.CDLL) -> None:
                                                           c.c_void_p, c.c_void_p, c.c_void_p]
     lib.cresso_spectral_workspace_gram.restype = c.c_int32
     lib.cresso_spectral_workspace_gram.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_void_p]
+    vp, i32, i64, f64 = c.c_void_p, c.c_int32, c.c_int64, c.c_double
+    lib.cresso_unit_workspace_bytes.restype = c.c_size_t
+    lib.cresso_unit_workspace_bytes.argtypes = [i32]
+    lib.cresso_hash_metric_update_log.restype = i32
+    lib.cresso_hash_metric_update_log.argtypes = [vp, i64, vp, i32, i32, i32, f64, f64, f64, f64, vp, vp, c.c_size_t, vp]
+    lib.cresso_hash_impulse_update_gather.restype = i32
+    lib.cresso_hash_impulse_update_gather.argtypes = [vp, i64, vp, vp, i32, i32, f64, f64, f64, vp, vp, c.c_size_t, vp]
+    lib.cresso_metric_update.restype = i32
+    lib.cresso_metric_update.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, f64, f64, vp]
+    lib.cresso_confidence_update.restype = i32
+    lib.cresso_confidence_update.argtypes = [vp, vp, vp, vp, vp, i32, f64, f64, vp]
+    lib.cresso_contact_update_pair.restype = i32
+    lib.cresso_contact_update_pair.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32] + [f64] * 9 + [vp]
+    lib.cresso_drive_update.restype = i32
+    lib.cresso_drive_update.argtypes = [vp, i32, vp, vp, vp, vp, vp, vp, vp, i64, i32, i32, c.POINTER(Hyper), vp,
+                                        c.c_size_t, vp]
     lib.cresso_spectral_workspace_basis.restype = c.c_int32
     lib.cresso_spectral_workspace_basis.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_int32, c.c_void_p,
                                                     c.c_void_p, c.c_void_p]

@@ -48,6 +48,19 @@ template <> __device__ __forceinline__ __hip_bfloat16 from_w<__hip_bfloat16>(flo
 template <typename T> __device__ __forceinline__ T from_wd(double v) { return from_w<T>((float)v); }
 template <> __device__ __forceinline__ double from_wd<double>(double v) { return v; }
 
+// The step of the parameter update p.add_(u, alpha=-lr) (cresso_v5.py:1353,
+// 1582, 1432) for a param of storage dtype T: torch's CPU add kernel rounds
+// alpha to the tensor's dtype for fp16/bf16 tensors (then computes in fp32),
+// so the reference's update uses -lr rounded to the param dtype there; fp32
+// and fp64 params keep it.
+template <typename T> __device__ __forceinline__ double update_alpha(double a) { return a; }
+template <> __device__ __forceinline__ double update_alpha<__half>(double a) {
+    return (double)__half2float(__float2half_rn((float)a));
+}
+template <> __device__ __forceinline__ double update_alpha<__hip_bfloat16>(double a) {
+    return (double)__bfloat162float(__float2bfloat16((float)a));
+}
+
 // ---------------------------------------------------------------------------
 // global-memory views of caller pointers: the address-space cast lets the
 // compiler emit global_load / global_store (no flat aperture handling, no LDS
@@ -238,6 +251,22 @@ __device__ __forceinline__ void block_sum(double (&v)[V], double* lds) {
         v[i] = s;
     }
     __syncthreads();
+}
+
+// Float (already scaled by a power of two, |x| < 2^62) to a 64-bit fixed-point
+// integer, rounded to nearest even (unbiased: a bin collects up to ~10^6
+// elements, so a one-sided rounding such as truncation would add a coherent
+// half quantum per element): rint, then two exact 32-bit conversions.
+__device__ __forceinline__ unsigned long long to_fixed_u(float x) {
+    x = rintf(x);
+    const float hf = floorf(x * 2.3283064365386963e-10f);  // x / 2^32 (exact scaling)
+    const float lf = fmaf(-hf, 4294967296.0f, x);           // x - hi*2^32: exact, in [0, 2^32)
+    return ((unsigned long long)(unsigned)hf << 32) | (unsigned long long)(unsigned)lf;
+}
+// two's complement of the magnitude's conversion (rounding is symmetric)
+__device__ __forceinline__ unsigned long long to_fixed_s(float x) {
+    const unsigned long long u = to_fixed_u(fabsf(x));
+    return x < 0.f ? (0ull - u) : u;
 }
 
 // ---------------------------------------------------------------------------

@@ -18,7 +18,9 @@
 namespace {
 
 struct BatchGuard {
-    std::vector<PyObject*> params;   // identities only (the optimizer's param groups keep them alive)
+    // Strong references: a parameter cannot be freed (and a new object created
+    // at its address) while the guard lives, so the identity test is exact.
+    std::vector<py::object> params;
     std::vector<const void*> pptr;   // param storage at plan time
     std::vector<int> gdtype;         // grad dtype at plan time (c10::ScalarType)
     std::vector<int64_t> numel;
@@ -33,7 +35,7 @@ struct BatchGuard {
             const at::Tensor& t = THPVariable_Unpack(o);
             const at::Tensor& g = t.grad();
             if (!g.defined()) throw std::invalid_argument("BatchGuard: every parameter needs a grad at plan time");
-            params.push_back(o);
+            params.push_back(py::reinterpret_borrow<py::object>(o));
             pptr.push_back(t.data_ptr());
             gdtype.push_back(static_cast<int>(g.scalar_type()));
             numel.push_back(t.numel());
@@ -49,7 +51,7 @@ struct BatchGuard {
         void** out = reinterpret_cast<void**>(out_addr);
         for (size_t i = 0; i < n; ++i) {
             PyObject* o = ps[i].ptr();
-            if (o != params[i]) return false;
+            if (o != params[i].ptr()) return false;
             const at::Tensor& t = THPVariable_Unpack(o);
             if (t.data_ptr() != pptr[i]) return false;
             const at::Tensor& g = t.grad();

@@ -209,7 +209,9 @@ __device__ DriveCoef<W> contact_and_coefs(const double* M, double dn, const cres
     align = align < (W)-1 ? (W)-1 : (align > (W)1 ? (W)1 : align);
     W agate = (align + (W)1) * (W)0.5;
     agate = agate < 0 ? (W)0 : (agate > 1 ? (W)1 : agate);
-    if (!(prms > (W)sqrt(h.eps))) agate = 0;
+    // the predicate prms > sqrt(eps) in fp64 (in fp32 it is a rounding tie
+    // when q1^2 is below half an ulp of eps)
+    if (!(sqrt((double)q1 * (double)q1 + h.eps) > sqrt(h.eps))) agate = 0;
     const double warm = h.warmup_steps == 0 ? 1.0 : 1.0 - exp(-(double)step / (double)(h.warmup_steps > 1 ? h.warmup_steps : 1));
     const W mix = (W)(h.prediction_mix * warm) * agate / ((W)1 + S);
     const W rms_rat = (W)sqrt((double)((W)(M[4] / dn) + eps));
@@ -647,7 +649,7 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
     const float gain = uni(clampf((float)h.target_update_rms / sqrtf(de + eps), (float)h.min_gain, (float)h.max_gain));
 
     // ---- pass E ----
-    const float nlr = uni((float)(-h.lr));
+    const float nlr = uni((float)update_alpha<PT>(-h.lr));
     if constexpr (FAST) {
         // groups of 4 slots; the param loads of group j+1 are issued before
         // group j is updated (two groups of loads in flight, bounded registers)
@@ -1094,7 +1096,7 @@ template <typename W, typename PT, typename GT> struct Stream {
     // param -= lr * cast(drive * gain); each element's grad and param are read
     // before this thread stores that element
     __device__ void passE(const StreamCtl<W>& c, int64_t i0, int64_t i1, int tid, int S) const {
-        const W nlr = (W)(-h.lr);
+        const W nlr = (W)update_alpha<PT>(-h.lr);
         int64_t i = i0 + tid;
         each<true, true>(i0, i1, tid, S, [&](W f, W pv, W fa, W fb) {
             const W d = drive(c, tangent(c, f, fa, fb));
@@ -1572,7 +1574,7 @@ __global__ __launch_bounds__(SR_NT) void micro_kernel(const ScalarRec* __restric
     gain = gain < (W)h.min_gain ? (W)h.min_gain : (gain > (W)h.max_gain ? (W)h.max_gain : gain);
 
     // ---- pass E ---- (force is recomputed before any param store of this thread)
-    const W nlr = (W)(-h.lr);
+    const W nlr = (W)update_alpha<PT>(-h.lr);
     for (int64_t i = tid; i < n; i += SR_NT) {
         const W d = drive(tangent(force(i), i), im[i]);
         const W u = to_w<W>(from_wd<PT>((double)(d * gain)));

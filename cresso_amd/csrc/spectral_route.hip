@@ -1,2950 +1,15 @@
-// Spectral / coordinate-hash route of CRESSO5 on gfx950 (large tensors).
-//
-// Math: the reference's PyTorch spectral step, cresso_v5.py:945-1353.  The
-// fused CUDA path of the reference (cresso_cuda_kernel.cu, ~46 custom + ~40
-// eager launches per tensor, fp64 basis evaluation per element) is not
-// followed; this is a from-scratch design:
-//
-// * Field view.  A tensor of shape (d0, d1, ..., dk) is viewed as rows x cols
-//   with rows = d0 and cols = d1*...*dk (rows = 1 for 1-D tensors).  Every
-//   basis mode is separable across that split (the phase is additive over
-//   axes and the window multiplicative), so each normalized carrier is
-//       C = a1(row) b1(col) - a2(row) b2(col)   (additive-phase kinds)
-//       S = a2(row) b1(col) + a1(row) b2(col)
-//   or C = a1 b1, S = a2 b2 (product kind).  The workspace holds, once per
-//   (shape, rank, max_frequency): a row table a[rows][2R], a table of the K
-//   distinct column carriers b[K][cols] (K <= 2R+1), the normalization stats
-//   in closed form (fp64 sums over the two tables), the hash bins of every
-//   element (data independent: packed bytes, computed once) and bin counts.
-// * Projection of a field x (mean(x C_r)) is a per-lane accumulation
-//   Z1_r = sum_rows a1_r x, Z2_r = sum_rows a2_r x over the lane's column,
-//   combined with the lane's b values at the end; reconstruction is
-//   out = alpha_0(row) + sum_k alpha_k(row) b_k(col) with alpha built per row
-//   panel in LDS from the mode coefficients.  On the fast path (MODE 1) sweeps
-//   3 and 4 run both as 16x16x4 fp32 MFMA tiles.
-// * Step = 5 sweeps over the field, each followed by a one-block finalize
-//   (deterministic fixed-order fp64 reductions of per-block partials) that
-//   runs the rank-level recurrences and writes the next sweep's coefficients:
-//     S1 sum f^2 -> F1 force RMS, scale
-//     S2 density: hash histograms (64-bit fixed point, integer atomics),
-//        log-density projection, axis density sums -> F2 hash metric tables,
-//        metric oscillator, recon coefficients; M1 instant-metric factors
-//     S3 tangent t (stored), t projection, port histograms, 13 moments of t
-//        -> F3 surprise, port projection (1 + tm) mean(t Xn) - G u_pred from
-//        the basis Gram matrix G, hash impulse, confidence, contact
-//        oscillator, drive coefficients (every RMS in closed form)
-//     S4 drive without the hash term (written over t); sum d^2, sum d h,
-//        sum h^2 -> F4 drive energy, gain.  Fast path: F3 already has the
-//        hash term's RMS in closed form (bin co-occurrence counts), so S4
-//        writes the full drive and sums drive^2
-//     S5 param -= lr * cast((d + c5 h) * gain), resp. cast(drive * gain)
-#include "common.hpp"
+// Spectral / coordinate-hash route of CRESSO5 on gfx950: plans, workspace set-up
+// and the C ABI.  The kernels and the step sequence are in spectral_kernels.hpp;
+// the step itself is instantiated per dtype pair in spectral_step_*.hip.
+#define CRESSO_SPECTRAL_WS_KERNELS 1
+#include "spectral_kernels.hpp"
 
-#include <algorithm>
 #include <atomic>
-#include <cmath>
-#include <cstring>
 #include <map>
 #include <mutex>
-#include <tuple>
-#include <vector>
 
 namespace cresso {
 namespace {
-
-constexpr int SP_NT = 256;
-constexpr int SP_MAXR = 16;
-constexpr int SP_MAXT = 8;
-constexpr int SP_FIN_NT = 1024;  // workspace set-up kernels
-constexpr int SP_FN_NT = 512;    // per-step finalize kernels (room for fp64 accumulators)
-// Fast-path histograms keep SP_NHIST interleaved copies ([bin][copy], copy =
-// lane & 3): lanes of one wave then collide on an address only when both the
-// bin and the copy match.  The copies are summed (integers: any order) before
-// the block's global atomics.  LDS is sized for the copies in every mode.
-constexpr int SP_NHIST = 4;
-
-enum ModeType : int32_t { M_ZERO = 0, M_ADD = 1, M_PROD = 2 };
-
-// fp32 constants of one (mode, axis) of the carrier (cast from double exactly
-// as the reference's torch expressions cast their Python scalars)
-struct AxisConst {
-    float pf;     // fl32(pi * f)
-    float pc;     // fl32(pi * c * max(1, f)) (chirp kinds)
-    float mu;     // fl32(center) (kind 3)
-    float sig;    // fl32(width)  (kind 3)
-    int32_t f;
-    int32_t pad[3];
-};
-
-struct ModeMeta {
-    int32_t type;   // ModeType
-    int32_t kind;   // r % 4 of the reference (0 additive, 1 product, 2 chirp, 3 chirp+window)
-    int32_t k1, k2; // column carriers (k2 = -1: identically zero)
-};
-
-struct CarrierSrc {  // which mode defines column carrier k and which component (0: b1, 1: b2)
-    int32_t mode, comp;
-};
-
-struct Geom {
-    int64_t n, rows, cols;
-    int32_t R, K, T, B;
-    int32_t ndim, ntrail;
-    int64_t tdim[8];  // dims of the column group, row-major
-    int32_t PR, slabs, panels, nblk;   // tiles of the field sweeps
-    int32_t nblk1;                     // blocks of the flat force-RMS sweep
-    int32_t KA;                        // alpha row width: 2*rmax+1 carriers (zero beyond K) + constant
-    int32_t RW;                        // row-table width: 2*rmax (zero beyond 2R)
-    int64_t chunk1;                    // elements per block of the flat sweep (multiple of 4)
-    double hs_row, hs_col;             // fixed-point scales of the axis density sums
-    int32_t binbytes, bpb, one_d, nblkg;   // nblkg: blocks of the Gram pair-sum kernel
-};
-
-struct Offs {
-    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins, tbuf, part, part1, sums, hist, lt,
-        imp, rowfx, colfx, colfac, terms, ctrl, total;
-};
-
-// per-step device scalars (written by finalize kernels)
-struct Ctrl {
-    float scale, inv_s;
-    float gden, kappa;
-    float rc[4][SP_MAXR][2];  // recon coefficients: 0 metric, 1 pred, 2 pred', 3 echo
-    float rconst[4];
-    float wpred[2 * SP_MAXR]; // weights of the pre-contact prediction on the normalized carriers
-    double hs_ds, hs_P;       // fixed-point scales of the histograms
-    float nscale, srms;
-    // drive = k_rat rat + k_ths tanh(t/clip) + k_root root + k_t t + k_pred pred' + k_echo echo
-    //         + k_nov tanh(err' nscale) + k_hash hash_pred
-    float k_rat, k_ths, k_root, k_t, k_pred, k_echo, k_nov, k_hash, gain;
-    float de_prev;            // drive_energy before this step (sweep 5 updates the state)
-    float fr_prev;            // force_rms before this step (sweep 2 updates the state)
-};
-
-// state pointers of one tensor (kernel argument)
-struct SpecState {
-    float *force_rms, *drive_energy, *surprise, *action;
-    const float* omega;
-    float *q_cos, *q_sin, *p_cos, *p_sin, *metric_cos, *metric_sin, *metric_p_cos, *metric_p_sin;
-    float *calcium_cos, *calcium_sin, *conf;
-    float *hash_energy, *hash_impulse, *hash_refractory;
-};
-
-constexpr int NV2 = 2 + 2 * SP_MAXR;            // sum L, sum dens, proj L (C,S)
-constexpr int NV3 = 15 + 2 * SP_MAXR;           // see sweep3
-constexpr int NV4 = 3;                          // sum d^2, sum d hp, sum hp^2
-constexpr int NVMAX = NV3;
-
-// ---------------------------------------------------------------------------
-// workspace construction
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float axis_u(int64_t k, int64_t dim) { return ((float)k + 0.5f) / (float)dim; }
-
-// per-axis phase of mode r on one axis (fp32 like cresso_v5.py:272-292)
-__device__ __forceinline__ float axis_phase(const AxisConst& a, float u, bool chirp) {
-    float ph = a.pf * u;
-    if (chirp) {
-        const float d = u - 0.5f;
-        ph = ph + a.pc * (d * d);
-    }
-    return ph;
-}
-__device__ __forceinline__ float axis_window(const AxisConst& a, float u) {
-    const float z = (u - a.mu) / a.sig;
-    return expf(-0.5f * (z * z));
-}
-
-// carriers of mode r over a set of axes given the element coordinates on them
-__device__ void group_carrier(const AxisConst* ax, int kind, int naxes, const int64_t* coord, const int64_t* dims,
-                              float& c1, float& c2) {
-    if (kind == 1) {
-        float cp = 1.f, sp = 1.f;
-        for (int a = 0; a < naxes; ++a) {
-            if (ax[a].f == 0) continue;
-            const float ph = ax[a].pf * axis_u(coord[a], dims[a]);
-            cp = cp * cosf(ph);
-            sp = sp * sinf(ph);
-        }
-        c1 = cp;
-        c2 = sp;
-        return;
-    }
-    const bool chirp = kind != 0;
-    float ph = 0.f, w = 1.f;
-    bool any = false;
-    for (int a = 0; a < naxes; ++a) {
-        if (ax[a].f == 0 && !chirp) continue;
-        const float u = axis_u(coord[a], dims[a]);
-        const float p = axis_phase(ax[a], u, chirp);
-        ph = any ? ph + p : p;
-        any = true;
-        if (kind == 3) w = (a == 0) ? axis_window(ax[a], u) : w * axis_window(ax[a], u);
-    }
-    c1 = w * cosf(ph);
-    c2 = w * sinf(ph);
-}
-
-__global__ void ws_rowtab_kernel(Geom g, const AxisConst* __restrict__ axc, const ModeMeta* __restrict__ meta,
-                                 float* __restrict__ rowtab) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= g.rows) return;
-    for (int r = 0; r < g.R; ++r) {
-        float a1 = 1.f, a2 = 0.f;
-        const int kind = meta[r].kind;
-        if (meta[r].type == M_ZERO) {
-            a1 = 1.f;
-            a2 = 0.f;
-        } else if (g.one_d) {
-            // empty leading group: phase 0, window 1 (kinds 0/2/3) or empty products (kind 1)
-            a1 = 1.f;
-            a2 = kind == 1 ? 1.f : 0.f;
-        } else {
-            const int64_t coord = i;
-            const int64_t dim = g.rows;
-            group_carrier(axc + (size_t)r * g.ndim, kind, 1, &coord, &dim, a1, a2);
-        }
-        rowtab[i * g.RW + 2 * r] = a1;
-        rowtab[i * g.RW + 2 * r + 1] = a2;
-    }
-    for (int j = 2 * g.R; j < g.RW; ++j) rowtab[i * g.RW + j] = 0.f;
-}
-
-__global__ void ws_coltab_kernel(Geom g, const AxisConst* __restrict__ axc, const ModeMeta* __restrict__ meta,
-                                 const CarrierSrc* __restrict__ csrc, float* __restrict__ coltab) {
-    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= g.cols) return;
-    int64_t coord[8];
-    int64_t rem = c;
-    for (int a = g.ntrail - 1; a >= 0; --a) {
-        coord[a] = rem % g.tdim[a];
-        rem /= g.tdim[a];
-    }
-    const int first_axis = g.one_d ? 0 : 1;
-    for (int k = 0; k < g.K; ++k) {
-        float v = 1.f;
-        if (csrc[k].mode >= 0) {
-            const int r = csrc[k].mode;
-            float b1, b2;
-            group_carrier(axc + (size_t)r * g.ndim + first_axis, meta[r].kind, g.ntrail, coord, g.tdim, b1, b2);
-            v = csrc[k].comp == 0 ? b1 : b2;
-        }
-        coltab[(size_t)k * g.cols + c] = v;
-    }
-    for (int k = g.K; k < g.KA - 1; ++k) coltab[(size_t)k * g.cols + c] = 0.f;
-}
-
-// block-wide max of two non-negative values; every thread receives them
-__device__ void block_max2(double (&v)[2], double* lds) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int i = 0; i < 2; ++i)
-        for (int m = 32; m >= 1; m >>= 1) v[i] = fmax(v[i], __shfl_xor(v[i], m, 64));
-    if (lane == 0) {
-        lds[2 * wave] = v[0];
-        lds[2 * wave + 1] = v[1];
-    }
-    __syncthreads();
-    double a = 0.0, b = 0.0;
-    for (int w = 0; w < nw; ++w) {
-        a = fmax(a, lds[2 * w]);
-        b = fmax(b, lds[2 * w + 1]);
-    }
-    v[0] = a;
-    v[1] = b;
-    __syncthreads();
-}
-
-// Closed-form normalization stats (cresso_v5.py:138-142 over the separable
-// carriers): per mode (mu_c, 1/max(sqrt(var_c+1e-12),1e-6), mu_s, ...) and a
-// bound of max|C_n|, max|S_n| used to size fixed-point histograms.
-__global__ __launch_bounds__(SP_FIN_NT) void ws_stats_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                             const float* __restrict__ rowtab,
-                                                             const float* __restrict__ coltab, double* __restrict__ stats,
-                                                             double* __restrict__ bounds) {
-    __shared__ double red[16 * 8];
-    const int tid = threadIdx.x;
-    for (int r = 0; r < g.R; ++r) {
-        // row sums of this mode
-        double v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (int64_t i = tid; i < g.rows; i += SP_FIN_NT) {
-            const double a1 = rowtab[i * g.RW + 2 * r], a2 = rowtab[i * g.RW + 2 * r + 1];
-            v[0] += a1; v[1] += a2; v[2] += a1 * a1; v[3] += a1 * a2; v[4] += a2 * a2;
-            v[5] = fmax(v[5], fabs(a1)); v[6] = fmax(v[6], fabs(a2));
-        }
-        double mx[2] = {v[5], v[6]};
-        v[5] = v[6] = 0.0;
-        block_sum<8>(v, red);
-        block_max2(mx, red);
-        const double Sa1 = v[0], Sa2 = v[1], Sa11 = v[2], Sa12 = v[3], Sa22 = v[4];
-        const double ma1 = mx[0], ma2 = mx[1];
-        const int k1 = meta[r].k1, k2 = meta[r].k2;
-        double u[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        double bm1 = 0.0, bm2 = 0.0;
-        for (int64_t c = tid; c < g.cols; c += SP_FIN_NT) {
-            const double b1 = coltab[(size_t)k1 * g.cols + c];
-            const double b2 = k2 >= 0 ? (double)coltab[(size_t)k2 * g.cols + c] : 0.0;
-            u[0] += b1; u[1] += b2; u[2] += b1 * b1; u[3] += b1 * b2; u[4] += b2 * b2;
-            bm1 = fmax(bm1, fabs(b1)); bm2 = fmax(bm2, fabs(b2));
-        }
-        block_sum<8>(u, red);
-        double bm[2] = {bm1, bm2};
-        block_max2(bm, red);
-        if (tid == 0) {
-            const double Sb1 = u[0], Sb2 = u[1], Sb11 = u[2], Sb12 = u[3], Sb22 = u[4];
-            const double mb1 = bm[0], mb2 = bm[1];
-            const double n = (double)g.n;
-            double sc, scc, ss, sss, mc, ms;
-            if (meta[r].type == M_ZERO) {
-                stats[4 * r + 0] = 0.0; stats[4 * r + 1] = 1.0;  // C = 1, unnormalized
-                stats[4 * r + 2] = 0.0; stats[4 * r + 3] = 0.0;  // S = 0
-                bounds[2 * r] = 1.0; bounds[2 * r + 1] = 0.0;
-            } else {
-                if (meta[r].type == M_ADD) {
-                    sc = Sa1 * Sb1 - Sa2 * Sb2;
-                    scc = Sa11 * Sb11 - 2.0 * Sa12 * Sb12 + Sa22 * Sb22;
-                    ss = Sa2 * Sb1 + Sa1 * Sb2;
-                    sss = Sa22 * Sb11 + 2.0 * Sa12 * Sb12 + Sa11 * Sb22;
-                    mc = ma1 * mb1 + ma2 * mb2;
-                    ms = ma2 * mb1 + ma1 * mb2;
-                } else {
-                    sc = Sa1 * Sb1; scc = Sa11 * Sb11; ss = Sa2 * Sb2; sss = Sa22 * Sb22;
-                    mc = ma1 * mb1; ms = ma2 * mb2;
-                }
-                const double muc = sc / n, mus = ss / n;
-                const double vc = fmax(scc / n - muc * muc, 0.0), vs = fmax(sss / n - mus * mus, 0.0);
-                const double ic = 1.0 / fmax(sqrt(vc + 1e-12), 1e-6), is = 1.0 / fmax(sqrt(vs + 1e-12), 1e-6);
-                stats[4 * r + 0] = muc; stats[4 * r + 1] = ic; stats[4 * r + 2] = mus; stats[4 * r + 3] = is;
-                bounds[2 * r] = (mc + fabs(muc)) * ic;
-                bounds[2 * r + 1] = (ms + fabs(mus)) * is;
-            }
-        }
-        __syncthreads();
-    }
-}
-
-// Gram matrix of the normalized basis, G[v][w] = mean over elements of
-// Xn_v Xn_w (v = 2r: C_r, v = 2r + 1: S_r), in closed form from the separable
-// tables: each raw carrier is a sum of at most two (row factor x column
-// carrier) terms, so sum_i X_v X_w is a combination of the row pair sums
-// sum_rows a_x a_y (x, y < 2R) and the column pair sums sum_cols b_k b_l
-// (k, l < K).  Pair sums are split over nblkg blocks (fixed-order partials).
-__global__ __launch_bounds__(256) void ws_pairsum_kernel(Geom g, const float* __restrict__ rowtab,
-                                                         const float* __restrict__ coltab, double* __restrict__ gpart) {
-    const int V = 2 * g.R, NA = V * V, NB = g.K * g.K;
-    const int nb = g.nblkg;
-    const int64_t r0 = g.rows * blockIdx.x / nb, r1 = g.rows * (blockIdx.x + 1) / nb;
-    const int64_t c0 = g.cols * blockIdx.x / nb, c1 = g.cols * (blockIdx.x + 1) / nb;
-    for (int p = threadIdx.x; p < NA + NB; p += blockDim.x) {
-        double s = 0.0;
-        if (p < NA) {
-            const int x = p / V, y = p - x * V;
-            for (int64_t i = r0; i < r1; ++i) s += (double)rowtab[i * g.RW + x] * (double)rowtab[i * g.RW + y];
-        } else {
-            const int q = p - NA, k = q / g.K, l = q - k * g.K;
-            for (int64_t c = c0; c < c1; ++c)
-                s += (double)coltab[(size_t)k * g.cols + c] * (double)coltab[(size_t)l * g.cols + c];
-        }
-        gpart[(size_t)blockIdx.x * (NA + NB) + p] = s;
-    }
-}
-
-// terms (sign, row factor x, column carrier k) of raw carrier v; returns the count
-__device__ int carrier_terms(const ModeMeta& m, int v, float* sg, int* x, int* k) {
-    const int r = v >> 1, c = v & 1;
-    int n = 0;
-    auto add = [&](float s_, int x_, int k_) {
-        if (k_ >= 0) { sg[n] = s_; x[n] = x_; k[n] = k_; ++n; }
-    };
-    if (m.type == M_ZERO) {
-        if (c == 0) add(1.f, 2 * r, m.k1);
-    } else if (m.type == M_ADD) {
-        if (c == 0) { add(1.f, 2 * r, m.k1); add(-1.f, 2 * r + 1, m.k2); }
-        else { add(1.f, 2 * r + 1, m.k1); add(1.f, 2 * r, m.k2); }
-    } else {
-        if (c == 0) add(1.f, 2 * r, m.k1);
-        else add(1.f, 2 * r + 1, m.k2);
-    }
-    return n;
-}
-
-__global__ __launch_bounds__(SP_FIN_NT) void ws_gram_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                            const double* __restrict__ stats,
-                                                            const double* __restrict__ gpart, double* __restrict__ gram) {
-    const int V = 2 * g.R, NA = V * V, NB = g.K * g.K;
-    extern __shared__ double s_pair[];   // [NA + NB]
-    for (int p = threadIdx.x; p < NA + NB; p += SP_FIN_NT) {
-        double s = 0.0;
-        for (int b = 0; b < g.nblkg; ++b) s += gpart[(size_t)b * (NA + NB) + p];
-        s_pair[p] = s;
-    }
-    __syncthreads();
-    const double n = (double)g.n;
-    for (int p = threadIdx.x; p < V * V; p += SP_FIN_NT) {
-        const int v = p / V, w = p - v * V;
-        float sv[2], sw[2];
-        int xv[2], xw[2], kv[2], kw[2];
-        const int nv = carrier_terms(meta[v >> 1], v, sv, xv, kv);
-        const int nw = carrier_terms(meta[w >> 1], w, sw, xw, kw);
-        double sum = 0.0;
-        for (int i = 0; i < nv; ++i)
-            for (int j = 0; j < nw; ++j)
-                sum += (double)(sv[i] * sw[j]) * s_pair[xv[i] * V + xw[j]] * s_pair[NA + kv[i] * g.K + kw[j]];
-        // Xn = (X - mu) ic with mu the normalization shift and m the true mean
-        // of X (equal, except the constant carrier: mu = 0, m = 1):
-        // mean(Xn_v Xn_w) = ic_v ic_w (mean(X_v X_w) - mu_v m_w - mu_w m_v + mu_v mu_w)
-        const double muv = stats[4 * (v >> 1) + 2 * (v & 1)], icv = stats[4 * (v >> 1) + 2 * (v & 1) + 1];
-        const double muw = stats[4 * (w >> 1) + 2 * (w & 1)], icw = stats[4 * (w >> 1) + 2 * (w & 1) + 1];
-        const double mv = (meta[v >> 1].type == M_ZERO && (v & 1) == 0) ? 1.0 : muv;
-        const double mw = (meta[w >> 1].type == M_ZERO && (w & 1) == 0) ? 1.0 : muw;
-        gram[p] = icv * icw * (sum / n - muv * mw - muw * mv + muv * muw);
-    }
-}
-
-// Packed bins of every element (data independent; computed once per shape)
-// and exact bin counts: per-block u32 counts in LDS when the [T][B] table
-// fits (integer adds, so the totals do not depend on arrival order), merged
-// into the u64 totals with one global atomic per non-empty bin.
-constexpr int WS_BINS_LDS = 8192;  // u32 counters privatised per block
-__global__ __launch_bounds__(256) void ws_bins_kernel(Geom g, unsigned char* __restrict__ bins,
-                                                      unsigned long long* __restrict__ counts) {
-    __shared__ unsigned int s_cnt[WS_BINS_LDS];
-    const int TB = g.T * g.B;
-    const bool priv = TB <= WS_BINS_LDS;
-    if (priv)
-        for (int i = threadIdx.x; i < TB; i += blockDim.x) s_cnt[i] = 0u;
-    __syncthreads();
-    const int64_t mask = (g.B & (g.B - 1)) == 0 ? (int64_t)g.B - 1 : -1;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
-        uint64_t packed = 0;
-        for (int t = 0; t < g.T; ++t) {
-            const HashSalt s = hash_salt(t);
-            const int b = hash_bin((uint64_t)i, s, g.B, mask);
-            packed |= (uint64_t)b << (8 * g.bpb * t);
-            if (priv)
-                atomicAdd(&s_cnt[t * g.B + b], 1u);
-            else
-                atomicAdd(&counts[(size_t)t * g.B + b], 1ull);
-        }
-        switch (g.binbytes) {
-            case 1: bins[i] = (unsigned char)packed; break;
-            case 2: reinterpret_cast<uint16_t*>(bins)[i] = (uint16_t)packed; break;
-            case 4: reinterpret_cast<uint32_t*>(bins)[i] = (uint32_t)packed; break;
-            default: reinterpret_cast<uint64_t*>(bins)[i] = packed; break;
-        }
-    }
-    __syncthreads();
-    if (priv)
-        for (int i = threadIdx.x; i < TB; i += blockDim.x)
-            if (s_cnt[i]) atomicAdd(&counts[i], (unsigned long long)s_cnt[i]);
-}
-
-// Co-occurrence counts of the two tables' bins, cooc[b0][b1] = #{i : bin0(i) =
-// b0, bin1(i) = b1} (data independent, once per shape).  With them the hash
-// prediction's sum of squares is a closed form over the impulse tables:
-//   sum_i ((imp0[b0] + imp1[b1]) / 2)^2
-//     = (sum_b cnt0 imp0^2 + sum_b cnt1 imp1^2 + 2 sum_{b0,b1} cooc imp0 imp1) / 4.
-// Used when there are two tables of one-byte bins (the sweeps' fast path).
-__host__ __device__ inline bool cooc_closed(const Geom& g) { return g.T == 2 && g.bpb == 1 && g.binbytes == 2; }
-constexpr int WS_COOC_LDS = 16384;  // u32 counters privatised per block (B <= 128)
-__global__ __launch_bounds__(256) void ws_cooc_kernel(Geom g, const uint16_t* __restrict__ bins,
-                                                      unsigned long long* __restrict__ cooc) {
-    __shared__ unsigned int s_cnt[WS_COOC_LDS];
-    const int BB = g.B * g.B;
-    const bool priv = BB <= WS_COOC_LDS;
-    if (priv)
-        for (int i = threadIdx.x; i < BB; i += blockDim.x) s_cnt[i] = 0u;
-    __syncthreads();
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
-        const unsigned v = bins[i];
-        const int k = (int)(v & 0xffu) * g.B + (int)(v >> 8);
-        if (priv)
-            atomicAdd(&s_cnt[k], 1u);
-        else
-            atomicAdd(&cooc[k], 1ull);
-    }
-    __syncthreads();
-    if (priv)
-        for (int i = threadIdx.x; i < BB; i += blockDim.x)
-            if (s_cnt[i]) atomicAdd(&cooc[i], (unsigned long long)s_cnt[i]);
-}
-
-__device__ __forceinline__ uint64_t load_bins(const unsigned char* __restrict__ bins, int64_t e, int binbytes) {
-    switch (binbytes) {
-        case 1: return bins[e];
-        case 2: return reinterpret_cast<const uint16_t*>(bins)[e];
-        case 4: return reinterpret_cast<const uint32_t*>(bins)[e];
-        default: return reinterpret_cast<const uint64_t*>(bins)[e];
-    }
-}
-__device__ __forceinline__ int bin_of(uint64_t packed, int t, int bpb) {
-    return (int)((packed >> (8 * bpb * t)) & (bpb == 1 ? 0xffull : 0xffffull));
-}
-
-// ---------------------------------------------------------------------------
-// workspace inspection (parity checks of what the sweeps consume)
-// ---------------------------------------------------------------------------
-// Bin of every element for every table, int32 [T][n].
-__global__ void ws_unpack_bins_kernel(Geom g, const unsigned char* __restrict__ bins, int32_t* __restrict__ out) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
-        const uint64_t pk = load_bins(bins, i, g.binbytes);
-        for (int t = 0; t < g.T; ++t) out[(size_t)t * g.n + i] = bin_of(pk, t, g.bpb);
-    }
-}
-
-// Normalized carriers C_r, S_r of mode r at every element, formed from the
-// row table, the column table and the closed-form stats exactly as the
-// sweeps' reconstruction coefficients combine them.
-__global__ void ws_basis_kernel(Geom g, const ModeMeta* __restrict__ meta, const float* __restrict__ rowtab,
-                                const float* __restrict__ coltab, const double* __restrict__ stats, int r,
-                                float* __restrict__ cout, float* __restrict__ sout) {
-    const ModeMeta m = meta[r];
-    const double muc = stats[4 * r], ic = stats[4 * r + 1], mus = stats[4 * r + 2], is = stats[4 * r + 3];
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
-        const int64_t row = i / g.cols, col = i - row * g.cols;
-        const float a1 = rowtab[row * g.RW + 2 * r], a2 = rowtab[row * g.RW + 2 * r + 1];
-        const float b1 = coltab[(size_t)m.k1 * g.cols + col];
-        const float b2 = m.k2 >= 0 ? coltab[(size_t)m.k2 * g.cols + col] : 0.f;
-        const float craw = m.type == M_ADD ? a1 * b1 - a2 * b2 : a1 * b1;
-        const float sraw = m.type == M_ADD ? a2 * b1 + a1 * b2 : a2 * b2;
-        cout[i] = (float)(((double)craw - muc) * ic);
-        sout[i] = (float)(((double)sraw - mus) * is);
-    }
-}
-
-// Unit entry points of the basis algebra (cresso_v5.py:351-376) on the
-// workspace's separable tables, for parity checks and callers that want the
-// reference's project/reconstruct: the normalized carriers of
-// ws_basis_kernel, evaluated per element.
-__device__ __forceinline__ void carrier_pair_n(const Geom& g, const ModeMeta& m, const float* __restrict__ rowtab,
-                                               const float* __restrict__ coltab, const double* __restrict__ stats,
-                                               int r, int64_t row, int64_t col, float& cn, float& sn) {
-    const float a1 = rowtab[row * g.RW + 2 * r], a2 = rowtab[row * g.RW + 2 * r + 1];
-    const float b1 = coltab[(size_t)m.k1 * g.cols + col];
-    const float b2 = m.k2 >= 0 ? coltab[(size_t)m.k2 * g.cols + col] : 0.f;
-    const float craw = m.type == M_ADD ? a1 * b1 - a2 * b2 : a1 * b1;
-    const float sraw = m.type == M_ADD ? a2 * b1 + a1 * b2 : a2 * b2;
-    cn = (float)(((double)craw - stats[4 * r]) * stats[4 * r + 1]);
-    sn = (float)(((double)sraw - stats[4 * r + 2]) * stats[4 * r + 3]);
-}
-
-// sum_i x_i C_r(i), sum_i x_i S_r(i) (fp32 products, fp64 sums), value-major
-// block partials part[2r + c][block]
-__global__ __launch_bounds__(256) void ws_project_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                         const float* __restrict__ rowtab,
-                                                         const float* __restrict__ coltab,
-                                                         const double* __restrict__ stats, const float* __restrict__ x,
-                                                         double* __restrict__ part) {
-    __shared__ double lds[4 * 2 * SP_MAXR];
-    double acc[2 * SP_MAXR];
-#pragma unroll
-    for (int v = 0; v < 2 * SP_MAXR; ++v) acc[v] = 0.0;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
-        const int64_t row = i / g.cols, col = i - row * g.cols;
-        const float xv = x[i];
-#pragma unroll
-        for (int r = 0; r < SP_MAXR; ++r) {
-            if (r < g.R) {
-                float cn, sn;
-                carrier_pair_n(g, meta[r], rowtab, coltab, stats, r, row, col, cn, sn);
-                acc[2 * r] += (double)(xv * cn);
-                acc[2 * r + 1] += (double)(xv * sn);
-            }
-        }
-    }
-    block_sum<2 * SP_MAXR>(acc, lds);
-    for (int v = threadIdx.x; v < 2 * g.R; v += blockDim.x) part[(size_t)v * gridDim.x + blockIdx.x] = acc[v];
-}
-
-__global__ void ws_mean_kernel(const double* __restrict__ sums, int V, double inv_n, double* __restrict__ out) {
-    const int v = threadIdx.x;
-    if (v < V) out[v] = sums[v] * inv_n;
-}
-
-// shrink * sum_r g_r (cc_r C_r + sc_r S_r) in mode order, a gate of exactly 0
-// skipping the mode (fp32 accumulation like the reference's add_(alpha))
-__global__ __launch_bounds__(256) void ws_reconstruct_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                             const float* __restrict__ rowtab,
-                                                             const float* __restrict__ coltab,
-                                                             const double* __restrict__ stats,
-                                                             const float* __restrict__ cc, const float* __restrict__ sc,
-                                                             const float* __restrict__ gates, double shrink,
-                                                             float* __restrict__ out) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
-        const int64_t row = i / g.cols, col = i - row * g.cols;
-        float o = 0.f;
-        for (int r = 0; r < g.R; ++r) {
-            const double gr = gates ? (double)gates[r] : 1.0;
-            if (gr == 0.0) continue;
-            float cn, sn;
-            carrier_pair_n(g, meta[r], rowtab, coltab, stats, r, row, col, cn, sn);
-            o = o + (float)((double)cc[r] * shrink * gr) * cn;
-            o = o + (float)((double)sc[r] * shrink * gr) * sn;
-        }
-        out[i] = o;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// sweep helpers
-// ---------------------------------------------------------------------------
-template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f(p[i]); }
-
-// 4 consecutive elements at e (e multiple of 4, base aligned to 4 elements)
-template <typename T> struct Ld4;
-template <> struct Ld4<float> {
-    __device__ static void go(const float* p, int64_t e, float* o) {
-        const float4 v = *reinterpret_cast<const float4*>(p + e);
-        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
-    }
-};
-template <typename T> struct Ld4h {
-    __device__ static void go(const T* p, int64_t e, float* o) {
-        const uint2 raw = *reinterpret_cast<const uint2*>(p + e);
-        const T* h = reinterpret_cast<const T*>(&raw);
-        o[0] = to_f(h[0]); o[1] = to_f(h[1]); o[2] = to_f(h[2]); o[3] = to_f(h[3]);
-    }
-};
-template <> struct Ld4<__half> : Ld4h<__half> {};
-template <> struct Ld4<__hip_bfloat16> : Ld4h<__hip_bfloat16> {};
-
-// 4 consecutive elements stored at e, rounded to the storage dtype
-template <typename T> struct St4;
-template <> struct St4<float> {
-    __device__ static void go(float* p, int64_t e, const float* v) {
-        *reinterpret_cast<float4*>(p + e) = make_float4(v[0], v[1], v[2], v[3]);
-    }
-};
-template <typename T> struct St4h {
-    __device__ static void go(T* p, int64_t e, const float* v) {
-        uint2 raw;
-        T* q = reinterpret_cast<T*>(&raw);
-        q[0] = from_w<T>(v[0]); q[1] = from_w<T>(v[1]); q[2] = from_w<T>(v[2]); q[3] = from_w<T>(v[3]);
-        *reinterpret_cast<uint2*>(p + e) = raw;
-    }
-};
-template <> struct St4<__half> : St4h<__half> {};
-template <> struct St4<__hip_bfloat16> : St4h<__hip_bfloat16> {};
-
-struct Tile {
-    int slab, panel;
-    int64_t col, r0, r1;
-    bool colok;
-};
-__device__ __forceinline__ Tile tile_of(const Geom& g) {
-    Tile t;
-    t.slab = blockIdx.x % g.slabs;
-    t.panel = blockIdx.x / g.slabs;
-    t.col = (int64_t)t.slab * SP_NT + threadIdx.x;
-    t.colok = t.col < g.cols;
-    t.r0 = (int64_t)t.panel * g.PR;
-    t.r1 = t.r0 + g.PR < g.rows ? t.r0 + g.PR : g.rows;
-    return t;
-}
-
-// Wave sum of a float in a fixed lane order with DPP (quad xor 1, 2; row
-// rotate 4, 8; row broadcasts 15, 31): the total lands in lane 63.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_add(float v) {
-    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
-                                                                        0xF, false));
-}
-__device__ __forceinline__ float wave_total(float v) {
-    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-    v = dpp_add<0x124, 0xF>(v);  // row_ror:4
-    v = dpp_add<0x128, 0xF>(v);  // row_ror:8
-    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
-    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
-    return v;                    // lane 63 holds the sum
-}
-
-// Block partials, one value at a time: DPP wave totals into LDS [wave][V],
-// then a fixed-order sum over the block's waves, written value-major
-// part[v][block] (consumers read each value's blocks contiguously).
-struct Partials {
-    float* lds;
-    int V;
-    int VS;   // values written (the consumer's fixed width; slots V..VS-1 zero)
-    __device__ __forceinline__ void add(int idx, float x) {
-        const float w = wave_total(x);
-        if ((threadIdx.x & 63) == 63) lds[(threadIdx.x >> 6) * V + idx] = w;
-    }
-    // value-major: part[v][gridDim.x], slots V..VS-1 zero
-    __device__ __forceinline__ void flush(double* part) {
-        __syncthreads();
-        for (int v = threadIdx.x; v < VS; v += SP_NT) {
-            double s = 0.0;
-            if (v < V)
-                for (int w = 0; w < SP_NT / 64; ++w) s += (double)lds[w * V + v];
-            part[(size_t)v * gridDim.x + blockIdx.x] = s;
-        }
-    }
-};
-
-// Non-negative float (already scaled by a power of two, < 2^62) to a 64-bit
-// fixed-point integer, truncating: two exact 32-bit conversions.
-__device__ __forceinline__ unsigned long long to_fixed_u(float x) {
-    const float hf = floorf(x * 2.3283064365386963e-10f);  // x / 2^32 (exact scaling)
-    const float lf = fmaf(-hf, 4294967296.0f, x);           // x - hi*2^32: exact, in [0, 2^32)
-    return ((unsigned long long)(unsigned)hf << 32) | (unsigned long long)(unsigned)lf;
-}
-__device__ __forceinline__ unsigned long long to_fixed_s(float x) {
-    const unsigned long long u = to_fixed_u(fabsf(x));
-    return x < 0.f ? (0ull - u) : u;
-}
-
-// Any float x with |x| < 2^62 (already scaled by a power of two) to the
-// 64-bit two's complement integer floor(x): exact in double, the high word is
-// floor(x / 2^32) and the low word the remainder in [0, 2^32).
-__device__ __forceinline__ unsigned long long to_fixed_floor(float x) {
-    const double d = (double)x;
-    const double hi = floor(d * 2.3283064365386963e-10);
-    const double lo = fmin(fma(-hi, 4294967296.0, d), 4294967295.0);
-    return ((unsigned long long)(unsigned)(int)hi << 32) | (unsigned long long)(unsigned)lo;
-}
-
-__device__ __forceinline__ float reservoir_f(float old, float cur, double decay, int step) {
-    if (step <= 1) return cur;
-    return old * (float)decay + (float)(1.0 - decay) * cur;
-}
-
-// All partial values of a sweep (value-major part[v][nblk]) reduced in a
-// fixed order into out[v] (LDS), visible after return: thread j accumulates
-// blocks j, j + NT, ... of every value in fp64 (coalesced loads, all in
-// flight), each wave reduces every value with DPP in fixed lane order, and the
-// wave totals are added in wave order.
-template <int VMAX>
-__device__ void reduce_bm(const double* __restrict__ part, int nblk, int V, double* out) {
-    __shared__ double s_w[SP_FN_NT / 64][VMAX];
-    double acc[VMAX];
-#pragma unroll
-    for (int v = 0; v < VMAX; ++v) acc[v] = 0.0;
-    for (int b = threadIdx.x; b < nblk; b += SP_FN_NT) {
-#pragma unroll
-        for (int v = 0; v < VMAX; ++v)
-            if (v < V) acc[v] += part[(size_t)v * nblk + b];
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int v = 0; v < VMAX; ++v) {
-        if (v < V) {
-            const double w = wave_total_d(acc[v]);
-            if (lane == 63) s_w[wave][v] = w;
-        }
-    }
-    __syncthreads();
-    for (int v = threadIdx.x; v < V; v += SP_FN_NT) {
-        double s = 0.0;
-        for (int w = 0; w < SP_FN_NT / 64; ++w) s += s_w[w][v];
-        out[v] = s;
-    }
-    __syncthreads();
-}
-
-// Cross-block merge of a sweep's partials spread over many CUs: block v sums
-// value v of every block (thread j: blocks j, j + 256, ... in order; then a
-// fixed-order DPP wave tree and the four wave totals in order) into sums[v].
-__global__ __launch_bounds__(256) void part_reduce_kernel(const double* __restrict__ part, int nblk, int VS,
-                                                          double* __restrict__ sums) {
-    __shared__ double s_w[4];
-    const int v = blockIdx.x;
-    (void)VS;
-    double a = 0.0;
-    for (int b = threadIdx.x; b < nblk; b += 256) a += part[(size_t)v * nblk + b];
-    a = wave_total_d(a);
-    if ((threadIdx.x & 63) == 63) s_w[threadIdx.x >> 6] = a;
-    __syncthreads();
-    if (threadIdx.x == 0) sums[v] = ((s_w[0] + s_w[1]) + s_w[2]) + s_w[3];
-}
-
-// The merged sums of a sweep into LDS (all loads in flight).
-__device__ void load_sums(const double* __restrict__ sums, int V, double* out) {
-    for (int v = threadIdx.x; v < V; v += blockDim.x) out[v] = sums[v];
-    __syncthreads();
-}
-
-// ---------------------------------------------------------------------------
-// S1: sum f^2 over contiguous chunks (float4 loads when aligned)
-// ---------------------------------------------------------------------------
-// Each block also clears its slice of the axis density sums (rows, then
-// columns) for this step's sweep 2.
-template <typename PT, typename GT, bool V4>
-__global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
-                                                       double* __restrict__ part, unsigned long long* __restrict__ rowfx,
-                                                       unsigned long long* __restrict__ colfx, Ctrl* __restrict__ ctrl,
-                                                       const float* __restrict__ fr_state, cresso_hyper h) {
-    __shared__ float red[4];
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        ctrl->fr_prev = *fr_state;   // every block of sweep 2 reads the old value
-        // density histogram scale: ds = rel^p <= (1e4)^p, at most n elements per bin
-        const double dsmax = pow(1.0e4, h.energy_power) + 1.0;
-        ctrl->hs_ds = ldexp(1.0, (int)floor(62.0 - log2(dsmax * (double)g.n)));
-    }
-    {
-        const int64_t na = g.rows + g.cols, per = (na + g.nblk1 - 1) / g.nblk1;
-        const int64_t a0 = (int64_t)blockIdx.x * per, a1 = a0 + per < na ? a0 + per : na;
-        for (int64_t i = a0 + threadIdx.x; i < a1; i += SP_NT) {
-            if (i < g.rows)
-                rowfx[i] = 0ull;
-            else
-                colfx[i - g.rows] = 0ull;
-        }
-    }
-    const float wd = (float)h.weight_decay;
-    const bool wd_on = h.weight_decay != 0.0;
-    const int64_t beg = (int64_t)blockIdx.x * g.chunk1;
-    const int64_t end = beg + g.chunk1 < g.n ? beg + g.chunk1 : g.n;
-    const float sg = h.maximize ? -1.f : 1.f;
-    float a = 0.f;
-    const int64_t vend = beg + ((end - beg) & ~(int64_t)3);
-    if (V4) {
-        // eight float4 loads per thread in flight per iteration, then the rest one by one
-        constexpr int UN = 8;
-        const int64_t st = 4 * (int64_t)SP_NT;
-        int64_t e = beg + 4 * (int64_t)threadIdx.x;
-        for (; e + (UN - 1) * st < vend; e += UN * st) {
-            float f[UN][4];
-#pragma unroll
-            for (int u = 0; u < UN; ++u) Ld4<GT>::go(grad, e + u * st, f[u]);
-            if (wd_on) {
-                float pv[UN][4];
-#pragma unroll
-                for (int u = 0; u < UN; ++u) Ld4<PT>::go(param, e + u * st, pv[u]);
-#pragma unroll
-                for (int u = 0; u < UN; ++u)
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) f[u][c] = sg * f[u][c] + wd * pv[u][c];
-            }
-#pragma unroll
-            for (int u = 0; u < UN; ++u)
-#pragma unroll
-                for (int c = 0; c < 4; ++c) a += f[u][c] * f[u][c];
-        }
-        for (; e < vend; e += st) {
-            float f[4];
-            Ld4<GT>::go(grad, e, f);
-            if (wd_on) {
-                float pv[4];
-                Ld4<PT>::go(param, e, pv);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) f[c] = sg * f[c] + wd * pv[c];
-            }
-#pragma unroll
-            for (int c = 0; c < 4; ++c) a += f[c] * f[c];
-        }
-    }
-    // scalar elements: the < 4 tail of a vectorized chunk, or the whole chunk
-    for (int64_t i = (V4 ? vend : beg) + threadIdx.x; i < end; i += SP_NT) {
-        float f = sg * ld(grad, i);
-        if (wd_on) f = f + wd * ld(param, i);
-        a += f * f;
-    }
-    Partials P{red, 1, 1};
-    P.add(0, a);
-    P.flush(part);
-}
-
-// F1, in every block of sweep 2: sweep 1's block partials summed in a fixed
-// order (so every block gets the same values), then the force-RMS reservoir
-// and the scale.  Block 0 stores the new force RMS and the values later
-// kernels read from ctrl; the reservoir starts from ctrl->fr_prev (stashed by
-// sweep 1, with the histogram scale hs_ds), so no block reads a value another
-// block of this launch writes.
-struct F1Values {
-    float inv_s;
-    double hs_ds;
-};
-__device__ F1Values fin1_values(const Geom& g, const double* __restrict__ part1, Ctrl* __restrict__ ctrl,
-                                float* __restrict__ fr_state, int step, const cresso_hyper& h) {
-    __shared__ double s_w[SP_NT / 64];
-    double a = 0.0;
-    for (int b = threadIdx.x; b < g.nblk1; b += SP_NT) a += part1[b];
-    const double w = wave_total_d(a);
-    if ((threadIdx.x & 63) == 63) s_w[threadIdx.x >> 6] = w;
-    __syncthreads();
-    double sum = 0.0;
-    for (int i = 0; i < SP_NT / 64; ++i) sum += s_w[i];
-    const float eps = (float)h.eps;
-    const float now = sqrtf((float)(sum / (double)g.n) + eps);
-    const float fr = reservoir_f(ctrl->fr_prev, now, h.reservoir_decay, step);
-    const float sc = fmaxf(fr, eps);
-    F1Values v;
-    v.inv_s = 1.0f / sc;
-    v.hs_ds = ctrl->hs_ds;   // set by sweep 1
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        *fr_state = fr;
-        ctrl->scale = sc;
-        ctrl->inv_s = v.inv_s;
-    }
-    return v;
-}
-
-// ---------------------------------------------------------------------------
-// reconstruction weights of a lane's column
-// ---------------------------------------------------------------------------
-// A reconstruction sum_r (wc_r Craw_r + ws_r Sraw_r) + const equals
-// sum_x a_x(row) gam_x(col) + const with the row factors a_{2r} = a1_r,
-// a_{2r+1} = a2_r of the row table and, per column,
-//   additive kinds:     gam_{2r} = wc b_k1 + ws b_k2, gam_{2r+1} = ws b_k1 - wc b_k2
-//   product / constant: gam_{2r} = wc b_k1,           gam_{2r+1} = ws b_k2
-// (C = a1 b1 - a2 b2, S = a2 b1 + a1 b2, resp. C = a1 b1, S = a2 b2).
-// The sweeps read the row factors of the row all lanes share as scalars.
-template <int RM, int KC>
-__device__ __forceinline__ void recon_weights(const Geom& g, const ModeMeta* __restrict__ meta, const float (&b)[KC],
-                                              const float (*rc)[2], float (&gam)[2 * RM]) {
-#pragma unroll
-    for (int r = 0; r < RM; ++r) {
-        float g1 = 0.f, g2 = 0.f;
-        if (r < g.R) {
-            const ModeMeta m = meta[r];
-            float b1 = 0.f, b2 = 0.f;
-#pragma unroll
-            for (int k = 0; k < KC; ++k) {
-                if (k == m.k1) b1 = b[k];
-                if (k == m.k2) b2 = b[k];
-            }
-            const float wc = rc[r][0], ws = rc[r][1];
-            if (m.type == M_ADD) {
-                g1 = wc * b1 + ws * b2;
-                g2 = ws * b1 - wc * b2;
-            } else {
-                g1 = wc * b1;
-                g2 = ws * b2;
-            }
-        }
-        gam[2 * r] = g1;
-        gam[2 * r + 1] = g2;
-    }
-}
-
-// Lane's column carriers (the table has 2*rmax+1 rows, zero beyond K).
-template <int KC>
-__device__ __forceinline__ void load_cols(const Geom& g, const float* __restrict__ coltab, const Tile& t, float (&b)[KC]) {
-#pragma unroll
-    for (int k = 0; k < KC; ++k) b[k] = t.colok ? coltab[(size_t)k * g.cols + t.col] : 0.f;
-}
-
-// Row coefficients of two reconstructions in the column-carrier form
-//   recon(row, col) = c + sum_k alpha_k(row) b_k(col)
-// (b_k: the lane's column carriers, b_0 = 1), for the block's nr rows: the
-// per-lane form sum_q a_q(row) gamma_q(col) has 2R terms, this one K.  Set
-// j's mode coefficients are w0[j] rc0[j] + w1[j] rc1[j] (rc1 may be null).
-// The block's row factors arrive staged in LDS (s_rows[lr][q], q < 2 RM).
-// Loops of dependent reads per entry (global or LDS) cost microseconds per
-// block at the start of a sweep, so the computation is a small dense product
-// with independent reads.  Ends with a barrier.
-// Out: s_al[lr][j][k], row stride 2 * KCP (KCP = KC rounded up to 4).
-template <int KC> constexpr int kcp() { return (KC + 3) & ~3; }
-// byte offset of sweep 3's row coefficients in its dynamic LDS
-__host__ __device__ inline size_t lds_al_off(const Geom& g) {
-    const size_t head = (sizeof(unsigned long long) * SP_NHIST + sizeof(float)) * (size_t)g.T * g.B +
-                        sizeof(float) * (size_t)g.PR;
-    return (head + 15) & ~(size_t)15;
-}
-template <int RM, int KC>
-__device__ void alpha_rows(const Geom& g, const ModeMeta* __restrict__ meta, const float* __restrict__ s_rows, int nr,
-                           const float (*const rc0[2])[2], const float w0[2], const float (*const rc1[2])[2],
-                           const float w1[2], float* __restrict__ s_al) {
-    // alpha = rows x Cm^T: Cm[j][k][q] is the coefficient of the row factor
-    // a_q (q = 2r + c: component c of mode r) in alpha_k of set j.  Every Cm
-    // entry is built by its own thread from the mode table; each (row, set)
-    // pair is then 2 RM x KP branch-free FMAs on values held in registers.
-    constexpr int KP = kcp<KC>();
-    constexpr int RW = 2 * RM;
-    __shared__ __align__(16) float s_cm[2][KP][RW];
-    for (int e = threadIdx.x; e < 2 * KP * RW; e += blockDim.x) {
-        const int j = e / (KP * RW), rem = e - j * (KP * RW), k = rem / RW, q = rem - k * RW;
-        const int r = q >> 1, c = q & 1;
-        float v = 0.f;
-        if (r < g.R && k < KC) {
-            const ModeMeta m = meta[r];
-            float wc = w0[j] * rc0[j][r][0], ws = w0[j] * rc0[j][r][1];
-            if (rc1[j]) {
-                wc += w1[j] * rc1[j][r][0];
-                ws += w1[j] * rc1[j][r][1];
-            }
-            if (m.type == M_ADD) {   // alpha_k1 += wc a1 + ws a2, alpha_k2 += ws a1 - wc a2
-                if (m.k1 == k) v += c == 0 ? wc : ws;
-                if (m.k2 == k) v += c == 0 ? ws : -wc;
-            } else {                 // alpha_k1 += wc a1, alpha_k2 += ws a2
-                if (m.k1 == k && c == 0) v += wc;
-                if (m.k2 == k && c == 1) v += ws;
-            }
-        }
-        s_cm[j][k][q] = v;
-    }
-    __syncthreads();   // Cm and the caller's staged rows are complete
-    for (int p = threadIdx.x; p < 2 * nr; p += blockDim.x) {
-        const int lr = p >> 1, j = p & 1;
-        float row[RW];
-#pragma unroll
-        for (int q = 0; q < RW; ++q) row[q] = s_rows[lr * RW + q];
-        float* __restrict__ out = s_al + lr * (2 * KP) + j * KP;
-#pragma unroll
-        for (int k = 0; k < KP; ++k) {
-            float a = 0.f;
-#pragma unroll
-            for (int q = 0; q < RW; ++q) a = fmaf(s_cm[j][k][q], row[q], a);
-            out[k] = a;
-        }
-    }
-    __syncthreads();
-}
-
-// The block's rows of the row-factor table into LDS: s_rows[lr][q], q < 2 RM
-// (the table's rows have g.RW >= 2 RM entries).  No barrier.
-template <int RM>
-__device__ __forceinline__ void stage_rows(const Geom& g, const float* __restrict__ rowtab, int64_t r0, int nr,
-                                           float* __restrict__ s_rows) {
-    constexpr int RW = 2 * RM;
-    for (int e = threadIdx.x; e < nr * RW; e += blockDim.x) {
-        const int lr = e / RW, q = e - lr * RW;
-        s_rows[e] = rowtab[(r0 + lr) * g.RW + q];
-    }
-}
-
-// Lane contribution of a projection: Z[2q] = sum over the lane's rows of
-// a1_q(row) x, Z[2q+1] = the same with a2_q; combined with the lane's column
-// carriers into the raw C/S projections of every mode, partial slots
-// base + 2r (C) and base + 2r + 1 (S).
-template <int RM, int KC>
-__device__ __forceinline__ void proj_finish(const Geom& g, const ModeMeta* __restrict__ meta, const float (&Z)[2 * RM],
-                                            const float (&b)[KC], Partials& P, int base) {
-#pragma unroll
-    for (int r = 0; r < RM; ++r) {
-        if (r < g.R) {
-            const ModeMeta m = meta[r];
-            float b1 = 0.f, b2 = 0.f;
-#pragma unroll
-            for (int k = 0; k < KC; ++k) {
-                if (k == m.k1) b1 = b[k];
-                if (k == m.k2) b2 = b[k];
-            }
-            float c, sn;
-            if (m.type == M_ADD) {
-                c = b1 * Z[2 * r] - b2 * Z[2 * r + 1];
-                sn = b1 * Z[2 * r + 1] + b2 * Z[2 * r];
-            } else {
-                c = b1 * Z[2 * r];
-                sn = b2 * Z[2 * r + 1];
-            }
-            P.add(base + 2 * r, c);
-            P.add(base + 2 * r + 1, sn);
-        }
-    }
-}
-
-// Instant-metric factor of an axis marginal (cresso_v5.py:243-262):
-// exp(kappa * log(max(mean/gden, eps))), mean from a fixed-point sum.
-__device__ __forceinline__ float marg_factor(unsigned long long fx, double hs, double count, float gden, float kappa,
-                                             float eps) {
-    const float mean = (float)((double)fx / hs / count);
-    return expf(kappa * logf(fmaxf(mean / gden, eps)));
-}
-
-constexpr int SP_U = 8;  // rows whose loads are in flight together
-
-// Keeps the scheduler from interleaving the arithmetic of consecutive
-// elements (their loads are already in flight): bounds register pressure.
-__device__ __forceinline__ void elem_fence() { __builtin_amdgcn_sched_barrier(0); }
-
-// Element addressing inside a block's panel: the element index of the panel's
-// first element (row r0, first column of the slab) is uniform, so each array
-// is addressed as (uniform base pointer) + (32-bit lane offset lr * cols +
-// lane); the planner keeps PR * cols below 2^29.
-__device__ __forceinline__ int64_t panel_base(const Geom& g, const Tile& t) { return t.r0 * g.cols + (int64_t)t.slab * SP_NT; }
-__device__ __forceinline__ uint32_t panel_off(const Geom& g, int lr) { return (uint32_t)lr * (uint32_t)g.cols + threadIdx.x; }
-__device__ __forceinline__ uint64_t load_bins_at(const unsigned char* __restrict__ bins, int64_t base, uint32_t off,
-                                                 int binbytes) {
-    switch (binbytes) {
-        case 1: return (bins + base)[off];
-        case 2: return (reinterpret_cast<const uint16_t*>(bins) + base)[off];
-        case 4: return (reinterpret_cast<const uint32_t*>(bins) + base)[off];
-        default: return (reinterpret_cast<const uint64_t*>(bins) + base)[off];
-    }
-}
-
-// Panel arrays of a full tile as buffer views: one descriptor per array (the
-// panel's first element as base), the lane's column as the VGPR offset and the
-// row as a uniform SGPR offset, so the row loop needs no address arithmetic.
-// Byte sizes stay below 2^31 (the planner keeps PR * cols below 2^29).
-struct PanelBuf {
-    __amdgpu_buffer_rsrc_t r;
-    uint32_t lane;   // byte offset of the lane's column
-    uint32_t row;    // bytes per row
-};
-template <typename T>
-__device__ __forceinline__ PanelBuf panel_buf(const T* panel0, const Geom& g, int nr) {
-    PanelBuf b;
-    b.r = make_rsrc(panel0, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(T)));
-    b.lane = (uint32_t)(threadIdx.x * sizeof(T));
-    b.row = (uint32_t)(g.cols * sizeof(T));
-    return b;
-}
-template <typename T> __device__ __forceinline__ float ldb_lane(const PanelBuf& b, int lr);
-template <> __device__ __forceinline__ float ldb_lane<float>(const PanelBuf& b, int lr) {
-    return bload1(b.r, b.lane, (uint32_t)lr * b.row);
-}
-template <> __device__ __forceinline__ float ldb_lane<__half>(const PanelBuf& b, int lr) {
-    return to_f(__builtin_bit_cast(__half, (unsigned short)bload1u16(b.r, b.lane, (uint32_t)lr * b.row)));
-}
-template <> __device__ __forceinline__ float ldb_lane<__hip_bfloat16>(const PanelBuf& b, int lr) {
-    return to_f(__builtin_bit_cast(__hip_bfloat16, (unsigned short)bload1u16(b.r, b.lane, (uint32_t)lr * b.row)));
-}
-__device__ __forceinline__ uint32_t ldb_bins16(const PanelBuf& b, int lr) {
-    return bload1u16(b.r, b.lane, (uint32_t)lr * b.row);
-}
-__device__ __forceinline__ void stb_lane(const PanelBuf& b, int lr, float v) {
-    bstore1(b.r, b.lane, (uint32_t)lr * b.row, v);
-}
-
-// Rows of a full panel in batches of U: the loads of batch i+1 are issued
-// before batch i is processed (two register sets, no copies).  nr is a
-// multiple of 2U.  load(lr, x, b) loads row lr's lane values, body(lr, x, b)
-// processes them.
-// The same with a per-batch body: batch(i0, x[U], b[U]) processes rows i0..i0+U-1.
-// xa/ba hold the first batch, loaded by the caller (at the top of the kernel,
-// so that its latency overlaps the block's set-up).
-template <int U, typename Load, typename Batch>
-__device__ __forceinline__ void pipelined_batches(int nr, Load&& load, Batch&& batch, float (&xa)[U],
-                                                  uint32_t (&ba)[U]) {
-    float xb[U];
-    uint32_t bb[U];
-    for (int i0 = 0; i0 < nr; i0 += 2 * U) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) load(i0 + U + u, xb[u], bb[u]);
-        batch(i0, xa, ba);
-        if (i0 + 2 * U < nr) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) load(i0 + 2 * U + u, xa[u], ba[u]);
-        }
-        batch(i0 + U, xb, bb);
-    }
-}
-template <int U, typename Load, typename Body>
-__device__ __forceinline__ void pipelined_rows(int nr, Load&& load, Body&& body, float (&xa)[U], uint32_t (&ba)[U]) {
-    pipelined_batches<U>(
-        nr, load,
-        [&](int i0, const float* x, const uint32_t* b) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) body(i0 + u, x[u], b[u]);
-        },
-        xa, ba);
-}
-
-// Sums of 8 per-lane values (rows i0..i0+7 of the lane's column) over the 16
-// lanes of each DPP row: lane l returns row (l & 7)'s partial (lanes l and
-// l ^ 8 hold the same sum).  Lanes pair xor 1, 2, 4 while the values halve
-// (each lane keeps the rows of its own bit and receives them from its
-// partner), then xor 8: 25 instructions instead of 8 full wave reductions.
-// DPP row_ror:n reads lane (l - n) mod 16, so xor 4 is ror 4 for lanes with
-// bit 2 set and ror 12 for the others.
-template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float rows8_lanesum16(const float (&v)[8]) {
-    const int l = threadIdx.x & 63;
-    const bool b0 = (l & 1) != 0, b1 = (l & 2) != 0, b2 = (l & 4) != 0;
-    float w4[4], w2[2];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float keep = b0 ? v[2 * j + 1] : v[2 * j], give = b0 ? v[2 * j] : v[2 * j + 1];
-        w4[j] = keep + dpp_mov<0xB1>(give);   // quad_perm [1,0,3,2]: xor 1
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const float keep = b1 ? w4[2 * j + 1] : w4[2 * j], give = b1 ? w4[2 * j] : w4[2 * j + 1];
-        w2[j] = keep + dpp_mov<0x4E>(give);   // quad_perm [2,3,0,1]: xor 2
-    }
-    const float keep = b2 ? w2[1] : w2[0], give = b2 ? w2[0] : w2[1];
-    const float from_below = dpp_mov<0x124>(give);   // row_ror:4  -> lane l - 4
-    const float from_above = dpp_mov<0x12C>(give);   // row_ror:12 -> lane l + 4
-    float w1 = keep + (b2 ? from_below : from_above);
-    w1 += dpp_mov<0x128>(w1);                        // row_ror:8: xor 8
-    return w1;
-}
-
-// Sweep variants: MODE 1 is the common large-matrix case with every option
-// fixed at compile time (2-D tensor, instant metric on, two hash tables of at
-// most 256 bins, no weight decay, no local sharpness); MODE 0 handles every
-// other combination with runtime flags.
-struct SweepFlags {
-    bool hash_on, axes_on, wd_on, ls_on;
-    int T, bpb, binbytes;
-};
-template <int MODE>
-__device__ __forceinline__ SweepFlags sweep_flags(const Geom& g, int hash_arg, int axes_arg, const cresso_hyper& h) {
-    SweepFlags f;
-    if (MODE == 1) {
-        f.hash_on = true; f.axes_on = true; f.wd_on = false; f.ls_on = false;
-        f.T = 2; f.bpb = 1; f.binbytes = 2;
-    } else {
-        f.hash_on = hash_arg != 0; f.axes_on = axes_arg != 0;
-        f.wd_on = h.weight_decay != 0.0; f.ls_on = h.local_sharpness != 0.0;
-        f.T = g.T; f.bpb = g.bpb; f.binbytes = g.binbytes;
-    }
-    return f;
-}
-// whether a tensor's step can use MODE 1 (host side)
-// (MODE 1 also needs full tiles: every row of every panel and every lane's
-// column valid, and panels of a multiple of 4 SP_U rows for the row pipelines.)
-inline bool fast_mode(const Geom& g, int hash_on, int axes_on, const cresso_hyper& h) {
-    return hash_on && axes_on && g.T == 2 && g.bpb == 1 && g.binbytes == 2 && !g.one_d && h.weight_decay == 0.0 &&
-           h.local_sharpness == 0.0 && (float)fmax(h.instant_metric_power, 0.25) == 1.0f && g.rows % g.PR == 0 &&
-           g.cols % SP_NT == 0 && g.PR % (4 * SP_U) == 0;
-}
-
-// ---------------------------------------------------------------------------
-// S2: density field
-// ---------------------------------------------------------------------------
-template <int RM, int KC, typename PT, typename GT, int MODE>
-__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
-    Geom g, const GT* __restrict__ grad, const PT* __restrict__ param, const float* __restrict__ rowtab,
-    const float* __restrict__ coltab, const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins,
-    Ctrl* __restrict__ ctrl, double* __restrict__ part, unsigned long long* __restrict__ hist,
-    unsigned long long* __restrict__ rowfx, unsigned long long* __restrict__ colfx, int hash_arg, int axes_arg,
-    const double* __restrict__ part1, float* __restrict__ fr_state, int step, cresso_hyper h) {
-    constexpr int RW = 2 * RM;
-    extern __shared__ __align__(16) unsigned char dyn[];
-    __shared__ float red[4 * NV2];
-    const SweepFlags F = sweep_flags<MODE>(g, hash_arg, axes_arg, h);
-    const Tile t = tile_of(g);
-    const int B = g.B;
-    const int TB = F.T * B;
-    const int nr = (int)(t.r1 - t.r0);
-    const int64_t base = panel_base(g, t);
-    const GT* __restrict__ gb = grad + base;
-    // MODE 1: the first batch's loads go out before the set-up below
-    PanelBuf gbv, bnv;
-    float x0[SP_U];
-    uint32_t b0[SP_U];
-    if constexpr (MODE == 1) {
-        gbv = panel_buf(gb, g, nr);
-        bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
-#pragma unroll
-        for (int u = 0; u < SP_U; ++u) {
-            x0[u] = ldb_lane<GT>(gbv, u);
-            b0[u] = ldb_bins16(bnv, u);
-        }
-    }
-    // LDS: histogram [T][B] u64 | row-sum partials [16][PR] (MODE 0: [4 waves][PR];
-    // MODE 1: [4 waves][4 DPP rows][PR]) | MODE 1 row factors [PR][RW]
-    unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
-    float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
-    constexpr int NH = MODE == 1 ? SP_NHIST : 1;   // histogram copies in use
-    float* s_ar = s_wrow + 16 * g.PR;
-    if (F.hash_on)
-        for (int i = threadIdx.x; i < NH * TB; i += SP_NT) s_hist[i] = 0ull;
-    if (MODE == 1) stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
-    __syncthreads();
-    const PT* __restrict__ pb = param + base;
-    const float* __restrict__ rt = rowtab + t.r0 * g.RW;
-    const F1Values f1 = fin1_values(g, part1, ctrl, fr_state, step, h);
-    const float inv_s = f1.inv_s;
-    const float eps = (float)h.eps;
-    const float pw = (float)h.energy_power;
-    const float ipw = (float)fmax(h.instant_metric_power, 0.25);
-    const bool ip_one = ipw == 1.0f;
-    const float wd = (float)h.weight_decay;
-    const float sg = h.maximize ? -1.f : 1.f;
-    const float hs = (float)f1.hs_ds;
-    float Z[RW];
-#pragma unroll
-    for (int q = 0; q < RW; ++q) Z[q] = 0.f;
-    float aL = 0.f, aD = 0.f;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // Sums of log(1 + ds) are kept in log2 units (fin2 scales them by ln 2).
-    if constexpr (MODE == 1) {
-        // full tile: rel >= eps and instant-metric power 1, so the density is rel
-        constexpr int U = SP_U;
-        const int hc = threadIdx.x & (SP_NHIST - 1);
-        pipelined_batches<U>(
-            nr,
-            [&](int lr, float& x, uint32_t& b) {
-                x = ldb_lane<GT>(gbv, lr);
-                b = ldb_bins16(bnv, lr);
-            },
-            [&](int i0, const float* x, const uint32_t* bv) {
-#pragma unroll
-                for (int h8 = 0; h8 < U / 8; ++h8) {
-                    float dn[8];
-#pragma unroll
-                    for (int v8 = 0; v8 < 8; ++v8) {
-                        const int u = 8 * h8 + v8;
-                        const float rel = fminf(fmaf(fabsf(x[u]), inv_s, eps), 1.0e4f);
-                        const float ds = fexp2(pw * flog2(rel));
-                        const float L = flog2(1.0f + ds);
-                        dn[v8] = rel;
-                        aL += L;
-                        aD += rel;
-                        const float* __restrict__ ar = s_ar + (i0 + u) * RW;
-#pragma unroll
-                        for (int q = 0; q < RW; ++q) Z[q] = fmaf(ar[q], L, Z[q]);
-                        const unsigned long long v = to_fixed_u(ds * hs);
-                        atomicAdd(&s_hist[bin_of(bv[u], 0, 1) * NH + hc], v);
-                        atomicAdd(&s_hist[(B + bin_of(bv[u], 1, 1)) * NH + hc], v);
-#pragma unroll
-                        for (int q = 0; q < RW; ++q) pin1(Z[q]);
-                        pin1(aL);
-                        pin1(aD);
-                        pin1(dn[v8]);
-                        elem_fence();
-                    }
-                    const float rs = rows8_lanesum16(dn);
-                    if ((lane & 8) == 0) s_wrow[((wave << 2) + (lane >> 4)) * g.PR + i0 + 8 * h8 + (lane & 7)] = rs;
-                }
-            },
-            x0, b0);
-    } else
-    for (int i0 = 0; i0 < nr; i0 += SP_U) {
-        float gv[SP_U], pv[SP_U];
-        uint64_t bv[SP_U];
-#pragma unroll
-        for (int u = 0; u < SP_U; ++u) {
-            gv[u] = 0.f;
-            pv[u] = 0.f;
-            bv[u] = 0;
-            if (i0 + u < nr && t.colok) {
-                const uint32_t o = panel_off(g, i0 + u);
-                gv[u] = to_f(gb[o]);
-                if (F.wd_on) pv[u] = to_f(pb[o]);
-                if (F.hash_on) bv[u] = load_bins_at(bins, base, o, F.binbytes);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < SP_U; ++u) {
-            const int lr = i0 + u;
-            if (lr >= nr) break;
-            float dens = 0.f;
-            if (t.colok) {
-                float f = sg * gv[u];
-                if (F.wd_on) f = f + wd * pv[u];
-                const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
-                const float ds = fpow(rel, pw);
-                const float L = flog2(1.0f + ds);
-                const float rl = fmaxf(rel, eps);
-                dens = fminf(ip_one ? rl : fpow(rl, ipw), 1.0e6f);
-                aL += L;
-                aD += dens;
-                const float* __restrict__ ar = rt + lr * g.RW;
-#pragma unroll
-                for (int q = 0; q < RW; ++q) Z[q] += ar[q] * L;
-                if (F.hash_on) {
-                    const unsigned long long v = to_fixed_u(ds * hs);
-#pragma unroll
-                    for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= F.T) break;
-                        atomicAdd(&s_hist[tt * B + bin_of(bv[u], tt, F.bpb)], v);
-                    }
-                }
-            }
-            if (F.axes_on) {
-                const float ws = wave_total(dens);
-                if (lane == 63) s_wrow[wave * g.PR + lr] = ws;
-            }
-            if (MODE == 0) elem_fence();
-        }
-    }
-    __syncthreads();
-    if (F.axes_on) {
-        // axis density sums: one fixed-point atomic per row of this slab and per column of this panel
-        for (int lr = threadIdx.x; lr < nr; lr += SP_NT) {
-            float s = 0.f;
-            for (int w = 0; w < (MODE == 1 ? 16 : SP_NT / 64); ++w) s += s_wrow[w * g.PR + lr];
-            atomicAdd(&rowfx[t.r0 + lr], to_fixed_u(s * (float)g.hs_row));
-        }
-        if (t.colok) atomicAdd(&colfx[t.col], to_fixed_u(aD * (float)g.hs_col));
-    }
-    if (F.hash_on)
-        for (int i = threadIdx.x; i < TB; i += SP_NT) {
-            unsigned long long v = 0ull;
-#pragma unroll
-            for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-            if (v) atomicAdd(&hist[i], v);
-        }
-    float b[KC];
-    load_cols<KC>(g, coltab, t, b);
-    Partials P{red, 2 + 2 * g.R, NV2};
-    P.add(0, aL);
-    P.add(1, aD);
-    proj_finish<RM, KC>(g, meta, Z, b, P, 2);
-    P.flush(part);
-}
-
-// Helpers of the matrix-core sweeps.
-typedef float f32x4m __attribute__((ext_vector_type(4)));
-constexpr int SP_BQS = SP_NT + 16;   // row stride of sweep3m's LDS carrier table
-template <typename GT> __device__ __forceinline__ float ldg_el(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff);
-template <> __device__ __forceinline__ float ldg_el<float>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return bload1(r, voff, soff);
-}
-template <> __device__ __forceinline__ float ldg_el<__half>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return to_f(__builtin_bit_cast(__half, (unsigned short)bload1u16(r, voff, soff)));
-}
-template <>
-__device__ __forceinline__ float ldg_el<__hip_bfloat16>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return to_f(__builtin_bit_cast(__hip_bfloat16, (unsigned short)bload1u16(r, voff, soff)));
-}
-
-// Sum over each 16-lane DPP row (every lane of the row gets its row's total,
-// in a fixed order).
-__device__ __forceinline__ float row16_total(float v) {
-    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-    v = dpp_add<0x124, 0xF>(v);  // row_ror:4
-    v = dpp_add<0x128, 0xF>(v);  // row_ror:8
-    return v;
-}
-
-// ---------------------------------------------------------------------------
-// S2 on the matrix cores (MODE 1 tiles, RM <= 8): sweep2_kernel's element
-// math in sweep3m_kernel's tile layout (lane l: rows 4 lg + r of column li of
-// each 16 x 16 tile, 4 tile columns per wave).  The log-density projection
-// Z_q(col) = sum_rows a_q(row) L(row, col) is 4 MFMAs per tile (A = the rows'
-// factors, B = L).  Row density sums: the lane's 4 tile columns are added in
-// registers, then each 16-lane row group sums its columns with DPP; column
-// sums stay per lane and tile column until the end.
-// ---------------------------------------------------------------------------
-template <int RM, int KC, typename GT>
-__global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
-    Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
-    const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl,
-    double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ rowfx,
-    unsigned long long* __restrict__ colfx, const double* __restrict__ part1, float* __restrict__ fr_state, int step,
-    cresso_hyper h) {
-    static_assert(RM <= 8, "16 projection rows");
-    constexpr int RW = 2 * RM;
-    extern __shared__ __align__(16) unsigned char dyn[];
-    __shared__ float red[4 * NV2];
-    const Tile t = tile_of(g);
-    const int B = g.B;
-    const int TB = 2 * B;
-    const int nr = g.PR;
-    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int li = l & 15, lg = l >> 4;
-    const int64_t base = panel_base(g, t);
-    const uint32_t cols = (uint32_t)g.cols;
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(grad + base, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(GT)));
-    const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(reinterpret_cast<const uint16_t*>(bins) + base, (uint32_t)((int64_t)nr * g.cols * 2));
-    const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
-    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vb = lane_el * 2u;
-    auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
-    // one register set, refilled tile by tile (loads three tiles ahead of use)
-    float xv[16];
-    uint32_t bv[16];
-    auto load_tile = [&](int tr, int tc) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t o = tile_off(tr, tc, r);
-            xv[4 * tc + r] = ldg_el<GT>(rg, vg, o * (uint32_t)sizeof(GT));
-            bv[4 * tc + r] = bload1u16(rb, vb, o * 2u);
-        }
-    };
-#pragma unroll
-    for (int tc = 0; tc < 4; ++tc) load_tile(0, tc);
-    // LDS: histogram copies [TB][NH] u64 | row-sum partials [4 waves][PR] | row factors [PR][RW]
-    constexpr int NH = SP_NHIST;
-    const int hc = (int)(threadIdx.x & (SP_NHIST - 1));
-    unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
-    float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
-    float* s_ar = s_wrow + 16 * g.PR;
-    for (int i = threadIdx.x; i < NH * TB; i += SP_NT) s_hist[i] = 0ull;
-    stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
-    __syncthreads();
-    const F1Values f1 = fin1_values(g, part1, ctrl, fr_state, step, h);
-    const float inv_s = f1.inv_s;
-    const float eps = (float)h.eps;
-    const float pw = (float)h.energy_power;
-    const float sg = h.maximize ? -1.f : 1.f;
-    const float hs = (float)f1.hs_ds;
-    f32x4m zacc[4];
-#pragma unroll
-    for (int tc = 0; tc < 4; ++tc) zacc[tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
-    float aL = 0.f;
-    float cD[4] = {0.f, 0.f, 0.f, 0.f};   // column density sums of the lane's 4 tile columns
-    // Sums of log(1 + ds) are kept in log2 units (fin2 scales them by ln 2).
-    const int ntr = nr / 16;
-    for (int tr = 0; tr < ntr; ++tr) {
-        float rs[4] = {0.f, 0.f, 0.f, 0.f};   // this row of tiles' density, per lane row
-#pragma unroll
-        for (int tc = 0; tc < 4; ++tc) {
-            const float* x = xv + 4 * tc;
-            const uint32_t* b = bv + 4 * tc;
-            float Ls[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                // full tile: rel >= eps and instant-metric power 1, so the density is rel
-                const float rel = fminf(fmaf(fabsf(sg * x[r]), inv_s, eps), 1.0e4f);
-                const float ds = fexp2(pw * flog2(rel));
-                const float L = flog2(1.0f + ds);
-                Ls[r] = L;
-                aL += L;
-                rs[r] += rel;
-                cD[tc] += rel;
-                const unsigned long long v = to_fixed_u(ds * hs);
-                atomicAdd(&s_hist[(b[r] & 0xffu) * NH + hc], v);
-                atomicAdd(&s_hist[(B + (b[r] >> 8)) * NH + hc], v);
-            }
-            // A of the projection: a_li(row 16 tr + 4 lg + r)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float aJ = li < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (li < RW ? li : 0)] : 0.f;
-                zacc[tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJ, Ls[r], zacc[tc], 0, 0, 0);
-            }
-            if (tr + 1 < ntr) load_tile(tr + 1, tc);
-            pin1(aL);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) pin1(rs[r]);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) pin1(cD[c]);
-            elem_fence();
-        }
-        // rows 16 tr + 4 lg + r: the 16 columns of the lane group, lane li = r writes
-        float rt[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) rt[r] = row16_total(rs[r]);
-        if (li < 4) s_wrow[wv * g.PR + 16 * tr + 4 * lg + li] = li == 0 ? rt[0] : (li == 1 ? rt[1] : (li == 2 ? rt[2] : rt[3]));
-    }
-    __syncthreads();
-    // axis density sums: one fixed-point atomic per row of this slab and per column of this panel
-    for (int lr = threadIdx.x; lr < nr; lr += SP_NT) {
-        float sr = 0.f;
-        for (int w = 0; w < SP_NT / 64; ++w) sr += s_wrow[w * g.PR + lr];
-        atomicAdd(&rowfx[t.r0 + lr], to_fixed_u(sr * (float)g.hs_row));
-    }
-    float aD = 0.f;
-    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
-#pragma unroll
-    for (int tc = 0; tc < 4; ++tc) {
-        // the column's 4 lane groups, in a fixed order
-        float c = cD[tc];
-        c += __shfl_xor(c, 16, 64);
-        c += __shfl_xor(c, 32, 64);
-        if (lg == 0) atomicAdd(&colfx[colw + 16 * tc + li], to_fixed_u(c * (float)g.hs_col));
-        aD += cD[tc];
-    }
-    for (int i = threadIdx.x; i < TB; i += SP_NT) {
-        unsigned long long v = 0ull;
-#pragma unroll
-        for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-        if (v) atomicAdd(&hist[i], v);
-    }
-    Partials P{red, 2 + 2 * g.R, NV2};
-    P.add(0, aL);
-    P.add(1, aD);
-    // projection: lane group lg holds Z_{4 lg + j}(col), both components of
-    // modes 2 lg and 2 lg + 1, for its 4 columns (proj_finish's form), summed
-    // over the columns and the group's 16 lanes into slots 2 + 4 lg + j
-    float cs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        const int r = 2 * lg + half;
-        if (r < g.R) {
-            const ModeMeta m = meta[r];
-#pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
-                const int64_t c = colw + 16 * tc + li;
-                // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
-                const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
-                const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
-                const float z1 = zacc[tc][2 * half], z2 = zacc[tc][2 * half + 1];
-                if (m.type == M_ADD) {
-                    cs[2 * half] += b1 * z1 - b2 * z2;
-                    cs[2 * half + 1] += b1 * z2 + b2 * z1;
-                } else {
-                    cs[2 * half] += b1 * z1;
-                    cs[2 * half + 1] += b2 * z2;
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float sm = row16_total(cs[j]);
-        const int slot = 4 * lg + j;
-        if (li == 15 && slot < 2 * g.R) red[wv * P.V + 2 + slot] = sm;
-    }
-    P.flush(part);
-}
-
-// ---------------------------------------------------------------------------
-// finalize helpers: one wave, one lane per mode
-// ---------------------------------------------------------------------------
-// Mode weights (the coefficient of each normalized carrier) and the
-// coefficients (wc, ws) of the raw carriers and the constant of
-//   shrink * sum_r g_r (cc_r Cn_r + sc_r Sn_r)  (cresso_v5.py:362-376)
-// with Cn = (Craw - mu_c) ic; a gate of exactly 0 drops the mode.  Lane r of
-// the calling wave handles mode r; the constant is summed in mode order.
-__device__ void set_recon_lanes(const Geom& g, const double* __restrict__ stats, float (*rc)[2], float* rconst,
-                                float cc, float sc, float gate, float* s_tmp, float* weights = nullptr) {
-    const int r = threadIdx.x & 63;
-    const double shrink = 1.0 / sqrt(fmax(1.0, 0.7 * log2((double)g.R + 1.0)));
-    float kc = 0.f, ks = 0.f, wc = 0.f, ws = 0.f, cterm = 0.f;
-    if (r < g.R) {
-        if (gate != 0.0f) {
-            kc = (float)((double)cc * shrink) * gate;
-            ks = (float)((double)sc * shrink) * gate;
-            wc = (float)((double)kc * stats[4 * r + 1]);
-            ws = (float)((double)ks * stats[4 * r + 3]);
-            cterm = (float)((double)wc * stats[4 * r + 0] + (double)ws * stats[4 * r + 2]);
-        }
-        rc[r][0] = wc;
-        rc[r][1] = ws;
-        s_tmp[r] = cterm;
-        if (weights) {
-            weights[2 * r] = kc;
-            weights[2 * r + 1] = ks;
-        }
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    if (r == 0) {
-        float cst = 0.f;
-        for (int q = 0; q < g.R; ++q) cst -= s_tmp[q];
-        *rconst = cst;
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-}
-
-// Sum over lanes 0..R-1 of a fully active wave (fp64), in the fixed order of
-// the DPP wave reduction, returned to every lane.
-__device__ double lanes_sum(double v, int R) {
-    const int r = threadIdx.x & 63;
-    const double t = wave_total_d(r < R ? v : 0.0);
-    const int lo = __builtin_amdgcn_readlane(__double2loint(t), 63);
-    const int hi = __builtin_amdgcn_readlane(__double2hiint(t), 63);
-    return __hiloint2double(hi, lo);
-}
-
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
-
-// ---------------------------------------------------------------------------
-// F2: hash metric, metric oscillator, recon coefficients
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                        const double* __restrict__ stats, const double* __restrict__ bounds,
-                                                        const double* __restrict__ part,
-                                                        unsigned long long* __restrict__ hist,
-                                                        const unsigned long long* __restrict__ counts,
-                                                        float* __restrict__ lt, SpecState st, Ctrl* __restrict__ ctrl,
-                                                        int step, int hash_on, int hard, cresso_hyper h) {
-    __shared__ double s_v[NV2];
-    __shared__ double red[SP_FN_NT / 64];
-    __shared__ float s_emean[SP_MAXT];
-    __shared__ float s_tmpf[64];
-    const int tid = threadIdx.x;
-    const float eps = (float)h.eps;
-    const double n = (double)g.n;
-    __shared__ double s_stats[4 * SP_MAXR], s_bounds[2 * SP_MAXR];
-    __shared__ float s_mode[SP_MAXR][9];
-    __shared__ int s_zero[SP_MAXR];
-    for (int i = tid; i < 4 * g.R; i += SP_FN_NT) s_stats[i] = stats[i];
-    for (int i = tid; i < 2 * g.R; i += SP_FN_NT) s_bounds[i] = bounds[i];
-    for (int i = tid; i < 9 * g.R; i += SP_FN_NT) {
-        const int r = i / 9, j = i - 9 * r;
-        const float* src[8] = {st.omega, st.metric_cos, st.metric_p_cos, st.metric_sin, st.metric_p_sin, st.q_cos,
-                               st.q_sin, st.conf};
-        if (j < 8) s_mode[r][j] = src[j][r];
-        else s_zero[r] = meta[r].type == M_ZERO;
-    }
-    load_sums(part, 2 + 2 * g.R, s_v);
-    // sweep 2 sums log(1 + ds) in log2 units
-    if (tid < 2 + 2 * g.R && tid != 1) s_v[tid] *= 0.6931471805599453;
-    __syncthreads();
-    // hash energy per table (cresso_v5.py:1012-1056)
-    if (hash_on) {
-        const int TB = g.T * g.B;
-        for (int i = tid; i < TB; i += SP_FN_NT) {
-            const double cnt = (double)counts[i];
-            const float cell = (float)((double)(long long)hist[i] / ctrl->hs_ds / fmax(cnt, 1.0));
-            hist[i] = 0ull;
-            float e = st.hash_energy[i];
-            e = step <= 1 ? cell : e * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * cell;
-            st.hash_energy[i] = e;
-        }
-        __syncthreads();
-        for (int tt = 0; tt < g.T; ++tt) {
-            double s[1] = {0.0};
-            for (int b = tid; b < g.B; b += SP_FN_NT) s[0] += (double)st.hash_energy[tt * g.B + b];
-            block_sum<1>(s, red);
-            if (tid == 0) s_emean[tt] = (float)(s[0] / (double)g.B);
-        }
-        __syncthreads();
-        const float ex = (float)(h.hash_metric_coupling / fmax(0.25, h.energy_power));
-        for (int i = tid; i < TB; i += SP_FN_NT) {
-            const int tt = i / g.B;
-            const float hm = fmaxf(st.hash_energy[i] / fmaxf(s_emean[tt], eps), eps);
-            lt[i] = logf(fmaxf(clampf(powf(hm, ex), 0.08f, 12.0f), eps));
-        }
-    }
-    if (tid < 64) {
-        // lane r: mode r
-        const int r = tid;
-        const bool on = r < g.R;
-        const double sumL = s_v[0], sumD = s_v[1];
-        // log-density projections: d = L/max(mean L, eps) - 1, mean(d Cn) = mean(L Cn)/m - mean(Cn)
-        const double m = fmax((double)(float)(sumL / n), (double)eps);
-        float pcos = 0.f, psin = 0.f;
-        if (on) {
-            const double prc = (s_v[2 + 2 * r] - s_stats[4 * r] * sumL) * s_stats[4 * r + 1] / n / m -
-                               (s_zero[r] ? 1.0 : 0.0);   // mean(Cn) = 1 for the constant mode
-            const double prs = (s_v[3 + 2 * r] - s_stats[4 * r + 2] * sumL) * s_stats[4 * r + 3] / n / m;
-            pcos = (float)prc;
-            psin = (float)prs;
-        }
-        // metric oscillator (cresso_v5.py:1064-1088)
-        const float mdt = (float)h.metric_dt;
-        const float damp = (float)fmax(0.0, 1.0 - h.metric_dt * h.metric_friction);
-        float mqc = 0.f, mqs = 0.f;
-        if (on) {
-            const float om = s_mode[r][0];
-            const float o2 = om * om;
-            float mq = s_mode[r][1], mp = s_mode[r][2];
-            mp = mp * damp;
-            mp = mp + mdt * (pcos - o2 * mq);
-            mq = clampf(mq + mdt * mp, -3.0f, 3.0f);
-            st.metric_cos[r] = mq;
-            st.metric_p_cos[r] = mp;
-            mqc = mq;
-            mq = s_mode[r][3];
-            mp = s_mode[r][4];
-            mp = mp * damp;
-            mp = mp + mdt * (psin - o2 * mq);
-            mq = clampf(mq + mdt * mp, -3.0f, 3.0f);
-            st.metric_sin[r] = mq;
-            st.metric_p_sin[r] = mp;
-            mqs = mq;
-        }
-        set_recon_lanes(g, s_stats, ctrl->rc[0], &ctrl->rconst[0], mqc, mqs, 1.0f, s_tmpf);
-        // prediction with the pre-contact state and gates
-        float qc = 0.f, qs = 0.f, gt = 0.f;
-        double pm = 0.0;
-        const double shrink = 1.0 / sqrt(fmax(1.0, 0.7 * log2((double)g.R + 1.0)));
-        if (on) {
-            qc = s_mode[r][5];
-            qs = s_mode[r][6];
-            gt = sigmoidf_((float)h.confidence_gain * s_mode[r][7]);
-            pm = shrink * gt * (fabs((double)qc) * s_bounds[2 * r] + fabs((double)qs) * s_bounds[2 * r + 1]);
-        }
-        set_recon_lanes(g, s_stats, ctrl->rc[1], &ctrl->rconst[1], qc, qs, gt, s_tmpf, ctrl->wpred);
-        const double pmax = lanes_sum(pm, g.R);
-        if (r == 0) {
-            // instant metric: mean density and coupling (cresso_v5.py:243-262)
-            ctrl->gden = (float)fmax(sumD / n, (double)eps);
-            const float icoup = hard ? (float)h.instant_metric_coupling : 0.0f;
-            ctrl->kappa = (float)((double)icoup / ((double)g.ndim * fmax(h.instant_metric_power, 0.25)));
-            // fixed-point scale of the port histogram: |P| <= (1+tm)*1e4 + max|pred|, <= n elements per bin
-            const double vmax = (1.0 + h.transport_mix) * 1.0e4 + pmax * 1.01 + 1.0;
-            ctrl->hs_P = ldexp(1.0, (int)floor(62.0 - log2(vmax * (double)g.n)));
-        }
-    }
-}
-
-// ndim >= 3: the factor of each column of the column group (the trailing
-// axes) is the product over those axes of (axis mean / global mean)^kappa.
-// marg_terms_kernel: one block per coordinate k of trailing axis a sums the
-// column sums that share it (64-bit integers: exact in any order) into the
-// axis term kappa log(max(mean / gden, eps)).
-constexpr int SP_MARG_NT = 256;
-__global__ __launch_bounds__(SP_MARG_NT) void marg_terms_kernel(Geom g, const unsigned long long* __restrict__ colfx,
-                                                                float* __restrict__ terms, const Ctrl* __restrict__ ctrl,
-                                                                float eps) {
-    __shared__ unsigned long long red[SP_MARG_NT];
-    // block -> (axis a, coordinate k); the axis terms are laid out axis after axis
-    int64_t k = blockIdx.x, off = 0;
-    int a = 0;
-    while (a + 1 < g.ntrail && k >= g.tdim[a]) {
-        k -= g.tdim[a];
-        off += g.tdim[a];
-        ++a;
-    }
-    int64_t inner = 1;
-    for (int b = a + 1; b < g.ntrail; ++b) inner *= g.tdim[b];
-    const int64_t dim = g.tdim[a];
-    const int64_t m = g.cols / dim;   // columns sharing coordinate k: outer x inner
-    unsigned long long s = 0ull;
-    for (int64_t j = threadIdx.x; j < m; j += SP_MARG_NT) {
-        const int64_t o = j / inner, in = j - o * inner;
-        s += colfx[(o * dim + k) * inner + in];
-    }
-    red[threadIdx.x] = s;
-    __syncthreads();
-    for (int w = SP_MARG_NT / 2; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-        const float mean = (float)((double)red[0] / g.hs_col / ((double)g.n / (double)dim));
-        terms[off + k] = ctrl->kappa * logf(fmaxf(mean / ctrl->gden, eps));
-    }
-}
-
-// marg_fac_kernel: one thread per column, exp of the sum of its axis terms.
-__global__ __launch_bounds__(SP_MARG_NT) void marg_fac_kernel(Geom g, const float* __restrict__ terms,
-                                                              float* __restrict__ colfac) {
-    const int64_t c = (int64_t)blockIdx.x * SP_MARG_NT + threadIdx.x;
-    if (c >= g.cols) return;
-    int64_t off = 0;
-    for (int a = 0; a < g.ntrail; ++a) off += g.tdim[a];
-    int64_t rem = c;
-    float acc = 0.f;
-    for (int a = g.ntrail - 1; a >= 0; --a) {
-        off -= g.tdim[a];
-        const int64_t k = rem % g.tdim[a];
-        rem /= g.tdim[a];
-        acc += terms[off + k];
-    }
-    colfac[c] = expf(acc);
-}
-
-// ---------------------------------------------------------------------------
-// S3: tangent force, prediction error, port projection / histograms, t projection
-// ---------------------------------------------------------------------------
-template <int RM, int KC, typename PT, typename GT, int MODE>
-__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
-    Geom g, const GT* __restrict__ grad, const PT* __restrict__ param, const float* __restrict__ rowtab,
-    const float* __restrict__ coltab, const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins,
-    const Ctrl* __restrict__ ctrl, const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx,
-    const unsigned long long* __restrict__ colfx, const float* __restrict__ colfac, float* __restrict__ tbuf,
-    double* __restrict__ part, unsigned long long* __restrict__ hist, int hash_arg, cresso_hyper h) {
-    constexpr int RW = 2 * RM;
-    extern __shared__ __align__(16) unsigned char dyn[];
-    __shared__ float red[4 * NV3];
-    const SweepFlags F = sweep_flags<MODE>(g, hash_arg, 1, h);
-    const Tile t = tile_of(g);
-    const int B = g.B;
-    const int TB = F.T * B;
-    const int nr = (int)(t.r1 - t.r0);
-    const int64_t base = panel_base(g, t);
-    const GT* __restrict__ gb = grad + base;
-    float* __restrict__ tb = tbuf + base;
-    // MODE 1: the first batch's loads go out before the set-up below
-    PanelBuf gbv, bnv, tbv;
-    float x0[SP_U];
-    uint32_t b0[SP_U];
-    if constexpr (MODE == 1) {
-        gbv = panel_buf(gb, g, nr);
-        bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
-        tbv = panel_buf(tb, g, nr);
-#pragma unroll
-        for (int u = 0; u < SP_U; ++u) {
-            x0[u] = ldb_lane<GT>(gbv, u);
-            b0[u] = ldb_bins16(bnv, u);
-        }
-    }
-    // LDS: histogram [T][B] u64 | log hash metric [T][B] | row metric factor [PR]
-    //      | row reconstruction coefficients [PR][2][KP] (16-byte aligned) | row factors [PR][RW]
-    unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
-    float* s_lt = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
-    constexpr int NH = MODE == 1 ? SP_NHIST : 1;   // histogram copies in use
-    const int hc = MODE == 1 ? (int)(threadIdx.x & (SP_NHIST - 1)) : 0;
-    float* s_rf = s_lt + TB;
-    const float eps = (float)h.eps;
-    const float kappa = ctrl->kappa, gden = ctrl->gden;
-    const bool inst_on = MODE == 1 ? true : kappa != 0.0f;
-    if (F.hash_on)
-        for (int i = threadIdx.x; i < TB; i += SP_NT) {
-            s_lt[i] = lt[i];
-#pragma unroll
-            for (int c = 0; c < NH; ++c) s_hist[i * NH + c] = 0ull;
-        }
-    for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
-        s_rf[lr] = (inst_on && !g.one_d) ? marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps) : 1.0f;
-    // the lane's column carriers and the rows' coefficients of the metric
-    // field (set 0) and the prediction (set 1)
-    constexpr int KP = kcp<KC>();
-    float bc[KC];
-    load_cols<KC>(g, coltab, t, bc);
-    float* s_al = reinterpret_cast<float*>(dyn + lds_al_off(g));
-    // the rows' factors a_q of the t projection, staged with the coefficients
-    // (uniform LDS reads in the loop instead of scalar loads of every row)
-    float* s_ar = s_al + 2 * KP * g.PR;
-    stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
-    {
-        const float (*const r0[2])[2] = {ctrl->rc[0], ctrl->rc[1]};
-        const float (*const r1[2])[2] = {nullptr, nullptr};
-        const float w0[2] = {1.f, 1.f}, w1[2] = {0.f, 0.f};
-        alpha_rows<RM, KC>(g, meta, s_ar, nr, r0, w0, r1, w1, s_al);
-    }
-    const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
-    __syncthreads();
-    const PT* __restrict__ pb = param + base;
-    const float inv_s = ctrl->inv_s, scale = ctrl->scale;
-    const float mcoup = (float)h.metric_coupling;
-    const float wd = (float)h.weight_decay;
-    const float sg = h.maximize ? -1.f : 1.f;
-    const float ls = (float)h.local_sharpness;
-    const float ipw = (float)fmax(h.instant_metric_power, 0.25);
-    float ec = 1.0f;
-    if (inst_on && !g.one_d && t.colok)
-        ec = g.ntrail == 1 ? marg_factor(colfx[t.col], g.hs_col, (double)g.rows, gden, kappa, eps) : colfac[t.col];
-    const float invT = 1.0f / (float)F.T;
-    const float tm = (float)h.transport_mix;
-    const float hs = (float)ctrl->hs_P;
-    const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
-    const float k2 = -2.8853900817779268f * iclip;   // -2 log2(e) / clip
-    // Only t is projected: the port P = (1 + tm) t - pred projects to
-    // (1 + tm) mean(t Xn) - G u_pred, formed in fin3 from the Gram matrix.
-    float ZT[RW];
-#pragma unroll
-    for (int q = 0; q < RW; ++q) ZT[q] = 0.f;
-    float m_ee = 0.f, m_t = 0.f, m_tt = 0.f, m_rr = 0.f, m_bb = 0.f, m_oo = 0.f, m_rb = 0.f, m_ro = 0.f,
-          m_bo = 0.f, m_tr = 0.f, m_tb = 0.f, m_to = 0.f;
-    // MODE 1 panel views (full tile)
-    // one row of the lane's column: f -> t (stored), moments, projection, histogram
-    auto row = [&](int lr, float gval, float pval, uint64_t bval) {
-                float f = sg * gval;
-                if (F.wd_on) f = f + wd * pval;
-                const float* __restrict__ ar = s_ar + lr * RW;
-                // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
-                const float* __restrict__ al = s_al + lr * (2 * KP);
-                float lm = cM;
-#pragma unroll
-                for (int k = 0; k < KC; ++k) lm = fmaf(al[k], bc[k], lm);
-                lm = med3f(lm, -3.0f, 3.0f);
-                const float M = med3f(fexp(mcoup * lm), 0.06f, 16.0f);
-                float den = scale * M;
-                if (F.ls_on) {
-                    const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
-                    den = den * clampf(1.0f + ls * fsqrt(fminf(rel, 100.0f)), 1.0f, 8.0f);
-                }
-                if (inst_on) {
-                    float I;
-                    if (MODE == 0 && g.one_d) {
-                        const float rel = fmaxf(fminf(fabsf(f) * inv_s + eps, 1.0e4f), eps);
-                        const float dens = fminf(ipw == 1.0f ? rel : fpow(rel, ipw), 1.0e6f);
-                        I = fexp(kappa * flog(fmaxf(dens / gden, eps)));
-                    } else {
-                        I = s_rf[lr] * ec;
-                    }
-                    den = den * med3f(I, 0.08f, 12.0f);
-                }
-                if (F.hash_on) {
-                    float lsum = 0.f;
-#pragma unroll
-                    for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= F.T) break;
-                        lsum += s_lt[tt * B + bin_of(bval, tt, F.bpb)];
-                    }
-                    den = den * med3f(fexp(lsum * invT), 0.08f, 12.0f);
-                }
-                const float tv = med3f(f * frcp(den + eps), -1.0e4f, 1.0e4f);
-                if (MODE == 1)
-                    stb_lane(tbv, lr, tv);
-                else
-                    tb[panel_off(g, lr)] = tv;
-                float pred = cP;
-#pragma unroll
-                for (int k = 0; k < KC; ++k) pred = fmaf(al[KP + k], bc[k], pred);
-                const float err = tv - pred;
-                const float P = err + tm * tv;
-                m_ee += err * err;
-                m_t += tv;
-                m_tt += tv * tv;
-                // |rat|, |tanh|, |root| share the sign of t: the moments take
-                // magnitudes, and fin3 scales the tanh ones by clip (bnd = clip tanh)
-                const float at = fabsf(tv);
-                const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
-                m_rr = fmaf(z.rat, z.rat, m_rr); m_bb = fmaf(z.th, z.th, m_bb); m_oo = fmaf(z.root, z.root, m_oo);
-                m_rb = fmaf(z.rat, z.th, m_rb); m_ro = fmaf(z.rat, z.root, m_ro); m_bo = fmaf(z.th, z.root, m_bo);
-                m_tr = fmaf(at, z.rat, m_tr); m_tb = fmaf(at, z.th, m_tb); m_to = fmaf(at, z.root, m_to);
-#pragma unroll
-                for (int q = 0; q < RW; ++q) ZT[q] += ar[q] * tv;
-                if (F.hash_on) {
-                    const unsigned long long v = to_fixed_s(P * hs);
-#pragma unroll
-                    for (int tt = 0; tt < SP_MAXT; ++tt) {
-                        if (tt >= F.T) break;
-                        atomicAdd(&s_hist[(tt * B + bin_of(bval, tt, F.bpb)) * NH + hc], v);
-                    }
-                }
-                if (MODE == 1) {
-                    // this row's contributions are complete here
-#pragma unroll
-                    for (int q = 0; q < RW; ++q) pin1(ZT[q]);
-                    pin1(m_ee); pin1(m_t); pin1(m_tt); pin1(m_rr); pin1(m_bb); pin1(m_oo);
-                    pin1(m_rb); pin1(m_ro); pin1(m_bo); pin1(m_tr); pin1(m_tb); pin1(m_to);
-                }
-                elem_fence();
-    };
-    if constexpr (MODE == 1) {
-        // full tile: no guards, next rows' loads in flight during these rows
-        pipelined_rows<SP_U>(
-            nr,
-            [&](int lr, float& x, uint32_t& b) {
-                x = ldb_lane<GT>(gbv, lr);
-                b = ldb_bins16(bnv, lr);
-            },
-            [&](int lr, float x, uint32_t b) { row(lr, x, 0.f, b); }, x0, b0);
-    } else if (t.colok) {
-        for (int i0 = 0; i0 < nr; i0 += SP_U) {
-            float gv[SP_U], pv[SP_U];
-            uint64_t bv[SP_U];
-#pragma unroll
-            for (int u = 0; u < SP_U; ++u) {
-                gv[u] = 0.f;
-                pv[u] = 0.f;
-                bv[u] = 0;
-                if (i0 + u < nr) {
-                    const uint32_t o = panel_off(g, i0 + u);
-                    gv[u] = to_f(gb[o]);
-                    if (F.wd_on) pv[u] = to_f(pb[o]);
-                    if (F.hash_on) bv[u] = load_bins_at(bins, base, o, F.binbytes);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < SP_U; ++u) {
-                if (i0 + u >= nr) break;
-                row(i0 + u, gv[u], pv[u], bv[u]);
-            }
-        }
-    }
-    __syncthreads();
-    if (F.hash_on)
-        for (int i = threadIdx.x; i < TB; i += SP_NT) {
-            unsigned long long v = 0ull;
-#pragma unroll
-            for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-            if (v) atomicAdd(&hist[i], v);
-        }
-    Partials P{red, 15 + 2 * g.R, NV3};
-    const float mm[13] = {m_ee, 0.f, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
-#pragma unroll
-    for (int k = 0; k < 13; ++k) P.add(k, mm[k]);
-    P.add(13, 0.f);
-    P.add(14, 0.f);
-    proj_finish<RM, KC>(g, meta, ZT, bc, P, 15);
-    P.flush(part);
-}
-
-// ---------------------------------------------------------------------------
-// S3 on the matrix cores (MODE 1 tiles, RM <= 8, KC <= 12).  The element math
-// is sweep3_kernel's; the contractions run as v_mfma_f32_16x16x4f32 on 16 x 16
-// tiles, each wave owning 64 columns of the panel as 4 tile columns:
-//   metric and prediction fields: 3 + 3 MFMAs per tile (column-carrier form,
-//     A = the rows' alpha coefficients, B = the columns' carriers);
-//   t projection Z_q(col) = sum_rows a_q(row) t(row, col): 4 MFMAs per tile,
-//     A[q][k] = a_q(row 4k + r), B[k][col] = t(row 4k + r, col) for the
-//     tile's element r of each lane, accumulated over the panel in D[q][col].
-// Layouts (lane l, li = l % 16, lg = l / 16): A[i][k] from lane (i = li,
-// k = lg), B[k][j] from lane (j = li, k = lg), D[i][j] in lane (j = li),
-// register r: i = 4 lg + r.  Lane l processes rows 4 lg + r of column li of
-// each tile.  The loads of the next row of tiles are in flight while a row is
-// processed.
-// ---------------------------------------------------------------------------
-
-template <int RM, int KC, typename GT>
-__global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
-    Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
-    const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
-    const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx, const unsigned long long* __restrict__ colfx,
-    const float* __restrict__ colfac, float* __restrict__ tbuf, double* __restrict__ part,
-    unsigned long long* __restrict__ hist, cresso_hyper h) {
-    static_assert(RM <= 8 && KC <= 12, "16 projection rows, three K-chunks of four carriers");
-    constexpr int RW = 2 * RM;
-    constexpr int KP = kcp<KC>();
-    extern __shared__ __align__(16) unsigned char dyn[];
-    __shared__ float red[4 * NV3];
-    const Tile t = tile_of(g);
-    const int B = g.B;
-    const int TB = 2 * B;
-    const int nr = g.PR;
-    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int li = l & 15, lg = l >> 4;
-    const int64_t base = panel_base(g, t);
-    const uint32_t cols = (uint32_t)g.cols;
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(grad + base, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(GT)));
-    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tbuf + base, (uint32_t)((int64_t)nr * g.cols * 4));
-    const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(reinterpret_cast<const uint16_t*>(bins) + base, (uint32_t)((int64_t)nr * g.cols * 2));
-    const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
-    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vt = lane_el * 4u, vb = lane_el * 2u;
-    // tile (tr, tc), lane element r: panel element (16 tr + 4 lg + r, 64 wv + 16 tc + li)
-    auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
-    // one register set, refilled tile by tile: the loads of tile (tr + 1, tc)
-    // go out as soon as tile (tr, tc) is done, three tiles ahead of their use
-    float xv[16];
-    uint32_t bv[16];
-    auto load_tile = [&](int tr, int tc) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t o = tile_off(tr, tc, r);
-            xv[4 * tc + r] = ldg_el<GT>(rg, vg, o * (uint32_t)sizeof(GT));
-            bv[4 * tc + r] = bload1u16(rb, vb, o * 2u);
-        }
-    };
-#pragma unroll
-    for (int tc = 0; tc < 4; ++tc) load_tile(0, tc);
-    // LDS as sweep3_kernel: histogram copies [TB][NH] u64 | log hash metric [TB]
-    //      | row metric factor [PR] | (16-aligned) alpha [PR][2][KP] | row factors [PR][RW]
-    constexpr int NH = SP_NHIST;
-    const int hc = (int)(threadIdx.x & (SP_NHIST - 1));
-    unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
-    float* s_lt = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
-    float* s_rf = s_lt + TB;
-    float* s_al = reinterpret_cast<float*>(dyn + lds_al_off(g));
-    float* s_ar = s_al + 2 * KP * g.PR;
-    const float eps = (float)h.eps;
-    const float kappa = ctrl->kappa, gden = ctrl->gden;
-    for (int i = threadIdx.x; i < TB; i += SP_NT) {
-        s_lt[i] = lt[i];
-#pragma unroll
-        for (int c = 0; c < NH; ++c) s_hist[i * NH + c] = 0ull;
-    }
-    for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
-        s_rf[lr] = marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps);
-    stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
-    // the block's column carriers (B operands of the reconstructions) and
-    // column instant-metric factors, in LDS: [KP][SP_BQS] (rows padded so that
-    // the 4 lane groups of a wave read distinct banks) | [SP_NT]
-    float* s_bq = s_ar + RW * g.PR;
-    float* s_ec = s_bq + KP * SP_BQS;
-    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
-    {
-        const int64_t c = (int64_t)t.slab * SP_NT + threadIdx.x;
-#pragma unroll
-        for (int k = 0; k < KP; ++k) s_bq[k * SP_BQS + threadIdx.x] = k < KC ? coltab[(size_t)k * g.cols + c] : 0.f;
-        s_ec[threadIdx.x] = g.ntrail == 1 ? marg_factor(colfx[c], g.hs_col, (double)g.rows, gden, kappa, eps) : colfac[c];
-    }
-    const float* __restrict__ bql = s_bq + lg * SP_BQS + 64 * wv + li;   // + 4 kc SP_BQS + 16 tc
-    const float* __restrict__ ecl = s_ec + 64 * wv + li;                  // + 16 tc
-    {
-        const float (*const r0[2])[2] = {ctrl->rc[0], ctrl->rc[1]};
-        const float (*const r1[2])[2] = {nullptr, nullptr};
-        const float w0[2] = {1.f, 1.f}, w1[2] = {0.f, 0.f};
-        alpha_rows<RM, KC>(g, meta, s_ar, nr, r0, w0, r1, w1, s_al);   // ends with a barrier
-    }
-    const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
-    const float scale = ctrl->scale;
-    const float mcoup = (float)h.metric_coupling;
-    const float sg = h.maximize ? -1.f : 1.f;
-    const float tm = (float)h.transport_mix;
-    const float hs = (float)ctrl->hs_P;
-    const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
-    const float k2 = -2.8853900817779268f * iclip;   // -2 log2(e) / clip
-    f32x4m zacc[4];
-#pragma unroll
-    for (int tc = 0; tc < 4; ++tc) zacc[tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
-    float m_ee = 0.f, m_t = 0.f, m_tt = 0.f, m_rr = 0.f, m_bb = 0.f, m_oo = 0.f, m_rb = 0.f, m_ro = 0.f,
-          m_bo = 0.f, m_tr = 0.f, m_tb = 0.f, m_to = 0.f;
-    // metric and prediction fields of tile column tc of the current row of tiles
-    float aM[3], aQ[3];
-    auto recon = [&](int tc, f32x4m& lm, f32x4m& pred) {
-        lm = f32x4m{cM, cM, cM, cM};
-        pred = f32x4m{cP, cP, cP, cP};
-#pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
-            const float bq = bql[4 * kc * SP_BQS + 16 * tc];
-            lm = __builtin_amdgcn_mfma_f32_16x16x4f32(aM[kc], bq, lm, 0, 0, 0);
-            pred = __builtin_amdgcn_mfma_f32_16x16x4f32(aQ[kc], bq, pred, 0, 0, 0);
-        }
-    };
-    // A operands of row of tiles tr: alpha_{4 kc + lg}(row 16 tr + li) of both fields
-    auto row_alpha = [&](int tr) {
-        const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
-#pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
-            aM[kc] = alr[4 * kc];
-            aQ[kc] = alr[KP + 4 * kc];
-        }
-    };
-    auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const f32x4m& lm, const f32x4m& pred) {
-        const float ec = ecl[16 * tc];
-        float tvs[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float f = sg * x[r];
-            // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
-            const float M = med3f(fexp(mcoup * med3f(lm[r], -3.0f, 3.0f)), 0.06f, 16.0f);
-            float den = scale * M;
-            den = den * med3f(s_rf[16 * tr + 4 * lg + r] * ec, 0.08f, 12.0f);
-            const float lsum = s_lt[b[r] & 0xffu] + s_lt[B + (b[r] >> 8)];
-            den = den * med3f(fexp(lsum * 0.5f), 0.08f, 12.0f);
-            const float tv = med3f(f * frcp(den + eps), -1.0e4f, 1.0e4f);
-            bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
-            tvs[r] = tv;
-            const float err = tv - pred[r];
-            const float P = err + tm * tv;
-            m_ee += err * err;
-            m_t += tv;
-            m_tt += tv * tv;
-            const float at = fabsf(tv);
-            const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
-            m_rr = fmaf(z.rat, z.rat, m_rr); m_bb = fmaf(z.th, z.th, m_bb); m_oo = fmaf(z.root, z.root, m_oo);
-            m_rb = fmaf(z.rat, z.th, m_rb); m_ro = fmaf(z.rat, z.root, m_ro); m_bo = fmaf(z.th, z.root, m_bo);
-            m_tr = fmaf(at, z.rat, m_tr); m_tb = fmaf(at, z.th, m_tb); m_to = fmaf(at, z.root, m_to);
-            const unsigned long long v = to_fixed_floor(P * hs);
-            atomicAdd(&s_hist[(b[r] & 0xffu) * NH + hc], v);
-            atomicAdd(&s_hist[(B + (b[r] >> 8)) * NH + hc], v);
-        }
-        // A of the projection: a_li(row 16 tr + 4 lg + r)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float aJ = li < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (li < RW ? li : 0)] : 0.f;
-            zacc[tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJ, tvs[r], zacc[tc], 0, 0, 0);
-        }
-        pin1(m_ee); pin1(m_t); pin1(m_tt); pin1(m_rr); pin1(m_bb); pin1(m_oo);
-        pin1(m_rb); pin1(m_ro); pin1(m_bo); pin1(m_tr); pin1(m_tb); pin1(m_to);
-        elem_fence();
-    };
-    const int ntr = nr / 16;
-    f32x4m lmA, prA, lmB, prB;
-    row_alpha(0);
-    recon(0, lmA, prA);
-    for (int tr = 0; tr < ntr; ++tr) {
-        // the fields of tile (tr, tc + 1), or of (tr + 1, 0), go to the matrix
-        // cores before tile (tr, tc)'s element math, which reads the fields
-        // issued one tile earlier
-#pragma unroll
-        for (int tc = 0; tc < 4; ++tc) {
-            if (tc < 3) {
-                recon(tc + 1, lmB, prB);
-            } else if (tr + 1 < ntr) {
-                row_alpha(tr + 1);
-                recon(0, lmB, prB);
-            }
-            tile(tr, tc, xv + 4 * tc, bv + 4 * tc, lmA, prA);
-            if (tr + 1 < ntr) load_tile(tr + 1, tc);
-            lmA = lmB;
-            prA = prB;
-        }
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < TB; i += SP_NT) {
-        unsigned long long v = 0ull;
-#pragma unroll
-        for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-        if (v) atomicAdd(&hist[i], v);
-    }
-    Partials P{red, 15 + 2 * g.R, NV3};
-    const float mm[13] = {m_ee, 0.f, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
-#pragma unroll
-    for (int k = 0; k < 13; ++k) P.add(k, mm[k]);
-    P.add(13, 0.f);
-    P.add(14, 0.f);
-    // projection: lane group lg holds Z_{4 lg + j}(col), j < 4, i.e. both
-    // components of modes 2 lg and 2 lg + 1, for its 4 columns; each mode's raw
-    // C/S (proj_finish's form) is summed over the columns, then over the 16
-    // lanes of the group, into slots 15 + 4 lg + j.
-    float cs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        const int r = 2 * lg + half;
-        if (r < g.R) {
-            const ModeMeta m = meta[r];
-#pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
-                const int64_t c = colw + 16 * tc + li;
-                // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
-                const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
-                const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
-                const float z1 = zacc[tc][2 * half], z2 = zacc[tc][2 * half + 1];
-                if (m.type == M_ADD) {
-                    cs[2 * half] += b1 * z1 - b2 * z2;
-                    cs[2 * half + 1] += b1 * z2 + b2 * z1;
-                } else {
-                    cs[2 * half] += b1 * z1;
-                    cs[2 * half + 1] += b2 * z2;
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float s = row16_total(cs[j]);
-        const int slot = 4 * lg + j;
-        if (li == 15 && slot < 2 * g.R) red[wv * P.V + 15 + slot] = s;
-    }
-    P.flush(part);
-}
-
-// ---------------------------------------------------------------------------
-// F3: surprise, hash impulse, confidence, contact, and every drive-shaping
-// coefficient that does not need the hash prediction's rms
-// ---------------------------------------------------------------------------
-// Contact oscillator of one bank (cresso_v5.py:914-943), lane r = mode r; the
-// energy and power sums over modes are summed in mode order.
-__device__ void contact_bank_lanes(float& q, float& p, float port, float omega, float& calcium, float& action, float S,
-                                   int R, const cresso_hyper& h) {
-    const int r = threadIdx.x & 63;
-    const bool on = r < R;
-    const float dt = (float)h.dt;
-    const float rd = (float)h.refractory_decay;
-    const float plast = 1.0f + (float)h.surprise_gain * S / (1.0f + S);
-    const float brake = 1.0f / (1.0f + (float)h.surprise_brake * S);
-    float gp = 0.f;
-    double e1 = 0.0, e2 = 0.0, pw = 0.0;
-    if (on) {
-        calcium = calcium * rd + (float)(1.0 - h.refractory_decay) * fabsf(port);
-        const float gate = 1.0f / (1.0f + (float)h.refractory_gain * calcium);
-        gp = port * gate * plast * brake;
-        e1 = (double)(p * p);
-        const float oq = omega * q;
-        e2 = (double)(oq * oq);
-        pw = (double)(gp * p);
-    }
-    const double E1 = lanes_sum(e1, R), E2 = lanes_sum(e2, R), PW = lanes_sum(pw, R);
-    if (R > 0) {
-        const float energy = 0.5f * ((float)(E1 / R) + (float)(E2 / R));
-        const float power = (float)(PW / R);
-        action = action * 0.985f + dt * (power - energy);
-    }
-    const float fric = (float)h.impulse_friction + (float)h.contact_gain * tanhf(fabsf(action));
-    const float damp = fmaxf(1.0f - dt * fric, 0.0f);
-    if (on) {
-        float pr = p * damp;
-        const float qq = q;
-        pr = pr + dt * (gp - (float)h.restoring * (omega * omega) * qq - (float)h.cubic * (qq * qq * qq));
-        p = pr;
-        q = clampf(qq + dt * pr, -8.0f, 8.0f);
-    }
-}
-
-// The drive (cresso_v5.py:1303-1353) is
-//   c0 core + c1 pred' + c2 nov + c3 err' + c4 echo + c5 hash
-// with core = cr rat + cb bnd + co root + ct t.  Every c except c5 depends on
-// rms values that are closed forms of this step's sweep-3 sums:
-//   * mean(core^2): a quadratic form in the 13 moments of t;
-//   * mean(pred'^2), mean(echo^2): u^T G u over the Gram matrix G of the
-//     normalized basis (pred' and echo are reconstructions with weights u);
-//   * mean(t pred') = sum_v u'_v mean(t Xn_v) (the t projection);
-//   * mean(err'^2) = mean(err^2) - 2 mean(err D) + mean(D^2), D = pred' - pred
-//     a reconstruction with weights du = u' - u, mean(err Xn_v) =
-//     mean(t Xn_v) - (G u)_v: small corrections to a directly summed term.
-// So sweep 4 can write the drive without c5; the hash term's rms comes from
-// sweep 4's sums and is added in sweep 5.
-__global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                        const double* __restrict__ stats, const double* __restrict__ gram,
-                                                        const double* __restrict__ part,
-                                                        unsigned long long* __restrict__ hist,
-                                                        const unsigned long long* __restrict__ counts,
-                                                        float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
-                                                        const unsigned long long* __restrict__ cooc, int step, int hash_on,
-                                                        int hard, int echo_on, int c5_closed, cresso_hyper h) {
-    if (threadIdx.x == 0) ctrl->de_prev = *st.drive_energy;   // every block of sweep 5 reads the old value
-    __shared__ double s_m[NV3];
-    __shared__ double s_ec[2 * SP_MAXR];    // mean(t Xn_v)
-    __shared__ double s_u[3][2 * SP_MAXR];  // weights of pred, pred', echo
-    __shared__ float s_wp[2 * SP_MAXR], s_we[2 * SP_MAXR];
-    __shared__ float s_tmpf[64];
-    const int tid = threadIdx.x;
-    const double n = (double)g.n;
-    const int R = g.R, V = 2 * g.R;
-    // everything the mode lanes read, staged in LDS by all threads (global
-    // loads in flight together instead of one round trip per use)
-    __shared__ double s_gram[4 * SP_MAXR * SP_MAXR];
-    __shared__ double s_stats[4 * SP_MAXR];
-    __shared__ float s_mode[SP_MAXR][9];
-    __shared__ float s_scal[2];
-    __shared__ float s_impv[2 * 256];
-    __shared__ double s_hhw[SP_FN_NT / 64];
-    __shared__ float s_srms;
-    for (int i = tid; i < V * V; i += SP_FN_NT) s_gram[i] = gram[i];
-    for (int i = tid; i < 4 * R; i += SP_FN_NT) s_stats[i] = stats[i];
-    for (int i = tid; i < 9 * R; i += SP_FN_NT) {
-        const int r = i / 9, j = i - 9 * r;
-        const float* src[8] = {st.omega, st.q_cos, st.q_sin, st.p_cos, st.p_sin, st.calcium_cos, st.calcium_sin, st.conf};
-        s_mode[r][j] = j < 8 ? src[j][r] : 0.f;
-    }
-    for (int i = tid; i < V; i += SP_FN_NT) s_u[0][i] = (double)ctrl->wpred[i];
-    if (tid == 0) {
-        s_scal[0] = *st.surprise;
-        s_scal[1] = *st.action;
-    }
-    load_sums(part, 15 + 2 * R, s_m);
-    const float eps = (float)h.eps;
-    // hash refractory / impulse (cresso_v5.py:1140-1184)
-    if (hash_on) {
-        const int TB = g.T * g.B;
-        for (int i = tid; i < TB; i += SP_FN_NT) {
-            const double cnt = fmax((double)counts[i], 1.0);
-            const float cp = (float)((double)(long long)hist[i] / ctrl->hs_P / cnt);
-            hist[i] = 0ull;
-            const float ref = st.hash_refractory[i] * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * fabsf(cp);
-            const float gate = 1.0f / (1.0f + (float)h.refractory_gain * ref);
-            const float im = st.hash_impulse[i] * (float)h.hash_impulse_decay + (float)(1.0 - h.hash_impulse_decay) * (cp * gate);
-            st.hash_refractory[i] = ref;
-            st.hash_impulse[i] = im;
-            imp_tab[i] = im;
-            if (c5_closed) s_impv[i] = im;
-        }
-    }
-    if (c5_closed) __syncthreads();   // s_impv complete
-    __shared__ double s_gu[2 * SP_MAXR];     // G u_pred: mean(pred Xn_v)
-    if (tid < 64) {
-        const int r = tid;
-        const bool on = r < R;
-        const double sT = s_m[2];
-        // surprise reservoir (cresso_v5.py:1127-1129)
-        const float sur = reservoir_f(s_scal[0], sqrtf((float)(s_m[0] / n) + eps), h.surprise_decay, step);
-        // t projections mean(t Xn) in fp64
-        float ecs = 0.f, ess = 0.f;
-        if (on) {
-            const double mc = s_stats[4 * r], ic = s_stats[4 * r + 1], ms = s_stats[4 * r + 2], is = s_stats[4 * r + 3];
-            const double ecd = (s_m[15 + 2 * r] - mc * sT) * ic / n;
-            const double esd = (s_m[16 + 2 * r] - ms * sT) * is / n;
-            ecs = (float)ecd;
-            ess = (float)esd;
-            s_ec[2 * r] = ecd;
-            s_ec[2 * r + 1] = esd;
-        }
-        // mean(pred Xn_v) = (G u_pred)_v, lane v = carrier v
-        if (r < V) {
-            double gu = 0.0;
-            for (int w = 0; w < V; ++w) gu += s_gram[r * V + w] * s_u[0][w];
-            s_gu[r] = gu;
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-        // port projections (cresso_v5.py:1136): P = err + tm t = (1 + tm) t - pred
-        float pc = 0.f, ps = 0.f;
-        if (on) {
-            const double k1 = 1.0 + (double)(float)h.transport_mix;
-            pc = (float)(k1 * s_ec[2 * r] - s_gu[2 * r]);
-            ps = (float)(k1 * s_ec[2 * r + 1] - s_gu[2 * r + 1]);
-        }
-        float om = 0.f, qc = 0.f, qs = 0.f, pcv = 0.f, psv = 0.f, cac = 0.f, cas = 0.f, conf = 0.f;
-        if (on) {
-            om = s_mode[r][0]; qc = s_mode[r][1]; qs = s_mode[r][2]; pcv = s_mode[r][3]; psv = s_mode[r][4];
-            cac = s_mode[r][5]; cas = s_mode[r][6]; conf = s_mode[r][7];
-        }
-        // confidence (cresso_v5.py:1199-1202) with the pre-contact q
-        float gt = 0.f;
-        if (on) {
-            const float pe = sqrtf(pc * pc + ps * ps + eps);
-            const float sup = (pc * qc + ps * qs) / (pe * sqrtf(qc * qc + qs * qs + eps) + eps);
-            const float c = conf * (float)h.confidence_decay + (float)(1.0 - h.confidence_decay) * clampf(sup, -1.0f, 1.0f);
-            conf = clampf(c, -4.0f, 4.0f);
-            gt = sigmoidf_((float)h.confidence_gain * conf);
-        }
-        // contact on the cos bank then the sin bank with the shared action
-        float action = s_scal[1];
-        contact_bank_lanes(qc, pcv, pc, om, cac, action, sur, R, h);
-        contact_bank_lanes(qs, psv, ps, om, cas, action, sur, R, h);
-        set_recon_lanes(g, s_stats, ctrl->rc[2], &ctrl->rconst[2], qc, qs, gt, s_tmpf, s_wp);
-        if (echo_on) set_recon_lanes(g, s_stats, ctrl->rc[3], &ctrl->rconst[3], ecs, ess, 1.0f, s_tmpf, s_we);
-        if (on) {
-            st.q_cos[r] = qc; st.q_sin[r] = qs; st.p_cos[r] = pcv; st.p_sin[r] = psv;
-            st.calcium_cos[r] = cac; st.calcium_sin[r] = cas; st.conf[r] = conf;
-            s_u[1][2 * r] = (double)s_wp[2 * r];
-            s_u[1][2 * r + 1] = (double)s_wp[2 * r + 1];
-            s_u[2][2 * r] = echo_on ? (double)s_we[2 * r] : 0.0;
-            s_u[2][2 * r + 1] = echo_on ? (double)s_we[2 * r + 1] : 0.0;
-        }
-        if (r == 0) {
-            *st.surprise = sur;
-            *st.action = action;
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-        // Gram products, lane v = carrier v (v < 2R <= 32)
-        double q0 = 0.0, q1 = 0.0, q2 = 0.0, q3 = 0.0, q4 = 0.0;
-        if (r < V) {
-            const int v = r;
-            const double gu = s_gu[v];
-            double gup = 0.0, gue = 0.0;
-            for (int w = 0; w < V; ++w) {
-                const double gvw = s_gram[v * V + w];
-                gup += gvw * s_u[1][w];
-                gue += gvw * s_u[2][w];
-            }
-            const double du = s_u[1][v] - s_u[0][v];
-            q0 = s_u[1][v] * gup;        // -> mean(pred'^2)
-            q1 = s_u[2][v] * gue;        // -> mean(echo^2)
-            q2 = du * (gup - gu);        // -> mean(D^2)
-            q3 = du * (s_ec[v] - gu);    // -> mean(err D)
-            q4 = s_u[1][v] * s_ec[v];    // -> mean(t pred')
-        }
-        const double Q0 = lanes_sum(q0, V), Q1 = lanes_sum(q1, V), Q2 = lanes_sum(q2, V);
-        const double Q3 = lanes_sum(q3, V), Q4 = lanes_sum(q4, V);
-        if (r == 0) {
-            const float S = sur;
-            // shaped / core coefficients from the moments of t (cresso_v5.py:1315-1337)
-            // sweep 3 sums |tanh| where the moments use bnd = clip tanh
-            const double cl = (double)(float)h.drive_clip;
-            const double Stt = s_m[3], Srr = s_m[4], Sbb = s_m[5] * cl * cl, Soo = s_m[6], Srb = s_m[7] * cl;
-            const double Sro = s_m[8], Sbo = s_m[9] * cl;
-            const double Str = s_m[10], Stb = s_m[11] * cl, Sto = s_m[12];
-            const float frms = sqrtf((float)(Stt / n) + eps);
-            const float rms_rat = sqrtf((float)(Srr / n) + eps);
-            const float rms_root = sqrtf((float)(Soo / n) + eps);
-            const float kroot = rms_rat / fmaxf(rms_root, eps);
-            const float spike = (float)h.spike_mix / (1.0f + S);
-            const float rmix = (hard ? (float)h.root_channel_mix : 0.0f) / (1.0f + 0.5f * S);
-            const double ar = (double)((1.0f - rmix) * (1.0f - spike));
-            const double ab = (double)((1.0f - rmix) * spike);
-            const double ao = (double)(rmix * kroot);
-            const double sh2 = ar * ar * Srr + ab * ab * Sbb + ao * ao * Soo + 2.0 * (ar * ab * Srb + ar * ao * Sro + ab * ao * Sbo);
-            const float srms = sqrtf((float)(sh2 / n) + eps);
-            const float dmix = (float)h.direct_force_mix / (1.0f + 0.35f * S);
-            const float kdir = srms / fmaxf(frms, eps);
-            const double cr = (1.0 - (double)dmix) * ar, cb = (1.0 - (double)dmix) * ab, co = (1.0 - (double)dmix) * ao;
-            const double ct = (double)(dmix * kdir);
-            const double core2 = cr * cr * Srr + cb * cb * Sbb + co * co * Soo + ct * ct * Stt +
-                                 2.0 * (cr * cb * Srb + cr * co * Sro + cb * co * Sbo + ct * cr * Str + ct * cb * Stb + ct * co * Sto);
-            // alignment gate and prediction mix (cresso_v5.py:1303-1313)
-            const float prms = sqrtf((float)Q0 + eps);
-            const float align = clampf((float)Q4 / (frms * prms + eps), -1.0f, 1.0f);
-            float agate = clampf((align + 1.0f) * 0.5f, 0.0f, 1.0f);
-            if (!(prms > (float)sqrt(h.eps))) agate = 0.0f;
-            const double warm = h.warmup_steps == 0 ? 1.0 : 1.0 - exp(-(double)step / (double)(h.warmup_steps > 1 ? h.warmup_steps : 1));
-            const float mix = (float)(h.prediction_mix * warm) * agate * (1.0f / (1.0f + S));
-            // residual feedback: err' rms from the directly summed err rms and the Gram corrections
-            const float crms = sqrtf((float)(core2 / n) + eps);
-            const double ee = fmax(s_m[0] / n - 2.0 * Q3 + Q2, 0.0);
-            const float erms = sqrtf((float)ee + eps);
-            const float kres = crms / fmaxf(erms, eps);
-            const float resmix = (float)h.residual_feedback_mix / (1.0f + S);
-            float kecho = 0.f;
-            if (hard && echo_on) kecho = srms / fmaxf(sqrtf((float)Q1 + eps), eps);
-            const double c0 = 1.0 - (double)mix, c1 = mix, c2 = h.novelty_mix, c3 = (double)(resmix * kres);
-            const double c4 = hard ? h.echo_mix * (double)kecho : 0.0;
-            const float clip = (float)h.drive_clip;
-            // drive without the hash term:
-            //   c0 cr rat + c0 cb clip tanh + c0 co root + (c0 ct + c3) t + (c1 - c3) pred' + c4 echo + c2 clip tanh(err' ns)
-            ctrl->k_rat = (float)(c0 * cr);
-            ctrl->k_ths = (float)(c0 * cb * (double)clip);
-            ctrl->k_root = (float)(c0 * co);
-            ctrl->k_t = (float)(c0 * ct + c3);
-            ctrl->k_pred = (float)(c1 - c3);
-            ctrl->k_echo = (float)c4;
-            ctrl->k_nov = (float)(c2 * (double)clip);
-            ctrl->nscale = 1.0f / (clip * (1.0f + S));
-            ctrl->srms = srms;
-            s_srms = srms;
-        }
-    } else if (c5_closed) {
-        // waves 1.. (while wave 0 runs the mode lanes): the hash prediction's
-        // sum of squares over the field, sum_i ((imp0[b0] + imp1[b1]) / 2)^2,
-        // in closed form from the bin and co-occurrence counts
-        const int B = g.B;
-        const int t1 = tid - 64, n1 = SP_FN_NT - 64;
-        double a = 0.0;
-        for (int k = t1; k < B * B; k += n1)
-            a += (double)cooc[k] * (2.0 * (double)s_impv[k / B] * (double)s_impv[B + k % B]);
-        for (int k = t1; k < 2 * B; k += n1) a += (double)counts[k] * ((double)s_impv[k] * (double)s_impv[k]);
-        const double w = wave_total_d(a);
-        if ((tid & 63) == 63) s_hhw[(tid >> 6) - 1] = w;
-    }
-    if (c5_closed) {
-        __syncthreads();
-        if (tid == 0) {
-            double hh = 0.0;
-            for (int w = 0; w < SP_FN_NT / 64 - 1; ++w) hh += s_hhw[w];
-            hh *= 0.25;
-            // the hash term's coefficient as fin4_values forms it, from sum hp^2
-            const float khp = s_srms / fmaxf(sqrtf((float)(hh / n) + eps), eps);
-            ctrl->k_hash = (float)(hard ? h.hash_drive_mix * (double)khp : 0.0);
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// S4: drive without the hash term, written over t; sums for the drive energy
-// ---------------------------------------------------------------------------
-template <int RM, int KC, int MODE>
-__global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
-    Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
-    const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
-    float* __restrict__ tbuf, double* __restrict__ part, int hash_arg, int echo_on, cresso_hyper h) {
-    extern __shared__ __align__(16) unsigned char dyn[];
-    __shared__ float red[4 * NV4];
-    const SweepFlags F = sweep_flags<MODE>(g, hash_arg, 1, h);
-    const Tile t = tile_of(g);
-    const int B = g.B;
-    const int TB = F.T * B;
-    const int nr = (int)(t.r1 - t.r0);
-    // LDS: impulse table [T][B] | row coefficients [PR][2][KP] of pred' (set 0)
-    // and of k_pred pred' + k_echo echo (set 1), 16-byte aligned | row factors [PR][2 RM]
-    constexpr int KP = kcp<KC>();
-    float* s_imp = reinterpret_cast<float*>(dyn);
-    float* s_al = reinterpret_cast<float*>(dyn + ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15));
-    float* s_rows = s_al + 2 * KP * g.PR;   // the block's row factors [PR][2 RM]
-    stage_rows<RM>(g, rowtab, t.r0, nr, s_rows);
-    if (F.hash_on)
-        for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
-    const float kp = ctrl->k_pred, ke = ctrl->k_echo;
-    float bc[KC];
-    load_cols<KC>(g, coltab, t, bc);
-    {
-        const float (*const r0[2])[2] = {ctrl->rc[2], ctrl->rc[2]};
-        const float (*const r1[2])[2] = {nullptr, echo_on ? ctrl->rc[3] : nullptr};
-        const float w0[2] = {1.f, kp}, w1[2] = {0.f, ke};
-        alpha_rows<RM, KC>(g, meta, s_rows, nr, r0, w0, r1, w1, s_al);
-    }
-    const float cQ = ctrl->rconst[2];
-    const float cX = kp * ctrl->rconst[2] + (echo_on ? ke * ctrl->rconst[3] : 0.f);
-    __syncthreads();
-    const int64_t base = panel_base(g, t);
-    float* __restrict__ tb = tbuf + base;
-    const float eps = (float)h.eps;
-    const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
-    const float k_rat = ctrl->k_rat, k_ths = ctrl->k_ths, k_root = ctrl->k_root, k_t = ctrl->k_t, k_nov = ctrl->k_nov;
-    const float k2 = -2.8853900817779268f * iclip;            // -2 log2(e) / clip
-    const float k2n = -2.8853900817779268f * ctrl->nscale;    // tanh(err' nscale)
-    const float invT = 1.0f / (float)F.T;
-    float a_dd = 0.f, a_dh = 0.f, a_hh = 0.f;
-    PanelBuf tbv, bnv;
-    if (MODE == 1) {
-        tbv = panel_buf(tb, g, nr);
-        bnv = panel_buf(reinterpret_cast<const uint16_t*>(bins) + base, g, nr);
-    }
-    // one row of the lane's column: t -> drive without the hash term (stored over t)
-    auto row = [&](int lr, float tv, uint64_t bval) {
-        const float* __restrict__ al = s_al + lr * (2 * KP);
-        float pred = cQ, mixed = cX;
-#pragma unroll
-        for (int k = 0; k < KC; ++k) {
-            pred = fmaf(al[k], bc[k], pred);
-            mixed = fmaf(al[KP + k], bc[k], mixed);
-        }
-        const float err = tv - pred;
-        const float nov = ftanh_k(err, k2n);
-        const float at = fabsf(tv);
-        const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
-        const float core = xorsign(fmaf(k_t, at, fmaf(k_root, z.root, fmaf(k_ths, z.th, k_rat * z.rat))), tv);
-        const float d = fmaf(k_nov, nov, core + mixed);
-        if (MODE == 1)
-            stb_lane(tbv, lr, d);
-        else
-            tb[panel_off(g, lr)] = d;
-        a_dd = fmaf(d, d, a_dd);
-        if (F.hash_on) {
-            float hp = 0.f;
-#pragma unroll
-            for (int tt = 0; tt < SP_MAXT; ++tt) {
-                if (tt >= F.T) break;
-                hp += s_imp[tt * B + bin_of(bval, tt, F.bpb)];
-            }
-            hp = hp * invT;
-            a_dh = fmaf(d, hp, a_dh);
-            a_hh = fmaf(hp, hp, a_hh);
-        }
-        if (MODE == 1) {
-            pin1(a_dd); pin1(a_dh); pin1(a_hh);
-        }
-        elem_fence();
-    };
-    if constexpr (MODE == 1) {
-        float x0[SP_U];
-        uint32_t b0[SP_U];
-#pragma unroll
-        for (int u = 0; u < SP_U; ++u) {
-            x0[u] = ldb_lane<float>(tbv, u);
-            b0[u] = ldb_bins16(bnv, u);
-        }
-        pipelined_rows<SP_U>(
-            nr,
-            [&](int lr, float& x, uint32_t& b) {
-                x = ldb_lane<float>(tbv, lr);
-                b = ldb_bins16(bnv, lr);
-            },
-            [&](int lr, float x, uint32_t b) { row(lr, x, b); }, x0, b0);
-    } else if (t.colok) {
-        for (int i0 = 0; i0 < nr; i0 += SP_U) {
-            float tvs[SP_U];
-            uint64_t bv[SP_U];
-#pragma unroll
-            for (int u = 0; u < SP_U; ++u) {
-                tvs[u] = 0.f;
-                bv[u] = 0;
-                if (i0 + u < nr) {
-                    const uint32_t o = panel_off(g, i0 + u);
-                    tvs[u] = tb[o];
-                    if (F.hash_on) bv[u] = load_bins_at(bins, base, o, F.binbytes);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < SP_U; ++u) {
-                if (i0 + u >= nr) break;
-                row(i0 + u, tvs[u], bv[u]);
-            }
-        }
-    }
-    Partials P{red, 3, NV4};
-    P.add(0, a_dd);
-    P.add(1, a_dh);
-    P.add(2, a_hh);
-    P.flush(part);
-}
-
-// ---------------------------------------------------------------------------
-// S4 on the matrix cores (MODE 1 tiles).  Each wave owns 64 columns of the
-// panel as 4 x 4 tiles of 16 x 16 elements.  A reconstruction of a tile is
-// 3 MFMAs (v_mfma_f32_16x16x4f32, the K = KC carriers in chunks of 4):
-//   A[i][k] = alpha_{4kc+k}(row i)   lane l supplies i = l % 16, k = l / 16
-//   B[k][j] = b_{4kc+k}(col j)       lane l supplies j = l % 16, k = l / 16
-//   D[i][j]                          lane l, register r: i = 4 (l / 16) + r, j = l % 16
-// so lane l processes rows 4 (l/16) + r of column l % 16 of each tile, and the
-// elementwise drive math is unchanged.  The loads of the next tile are in
-// flight while a tile is processed.  The hash term's coefficient c5 is known
-// here (fin3 forms the hash prediction's RMS from the co-occurrence counts),
-// so the full drive is written and sum drive^2 is summed directly.
-// ---------------------------------------------------------------------------
-template <int RM, int KC>
-__global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
-    Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
-    const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
-    float* __restrict__ tbuf, double* __restrict__ part, int echo_on, cresso_hyper h) {
-    static_assert(KC <= 12, "three K-chunks of four carriers");
-    extern __shared__ __align__(16) unsigned char dyn[];
-    __shared__ float red[4 * NV4];
-    const Tile t = tile_of(g);
-    const int B = g.B;
-    const int TB = 2 * B;
-    const int nr = g.PR;
-    constexpr int KP = kcp<KC>();
-    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int li = l & 15, lg = l >> 4;
-    const int64_t base = panel_base(g, t);
-    float* __restrict__ tb = tbuf + base;
-    const uint32_t cols = (uint32_t)g.cols;
-    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tb, (uint32_t)((int64_t)nr * g.cols * 4));
-    const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(reinterpret_cast<const uint16_t*>(bins) + base, (uint32_t)((int64_t)nr * g.cols * 2));
-    const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
-    const uint32_t vt = lane_el * 4u, vb = lane_el * 2u;
-    // tile (tr, tc), lane element r: panel element (16 tr + 4 lg + r, 64 wv + 16 tc + li)
-    auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
-    // A row of tiles (4 tiles x 4 elements) is in flight while the previous row
-    // is processed; the first row's loads go out before the block's set-up, so
-    // that memory is busy during it.
-    float xa[16], xb[16];
-    uint32_t ba[16], bb[16];
-    auto load_row = [&](int tr, float* x, uint32_t* b) {
-#pragma unroll
-        for (int tc = 0; tc < 4; ++tc)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t o = tile_off(tr, tc, r);
-                x[4 * tc + r] = bload1(rt, vt, o * 4u);
-                b[4 * tc + r] = bload1u16(rb, vb, o * 2u);
-            }
-    };
-    load_row(0, xa, ba);
-    float* s_imp = reinterpret_cast<float*>(dyn);
-    float* s_al = reinterpret_cast<float*>(dyn + ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15));
-    float* s_rows = s_al + 2 * KP * g.PR;   // the block's row factors [PR][2 RM]
-    stage_rows<RM>(g, rowtab, t.r0, nr, s_rows);
-    // B operands: carriers 4 kc + lg of the lane's column in each column tile
-    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
-    float bq[4][3];
-#pragma unroll
-    for (int tc = 0; tc < 4; ++tc)
-#pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
-            const int k = 4 * kc + lg;
-            bq[tc][kc] = k < KC ? coltab[(size_t)k * g.cols + colw + 16 * tc + li] : 0.f;
-        }
-    for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
-    const float kp = ctrl->k_pred, ke = ctrl->k_echo;
-    {
-        const float (*const r0[2])[2] = {ctrl->rc[2], ctrl->rc[2]};
-        const float (*const r1[2])[2] = {nullptr, echo_on ? ctrl->rc[3] : nullptr};
-        const float w0[2] = {1.f, kp}, w1[2] = {0.f, ke};
-        alpha_rows<RM, KC>(g, meta, s_rows, nr, r0, w0, r1, w1, s_al);
-    }
-    const float cQ = ctrl->rconst[2];
-    const float cX = kp * ctrl->rconst[2] + (echo_on ? ke * ctrl->rconst[3] : 0.f);
-    __syncthreads();
-    const float eps = (float)h.eps;
-    const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
-    const float k_rat = ctrl->k_rat, k_ths = ctrl->k_ths, k_root = ctrl->k_root, k_t = ctrl->k_t, k_nov = ctrl->k_nov;
-    const float k2 = -2.8853900817779268f * iclip;
-    const float k2n = -2.8853900817779268f * ctrl->nscale;
-    const float c5 = ctrl->k_hash;   // set by fin3 (closed-form hash-term RMS)
-    float a_dd = 0.f;
-    auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const float* aP, const float* aX) {
-        f32x4m pred = {cQ, cQ, cQ, cQ}, mixed = {cX, cX, cX, cX};
-#pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
-            pred = __builtin_amdgcn_mfma_f32_16x16x4f32(aP[kc], bq[tc][kc], pred, 0, 0, 0);
-            mixed = __builtin_amdgcn_mfma_f32_16x16x4f32(aX[kc], bq[tc][kc], mixed, 0, 0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float tv = x[r];
-            const float err = tv - pred[r];
-            const float nov = ftanh_k(err, k2n);
-            const float at = fabsf(tv);
-            const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
-            const float core = xorsign(fmaf(k_t, at, fmaf(k_root, z.root, fmaf(k_ths, z.th, k_rat * z.rat))), tv);
-            const float hp = (s_imp[b[r] & 0xffu] + s_imp[B + (b[r] >> 8)]) * 0.5f;
-            const float d = fmaf(c5, hp, fmaf(k_nov, nov, core + mixed[r]));
-            bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
-            a_dd = fmaf(d, d, a_dd);
-        }
-        pin1(a_dd);
-        elem_fence();
-    };
-    auto row_tiles = [&](int tr, const float* x, const uint32_t* b) {
-        // A operands of this row of tiles: alpha_{4 kc + lg}(row 16 tr + li)
-        const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
-        float aP[3], aX[3];
-#pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
-            aP[kc] = alr[4 * kc];
-            aX[kc] = alr[KP + 4 * kc];
-        }
-#pragma unroll
-        for (int tc = 0; tc < 4; ++tc) tile(tr, tc, x + 4 * tc, b + 4 * tc, aP, aX);
-    };
-    const int ntr = nr / 16;   // even: PR is a multiple of 32 on this path
-    for (int tr = 0; tr < ntr; tr += 2) {
-        load_row(tr + 1, xb, bb);
-        row_tiles(tr, xa, ba);
-        if (tr + 2 < ntr) load_row(tr + 2, xa, ba);
-        row_tiles(tr + 1, xb, bb);
-    }
-    Partials P{red, 3, NV4};
-    P.add(0, a_dd);
-    P.add(1, 0.f);
-    P.add(2, 0.f);
-    P.flush(part);
-}
-
-// F4, in every block of sweep 5: sweep 4's block partials summed in a fixed
-// order (so every block gets the same values), then the hash-term
-// coefficient, the drive-energy reservoir and the gain.  Block 0 stores the
-// new drive energy; the reservoir starts from ctrl->de_prev (stashed by fin3),
-// so no block reads a value another block of this launch wrote.
-//   sum drive^2 = sum d^2 + 2 c5 sum d hp + c5^2 sum hp^2
-__device__ void fin4_values(const Geom& g, const double* __restrict__ part, const Ctrl* __restrict__ ctrl,
-                            float* __restrict__ de_state, int step, int hash_on, int hard, int c5_closed,
-                            const cresso_hyper& h, float& gain, float& c5f) {
-    __shared__ double s_w[SP_NT / 64][NV4];
-    double acc[NV4] = {0.0, 0.0, 0.0};
-    for (int b = threadIdx.x; b < g.nblk; b += SP_NT)
-#pragma unroll
-        for (int v = 0; v < NV4; ++v) acc[v] += part[(size_t)v * g.nblk + b];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int v = 0; v < NV4; ++v) {
-        const double w = wave_total_d(acc[v]);
-        if (lane == 63) s_w[wave][v] = w;
-    }
-    __syncthreads();
-    double m[NV4];
-#pragma unroll
-    for (int v = 0; v < NV4; ++v) {
-        m[v] = 0.0;
-        for (int w = 0; w < SP_NT / 64; ++w) m[v] += s_w[w][v];
-    }
-    const double n = (double)g.n;
-    const float eps = (float)h.eps;
-    double c5, dd;
-    if (c5_closed) {
-        // sweep 4 summed the full drive (the hash term's coefficient came from fin3)
-        c5 = (double)ctrl->k_hash;
-        dd = m[0];
-    } else {
-        float khp = 0.f;
-        if (hard && hash_on) khp = ctrl->srms / fmaxf(sqrtf((float)(m[2] / n) + eps), eps);
-        c5 = hard ? h.hash_drive_mix * (double)khp : 0.0;
-        dd = m[0] + 2.0 * c5 * m[1] + c5 * c5 * m[2];
-    }
-    const float de_now = (float)(fmax(dd, 0.0) / n);
-    const float de = reservoir_f(ctrl->de_prev, de_now, h.reservoir_decay, step);
-    if (blockIdx.x == 0 && threadIdx.x == 0) *de_state = de;
-    c5f = (float)c5;
-    gain = clampf((float)h.target_update_rms / sqrtf(de + eps), (float)h.min_gain, (float)h.max_gain);
-}
-
-// ---------------------------------------------------------------------------
-// S5: parameter update, param -= lr * cast(drive * gain) (cresso_v5.py:1353)
-// ---------------------------------------------------------------------------
-template <typename PT>
-__device__ __forceinline__ void apply1(PT* __restrict__ param, int64_t e, float drive, float gain, float nlr) {
-    const float u = to_f(from_w<PT>(drive * gain));
-    param[e] = from_w<PT>(to_f(param[e]) + nlr * u);
-}
-
-template <typename PT, bool HASH, bool V4>
-__global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ param, const float* __restrict__ dbuf,
-                                                       const unsigned char* __restrict__ bins,
-                                                       const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
-                                                       const double* __restrict__ part, float* __restrict__ de_state,
-                                                       int step, int hash_on, int hard, int c5_closed, cresso_hyper h) {
-    extern __shared__ __align__(16) unsigned char dyn[];
-    const int64_t beg = (int64_t)blockIdx.x * g.chunk1;
-    const int64_t end = beg + g.chunk1 < g.n ? beg + g.chunk1 : g.n;
-    // chunks are multiples of 4 elements: float4 drive loads (param 4-element aligned)
-    const int64_t vend = V4 ? beg + ((end - beg) & ~(int64_t)3) : beg;
-    const int64_t st = 4 * (int64_t)SP_NT;
-    int64_t e = beg + 4 * (int64_t)threadIdx.x;
-    // the first two float4 of drive and param go out before the gain is known
-    // (their loads stay in flight through the finish's reduction)
-    const bool pre = e + st < vend;
-    float4 d0 = make_float4(0.f, 0.f, 0.f, 0.f), d1 = d0;
-    float p0[4] = {0.f, 0.f, 0.f, 0.f}, p1[4] = {0.f, 0.f, 0.f, 0.f};
-    if (pre) {
-        d0 = *reinterpret_cast<const float4*>(dbuf + e);
-        d1 = *reinterpret_cast<const float4*>(dbuf + e + st);
-        Ld4<PT>::go(param, e, p0);
-        Ld4<PT>::go(param, e + st, p1);
-    }
-    float gain, c5;
-    fin4_values(g, part, ctrl, de_state, step, hash_on, hard, c5_closed, h, gain, c5);
-    const int TB = g.T * g.B;
-    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
-    float* s_imp = reinterpret_cast<float*>(dyn);
-    if (HASH) {
-        for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
-        __syncthreads();
-    }
-    const float kh = c5 * (1.0f / (float)T);
-    const float nlr = (float)(-h.lr);
-    auto drive_at = [&](int64_t e, float d) -> float {
-        if (!HASH) return d;
-        const uint64_t pk = load_bins(bins, e, binbytes);
-        float hp = 0.f;
-#pragma unroll
-        for (int tt = 0; tt < SP_MAXT; ++tt) {
-            if (tt >= T) break;
-            hp += s_imp[tt * B + bin_of(pk, tt, bpb)];
-        }
-        return d + kh * hp;
-    };
-    auto apply4 = [&](int64_t e, const float4& d4, const float* pv) {
-        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-        float o[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float u = to_f(from_w<PT>(drive_at(e + c, dv[c]) * gain));
-            o[c] = pv[c] + nlr * u;
-        }
-        St4<PT>::go(param, e, o);
-    };
-    // two float4 of drive and param per thread in flight per iteration, then the rest
-    if (pre) {
-        apply4(e, d0, p0);
-        apply4(e + st, d1, p1);
-        e += 2 * st;
-    }
-    for (; e + st < vend; e += 2 * st) {
-        const float4 da = *reinterpret_cast<const float4*>(dbuf + e);
-        const float4 db = *reinterpret_cast<const float4*>(dbuf + e + st);
-        float pa[4], pb[4];
-        Ld4<PT>::go(param, e, pa);
-        Ld4<PT>::go(param, e + st, pb);
-        apply4(e, da, pa);
-        apply4(e + st, db, pb);
-    }
-    for (; e < vend; e += st) {
-        const float4 d4 = *reinterpret_cast<const float4*>(dbuf + e);
-        float pv[4];
-        Ld4<PT>::go(param, e, pv);
-        apply4(e, d4, pv);
-    }
-    for (int64_t e = vend + threadIdx.x; e < end; e += SP_NT) apply1(param, e, drive_at(e, dbuf[e]), gain, nlr);
-}
 
 // ---------------------------------------------------------------------------
 // host-side planning
@@ -2960,24 +25,6 @@ double hash_unit_host(int64_t n, int64_t salt) {
     return (double)(y & 0xFFFFFF) / (double)(1 << 24);
 }
 
-}  // namespace
-}  // namespace cresso
-
-struct cresso_spectral_plan {
-    cresso::Geom g;
-    cresso::Offs o;
-    std::vector<cresso::AxisConst> axc;
-    std::vector<cresso::ModeMeta> meta;
-    std::vector<cresso::CarrierSrc> csrc;
-    std::vector<int64_t> freqs;
-    int64_t shape[8];
-    int32_t rmax;
-    int32_t bins_off;   // hash_bins == 0: no bin tables (bins/counts hold a dummy single bin)
-    uint64_t serial;    // unique per created plan (never reused): names the tables a workspace holds
-};
-
-namespace cresso {
-namespace {
 
 size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -3134,7 +181,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.bins = take((size_t)g.binbytes * (size_t)g.n);
     o.tbuf = take(sizeof(float) * (size_t)g.n);
     o.part = take(sizeof(double) * (size_t)NVMAX * std::max(g.nblk, g.nblk1));
-    o.part1 = take(sizeof(double) * (size_t)g.nblk1);   // sweep 1's partials, read by every block of sweep 2
+    o.part1 = take(sizeof(double) * 2 * (size_t)g.nblk1);   // sweep 1's sums and maxima, read by every block of sweep 2
     o.sums = take(sizeof(double) * (size_t)NVMAX);
     o.hist = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
     o.lt = take(sizeof(float) * (size_t)g.T * g.B);
@@ -3150,152 +197,20 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     return CRESSO_OK;
 }
 
-template <typename T> T* at(void* ws, size_t off) { return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off); }
-
-size_t lds_sweep2(const Geom& g, int rw) {
-    return sizeof(unsigned long long) * SP_NHIST * g.T * g.B + sizeof(float) * (16 + (size_t)rw) * g.PR;
-}
-size_t lds_sweep3(const Geom& g, int kp, int rw) {
-    return lds_al_off(g) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
-}
-size_t lds_sweep3m(const Geom& g, int kp, int rw) { return lds_sweep3(g, kp, rw) + sizeof(float) * ((size_t)kp * SP_BQS + SP_NT); }
-size_t lds_sweep4(const Geom& g, int kp, int rw) {
-    return ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
-}
-constexpr size_t SP_LDS_MAX = 64 * 1024;
-
-template <int RM, int KC, typename PT, typename GT>
-int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws, const cresso_hyper& h,
-                 hipStream_t s) {
-    const Geom& g = P.g;
-    const Offs& o = P.o;
-    SpecState st;
-    st.force_rms = (float*)d.force_rms; st.drive_energy = (float*)d.drive_energy;
-    st.surprise = (float*)d.surprise; st.action = (float*)d.action; st.omega = (const float*)d.omega;
-    st.q_cos = (float*)d.q_cos; st.q_sin = (float*)d.q_sin; st.p_cos = (float*)d.p_cos; st.p_sin = (float*)d.p_sin;
-    st.metric_cos = (float*)d.metric_cos; st.metric_sin = (float*)d.metric_sin;
-    st.metric_p_cos = (float*)d.metric_p_cos; st.metric_p_sin = (float*)d.metric_p_sin;
-    st.calcium_cos = (float*)d.calcium_cos; st.calcium_sin = (float*)d.calcium_sin; st.conf = (float*)d.mode_confidence;
-    st.hash_energy = (float*)d.hash_energy; st.hash_impulse = (float*)d.hash_impulse;
-    st.hash_refractory = (float*)d.hash_refractory;
-    const int hash_on = d.hash_energy != nullptr && g.B > 0 && P.g.T > 0 ? 1 : 0;
-    const int hard = d.hard ? 1 : 0;
-    const int echo_on = (hard && h.echo_mix != 0.0) ? 1 : 0;
-    const GT* grad = (const GT*)d.grad;
-    PT* param = (PT*)d.param;
-    const float* rowtab = at<float>(ws, o.rowtab);
-    const float* coltab = at<float>(ws, o.coltab);
-    const ModeMeta* meta = at<ModeMeta>(ws, o.meta);
-    const unsigned char* bins = at<unsigned char>(ws, o.bins);
-    const unsigned long long* counts = at<unsigned long long>(ws, o.counts);
-    double* part = at<double>(ws, o.part);
-    double* sums = at<double>(ws, o.sums);
-    unsigned long long* hist = at<unsigned long long>(ws, o.hist);
-    const unsigned long long* cooc = at<unsigned long long>(ws, o.cooc);
-    float* lt = at<float>(ws, o.lt);
-    float* imp = at<float>(ws, o.imp);
-    unsigned long long* rowfx = at<unsigned long long>(ws, o.rowfx);
-    unsigned long long* colfx = at<unsigned long long>(ws, o.colfx);
-    float* colfac = at<float>(ws, o.colfac);
-    float* terms = at<float>(ws, o.terms);
-    float* tbuf = at<float>(ws, o.tbuf);
-    Ctrl* ctrl = at<Ctrl>(ws, o.ctrl);
-    const double* stats = at<double>(ws, o.stats);
-    const double* bounds = at<double>(ws, o.bounds);
-    const double* gram = at<double>(ws, o.gram);
-    double* part1 = at<double>(ws, o.part1);
-    const int step = d.step;
-    const int axes_on = (hard && h.instant_metric_coupling != 0.0 && !g.one_d) ? 1 : 0;
-    const size_t l2 = lds_sweep2(g, 2 * RM), l3 = lds_sweep3(g, kcp<KC>(), 2 * RM), l4 = lds_sweep4(g, kcp<KC>(), 2 * RM);
-    if (l2 > SP_LDS_MAX || l3 > SP_LDS_MAX || l4 > SP_LDS_MAX)
-        return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_tables x hash_bins = %d needs %zu bytes of LDS per block",
-                    g.T * g.B, std::max(l2, std::max(l3, l4)));
-    const dim3 grid(g.nblk), blk(SP_NT);
-    const bool v4 = ((uintptr_t)grad % (4 * sizeof(GT))) == 0 && ((uintptr_t)param % (4 * sizeof(PT))) == 0;
-    if (v4)
-        hipLaunchKernelGGL((sweep1_kernel<PT, GT, true>), dim3(g.nblk1), blk, 0, s, g, grad, param, part1, rowfx, colfx,
-                           ctrl, st.force_rms, h);
-    else
-        hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part1, rowfx, colfx,
-                           ctrl, st.force_rms, h);
-    const bool fast = fast_mode(g, hash_on, axes_on, h);
-    if constexpr (RM <= 8) {
-        if (fast) {
-            hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl, part,
-                               hist, rowfx, colfx, part1, st.force_rms, step, h);
-            goto swept2;
-        }
+// The largest bin count of any table (data independent): with it the
+// histograms' fixed-point scales keep every bin sum below 2^62.
+__global__ void ws_cmax_kernel(const unsigned long long* __restrict__ counts, int64_t tb, int64_t n, int bins_off,
+                               Ctrl* __restrict__ ctrl) {
+    __shared__ unsigned long long s[256];
+    unsigned long long m = 1;
+    for (int64_t i = threadIdx.x; i < tb; i += blockDim.x) m = counts[i] > m ? counts[i] : m;
+    s[threadIdx.x] = m;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w && s[threadIdx.x + w] > s[threadIdx.x]) s[threadIdx.x] = s[threadIdx.x + w];
+        __syncthreads();
     }
-    if (fast)
-        hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, h);
-    else
-        hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 0>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, h);
-swept2:
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2), dim3(256), 0, s, part, g.nblk, NV2, sums);
-    hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st,
-                       ctrl, step, hash_on, hard, h);
-    if (axes_on && g.ntrail > 1) {
-        int64_t nterms = 0;
-        for (int a = 0; a < g.ntrail; ++a) nterms += g.tdim[a];
-        hipLaunchKernelGGL(marg_terms_kernel, dim3((unsigned)nterms), dim3(SP_MARG_NT), 0, s, g, colfx, terms, ctrl,
-                           (float)h.eps);
-        hipLaunchKernelGGL(marg_fac_kernel, dim3((unsigned)((g.cols + SP_MARG_NT - 1) / SP_MARG_NT)), dim3(SP_MARG_NT), 0,
-                           s, g, terms, colfac);
-    }
-    if constexpr (RM <= 8 && KC <= 12) {
-        const size_t l3m = lds_sweep3m(g, kcp<KC>(), 2 * RM);
-        if (fast && l3m <= SP_LDS_MAX) {
-            hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl, lt,
-                               rowfx, colfx, colfac, tbuf, part, hist, h);
-            goto swept3;
-        }
-    }
-    if (fast)
-        hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 1>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
-    else
-        hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 0>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
-swept3:
-    // sweep4m writes the full drive: fin3 then forms the hash term's RMS from
-    // the co-occurrence counts, and sweep 5 needs no bins
-    const int c5c = (KC <= 12 && fast && cooc_closed(g)) ? 1 : 0;
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3), dim3(256), 0, s, part, g.nblk, NV3, sums);
-    hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
-                       cooc, step, hash_on, hard, echo_on, c5c, h);
-    if constexpr (KC <= 12) {
-        if (c5c) {
-            hipLaunchKernelGGL((sweep4m_kernel<RM, KC>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf,
-                               part, echo_on, h);
-            goto swept4;
-        }
-    }
-    if (fast)
-        hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
-                           hash_on, echo_on, h);
-    else
-        hipLaunchKernelGGL((sweep4_kernel<RM, KC, 0>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
-                           hash_on, echo_on, h);
-swept4:
-    const bool hash5 = hash_on && !c5c;   // sweep 5 adds the hash term itself
-    const size_t l5 = hash5 ? sizeof(float) * (size_t)g.T * g.B : 0;
-    const bool pv4 = ((uintptr_t)param % (4 * sizeof(PT))) == 0;
-    if (hash5 && pv4)
-        hipLaunchKernelGGL((sweep5_kernel<PT, true, true>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, part,
-                           st.drive_energy, step, hash_on, hard, c5c, h);
-    else if (hash5)
-        hipLaunchKernelGGL((sweep5_kernel<PT, true, false>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, part,
-                           st.drive_energy, step, hash_on, hard, c5c, h);
-    else if (pv4)
-        hipLaunchKernelGGL((sweep5_kernel<PT, false, true>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, part,
-                           st.drive_energy, step, hash_on, hard, c5c, h);
-    else
-        hipLaunchKernelGGL((sweep5_kernel<PT, false, false>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, part,
-                           st.drive_energy, step, hash_on, hard, c5c, h);
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: launch");
+    if (threadIdx.x == 0) ctrl->cmax = bins_off ? (double)n : (double)s[0];
 }
 
 __global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
@@ -3305,6 +220,7 @@ __global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
 
 }  // namespace
 }  // namespace cresso
+
 
 using namespace cresso;
 
@@ -3363,6 +279,8 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
     const int64_t bins_blocks = std::max<int64_t>(1, std::min<int64_t>(2048, (g.n + 255) / 256));
     hipLaunchKernelGGL(ws_bins_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g, at<unsigned char>(ws, o.bins),
                        at<unsigned long long>(ws, o.counts));
+    hipLaunchKernelGGL(ws_cmax_kernel, dim3(1), dim3(256), 0, s, at<unsigned long long>(ws, o.counts), TB, g.n,
+                       P->bins_off, at<Ctrl>(ws, o.ctrl));
     if (cooc_closed(g)) {
         const int64_t BB = (int64_t)g.B * g.B;
         hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((BB + 255) / 256)), dim3(256), 0, s,
@@ -3393,23 +311,16 @@ extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cre
     if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "spectral route: drive_clip must be positive");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int pt = d->param_dtype, gt = d->grad_dtype;
-    // carrier-count variant: (modes, column carriers) fixed at compile time
-    const int R = g.R, K = g.K;
-    const int var = (R <= 4 && K <= 9) ? 0 : (R <= 8 && K <= 11) ? 1 : (R <= 8) ? 2 : 3;
-#define CRESSO_SP_RUN(PTy, GTy)                                                  \
-    switch (var) {                                                               \
-        case 0: return run_step<4, 9, PTy, GTy>(*P, *d, ws, *hyper, s);          \
-        case 1: return run_step<8, 11, PTy, GTy>(*P, *d, ws, *hyper, s);         \
-        case 2: return run_step<8, 17, PTy, GTy>(*P, *d, ws, *hyper, s);         \
-        default: return run_step<16, 33, PTy, GTy>(*P, *d, ws, *hyper, s);       \
-    }
-#define CRESSO_SP_CASE(PC, GC, PTy, GTy) \
-    if (pt == PC && gt == GC) { CRESSO_SP_RUN(PTy, GTy) }
-    CRESSO_SP_CASE(CRESSO_F32, CRESSO_F32, float, float)
-    CRESSO_SP_CASE(CRESSO_BF16, CRESSO_BF16, __hip_bfloat16, __hip_bfloat16)
-    CRESSO_SP_CASE(CRESSO_F16, CRESSO_F16, __half, __half)
-#undef CRESSO_SP_CASE
-#undef CRESSO_SP_RUN
+    // (param dtype, grad dtype) -> the unit that instantiates the step for it
+    static const struct { int pt, gt; SpectralRunFn fn; } table[] = {
+        {CRESSO_F32, CRESSO_F32, spectral_run_f32_f32},
+        {CRESSO_BF16, CRESSO_BF16, spectral_run_bf16_bf16},
+        {CRESSO_F16, CRESSO_F16, spectral_run_f16_f16},
+        {CRESSO_F32, CRESSO_BF16, spectral_run_f32_bf16},
+        {CRESSO_F32, CRESSO_F16, spectral_run_f32_f16},
+    };
+    for (const auto& e : table)
+        if (e.pt == pt && e.gt == gt) return e.fn(*P, *d, ws, *hyper, s);
     return fail(CRESSO_E_UNSUPPORTED, "spectral route: param/grad dtype pair (%d,%d) not supported by this build", pt, gt);
 }
 

@@ -1,0 +1,10 @@
+// Spectral step instantiated for __hip_bfloat16 params and __hip_bfloat16 grads (one translation
+// unit per dtype pair, so that the pairs compile in parallel).
+#include "spectral_kernels.hpp"
+
+namespace cresso {
+int32_t spectral_run_bf16_bf16(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws,
+                              const cresso_hyper& h, hipStream_t s) {
+    return spectral_run<__hip_bfloat16, __hip_bfloat16>(P, d, ws, h, s);
+}
+}  // namespace cresso

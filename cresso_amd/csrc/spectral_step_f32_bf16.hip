@@ -1,0 +1,10 @@
+// Spectral step instantiated for float params and __hip_bfloat16 grads (one translation
+// unit per dtype pair, so that the pairs compile in parallel).
+#include "spectral_kernels.hpp"
+
+namespace cresso {
+int32_t spectral_run_f32_bf16(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws,
+                             const cresso_hyper& h, hipStream_t s) {
+    return spectral_run<float, __hip_bfloat16>(P, d, ws, h, s);
+}
+}  // namespace cresso

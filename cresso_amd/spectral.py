@@ -24,6 +24,11 @@ import torch
 
 from . import _native
 
+# (param dtype, grad dtype) pairs of the library's spectral step; the force is
+# the grad converted to the work dtype (fp32), as in cresso_v5.py:907-912
+_DTYPE_PAIRS = {(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                (torch.float32, torch.bfloat16), (torch.float32, torch.float16)}
+
 _VEC_KEYS = ("q_cos", "q_sin", "p_cos", "p_sin", "metric_cos", "metric_sin", "metric_p_cos", "metric_p_sin",
              "calcium_cos", "calcium_sin", "mode_confidence")
 
@@ -112,9 +117,9 @@ class SpectralEngine:
 
     def _prepare(self, param: torch.Tensor, grad: torch.Tensor, st: dict, group: dict):
         """Validate one tensor's state and build its descriptor; -> (key, rank, desc)."""
-        if param.dtype not in (torch.float32, torch.bfloat16, torch.float16) or grad.dtype != param.dtype:
+        if (param.dtype, grad.dtype) not in _DTYPE_PAIRS:
             raise RuntimeError(f"CRESSO5 spectral route on MI355X supports fp32/bf16/fp16 params with grads of the "
-                               f"same dtype (got {param.dtype} / {grad.dtype})")
+                               f"same dtype, and fp32 params with bf16/fp16 grads (got {param.dtype} / {grad.dtype})")
         for k in ("force_rms", "omega") + _VEC_KEYS:
             if st[k].dtype != torch.float32:
                 raise RuntimeError(f"CRESSO5 spectral state {k} has dtype {st[k].dtype}, expected float32")

@@ -242,6 +242,80 @@ int32_t cresso_spectral_workspace_reconstruct(const cresso_spectral_plan* plan, 
                                               size_t workspace_bytes, const float* cc, const float* sc,
                                               const float* gates, float* out, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Unit operations of the spectral route.
+ *
+ * One entry point per op of the reference's fused CUDA path
+ * (cresso_cuda.cpp:44-125), with the same arguments and in-place state
+ * semantics, on explicit device fields (fp32).  cresso_spectral_step fuses
+ * all of them; these serve callers that compose a step themselves and the
+ * per-op parity checks.  The hash ops and cresso_drive_update take a
+ * caller-allocated scratch workspace (256-byte aligned) of at least
+ * cresso_unit_workspace_bytes(bins) bytes (bins = 1 for the drive); calls
+ * sharing a workspace must not overlap.  Hash bins and counts follow
+ * _hash_index_tensor (cresso_v5.py:495-516) bit for bit.
+ * ------------------------------------------------------------------------- */
+size_t cresso_unit_workspace_bytes(int32_t bins);
+
+/* One hash table's metric (cresso_v5.py:1014-1026): bin means of
+ * density_source [numel] (row-major linear index, table salt `salt`), EMA into
+ * hash_energy [bins] in place (copied when step <= 1), normalized by its
+ * mean, raised to hash_metric_coupling / max(0.25, energy_power), gathered per
+ * element, clamped to [0.08, 12] and logged into term_out [numel].
+ * Replaces hash_metric_update_log_cuda (cresso_cuda_kernel.cu:1515-1591;
+ * binding cresso_cuda.cpp:44-53).  bins <= 4096. */
+int32_t cresso_hash_metric_update_log(const float* density_source, int64_t numel, float* hash_energy, int32_t bins,
+                                      int32_t salt, int32_t step, double hash_decay, double hash_metric_coupling,
+                                      double energy_power, double eps, float* term_out, void* workspace,
+                                      size_t workspace_bytes, void* stream);
+
+/* One hash table's impulse (cresso_v5.py:1153-1160): bin means cp of
+ * port_source, hash_refractory <- decay * r + (1 - decay) |cp|, gate
+ * 1/(1 + refractory_gain * r), hash_impulse <- impulse_decay * i +
+ * (1 - impulse_decay) cp * gate (both [bins], in place), gathered per element
+ * into retrieved_out [numel].  Replaces hash_impulse_update_gather_cuda
+ * (cresso_cuda_kernel.cu:1593-1661; binding cresso_cuda.cpp:54-62). */
+int32_t cresso_hash_impulse_update_gather(const float* port_source, int64_t numel, float* hash_refractory,
+                                          float* hash_impulse, int32_t bins, int32_t salt, double hash_decay,
+                                          double hash_impulse_decay, double refractory_gain, float* retrieved_out,
+                                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Metric oscillator of both banks, in place (cresso_v5.py:1064-1088).
+ * Replaces metric_update_cuda (cresso_cuda_kernel.cu:1829-1867; binding
+ * cresso_cuda.cpp:64-73).  rank <= 4096. */
+int32_t cresso_metric_update(float* metric_cos, float* metric_sin, float* metric_p_cos, float* metric_p_sin,
+                             const float* mcos_port, const float* msin_port, const float* omega, int32_t rank,
+                             double metric_dt, double metric_friction, void* stream);
+
+/* Mode confidence, in place, from the port projections and the pre-contact q
+ * (cresso_v5.py:1199-1202 and its PyTorch branch).  Replaces
+ * confidence_update_cuda (cresso_cuda_kernel.cu:1869-1901; binding
+ * cresso_cuda.cpp:74-81).  rank <= 4096. */
+int32_t cresso_confidence_update(float* confidence, const float* pcos_port, const float* psin_port, const float* qcos,
+                                 const float* qsin, int32_t rank, double confidence_decay, double eps, void* stream);
+
+/* Contact oscillator of one bank (q, p) with its calcium trace, the shared
+ * action (0-dim) and the surprise (0-dim, read), in place
+ * (cresso_v5.py:914-943; the step calls it for the cos bank, then the sin
+ * bank).  Replaces contact_update_pair_cuda (cresso_cuda_kernel.cu:1903-1965;
+ * binding cresso_cuda.cpp:82-98).  rank <= 4096. */
+int32_t cresso_contact_update_pair(float* q, float* p, const float* port, const float* omega, float* calcium,
+                                   float* action, const float* surprise, int32_t rank, double dt,
+                                   double refractory_decay, double refractory_gain, double surprise_gain,
+                                   double surprise_brake, double impulse_friction, double contact_gain,
+                                   double restoring, double cubic, void* stream);
+
+/* Drive shaping, drive-energy reservoir (0-dim drive_energy, in place) and
+ * the update param -= lr * cast(drive * gain) (cresso_v5.py:1303-1353) from
+ * the tangent, prediction and error fields [numel]; echo and hash_pred may be
+ * NULL (no echo / hash term); surprise is read.  param_dtype: CRESSO_F32,
+ * CRESSO_BF16 or CRESSO_F16.  Replaces drive_update_cuda
+ * (cresso_cuda_kernel.cu:2995-3223; binding cresso_cuda.cpp:99-125). */
+int32_t cresso_drive_update(void* param, int32_t param_dtype, const float* tangent, const float* pred,
+                            const float* error, const float* echo, const float* hash_pred, const float* surprise,
+                            float* drive_energy, int64_t numel, int32_t step, int32_t hard, const cresso_hyper* hyper,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

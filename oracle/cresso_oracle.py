@@ -27,6 +27,18 @@ Pinning of each part (what would catch a plausible mistake):
                                 state tensor) from the reference.
   * reservoir                -- known answers 3.0 then 4.0.
   * micro route              -- golden trajectory (one fixture).
+  * unit operations          -- hash_metric_update_log, hash_impulse_update_gather,
+                                metric_update, confidence_update,
+                                contact_update_pair are the pieces the spectral
+                                step calls, so the trajectories pin them.
+
+One deliberate difference from the reference's PyTorch path: the alignment
+gate's predicate sqrt(mean(pred^2) + eps) > sqrt(eps) (cresso_v5.py:1307,
+1554) is decided in fp64, as the reference's fused kernels decide it.  In
+fp32 it is a rounding tie whenever mean(pred^2) is below half an fp32 ulp of
+eps, and torch's CPU result then differs between hosts (see _drive_apply).
+The update of fp16/bf16 params keeps the reference's torch call
+p.add_(u, alpha=-lr), whose CPU kernel rounds alpha to the param dtype.
 """
 
 from __future__ import annotations
@@ -418,6 +430,91 @@ def reservoir(old: Tensor, cur: Tensor, decay: float, step: int) -> Tensor:
 # The optimizer restatement
 # --------------------------------------------------------------------------
 
+# --------------------------------------------------------------------------
+# Unit operations of the spectral step (each is one op of the reference's
+# fused CUDA path, cresso_cuda.cpp:44-125; the step below calls them)
+# --------------------------------------------------------------------------
+
+def hash_metric_update_log(dsrc: Tensor, energy: Tensor, idx: Tensor, bins: int, step: int, h: dict, dtype,
+                           accum: str = "native") -> Tensor:
+    """One table of the hash metric (cresso_v5.py:1014-1026; the reference op
+    hash_metric_update_log_cuda, cresso_cuda_kernel.cu:1515-1591): bin means of
+    the density source, EMA into ``energy`` (this table's row of hash_energy,
+    copied on step <= 1, in place), normalized by its mean, raised to
+    coupling / max(0.25, energy_power), gathered per element, clamped to
+    [0.08, 12] and logged.  -> per-element log term."""
+    eps = float(h["eps"])
+    cell = hash_reduce_mean(dsrc, idx, bins, accum)
+    if step <= 1:
+        energy.copy_(cell.to(energy.dtype))
+    else:
+        energy.mul_(float(h["hash_decay"])).add_(cell.to(energy.dtype), alpha=1.0 - float(h["hash_decay"]))
+    hm = (energy.to(dtype) / energy.to(dtype).mean().clamp_min(eps)).clamp_min(eps)
+    hmp = hm.pow(float(h["hash_metric_coupling"]) / max(0.25, float(h["energy_power"])))
+    return torch.log(hmp[idx].clamp(0.08, 12.0).clamp_min(eps))
+
+
+def hash_impulse_update_gather(psrc: Tensor, refractory: Tensor, impulse: Tensor, idx: Tensor, bins: int, h: dict,
+                               dtype, accum: str = "native") -> Tensor:
+    """One table of the hash impulse (cresso_v5.py:1153-1160; the reference op
+    hash_impulse_update_gather_cuda, cresso_cuda_kernel.cu:1593-1661): bin means
+    of the port source, refractory EMA of their magnitude (no first-step copy),
+    gate 1/(1 + refractory_gain * refractory), impulse EMA of mean * gate (both
+    rows in place), gathered per element.  -> per-element impulse."""
+    cp = hash_reduce_mean(psrc, idx, bins, accum).to(impulse.dtype)
+    refractory.mul_(float(h["hash_decay"])).add_(cp.abs(), alpha=1.0 - float(h["hash_decay"]))
+    gate = 1.0 / (1.0 + float(h["refractory_gain"]) * refractory)
+    impulse.mul_(float(h["hash_impulse_decay"])).add_(cp * gate, alpha=1.0 - float(h["hash_impulse_decay"]))
+    return impulse.to(dtype)[idx]
+
+
+def metric_update(mq_cos: Tensor, mq_sin: Tensor, mp_cos: Tensor, mp_sin: Tensor, port_cos: Tensor,
+                  port_sin: Tensor, omega: Tensor, metric_dt: float, metric_friction: float) -> None:
+    """Metric oscillator of both banks, in place (cresso_v5.py:1064-1088; the
+    reference op metric_update_cuda, cresso_cuda_kernel.cu:1368-1395)."""
+    for mq, mp, port in ((mq_cos, mp_cos, port_cos), (mq_sin, mp_sin, port_sin)):
+        mp.mul_(max(0.0, 1.0 - metric_dt * metric_friction))
+        mp.add_(port - (omega * omega) * mq, alpha=metric_dt)
+        mq.add_(mp, alpha=metric_dt)
+        mq.clamp_(-3.0, 3.0)
+
+
+def confidence_update(conf: Tensor, pcp: Tensor, psp: Tensor, qc: Tensor, qs: Tensor, decay: float,
+                      eps: float) -> None:
+    """Mode confidence, in place (cresso_v5.py:1199-1202 and the PyTorch branch
+    that follows; the reference op confidence_update_cuda,
+    cresso_cuda_kernel.cu:1397-1421).  Uses the pre-contact q."""
+    pe = torch.sqrt(pcp.pow(2) + psp.pow(2) + eps)
+    support = (pcp * qc + psp * qs) / (pe * torch.sqrt(qc.pow(2) + qs.pow(2) + eps) + eps)
+    conf.mul_(decay).add_(support.clamp(-1.0, 1.0), alpha=1.0 - decay)
+    conf.clamp_(-4.0, 4.0)
+
+
+def contact_update_pair(q: Tensor, pm: Tensor, port: Tensor, omega: Tensor, calcium: Tensor, action: Tensor,
+                        surprise: Tensor, h: dict) -> Tensor:
+    """Contact oscillator of one (cos | sin) bank, in place
+    (cresso_v5.py:914-943; the reference op contact_update_pair_cuda,
+    cresso_cuda_kernel.cu:1423-1498).  -> the updated action (same tensor)."""
+    rank = int(q.numel())
+    dt = float(h["dt"])
+    rd = float(h["refractory_decay"])
+    calcium.mul_(rd).add_(port.abs(), alpha=1.0 - rd)
+    gate = 1.0 / (1.0 + float(h["refractory_gain"]) * calcium)
+    sur = surprise.to(q.dtype)
+    plast = 1.0 + float(h["surprise_gain"]) * sur / (1.0 + sur)
+    brake = 1.0 / (1.0 + float(h["surprise_brake"]) * sur)
+    gp = port * gate * plast * brake
+    energy = 0.5 * (pm.pow(2).mean() + ((omega * q).pow(2)).mean()) if rank > 0 else torch.zeros_like(action)
+    power = (gp * pm).mean() if rank > 0 else torch.zeros_like(action)
+    action.mul_(0.985).add_((power - energy).to(action.dtype), alpha=dt)
+    fr = float(h["impulse_friction"]) + float(h["contact_gain"]) * torch.tanh(action.abs()).to(pm.dtype)
+    pm.mul_(torch.clamp(1.0 - dt * fr, min=0.0))
+    pm.add_(gp - float(h["restoring"]) * (omega * omega) * q - float(h["cubic"]) * q.pow(3), alpha=dt)
+    q.add_(pm, alpha=dt)
+    q.clamp_(-8.0, 8.0)
+    return action
+
+
 class OracleCRESSO5:
     """CRESSO5 with ``cuda_ops="off"`` on CPU tensors.
 
@@ -502,24 +599,7 @@ class OracleCRESSO5:
 
     def _contact(self, q, pm, port, omega, calcium, action, surprise, rank) -> Tensor:
         """Contact oscillator for one (cos|sin) bank (cresso_v5.py:914-943)."""
-        h = self.h
-        dt = float(h["dt"])
-        rd = float(h["refractory_decay"])
-        calcium.mul_(rd).add_(port.abs(), alpha=1.0 - rd)
-        gate = 1.0 / (1.0 + float(h["refractory_gain"]) * calcium)
-        sur = surprise.to(q.dtype)
-        plast = 1.0 + float(h["surprise_gain"]) * sur / (1.0 + sur)
-        brake = 1.0 / (1.0 + float(h["surprise_brake"]) * sur)
-        gp = port * gate * plast * brake
-        energy = 0.5 * (pm.pow(2).mean() + ((omega * q).pow(2)).mean()) if rank > 0 else torch.zeros_like(action)
-        power = (gp * pm).mean() if rank > 0 else torch.zeros_like(action)
-        action.mul_(0.985).add_((power - energy).to(action.dtype), alpha=dt)
-        fr = float(h["impulse_friction"]) + float(h["contact_gain"]) * torch.tanh(action.abs()).to(pm.dtype)
-        pm.mul_(torch.clamp(1.0 - dt * fr, min=0.0))
-        pm.add_(gp - float(h["restoring"]) * (omega * omega) * q - float(h["cubic"]) * q.pow(3), alpha=dt)
-        q.add_(pm, alpha=dt)
-        q.clamp_(-8.0, 8.0)
-        return action
+        return contact_update_pair(q, pm, port, omega, calcium, action, surprise, self.h)
 
     def _spectral(self, p: Tensor, g: Tensor, st: dict) -> None:
         """Spectral/hash large-tensor route (cresso_v5.py:945-1353, PyTorch branch)."""
@@ -559,15 +639,7 @@ class OracleCRESSO5:
             for t in range(tables):
                 idx = hash_index(shape, bins, t)
                 hash_idx.append(idx)
-                cell = hash_reduce_mean(dsrc, idx, bins, self.hash_accum)
-                e_t = st["hash_energy"][t]
-                if step <= 1:
-                    e_t.copy_(cell.to(e_t.dtype))
-                else:
-                    e_t.mul_(float(h["hash_decay"])).add_(cell.to(e_t.dtype), alpha=1.0 - float(h["hash_decay"]))
-                hm = (e_t.to(dtype) / e_t.to(dtype).mean().clamp_min(eps)).clamp_min(eps)
-                hmp = hm.pow(float(h["hash_metric_coupling"]) / max(0.25, float(h["energy_power"])))
-                term = torch.log(hmp[idx].clamp(0.08, 12.0).clamp_min(eps))
+                term = hash_metric_update_log(dsrc, st["hash_energy"][t], idx, bins, step, h, dtype, self.hash_accum)
                 logsum = term if logsum is None else logsum + term
             hash_metric = torch.exp(logsum / float(tables)).clamp(0.08, 12.0)
         if dsrc is None:
@@ -577,13 +649,8 @@ class OracleCRESSO5:
         mcp, msp = basis.project(dens)
         mcp = mcp.to(st["metric_cos"].dtype)
         msp = msp.to(st["metric_sin"].dtype)
-        mdt, mf = float(h["metric_dt"]), float(h["metric_friction"])
-        for qk, pk, port in (("metric_cos", "metric_p_cos", mcp), ("metric_sin", "metric_p_sin", msp)):
-            mq, mp = st[qk], st[pk]
-            mp.mul_(max(0.0, 1.0 - mdt * mf))
-            mp.add_(port - (omega * omega) * mq, alpha=mdt)
-            mq.add_(mp, alpha=mdt)
-            mq.clamp_(-3.0, 3.0)
+        metric_update(st["metric_cos"], st["metric_sin"], st["metric_p_cos"], st["metric_p_sin"], mcp, msp, omega,
+                      float(h["metric_dt"]), float(h["metric_friction"]))
 
         logm = basis.reconstruct(st["metric_cos"].to(dtype), st["metric_sin"].to(dtype)).clamp(-3.0, 3.0)
         metric = torch.exp(float(h["metric_coupling"]) * logm).clamp(0.06, 16.0)
@@ -609,21 +676,12 @@ class OracleCRESSO5:
         if hash_idx is not None and "hash_impulse" in st:
             acc: Optional[Tensor] = None
             for t, idx in enumerate(hash_idx):
-                cp = hash_reduce_mean(psrc, idx, bins, self.hash_accum).to(st["hash_impulse"].dtype)
-                ref_t = st["hash_refractory"][t]
-                imp_t = st["hash_impulse"][t]
-                ref_t.mul_(float(h["hash_decay"])).add_(cp.abs(), alpha=1.0 - float(h["hash_decay"]))
-                gate_t = 1.0 / (1.0 + float(h["refractory_gain"]) * ref_t)
-                imp_t.mul_(float(h["hash_impulse_decay"])).add_(cp * gate_t, alpha=1.0 - float(h["hash_impulse_decay"]))
-                got = imp_t.to(dtype)[idx]
+                got = hash_impulse_update_gather(psrc, st["hash_refractory"][t], st["hash_impulse"][t], idx, bins, h,
+                                                 dtype, self.hash_accum)
                 acc = got if acc is None else acc + got
             hash_pred = acc / float(len(hash_idx))
 
-        pe = torch.sqrt(pcp.pow(2) + psp.pow(2) + eps)
-        support = (pcp * qc + psp * qs) / (pe * torch.sqrt(qc.pow(2) + qs.pow(2) + eps) + eps)
-        cd = float(h["confidence_decay"])
-        conf.mul_(cd).add_(support.clamp(-1.0, 1.0), alpha=1.0 - cd)
-        conf.clamp_(-4.0, 4.0)
+        confidence_update(conf, pcp, psp, qc, qs, float(h["confidence_decay"]), eps)
 
         action = st["action"]
         action = self._contact(qc, st["p_cos"], pcp, omega, st["calcium_cos"], action, surprise, rank)
@@ -649,8 +707,17 @@ class OracleCRESSO5:
         frms = torch.sqrt(tangent.pow(2).mean() + eps)
         prms = torch.sqrt(pred.pow(2).mean() + eps)
         align = ((tangent * pred).mean() / (frms * prms + eps)).clamp(-1.0, 1.0)
-        agate = torch.where(prms > math.sqrt(eps), ((align + 1.0) * 0.5).clamp(0.0, 1.0),
-                            torch.zeros((), dtype=dtype))
+        # The gate's predicate prms > sqrt(eps) (cresso_v5.py:1307, 1554) is
+        # decided in fp64, as the reference's fused kernels decide it
+        # (cresso_cuda_kernel.cu:2080-2085, 2703-2708).  Evaluated in fp32 it
+        # is a rounding tie whenever mean(pred^2) is below half an fp32 ulp of
+        # eps (a nonzero but tiny prediction, e.g. C3 tensors whose force RMS
+        # is eps-dominated), and torch's CPU result then differs between hosts
+        # (observed: True on the GPU box's EPYC host, False in this container,
+        # for the same inputs).
+        pm2 = float(pred.double().pow(2).mean())
+        agate = torch.where(torch.tensor(math.sqrt(pm2 + eps) > math.sqrt(eps)),
+                            ((align + 1.0) * 0.5).clamp(0.0, 1.0), torch.zeros((), dtype=dtype))
         ws = int(h["warmup_steps"])
         warm = 1.0 if ws == 0 else (1.0 - math.exp(-step / max(1, ws)))
         sur = st["surprise"].to(dtype)
@@ -693,7 +760,8 @@ class OracleCRESSO5:
         st["drive_energy"] = reservoir(st["drive_energy"], de_now, h["reservoir_decay"], step)
         gain = (float(h["target_update_rms"]) / torch.sqrt(st["drive_energy"].to(dtype) + eps)).clamp(
             float(h["min_gain"]), float(h["max_gain"]))
-        p.add_((drive * gain).to(dtype=p.dtype), alpha=-float(h["lr"]))
+        self.last_update = drive * gain   # the fp32 update before its cast (inspection by tests)
+        p.add_(self.last_update.to(dtype=p.dtype), alpha=-float(h["lr"]))
 
     def _scalar(self, p: Tensor, g: Tensor, st: dict) -> None:
         """Scalar contact route (cresso_v5.py:1434-1582, PyTorch branch)."""
@@ -805,4 +873,5 @@ class OracleCRESSO5:
         st["drive_energy"] = reservoir(st["drive_energy"], de_now, h["reservoir_decay"], step)
         gain = (float(h["target_update_rms"]) / torch.sqrt(st["drive_energy"].to(dtype) + eps)).clamp(
             float(h["min_gain"]), float(h["max_gain"]))
-        p.add_((drive * gain).to(dtype=p.dtype), alpha=-float(h["lr"]))
+        self.last_update = drive * gain   # the fp32 update before its cast (inspection by tests)
+        p.add_(self.last_update.to(dtype=p.dtype), alpha=-float(h["lr"]))

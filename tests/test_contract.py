@@ -235,6 +235,33 @@ def test_host_batch_guard_cpu_behaviour():
         hb.BatchGuard(ps)
 
 
+def test_host_batch_guard_holds_references_and_refuses_replaced_params():
+    # The guard keeps each planned parameter alive (so no new object can take
+    # its address) and refuses the fast path once a parameter object is replaced.
+    import ctypes
+    import gc
+    import weakref
+
+    hb = _native.host_batch()
+    assert hb is not None, "cresso_amd/_hostbatch extension not built"
+    ps = [torch.nn.Parameter(torch.zeros(4, 4)) for _ in range(3)]
+    for p in ps:
+        p.grad = torch.zeros(4, 4)
+    guard = hb.BatchGuard(ps)
+    ref = weakref.ref(ps[1])
+    old = ps[1]
+    ps[1] = torch.nn.Parameter(torch.zeros(4, 4))
+    ps[1].grad = torch.zeros(4, 4)
+    del old
+    gc.collect()
+    assert ref() is not None          # still referenced by the guard
+    buf = (ctypes.c_void_p * 3)()
+    assert guard.gather(ps, ctypes.addressof(buf)) is False
+    del guard
+    gc.collect()
+    assert ref() is None              # released with the guard
+
+
 def test_spectral_lane_assignment():
     # the multi-tensor spectral step: m tensors of one shape use min(4, m)
     # distinct lanes (one workspace each), shapes spread over the lanes
