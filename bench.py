@@ -1,17 +1,21 @@
 """Benchmark of the CRESSO5 hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|copy] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c2|c3|c4|c5|copy] [--no-cpu]
 
-With no --workload, both headline configs run: C2 gives the line's `value`,
-`ms_per_step`, `roofline` and `cpu_baseline`; C3 follows under `secondary`
-with the same fields.
+With no --workload, the headline configs run first: C2 gives the line's
+`value`, `ms_per_step`, `roofline`, `cpu_baseline` and `parity`; C3 (the
+metric's second config, with its own CPU leg and parity) and the timing-only
+C4 and C5 lines follow under `secondary`.
     python bench.py --rocprof-summary DIR [DIR ...] [--calib DIR ...] [--launches N]
 
 Workloads:
+  c1: one fp32 (2048,2048) parameter, rank 8 (the reference's CPU-runnable case).
   c2: one fp32 (4096,4096) parameter, spectral/hash route, rank 8, F=5, B=64, T=2;
       grads N(0,1e-3) with 1% of entries x50, fresh per step.
   c3: 840 LoRA-thin fp32 matrices alternating (4096,16)/(16,4096), scalar route,
       rank 4; per-tensor scale 10^U(-4,-1) times N(0,1e-2).
+  c4: the 1.2 B-element transformer set (fp32, rank 8; inputs drawn on the device).
+  c5: bf16 (8192,8192) and fp32 conv / 3-D tensors at rank 16, F=7, B=256, T=4.
   copy: calibration only -- torch's device copy of a 256 MiB fp32 buffer, the
       plain copy kernel of known size that scales rocprofv3's FETCH_SIZE and
       WRITE_SIZE counters to bytes.
@@ -110,14 +114,21 @@ def c4_layer_shapes(layers=22):
     return out
 
 
-def make_c4(device, pool=2, seed=0, shapes=None):
+def make_c4(device, pool=2, seed=0, shapes=None, on_device=False):
     """C4: fp32 tensors, grads N(0, sigma) with sigma = 10^U(-5,-2) per tensor; p0 = 0.02 randn.
-    shapes=None is the full 1.2 B-element set; C4_SHAPES is one tensor of each distinct shape."""
+    shapes=None is the full 1.2 B-element set; C4_SHAPES is one tensor of each distinct shape.
+    on_device: draw params and grads with a generator on `device` (the timing leg of the full
+    set; 3.6 G draws on the host would take minutes)."""
     shapes = c4_layer_shapes() if shapes is None else shapes
     gen = torch.Generator().manual_seed(seed)
     sig = (10.0 ** (torch.rand(len(shapes), generator=gen, dtype=torch.float64) * 3.0 - 5.0)).tolist()
-    params = [torch.nn.Parameter((0.02 * torch.randn(s, generator=gen)).to(device)) for s in shapes]
-    grads = [[(sc * torch.randn(s, generator=gen)).to(device) for s, sc in zip(shapes, sig)] for _ in range(pool)]
+    if on_device:
+        gen = torch.Generator(device=device).manual_seed(seed)
+        draw = lambda s: torch.randn(s, generator=gen, device=device)   # noqa: E731
+    else:
+        draw = lambda s: torch.randn(s, generator=gen).to(device)   # noqa: E731
+    params = [torch.nn.Parameter(0.02 * draw(s)) for s in shapes]
+    grads = [[sc * draw(s) for s, sc in zip(shapes, sig)] for _ in range(pool)]
     kwargs = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2)
     return params, grads, kwargs, shapes, sig
 
@@ -173,16 +184,19 @@ def measured_traffic(workload):
     return nbytes, f"{TRAFFIC_FILES[workload]} (rocprofv3 FETCH_SIZE + WRITE_SIZE, kernel sources {cur})"
 
 
-def algorithmic_bytes(shapes, elem_bytes=4):
-    n = sum(int(torch.Size(s).numel()) for s in shapes)
-    return 3 * elem_bytes * n, n
+def algorithmic_bytes(params):
+    """Compulsory bytes of a step: grad read + param read + param write per element, in the
+    param's dtype (12 B fp32, 6 B bf16); state traffic (< 4 KiB a tensor) is ignored."""
+    n = sum(p.numel() for p in params)
+    return sum(3 * p.element_size() * p.numel() for p in params), n
 
 
 def time_gpu(workload, steps, warmup):
     import cresso_amd
 
     device = torch.device("cuda:0")
-    params, grads, kwargs, shapes, _ = MAKERS[workload](device)
+    params, grads, kwargs, shapes, _ = TIMING_MAKERS.get(workload, MAKERS[workload])(device)
+    nbytes, n = algorithmic_bytes(params)
     opt = cresso_amd.CRESSO5(params, cuda_ops="required", **kwargs)
     pool = len(grads)
 
@@ -209,7 +223,8 @@ def time_gpu(workload, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     total_ms = start.elapsed_time(end)
-    return dict(ms_per_step=total_ms / steps, wall_ms_per_step=1e3 * wall / steps, shapes=shapes, kwargs=kwargs)
+    return dict(ms_per_step=total_ms / steps, wall_ms_per_step=1e3 * wall / steps, shapes=shapes, kwargs=kwargs,
+                nbytes=nbytes, n=n)
 
 
 def copy_calibration(steps, warmup, nbytes=256 << 20):
@@ -375,7 +390,10 @@ def rocprof_summary(dirs, calib=None, launches=None):
     print("\n".join(out))
 
 
-MAKERS = {"c2": make_c2, "c3": make_c3}
+MAKERS = {"c1": make_c1, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5}
+# the timing leg of the full C4 set draws its inputs on the device
+TIMING_MAKERS = {"c4": lambda device: make_c4(device, pool=1, on_device=True)}
+CPU_LEG = ("c2", "c3")   # C4/C5 take minutes per step on the CPU: their parity is tests/test_gpu_full_configs.py
 
 
 def cpu_and_parity(workload, steps=4):
@@ -488,14 +506,19 @@ def _cpu_model():
     return "unknown"
 
 
-WORKLOAD_NAMES = {"c2": "C2: (4096,4096) fp32 spectral/hash route, rank 8, F=5, B=64, T=2",
-                  "c3": "C3: 840 LoRA-thin fp32 (4096,16)/(16,4096), scalar route, rank 4"}
+WORKLOAD_NAMES = {"c1": "C1: (2048,2048) fp32 spectral/hash route, rank 8, F=5, B=64, T=2",
+                  "c2": "C2: (4096,4096) fp32 spectral/hash route, rank 8, F=5, B=64, T=2",
+                  "c3": "C3: 840 LoRA-thin fp32 (4096,16)/(16,4096), scalar route, rank 4",
+                  "c4": "C4: 1.2 B fp32 params (embedding (32000,2048), 22 layers of q,k,v,o (2048,2048), gate/up "
+                        "(5632,2048), down (2048,5632), two (2048,) norms), rank 8, F=5, B=64, T=2",
+                  "c5": "C5: bf16 (8192,8192), fp32 (512,256,3,3), (256,256,3,3), (64,512,512), rank 16, F=7, "
+                        "B=256, T=4"}
 
 
 def measure(workload, args):
     """Time one workload on the GPU (and its CPU baseline); one record."""
     res = time_gpu(workload, args.steps, args.warmup)
-    nbytes, n = algorithmic_bytes(res["shapes"])
+    nbytes, n = res["nbytes"], res["n"]
     traffic, traffic_note = measured_traffic(workload)
     ms = res["ms_per_step"]
     achieved = nbytes / (ms * 1e-3) / 1e9   # the launch = one step; its mean duration over the timed region
@@ -510,8 +533,11 @@ def measure(workload, args):
                      "launch": "one optimizer step (the library's kernel sequence); mean over the timed region, "
                                "HIP events on the launch stream"},
     }
-    if not args.no_cpu:
+    if not args.no_cpu and workload in CPU_LEG:
         rec["cpu_baseline"], rec["parity"] = cpu_and_parity(workload)
+    elif workload not in CPU_LEG:
+        rec["parity"] = {"in_run": False, "covered_by": "tests/test_gpu_full_configs.py (oracle trajectories at "
+                         "this config's shapes)"}
     return rec
 
 
@@ -520,7 +546,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["c2", "c3", "copy"], default=None)
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "c5", "copy"], default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--rocprof-summary", default=None, nargs="+", metavar="DIR")
     ap.add_argument("--calib", default=None, nargs="+", metavar="DIR")
@@ -533,7 +559,7 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
               "(every GPU box here has one GPU)", file=sys.stderr)
         sys.exit(2)
-    workloads = [args.workload] if args.workload else ["c2", "c3"]
+    workloads = [args.workload] if args.workload else ["c2", "c3", "c4", "c5"]
     if workloads == ["copy"]:
         print(json.dumps({"calibration": "device copy", **copy_calibration(args.steps, args.warmup)}))
         return

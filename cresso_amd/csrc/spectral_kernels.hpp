@@ -108,7 +108,7 @@ struct Geom {
 };
 
 struct Offs {
-    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins, tbuf, part, part1, sums, hist, lt,
+    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins, tbuf, part, part1, sums, hist, hpart, lt,
         imp, rowfx, colfx, colfac, terms, ctrl, total;
 };
 
@@ -744,11 +744,25 @@ __device__ void reduce_bm(const double* __restrict__ part, int nblk, int V, doub
 // Cross-block merge of a sweep's partials spread over many CUs: block v sums
 // value v of every block (thread j: blocks j, j + 256, ... in order; then a
 // fixed-order DPP wave tree and the four wave totals in order) into sums[v].
+// Blocks VS.. reduce the matrix-core sweeps' per-block histogram partials
+// (hpart[bin][block], 64-bit fixed point; integer sums) into hist[bin].
 __global__ __launch_bounds__(256) void part_reduce_kernel(const double* __restrict__ part, int nblk, int VS,
-                                                          double* __restrict__ sums) {
+                                                          double* __restrict__ sums,
+                                                          const unsigned long long* __restrict__ hpart,
+                                                          unsigned long long* __restrict__ hist) {
     __shared__ double s_w[4];
+    __shared__ unsigned long long s_h[4];
     const int v = blockIdx.x;
-    (void)VS;
+    if (v >= VS) {
+        const int i = v - VS;
+        unsigned long long a = 0ull;
+        for (int b = threadIdx.x; b < nblk; b += 256) a += hpart[(size_t)i * nblk + b];
+        for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
+        if ((threadIdx.x & 63) == 0) s_h[threadIdx.x >> 6] = a;
+        __syncthreads();
+        if (threadIdx.x == 0) hist[i] = s_h[0] + s_h[1] + s_h[2] + s_h[3];
+        return;
+    }
     double a = 0.0;
     for (int b = threadIdx.x; b < nblk; b += 256) a += part[(size_t)v * nblk + b];
     a = wave_total_d(a);
@@ -894,9 +908,10 @@ __device__ F1Values fin1_values(const Geom& g, const double* __restrict__ part1,
     // density histogram scale from this step's largest density: ds = rel^p with
     // rel = min(|f|/s + eps, 1e4) (margin for the hardware exp2/log2), times
     // the largest bin count, below 2^62
-    const double rmax = fmin(mx * (double)v.inv_s + (double)eps, 1.0e4);
-    const double dsmax = pow(rmax, h.energy_power) * 1.01 + 1.0;
-    v.hs_ds = ldexp(1.0, (int)floor(62.0 - log2(dsmax * ctrl->cmax)));
+    // (fp32 hardware log2 with margins: every block computes the same bound)
+    const float rmax = fminf(fmaf((float)mx, v.inv_s, eps), 1.0e4f);
+    const float l2ds = fmaxf((float)h.energy_power * flog2(rmax) + 0.0144f, 0.0f) + 1.01f;  // >= log2(rmax^p 1.01 + 1)
+    v.hs_ds = ldexp(1.0, (int)floorf(62.0f - l2ds - flog2((float)ctrl->cmax) - 0.01f));
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         *fr_state = fr;
         ctrl->scale = sc;
@@ -1485,14 +1500,25 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
     const float pw = (float)h.energy_power;
     const float sg = h.maximize ? -1.f : 1.f;
     const float hs = (float)f1.hs_ds;
+    // the lane's projection A operands, a_li(row 16 tr + 4 lg + r), held in
+    // registers: read from LDS inside the loop they would queue behind the
+    // histogram atomics (LDS operations complete in order)
+    float aJv[4][4];
+#pragma unroll
+    for (int tr = 0; tr < 4; ++tr)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            aJv[tr][r] = (li < RW && tr < nr / 16) ? s_ar[(16 * tr + 4 * lg + r) * RW + (li < RW ? li : 0)] : 0.f;
     f32x4m zacc[4];
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc) zacc[tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
     float aL = 0.f;
     float cD[4] = {0.f, 0.f, 0.f, 0.f};   // column density sums of the lane's 4 tile columns
     // Sums of log(1 + ds) are kept in log2 units (fin2 scales them by ln 2).
-    const int ntr = nr / 16;
-    for (int tr = 0; tr < ntr; ++tr) {
+    const int ntr = nr / 16;   // 2 or 4 (panels of 32 or 64 rows)
+#pragma unroll
+    for (int tr = 0; tr < 4; ++tr) {
+        if (tr >= ntr) break;
         float rs[4] = {0.f, 0.f, 0.f, 0.f};   // this row of tiles' density, per lane row
 #pragma unroll
         for (int tc = 0; tc < 4; ++tc) {
@@ -1515,10 +1541,7 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
             }
             // A of the projection: a_li(row 16 tr + 4 lg + r)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float aJ = li < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (li < RW ? li : 0)] : 0.f;
-                zacc[tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJ, Ls[r], zacc[tc], 0, 0, 0);
-            }
+            for (int r = 0; r < 4; ++r) zacc[tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJv[tr][r], Ls[r], zacc[tc], 0, 0, 0);
             if (tr + 1 < ntr) load_tile(tr + 1, tc);
             pin1(aL);
 #pragma unroll
@@ -1555,7 +1578,7 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
         unsigned long long v = 0ull;
 #pragma unroll
         for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-        if (v) atomicAdd(&hist[i], v);
+        hist[(size_t)i * gridDim.x + blockIdx.x] = v;   // this block's partial (hpart[bin][block])
     }
     Partials P{red, 2 + 2 * g.R, NV2};
     P.add(0, aL);
@@ -2243,7 +2266,7 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
         unsigned long long v = 0ull;
 #pragma unroll
         for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-        if (v) atomicAdd(&hist[i], v);
+        hist[(size_t)i * gridDim.x + blockIdx.x] = v;   // this block's partial (hpart[bin][block])
     }
     Partials P{red, 15 + 2 * g.R, NV3};
     const float mm[13] = {m_ee, 0.f, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
@@ -3030,6 +3053,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     double* part = at<double>(ws, o.part);
     double* sums = at<double>(ws, o.sums);
     unsigned long long* hist = at<unsigned long long>(ws, o.hist);
+    unsigned long long* hpart = at<unsigned long long>(ws, o.hpart);
     const unsigned long long* cooc = at<unsigned long long>(ws, o.cooc);
     float* lt = at<float>(ws, o.lt);
     float* imp = at<float>(ws, o.imp);
@@ -3058,10 +3082,14 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
         hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part1, rowfx, colfx,
                            ctrl, st.force_rms, h);
     const bool fast = fast_mode(g, hash_on, axes_on, h);
+    // the matrix-core sweeps write per-block histogram partials (hpart),
+    // which part_reduce sums into hist; the general sweeps add into hist
+    const bool m2 = fast && RM <= 8;
+    const bool m3 = fast && RM <= 8 && KC <= 12 && lds_sweep3m(g, kcp<KC>(), 2 * RM) <= SP_LDS_MAX;
     if constexpr (RM <= 8) {
-        if (fast) {
+        if (m2) {
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl, part,
-                               hist, rowfx, colfx, part1, st.force_rms, step, h);
+                               hpart, rowfx, colfx, part1, st.force_rms, step, h);
             goto swept2;
         }
     }
@@ -3072,7 +3100,8 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 0>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, h);
 swept2:
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2), dim3(256), 0, s, part, g.nblk, NV2, sums);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2 + (m2 ? g.T * g.B : 0)), dim3(256), 0, s, part, g.nblk, NV2, sums,
+                       hpart, hist);
     hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st,
                        ctrl, step, hash_on, hard, h);
     if (axes_on && g.ntrail > 1) {
@@ -3084,10 +3113,9 @@ swept2:
                            s, g, terms, colfac);
     }
     if constexpr (RM <= 8 && KC <= 12) {
-        const size_t l3m = lds_sweep3m(g, kcp<KC>(), 2 * RM);
-        if (fast && l3m <= SP_LDS_MAX) {
-            hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl, lt,
-                               rowfx, colfx, colfac, tbuf, part, hist, h);
+        if (m3) {
+            hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT>), grid, blk, lds_sweep3m(g, kcp<KC>(), 2 * RM), s, g, grad, rowtab,
+                               coltab, meta, bins, ctrl, lt, rowfx, colfx, colfac, tbuf, part, hpart, h);
             goto swept3;
         }
     }
@@ -3101,7 +3129,8 @@ swept3:
     // sweep4m writes the full drive: fin3 then forms the hash term's RMS from
     // the co-occurrence counts, and sweep 5 needs no bins
     const int c5c = (KC <= 12 && fast && cooc_closed(g)) ? 1 : 0;
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3), dim3(256), 0, s, part, g.nblk, NV3, sums);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 ? g.T * g.B : 0)), dim3(256), 0, s, part, g.nblk, NV3, sums,
+                       hpart, hist);
     hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
                        cooc, step, hash_on, hard, echo_on, c5c, h);
     if constexpr (KC <= 12) {

@@ -184,6 +184,8 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.part1 = take(sizeof(double) * 2 * (size_t)g.nblk1);   // sweep 1's sums and maxima, read by every block of sweep 2
     o.sums = take(sizeof(double) * (size_t)NVMAX);
     o.hist = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
+    // per-block histogram partials of the matrix-core sweeps (two tables of one-byte bins)
+    o.hpart = take(g.T == 2 && g.bpb == 1 ? sizeof(unsigned long long) * (size_t)g.T * g.B * g.nblk : 0);
     o.lt = take(sizeof(float) * (size_t)g.T * g.B);
     o.imp = take(sizeof(float) * (size_t)g.T * g.B);
     o.rowfx = take(sizeof(unsigned long long) * (size_t)g.rows);
@@ -422,7 +424,8 @@ extern "C" int32_t cresso_spectral_workspace_project(const cresso_spectral_plan*
     double* sums = at<double>(ws, P->o.sums);
     hipLaunchKernelGGL(ws_project_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, at<ModeMeta>(ws, P->o.meta),
                        at<float>(ws, P->o.rowtab), at<float>(ws, P->o.coltab), at<double>(ws, P->o.stats), x, part);
-    hipLaunchKernelGGL(part_reduce_kernel, dim3((unsigned)(2 * g.R)), dim3(256), 0, s, part, (int)blocks, 2 * g.R, sums);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3((unsigned)(2 * g.R)), dim3(256), 0, s, part, (int)blocks, 2 * g.R, sums,
+                       nullptr, nullptr);
     hipLaunchKernelGGL(ws_mean_kernel, dim3(1), dim3(64), 0, s, sums, 2 * g.R, 1.0 / (double)g.n, out);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace project");
