@@ -607,12 +607,25 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
                 for (int c = 0; c < 4; ++c) {
                     const float t = xk[c];
                     const float at = fabsf(t);
-                    const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+                    const float e = t - q1;
+                    // shape3a's 1/(d1 d2) and the novelty's 1/(1 + ex) from one reciprocal
+                    const float es = fexp2(k2 * at);
+                    const float d1 = 1.0f + es;
+                    const float d2 = fmaf(at, iclip, 1.0f);
+                    const float ex = fexp2(k2n * fabsf(e));
+                    const float dn1 = 1.0f + ex;
+                    const float d12 = d1 * d2;
+                    const float rr = frcp(d12 * dn1);
+                    const float inv = dn1 * rr;    // 1/(d1 d2)
+                    const float ri = d12 * rr;     // 1/(1 + ex)
+                    const float u = d2 * inv;      // 1/d1
+                    Shape3A z;
+                    z.th = fmaf(-es, u, u);
+                    z.rat = at * (d1 * inv);
+                    const float rt = fsqrt(fminf(at, clip2) + eps);
+                    z.root = at > 0.0f ? rt : 0.0f;
                     const float cm = fmaf(kt, at, fmaf(ko, z.root, fmaf(kb, z.th, kr * z.rat)));
                     const float core = xorsign(cm, t);
-                    const float e = t - q1;
-                    const float ex = fexp2(k2n * fabsf(e));
-                    const float ri = frcp(1.0f + ex);
                     const float nov = with_sign(fmaf(-ex, ri, ri), e);
                     const float drv = fmaf(kN, nov, fmaf(cD, e, core + cB));
                     xk[c] = drv;
@@ -698,13 +711,30 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
 
 // Both resident layouts in one launch (the layout is uniform per workgroup),
 // so the plan's resident tensors fill the CUs in one sequence of rounds.
+// Staggered start of a multi-round launch.  A resident workgroup streams its
+// tensor from HBM (pass A), computes on chip (passes B-D, no HBM traffic), then
+// streams the update (pass E).  With identical tensors on every CU all CUs are
+// in the same phase, so the HBM phases of the whole chip do not overlap any
+// compute phase.  Workgroups [lo, hi) of the first round (the second half of
+// the CUs) wait `ticks` of the constant 100 MHz clock before starting, which
+// keeps the two halves of the CUs in different phases for the whole launch.
+// The wait is bounded; results do not depend on it.
+struct Stagger {
+    int32_t lo, hi;
+    uint32_t ticks;
+};
+
 template <typename PT, typename GT, bool FAST>
 __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec* __restrict__ recs,
                                                                  int32_t* __restrict__ steps,
                                                                  const void* const* __restrict__ grads, int32_t first,
-                                                                 cresso_hyper h) {
+                                                                 cresso_hyper h, Stagger sg) {
     __shared__ double red[16 * SR_SLOTS];
     __shared__ int s_step;
+    if ((int32_t)blockIdx.x >= sg.lo && (int32_t)blockIdx.x < sg.hi) {
+        const uint64_t t0 = wall_clock64();
+        while (wall_clock64() - t0 < (uint64_t)sg.ticks) __builtin_amdgcn_s_sleep(32);
+    }
     if (recs[first + blockIdx.x].layout == L_ROWGROUP)
         resident_body<PT, GT, L_ROWGROUP, FAST>(recs, steps, grads, first, h, red, s_step);
     else
@@ -1724,7 +1754,16 @@ hipError_t launch_resident_v(const ScalarRec* recs, int32_t* steps, const void* 
                              size_t lds, const cresso_hyper& h, hipStream_t s) {
     const hipError_t e = allow_resident_lds<PT, GT, FAST>();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, FAST>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads, first, h);
+    // one resident workgroup per CU: a launch of more workgroups than CUs runs
+    // in rounds, staggered (see Stagger); 35 us is about 40 % of one 64 Ki-element
+    // tensor's time, the best of the offsets measured on MI355X
+    Stagger sg{0, 0, 0u};
+    int dev = 0, cus = 0;
+    if (FAST && hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 1 && cnt > cus)
+        sg = Stagger{cus / 2, cus, 3500u};
+    hipLaunchKernelGGL((scalar_resident_kernel<PT, GT, FAST>), dim3(cnt), dim3(SR_NT), lds, s, recs, steps, grads, first, h,
+                       sg);
     return hipGetLastError();
 }
 
