@@ -19,6 +19,7 @@ LIB_NAME = "libcresso_hip.so"
 ABI_VERSION = 2
 
 F32, F64, F16, BF16 = 0, 1, 2, 3
+CRESSO_OK, CRESSO_E_INVALID, CRESSO_E_HIP, CRESSO_E_UNSUPPORTED = 0, -1, -2, -3
 SPECTRAL_NOALLOC_MAX_BYTES = 32 << 20   # CRESSO_SPECTRAL_NOALLOC_MAX_BYTES
 DTYPE_CODE = {torch.float32: F32, torch.float64: F64, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -128,6 +129,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cresso_spectral_step.restype = c.c_int32
     lib.cresso_spectral_step.argtypes = [c.c_void_p, c.POINTER(SpectralDesc), c.c_void_p, c.c_size_t,
                                          c.POINTER(Hyper), c.c_void_p]
+    lib.cresso_spectral_batched_workspace_bytes.restype = c.c_size_t
+    lib.cresso_spectral_batched_workspace_bytes.argtypes = [c.c_void_p, c.c_int32]
+    lib.cresso_spectral_batched_workspace_init.restype = c.c_int32
+    lib.cresso_spectral_batched_workspace_init.argtypes = [c.c_void_p, c.c_int32, c.c_void_p, c.c_size_t,
+                                                           c.POINTER(Hyper), c.c_void_p]
+    lib.cresso_spectral_step_batched.restype = c.c_int32
+    lib.cresso_spectral_step_batched.argtypes = [c.c_void_p, c.POINTER(SpectralDesc), c.c_int32, c.c_void_p,
+                                                 c.c_size_t, c.POINTER(Hyper), c.c_void_p]
     lib.cresso_spectral_step_noalloc.restype = c.c_int32
     lib.cresso_spectral_step_noalloc.argtypes = [c.c_void_p, c.POINTER(SpectralDesc), c.POINTER(Hyper), c.c_void_p]
     lib.cresso_spectral_workspace_bins.restype = c.c_int32

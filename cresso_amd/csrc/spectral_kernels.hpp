@@ -108,8 +108,9 @@ struct Geom {
 };
 
 struct Offs {
-    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins, tbuf, part, part1, sums, hist, hpart, lt,
-        imp, rowfx, colfx, colfac, terms, ctrl, total;
+    size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins;   // shape tables
+    size_t tbuf, part, part1, sums, hist, hpart, lt, imp, rowfx, colfx, colfac, terms, ctrl, desc;   // per-step scratch
+    size_t total;
 };
 
 // per-step device scalars (written by finalize kernels)
@@ -137,6 +138,37 @@ struct SpecState {
     float *calcium_cos, *calcium_sin, *conf;
     float *hash_energy, *hash_impulse, *hash_refractory;
 };
+
+__host__ __device__ inline SpecState spec_state(const cresso_spectral_desc& d) {
+    SpecState st;
+    st.force_rms = (float*)d.force_rms; st.drive_energy = (float*)d.drive_energy;
+    st.surprise = (float*)d.surprise; st.action = (float*)d.action; st.omega = (const float*)d.omega;
+    st.q_cos = (float*)d.q_cos; st.q_sin = (float*)d.q_sin; st.p_cos = (float*)d.p_cos; st.p_sin = (float*)d.p_sin;
+    st.metric_cos = (float*)d.metric_cos; st.metric_sin = (float*)d.metric_sin;
+    st.metric_p_cos = (float*)d.metric_p_cos; st.metric_p_sin = (float*)d.metric_p_sin;
+    st.calcium_cos = (float*)d.calcium_cos; st.calcium_sin = (float*)d.calcium_sin; st.conf = (float*)d.mode_confidence;
+    st.hash_energy = (float*)d.hash_energy; st.hash_impulse = (float*)d.hash_impulse;
+    st.hash_refractory = (float*)d.hash_refractory;
+    return st;
+}
+
+// Tensors of one step launch.  A batched step runs several tensors of one
+// plan in each launch: blockIdx.y picks the tensor, whose per-step scratch
+// (tangent field, partials, histograms, control block, and a device copy of
+// its descriptor: grad, param, state pointers, step) sits blockIdx.y * ls
+// bytes after the first tensor's.  The shape tables (carrier tables, bins,
+// counts, closed-form stats) are shared.  A single-tensor launch passes
+// dv = nullptr and ls = 0 and takes its pointers from the kernel arguments;
+// its grid has one row.
+struct Lanes {
+    const cresso_spectral_desc* dv;   // the first tensor's descriptor copy, or nullptr
+    size_t ls;
+};
+template <typename T> __device__ __forceinline__ T* lane_at(T* p, const Lanes& L) {
+    using C = typename std::conditional<std::is_const<T>::value, const char, char>::type;
+    return reinterpret_cast<T*>(reinterpret_cast<C*>(p) + (size_t)blockIdx.y * L.ls);
+}
+__device__ __forceinline__ const cresso_spectral_desc& lane_desc(const Lanes& L) { return *lane_at(L.dv, L); }
 
 constexpr int NV2 = 2 + 2 * SP_MAXR;            // sum L, sum dens, proj L (C,S)
 constexpr int NV3 = 15 + 2 * SP_MAXR;           // see sweep3
@@ -746,10 +778,10 @@ __device__ void reduce_bm(const double* __restrict__ part, int nblk, int V, doub
 // fixed-order DPP wave tree and the four wave totals in order) into sums[v].
 // Blocks VS.. reduce the matrix-core sweeps' per-block histogram partials
 // (hpart[bin][block], 64-bit fixed point; integer sums) into hist[bin].
-__global__ __launch_bounds__(256) void part_reduce_kernel(const double* __restrict__ part, int nblk, int VS,
-                                                          double* __restrict__ sums,
-                                                          const unsigned long long* __restrict__ hpart,
-                                                          unsigned long long* __restrict__ hist) {
+__global__ __launch_bounds__(256) void part_reduce_kernel(
+    const double* __restrict__ part, int nblk, int VS, double* __restrict__ sums,
+    const unsigned long long* __restrict__ hpart, unsigned long long* __restrict__ hist, Lanes L) {
+    part = lane_at(part, L); sums = lane_at(sums, L); hpart = lane_at(hpart, L); hist = lane_at(hist, L);
     __shared__ double s_w[4];
     __shared__ unsigned long long s_h[4];
     const int v = blockIdx.x;
@@ -771,6 +803,8 @@ __global__ __launch_bounds__(256) void part_reduce_kernel(const double* __restri
     if (threadIdx.x == 0) sums[v] = ((s_w[0] + s_w[1]) + s_w[2]) + s_w[3];
 }
 
+
+
 // The merged sums of a sweep into LDS (all loads in flight).
 __device__ void load_sums(const double* __restrict__ sums, int V, double* out) {
     for (int v = threadIdx.x; v < V; v += blockDim.x) out[v] = sums[v];
@@ -783,10 +817,15 @@ __device__ void load_sums(const double* __restrict__ sums, int V, double* out) {
 // Each block also clears its slice of the axis density sums (rows, then
 // columns) for this step's sweep 2.
 template <typename PT, typename GT, bool V4>
-__global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restrict__ grad, const PT* __restrict__ param,
-                                                       double* __restrict__ part, unsigned long long* __restrict__ rowfx,
-                                                       unsigned long long* __restrict__ colfx, Ctrl* __restrict__ ctrl,
-                                                       const float* __restrict__ fr_state, cresso_hyper h) {
+__global__ __launch_bounds__(SP_NT) void sweep1_kernel(
+    Geom g, const GT* __restrict__ grad, const PT* __restrict__ param, double* __restrict__ part,
+    unsigned long long* __restrict__ rowfx, unsigned long long* __restrict__ colfx, Ctrl* __restrict__ ctrl,
+    const float* __restrict__ fr_state, Lanes L, cresso_hyper h) {
+    if (L.dv) {
+        const cresso_spectral_desc& d = lane_desc(L);
+        grad = (const GT*)d.grad; param = (const PT*)d.param; fr_state = (const float*)d.force_rms;
+    }
+    part = lane_at(part, L); rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L); ctrl = lane_at(ctrl, L);
     __shared__ float red[4];
     if (blockIdx.x == 0 && threadIdx.x == 0) ctrl->fr_prev = *fr_state;   // every block of sweep 2 reads the old value
     {
@@ -869,6 +908,8 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(Geom g, const GT* __restr
         part[(size_t)g.nblk1 + blockIdx.x] = (double)mm;
     }
 }
+
+
 
 // F1, in every block of sweep 2: sweep 1's block partials summed in a fixed
 // order (so every block gets the same values), then the force-RMS reservoir
@@ -1245,7 +1286,13 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     const float* __restrict__ coltab, const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins,
     Ctrl* __restrict__ ctrl, double* __restrict__ part, unsigned long long* __restrict__ hist,
     unsigned long long* __restrict__ rowfx, unsigned long long* __restrict__ colfx, int hash_arg, int axes_arg,
-    const double* __restrict__ part1, float* __restrict__ fr_state, int step, cresso_hyper h) {
+    const double* __restrict__ part1, float* __restrict__ fr_state, int step, Lanes L, cresso_hyper h) {
+    if (L.dv) {
+        const cresso_spectral_desc& d = lane_desc(L);
+        grad = (const GT*)d.grad; param = (const PT*)d.param; fr_state = (float*)d.force_rms; step = d.step;
+    }
+    ctrl = lane_at(ctrl, L); part = lane_at(part, L); hist = lane_at(hist, L);
+    rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L); part1 = lane_at(part1, L);
     constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV2];
@@ -1413,6 +1460,8 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     P.flush(part);
 }
 
+
+
 // Helpers of the matrix-core sweeps.
 typedef float f32x4m __attribute__((ext_vector_type(4)));
 constexpr int SP_BQS = SP_NT + 16;   // row stride of sweep3m's LDS carrier table
@@ -1453,7 +1502,13 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl,
     double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ rowfx,
     unsigned long long* __restrict__ colfx, const double* __restrict__ part1, float* __restrict__ fr_state, int step,
-    cresso_hyper h) {
+    Lanes L, cresso_hyper h) {
+    if (L.dv) {
+        const cresso_spectral_desc& d = lane_desc(L);
+        grad = (const GT*)d.grad; fr_state = (float*)d.force_rms; step = d.step;
+    }
+    ctrl = lane_at(ctrl, L); part = lane_at(part, L); hist = lane_at(hist, L);
+    rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L); part1 = lane_at(part1, L);
     static_assert(RM <= 8, "16 projection rows");
     constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
@@ -1618,6 +1673,8 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
     P.flush(part);
 }
 
+
+
 // ---------------------------------------------------------------------------
 // finalize helpers: one wave, one lane per mode
 // ---------------------------------------------------------------------------
@@ -1673,13 +1730,16 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf
 // ---------------------------------------------------------------------------
 // F2: hash metric, metric oscillator, recon coefficients
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                        const double* __restrict__ stats, const double* __restrict__ bounds,
-                                                        const double* __restrict__ part,
-                                                        unsigned long long* __restrict__ hist,
-                                                        const unsigned long long* __restrict__ counts,
-                                                        float* __restrict__ lt, SpecState st, Ctrl* __restrict__ ctrl,
-                                                        int step, int hash_on, int hard, cresso_hyper h) {
+__global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
+    Geom g, const ModeMeta* __restrict__ meta, const double* __restrict__ stats, const double* __restrict__ bounds,
+    const double* __restrict__ part, unsigned long long* __restrict__ hist,
+    const unsigned long long* __restrict__ counts, float* __restrict__ lt, SpecState st, Ctrl* __restrict__ ctrl,
+    int step, int hash_on, int hard, Lanes L, cresso_hyper h) {
+    if (L.dv) {
+        st = spec_state(lane_desc(L));
+        step = lane_desc(L).step;
+    }
+    part = lane_at(part, L); hist = lane_at(hist, L); lt = lane_at(lt, L); ctrl = lane_at(ctrl, L);
     __shared__ double s_v[NV2];
     __shared__ double red[SP_FN_NT / 64];
     __shared__ float s_emean[SP_MAXT];
@@ -1792,15 +1852,18 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(Geom g, const ModeMeta* 
     }
 }
 
+
+
 // ndim >= 3: the factor of each column of the column group (the trailing
 // axes) is the product over those axes of (axis mean / global mean)^kappa.
 // marg_terms_kernel: one block per coordinate k of trailing axis a sums the
 // column sums that share it (64-bit integers: exact in any order) into the
 // axis term kappa log(max(mean / gden, eps)).
 constexpr int SP_MARG_NT = 256;
-__global__ __launch_bounds__(SP_MARG_NT) void marg_terms_kernel(Geom g, const unsigned long long* __restrict__ colfx,
-                                                                float* __restrict__ terms, const Ctrl* __restrict__ ctrl,
-                                                                float eps) {
+__global__ __launch_bounds__(SP_MARG_NT) void marg_terms_kernel(
+    Geom g, const unsigned long long* __restrict__ colfx, float* __restrict__ terms, const Ctrl* __restrict__ ctrl,
+    float eps, Lanes L) {
+    colfx = lane_at(colfx, L); terms = lane_at(terms, L); ctrl = lane_at(ctrl, L);
     __shared__ unsigned long long red[SP_MARG_NT];
     // block -> (axis a, coordinate k); the axis terms are laid out axis after axis
     int64_t k = blockIdx.x, off = 0;
@@ -1831,9 +1894,12 @@ __global__ __launch_bounds__(SP_MARG_NT) void marg_terms_kernel(Geom g, const un
     }
 }
 
+
+
 // marg_fac_kernel: one thread per column, exp of the sum of its axis terms.
-__global__ __launch_bounds__(SP_MARG_NT) void marg_fac_kernel(Geom g, const float* __restrict__ terms,
-                                                              float* __restrict__ colfac) {
+__global__ __launch_bounds__(SP_MARG_NT) void marg_fac_kernel(
+    Geom g, const float* __restrict__ terms, float* __restrict__ colfac, Lanes L) {
+    terms = lane_at(terms, L); colfac = lane_at(colfac, L);
     const int64_t c = (int64_t)blockIdx.x * SP_MARG_NT + threadIdx.x;
     if (c >= g.cols) return;
     int64_t off = 0;
@@ -1849,6 +1915,8 @@ __global__ __launch_bounds__(SP_MARG_NT) void marg_fac_kernel(Geom g, const floa
     colfac[c] = expf(acc);
 }
 
+
+
 // ---------------------------------------------------------------------------
 // S3: tangent force, prediction error, port projection / histograms, t projection
 // ---------------------------------------------------------------------------
@@ -1858,7 +1926,13 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     const float* __restrict__ coltab, const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins,
     const Ctrl* __restrict__ ctrl, const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx,
     const unsigned long long* __restrict__ colfx, const float* __restrict__ colfac, float* __restrict__ tbuf,
-    double* __restrict__ part, unsigned long long* __restrict__ hist, int hash_arg, cresso_hyper h) {
+    double* __restrict__ part, unsigned long long* __restrict__ hist, int hash_arg, Lanes L, cresso_hyper h) {
+    if (L.dv) {
+        const cresso_spectral_desc& d = lane_desc(L);
+        grad = (const GT*)d.grad; param = (const PT*)d.param;
+    }
+    ctrl = lane_at(ctrl, L); lt = lane_at(lt, L); rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L);
+    colfac = lane_at(colfac, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L); hist = lane_at(hist, L);
     constexpr int RW = 2 * RM;
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV3];
@@ -2069,6 +2143,8 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     P.flush(part);
 }
 
+
+
 // ---------------------------------------------------------------------------
 // S3 on the matrix cores (MODE 1 tiles, RM <= 8, KC <= 12).  The element math
 // is sweep3_kernel's; the contractions run as v_mfma_f32_16x16x4f32 on 16 x 16
@@ -2089,9 +2165,12 @@ template <int RM, int KC, typename GT>
 __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
     Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
-    const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx, const unsigned long long* __restrict__ colfx,
-    const float* __restrict__ colfac, float* __restrict__ tbuf, double* __restrict__ part,
-    unsigned long long* __restrict__ hist, cresso_hyper h) {
+    const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx,
+    const unsigned long long* __restrict__ colfx, const float* __restrict__ colfac, float* __restrict__ tbuf,
+    double* __restrict__ part, unsigned long long* __restrict__ hist, Lanes L, cresso_hyper h) {
+    if (L.dv) grad = (const GT*)lane_desc(L).grad;
+    ctrl = lane_at(ctrl, L); lt = lane_at(lt, L); rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L);
+    colfac = lane_at(colfac, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L); hist = lane_at(hist, L);
     static_assert(RM <= 8 && KC <= 12, "16 projection rows, three K-chunks of four carriers");
     constexpr int RW = 2 * RM;
     constexpr int KP = kcp<KC>();
@@ -2310,6 +2389,8 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
     P.flush(part);
 }
 
+
+
 // ---------------------------------------------------------------------------
 // F3: surprise, hash impulse, confidence, contact, and every drive-shaping
 // coefficient that does not need the hash prediction's rms
@@ -2365,14 +2446,17 @@ __device__ void contact_bank_lanes(float& q, float& p, float port, float omega, 
 //     mean(t Xn_v) - (G u)_v: small corrections to a directly summed term.
 // So sweep 4 can write the drive without c5; the hash term's rms comes from
 // sweep 4's sums and is added in sweep 5.
-__global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* __restrict__ meta,
-                                                        const double* __restrict__ stats, const double* __restrict__ gram,
-                                                        const double* __restrict__ part,
-                                                        unsigned long long* __restrict__ hist,
-                                                        const unsigned long long* __restrict__ counts,
-                                                        float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
-                                                        const unsigned long long* __restrict__ cooc, int step, int hash_on,
-                                                        int hard, int echo_on, int c5_closed, cresso_hyper h) {
+__global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
+    Geom g, const ModeMeta* __restrict__ meta, const double* __restrict__ stats, const double* __restrict__ gram,
+    const double* __restrict__ part, unsigned long long* __restrict__ hist,
+    const unsigned long long* __restrict__ counts, float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
+    const unsigned long long* __restrict__ cooc, int step, int hash_on, int hard, int echo_on, int c5_closed, Lanes L,
+    cresso_hyper h) {
+    if (L.dv) {
+        st = spec_state(lane_desc(L));
+        step = lane_desc(L).step;
+    }
+    part = lane_at(part, L); hist = lane_at(hist, L); imp_tab = lane_at(imp_tab, L); ctrl = lane_at(ctrl, L);
     if (threadIdx.x == 0) ctrl->de_prev = *st.drive_energy;   // every block of sweep 5 reads the old value
     __shared__ double s_m[NV3];
     __shared__ double s_ec[2 * SP_MAXR];    // mean(t Xn_v)
@@ -2593,6 +2677,8 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(Geom g, const ModeMeta* 
     }
 }
 
+
+
 // ---------------------------------------------------------------------------
 // S4: drive without the hash term, written over t; sums for the drive energy
 // ---------------------------------------------------------------------------
@@ -2600,7 +2686,8 @@ template <int RM, int KC, int MODE>
 __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
     const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
-    float* __restrict__ tbuf, double* __restrict__ part, int hash_arg, int echo_on, cresso_hyper h) {
+    float* __restrict__ tbuf, double* __restrict__ part, int hash_arg, int echo_on, Lanes L, cresso_hyper h) {
+    ctrl = lane_at(ctrl, L); imp_tab = lane_at(imp_tab, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L);
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV4];
     const SweepFlags F = sweep_flags<MODE>(g, hash_arg, 1, h);
@@ -2722,6 +2809,8 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
     P.flush(part);
 }
 
+
+
 // ---------------------------------------------------------------------------
 // S4 on the matrix cores (MODE 1 tiles).  Each wave owns 64 columns of the
 // panel as 4 x 4 tiles of 16 x 16 elements.  A reconstruction of a tile is
@@ -2739,7 +2828,8 @@ template <int RM, int KC>
 __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
     const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
-    float* __restrict__ tbuf, double* __restrict__ part, int echo_on, cresso_hyper h) {
+    float* __restrict__ tbuf, double* __restrict__ part, int echo_on, Lanes L, cresso_hyper h) {
+    ctrl = lane_at(ctrl, L); imp_tab = lane_at(imp_tab, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L);
     static_assert(KC <= 12, "three K-chunks of four carriers");
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV4];
@@ -2857,6 +2947,8 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
     P.flush(part);
 }
 
+
+
 // F4, in every block of sweep 5: sweep 4's block partials summed in a fixed
 // order (so every block gets the same values), then the hash-term
 // coefficient, the drive-energy reservoir and the gain.  Block 0 stores the
@@ -2914,11 +3006,15 @@ __device__ __forceinline__ void apply1(PT* __restrict__ param, int64_t e, float 
 }
 
 template <typename PT, bool HASH, bool V4>
-__global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ param, const float* __restrict__ dbuf,
-                                                       const unsigned char* __restrict__ bins,
-                                                       const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
-                                                       const double* __restrict__ part, float* __restrict__ de_state,
-                                                       int step, int hash_on, int hard, int c5_closed, cresso_hyper h) {
+__global__ __launch_bounds__(SP_NT) void sweep5_kernel(
+    Geom g, PT* __restrict__ param, const float* __restrict__ dbuf, const unsigned char* __restrict__ bins,
+    const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab, const double* __restrict__ part,
+    float* __restrict__ de_state, int step, int hash_on, int hard, int c5_closed, Lanes L, cresso_hyper h) {
+    if (L.dv) {
+        const cresso_spectral_desc& d = lane_desc(L);
+        param = (PT*)d.param; de_state = (float*)d.drive_energy; step = d.step;
+    }
+    dbuf = lane_at(dbuf, L); ctrl = lane_at(ctrl, L); imp_tab = lane_at(imp_tab, L); part = lane_at(part, L);
     extern __shared__ __align__(16) unsigned char dyn[];
     const int64_t beg = (int64_t)blockIdx.x * g.chunk1;
     const int64_t end = beg + g.chunk1 < g.n ? beg + g.chunk1 : g.n;
@@ -2993,6 +3089,8 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(Geom g, PT* __restrict__ 
     for (int64_t e = vend + threadIdx.x; e < end; e += SP_NT) apply1(param, e, drive_at(e, dbuf[e]), gain, nlr);
 }
 
+
+
 }  // namespace
 }  // namespace cresso
 
@@ -3026,20 +3124,20 @@ size_t lds_sweep4(const Geom& g, int kp, int rw) {
 }
 constexpr size_t SP_LDS_MAX = 64 * 1024;
 
+// One step of `count` tensors of plan P: hd[0..count) are their descriptors
+// on the host; for count > 1, dv is the same array in device memory and each
+// tensor's per-step scratch follows the previous one's at a stride of ls
+// bytes (a single tensor passes dv = nullptr, ls = 0).  Each tensor's results
+// are bit-identical to a single-tensor step of it.
 template <int RM, int KC, typename PT, typename GT>
-int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws, const cresso_hyper& h,
-                 hipStream_t s) {
+int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, int count,
+                 const cresso_spectral_desc* dv, size_t ls, void* ws, const cresso_hyper& h, hipStream_t s) {
     const Geom& g = P.g;
     const Offs& o = P.o;
-    SpecState st;
-    st.force_rms = (float*)d.force_rms; st.drive_energy = (float*)d.drive_energy;
-    st.surprise = (float*)d.surprise; st.action = (float*)d.action; st.omega = (const float*)d.omega;
-    st.q_cos = (float*)d.q_cos; st.q_sin = (float*)d.q_sin; st.p_cos = (float*)d.p_cos; st.p_sin = (float*)d.p_sin;
-    st.metric_cos = (float*)d.metric_cos; st.metric_sin = (float*)d.metric_sin;
-    st.metric_p_cos = (float*)d.metric_p_cos; st.metric_p_sin = (float*)d.metric_p_sin;
-    st.calcium_cos = (float*)d.calcium_cos; st.calcium_sin = (float*)d.calcium_sin; st.conf = (float*)d.mode_confidence;
-    st.hash_energy = (float*)d.hash_energy; st.hash_impulse = (float*)d.hash_impulse;
-    st.hash_refractory = (float*)d.hash_refractory;
+    const cresso_spectral_desc& d = hd[0];
+    const SpecState st = spec_state(d);
+    const Lanes L{dv, ls};
+    const unsigned ny = (unsigned)count;
     const int hash_on = d.hash_energy != nullptr && g.B > 0 && P.g.T > 0 ? 1 : 0;
     const int hard = d.hard ? 1 : 0;
     const int echo_on = (hard && h.echo_mix != 0.0) ? 1 : 0;
@@ -3073,14 +3171,20 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     if (l2 > SP_LDS_MAX || l3 > SP_LDS_MAX || l4 > SP_LDS_MAX)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_tables x hash_bins = %d needs %zu bytes of LDS per block",
                     g.T * g.B, std::max(l2, std::max(l3, l4)));
-    const dim3 grid(g.nblk), blk(SP_NT);
-    const bool v4 = ((uintptr_t)grad % (4 * sizeof(GT))) == 0 && ((uintptr_t)param % (4 * sizeof(PT))) == 0;
+    const dim3 grid(g.nblk, ny), grid1(g.nblk1, ny), fin(1, ny), blk(SP_NT);
+    // float4 loads and stores when every tensor's grad and param allow them
+    bool v4 = true, pv4 = true;
+    for (int i = 0; i < count; ++i) {
+        pv4 = pv4 && ((uintptr_t)hd[i].param % (4 * sizeof(PT))) == 0;
+        v4 = v4 && ((uintptr_t)hd[i].grad % (4 * sizeof(GT))) == 0;
+    }
+    v4 = v4 && pv4;
     if (v4)
-        hipLaunchKernelGGL((sweep1_kernel<PT, GT, true>), dim3(g.nblk1), blk, 0, s, g, grad, param, part1, rowfx, colfx,
-                           ctrl, st.force_rms, h);
+        hipLaunchKernelGGL((sweep1_kernel<PT, GT, true>), grid1, blk, 0, s, g, grad, param, part1, rowfx, colfx, ctrl,
+                           st.force_rms, L, h);
     else
-        hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), dim3(g.nblk1), blk, 0, s, g, grad, param, part1, rowfx, colfx,
-                           ctrl, st.force_rms, h);
+        hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), grid1, blk, 0, s, g, grad, param, part1, rowfx, colfx, ctrl,
+                           st.force_rms, L, h);
     const bool fast = fast_mode(g, hash_on, axes_on, h);
     // the matrix-core sweeps write per-block histogram partials (hpart),
     // which part_reduce sums into hist; the general sweeps add into hist
@@ -3089,94 +3193,93 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc& d, v
     if constexpr (RM <= 8) {
         if (m2) {
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl, part,
-                               hpart, rowfx, colfx, part1, st.force_rms, step, h);
+                               hpart, rowfx, colfx, part1, st.force_rms, step, L, h);
             goto swept2;
         }
     }
     if (fast)
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, h);
+                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
     else
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 0>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, h);
+                           ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
 swept2:
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2 + (m2 ? g.T * g.B : 0)), dim3(256), 0, s, part, g.nblk, NV2, sums,
-                       hpart, hist);
-    hipLaunchKernelGGL(fin2_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st,
-                       ctrl, step, hash_on, hard, h);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2 + (m2 ? g.T * g.B : 0), ny), dim3(256), 0, s, part, g.nblk, NV2, sums,
+                       hpart, hist, L);
+    hipLaunchKernelGGL(fin2_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st, ctrl,
+                       step, hash_on, hard, L, h);
     if (axes_on && g.ntrail > 1) {
         int64_t nterms = 0;
         for (int a = 0; a < g.ntrail; ++a) nterms += g.tdim[a];
-        hipLaunchKernelGGL(marg_terms_kernel, dim3((unsigned)nterms), dim3(SP_MARG_NT), 0, s, g, colfx, terms, ctrl,
-                           (float)h.eps);
-        hipLaunchKernelGGL(marg_fac_kernel, dim3((unsigned)((g.cols + SP_MARG_NT - 1) / SP_MARG_NT)), dim3(SP_MARG_NT), 0,
-                           s, g, terms, colfac);
+        hipLaunchKernelGGL(marg_terms_kernel, dim3((unsigned)nterms, ny), dim3(SP_MARG_NT), 0, s, g, colfx, terms, ctrl,
+                           (float)h.eps, L);
+        hipLaunchKernelGGL(marg_fac_kernel, dim3((unsigned)((g.cols + SP_MARG_NT - 1) / SP_MARG_NT), ny), dim3(SP_MARG_NT),
+                           0, s, g, terms, colfac, L);
     }
     if constexpr (RM <= 8 && KC <= 12) {
         if (m3) {
             hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT>), grid, blk, lds_sweep3m(g, kcp<KC>(), 2 * RM), s, g, grad, rowtab,
-                               coltab, meta, bins, ctrl, lt, rowfx, colfx, colfac, tbuf, part, hpart, h);
+                               coltab, meta, bins, ctrl, lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h);
             goto swept3;
         }
     }
     if (fast)
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 1>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
+                           ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, L, h);
     else
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 0>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
-                           ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, h);
+                           ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, L, h);
 swept3:
     // sweep4m writes the full drive: fin3 then forms the hash term's RMS from
     // the co-occurrence counts, and sweep 5 needs no bins
     const int c5c = (KC <= 12 && fast && cooc_closed(g)) ? 1 : 0;
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 ? g.T * g.B : 0)), dim3(256), 0, s, part, g.nblk, NV3, sums,
-                       hpart, hist);
-    hipLaunchKernelGGL(fin3_kernel, dim3(1), dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
-                       cooc, step, hash_on, hard, echo_on, c5c, h);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 ? g.T * g.B : 0), ny), dim3(256), 0, s, part, g.nblk, NV3, sums,
+                       hpart, hist, L);
+    hipLaunchKernelGGL(fin3_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
+                       cooc, step, hash_on, hard, echo_on, c5c, L, h);
     if constexpr (KC <= 12) {
         if (c5c) {
             hipLaunchKernelGGL((sweep4m_kernel<RM, KC>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf,
-                               part, echo_on, h);
+                               part, echo_on, L, h);
             goto swept4;
         }
     }
     if (fast)
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
-                           hash_on, echo_on, h);
+                           hash_on, echo_on, L, h);
     else
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 0>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
-                           hash_on, echo_on, h);
+                           hash_on, echo_on, L, h);
 swept4:
     const bool hash5 = hash_on && !c5c;   // sweep 5 adds the hash term itself
     const size_t l5 = hash5 ? sizeof(float) * (size_t)g.T * g.B : 0;
-    const bool pv4 = ((uintptr_t)param % (4 * sizeof(PT))) == 0;
     if (hash5 && pv4)
-        hipLaunchKernelGGL((sweep5_kernel<PT, true, true>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, part,
-                           st.drive_energy, step, hash_on, hard, c5c, h);
+        hipLaunchKernelGGL((sweep5_kernel<PT, true, true>), grid1, blk, l5, s, g, param, tbuf, bins, ctrl, imp, part,
+                           st.drive_energy, step, hash_on, hard, c5c, L, h);
     else if (hash5)
-        hipLaunchKernelGGL((sweep5_kernel<PT, true, false>), dim3(g.nblk1), blk, l5, s, g, param, tbuf, bins, ctrl, imp, part,
-                           st.drive_energy, step, hash_on, hard, c5c, h);
+        hipLaunchKernelGGL((sweep5_kernel<PT, true, false>), grid1, blk, l5, s, g, param, tbuf, bins, ctrl, imp, part,
+                           st.drive_energy, step, hash_on, hard, c5c, L, h);
     else if (pv4)
-        hipLaunchKernelGGL((sweep5_kernel<PT, false, true>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, part,
-                           st.drive_energy, step, hash_on, hard, c5c, h);
+        hipLaunchKernelGGL((sweep5_kernel<PT, false, true>), grid1, blk, 0, s, g, param, tbuf, bins, ctrl, imp, part,
+                           st.drive_energy, step, hash_on, hard, c5c, L, h);
     else
-        hipLaunchKernelGGL((sweep5_kernel<PT, false, false>), dim3(g.nblk1), blk, 0, s, g, param, tbuf, bins, ctrl, imp, part,
-                           st.drive_energy, step, hash_on, hard, c5c, h);
+        hipLaunchKernelGGL((sweep5_kernel<PT, false, false>), grid1, blk, 0, s, g, param, tbuf, bins, ctrl, imp, part,
+                           st.drive_energy, step, hash_on, hard, c5c, L, h);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: launch");
 }
 
 // Variant dispatch shared by the instantiation units.
 template <typename PT, typename GT>
-int32_t spectral_run(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws, const cresso_hyper& h,
-                     hipStream_t s) {
+int32_t spectral_run(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, int count,
+                     const cresso_spectral_desc* dv, size_t ls, void* ws, const cresso_hyper& h, hipStream_t s) {
     const int R = P.g.R, K = P.g.K;
     const int var = (R <= 4 && K <= 9) ? 0 : (R <= 8 && K <= 11) ? 1 : (R <= 8) ? 2 : 3;
     switch (var) {
-        case 0: return run_step<4, 9, PT, GT>(P, d, ws, h, s);
-        case 1: return run_step<8, 11, PT, GT>(P, d, ws, h, s);
-        case 2: return run_step<8, 17, PT, GT>(P, d, ws, h, s);
-        default: return run_step<16, 33, PT, GT>(P, d, ws, h, s);
+        case 0: return run_step<4, 9, PT, GT>(P, hd, count, dv, ls, ws, h, s);
+        case 1: return run_step<8, 11, PT, GT>(P, hd, count, dv, ls, ws, h, s);
+        case 2: return run_step<8, 17, PT, GT>(P, hd, count, dv, ls, ws, h, s);
+        default: return run_step<16, 33, PT, GT>(P, hd, count, dv, ls, ws, h, s);
     }
 }
 
@@ -3186,9 +3289,11 @@ int32_t spectral_run(const cresso_spectral_plan& P, const cresso_spectral_desc& 
 // its own translation unit (spectral_step_<pt>_<gt>.hip) so they compile in
 // parallel.  The carrier-count variant (rank and distinct column carriers
 // fixed at compile time) is chosen inside.
-typedef int32_t (*SpectralRunFn)(const cresso_spectral_plan&, const cresso_spectral_desc&, void*, const cresso_hyper&,
-                                 hipStream_t);
-#define CRESSO_SP_DECL(NAME) int32_t NAME(const cresso_spectral_plan&, const cresso_spectral_desc&, void*, const cresso_hyper&, hipStream_t);
+typedef int32_t (*SpectralRunFn)(const cresso_spectral_plan&, const cresso_spectral_desc*, int,
+                                 const cresso_spectral_desc*, size_t, void*, const cresso_hyper&, hipStream_t);
+#define CRESSO_SP_DECL(NAME)                                                                                      \
+    int32_t NAME(const cresso_spectral_plan&, const cresso_spectral_desc*, int, const cresso_spectral_desc*, size_t, \
+                 void*, const cresso_hyper&, hipStream_t);
 CRESSO_SP_DECL(spectral_run_f32_f32)
 CRESSO_SP_DECL(spectral_run_bf16_bf16)
 CRESSO_SP_DECL(spectral_run_f16_f16)

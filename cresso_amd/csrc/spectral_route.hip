@@ -195,6 +195,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     for (int a = 0; a < g.ntrail; ++a) sum_trail += g.tdim[a];
     o.terms = take(sizeof(float) * (size_t)std::max<int64_t>(1, sum_trail));
     o.ctrl = take(sizeof(Ctrl));
+    o.desc = take(sizeof(cresso_spectral_desc));   // the tensor's descriptor in a batched step
     o.total = off;
     return CRESSO_OK;
 }
@@ -295,10 +296,8 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace init");
 }
 
-extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cresso_spectral_desc* d, void* ws,
-                                        size_t ws_bytes, const cresso_hyper* hyper, void* stream) {
-    if (!P || !d || !ws || !hyper) return fail(CRESSO_E_INVALID, "spectral route: null argument");
-    if (ws_bytes < P->o.total) return fail(CRESSO_E_INVALID, "spectral route: workspace too small");
+namespace {
+int32_t check_desc(const cresso_spectral_plan* P, const cresso_spectral_desc* d) {
     const Geom& g = P->g;
     if (d->numel != g.n) return fail(CRESSO_E_INVALID, "spectral route: numel %lld does not match the plan", (long long)d->numel);
     if (!d->param || !d->grad) return fail(CRESSO_E_INVALID, "spectral route: null param or grad");
@@ -310,10 +309,11 @@ extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cre
     if (d->hash_energy && (!d->hash_impulse || !d->hash_refractory))
         return fail(CRESSO_E_INVALID, "spectral route: partial hash state");
     if (d->step < 1) return fail(CRESSO_E_INVALID, "spectral route: step must be >= 1 (after the increment)");
-    if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "spectral route: drive_clip must be positive");
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int pt = d->param_dtype, gt = d->grad_dtype;
-    // (param dtype, grad dtype) -> the unit that instantiates the step for it
+    return CRESSO_OK;
+}
+
+// (param dtype, grad dtype) -> the unit that instantiates the step for it
+SpectralRunFn find_run(int pt, int gt) {
     static const struct { int pt, gt; SpectralRunFn fn; } table[] = {
         {CRESSO_F32, CRESSO_F32, spectral_run_f32_f32},
         {CRESSO_BF16, CRESSO_BF16, spectral_run_bf16_bf16},
@@ -322,8 +322,111 @@ extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cre
         {CRESSO_F32, CRESSO_F16, spectral_run_f32_f16},
     };
     for (const auto& e : table)
-        if (e.pt == pt && e.gt == gt) return e.fn(*P, *d, ws, *hyper, s);
-    return fail(CRESSO_E_UNSUPPORTED, "spectral route: param/grad dtype pair (%d,%d) not supported by this build", pt, gt);
+        if (e.pt == pt && e.gt == gt) return e.fn;
+    fail(CRESSO_E_UNSUPPORTED, "spectral route: param/grad dtype pair (%d,%d) not supported by this build", pt, gt);
+    return nullptr;
+}
+
+// Layout of a batched workspace: the plan's shape tables once, then `count`
+// lanes, each a copy of the single workspace's per-step scratch (from tbuf to
+// the end, its device copy of the tensor's descriptor included).
+size_t lane_stride(const cresso_spectral_plan* P) { return P->o.total - P->o.tbuf; }
+size_t batched_bytes(const cresso_spectral_plan* P, int count) { return P->o.tbuf + (size_t)count * lane_stride(P); }
+
+// The descriptors travel to the device as kernel arguments, DESC_CHUNK per
+// launch (no staging buffer, no host synchronization).
+constexpr int DESC_CHUNK = 16;
+struct DescChunk {
+    cresso_spectral_desc d[DESC_CHUNK];
+};
+static_assert(sizeof(DescChunk) + 16 <= 4096, "descriptor chunk exceeds the kernel argument limit");
+static_assert(sizeof(cresso_spectral_desc) % 8 == 0, "descriptor copied as 64-bit words");
+__global__ __launch_bounds__(256) void put_descs_kernel(DescChunk c, int n, unsigned char* __restrict__ dst, size_t ls) {
+    constexpr int W = (int)(sizeof(cresso_spectral_desc) / 8);
+    const unsigned long long* src = reinterpret_cast<const unsigned long long*>(&c.d[0]);
+    for (int i = threadIdx.x; i < n * W; i += blockDim.x)
+        reinterpret_cast<unsigned long long*>(dst + (size_t)(i / W) * ls)[i % W] = src[i];
+}
+
+// Lanes 1.. of a batched workspace start as lane 0 after its set-up: the same
+// control block (its data-independent scale bound) and cleared histograms.
+__global__ __launch_bounds__(256) void ws_lanes_kernel(unsigned char* __restrict__ lane0, size_t ls, size_t ctrl_off,
+                                                       size_t hist_off, int64_t tb) {
+    unsigned char* ln = lane0 + (size_t)(blockIdx.x + 1) * ls;
+    const unsigned long long* c0 = reinterpret_cast<const unsigned long long*>(lane0 + ctrl_off);
+    unsigned long long* c = reinterpret_cast<unsigned long long*>(ln + ctrl_off);
+    for (int i = threadIdx.x; i < (int)(sizeof(Ctrl) / 8); i += blockDim.x) c[i] = c0[i];
+    unsigned long long* hh = reinterpret_cast<unsigned long long*>(ln + hist_off);
+    for (int64_t i = threadIdx.x; i < tb; i += blockDim.x) hh[i] = 0ull;
+}
+static_assert(sizeof(Ctrl) % 8 == 0, "control block copied as 64-bit words");
+}  // namespace
+
+extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cresso_spectral_desc* d, void* ws,
+                                        size_t ws_bytes, const cresso_hyper* hyper, void* stream) {
+    if (!P || !d || !ws || !hyper) return fail(CRESSO_E_INVALID, "spectral route: null argument");
+    if (ws_bytes < P->o.total) return fail(CRESSO_E_INVALID, "spectral route: workspace too small");
+    const int32_t rc = check_desc(P, d);
+    if (rc != CRESSO_OK) return rc;
+    if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "spectral route: drive_clip must be positive");
+    const SpectralRunFn fn = find_run(d->param_dtype, d->grad_dtype);
+    if (!fn) return CRESSO_E_UNSUPPORTED;
+    return fn(*P, d, 1, nullptr, 0, ws, *hyper, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t cresso_spectral_batched_workspace_bytes(const cresso_spectral_plan* P, int32_t count) {
+    return P && count >= 1 ? batched_bytes(P, count) : 0;
+}
+
+extern "C" int32_t cresso_spectral_batched_workspace_init(const cresso_spectral_plan* P, int32_t count, void* ws,
+                                                          size_t ws_bytes, const cresso_hyper* hyper, void* stream) {
+    if (!P || !ws || !hyper) return fail(CRESSO_E_INVALID, "spectral route: null argument");
+    if (count < 1) return fail(CRESSO_E_INVALID, "spectral route: batch of %d tensors", count);
+    if (ws_bytes < batched_bytes(P, count))
+        return fail(CRESSO_E_INVALID, "spectral route: batched workspace of %zu bytes is smaller than %zu", ws_bytes,
+                    batched_bytes(P, count));
+    int32_t rc = cresso_spectral_workspace_init(P, ws, P->o.total, hyper, stream);
+    if (rc != CRESSO_OK || count == 1) return rc;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const Offs& o = P->o;
+    hipLaunchKernelGGL(ws_lanes_kernel, dim3((unsigned)(count - 1)), dim3(256), 0, s, at<unsigned char>(ws, o.tbuf),
+                       lane_stride(P), o.ctrl - o.tbuf, o.hist - o.tbuf, (int64_t)P->g.T * P->g.B);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: batched workspace init");
+}
+
+extern "C" int32_t cresso_spectral_step_batched(const cresso_spectral_plan* P, const cresso_spectral_desc* descs,
+                                                int32_t count, void* ws, size_t ws_bytes, const cresso_hyper* hyper,
+                                                void* stream) {
+    if (!P || !descs || !ws || !hyper) return fail(CRESSO_E_INVALID, "spectral route: null argument");
+    if (count < 1) return fail(CRESSO_E_INVALID, "spectral route: batch of %d tensors", count);
+    if (ws_bytes < batched_bytes(P, count))
+        return fail(CRESSO_E_INVALID, "spectral route: batched workspace too small for %d tensors", count);
+    if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "spectral route: drive_clip must be positive");
+    const cresso_spectral_desc& d0 = descs[0];
+    for (int i = 0; i < count; ++i) {
+        const cresso_spectral_desc& d = descs[i];
+        const int32_t rc = check_desc(P, &d);
+        if (rc != CRESSO_OK) return rc;
+        if (d.param_dtype != d0.param_dtype || d.grad_dtype != d0.grad_dtype)
+            return fail(CRESSO_E_INVALID, "spectral route: tensor %d of a batch has other dtypes than tensor 0", i);
+        if ((d.hard != 0) != (d0.hard != 0) || (d.hash_energy != nullptr) != (d0.hash_energy != nullptr))
+            return fail(CRESSO_E_INVALID, "spectral route: tensor %d of a batch differs from tensor 0 in the hard "
+                        "channel or the hash state", i);
+    }
+    const SpectralRunFn fn = find_run(d0.param_dtype, d0.grad_dtype);
+    if (!fn) return CRESSO_E_UNSUPPORTED;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const size_t ls = lane_stride(P);
+    for (int i0 = 0; i0 < count; i0 += DESC_CHUNK) {
+        DescChunk c;
+        const int n = std::min(DESC_CHUNK, count - i0);
+        std::memset(&c, 0, sizeof(c));
+        std::memcpy(&c.d[0], descs + i0, sizeof(cresso_spectral_desc) * (size_t)n);
+        hipLaunchKernelGGL(put_descs_kernel, dim3(1), dim3(256), 0, s, c, n, at<unsigned char>(ws, P->o.desc + i0 * ls), ls);
+    }
+    return fn(*P, descs, count, at<cresso_spectral_desc>(ws, P->o.desc), ls, ws, *hyper, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -425,7 +528,7 @@ extern "C" int32_t cresso_spectral_workspace_project(const cresso_spectral_plan*
     hipLaunchKernelGGL(ws_project_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, at<ModeMeta>(ws, P->o.meta),
                        at<float>(ws, P->o.rowtab), at<float>(ws, P->o.coltab), at<double>(ws, P->o.stats), x, part);
     hipLaunchKernelGGL(part_reduce_kernel, dim3((unsigned)(2 * g.R)), dim3(256), 0, s, part, (int)blocks, 2 * g.R, sums,
-                       nullptr, nullptr);
+                       nullptr, nullptr, Lanes{nullptr, 0});
     hipLaunchKernelGGL(ws_mean_kernel, dim3(1), dim3(64), 0, s, sums, 2 * g.R, 1.0 / (double)g.n, out);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace project");

@@ -3,8 +3,8 @@
 #include "spectral_kernels.hpp"
 
 namespace cresso {
-int32_t spectral_run_f32_bf16(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws,
-                             const cresso_hyper& h, hipStream_t s) {
-    return spectral_run<float, __hip_bfloat16>(P, d, ws, h, s);
+int32_t spectral_run_f32_bf16(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, int count,
+                            const cresso_spectral_desc* dv, size_t ls, void* ws, const cresso_hyper& h, hipStream_t s) {
+    return spectral_run<float, __hip_bfloat16>(P, hd, count, dv, ls, ws, h, s);
 }
 }  // namespace cresso

@@ -1,18 +1,28 @@
-"""Host orchestration of the spectral/hash route (one C call per tensor and step).
+"""Host orchestration of the spectral/hash route.
 
 The library keeps no state of its own: plans live here, keyed by
 (device, shape, freqs, hash_bins, hash_tables), together with their device
 workspace (carrier tables, cached coordinate-hash bins, scratch).
 
-A step of several spectral tensors (`step_many`) spreads them over up to
-LANES side streams (default priority), so that one tensor's small finish
-kernels and partly filled sweeps overlap with another's work.  Every lane
-has its own workspace per shape: tensors that share a workspace run one
-after another on that lane's stream, so its per-step scratch is never used
-concurrently.  The side streams wait for the caller's stream before the
-first launch and the caller's stream waits for all of them after the last,
-so the step is ordered like any other work on the caller's stream.  A
-single spectral tensor runs on the caller's stream directly.
+A step of several spectral tensors (`step_many`) first batches the tensors
+that share a plan (and dtypes, hard channel and hash state): one batched C
+call steps a batch, every launch covering all its tensors, with the plan's
+tables held once and per-step scratch (about 4 bytes per element plus a few
+KB) once per tensor.  A batch holds at most BATCH_BYTES of such scratch;
+larger groups are cut into that many chunks.  The units of work (batches and
+single tensors) are spread over up to LANES side streams (default priority),
+so that one unit's small finish kernels and partly filled sweeps overlap
+with another's work.  Every lane has its own workspace per unit kind: units
+that share a workspace run one after another on that lane's stream, so its
+per-step scratch is never used concurrently.  The side streams wait for the
+caller's stream before the first launch and the caller's stream waits for
+all of them after the last, so the step is ordered like any other work on
+the caller's stream.  A single spectral tensor runs on the caller's stream
+directly.
+
+Device memory held: per (plan, lane) a workspace of the plan's tables (about
+(2 + 4) bytes per element at two tables of <= 256 bins) and its scratch;
+`reset()` (called by the optimizer's load_state_dict) frees them all.
 """
 
 from __future__ import annotations
@@ -57,9 +67,13 @@ def assign_lanes(keys: Sequence[tuple], lanes: int) -> List[int]:
 
 
 class _Workspace:
+    """A plan with its device workspace: for one tensor (count=None) or for
+    batches of up to `count` tensors."""
+
     def __init__(self, lib, shape, freqs_host: Tuple[int, ...], rank: int, bins: int, tables: int, group: dict,
-                 device: torch.device):
+                 device: torch.device, count=None):
         self.lib = lib
+        self.count = count
         nd = len(shape)
         shp = (ctypes.c_int64 * 8)(*shape)
         fr = (ctypes.c_int64 * max(1, len(freqs_host)))(*freqs_host)
@@ -67,13 +81,19 @@ class _Workspace:
         if not plan:
             _native.check(-1, "spectral route plan")
         self.plan = ctypes.c_void_p(plan)
-        nbytes = int(lib.cresso_spectral_workspace_bytes(self.plan))
-        self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
         hyper = _native.hyper_from_group(group)
-        stream = _native.stream_handle(device)
-        _native.check(lib.cresso_spectral_workspace_init(self.plan, ctypes.c_void_p(self.buf.data_ptr()),
-                                                         ctypes.c_size_t(nbytes), ctypes.byref(hyper),
-                                                         ctypes.c_void_p(stream)), "spectral workspace init")
+        stream = ctypes.c_void_p(_native.stream_handle(device))
+        if count is None:
+            nbytes = int(lib.cresso_spectral_workspace_bytes(self.plan))
+            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            rc = lib.cresso_spectral_workspace_init(self.plan, ctypes.c_void_p(self.buf.data_ptr()),
+                                                    ctypes.c_size_t(nbytes), ctypes.byref(hyper), stream)
+        else:
+            nbytes = int(lib.cresso_spectral_batched_workspace_bytes(self.plan, count))
+            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            rc = lib.cresso_spectral_batched_workspace_init(self.plan, count, ctypes.c_void_p(self.buf.data_ptr()),
+                                                            ctypes.c_size_t(nbytes), ctypes.byref(hyper), stream)
+        _native.check(rc, "spectral workspace init")
 
     def __del__(self):
         plan = getattr(self, "plan", None)
@@ -84,18 +104,29 @@ class _Workspace:
                 pass
 
 
+def lane_scratch_bytes(numel: int) -> int:
+    """Per-tensor scratch of a batched step, for sizing chunks: the tangent
+    field (4 bytes per element) dominates; the rest is a few KB per tensor
+    plus small per-row and per-column sums."""
+    return 4 * numel + (1 << 16)
+
+
 class SpectralEngine:
     READY = True
-    LANES = 4   # side streams of a multi-tensor step
+    LANES = 4                 # side streams of a multi-tensor step
+    BATCH = True              # batch same-plan tensors into one launch per kernel
+    BATCH_BYTES = 256 << 20   # per-tensor scratch held by one batch
 
     def __init__(self):
         self.lib = _native.load()
-        self.ws: Dict[tuple, _Workspace] = {}   # (plan key, lane) -> workspace
+        self.ws: Dict[tuple, _Workspace] = {}   # (plan key, unit kind, lane) -> workspace
         self.side: Dict[torch.device, List[torch.cuda.Stream]] = {}
         self.freq_cache: Dict[int, Tuple[int, ...]] = {}
 
     def reset(self) -> None:
+        """Forget cached frequency lists and free every workspace."""
         self.freq_cache.clear()
+        self.ws.clear()
 
     def _freqs(self, st: dict) -> Tuple[int, ...]:
         fr = st["freqs"]
@@ -107,12 +138,15 @@ class SpectralEngine:
             self.freq_cache[key] = got
         return got[1]
 
-    def _workspace(self, key: tuple, lane: int, rank: int, group: dict) -> _Workspace:
-        ws = self.ws.get((key, lane))
-        if ws is None:
+    def _workspace(self, key: tuple, lane: int, rank: int, group: dict, count=None) -> _Workspace:
+        wkey = (key, count is not None, lane)
+        ws = self.ws.get(wkey)
+        if ws is None or (count is not None and ws.count < count):
             device, shape, freqs, bins, tables = key
-            ws = _Workspace(self.lib, shape, freqs, rank, bins, tables, group, device)
-            self.ws[(key, lane)] = ws
+            ws = None
+            self.ws.pop(wkey, None)
+            ws = _Workspace(self.lib, shape, freqs, rank, bins, tables, group, device, count)
+            self.ws[wkey] = ws
         return ws
 
     def _prepare(self, param: torch.Tensor, grad: torch.Tensor, st: dict, group: dict):
@@ -161,6 +195,12 @@ class SpectralEngine:
                                                     ctypes.c_size_t(ws.buf.numel()), ctypes.byref(hyper),
                                                     ctypes.c_void_p(stream)), "spectral route step")
 
+    def _launch_batch(self, ws: _Workspace, descs: list, hyper, stream: int) -> None:
+        arr = (_native.SpectralDesc * len(descs))(*descs)
+        _native.check(self.lib.cresso_spectral_step_batched(ws.plan, arr, len(descs), ctypes.c_void_p(ws.buf.data_ptr()),
+                                                            ctypes.c_size_t(ws.buf.numel()), ctypes.byref(hyper),
+                                                            ctypes.c_void_p(stream)), "spectral route batched step")
+
     def step(self, param: torch.Tensor, grad: torch.Tensor, st: dict, group: dict) -> None:
         """One tensor on the caller's stream."""
         key, rank, d = self._prepare(param, grad, st, group)
@@ -173,6 +213,27 @@ class SpectralEngine:
         while len(have) < n:
             have.append(torch.cuda.Stream(device=device))   # default priority
         return have[:n]
+
+    def _units(self, prepared: list, sts: list) -> list:
+        """Cut a step's tensors into units: (unit key, plan key, rank, [desc], [state]).
+        Tensors batch when they share the plan, dtypes, hard channel and hash state."""
+        groups: Dict[tuple, list] = {}
+        for i, (key, rank, d) in enumerate(prepared):
+            bkey = (key, d.param_dtype, d.grad_dtype, d.hard, bool(d.hash_energy))
+            groups.setdefault(bkey if self.BATCH else (bkey, i), []).append(i)
+        units = []
+        for bkey, idx in groups.items():
+            key, rank, _ = prepared[idx[0]]
+            if len(idx) == 1:
+                units.append(((key, False), key, rank, [prepared[idx[0]][2]], [sts[idx[0]]]))
+                continue
+            per = lane_scratch_bytes(prepared[idx[0]][2].numel)
+            chunks = -(-len(idx) * per // self.BATCH_BYTES)
+            m = -(-len(idx) // chunks)
+            for c in range(0, len(idx), m):
+                sel = idx[c:c + m]
+                units.append(((key, True, m), key, rank, [prepared[i][2] for i in sel], [sts[i] for i in sel]))
+        return units
 
     def step_many(self, items: Sequence[Tuple[torch.Tensor, torch.Tensor, dict]], group: dict) -> None:
         """Every spectral tensor of a param group: (param, grad, state) each."""
@@ -187,16 +248,23 @@ class SpectralEngine:
             # descriptors and workspaces first: a workspace created now is
             # initialised on the caller's stream, before the lanes fork from it
             prepared = [self._prepare(p, g, st, group) for p, g, st in its]
-            nl = min(self.LANES, len(its))
-            lanes = assign_lanes([key for key, _, _ in prepared], nl)
-            plan = [(self._workspace(key, lane, rank, group), d, lane, st)
-                    for (key, rank, d), (_, _, st), lane in zip(prepared, its, lanes)]
+            units = self._units(prepared, [st for _, _, st in its])
+            nl = min(self.LANES, len(units))
+            lanes = assign_lanes([u[0][:2] for u in units], nl)
+            plan = []
+            for (ukey, key, rank, descs, sts), lane in zip(units, lanes):
+                count = ukey[2] if ukey[1] else None
+                plan.append((self._workspace(key, lane, rank, group, count), descs, sts, lane))
             cur = torch.cuda.current_stream(device)
             side = self._streams(device, nl)
             for s in side:
                 s.wait_stream(cur)
-            for ws, d, lane, st in plan:
-                st["step"] += 1
-                self._launch(ws, d, hyper, int(side[lane].cuda_stream))
+            for ws, descs, sts, lane in plan:
+                for st in sts:
+                    st["step"] += 1
+                if ws.count is None:
+                    self._launch(ws, descs[0], hyper, int(side[lane].cuda_stream))
+                else:
+                    self._launch_batch(ws, descs, hyper, int(side[lane].cuda_stream))
             for s in side:
                 cur.wait_stream(s)

@@ -174,6 +174,29 @@ typedef struct cresso_spectral_desc {
 int32_t cresso_spectral_step(const cresso_spectral_plan* plan, const cresso_spectral_desc* desc, void* workspace,
                              size_t workspace_bytes, const cresso_hyper* hyper, void* stream);
 
+/* One optimizer step of `count` tensors of one plan, each launch of the step
+ * covering all of them (the tensor is the grid's second dimension).  Replaces
+ * the reference's loop over a group's same-shape spectral params
+ * (cresso_v5.py:828-843 with _spectral_step, v5.py:885), whose per-step basis
+ * cache (transient_basis_workspace, v5.py:827) is shared the same way: the
+ * plan's shape tables are held once, the per-step scratch once per tensor.
+ *
+ * descs: host array of `count` descriptors of distinct tensors; they may
+ * differ in every pointer and in `step`, not in dtypes, `hard` or whether
+ * hash state is given.  The library copies them to the device as kernel
+ * arguments on `stream` (no host synchronization).  Every tensor's results
+ * are bit-identical to cresso_spectral_step of it.
+ *
+ * The workspace: cresso_spectral_batched_workspace_bytes(plan, count) bytes,
+ * set up once by cresso_spectral_batched_workspace_init (which synchronizes
+ * `stream` once).  It serves any batch of up to `count` tensors; calls that
+ * share it must be ordered (one stream). */
+size_t cresso_spectral_batched_workspace_bytes(const cresso_spectral_plan* plan, int32_t count);
+int32_t cresso_spectral_batched_workspace_init(const cresso_spectral_plan* plan, int32_t count, void* workspace,
+                                               size_t workspace_bytes, const cresso_hyper* hyper, void* stream);
+int32_t cresso_spectral_step_batched(const cresso_spectral_plan* plan, const cresso_spectral_desc* descs, int32_t count,
+                                     void* workspace, size_t workspace_bytes, const cresso_hyper* hyper, void* stream);
+
 /* cresso_spectral_step without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.

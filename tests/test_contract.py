@@ -278,3 +278,32 @@ def test_spectral_lane_assignment():
     assert by["b"] == [1] and by["c"] == [2, 3] and by["d"] == [3]  # start lane moves with each new key
     assert assign_lanes(["x", "y"], 1) == [0, 0]
     assert assign_lanes([], 4) == []
+
+
+def test_spectral_batch_units_and_chunks():
+    # the multi-tensor spectral step's units: same plan, dtypes, hard channel
+    # and hash state batch together; a batch holds at most BATCH_BYTES of
+    # per-tensor scratch, larger groups are cut into near-equal chunks
+    from cresso_amd import _native
+    from cresso_amd.spectral import SpectralEngine, lane_scratch_bytes
+
+    eng = SpectralEngine.__new__(SpectralEngine)   # no library needed for the grouping
+    eng.BATCH, eng.BATCH_BYTES = True, 3 * lane_scratch_bytes(100)
+
+    def desc(numel, hard=1, hash_on=True, pdt=_native.F32):
+        d = _native.SpectralDesc()
+        d.numel, d.hard, d.param_dtype, d.grad_dtype = numel, hard, pdt, pdt
+        d.hash_energy = 4096 if hash_on else None
+        return d
+
+    prepared = [("a", 8, desc(100)) for _ in range(7)] + [("b", 8, desc(50))] + [("a", 8, desc(100, hard=0))] \
+        + [("a", 8, desc(100, pdt=_native.BF16))] + [("c", 8, desc(10)), ("c", 8, desc(10, hash_on=False))]
+    sts = [{"i": i} for i in range(len(prepared))]
+    units = eng._units(prepared, sts)
+    got = [(u[0], [s["i"] for s in u[4]]) for u in units]
+    # seven "a" tensors at three per batch: chunks of 3, 3, 1 (ceil(7 / ceil(7/3)) = 3)
+    assert got[:3] == [(("a", True, 3), [0, 1, 2]), (("a", True, 3), [3, 4, 5]), (("a", True, 3), [6])]
+    assert [g[1] for g in got[3:]] == [[7], [8], [9], [10], [11]]
+    assert all(not u[0][1] for u in units[3:])
+    eng.BATCH = False
+    assert [len(u[4]) for u in eng._units(prepared, sts)] == [1] * len(prepared)
