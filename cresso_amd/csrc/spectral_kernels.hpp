@@ -1276,6 +1276,17 @@ inline bool fast_mode(const Geom& g, int hash_on, int axes_on, const cresso_hype
            h.local_sharpness == 0.0 && (float)fmax(h.instant_metric_power, 0.25) == 1.0f && g.rows % g.PR == 0 &&
            g.cols % SP_NT == 0 && g.PR % (4 * SP_U) == 0;
 }
+// tables the matrix-core sweeps take: 2 or 4 tables of one-byte bins, packed
+__host__ __device__ inline bool mtables(const Geom& g) {
+    return (g.T == 2 || g.T == 4) && g.bpb == 1 && g.binbytes == g.T;
+}
+// whether a tensor's step can use the matrix-core sweeps (host side): MODE 1's
+// conditions with 2 or 4 tables
+inline bool mfast_mode(const Geom& g, int hash_on, int axes_on, const cresso_hyper& h) {
+    return hash_on && axes_on && mtables(g) && !g.one_d && h.weight_decay == 0.0 && h.local_sharpness == 0.0 &&
+           (float)fmax(h.instant_metric_power, 0.25) == 1.0f && g.rows % g.PR == 0 && g.cols % SP_NT == 0 &&
+           g.PR % (4 * SP_U) == 0;
+}
 
 // ---------------------------------------------------------------------------
 // S2: density field
@@ -1487,17 +1498,34 @@ __device__ __forceinline__ float row16_total(float v) {
     return v;
 }
 
+// The matrix-core sweeps take TT = 2 or 4 tables of one-byte bins, packed in
+// TT bytes per element (table t in byte t).
+template <int TT> __device__ __forceinline__ uint32_t ldg_bins(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    static_assert(TT == 2 || TT == 4, "two or four tables of one-byte bins");
+    if constexpr (TT == 2)
+        return bload1u16(r, voff, soff);
+    else
+        return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+template <int TT> __device__ __forceinline__ uint32_t bin_byte(uint32_t b, int tt) {
+    return tt == TT - 1 ? (b >> (8 * tt)) : ((b >> (8 * tt)) & 0xffu);
+}
+// projection rows of rank RM in 16-row tiles; carriers in chunks of 4
+template <int RM> constexpr int nqt() { return (2 * RM + 15) / 16; }
+template <int KC> constexpr int kch() { return (KC + 3) / 4; }
+
 // ---------------------------------------------------------------------------
-// S2 on the matrix cores (MODE 1 tiles, RM <= 8): sweep2_kernel's element
-// math in sweep3m_kernel's tile layout (lane l: rows 4 lg + r of column li of
-// each 16 x 16 tile, 4 tile columns per wave).  The log-density projection
-// Z_q(col) = sum_rows a_q(row) L(row, col) is 4 MFMAs per tile (A = the rows'
-// factors, B = L).  Row density sums: the lane's 4 tile columns are added in
-// registers, then each 16-lane row group sums its columns with DPP; column
-// sums stay per lane and tile column until the end.
+// S2 on the matrix cores (MODE 1 tiles, RM <= 16, TT = 2 or 4 tables of
+// one-byte bins): sweep2_kernel's element math in sweep3m_kernel's tile
+// layout (lane l: rows 4 lg + r of column li of each 16 x 16 tile, 4 tile
+// columns per wave).  The log-density projection Z_q(col) = sum_rows a_q(row)
+// L(row, col) is 4 MFMAs per tile and 16-row tile of q (A = the rows' factors,
+// B = L).  Row density sums: the lane's 4 tile columns are added in registers,
+// then each 16-lane row group sums its columns with DPP; column sums stay per
+// lane and tile column until the end.
 // ---------------------------------------------------------------------------
-template <int RM, int KC, typename GT>
-__global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
+template <int RM, int KC, typename GT, int TT>
+__global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
     Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl,
     double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ rowfx,
@@ -1509,23 +1537,23 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
     }
     ctrl = lane_at(ctrl, L); part = lane_at(part, L); hist = lane_at(hist, L);
     rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L); part1 = lane_at(part1, L);
-    static_assert(RM <= 8, "16 projection rows");
+    static_assert(RM <= 16, "two 16-row tiles of projection rows at most");
     constexpr int RW = 2 * RM;
+    constexpr int NQ = nqt<RM>();
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV2];
     const Tile t = tile_of(g);
     const int B = g.B;
-    const int TB = 2 * B;
+    const int TB = TT * B;
     const int nr = g.PR;
     const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int li = l & 15, lg = l >> 4;
     const int64_t base = panel_base(g, t);
     const uint32_t cols = (uint32_t)g.cols;
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(grad + base, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(GT)));
-    const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(reinterpret_cast<const uint16_t*>(bins) + base, (uint32_t)((int64_t)nr * g.cols * 2));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bins + (size_t)TT * base, (uint32_t)((int64_t)nr * g.cols * TT));
     const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
-    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vb = lane_el * 2u;
+    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vb = lane_el * (uint32_t)TT;
     auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
     // one register set, refilled tile by tile (loads three tiles ahead of use)
     float xv[16];
@@ -1535,7 +1563,7 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
         for (int r = 0; r < 4; ++r) {
             const uint32_t o = tile_off(tr, tc, r);
             xv[4 * tc + r] = ldg_el<GT>(rg, vg, o * (uint32_t)sizeof(GT));
-            bv[4 * tc + r] = bload1u16(rb, vb, o * 2u);
+            bv[4 * tc + r] = ldg_bins<TT>(rb, vb, o * (uint32_t)TT);
         }
     };
 #pragma unroll
@@ -1555,18 +1583,24 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
     const float pw = (float)h.energy_power;
     const float sg = h.maximize ? -1.f : 1.f;
     const float hs = (float)f1.hs_ds;
-    // the lane's projection A operands, a_li(row 16 tr + 4 lg + r), held in
-    // registers: read from LDS inside the loop they would queue behind the
-    // histogram atomics (LDS operations complete in order)
-    float aJv[4][4];
+    // the lane's projection A operands, a_{16 qt + li}(row 16 tr + 4 lg + r),
+    // held in registers: read from LDS inside the loop they would queue
+    // behind the histogram atomics (LDS operations complete in order)
+    float aJv[NQ][4][4];
 #pragma unroll
-    for (int tr = 0; tr < 4; ++tr)
+    for (int qt = 0; qt < NQ; ++qt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            aJv[tr][r] = (li < RW && tr < nr / 16) ? s_ar[(16 * tr + 4 * lg + r) * RW + (li < RW ? li : 0)] : 0.f;
-    f32x4m zacc[4];
+        for (int tr = 0; tr < 4; ++tr)
 #pragma unroll
-    for (int tc = 0; tc < 4; ++tc) zacc[tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
+            for (int r = 0; r < 4; ++r) {
+                const int q = 16 * qt + li;
+                aJv[qt][tr][r] = (q < RW && tr < nr / 16) ? s_ar[(16 * tr + 4 * lg + r) * RW + (q < RW ? q : 0)] : 0.f;
+            }
+    f32x4m zacc[NQ][4];
+#pragma unroll
+    for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) zacc[qt][tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
     float aL = 0.f;
     float cD[4] = {0.f, 0.f, 0.f, 0.f};   // column density sums of the lane's 4 tile columns
     // Sums of log(1 + ds) are kept in log2 units (fin2 scales them by ln 2).
@@ -1591,12 +1625,15 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
                 rs[r] += rel;
                 cD[tc] += rel;
                 const unsigned long long v = to_fixed_u(ds * hs);
-                atomicAdd(&s_hist[(b[r] & 0xffu) * NH + hc], v);
-                atomicAdd(&s_hist[(B + (b[r] >> 8)) * NH + hc], v);
-            }
-            // A of the projection: a_li(row 16 tr + 4 lg + r)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) zacc[tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJv[tr][r], Ls[r], zacc[tc], 0, 0, 0);
+                for (int tt = 0; tt < TT; ++tt) atomicAdd(&s_hist[(tt * B + bin_byte<TT>(b[r], tt)) * NH + hc], v);
+            }
+            // A of the projection: a_q(row 16 tr + 4 lg + r)
+#pragma unroll
+            for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    zacc[qt][tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJv[qt][tr][r], Ls[r], zacc[qt][tc], 0, 0, 0);
             if (tr + 1 < ntr) load_tile(tr + 1, tc);
             pin1(aL);
 #pragma unroll
@@ -1638,37 +1675,41 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep2m_kernel(
     Partials P{red, 2 + 2 * g.R, NV2};
     P.add(0, aL);
     P.add(1, aD);
-    // projection: lane group lg holds Z_{4 lg + j}(col), both components of
-    // modes 2 lg and 2 lg + 1, for its 4 columns (proj_finish's form), summed
-    // over the columns and the group's 16 lanes into slots 2 + 4 lg + j
-    float cs[4] = {0.f, 0.f, 0.f, 0.f};
+    // projection: in q-tile qt, lane group lg holds Z_{16 qt + 4 lg + j}(col),
+    // both components of modes 8 qt + 2 lg and 8 qt + 2 lg + 1, for its 4
+    // columns (proj_finish's form), summed over the columns and the group's
+    // 16 lanes into slots 2 + 16 qt + 4 lg + j
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        const int r = 2 * lg + half;
-        if (r < g.R) {
-            const ModeMeta m = meta[r];
+    for (int qt = 0; qt < NQ; ++qt) {
+        float cs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
-                const int64_t c = colw + 16 * tc + li;
-                // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
-                const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
-                const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
-                const float z1 = zacc[tc][2 * half], z2 = zacc[tc][2 * half + 1];
-                if (m.type == M_ADD) {
-                    cs[2 * half] += b1 * z1 - b2 * z2;
-                    cs[2 * half + 1] += b1 * z2 + b2 * z1;
-                } else {
-                    cs[2 * half] += b1 * z1;
-                    cs[2 * half + 1] += b2 * z2;
+        for (int half = 0; half < 2; ++half) {
+            const int r = 8 * qt + 2 * lg + half;
+            if (r < g.R) {
+                const ModeMeta m = meta[r];
+#pragma unroll
+                for (int tc = 0; tc < 4; ++tc) {
+                    const int64_t c = colw + 16 * tc + li;
+                    // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
+                    const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
+                    const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
+                    const float z1 = zacc[qt][tc][2 * half], z2 = zacc[qt][tc][2 * half + 1];
+                    if (m.type == M_ADD) {
+                        cs[2 * half] += b1 * z1 - b2 * z2;
+                        cs[2 * half + 1] += b1 * z2 + b2 * z1;
+                    } else {
+                        cs[2 * half] += b1 * z1;
+                        cs[2 * half + 1] += b2 * z2;
+                    }
                 }
             }
         }
-    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float sm = row16_total(cs[j]);
-        const int slot = 4 * lg + j;
-        if (li == 15 && slot < 2 * g.R) red[wv * P.V + 2 + slot] = sm;
+        for (int j = 0; j < 4; ++j) {
+            const float sm = row16_total(cs[j]);
+            const int slot = 16 * qt + 4 * lg + j;
+            if (li == 15 && slot < 2 * g.R) red[wv * P.V + 2 + slot] = sm;
+        }
     }
     P.flush(part);
 }
@@ -2146,23 +2187,28 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
 
 
 // ---------------------------------------------------------------------------
-// S3 on the matrix cores (MODE 1 tiles, RM <= 8, KC <= 12).  The element math
-// is sweep3_kernel's; the contractions run as v_mfma_f32_16x16x4f32 on 16 x 16
-// tiles, each wave owning 64 columns of the panel as 4 tile columns:
-//   metric and prediction fields: 3 + 3 MFMAs per tile (column-carrier form,
-//     A = the rows' alpha coefficients, B = the columns' carriers);
-//   t projection Z_q(col) = sum_rows a_q(row) t(row, col): 4 MFMAs per tile,
-//     A[q][k] = a_q(row 4k + r), B[k][col] = t(row 4k + r, col) for the
-//     tile's element r of each lane, accumulated over the panel in D[q][col].
+// S3 on the matrix cores (MODE 1 tiles, RM <= 16, TT = 2 or 4 tables of
+// one-byte bins).  The element math is sweep3_kernel's; the contractions run
+// as v_mfma_f32_16x16x4f32 on 16 x 16 tiles, each wave owning 64 columns of
+// the panel as 4 tile columns:
+//   metric and prediction fields: 2 KCH MFMAs per tile, KCH = KC / 4 rounded
+//     up (column-carrier form, A = the rows' alpha coefficients, B = the
+//     columns' carriers);
+//   t projection Z_q(col) = sum_rows a_q(row) t(row, col): 4 MFMAs per tile
+//     and 16-row tile of q, A[q][k] = a_q(row 4k + r), B[k][col] =
+//     t(row 4k + r, col) for the tile's element r of each lane, accumulated
+//     over the panel in D[q][col].
 // Layouts (lane l, li = l % 16, lg = l / 16): A[i][k] from lane (i = li,
 // k = lg), B[k][j] from lane (j = li, k = lg), D[i][j] in lane (j = li),
 // register r: i = 4 lg + r.  Lane l processes rows 4 lg + r of column li of
 // each tile.  The loads of the next row of tiles are in flight while a row is
-// processed.
+// processed.  Up to three chunks of carriers (rank <= 8) the B operands are
+// read from an LDS table; more chunks stay in registers (rank 16: 36 per lane,
+// within the 256 registers of two waves per SIMD).
 // ---------------------------------------------------------------------------
-
-template <int RM, int KC, typename GT>
-__global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
+template <int KC> constexpr bool bq_in_regs() { return kch<KC>() > 3; }
+template <int RM, int KC, typename GT, int TT>
+__global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void sweep3m_kernel(
     Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
     const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx,
@@ -2171,14 +2217,17 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
     if (L.dv) grad = (const GT*)lane_desc(L).grad;
     ctrl = lane_at(ctrl, L); lt = lane_at(lt, L); rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L);
     colfac = lane_at(colfac, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L); hist = lane_at(hist, L);
-    static_assert(RM <= 8 && KC <= 12, "16 projection rows, three K-chunks of four carriers");
+    static_assert(RM <= 16, "two 16-row tiles of projection rows at most");
     constexpr int RW = 2 * RM;
+    constexpr int NQ = nqt<RM>();
     constexpr int KP = kcp<KC>();
+    constexpr int KCH = kch<KC>();
+    constexpr bool BQR = bq_in_regs<KC>();
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV3];
     const Tile t = tile_of(g);
     const int B = g.B;
-    const int TB = 2 * B;
+    const int TB = TT * B;
     const int nr = g.PR;
     const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int li = l & 15, lg = l >> 4;
@@ -2186,10 +2235,9 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
     const uint32_t cols = (uint32_t)g.cols;
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(grad + base, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(GT)));
     const __amdgpu_buffer_rsrc_t rt = make_rsrc(tbuf + base, (uint32_t)((int64_t)nr * g.cols * 4));
-    const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(reinterpret_cast<const uint16_t*>(bins) + base, (uint32_t)((int64_t)nr * g.cols * 2));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bins + (size_t)TT * base, (uint32_t)((int64_t)nr * g.cols * TT));
     const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
-    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vt = lane_el * 4u, vb = lane_el * 2u;
+    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vt = lane_el * 4u, vb = lane_el * (uint32_t)TT;
     // tile (tr, tc), lane element r: panel element (16 tr + 4 lg + r, 64 wv + 16 tc + li)
     auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
     // one register set, refilled tile by tile: the loads of tile (tr + 1, tc)
@@ -2201,7 +2249,7 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
         for (int r = 0; r < 4; ++r) {
             const uint32_t o = tile_off(tr, tc, r);
             xv[4 * tc + r] = ldg_el<GT>(rg, vg, o * (uint32_t)sizeof(GT));
-            bv[4 * tc + r] = bload1u16(rb, vb, o * 2u);
+            bv[4 * tc + r] = ldg_bins<TT>(rb, vb, o * (uint32_t)TT);
         }
     };
 #pragma unroll
@@ -2225,16 +2273,28 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
     for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
         s_rf[lr] = marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps);
     stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
-    // the block's column carriers (B operands of the reconstructions) and
-    // column instant-metric factors, in LDS: [KP][SP_BQS] (rows padded so that
-    // the 4 lane groups of a wave read distinct banks) | [SP_NT]
+    // the block's column instant-metric factors in LDS [SP_NT], after the
+    // column carriers (B operands of the reconstructions) when those are in
+    // LDS too: [KP][SP_BQS] (rows padded so that the 4 lane groups of a wave
+    // read distinct banks)
     float* s_bq = s_ar + RW * g.PR;
-    float* s_ec = s_bq + KP * SP_BQS;
+    float* s_ec = s_bq + (BQR ? 0 : KP * SP_BQS);
     const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
+    float bqr[BQR ? 4 : 1][BQR ? KCH : 1];
     {
         const int64_t c = (int64_t)t.slab * SP_NT + threadIdx.x;
+        if constexpr (BQR) {
 #pragma unroll
-        for (int k = 0; k < KP; ++k) s_bq[k * SP_BQS + threadIdx.x] = k < KC ? coltab[(size_t)k * g.cols + c] : 0.f;
+            for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+                for (int kc = 0; kc < KCH; ++kc) {
+                    const int k = 4 * kc + lg;
+                    bqr[tc][kc] = k < KC ? coltab[(size_t)k * g.cols + colw + 16 * tc + li] : 0.f;
+                }
+        } else {
+#pragma unroll
+            for (int k = 0; k < KP; ++k) s_bq[k * SP_BQS + threadIdx.x] = k < KC ? coltab[(size_t)k * g.cols + c] : 0.f;
+        }
         s_ec[threadIdx.x] = g.ntrail == 1 ? marg_factor(colfx[c], g.hs_col, (double)g.rows, gden, kappa, eps) : colfac[c];
     }
     const float* __restrict__ bql = s_bq + lg * SP_BQS + 64 * wv + li;   // + 4 kc SP_BQS + 16 tc
@@ -2253,19 +2313,26 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
     const float hs = (float)ctrl->hs_P;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
     const float k2 = -2.8853900817779268f * iclip;   // -2 log2(e) / clip
-    f32x4m zacc[4];
+    constexpr float invT = 1.0f / (float)TT;
+    f32x4m zacc[NQ][4];
 #pragma unroll
-    for (int tc = 0; tc < 4; ++tc) zacc[tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
+    for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) zacc[qt][tc] = f32x4m{0.f, 0.f, 0.f, 0.f};
     float m_ee = 0.f, m_t = 0.f, m_tt = 0.f, m_rr = 0.f, m_bb = 0.f, m_oo = 0.f, m_rb = 0.f, m_ro = 0.f,
           m_bo = 0.f, m_tr = 0.f, m_tb = 0.f, m_to = 0.f;
     // metric and prediction fields of tile column tc of the current row of tiles
-    float aM[3], aQ[3];
+    float aM[KCH], aQ[KCH];
     auto recon = [&](int tc, f32x4m& lm, f32x4m& pred) {
         lm = f32x4m{cM, cM, cM, cM};
         pred = f32x4m{cP, cP, cP, cP};
 #pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
-            const float bq = bql[4 * kc * SP_BQS + 16 * tc];
+        for (int kc = 0; kc < KCH; ++kc) {
+            float bq;
+            if constexpr (BQR)
+                bq = bqr[tc][kc];
+            else
+                bq = bql[4 * kc * SP_BQS + 16 * tc];
             lm = __builtin_amdgcn_mfma_f32_16x16x4f32(aM[kc], bq, lm, 0, 0, 0);
             pred = __builtin_amdgcn_mfma_f32_16x16x4f32(aQ[kc], bq, pred, 0, 0, 0);
         }
@@ -2274,7 +2341,7 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
     auto row_alpha = [&](int tr) {
         const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
 #pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
+        for (int kc = 0; kc < KCH; ++kc) {
             aM[kc] = alr[4 * kc];
             aQ[kc] = alr[KP + 4 * kc];
         }
@@ -2289,8 +2356,10 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
             const float M = med3f(fexp(mcoup * med3f(lm[r], -3.0f, 3.0f)), 0.06f, 16.0f);
             float den = scale * M;
             den = den * med3f(s_rf[16 * tr + 4 * lg + r] * ec, 0.08f, 12.0f);
-            const float lsum = s_lt[b[r] & 0xffu] + s_lt[B + (b[r] >> 8)];
-            den = den * med3f(fexp(lsum * 0.5f), 0.08f, 12.0f);
+            float lsum = s_lt[bin_byte<TT>(b[r], 0)];
+#pragma unroll
+            for (int tt = 1; tt < TT; ++tt) lsum += s_lt[tt * B + bin_byte<TT>(b[r], tt)];
+            den = den * med3f(fexp(lsum * invT), 0.08f, 12.0f);
             const float tv = med3f(f * frcp(den + eps), -1.0e4f, 1.0e4f);
             bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
             tvs[r] = tv;
@@ -2305,15 +2374,18 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
             m_rb = fmaf(z.rat, z.th, m_rb); m_ro = fmaf(z.rat, z.root, m_ro); m_bo = fmaf(z.th, z.root, m_bo);
             m_tr = fmaf(at, z.rat, m_tr); m_tb = fmaf(at, z.th, m_tb); m_to = fmaf(at, z.root, m_to);
             const unsigned long long v = to_fixed_s(P * hs);
-            atomicAdd(&s_hist[(b[r] & 0xffu) * NH + hc], v);
-            atomicAdd(&s_hist[(B + (b[r] >> 8)) * NH + hc], v);
-        }
-        // A of the projection: a_li(row 16 tr + 4 lg + r)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float aJ = li < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (li < RW ? li : 0)] : 0.f;
-            zacc[tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJ, tvs[r], zacc[tc], 0, 0, 0);
+            for (int tt = 0; tt < TT; ++tt) atomicAdd(&s_hist[(tt * B + bin_byte<TT>(b[r], tt)) * NH + hc], v);
         }
+        // A of the projection: a_q(row 16 tr + 4 lg + r), q = 16 qt + li
+#pragma unroll
+        for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int q = 16 * qt + li;
+                const float aJ = q < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (q < RW ? q : 0)] : 0.f;
+                zacc[qt][tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJ, tvs[r], zacc[qt][tc], 0, 0, 0);
+            }
         pin1(m_ee); pin1(m_t); pin1(m_tt); pin1(m_rr); pin1(m_bb); pin1(m_oo);
         pin1(m_rb); pin1(m_ro); pin1(m_bo); pin1(m_tr); pin1(m_tb); pin1(m_to);
         elem_fence();
@@ -2353,38 +2425,42 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep3m_kernel(
     for (int k = 0; k < 13; ++k) P.add(k, mm[k]);
     P.add(13, 0.f);
     P.add(14, 0.f);
-    // projection: lane group lg holds Z_{4 lg + j}(col), j < 4, i.e. both
-    // components of modes 2 lg and 2 lg + 1, for its 4 columns; each mode's raw
-    // C/S (proj_finish's form) is summed over the columns, then over the 16
-    // lanes of the group, into slots 15 + 4 lg + j.
-    float cs[4] = {0.f, 0.f, 0.f, 0.f};
+    // projection: in q-tile qt, lane group lg holds Z_{16 qt + 4 lg + j}(col),
+    // j < 4, i.e. both components of modes 8 qt + 2 lg and 8 qt + 2 lg + 1,
+    // for its 4 columns; each mode's raw C/S (proj_finish's form) is summed
+    // over the columns, then over the 16 lanes of the group, into slots
+    // 15 + 16 qt + 4 lg + j.
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        const int r = 2 * lg + half;
-        if (r < g.R) {
-            const ModeMeta m = meta[r];
+    for (int qt = 0; qt < NQ; ++qt) {
+        float cs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
-                const int64_t c = colw + 16 * tc + li;
-                // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
-                const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
-                const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
-                const float z1 = zacc[tc][2 * half], z2 = zacc[tc][2 * half + 1];
-                if (m.type == M_ADD) {
-                    cs[2 * half] += b1 * z1 - b2 * z2;
-                    cs[2 * half + 1] += b1 * z2 + b2 * z1;
-                } else {
-                    cs[2 * half] += b1 * z1;
-                    cs[2 * half + 1] += b2 * z2;
+        for (int half = 0; half < 2; ++half) {
+            const int r = 8 * qt + 2 * lg + half;
+            if (r < g.R) {
+                const ModeMeta m = meta[r];
+#pragma unroll
+                for (int tc = 0; tc < 4; ++tc) {
+                    const int64_t c = colw + 16 * tc + li;
+                    // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
+                    const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
+                    const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
+                    const float z1 = zacc[qt][tc][2 * half], z2 = zacc[qt][tc][2 * half + 1];
+                    if (m.type == M_ADD) {
+                        cs[2 * half] += b1 * z1 - b2 * z2;
+                        cs[2 * half + 1] += b1 * z2 + b2 * z1;
+                    } else {
+                        cs[2 * half] += b1 * z1;
+                        cs[2 * half + 1] += b2 * z2;
+                    }
                 }
             }
         }
-    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float s = row16_total(cs[j]);
-        const int slot = 4 * lg + j;
-        if (li == 15 && slot < 2 * g.R) red[wv * P.V + 15 + slot] = s;
+        for (int j = 0; j < 4; ++j) {
+            const float sm = row16_total(cs[j]);
+            const int slot = 16 * qt + 4 * lg + j;
+            if (li == 15 && slot < 2 * g.R) red[wv * P.V + 15 + slot] = sm;
+        }
     }
     P.flush(part);
 }
@@ -2812,42 +2888,45 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
 
 
 // ---------------------------------------------------------------------------
-// S4 on the matrix cores (MODE 1 tiles).  Each wave owns 64 columns of the
-// panel as 4 x 4 tiles of 16 x 16 elements.  A reconstruction of a tile is
-// 3 MFMAs (v_mfma_f32_16x16x4f32, the K = KC carriers in chunks of 4):
+// S4 on the matrix cores (MODE 1 tiles, TT = 2 or 4 tables of one-byte bins).
+// Each wave owns 64 columns of the panel as 4 x 4 tiles of 16 x 16 elements.
+// A reconstruction of a tile is KCH MFMAs (v_mfma_f32_16x16x4f32, the K = KC
+// carriers in chunks of 4):
 //   A[i][k] = alpha_{4kc+k}(row i)   lane l supplies i = l % 16, k = l / 16
 //   B[k][j] = b_{4kc+k}(col j)       lane l supplies j = l % 16, k = l / 16
 //   D[i][j]                          lane l, register r: i = 4 (l / 16) + r, j = l % 16
 // so lane l processes rows 4 (l/16) + r of column l % 16 of each tile, and the
 // elementwise drive math is unchanged.  The loads of the next tile are in
-// flight while a tile is processed.  The hash term's coefficient c5 is known
-// here (fin3 forms the hash prediction's RMS from the co-occurrence counts),
-// so the full drive is written and sum drive^2 is summed directly.
+// flight while a tile is processed.  C5C: the hash term's coefficient c5 is
+// known here (fin3 forms the hash prediction's RMS from the co-occurrence
+// counts), so the full drive is written and sum drive^2 is summed directly;
+// otherwise (sweep4_kernel's form) the drive without the hash term is written
+// and the sums of d^2, d hp and hp^2 go to sweep 5.
 // ---------------------------------------------------------------------------
-template <int RM, int KC>
-__global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
+template <int RM, int KC, int TT, bool C5C>
+__global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void sweep4m_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
     const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
     float* __restrict__ tbuf, double* __restrict__ part, int echo_on, Lanes L, cresso_hyper h) {
     ctrl = lane_at(ctrl, L); imp_tab = lane_at(imp_tab, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L);
-    static_assert(KC <= 12, "three K-chunks of four carriers");
+    static_assert(!C5C || TT == 2, "closed-form hash term with two tables");
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV4];
     const Tile t = tile_of(g);
     const int B = g.B;
-    const int TB = 2 * B;
+    const int TB = TT * B;
     const int nr = g.PR;
     constexpr int KP = kcp<KC>();
+    constexpr int KCH = kch<KC>();
     const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int li = l & 15, lg = l >> 4;
     const int64_t base = panel_base(g, t);
     float* __restrict__ tb = tbuf + base;
     const uint32_t cols = (uint32_t)g.cols;
     const __amdgpu_buffer_rsrc_t rt = make_rsrc(tb, (uint32_t)((int64_t)nr * g.cols * 4));
-    const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(reinterpret_cast<const uint16_t*>(bins) + base, (uint32_t)((int64_t)nr * g.cols * 2));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bins + (size_t)TT * base, (uint32_t)((int64_t)nr * g.cols * TT));
     const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
-    const uint32_t vt = lane_el * 4u, vb = lane_el * 2u;
+    const uint32_t vt = lane_el * 4u, vb = lane_el * (uint32_t)TT;
     // tile (tr, tc), lane element r: panel element (16 tr + 4 lg + r, 64 wv + 16 tc + li)
     auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
     // A row of tiles (4 tiles x 4 elements) is in flight while the previous row
@@ -2862,7 +2941,7 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
             for (int r = 0; r < 4; ++r) {
                 const uint32_t o = tile_off(tr, tc, r);
                 x[4 * tc + r] = bload1(rt, vt, o * 4u);
-                b[4 * tc + r] = bload1u16(rb, vb, o * 2u);
+                b[4 * tc + r] = ldg_bins<TT>(rb, vb, o * (uint32_t)TT);
             }
     };
     load_row(0, xa, ba);
@@ -2872,11 +2951,11 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
     stage_rows<RM>(g, rowtab, t.r0, nr, s_rows);
     // B operands: carriers 4 kc + lg of the lane's column in each column tile
     const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
-    float bq[4][3];
+    float bq[4][KCH];
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc)
 #pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
+        for (int kc = 0; kc < KCH; ++kc) {
             const int k = 4 * kc + lg;
             bq[tc][kc] = k < KC ? coltab[(size_t)k * g.cols + colw + 16 * tc + li] : 0.f;
         }
@@ -2896,12 +2975,13 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
     const float k_rat = ctrl->k_rat, k_ths = ctrl->k_ths, k_root = ctrl->k_root, k_t = ctrl->k_t, k_nov = ctrl->k_nov;
     const float k2 = -2.8853900817779268f * iclip;
     const float k2n = -2.8853900817779268f * ctrl->nscale;
-    const float c5 = ctrl->k_hash;   // set by fin3 (closed-form hash-term RMS)
-    float a_dd = 0.f;
+    const float c5 = C5C ? ctrl->k_hash : 0.f;   // set by fin3 (closed-form hash-term RMS)
+    constexpr float invT = 1.0f / (float)TT;
+    float a_dd = 0.f, a_dh = 0.f, a_hh = 0.f;
     auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const float* aP, const float* aX) {
         f32x4m pred = {cQ, cQ, cQ, cQ}, mixed = {cX, cX, cX, cX};
 #pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
+        for (int kc = 0; kc < KCH; ++kc) {
             pred = __builtin_amdgcn_mfma_f32_16x16x4f32(aP[kc], bq[tc][kc], pred, 0, 0, 0);
             mixed = __builtin_amdgcn_mfma_f32_16x16x4f32(aX[kc], bq[tc][kc], mixed, 0, 0, 0);
         }
@@ -2913,20 +2993,35 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
             const float at = fabsf(tv);
             const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
             const float core = xorsign(fmaf(k_t, at, fmaf(k_root, z.root, fmaf(k_ths, z.th, k_rat * z.rat))), tv);
-            const float hp = (s_imp[b[r] & 0xffu] + s_imp[B + (b[r] >> 8)]) * 0.5f;
-            const float d = fmaf(c5, hp, fmaf(k_nov, nov, core + mixed[r]));
-            bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
-            a_dd = fmaf(d, d, a_dd);
+            float hp = s_imp[bin_byte<TT>(b[r], 0)];
+#pragma unroll
+            for (int tt = 1; tt < TT; ++tt) hp += s_imp[tt * B + bin_byte<TT>(b[r], tt)];
+            hp = hp * invT;
+            if constexpr (C5C) {
+                const float d = fmaf(c5, hp, fmaf(k_nov, nov, core + mixed[r]));
+                bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
+                a_dd = fmaf(d, d, a_dd);
+            } else {
+                const float d = fmaf(k_nov, nov, core + mixed[r]);
+                bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
+                a_dd = fmaf(d, d, a_dd);
+                a_dh = fmaf(d, hp, a_dh);
+                a_hh = fmaf(hp, hp, a_hh);
+            }
         }
         pin1(a_dd);
+        if constexpr (!C5C) {
+            pin1(a_dh);
+            pin1(a_hh);
+        }
         elem_fence();
     };
     auto row_tiles = [&](int tr, const float* x, const uint32_t* b) {
         // A operands of this row of tiles: alpha_{4 kc + lg}(row 16 tr + li)
         const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
-        float aP[3], aX[3];
+        float aP[KCH], aX[KCH];
 #pragma unroll
-        for (int kc = 0; kc < 3; ++kc) {
+        for (int kc = 0; kc < KCH; ++kc) {
             aP[kc] = alr[4 * kc];
             aX[kc] = alr[KP + 4 * kc];
         }
@@ -2942,8 +3037,8 @@ __global__ __launch_bounds__(SP_NT, 4) void sweep4m_kernel(
     }
     Partials P{red, 3, NV4};
     P.add(0, a_dd);
-    P.add(1, 0.f);
-    P.add(2, 0.f);
+    P.add(1, a_dh);
+    P.add(2, a_hh);
     P.flush(part);
 }
 
@@ -3118,11 +3213,14 @@ size_t lds_sweep2(const Geom& g, int rw) {
 size_t lds_sweep3(const Geom& g, int kp, int rw) {
     return lds_al_off(g) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
 }
-size_t lds_sweep3m(const Geom& g, int kp, int rw) { return lds_sweep3(g, kp, rw) + sizeof(float) * ((size_t)kp * SP_BQS + SP_NT); }
+template <int KC> size_t lds_sweep3m(const Geom& g, int rw) {
+    return lds_sweep3(g, kcp<KC>(), rw) + sizeof(float) * ((bq_in_regs<KC>() ? 0 : (size_t)kcp<KC>() * SP_BQS) + SP_NT);
+}
 size_t lds_sweep4(const Geom& g, int kp, int rw) {
     return ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
 }
 constexpr size_t SP_LDS_MAX = 64 * 1024;
+constexpr size_t SP_LDS_MAX_M = 96 * 1024;   // dynamic LDS of a matrix-core sweep (gfx950: 160 KB per workgroup)
 
 // One step of `count` tensors of plan P: hd[0..count) are their descriptors
 // on the host; for count > 1, dv is the same array in device memory and each
@@ -3185,25 +3283,27 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     else
         hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), grid1, blk, 0, s, g, grad, param, part1, rowfx, colfx, ctrl,
                            st.force_rms, L, h);
-    const bool fast = fast_mode(g, hash_on, axes_on, h);
+    const bool fast = fast_mode(g, hash_on, axes_on, h);    // MODE 1 tiles of the general sweeps (two tables)
+    const bool mf = mfast_mode(g, hash_on, axes_on, h);     // the matrix-core sweeps (two or four tables)
+    const bool t4 = g.T == 4;
     // the matrix-core sweeps write per-block histogram partials (hpart),
     // which part_reduce sums into hist; the general sweeps add into hist
-    const bool m2 = fast && RM <= 8;
-    const bool m3 = fast && RM <= 8 && KC <= 12 && lds_sweep3m(g, kcp<KC>(), 2 * RM) <= SP_LDS_MAX;
-    if constexpr (RM <= 8) {
-        if (m2) {
-            hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl, part,
-                               hpart, rowfx, colfx, part1, st.force_rms, step, L, h);
-            goto swept2;
-        }
-    }
-    if (fast)
+    const bool m2 = mf;
+    const bool m3 = mf && lds_sweep3m<KC>(g, 2 * RM) <= SP_LDS_MAX_M;
+    if (m2) {
+        if (t4)
+            hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 4>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
+                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h);
+        else
+            hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 2>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
+                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h);
+    } else if (fast) {
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
-    else
+    } else {
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 0>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
-swept2:
+    }
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2 + (m2 ? g.T * g.B : 0), ny), dim3(256), 0, s, part, g.nblk, NV2, sums,
                        hpart, hist, L);
     hipLaunchKernelGGL(fin2_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st, ctrl,
@@ -3216,41 +3316,40 @@ swept2:
         hipLaunchKernelGGL(marg_fac_kernel, dim3((unsigned)((g.cols + SP_MARG_NT - 1) / SP_MARG_NT), ny), dim3(SP_MARG_NT),
                            0, s, g, terms, colfac, L);
     }
-    if constexpr (RM <= 8 && KC <= 12) {
-        if (m3) {
-            hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT>), grid, blk, lds_sweep3m(g, kcp<KC>(), 2 * RM), s, g, grad, rowtab,
-                               coltab, meta, bins, ctrl, lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h);
-            goto swept3;
-        }
-    }
-    if (fast)
+    if (m3) {
+        const size_t l3m = lds_sweep3m<KC>(g, 2 * RM);
+        if (t4)
+            hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 4>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
+                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h);
+        else
+            hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 2>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
+                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h);
+    } else if (fast) {
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 1>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, L, h);
-    else
+    } else {
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 0>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, L, h);
-swept3:
-    // sweep4m writes the full drive: fin3 then forms the hash term's RMS from
-    // the co-occurrence counts, and sweep 5 needs no bins
-    const int c5c = (KC <= 12 && fast && cooc_closed(g)) ? 1 : 0;
+    }
+    // with two tables sweep4m writes the full drive: fin3 then forms the hash
+    // term's RMS from the co-occurrence counts, and sweep 5 needs no bins
+    const int c5c = (mf && cooc_closed(g)) ? 1 : 0;
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 ? g.T * g.B : 0), ny), dim3(256), 0, s, part, g.nblk, NV3, sums,
                        hpart, hist, L);
     hipLaunchKernelGGL(fin3_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
                        cooc, step, hash_on, hard, echo_on, c5c, L, h);
-    if constexpr (KC <= 12) {
-        if (c5c) {
-            hipLaunchKernelGGL((sweep4m_kernel<RM, KC>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf,
-                               part, echo_on, L, h);
-            goto swept4;
-        }
-    }
-    if (fast)
+    if (c5c)
+        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
+                           tbuf, part, echo_on, L, h);
+    else if (mf && t4)
+        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
+                           tbuf, part, echo_on, L, h);
+    else if (fast)
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
                            hash_on, echo_on, L, h);
     else
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 0>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
                            hash_on, echo_on, L, h);
-swept4:
     const bool hash5 = hash_on && !c5c;   // sweep 5 adds the hash term itself
     const size_t l5 = hash5 ? sizeof(float) * (size_t)g.T * g.B : 0;
     if (hash5 && pv4)

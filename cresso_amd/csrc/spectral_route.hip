@@ -184,8 +184,8 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.part1 = take(sizeof(double) * 2 * (size_t)g.nblk1);   // sweep 1's sums and maxima, read by every block of sweep 2
     o.sums = take(sizeof(double) * (size_t)NVMAX);
     o.hist = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
-    // per-block histogram partials of the matrix-core sweeps (two tables of one-byte bins)
-    o.hpart = take(g.T == 2 && g.bpb == 1 ? sizeof(unsigned long long) * (size_t)g.T * g.B * g.nblk : 0);
+    // per-block histogram partials of the matrix-core sweeps (two or four tables of one-byte bins)
+    o.hpart = take(mtables(g) ? sizeof(unsigned long long) * (size_t)g.T * g.B * g.nblk : 0);
     o.lt = take(sizeof(float) * (size_t)g.T * g.B);
     o.imp = take(sizeof(float) * (size_t)g.T * g.B);
     o.rowfx = take(sizeof(unsigned long long) * (size_t)g.rows);
