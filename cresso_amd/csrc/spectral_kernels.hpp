@@ -109,7 +109,7 @@ struct Geom {
 
 struct Offs {
     size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins;   // shape tables
-    size_t tbuf, part, part1, sums, hist, hpart, lt, imp, rowfx, colfx, colfac, terms, ctrl, desc;   // per-step scratch
+    size_t tbuf, part, part1, sums, hist, hpart, lt, imp, rowfx, colfx, colfac, terms, ctrl, desc, shadow;   // per-step scratch
     size_t total;
 };
 
@@ -660,6 +660,13 @@ template <typename T> struct Ld4h {
 };
 template <> struct Ld4<__half> : Ld4h<__half> {};
 template <> struct Ld4<__hip_bfloat16> : Ld4h<__hip_bfloat16> {};
+template <> struct Ld4<double> {
+    __device__ static void go(const double* p, int64_t e, float* o) {
+        const double2 a = *reinterpret_cast<const double2*>(p + e);
+        const double2 b = *reinterpret_cast<const double2*>(p + e + 2);
+        o[0] = (float)a.x; o[1] = (float)a.y; o[2] = (float)b.x; o[3] = (float)b.y;
+    }
+};
 
 // 4 consecutive elements stored at e, rounded to the storage dtype
 template <typename T> struct St4;
@@ -1174,6 +1181,9 @@ template <> __device__ __forceinline__ float ldb_lane<__half>(const PanelBuf& b,
 template <> __device__ __forceinline__ float ldb_lane<__hip_bfloat16>(const PanelBuf& b, int lr) {
     return to_f(__builtin_bit_cast(__hip_bfloat16, (unsigned short)bload1u16(b.r, b.lane, (uint32_t)lr * b.row)));
 }
+template <> __device__ __forceinline__ float ldb_lane<double>(const PanelBuf& b, int lr) {
+    return (float)__builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(b.r, b.lane, (uint32_t)lr * b.row, 0));
+}
 __device__ __forceinline__ uint32_t ldb_bins16(const PanelBuf& b, int lr) {
     return bload1u16(b.r, b.lane, (uint32_t)lr * b.row);
 }
@@ -1486,6 +1496,9 @@ template <> __device__ __forceinline__ float ldg_el<__half>(__amdgpu_buffer_rsrc
 template <>
 __device__ __forceinline__ float ldg_el<__hip_bfloat16>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return to_f(__builtin_bit_cast(__hip_bfloat16, (unsigned short)bload1u16(r, voff, soff)));
+}
+template <> __device__ __forceinline__ float ldg_el<double>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (float)__builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
 
 // Sum over each 16-lane DPP row (every lane of the row gets its row's total,
@@ -3099,6 +3112,17 @@ __device__ __forceinline__ void apply1(PT* __restrict__ param, int64_t e, float 
     const float u = to_f(from_w<PT>(drive * gain));
     param[e] = from_w<PT>(to_f(param[e]) + nlr * u);
 }
+// sweep 5's param loads for the fp32 update (fp64 params are read where the
+// fp64 update is formed)
+template <typename PT> __device__ __forceinline__ void pre4(const PT* __restrict__ p, int64_t e, float* o) {
+    if constexpr (!std::is_same<PT, double>::value) Ld4<PT>::go(p, e, o);
+}
+// fp64 params: the step's drive and gain come from the fp32 sweeps; the
+// update p + (-lr) (drive gain) is formed in fp64 as the reference's fp64
+// add_ forms it (cresso_v5.py:1353)
+__device__ __forceinline__ void apply1d(double* __restrict__ param, int64_t e, float drive, float gain, double nlr) {
+    param[e] = param[e] + nlr * (double)(drive * gain);
+}
 
 template <typename PT, bool HASH, bool V4>
 __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
@@ -3125,8 +3149,8 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
     if (pre) {
         d0 = *reinterpret_cast<const float4*>(dbuf + e);
         d1 = *reinterpret_cast<const float4*>(dbuf + e + st);
-        Ld4<PT>::go(param, e, p0);
-        Ld4<PT>::go(param, e + st, p1);
+        pre4<PT>(param, e, p0);
+        pre4<PT>(param, e + st, p1);
     }
     float gain, c5;
     fin4_values(g, part, ctrl, de_state, step, hash_on, hard, c5_closed, h, gain, c5);
@@ -3152,13 +3176,25 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
     };
     auto apply4 = [&](int64_t e, const float4& d4, const float* pv) {
         const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-        float o[4];
+        if constexpr (std::is_same<PT, double>::value) {
+            const double nlrd = -h.lr;
+            double2* q = reinterpret_cast<double2*>(param + e);
+            double2 a = q[0], b = q[1];
+            a.x += nlrd * (double)(drive_at(e, dv[0]) * gain);
+            a.y += nlrd * (double)(drive_at(e + 1, dv[1]) * gain);
+            b.x += nlrd * (double)(drive_at(e + 2, dv[2]) * gain);
+            b.y += nlrd * (double)(drive_at(e + 3, dv[3]) * gain);
+            q[0] = a;
+            q[1] = b;
+        } else {
+            float o[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float u = to_f(from_w<PT>(drive_at(e + c, dv[c]) * gain));
-            o[c] = pv[c] + nlr * u;
+            for (int c = 0; c < 4; ++c) {
+                const float u = to_f(from_w<PT>(drive_at(e + c, dv[c]) * gain));
+                o[c] = pv[c] + nlr * u;
+            }
+            St4<PT>::go(param, e, o);
         }
-        St4<PT>::go(param, e, o);
     };
     // two float4 of drive and param per thread in flight per iteration, then the rest
     if (pre) {
@@ -3170,18 +3206,23 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
         const float4 da = *reinterpret_cast<const float4*>(dbuf + e);
         const float4 db = *reinterpret_cast<const float4*>(dbuf + e + st);
         float pa[4], pb[4];
-        Ld4<PT>::go(param, e, pa);
-        Ld4<PT>::go(param, e + st, pb);
+        pre4<PT>(param, e, pa);
+        pre4<PT>(param, e + st, pb);
         apply4(e, da, pa);
         apply4(e + st, db, pb);
     }
     for (; e < vend; e += st) {
         const float4 d4 = *reinterpret_cast<const float4*>(dbuf + e);
         float pv[4];
-        Ld4<PT>::go(param, e, pv);
+        pre4<PT>(param, e, pv);
         apply4(e, d4, pv);
     }
-    for (int64_t e = vend + threadIdx.x; e < end; e += SP_NT) apply1(param, e, drive_at(e, dbuf[e]), gain, nlr);
+    for (int64_t e = vend + threadIdx.x; e < end; e += SP_NT) {
+        if constexpr (std::is_same<PT, double>::value)
+            apply1d(param, e, drive_at(e, dbuf[e]), gain, -h.lr);
+        else
+            apply1(param, e, drive_at(e, dbuf[e]), gain, nlr);
+    }
 }
 
 
@@ -3398,6 +3439,7 @@ CRESSO_SP_DECL(spectral_run_bf16_bf16)
 CRESSO_SP_DECL(spectral_run_f16_f16)
 CRESSO_SP_DECL(spectral_run_f32_bf16)
 CRESSO_SP_DECL(spectral_run_f32_f16)
+CRESSO_SP_DECL(spectral_run_f64_f64)
 #undef CRESSO_SP_DECL
 
 }  // namespace cresso

@@ -196,6 +196,8 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.terms = take(sizeof(float) * (size_t)std::max<int64_t>(1, sum_trail));
     o.ctrl = take(sizeof(Ctrl));
     o.desc = take(sizeof(cresso_spectral_desc));   // the tensor's descriptor in a batched step
+    // fp32 copy of an fp64 param's state (4 scalars, 12 rank vectors, 3 hash tables)
+    o.shadow = take(sizeof(float) * (4 + 12 * (size_t)g.R + 3 * (size_t)g.T * g.B));
     o.total = off;
     return CRESSO_OK;
 }
@@ -320,6 +322,7 @@ SpectralRunFn find_run(int pt, int gt) {
         {CRESSO_F16, CRESSO_F16, spectral_run_f16_f16},
         {CRESSO_F32, CRESSO_BF16, spectral_run_f32_bf16},
         {CRESSO_F32, CRESSO_F16, spectral_run_f32_f16},
+        {CRESSO_F64, CRESSO_F64, spectral_run_f64_f64},
     };
     for (const auto& e : table)
         if (e.pt == pt && e.gt == gt) return e.fn;
@@ -360,6 +363,68 @@ __global__ __launch_bounds__(256) void ws_lanes_kernel(unsigned char* __restrict
     for (int64_t i = threadIdx.x; i < tb; i += blockDim.x) hh[i] = 0ull;
 }
 static_assert(sizeof(Ctrl) % 8 == 0, "control block copied as 64-bit words");
+
+// fp64 params keep fp64 state (the reference's state dtype follows the work
+// dtype, cresso_v5.py:119-124).  The step's finishes read and write fp32
+// state: the state goes through an fp32 copy in the workspace, converted
+// before and after the step's kernels on the same stream.
+constexpr int XFER_MAX = 19;
+struct StateXfer {
+    const void* src[XFER_MAX];
+    void* dst[XFER_MAX];
+    int32_t n[XFER_MAX];
+    int32_t count, to_f32;
+};
+__global__ __launch_bounds__(256) void state_xfer_kernel(StateXfer x) {
+    for (int a = 0; a < x.count; ++a)
+        for (int i = threadIdx.x; i < x.n[a]; i += blockDim.x) {
+            if (x.to_f32)
+                reinterpret_cast<float*>(x.dst[a])[i] = (float)reinterpret_cast<const double*>(x.src[a])[i];
+            else
+                reinterpret_cast<double*>(x.dst[a])[i] = (double)reinterpret_cast<const float*>(x.src[a])[i];
+        }
+}
+
+// The descriptor of the step on the fp32 copy (state pointers into the
+// workspace's shadow) and the two transfers (in: every state array; out:
+// every array but the constant omega).
+void shadow_state(const cresso_spectral_plan* P, const cresso_spectral_desc& d, void* ws, cresso_spectral_desc& sd,
+                  StateXfer& in, StateXfer& out) {
+    const Geom& g = P->g;
+    sd = d;
+    float* sh = at<float>(ws, P->o.shadow);
+    std::memset(&in, 0, sizeof(in));
+    std::memset(&out, 0, sizeof(out));
+    in.to_f32 = 1;
+    out.to_f32 = 0;
+    auto add = [&](void*& field, int n, bool writes) {
+        if (!field) return;
+        in.src[in.count] = field;
+        in.dst[in.count] = sh;
+        in.n[in.count++] = n;
+        if (writes) {
+            out.src[out.count] = sh;
+            out.dst[out.count] = field;
+            out.n[out.count++] = n;
+        }
+        field = sh;
+        sh += n;
+    };
+    const int R = g.R, TB = g.T * g.B;
+    add(sd.force_rms, 1, true);
+    add(sd.drive_energy, 1, true);
+    add(sd.surprise, 1, true);
+    add(sd.action, 1, true);
+    void* om = const_cast<void*>(sd.omega);
+    add(om, R, false);
+    sd.omega = om;
+    void** vecs[] = {&sd.q_cos, &sd.q_sin, &sd.p_cos, &sd.p_sin, &sd.metric_cos, &sd.metric_sin, &sd.metric_p_cos,
+                     &sd.metric_p_sin, &sd.calcium_cos, &sd.calcium_sin, &sd.mode_confidence};
+    for (void** v : vecs) add(*v, R, true);
+    add(sd.hash_energy, TB, true);
+    add(sd.hash_impulse, TB, true);
+    add(sd.hash_refractory, TB, true);
+}
 }  // namespace
 
 extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cresso_spectral_desc* d, void* ws,
@@ -371,7 +436,17 @@ extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cre
     if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "spectral route: drive_clip must be positive");
     const SpectralRunFn fn = find_run(d->param_dtype, d->grad_dtype);
     if (!fn) return CRESSO_E_UNSUPPORTED;
-    return fn(*P, d, 1, nullptr, 0, ws, *hyper, reinterpret_cast<hipStream_t>(stream));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (d->param_dtype != CRESSO_F64) return fn(*P, d, 1, nullptr, 0, ws, *hyper, s);
+    cresso_spectral_desc sd;
+    StateXfer in, out;
+    shadow_state(P, *d, ws, sd, in, out);
+    hipLaunchKernelGGL(state_xfer_kernel, dim3(1), dim3(256), 0, s, in);
+    const int32_t r = fn(*P, &sd, 1, nullptr, 0, ws, *hyper, s);
+    if (r != CRESSO_OK) return r;
+    hipLaunchKernelGGL(state_xfer_kernel, dim3(1), dim3(256), 0, s, out);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: fp64 state transfer");
 }
 
 extern "C" size_t cresso_spectral_batched_workspace_bytes(const cresso_spectral_plan* P, int32_t count) {
@@ -405,6 +480,8 @@ extern "C" int32_t cresso_spectral_step_batched(const cresso_spectral_plan* P, c
         return fail(CRESSO_E_INVALID, "spectral route: batched workspace too small for %d tensors", count);
     if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "spectral route: drive_clip must be positive");
     const cresso_spectral_desc& d0 = descs[0];
+    if (d0.param_dtype == CRESSO_F64)
+        return fail(CRESSO_E_UNSUPPORTED, "spectral route: fp64 params step one tensor at a time (cresso_spectral_step)");
     for (int i = 0; i < count; ++i) {
         const cresso_spectral_desc& d = descs[i];
         const int32_t rc = check_desc(P, &d);

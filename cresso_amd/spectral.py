@@ -35,9 +35,11 @@ import torch
 from . import _native
 
 # (param dtype, grad dtype) pairs of the library's spectral step; the force is
-# the grad converted to the work dtype (fp32), as in cresso_v5.py:907-912
+# the grad converted to the work dtype (fp32), as in cresso_v5.py:907-912.
+# fp64 params keep fp64 state (cresso_v5.py:119-124); the library steps them
+# in fp32 with the update added in fp64.
 _DTYPE_PAIRS = {(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
-                (torch.float32, torch.bfloat16), (torch.float32, torch.float16)}
+                (torch.float32, torch.bfloat16), (torch.float32, torch.float16), (torch.float64, torch.float64)}
 
 _VEC_KEYS = ("q_cos", "q_sin", "p_cos", "p_sin", "metric_cos", "metric_sin", "metric_p_cos", "metric_p_sin",
              "calcium_cos", "calcium_sin", "mode_confidence")
@@ -152,11 +154,12 @@ class SpectralEngine:
     def _prepare(self, param: torch.Tensor, grad: torch.Tensor, st: dict, group: dict):
         """Validate one tensor's state and build its descriptor; -> (key, rank, desc)."""
         if (param.dtype, grad.dtype) not in _DTYPE_PAIRS:
-            raise RuntimeError(f"CRESSO5 spectral route on MI355X supports fp32/bf16/fp16 params with grads of the "
-                               f"same dtype, and fp32 params with bf16/fp16 grads (got {param.dtype} / {grad.dtype})")
-        for k in ("force_rms", "omega") + _VEC_KEYS:
-            if st[k].dtype != torch.float32:
-                raise RuntimeError(f"CRESSO5 spectral state {k} has dtype {st[k].dtype}, expected float32")
+            raise RuntimeError(f"CRESSO5 spectral route on MI355X supports fp64/fp32/bf16/fp16 params with grads of "
+                               f"the same dtype, and fp32 params with bf16/fp16 grads (got {param.dtype} / {grad.dtype})")
+        sdt = torch.float64 if param.dtype == torch.float64 else torch.float32
+        for k in ("force_rms", "drive_energy", "surprise", "action", "omega") + _VEC_KEYS:
+            if st[k].dtype != sdt:
+                raise RuntimeError(f"CRESSO5 spectral state {k} has dtype {st[k].dtype}, expected {sdt}")
         rank = int(st["omega"].numel())
         freqs = self._freqs(st)
         bins, tables = int(group["hash_bins"]), int(group["hash_tables"])
@@ -180,9 +183,9 @@ class SpectralEngine:
             setattr(d, k, st[k].data_ptr())
         if hard and bins > 0 and "hash_energy" in st:
             for k in ("hash_energy", "hash_impulse", "hash_refractory"):
-                if tuple(st[k].shape) != (tables, bins) or st[k].dtype != torch.float32:
+                if tuple(st[k].shape) != (tables, bins) or st[k].dtype != sdt:
                     raise RuntimeError(f"CRESSO5 spectral state {k} has shape {tuple(st[k].shape)}, expected "
-                                       f"({tables}, {bins}) float32 (hash_bins/hash_tables changed after init?)")
+                                       f"({tables}, {bins}) {sdt} (hash_bins/hash_tables changed after init?)")
             d.hash_energy = st["hash_energy"].data_ptr()
             d.hash_impulse = st["hash_impulse"].data_ptr()
             d.hash_refractory = st["hash_refractory"].data_ptr()
@@ -216,11 +219,14 @@ class SpectralEngine:
 
     def _units(self, prepared: list, sts: list) -> list:
         """Cut a step's tensors into units: (unit key, plan key, rank, [desc], [state]).
-        Tensors batch when they share the plan, dtypes, hard channel and hash state."""
+        Tensors batch when they share the plan, dtypes, hard channel and hash
+        state; fp64 tensors step one at a time (the library's fp64 state
+        transfer is per tensor)."""
         groups: Dict[tuple, list] = {}
         for i, (key, rank, d) in enumerate(prepared):
             bkey = (key, d.param_dtype, d.grad_dtype, d.hard, bool(d.hash_energy))
-            groups.setdefault(bkey if self.BATCH else (bkey, i), []).append(i)
+            alone = not self.BATCH or d.param_dtype == _native.F64
+            groups.setdefault((bkey, i) if alone else bkey, []).append(i)
         units = []
         for bkey, idx in groups.items():
             key, rank, _ = prepared[idx[0]]

@@ -159,7 +159,10 @@ typedef struct cresso_spectral_desc {
     int32_t param_dtype;
     int32_t grad_dtype;
     int64_t numel;
-    /* state of cresso_v5.py:857-883, fp32, updated in place */
+    /* state of cresso_v5.py:857-883, updated in place: fp32, or fp64 when
+     * param_dtype is F64 (the reference's state follows the work dtype,
+     * v5.py:119-124; an F64 step computes in fp32 through an fp32 copy of the
+     * state in the workspace and adds the update to the param in fp64) */
     void *force_rms, *drive_energy, *surprise, *action;       /* 0-dim       */
     const void* omega;                                         /* [rank]      */
     void *q_cos, *q_sin, *p_cos, *p_sin;                       /* [rank]      */
@@ -170,7 +173,9 @@ typedef struct cresso_spectral_desc {
     int32_t hard;             /* hard channel on (cresso_v5.py:981-983)     */
 } cresso_spectral_desc;
 
-/* One optimizer step of one tensor on the spectral route. */
+/* One optimizer step of one tensor on the spectral route.  (param, grad)
+ * dtype pairs: (F32,F32), (BF16,BF16), (F16,F16), (F32,BF16), (F32,F16),
+ * (F64,F64). */
 int32_t cresso_spectral_step(const cresso_spectral_plan* plan, const cresso_spectral_desc* desc, void* workspace,
                              size_t workspace_bytes, const cresso_hyper* hyper, void* stream);
 
@@ -185,7 +190,8 @@ int32_t cresso_spectral_step(const cresso_spectral_plan* plan, const cresso_spec
  * differ in every pointer and in `step`, not in dtypes, `hard` or whether
  * hash state is given.  The library copies them to the device as kernel
  * arguments on `stream` (no host synchronization).  Every tensor's results
- * are bit-identical to cresso_spectral_step of it.
+ * are bit-identical to cresso_spectral_step of it.  F64 params are not batched (CRESSO_E_UNSUPPORTED):
+ * step them with cresso_spectral_step.
  *
  * The workspace: cresso_spectral_batched_workspace_bytes(plan, count) bytes,
  * set up once by cresso_spectral_batched_workspace_init (which synchronizes

@@ -108,7 +108,7 @@ def check_update(dg: np.ndarray, de: np.ndarray, rtol: float, what: str) -> floa
     return worst
 
 
-def compare(hp, hopt, op, oopt, param_tol=F32_TOL, state_tol=F32_TOL, skip_keys=()):
+def compare(hp, hopt, op, oopt, param_tol=F32_TOL, state_tol=F32_TOL, skip_keys=(), dp_rtol=None):
     prev = _PREV.get(hopt)
     for i, (a, b) in enumerate(zip(hp, op)):
         what = f"param {i} shape {tuple(b.shape)} {b.dtype}"
@@ -123,7 +123,7 @@ def compare(hp, hopt, op, oopt, param_tol=F32_TOL, state_tol=F32_TOL, skip_keys=
             if prev is not None and b.dtype in DP_RTOL:
                 dg = got - prev[0][i].double().cpu().numpy()
                 de = exp - prev[1][i].double().numpy()
-                check_update(dg, de, DP_RTOL[b.dtype], what)
+                check_update(dg, de, DP_RTOL[b.dtype] if dp_rtol is None else dp_rtol, what)
         sa = hopt.state[a]
         sb = oopt.state[i]
         assert set(sa.keys()) == set(sb.keys()), (sorted(sa), sorted(sb))

@@ -377,3 +377,40 @@ def test_spectral_loads_float_cast_checkpoint():
         oopt.step([grads[k]])
     torch.cuda.synchronize()
     compare([hp2], hopt2, [op], oopt, param_tol=BF16_PARAM_TOL)
+
+
+# fp64 params on the spectral route: fp64 param and grad I/O with the update
+# added in fp64 (cresso_v5.py:1353) and fp64 state (v5.py:119-124), the
+# step's arithmetic in fp32 -- so the fp64 oracle is matched to the fp32
+# tolerances (params, states, and the update at DP_RTOL[float32]).
+FP64_CASES = [("general", (300, 257), 3), ("fast_tiles", (2048, 4096), 2)]
+
+
+@pytest.mark.parametrize("case", FP64_CASES, ids=[c[0] for c in FP64_CASES])
+def test_spectral_fp64_params(case):
+    name, shape, steps = case
+    announce(f"spectral fp64 {name} {shape}")
+    import cresso_amd
+    from gpu_util import DP_RTOL
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    kw = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2)
+    gen = torch.Generator().manual_seed(23)
+    p0 = 0.02 * torch.randn(shape, generator=gen, dtype=torch.float64)
+    hp = torch.nn.Parameter(p0.clone().cuda())
+    hopt = cresso_amd.CRESSO5([hp], cuda_ops="required", **kw)
+    op = p0.clone()
+    oopt = OracleCRESSO5([op], hash_accum="fp64", **kw)
+    from gpu_util import _PREV
+    for k in range(steps):
+        g = 1e-3 * torch.randn(shape, generator=gen, dtype=torch.float64)
+        g = torch.where(torch.rand(shape, generator=gen, dtype=torch.float64) < 0.01, g * 50.0, g)
+        if k == steps - 1:
+            torch.cuda.synchronize()
+            _PREV[hopt] = ([hp.detach().clone()], [op.clone()])
+        hp.grad = g.cuda()
+        hopt.step()
+        oopt.step([g])
+    torch.cuda.synchronize()
+    assert hp.dtype == torch.float64 and hopt.state[hp]["q_cos"].dtype == torch.float64
+    compare([hp], hopt, [op], oopt, dp_rtol=DP_RTOL[torch.float32])
