@@ -150,7 +150,8 @@ def make_c5(device, pool=2, seed=0):
     return params, grads, kwargs, C5_SHAPES, None
 
 
-TRAFFIC_FILES = {"c2": "profiles/spectral_step_c2_hbm_traffic.md", "c3": "profiles/scalar_step_c3_hbm_traffic.md"}
+TRAFFIC_FILES = {"c2": "profiles/spectral_step_c2_hbm_traffic.md", "c3": "profiles/scalar_step_c3_hbm_traffic.md",
+                 "c4": "profiles/spectral_step_c4_hbm_traffic.md", "c5": "profiles/spectral_step_c5_hbm_traffic.md"}
 SOURCE_GLOBS = ("cresso_amd/csrc/*.hip", "cresso_amd/csrc/*.hpp", "cresso_amd/csrc/*.cpp")
 
 
@@ -337,6 +338,27 @@ def rocprof_summary(dirs, calib=None, launches=None):
         if launches:
             out.append(f"\nkernel time per launch of the hot path (library kernels without one-time set-up, "
                        f"{launches} launches): {per_launch:.2f} us\n")
+    for path in found("*kernel_trace.csv"):
+        # per (kernel, grid): workloads of several shapes launch each kernel at several grids
+        from collections import defaultdict
+        acc = defaultdict(lambda: [0, 0.0])
+        for r in _read_csv(path):
+            if not _hot(r["Kernel_Name"]):
+                continue
+            wg = max(1, int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"]))
+            blocks = (int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])) // wg
+            a = acc[(_short_kernel(r["Kernel_Name"]), blocks)]
+            a[0] += 1
+            a[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if len({k for k, _ in acc}) == len(acc):
+            continue   # one grid per kernel: the table above says it all
+        out.append(f"### Kernel durations per grid ({os.path.basename(path)}, library kernels of the step)\n")
+        out.append("| kernel | workgroups | calls | avg us | us per launch |")
+        out.append("|---|---:|---:|---:|---:|")
+        for (k, blocks), (calls, tot) in sorted(acc.items(), key=lambda kv: -kv[1][1]):
+            per = f"{tot / launches:.1f}" if launches else ""
+            out.append(f"| {k} | {blocks} | {calls} | {tot / calls:.2f} | {per} |")
+        out.append("")
     cc = found("*counter_collection.csv")
     if cc:
         means = _counter_means(cc)

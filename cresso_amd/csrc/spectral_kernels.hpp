@@ -50,6 +50,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -1290,12 +1291,22 @@ inline bool fast_mode(const Geom& g, int hash_on, int axes_on, const cresso_hype
 __host__ __device__ inline bool mtables(const Geom& g) {
     return (g.T == 2 || g.T == 4) && g.bpb == 1 && g.binbytes == g.T;
 }
+// The environment variable CRESSO_SPECTRAL_MATRIX_CORES=0 turns the
+// matrix-core sweeps off (the general sweeps run instead, same results within
+// rounding): a measurement switch for comparing the two forms on one build.
+inline bool matrix_cores_enabled() {
+    static const bool on = [] {
+        const char* v = std::getenv("CRESSO_SPECTRAL_MATRIX_CORES");
+        return !(v && v[0] == '0' && v[1] == 0);
+    }();
+    return on;
+}
 // whether a tensor's step can use the matrix-core sweeps (host side): MODE 1's
 // conditions with 2 or 4 tables
 inline bool mfast_mode(const Geom& g, int hash_on, int axes_on, const cresso_hyper& h) {
     return hash_on && axes_on && mtables(g) && !g.one_d && h.weight_decay == 0.0 && h.local_sharpness == 0.0 &&
            (float)fmax(h.instant_metric_power, 0.25) == 1.0f && g.rows % g.PR == 0 && g.cols % SP_NT == 0 &&
-           g.PR % (4 * SP_U) == 0;
+           g.PR % (4 * SP_U) == 0 && matrix_cores_enabled();
 }
 
 // ---------------------------------------------------------------------------
