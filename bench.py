@@ -278,9 +278,10 @@ def _read_csv(path):
         return list(csv.DictReader(fh))
 
 
-def _counter_means(paths):
+def _counter_means(paths, by_grid=False):
     """{kernel: {counter: (mean value per dispatch, dispatches)}}; rows of one
-    dispatch (counter dimensions) are summed first."""
+    dispatch (counter dimensions) are summed first.  by_grid: keyed by
+    "kernel @ workgroups" instead."""
     from collections import defaultdict
     per = defaultdict(float)
     names = {}
@@ -288,8 +289,10 @@ def _counter_means(paths):
         for row in _read_csv(path):
             key = (path, row["Dispatch_Id"], row["Counter_Name"])
             per[key] += float(row["Counter_Value"])
-            names[(path, row["Dispatch_Id"])] = ("*" if _hot(row["Kernel_Name"]) else "") + \
-                _short_kernel(row["Kernel_Name"])
+            name = ("*" if _hot(row["Kernel_Name"]) else "") + _short_kernel(row["Kernel_Name"])
+            if by_grid:
+                name += f" @ {int(row['Grid_Size']) // max(1, int(row['Workgroup_Size']))}"
+            names[(path, row["Dispatch_Id"])] = name
     agg = defaultdict(lambda: defaultdict(list))
     for (path, did, cn), v in per.items():
         agg[names[(path, did)]][cn].append(v)
@@ -412,6 +415,26 @@ def rocprof_summary(dirs, calib=None, launches=None):
                 t_v = (iv - mf + 3.0 * tr) * 4 / 1024 / 2.4e9 * 1e6
                 t_m = mf * 32 / 1024 / 2.4e9 * 1e6
                 out.append(f"| {k} | {iv:.4g} | {100 * tr / max(iv, 1):.1f} | {t_v:.1f} | {mf:.4g} | {t_m:.1f} |")
+        # workloads of several shapes: the same per launch grid of the library's kernels
+        gm = {k: d_ for k, d_ in _counter_means(cc, by_grid=True).items() if k.startswith("*")}
+        if len(gm) > len([k for k in means if k.startswith("*")]):
+            hdr = [cn for cn in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "FETCH_SIZE", "WRITE_SIZE") if cn in counters]
+            out.append("\n### Per launch grid (kernel @ workgroups), mean per dispatch\n")
+            cols = hdr + (["VALU issue us", "MFMA busy us"] if "SQ_INSTS_VALU" in hdr else [])
+            cols += [f"{cn} bytes" for cn in ("FETCH_SIZE", "WRITE_SIZE") if cn in hdr and cn in scale]
+            out.append("| kernel @ workgroups | dispatches | " + " | ".join(cols) + " |")
+            out.append("|---|---:|" + "---:|" * len(cols))
+            for k, d_ in sorted(gm.items(), key=lambda kv: kv[0]):
+                n = max(v[1] for v in d_.values())
+                vals = [f"{d_[cn][0]:.5g}" if cn in d_ else "" for cn in hdr]
+                if "SQ_INSTS_VALU" in hdr:
+                    iv = d_.get("SQ_INSTS_VALU", (0.0, 0))[0]
+                    tr = d_.get("SQ_INSTS_VALU_TRANS_F32", (0.0, 0))[0]
+                    mf = d_.get("SQ_INSTS_MFMA", (0.0, 0))[0]
+                    vals += [f"{(iv - mf + 3.0 * tr) * 4 / 1024 / 2.4e9 * 1e6:.1f}", f"{mf * 32 / 1024 / 2.4e9 * 1e6:.1f}"]
+                vals += [f"{d_[cn][0] * 1024.0 * scale[cn]:.4g}" for cn in ("FETCH_SIZE", "WRITE_SIZE")
+                         if cn in hdr and cn in scale and cn in d_]
+                out.append(f"| {k} | {n} | " + " | ".join(vals) + " |")
     print("\n".join(out))
 
 
