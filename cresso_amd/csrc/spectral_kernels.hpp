@@ -3135,6 +3135,41 @@ __device__ __forceinline__ void apply1d(double* __restrict__ param, int64_t e, f
     param[e] = param[e] + nlr * (double)(drive * gain);
 }
 
+// The packed bins of 4 consecutive elements (e a multiple of 4), one vector
+// load for all four (the bins array is 256-byte aligned).
+struct Bins4 {
+    uint64_t pk[4];
+};
+__device__ __forceinline__ Bins4 ld_bins4(const unsigned char* __restrict__ bins, int64_t e, int binbytes) {
+    Bins4 r;
+    switch (binbytes) {
+        case 1: {
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(bins + e);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) r.pk[c] = (v >> (8 * c)) & 0xffu;
+            break;
+        }
+        case 2: {
+            const uint2 v = *reinterpret_cast<const uint2*>(bins + 2 * e);
+            r.pk[0] = v.x & 0xffffu; r.pk[1] = v.x >> 16; r.pk[2] = v.y & 0xffffu; r.pk[3] = v.y >> 16;
+            break;
+        }
+        case 4: {
+            const uint4 v = *reinterpret_cast<const uint4*>(bins + 4 * e);
+            r.pk[0] = v.x; r.pk[1] = v.y; r.pk[2] = v.z; r.pk[3] = v.w;
+            break;
+        }
+        default: {
+            const uint4 a = *reinterpret_cast<const uint4*>(bins + 8 * e);
+            const uint4 b = *reinterpret_cast<const uint4*>(bins + 8 * e + 16);
+            r.pk[0] = ((uint64_t)a.y << 32) | a.x; r.pk[1] = ((uint64_t)a.w << 32) | a.z;
+            r.pk[2] = ((uint64_t)b.y << 32) | b.x; r.pk[3] = ((uint64_t)b.w << 32) | b.z;
+            break;
+        }
+    }
+    return r;
+}
+
 template <typename PT, bool HASH, bool V4>
 __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
     Geom g, PT* __restrict__ param, const float* __restrict__ dbuf, const unsigned char* __restrict__ bins,
@@ -3152,21 +3187,26 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
     const int64_t vend = V4 ? beg + ((end - beg) & ~(int64_t)3) : beg;
     const int64_t st = 4 * (int64_t)SP_NT;
     int64_t e = beg + 4 * (int64_t)threadIdx.x;
-    // the first two float4 of drive and param go out before the gain is known
-    // (their loads stay in flight through the finish's reduction)
+    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
+    // the first two float4 of drive and param (and their bins) go out before
+    // the gain is known (their loads stay in flight through the finish's reduction)
     const bool pre = e + st < vend;
     float4 d0 = make_float4(0.f, 0.f, 0.f, 0.f), d1 = d0;
     float p0[4] = {0.f, 0.f, 0.f, 0.f}, p1[4] = {0.f, 0.f, 0.f, 0.f};
+    Bins4 b0{}, b1{};
     if (pre) {
         d0 = *reinterpret_cast<const float4*>(dbuf + e);
         d1 = *reinterpret_cast<const float4*>(dbuf + e + st);
         pre4<PT>(param, e, p0);
         pre4<PT>(param, e + st, p1);
+        if (HASH) {
+            b0 = ld_bins4(bins, e, binbytes);
+            b1 = ld_bins4(bins, e + st, binbytes);
+        }
     }
     float gain, c5;
     fin4_values(g, part, ctrl, de_state, step, hash_on, hard, c5_closed, h, gain, c5);
-    const int TB = g.T * g.B;
-    const int T = g.T, B = g.B, bpb = g.bpb, binbytes = g.binbytes;
+    const int TB = T * B;
     float* s_imp = reinterpret_cast<float*>(dyn);
     if (HASH) {
         for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
@@ -3174,9 +3214,8 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
     }
     const float kh = c5 * (1.0f / (float)T);
     const float nlr = (float)update_alpha<PT>(-h.lr);
-    auto drive_at = [&](int64_t e, float d) -> float {
+    auto drive_pk = [&](uint64_t pk, float d) -> float {
         if (!HASH) return d;
-        const uint64_t pk = load_bins(bins, e, binbytes);
         float hp = 0.f;
 #pragma unroll
         for (int tt = 0; tt < SP_MAXT; ++tt) {
@@ -3185,32 +3224,33 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
         }
         return d + kh * hp;
     };
-    auto apply4 = [&](int64_t e, const float4& d4, const float* pv) {
+    auto drive_at = [&](int64_t e, float d) -> float { return HASH ? drive_pk(load_bins(bins, e, binbytes), d) : d; };
+    auto apply4 = [&](int64_t e, const float4& d4, const float* pv, const Bins4& bk) {
         const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
         if constexpr (std::is_same<PT, double>::value) {
             const double nlrd = -h.lr;
             double2* q = reinterpret_cast<double2*>(param + e);
             double2 a = q[0], b = q[1];
-            a.x += nlrd * (double)(drive_at(e, dv[0]) * gain);
-            a.y += nlrd * (double)(drive_at(e + 1, dv[1]) * gain);
-            b.x += nlrd * (double)(drive_at(e + 2, dv[2]) * gain);
-            b.y += nlrd * (double)(drive_at(e + 3, dv[3]) * gain);
+            a.x += nlrd * (double)(drive_pk(bk.pk[0], dv[0]) * gain);
+            a.y += nlrd * (double)(drive_pk(bk.pk[1], dv[1]) * gain);
+            b.x += nlrd * (double)(drive_pk(bk.pk[2], dv[2]) * gain);
+            b.y += nlrd * (double)(drive_pk(bk.pk[3], dv[3]) * gain);
             q[0] = a;
             q[1] = b;
         } else {
             float o[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const float u = to_f(from_w<PT>(drive_at(e + c, dv[c]) * gain));
+                const float u = to_f(from_w<PT>(drive_pk(bk.pk[c], dv[c]) * gain));
                 o[c] = pv[c] + nlr * u;
             }
             St4<PT>::go(param, e, o);
         }
     };
-    // two float4 of drive and param per thread in flight per iteration, then the rest
+    // two float4 of drive and param (and their bins) per thread in flight per iteration, then the rest
     if (pre) {
-        apply4(e, d0, p0);
-        apply4(e + st, d1, p1);
+        apply4(e, d0, p0, b0);
+        apply4(e + st, d1, p1, b1);
         e += 2 * st;
     }
     for (; e + st < vend; e += 2 * st) {
@@ -3219,14 +3259,21 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
         float pa[4], pb[4];
         pre4<PT>(param, e, pa);
         pre4<PT>(param, e + st, pb);
-        apply4(e, da, pa);
-        apply4(e + st, db, pb);
+        Bins4 ba{}, bb{};
+        if (HASH) {
+            ba = ld_bins4(bins, e, binbytes);
+            bb = ld_bins4(bins, e + st, binbytes);
+        }
+        apply4(e, da, pa, ba);
+        apply4(e + st, db, pb, bb);
     }
     for (; e < vend; e += st) {
         const float4 d4 = *reinterpret_cast<const float4*>(dbuf + e);
         float pv[4];
         pre4<PT>(param, e, pv);
-        apply4(e, d4, pv);
+        Bins4 bk{};
+        if (HASH) bk = ld_bins4(bins, e, binbytes);
+        apply4(e, d4, pv, bk);
     }
     for (int64_t e = vend + threadIdx.x; e < end; e += SP_NT) {
         if constexpr (std::is_same<PT, double>::value)
