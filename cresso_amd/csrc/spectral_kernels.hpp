@@ -2330,14 +2330,15 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
         alpha_rows<RM, KC>(g, meta, s_ar, nr, r0, w0, r1, w1, s_al);   // ends with a barrier
     }
     const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
-    const float scale = ctrl->scale;
-    const float mcoup = (float)h.metric_coupling;
+    // the force's sign (maximize) rides on the denominator: f / den = grad / (sign den)
     const float sg = h.maximize ? -1.f : 1.f;
+    const float scale_s = sg * ctrl->scale, eps_s = sg * eps;
+    const float kM = (float)h.metric_coupling * 1.4426950408889634f;   // exp(c x) = exp2((c log2 e) x)
     const float tm = (float)h.transport_mix;
     const float hs = (float)ctrl->hs_P;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
     const float k2 = -2.8853900817779268f * iclip;   // -2 log2(e) / clip
-    constexpr float invT = 1.0f / (float)TT;
+    constexpr float kT = 1.4426950408889634f / (float)TT;   // exp(mean over tables) = exp2(sum kT)
     f32x4m zacc[NQ][4];
 #pragma unroll
     for (int qt = 0; qt < NQ; ++qt)
@@ -2375,16 +2376,15 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
         float tvs[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float f = sg * x[r];
             // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
-            const float M = med3f(fexp(mcoup * med3f(lm[r], -3.0f, 3.0f)), 0.06f, 16.0f);
-            float den = scale * M;
+            const float M = med3f(fexp2(kM * med3f(lm[r], -3.0f, 3.0f)), 0.06f, 16.0f);
+            float den = scale_s * M;
             den = den * med3f(s_rf[16 * tr + 4 * lg + r] * ec, 0.08f, 12.0f);
             float lsum = s_lt[bin_byte<TT>(b[r], 0)];
 #pragma unroll
             for (int tt = 1; tt < TT; ++tt) lsum += s_lt[tt * B + bin_byte<TT>(b[r], tt)];
-            den = den * med3f(fexp(lsum * invT), 0.08f, 12.0f);
-            const float tv = med3f(f * frcp(den + eps), -1.0e4f, 1.0e4f);
+            den = den * med3f(fexp2(lsum * kT), 0.08f, 12.0f);
+            const float tv = med3f(x[r] * frcp(den + eps_s), -1.0e4f, 1.0e4f);
             bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
             tvs[r] = tv;
             const float err = tv - pred[r];
