@@ -230,6 +230,53 @@ __device__ __forceinline__ double wave_total_d(double v) {
     return v;
 }
 
+// Wave sum of a float in a fixed lane order with DPP (quad xor 1, 2; row
+// rotate 4, 8; row broadcasts 15, 31): the total lands in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                        0xF, false));
+}
+__device__ __forceinline__ float wave_total(float v) {
+    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x124, 0xF>(v);  // row_ror:4
+    v = dpp_add<0x128, 0xF>(v);  // row_ror:8
+    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
+    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
+    return v;                    // lane 63 holds the sum
+}
+
+// Sum V floats over the block; every thread receives the totals (fp64).  Each
+// wave sums a value in fp32 with DPP (full-rate adds; a wave holds 64 lanes'
+// partials, so fp32 loses nothing the lanes' own fp32 sums kept), threads
+// v < V add the wave totals in wave order in fp64 and publish the block total
+// once, and every thread reads the V published totals.
+//   lds: (blockDim.x / 64) * V doubles;  pub: V doubles, not inside lds.
+// Two barriers; the next call may reuse both areas at once.
+template <int V>
+__device__ __forceinline__ void block_sum_f(const float (&x)[V], double (&out)[V], double* lds, double* pub) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int nw = blockDim.x / kWave;
+    float w[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) w[i] = wave_total(x[i]);
+    if (lane == kWave - 1) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) lds[wave * V + i] = (double)w[i];
+    }
+    __syncthreads();
+    if (threadIdx.x < V) {
+        double s = 0.0;
+        for (int k = 0; k < nw; ++k) s += lds[k * V + threadIdx.x];
+        pub[threadIdx.x] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < V; ++i) out[i] = pub[i];
+}
+
 // Sum V values over the block; every thread receives the totals.
 // lds must hold (blockDim.x/64) * V doubles.  Two barriers.
 template <int V>

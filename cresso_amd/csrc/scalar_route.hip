@@ -275,6 +275,8 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
     const int G = R.group;                        // ROWGROUP: a power of two <= 64
     const int lgG = G > 0 ? __builtin_ctz(G) : 0;
     const float eps = (float)h.eps;
+    double* const pub = red + 16 * SR_SLOTS;                          // block totals (block_sum_f)
+    float* const s_dc = reinterpret_cast<float*>(pub + SR_SLOTS);     // drive coefficients, wave 0 -> all
     float* sp[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) sp[i] = reinterpret_cast<float*>(R.d.state[i]);
@@ -360,8 +362,9 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
     const int step = s_step;
     const double dn = (double)n;
     {
-        double v[1] = {(double)a_ff};
-        block_sum<1>(v, red);
+        const float x[1] = {a_ff};
+        double v[1];
+        block_sum_f<1>(x, v, red, pub);
         fr = reservoir(fr, sqrtf((float)(v[0] / dn) + eps), h.reservoir_decay, step);
     }
     const float scale = fmaxf(fr, eps);
@@ -423,10 +426,10 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
             const int row = (k * SR_NT + tid) >> lgG;
             if (ok && (tid & (G - 1)) == 0) rowfac[row] = rs;
         } else if (FAST) {
-            // the row of slot k is the whole block: its wave totals now (fp64,
-            // DPP), summed over the waves after the pass
-            const double w = wave_total_d((double)rs);
-            if (lane == 63) red[(tid >> 6) * SR_SLOTS + k] = w;
+            // the row of slot k is the whole block: its wave totals now (DPP),
+            // summed over the waves in fp64 after the pass
+            const float w = wave_total(rs);
+            if (lane == 63) red[(tid >> 6) * SR_SLOTS + k] = (double)w;
         } else {
             slotrow[k] = rs;
         }
@@ -440,8 +443,9 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
     }
     double gmean;
     {
-        double v[2] = {(double)a_L, (double)a_dens};
-        block_sum<2>(v, red);
+        const float x[2] = {a_L, a_dens};
+        double v[2];
+        block_sum_f<2>(x, v, red, pub);
         const float dens_mean = (float)((FAST ? v[0] * 0.6931471805599453 : v[0]) / dn);
         gmean = v[1] / dn;
         // scalar metric oscillator (cresso_v5.py:1510-1518)
@@ -473,11 +477,11 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
             double s = 0.0;
             for (int w = 0; w < SR_NT / 64; ++w) s += colred[w * C0 + tid];
             const float cm = (float)(s / (double)rows);
-            colfac[tid] = expf(kappa * logf(fmaxf(cm / gden, eps)));
+            colfac[tid] = fexp2(kappa * flog2(fmaxf(cm / gden, eps)));
         }
         for (int64_t i = tid; i < rows; i += SR_NT) {
             const float rm = rowfac[i] / (float)C0;
-            rowfac[i] = expf(kappa * logf(fmaxf(rm / gden, eps)));
+            rowfac[i] = fexp2(kappa * flog2(fmaxf(rm / gden, eps)));
         }
         __syncthreads();
         const int cg = tid & (G - 1);
@@ -486,19 +490,17 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
     } else {
         if (!FAST) {
             double v[SR_SLOTS];
-#pragma unroll
-            for (int k = 0; k < SR_SLOTS; ++k) v[k] = (double)slotrow[k];
-            block_sum<SR_SLOTS>(v, red);
+            block_sum_f<SR_SLOTS>(slotrow, v, red, pub);
             if (tid < SR_SLOTS) rowsum = v[tid];
         }
         if (tid < SR_SLOTS && tid < rows) {
             const float rm = (float)(rowsum / (double)C0);
-            rowfac[tid] = expf(kappa * logf(fmaxf(rm / gden, eps)));
+            rowfac[tid] = fexp2(kappa * flog2(fmaxf(rm / gden, eps)));
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const float cm = colacc[c] / (float)rows;
-            Ec[c] = expf(kappa * logf(fmaxf(cm / gden, eps)));
+            Ec[c] = fexp2(kappa * flog2(fmaxf(cm / gden, eps)));
         }
         __syncthreads();
     }
@@ -574,9 +576,7 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
         stx(k, xk);
     }
     double M[13];
-#pragma unroll
-    for (int i = 0; i < 13; ++i) M[i] = (double)m[i];
-    block_sum<13>(M, red);
+    block_sum_f<13>(m, M, red, pub);
     if (FAST) {
         // the FAST sums hold |tanh| where the moments need bnd = clip tanh
         const double dc_ = (double)clip;
@@ -585,7 +585,19 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
         M[9] *= dc_;
         M[11] *= dc_;
     }
-    const DriveCoef<float> dc = contact_and_coefs<float>(M, dn, h, step, q0, imp, act, sur);
+    // the scalar-state update and the coefficients: wave 0 computes them (the
+    // other waves would repeat the same uniform fp64 work), LDS hands them out
+    if (tid < kWave) {
+        const DriveCoef<float> c = contact_and_coefs<float>(M, dn, h, step, q0, imp, act, sur);
+        if (tid == 0) {
+            s_dc[0] = c.q1; s_dc[1] = c.cA; s_dc[2] = c.cB; s_dc[3] = c.cN; s_dc[4] = c.cD;
+            s_dc[5] = c.cr; s_dc[6] = c.cb; s_dc[7] = c.co; s_dc[8] = c.ct; s_dc[9] = c.nscale;
+        }
+    }
+    __syncthreads();
+    DriveCoef<float> dc;
+    dc.q1 = uni(s_dc[0]); dc.cA = uni(s_dc[1]); dc.cB = uni(s_dc[2]); dc.cN = uni(s_dc[3]); dc.cD = uni(s_dc[4]);
+    dc.cr = uni(s_dc[5]); dc.cb = uni(s_dc[6]); dc.co = uni(s_dc[7]); dc.ct = uni(s_dc[8]); dc.nscale = uni(s_dc[9]);
 
     // ---- pass D ----
     const float q1 = uni(dc.q1), cA = uni(dc.cA), cB = uni(dc.cB), cN = uni(dc.cN), cD = uni(dc.cD);
@@ -655,8 +667,9 @@ __device__ __forceinline__ void resident_body(const ScalarRec* __restrict__ recs
         stx(k, xk);
     }
     {
-        double v[1] = {(double)a_dd};
-        block_sum<1>(v, red);
+        const float x[1] = {a_dd};
+        double v[1];
+        block_sum_f<1>(x, v, red, pub);
         de = reservoir(de, (float)(v[0] / dn), h.reservoir_decay, step);
     }
     const float gain = uni(clampf((float)h.target_update_rms / sqrtf(de + eps), (float)h.min_gain, (float)h.max_gain));
@@ -729,7 +742,8 @@ __global__ __launch_bounds__(SR_NT) void scalar_resident_kernel(const ScalarRec*
                                                                  int32_t* __restrict__ steps,
                                                                  const void* const* __restrict__ grads, int32_t first,
                                                                  cresso_hyper h, Stagger sg) {
-    __shared__ double red[16 * SR_SLOTS];
+    // wave totals [16][<= SR_SLOTS] | published block totals [SR_SLOTS] | drive coefficients
+    __shared__ double red[16 * SR_SLOTS + SR_SLOTS + 8];
     __shared__ int s_step;
     if ((int32_t)blockIdx.x >= sg.lo && (int32_t)blockIdx.x < sg.hi) {
         const uint64_t t0 = wall_clock64();

@@ -703,23 +703,6 @@ __device__ __forceinline__ Tile tile_of(const Geom& g) {
     return t;
 }
 
-// Wave sum of a float in a fixed lane order with DPP (quad xor 1, 2; row
-// rotate 4, 8; row broadcasts 15, 31): the total lands in lane 63.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_add(float v) {
-    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
-                                                                        0xF, false));
-}
-__device__ __forceinline__ float wave_total(float v) {
-    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-    v = dpp_add<0x124, 0xF>(v);  // row_ror:4
-    v = dpp_add<0x128, 0xF>(v);  // row_ror:8
-    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
-    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
-    return v;                    // lane 63 holds the sum
-}
-
 // Block partials, one value at a time: DPP wave totals into LDS [wave][V],
 // then a fixed-order sum over the block's waves, written value-major
 // part[v][block] (consumers read each value's blocks contiguously).
