@@ -604,7 +604,7 @@ __global__ __launch_bounds__(256) void ws_project_kernel(Geom g, const ModeMeta*
         }
     }
     block_sum<2 * SP_MAXR>(acc, lds);
-    for (int v = threadIdx.x; v < 2 * g.R; v += blockDim.x) part[(size_t)v * gridDim.x + blockIdx.x] = acc[v];
+    for (int v = threadIdx.x; v < 2 * g.R; v += blockDim.x) part[(size_t)blockIdx.x * (2 * g.R) + v] = acc[v];
 }
 
 __global__ void ws_mean_kernel(const double* __restrict__ sums, int V, double inv_n, double* __restrict__ out) {
@@ -704,8 +704,11 @@ __device__ __forceinline__ Tile tile_of(const Geom& g) {
 }
 
 // Block partials, one value at a time: DPP wave totals into LDS [wave][V],
-// then a fixed-order sum over the block's waves, written value-major
-// part[v][block] (consumers read each value's blocks contiguously).
+// then a fixed-order sum over the block's waves, written block-major
+// part[block][VS]: a block's values are one contiguous row, written as whole
+// cache lines.  (Value-major rows, part[v][block], put 8 bytes of 16 blocks
+// spread over all XCDs in every line: the partial-line writebacks cost sweeps
+// 2 and 3 about 4 us each at C2.)
 struct Partials {
     float* lds;
     int V;
@@ -714,14 +717,15 @@ struct Partials {
         const float w = wave_total(x);
         if ((threadIdx.x & 63) == 63) lds[(threadIdx.x >> 6) * V + idx] = w;
     }
-    // value-major: part[v][gridDim.x], slots V..VS-1 zero
-    __device__ __forceinline__ void flush(double* part) {
+    // block-major: part[block][stride], slots V..VS-1 zero (stride >= VS, default VS)
+    __device__ __forceinline__ void flush(double* part, int stride = 0) {
         __syncthreads();
+        const size_t row = (size_t)blockIdx.x * (stride > 0 ? stride : VS);
         for (int v = threadIdx.x; v < VS; v += SP_NT) {
             double s = 0.0;
             if (v < V)
                 for (int w = 0; w < SP_NT / 64; ++w) s += (double)lds[w * V + v];
-            part[(size_t)v * gridDim.x + blockIdx.x] = s;
+            part[row + v] = s;
         }
     }
 };
@@ -731,44 +735,12 @@ __device__ __forceinline__ float reservoir_f(float old, float cur, double decay,
     return old * (float)decay + (float)(1.0 - decay) * cur;
 }
 
-// All partial values of a sweep (value-major part[v][nblk]) reduced in a
-// fixed order into out[v] (LDS), visible after return: thread j accumulates
-// blocks j, j + NT, ... of every value in fp64 (coalesced loads, all in
-// flight), each wave reduces every value with DPP in fixed lane order, and the
-// wave totals are added in wave order.
-template <int VMAX>
-__device__ void reduce_bm(const double* __restrict__ part, int nblk, int V, double* out) {
-    __shared__ double s_w[SP_FN_NT / 64][VMAX];
-    double acc[VMAX];
-#pragma unroll
-    for (int v = 0; v < VMAX; ++v) acc[v] = 0.0;
-    for (int b = threadIdx.x; b < nblk; b += SP_FN_NT) {
-#pragma unroll
-        for (int v = 0; v < VMAX; ++v)
-            if (v < V) acc[v] += part[(size_t)v * nblk + b];
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int v = 0; v < VMAX; ++v) {
-        if (v < V) {
-            const double w = wave_total_d(acc[v]);
-            if (lane == 63) s_w[wave][v] = w;
-        }
-    }
-    __syncthreads();
-    for (int v = threadIdx.x; v < V; v += SP_FN_NT) {
-        double s = 0.0;
-        for (int w = 0; w < SP_FN_NT / 64; ++w) s += s_w[w][v];
-        out[v] = s;
-    }
-    __syncthreads();
-}
-
 // Cross-block merge of a sweep's partials spread over many CUs: block v sums
-// value v of every block (thread j: blocks j, j + 256, ... in order; then a
-// fixed-order DPP wave tree and the four wave totals in order) into sums[v].
-// Blocks VS.. reduce the matrix-core sweeps' per-block histogram partials
-// (hpart[bin][block], 64-bit fixed point; integer sums) into hist[bin].
+// value v of every block's row part[block][VS] (thread j: blocks j, j + 256,
+// ... in order; then a fixed-order DPP wave tree and the four wave totals in
+// order) into sums[v].  Blocks VS.. reduce the matrix-core sweeps' per-block
+// histogram partials (hpart[block][bin], 64-bit fixed point: integer sums, in
+// any order the same) into hist[bin], one bin per block.
 __global__ __launch_bounds__(256) void part_reduce_kernel(
     const double* __restrict__ part, int nblk, int VS, double* __restrict__ sums,
     const unsigned long long* __restrict__ hpart, unsigned long long* __restrict__ hist, Lanes L) {
@@ -779,7 +751,8 @@ __global__ __launch_bounds__(256) void part_reduce_kernel(
     if (v >= VS) {
         const int i = v - VS;
         unsigned long long a = 0ull;
-        for (int b = threadIdx.x; b < nblk; b += 256) a += hpart[(size_t)i * nblk + b];
+        const int TB = (int)gridDim.x - VS;
+        for (int b = threadIdx.x; b < nblk; b += 256) a += hpart[(size_t)b * TB + i];
         for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
         if ((threadIdx.x & 63) == 0) s_h[threadIdx.x >> 6] = a;
         __syncthreads();
@@ -787,7 +760,7 @@ __global__ __launch_bounds__(256) void part_reduce_kernel(
         return;
     }
     double a = 0.0;
-    for (int b = threadIdx.x; b < nblk; b += 256) a += part[(size_t)v * nblk + b];
+    for (int b = threadIdx.x; b < nblk; b += 256) a += part[(size_t)b * VS + v];
     a = wave_total_d(a);
     if ((threadIdx.x & 63) == 63) s_w[threadIdx.x >> 6] = a;
     __syncthreads();
@@ -887,8 +860,8 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(
     }
     Partials P{red, 1, 1};
     P.add(0, a);
-    P.flush(part);
-    // block max |f| after the block's sums (part[nblk1 + block]): max is order independent
+    P.flush(part, 2);
+    // block max |f| after the block's sum (part[block][1]): max is order independent
     __shared__ float smax[SP_NT / 64];
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = m;
@@ -896,7 +869,7 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(
     if (threadIdx.x == 0) {
         float mm = smax[0];
         for (int i = 1; i < SP_NT / 64; ++i) mm = fmaxf(mm, smax[i]);
-        part[(size_t)g.nblk1 + blockIdx.x] = (double)mm;
+        part[(size_t)blockIdx.x * 2 + 1] = (double)mm;
     }
 }
 
@@ -908,7 +881,7 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(
 // kernels read from ctrl; the reservoir starts from ctrl->fr_prev (stashed by
 // sweep 1), so no block reads a value another block of this launch writes.
 // The density histogram's fixed-point scale comes from sweep 1's block maxima
-// of |f| (after its sums, part1[nblk1 + block]).
+// of |f| (each block's row of part1 holds its sum, then its maximum).
 struct F1Values {
     float inv_s;
     double hs_ds;
@@ -918,8 +891,8 @@ __device__ F1Values fin1_values(const Geom& g, const double* __restrict__ part1,
     __shared__ double s_w[SP_NT / 64], s_m[SP_NT / 64];
     double a = 0.0, mx = 0.0;
     for (int b = threadIdx.x; b < g.nblk1; b += SP_NT) {
-        a += part1[b];
-        mx = fmax(mx, part1[(size_t)g.nblk1 + b]);
+        a += part1[(size_t)b * 2];
+        mx = fmax(mx, part1[(size_t)b * 2 + 1]);
     }
     const double w = wave_total_d(a);
     for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
@@ -1519,6 +1492,91 @@ template <int TT> __device__ __forceinline__ uint32_t bin_byte(uint32_t b, int t
 }
 // projection rows of rank RM in 16-row tiles; carriers in chunks of 4
 template <int RM> constexpr int nqt() { return (2 * RM + 15) / 16; }
+
+// Inputs of a matrix-core sweep's projection finish: lane group lg's modes
+// r = 8 qt + 2 lg + h (h = 0, 1) and their column carriers b1, b2 at the
+// lane's 4 columns.  Fetched in the prologue, so that the finish after the
+// last tile is not a dependent global round trip (mode table, then carriers).
+template <int NQ>
+struct ProjCols {
+    int on[NQ][2], add[NQ][2], k1[NQ][2], k2[NQ][2];
+    float b1[NQ][2][4], b2[NQ][2][4];
+    // modes, first thing in the kernel
+    __device__ __forceinline__ void modes(const Geom& g, const ModeMeta* __restrict__ meta, int lg, int KC) {
+#pragma unroll
+        for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int r = 8 * qt + 2 * lg + hh;
+                const ModeMeta m = meta[r < g.R ? r : 0];
+                on[qt][hh] = r < g.R;
+                add[qt][hh] = m.type == M_ADD;
+                // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
+                k1[qt][hh] = (m.k1 >= 0 && m.k1 < KC) ? m.k1 : -1;
+                k2[qt][hh] = (m.k2 >= 0 && m.k2 < KC) ? m.k2 : -1;
+            }
+    }
+    // carriers of the lane's columns colw + 16 tc + li from the column table
+    __device__ __forceinline__ void load(const Geom& g, const float* __restrict__ coltab, int64_t colw, int li) {
+#pragma unroll
+        for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int tc = 0; tc < 4; ++tc) {
+                    const int64_t c = colw + 16 * tc + li;
+                    b1[qt][hh][tc] = k1[qt][hh] >= 0 ? coltab[(size_t)k1[qt][hh] * g.cols + c] : 0.f;
+                    b2[qt][hh][tc] = k2[qt][hh] >= 0 ? coltab[(size_t)k2[qt][hh] * g.cols + c] : 0.f;
+                }
+    }
+    // the same carriers from an LDS copy of the block's column table rows (row stride ls)
+    __device__ __forceinline__ void load_lds(const float* __restrict__ s_col, int ls, int wcol, int li) {
+#pragma unroll
+        for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int tc = 0; tc < 4; ++tc) {
+                    const int c = wcol + 16 * tc + li;
+                    b1[qt][hh][tc] = k1[qt][hh] >= 0 ? s_col[k1[qt][hh] * ls + c] : 0.f;
+                    b2[qt][hh][tc] = k2[qt][hh] >= 0 ? s_col[k2[qt][hh] * ls + c] : 0.f;
+                }
+    }
+    // in q-tile qt, lane group lg holds Z_{16 qt + 4 lg + j}(col), j < 4: both
+    // components of its two modes for its 4 columns (proj_finish's form); each
+    // mode's raw C/S is summed over the columns, then over the 16 lanes of the
+    // group, into LDS slots base + 16 qt + 4 lg + j of wave wv's row of red
+    __device__ __forceinline__ void finish(const Geom& g, const f32x4m (&zacc)[NQ][4], float* red, int rowV, int base,
+                                           int wv, int lg, int li) const {
+#pragma unroll
+        for (int qt = 0; qt < NQ; ++qt) {
+            float cs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                if (on[qt][hh]) {
+#pragma unroll
+                    for (int tc = 0; tc < 4; ++tc) {
+                        const float z1 = zacc[qt][tc][2 * hh], z2 = zacc[qt][tc][2 * hh + 1];
+                        const float c1 = b1[qt][hh][tc], c2 = b2[qt][hh][tc];
+                        if (add[qt][hh]) {
+                            cs[2 * hh] += c1 * z1 - c2 * z2;
+                            cs[2 * hh + 1] += c1 * z2 + c2 * z1;
+                        } else {
+                            cs[2 * hh] += c1 * z1;
+                            cs[2 * hh + 1] += c2 * z2;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float sm = row16_total(cs[j]);
+                const int slot = 16 * qt + 4 * lg + j;
+                if (li == 15 && slot < 2 * g.R) red[wv * rowV + base + slot] = sm;
+            }
+        }
+    }
+};
 template <int KC> constexpr int kch() { return (KC + 3) / 4; }
 
 // ---------------------------------------------------------------------------
@@ -1555,6 +1613,8 @@ __global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
     const int nr = g.PR;
     const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int li = l & 15, lg = l >> 4;
+    ProjCols<NQ> pc;
+    pc.modes(g, meta, lg, KC);
     const int64_t base = panel_base(g, t);
     const uint32_t cols = (uint32_t)g.cols;
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(grad + base, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(GT)));
@@ -1590,6 +1650,8 @@ __global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
     const float pw = (float)h.energy_power;
     const float sg = h.maximize ? -1.f : 1.f;
     const float hs = (float)f1.hs_ds;
+    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
+    pc.load(g, coltab, colw, li);
     // the lane's projection A operands, a_{16 qt + li}(row 16 tr + 4 lg + r),
     // held in registers: read from LDS inside the loop they would queue
     // behind the histogram atomics (LDS operations complete in order)
@@ -1663,7 +1725,6 @@ __global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
         atomicAdd(&rowfx[t.r0 + lr], to_fixed_u(sr * (float)g.hs_row));
     }
     float aD = 0.f;
-    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc) {
         // the column's 4 lane groups, in a fixed order
@@ -1677,47 +1738,12 @@ __global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
         unsigned long long v = 0ull;
 #pragma unroll
         for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-        hist[(size_t)i * gridDim.x + blockIdx.x] = v;   // this block's partial (hpart[bin][block])
+        hist[(size_t)blockIdx.x * TB + i] = v;   // this block's partial (hpart[block][bin])
     }
     Partials P{red, 2 + 2 * g.R, NV2};
     P.add(0, aL);
     P.add(1, aD);
-    // projection: in q-tile qt, lane group lg holds Z_{16 qt + 4 lg + j}(col),
-    // both components of modes 8 qt + 2 lg and 8 qt + 2 lg + 1, for its 4
-    // columns (proj_finish's form), summed over the columns and the group's
-    // 16 lanes into slots 2 + 16 qt + 4 lg + j
-#pragma unroll
-    for (int qt = 0; qt < NQ; ++qt) {
-        float cs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int r = 8 * qt + 2 * lg + half;
-            if (r < g.R) {
-                const ModeMeta m = meta[r];
-#pragma unroll
-                for (int tc = 0; tc < 4; ++tc) {
-                    const int64_t c = colw + 16 * tc + li;
-                    // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
-                    const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
-                    const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
-                    const float z1 = zacc[qt][tc][2 * half], z2 = zacc[qt][tc][2 * half + 1];
-                    if (m.type == M_ADD) {
-                        cs[2 * half] += b1 * z1 - b2 * z2;
-                        cs[2 * half + 1] += b1 * z2 + b2 * z1;
-                    } else {
-                        cs[2 * half] += b1 * z1;
-                        cs[2 * half + 1] += b2 * z2;
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float sm = row16_total(cs[j]);
-            const int slot = 16 * qt + 4 * lg + j;
-            if (li == 15 && slot < 2 * g.R) red[wv * P.V + 2 + slot] = sm;
-        }
-    }
+    pc.finish(g, zacc, red, P.V, 2, wv, lg, li);
     P.flush(part);
 }
 
@@ -2238,6 +2264,8 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
     const int nr = g.PR;
     const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int li = l & 15, lg = l >> 4;
+    ProjCols<NQ> pc;
+    pc.modes(g, meta, lg, KC);
     const int64_t base = panel_base(g, t);
     const uint32_t cols = (uint32_t)g.cols;
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(grad + base, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(GT)));
@@ -2312,6 +2340,9 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
         const float w0[2] = {1.f, 1.f}, w1[2] = {0.f, 0.f};
         alpha_rows<RM, KC>(g, meta, s_ar, nr, r0, w0, r1, w1, s_al);   // ends with a barrier
     }
+    // the projection finish's carriers: from the LDS table after the last
+    // tile, or (carriers held in registers) loaded now
+    if constexpr (BQR) pc.load(g, coltab, colw, li);
     const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
     // the force's sign (maximize) rides on the denominator: f / den = grad / (sign den)
     const float sg = h.maximize ? -1.f : 1.f;
@@ -2424,7 +2455,7 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
         unsigned long long v = 0ull;
 #pragma unroll
         for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-        hist[(size_t)i * gridDim.x + blockIdx.x] = v;   // this block's partial (hpart[bin][block])
+        hist[(size_t)blockIdx.x * TB + i] = v;   // this block's partial (hpart[block][bin])
     }
     Partials P{red, 15 + 2 * g.R, NV3};
     const float mm[13] = {m_ee, 0.f, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
@@ -2432,43 +2463,8 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
     for (int k = 0; k < 13; ++k) P.add(k, mm[k]);
     P.add(13, 0.f);
     P.add(14, 0.f);
-    // projection: in q-tile qt, lane group lg holds Z_{16 qt + 4 lg + j}(col),
-    // j < 4, i.e. both components of modes 8 qt + 2 lg and 8 qt + 2 lg + 1,
-    // for its 4 columns; each mode's raw C/S (proj_finish's form) is summed
-    // over the columns, then over the 16 lanes of the group, into slots
-    // 15 + 16 qt + 4 lg + j.
-#pragma unroll
-    for (int qt = 0; qt < NQ; ++qt) {
-        float cs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int r = 8 * qt + 2 * lg + half;
-            if (r < g.R) {
-                const ModeMeta m = meta[r];
-#pragma unroll
-                for (int tc = 0; tc < 4; ++tc) {
-                    const int64_t c = colw + 16 * tc + li;
-                    // carrier index outside [0, KC) (k2 = -1: identically zero) reads as 0
-                    const float b1 = (m.k1 >= 0 && m.k1 < KC) ? coltab[(size_t)m.k1 * g.cols + c] : 0.f;
-                    const float b2 = (m.k2 >= 0 && m.k2 < KC) ? coltab[(size_t)m.k2 * g.cols + c] : 0.f;
-                    const float z1 = zacc[qt][tc][2 * half], z2 = zacc[qt][tc][2 * half + 1];
-                    if (m.type == M_ADD) {
-                        cs[2 * half] += b1 * z1 - b2 * z2;
-                        cs[2 * half + 1] += b1 * z2 + b2 * z1;
-                    } else {
-                        cs[2 * half] += b1 * z1;
-                        cs[2 * half + 1] += b2 * z2;
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float sm = row16_total(cs[j]);
-            const int slot = 16 * qt + 4 * lg + j;
-            if (li == 15 && slot < 2 * g.R) red[wv * P.V + 15 + slot] = sm;
-        }
-    }
+    if constexpr (!BQR) pc.load_lds(s_bq, SP_BQS, 64 * wv, li);
+    pc.finish(g, zacc, red, P.V, 15, wv, lg, li);
     P.flush(part);
 }
 
@@ -3064,7 +3060,7 @@ __device__ void fin4_values(const Geom& g, const double* __restrict__ part, cons
     double acc[NV4] = {0.0, 0.0, 0.0};
     for (int b = threadIdx.x; b < g.nblk; b += SP_NT)
 #pragma unroll
-        for (int v = 0; v < NV4; ++v) acc[v] += part[(size_t)v * g.nblk + b];
+        for (int v = 0; v < NV4; ++v) acc[v] += part[(size_t)b * NV4 + v];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int v = 0; v < NV4; ++v) {
