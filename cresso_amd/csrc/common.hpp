@@ -185,6 +185,28 @@ __device__ __forceinline__ Shape3A shape3a(float at, float k2, float iclip, floa
     return s;
 }
 
+// shape3a of at together with the unsigned novelty tanh(|e| k) (k2n = -2 k
+// log2 e), the two quotients from one reciprocal:
+// 1/(d1 d2) = dn rr, 1/dn = d1 d2 rr with rr = 1/(d1 d2 dn).  Returns tanh(e k).
+__device__ __forceinline__ float shape3a_nov(float at, float e, float k2, float k2n, float iclip, float clip2,
+                                             float eps, Shape3A& s) {
+    const float es = fexp2(k2 * at);
+    const float d1 = 1.0f + es;
+    const float d2 = fmaf(at, iclip, 1.0f);
+    const float ex = fexp2(k2n * fabsf(e));
+    const float dn = 1.0f + ex;
+    const float d12 = d1 * d2;
+    const float rr = frcp(d12 * dn);
+    const float inv = dn * rr;   // 1/(d1 d2)
+    const float ri = d12 * rr;   // 1/dn
+    const float u = d2 * inv;    // 1/d1
+    s.th = fmaf(-es, u, u);
+    s.rat = at * (d1 * inv);
+    const float r = fsqrt(fminf(at, clip2) + eps);
+    s.root = at > 0.0f ? r : 0.0f;
+    return copysignf(fmaf(-ex, ri, ri), e);
+}
+
 // double versions for the f64 work dtype (accurate libm)
 __device__ __forceinline__ double fexp(double x) { return exp(x); }
 __device__ __forceinline__ double flog(double x) { return log(x); }

@@ -1021,17 +1021,19 @@ __device__ void alpha_rows(const Geom& g, const ModeMeta* __restrict__ meta, con
         s_cm[j][k][q] = v;
     }
     __syncthreads();   // Cm and the caller's staged rows are complete
-    for (int p = threadIdx.x; p < 2 * nr; p += blockDim.x) {
-        const int lr = p >> 1, j = p & 1;
+    // (row, set, half of the carriers) per thread: 4 nr items, all threads busy
+    constexpr int KH = KP / 2;
+    for (int p = threadIdx.x; p < 4 * nr; p += blockDim.x) {
+        const int lr = p >> 2, j = (p >> 1) & 1, k0 = (p & 1) * KH;
         float row[RW];
 #pragma unroll
         for (int q = 0; q < RW; ++q) row[q] = s_rows[lr * RW + q];
-        float* __restrict__ out = s_al + lr * (2 * KP) + j * KP;
+        float* __restrict__ out = s_al + lr * (2 * KP) + j * KP + k0;
 #pragma unroll
-        for (int k = 0; k < KP; ++k) {
+        for (int k = 0; k < KH; ++k) {
             float a = 0.f;
 #pragma unroll
-            for (int q = 0; q < RW; ++q) a = fmaf(s_cm[j][k][q], row[q], a);
+            for (int q = 0; q < RW; ++q) a = fmaf(s_cm[j][k0 + k][q], row[q], a);
             out[k] = a;
         }
     }
@@ -1082,11 +1084,11 @@ __device__ __forceinline__ void proj_finish(const Geom& g, const ModeMeta* __res
 }
 
 // Instant-metric factor of an axis marginal (cresso_v5.py:243-262):
-// exp(kappa * log(max(mean/gden, eps))), mean from a fixed-point sum.
-__device__ __forceinline__ float marg_factor(unsigned long long fx, double hs, double count, float gden, float kappa,
-                                             float eps) {
-    const float mean = (float)((double)fx / hs / count);
-    return expf(kappa * logf(fmaxf(mean / gden, eps)));
+// exp(kappa * log(max(mean/gden, eps))), mean from a fixed-point sum;
+// inv_hc = 1 / (hs * count), hs the sum's power-of-two scale.
+__device__ __forceinline__ float marg_factor(unsigned long long fx, double inv_hc, float gden, float kappa, float eps) {
+    const float mean = (float)((double)fx * inv_hc);
+    return fexp2(kappa * flog2(fmaxf(mean / gden, eps)));
 }
 
 constexpr int SP_U = 8;  // rows whose loads are in flight together
@@ -2049,7 +2051,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
             for (int c = 0; c < NH; ++c) s_hist[i * NH + c] = 0ull;
         }
     for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
-        s_rf[lr] = (inst_on && !g.one_d) ? marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps) : 1.0f;
+        s_rf[lr] = (inst_on && !g.one_d) ? marg_factor(rowfx[t.r0 + lr], 1.0 / (g.hs_row * (double)g.cols), gden, kappa, eps) : 1.0f;
     // the lane's column carriers and the rows' coefficients of the metric
     // field (set 0) and the prediction (set 1)
     constexpr int KP = kcp<KC>();
@@ -2077,7 +2079,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
     const float ipw = (float)fmax(h.instant_metric_power, 0.25);
     float ec = 1.0f;
     if (inst_on && !g.one_d && t.colok)
-        ec = g.ntrail == 1 ? marg_factor(colfx[t.col], g.hs_col, (double)g.rows, gden, kappa, eps) : colfac[t.col];
+        ec = g.ntrail == 1 ? marg_factor(colfx[t.col], 1.0 / (g.hs_col * (double)g.rows), gden, kappa, eps) : colfac[t.col];
     const float invT = 1.0f / (float)F.T;
     const float tm = (float)h.transport_mix;
     const float hs = (float)ctrl->hs_P;
@@ -2301,12 +2303,12 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
     const float eps = (float)h.eps;
     const float kappa = ctrl->kappa, gden = ctrl->gden;
     for (int i = threadIdx.x; i < TB; i += SP_NT) {
-        s_lt[i] = lt[i];
+        s_lt[i] = fexp2(lt[i] * (1.4426950408889634f / (float)TT));   // exp(lt / T)
 #pragma unroll
         for (int c = 0; c < NH; ++c) s_hist[i * NH + c] = 0ull;
     }
     for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
-        s_rf[lr] = marg_factor(rowfx[t.r0 + lr], g.hs_row, (double)g.cols, gden, kappa, eps);
+        s_rf[lr] = marg_factor(rowfx[t.r0 + lr], 1.0 / (g.hs_row * (double)g.cols), gden, kappa, eps);
     stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
     // the block's column instant-metric factors in LDS [SP_NT], after the
     // column carriers (B operands of the reconstructions) when those are in
@@ -2330,7 +2332,7 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
 #pragma unroll
             for (int k = 0; k < KP; ++k) s_bq[k * SP_BQS + threadIdx.x] = k < KC ? coltab[(size_t)k * g.cols + c] : 0.f;
         }
-        s_ec[threadIdx.x] = g.ntrail == 1 ? marg_factor(colfx[c], g.hs_col, (double)g.rows, gden, kappa, eps) : colfac[c];
+        s_ec[threadIdx.x] = g.ntrail == 1 ? marg_factor(colfx[c], 1.0 / (g.hs_col * (double)g.rows), gden, kappa, eps) : colfac[c];
     }
     const float* __restrict__ bql = s_bq + lg * SP_BQS + 64 * wv + li;   // + 4 kc SP_BQS + 16 tc
     const float* __restrict__ ecl = s_ec + 64 * wv + li;                  // + 16 tc
@@ -2352,7 +2354,6 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
     const float hs = (float)ctrl->hs_P;
     const float clip = (float)h.drive_clip, iclip = 1.0f / clip, clip2 = clip * clip;
     const float k2 = -2.8853900817779268f * iclip;   // -2 log2(e) / clip
-    constexpr float kT = 1.4426950408889634f / (float)TT;   // exp(mean over tables) = exp2(sum kT)
     f32x4m zacc[NQ][4];
 #pragma unroll
     for (int qt = 0; qt < NQ; ++qt)
@@ -2394,10 +2395,11 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
             const float M = med3f(fexp2(kM * med3f(lm[r], -3.0f, 3.0f)), 0.06f, 16.0f);
             float den = scale_s * M;
             den = den * med3f(s_rf[16 * tr + 4 * lg + r] * ec, 0.08f, 12.0f);
-            float lsum = s_lt[bin_byte<TT>(b[r], 0)];
+            // hash metric exp(mean over tables of lt) as the product of the tables' exp(lt / T)
+            float hm = s_lt[bin_byte<TT>(b[r], 0)];
 #pragma unroll
-            for (int tt = 1; tt < TT; ++tt) lsum += s_lt[tt * B + bin_byte<TT>(b[r], tt)];
-            den = den * med3f(fexp2(lsum * kT), 0.08f, 12.0f);
+            for (int tt = 1; tt < TT; ++tt) hm *= s_lt[tt * B + bin_byte<TT>(b[r], tt)];
+            den = den * med3f(hm, 0.08f, 12.0f);
             const float tv = med3f(x[r] * frcp(den + eps_s), -1.0e4f, 1.0e4f);
             bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
             tvs[r] = tv;
@@ -2992,9 +2994,9 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
         for (int r = 0; r < 4; ++r) {
             const float tv = x[r];
             const float err = tv - pred[r];
-            const float nov = ftanh_k(err, k2n);
             const float at = fabsf(tv);
-            const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+            Shape3A z;
+            const float nov = shape3a_nov(at, err, k2, k2n, iclip, clip2, eps, z);
             const float core = xorsign(fmaf(k_t, at, fmaf(k_root, z.root, fmaf(k_ths, z.th, k_rat * z.rat))), tv);
             float hp = s_imp[bin_byte<TT>(b[r], 0)];
 #pragma unroll
