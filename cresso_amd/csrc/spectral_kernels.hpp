@@ -105,6 +105,8 @@ struct Geom {
     int32_t RW;                        // row-table width: 2*rmax (zero beyond 2R)
     int64_t chunk1;                    // elements per block of the flat sweep (multiple of 4)
     double hs_row, hs_col;             // fixed-point scales of the axis density sums
+    double shrink;                     // 1/sqrt(max(1, 0.7 log2(R + 1))) (cresso_v5.py:362-376)
+    double inv_n;                      // 1/n
     int32_t binbytes, bpb, one_d, nblkg;   // nblkg: blocks of the Gram pair-sum kernel
 };
 
@@ -1762,7 +1764,7 @@ __global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
 __device__ void set_recon_lanes(const Geom& g, const double* __restrict__ stats, float (*rc)[2], float* rconst,
                                 float cc, float sc, float gate, float* s_tmp, float* weights = nullptr) {
     const int r = threadIdx.x & 63;
-    const double shrink = 1.0 / sqrt(fmax(1.0, 0.7 * log2((double)g.R + 1.0)));
+    const double shrink = g.shrink;
     float kc = 0.f, ks = 0.f, wc = 0.f, ws = 0.f, cterm = 0.f;
     if (r < g.R) {
         if (gate != 0.0f) {
@@ -1803,6 +1805,18 @@ __device__ double lanes_sum(double v, int R) {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Barrier of waves 1.. of a finalize block while wave 0 runs the mode lanes:
+// each arriving wave publishes its earlier stores (workgroup-scope release),
+// counts itself in an LDS counter and waits until the counter reaches
+// `target`.  Every wave 1.. calls each such barrier, so every wait ends;
+// targets are cumulative (k-th barrier: k times the number of waves 1..).
+__device__ __forceinline__ void waves_sync(unsigned int* cnt, unsigned int target) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
 // ---------------------------------------------------------------------------
 // F2: hash metric, metric oscillator, recon coefficients
 // ---------------------------------------------------------------------------
@@ -1817,12 +1831,13 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
     }
     part = lane_at(part, L); hist = lane_at(hist, L); lt = lane_at(lt, L); ctrl = lane_at(ctrl, L);
     __shared__ double s_v[NV2];
-    __shared__ double red[SP_FN_NT / 64];
+    __shared__ double s_wsum[SP_MAXT][SP_FN_NT / 64];
     __shared__ float s_emean[SP_MAXT];
     __shared__ float s_tmpf[64];
+    __shared__ unsigned int s_sync;
     const int tid = threadIdx.x;
+    if (tid == 0) s_sync = 0u;   // published by load_sums' barrier
     const float eps = (float)h.eps;
-    const double n = (double)g.n;
     __shared__ double s_stats[4 * SP_MAXR], s_bounds[2 * SP_MAXR];
     __shared__ float s_mode[SP_MAXR][9];
     __shared__ int s_zero[SP_MAXR];
@@ -1839,10 +1854,12 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
     // sweep 2 sums log(1 + ds) in log2 units
     if (tid < 2 + 2 * g.R && tid != 1) s_v[tid] *= 0.6931471805599453;
     __syncthreads();
-    // hash energy per table (cresso_v5.py:1012-1056)
-    if (hash_on) {
-        const int TB = g.T * g.B;
-        for (int i = tid; i < TB; i += SP_FN_NT) {
+    // hash energy per table (cresso_v5.py:1012-1056), on waves 1.. while wave 0
+    // runs the mode lanes (which read none of it)
+    if (hash_on && tid >= 64) {
+        const int TB = g.T * g.B, t1 = tid - 64, n1 = SP_FN_NT - 64;
+        constexpr unsigned nw1 = SP_FN_NT / 64 - 1;
+        for (int i = t1; i < TB; i += n1) {
             const double cnt = (double)counts[i];
             const float cell = (float)((double)(long long)hist[i] / ctrl->hs_ds / fmax(cnt, 1.0));
             hist[i] = 0ull;
@@ -1850,16 +1867,23 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
             e = step <= 1 ? cell : e * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * cell;
             st.hash_energy[i] = e;
         }
-        __syncthreads();
+        waves_sync(&s_sync, nw1);
+        // each table's mean: the waves' fp64 totals added in wave order
         for (int tt = 0; tt < g.T; ++tt) {
-            double s[1] = {0.0};
-            for (int b = tid; b < g.B; b += SP_FN_NT) s[0] += (double)st.hash_energy[tt * g.B + b];
-            block_sum<1>(s, red);
-            if (tid == 0) s_emean[tt] = (float)(s[0] / (double)g.B);
+            double a = 0.0;
+            for (int b = t1; b < g.B; b += n1) a += (double)st.hash_energy[tt * g.B + b];
+            const double w = wave_total_d(a);
+            if ((tid & 63) == 63) s_wsum[tt][(tid >> 6) - 1] = w;
         }
-        __syncthreads();
+        waves_sync(&s_sync, 2 * nw1);
+        if (t1 < g.T) {
+            double a = 0.0;
+            for (int w = 0; w < (int)nw1; ++w) a += s_wsum[t1][w];
+            s_emean[t1] = (float)(a / (double)g.B);
+        }
+        waves_sync(&s_sync, 3 * nw1);
         const float ex = (float)(h.hash_metric_coupling / fmax(0.25, h.energy_power));
-        for (int i = tid; i < TB; i += SP_FN_NT) {
+        for (int i = t1; i < TB; i += n1) {
             const int tt = i / g.B;
             const float hm = fmaxf(st.hash_energy[i] / fmaxf(s_emean[tt], eps), eps);
             lt[i] = logf(fmaxf(clampf(powf(hm, ex), 0.08f, 12.0f), eps));
@@ -1871,12 +1895,12 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
         const bool on = r < g.R;
         const double sumL = s_v[0], sumD = s_v[1];
         // log-density projections: d = L/max(mean L, eps) - 1, mean(d Cn) = mean(L Cn)/m - mean(Cn)
-        const double m = fmax((double)(float)(sumL / n), (double)eps);
+        const double m = fmax((double)(float)(sumL * g.inv_n), (double)eps);
         float pcos = 0.f, psin = 0.f;
         if (on) {
-            const double prc = (s_v[2 + 2 * r] - s_stats[4 * r] * sumL) * s_stats[4 * r + 1] / n / m -
+            const double prc = (s_v[2 + 2 * r] - s_stats[4 * r] * sumL) * s_stats[4 * r + 1] * g.inv_n / m -
                                (s_zero[r] ? 1.0 : 0.0);   // mean(Cn) = 1 for the constant mode
-            const double prs = (s_v[3 + 2 * r] - s_stats[4 * r + 2] * sumL) * s_stats[4 * r + 3] / n / m;
+            const double prs = (s_v[3 + 2 * r] - s_stats[4 * r + 2] * sumL) * s_stats[4 * r + 3] * g.inv_n / m;
             pcos = (float)prc;
             psin = (float)prs;
         }
@@ -1907,7 +1931,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
         // prediction with the pre-contact state and gates
         float qc = 0.f, qs = 0.f, gt = 0.f;
         double pm = 0.0;
-        const double shrink = 1.0 / sqrt(fmax(1.0, 0.7 * log2((double)g.R + 1.0)));
+        const double shrink = g.shrink;
         if (on) {
             qc = s_mode[r][5];
             qs = s_mode[r][6];
@@ -1918,7 +1942,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
         const double pmax = lanes_sum(pm, g.R);
         if (r == 0) {
             // instant metric: mean density and coupling (cresso_v5.py:243-262)
-            ctrl->gden = (float)fmax(sumD / n, (double)eps);
+            ctrl->gden = (float)fmax(sumD * g.inv_n, (double)eps);
             const float icoup = hard ? (float)h.instant_metric_coupling : 0.0f;
             ctrl->kappa = (float)((double)icoup / ((double)g.ndim * fmax(h.instant_metric_power, 0.25)));
             // fixed-point scale of the port histogram: |P| <= (1+tm)*1e4 + max|pred|, <= cmax elements per bin
@@ -2499,8 +2523,9 @@ __device__ void contact_bank_lanes(float& q, float& p, float port, float omega, 
     }
     const double E1 = lanes_sum(e1, R), E2 = lanes_sum(e2, R), PW = lanes_sum(pw, R);
     if (R > 0) {
-        const float energy = 0.5f * ((float)(E1 / R) + (float)(E2 / R));
-        const float power = (float)(PW / R);
+        const double iR = 1.0 / (double)R;
+        const float energy = 0.5f * ((float)(E1 * iR) + (float)(E2 * iR));
+        const float power = (float)(PW * iR);
         action = action * 0.985f + dt * (power - energy);
     }
     const float fric = (float)h.impulse_friction + (float)h.contact_gain * tanhf(fabsf(action));
@@ -2545,7 +2570,6 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
     __shared__ float s_wp[2 * SP_MAXR], s_we[2 * SP_MAXR];
     __shared__ float s_tmpf[64];
     const int tid = threadIdx.x;
-    const double n = (double)g.n;
     const int R = g.R, V = 2 * g.R;
     // everything the mode lanes read, staged in LDS by all threads (global
     // loads in flight together instead of one round trip per use)
@@ -2556,6 +2580,8 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
     __shared__ float s_impv[2 * 256];
     __shared__ double s_hhw[SP_FN_NT / 64];
     __shared__ float s_srms;
+    __shared__ unsigned int s_sync;
+    if (tid == 0) s_sync = 0u;   // published by load_sums' barrier
     for (int i = tid; i < V * V; i += SP_FN_NT) s_gram[i] = gram[i];
     for (int i = tid; i < 4 * R; i += SP_FN_NT) s_stats[i] = stats[i];
     for (int i = tid; i < 9 * R; i += SP_FN_NT) {
@@ -2570,36 +2596,19 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
     }
     load_sums(part, 15 + 2 * R, s_m);
     const float eps = (float)h.eps;
-    // hash refractory / impulse (cresso_v5.py:1140-1184)
-    if (hash_on) {
-        const int TB = g.T * g.B;
-        for (int i = tid; i < TB; i += SP_FN_NT) {
-            const double cnt = fmax((double)counts[i], 1.0);
-            const float cp = (float)((double)(long long)hist[i] / ctrl->hs_P / cnt);
-            hist[i] = 0ull;
-            const float ref = st.hash_refractory[i] * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * fabsf(cp);
-            const float gate = 1.0f / (1.0f + (float)h.refractory_gain * ref);
-            const float im = st.hash_impulse[i] * (float)h.hash_impulse_decay + (float)(1.0 - h.hash_impulse_decay) * (cp * gate);
-            st.hash_refractory[i] = ref;
-            st.hash_impulse[i] = im;
-            imp_tab[i] = im;
-            if (c5_closed) s_impv[i] = im;
-        }
-    }
-    if (c5_closed) __syncthreads();   // s_impv complete
     __shared__ double s_gu[2 * SP_MAXR];     // G u_pred: mean(pred Xn_v)
     if (tid < 64) {
         const int r = tid;
         const bool on = r < R;
         const double sT = s_m[2];
         // surprise reservoir (cresso_v5.py:1127-1129)
-        const float sur = reservoir_f(s_scal[0], sqrtf((float)(s_m[0] / n) + eps), h.surprise_decay, step);
+        const float sur = reservoir_f(s_scal[0], sqrtf((float)(s_m[0] * g.inv_n) + eps), h.surprise_decay, step);
         // t projections mean(t Xn) in fp64
         float ecs = 0.f, ess = 0.f;
         if (on) {
             const double mc = s_stats[4 * r], ic = s_stats[4 * r + 1], ms = s_stats[4 * r + 2], is = s_stats[4 * r + 3];
-            const double ecd = (s_m[15 + 2 * r] - mc * sT) * ic / n;
-            const double esd = (s_m[16 + 2 * r] - ms * sT) * is / n;
+            const double ecd = (s_m[15 + 2 * r] - mc * sT) * ic * g.inv_n;
+            const double esd = (s_m[16 + 2 * r] - ms * sT) * is * g.inv_n;
             ecs = (float)ecd;
             ess = (float)esd;
             s_ec[2 * r] = ecd;
@@ -2682,9 +2691,9 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             const double Stt = s_m[3], Srr = s_m[4], Sbb = s_m[5] * cl * cl, Soo = s_m[6], Srb = s_m[7] * cl;
             const double Sro = s_m[8], Sbo = s_m[9] * cl;
             const double Str = s_m[10], Stb = s_m[11] * cl, Sto = s_m[12];
-            const float frms = sqrtf((float)(Stt / n) + eps);
-            const float rms_rat = sqrtf((float)(Srr / n) + eps);
-            const float rms_root = sqrtf((float)(Soo / n) + eps);
+            const float frms = sqrtf((float)(Stt * g.inv_n) + eps);
+            const float rms_rat = sqrtf((float)(Srr * g.inv_n) + eps);
+            const float rms_root = sqrtf((float)(Soo * g.inv_n) + eps);
             const float kroot = rms_rat / fmaxf(rms_root, eps);
             const float spike = (float)h.spike_mix / (1.0f + S);
             const float rmix = (hard ? (float)h.root_channel_mix : 0.0f) / (1.0f + 0.5f * S);
@@ -2692,7 +2701,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             const double ab = (double)((1.0f - rmix) * spike);
             const double ao = (double)(rmix * kroot);
             const double sh2 = ar * ar * Srr + ab * ab * Sbb + ao * ao * Soo + 2.0 * (ar * ab * Srb + ar * ao * Sro + ab * ao * Sbo);
-            const float srms = sqrtf((float)(sh2 / n) + eps);
+            const float srms = sqrtf((float)(sh2 * g.inv_n) + eps);
             const float dmix = (float)h.direct_force_mix / (1.0f + 0.35f * S);
             const float kdir = srms / fmaxf(frms, eps);
             const double cr = (1.0 - (double)dmix) * ar, cb = (1.0 - (double)dmix) * ab, co = (1.0 - (double)dmix) * ao;
@@ -2709,8 +2718,8 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             const double warm = h.warmup_steps == 0 ? 1.0 : 1.0 - exp(-(double)step / (double)(h.warmup_steps > 1 ? h.warmup_steps : 1));
             const float mix = (float)(h.prediction_mix * warm) * agate * (1.0f / (1.0f + S));
             // residual feedback: err' rms from the directly summed err rms and the Gram corrections
-            const float crms = sqrtf((float)(core2 / n) + eps);
-            const double ee = fmax(s_m[0] / n - 2.0 * Q3 + Q2, 0.0);
+            const float crms = sqrtf((float)(core2 * g.inv_n) + eps);
+            const double ee = fmax(s_m[0] * g.inv_n - 2.0 * Q3 + Q2, 0.0);
             const float erms = sqrtf((float)ee + eps);
             const float kres = crms / fmaxf(erms, eps);
             const float resmix = (float)h.residual_feedback_mix / (1.0f + S);
@@ -2732,18 +2741,39 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             ctrl->srms = srms;
             s_srms = srms;
         }
-    } else if (c5_closed) {
-        // waves 1.. (while wave 0 runs the mode lanes): the hash prediction's
-        // sum of squares over the field, sum_i ((imp0[b0] + imp1[b1]) / 2)^2,
-        // in closed form from the bin and co-occurrence counts
-        const int B = g.B;
+    } else {
+        // waves 1.. while wave 0 runs the mode lanes: hash refractory / impulse
+        // (cresso_v5.py:1140-1184)
         const int t1 = tid - 64, n1 = SP_FN_NT - 64;
-        double a = 0.0;
-        for (int k = t1; k < B * B; k += n1)
-            a += (double)cooc[k] * (2.0 * (double)s_impv[k / B] * (double)s_impv[B + k % B]);
-        for (int k = t1; k < 2 * B; k += n1) a += (double)counts[k] * ((double)s_impv[k] * (double)s_impv[k]);
-        const double w = wave_total_d(a);
-        if ((tid & 63) == 63) s_hhw[(tid >> 6) - 1] = w;
+        if (hash_on) {
+            const int TB = g.T * g.B;
+            for (int i = t1; i < TB; i += n1) {
+                const double cnt = fmax((double)counts[i], 1.0);
+                const float cp = (float)((double)(long long)hist[i] / ctrl->hs_P / cnt);
+                hist[i] = 0ull;
+                const float ref = st.hash_refractory[i] * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * fabsf(cp);
+                const float gate = 1.0f / (1.0f + (float)h.refractory_gain * ref);
+                const float im =
+                    st.hash_impulse[i] * (float)h.hash_impulse_decay + (float)(1.0 - h.hash_impulse_decay) * (cp * gate);
+                st.hash_refractory[i] = ref;
+                st.hash_impulse[i] = im;
+                imp_tab[i] = im;
+                if (c5_closed) s_impv[i] = im;
+            }
+        }
+        if (c5_closed) {
+            waves_sync(&s_sync, SP_FN_NT / 64 - 1);   // s_impv complete
+            // the hash prediction's sum of squares over the field,
+            // sum_i ((imp0[b0] + imp1[b1]) / 2)^2, in closed form from the bin
+            // and co-occurrence counts
+            const int B = g.B;
+            double a = 0.0;
+            for (int k = t1; k < B * B; k += n1)
+                a += (double)cooc[k] * (2.0 * (double)s_impv[k / B] * (double)s_impv[B + k % B]);
+            for (int k = t1; k < 2 * B; k += n1) a += (double)counts[k] * ((double)s_impv[k] * (double)s_impv[k]);
+            const double w = wave_total_d(a);
+            if ((tid & 63) == 63) s_hhw[(tid >> 6) - 1] = w;
+        }
     }
     if (c5_closed) {
         __syncthreads();
@@ -2752,7 +2782,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             for (int w = 0; w < SP_FN_NT / 64 - 1; ++w) hh += s_hhw[w];
             hh *= 0.25;
             // the hash term's coefficient as fin4_values forms it, from sum hp^2
-            const float khp = s_srms / fmaxf(sqrtf((float)(hh / n) + eps), eps);
+            const float khp = s_srms / fmaxf(sqrtf((float)(hh * g.inv_n) + eps), eps);
             ctrl->k_hash = (float)(hard ? h.hash_drive_mix * (double)khp : 0.0);
         }
     }
@@ -3076,7 +3106,6 @@ __device__ void fin4_values(const Geom& g, const double* __restrict__ part, cons
         m[v] = 0.0;
         for (int w = 0; w < SP_NT / 64; ++w) m[v] += s_w[w][v];
     }
-    const double n = (double)g.n;
     const float eps = (float)h.eps;
     double c5, dd;
     if (c5_closed) {
@@ -3085,11 +3114,11 @@ __device__ void fin4_values(const Geom& g, const double* __restrict__ part, cons
         dd = m[0];
     } else {
         float khp = 0.f;
-        if (hard && hash_on) khp = ctrl->srms / fmaxf(sqrtf((float)(m[2] / n) + eps), eps);
+        if (hard && hash_on) khp = ctrl->srms / fmaxf(sqrtf((float)(m[2] * g.inv_n) + eps), eps);
         c5 = hard ? h.hash_drive_mix * (double)khp : 0.0;
         dd = m[0] + 2.0 * c5 * m[1] + c5 * c5 * m[2];
     }
-    const float de_now = (float)(fmax(dd, 0.0) / n);
+    const float de_now = (float)(fmax(dd, 0.0) * g.inv_n);
     const float de = reservoir_f(ctrl->de_prev, de_now, h.reservoir_decay, step);
     if (blockIdx.x == 0 && threadIdx.x == 0) *de_state = de;
     c5f = (float)c5;

@@ -163,6 +163,8 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     g.chunk1 = (((g.n + g.nblk1 - 1) / g.nblk1) + 3) & ~(int64_t)3;
     g.nblk1 = (int32_t)((g.n + g.chunk1 - 1) / g.chunk1);
     // axis density sums: density <= 1e6 per element, sums below 2^62
+    g.shrink = 1.0 / std::sqrt(std::fmax(1.0, 0.7 * std::log2((double)g.R + 1.0)));
+    g.inv_n = 1.0 / (double)g.n;
     g.hs_row = ldexp(1.0, (int)std::floor(62.0 - std::log2(1.0e6 * (double)g.cols)));
     g.hs_col = ldexp(1.0, (int)std::floor(62.0 - std::log2(1.0e6 * (double)g.rows)));
     // workspace layout
