@@ -1783,14 +1783,14 @@ __device__ void set_recon_lanes(const Geom& g, const double* __restrict__ stats,
         }
     }
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup", "local");   // LDS only: pending global stores need not complete
     if (r == 0) {
         float cst = 0.f;
         for (int q = 0; q < g.R; ++q) cst -= s_tmp[q];
         *rconst = cst;
     }
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup", "local");   // LDS only: pending global stores need not complete
 }
 
 // Sum over lanes 0..R-1 of a fully active wave (fp64), in the fixed order of
@@ -2621,7 +2621,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             s_gu[r] = gu;
         }
         __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup", "local");   // LDS only: pending global stores need not complete
         // port projections (cresso_v5.py:1136): P = err + tm t = (1 + tm) t - pred
         float pc = 0.f, ps = 0.f;
         if (on) {
@@ -2662,7 +2662,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             *st.action = action;
         }
         __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup", "local");   // LDS only: pending global stores need not complete
         // Gram products, lane v = carrier v (v < 2R <= 32)
         double q0 = 0.0, q1 = 0.0, q2 = 0.0, q3 = 0.0, q4 = 0.0;
         if (r < V) {
