@@ -252,6 +252,23 @@ __device__ __forceinline__ double wave_total_d(double v) {
     return v;
 }
 
+// Issue priority that falls as a wave works through its share: q = the
+// quarter of the work reached (0..3).  Several blocks share each CU's SIMDs
+// and the arbiter favours the oldest wave, so in a launch of one round the
+// blocks of a CU otherwise finish one after another, and the last ones run
+// alone at a fraction of the occupancy; with the priority, waves that are
+// behind win the arbitration and the blocks finish together.
+__device__ __forceinline__ void progress_prio(int q) {
+    if (q <= 0)
+        __builtin_amdgcn_s_setprio(3);
+    else if (q == 1)
+        __builtin_amdgcn_s_setprio(2);
+    else if (q == 2)
+        __builtin_amdgcn_s_setprio(1);
+    else
+        __builtin_amdgcn_s_setprio(0);
+}
+
 // Wave sum of a float in a fixed lane order with DPP (quad xor 1, 2; row
 // rotate 4, 8; row broadcasts 15, 31): the total lands in lane 63.
 template <int CTRL, int ROW_MASK>

@@ -1681,6 +1681,7 @@ __global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
 #pragma unroll
     for (int tr = 0; tr < 4; ++tr) {
         if (tr >= ntr) break;
+        progress_prio(4 * tr / ntr);
         float rs[4] = {0.f, 0.f, 0.f, 0.f};   // this row of tiles' density, per lane row
 #pragma unroll
         for (int tc = 0; tc < 4; ++tc) {
@@ -2459,6 +2460,7 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
     row_alpha(0);
     recon(0, lmA, prA);
     for (int tr = 0; tr < ntr; ++tr) {
+        progress_prio(4 * tr / ntr);
         // the fields of tile (tr, tc + 1), or of (tr + 1, 0), go to the matrix
         // cores before tile (tr, tc)'s element math, which reads the fields
         // issued one tile earlier
@@ -3052,6 +3054,7 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
         elem_fence();
     };
     auto row_tiles = [&](int tr, const float* x, const uint32_t* b) {
+        progress_prio(64 * tr / nr);   // rows of tiles done of nr / 16
         // A operands of this row of tiles: alpha_{4 kc + lg}(row 16 tr + li)
         const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
         float aP[KCH], aX[KCH];
