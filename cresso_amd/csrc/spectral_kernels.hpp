@@ -1599,7 +1599,7 @@ __global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl,
     double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ rowfx,
     unsigned long long* __restrict__ colfx, const double* __restrict__ part1, float* __restrict__ fr_state, int step,
-    Lanes L, cresso_hyper h) {
+    Lanes L, cresso_hyper h, int one_round) {
     if (L.dv) {
         const cresso_spectral_desc& d = lane_desc(L);
         grad = (const GT*)d.grad; fr_state = (float*)d.force_rms; step = d.step;
@@ -1681,7 +1681,7 @@ __global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
 #pragma unroll
     for (int tr = 0; tr < 4; ++tr) {
         if (tr >= ntr) break;
-        progress_prio(4 * tr / ntr);
+        if (one_round) progress_prio(4 * tr / ntr);
         float rs[4] = {0.f, 0.f, 0.f, 0.f};   // this row of tiles' density, per lane row
 #pragma unroll
         for (int tc = 0; tc < 4; ++tc) {
@@ -2273,7 +2273,7 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
     const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx,
     const unsigned long long* __restrict__ colfx, const float* __restrict__ colfac, float* __restrict__ tbuf,
-    double* __restrict__ part, unsigned long long* __restrict__ hist, Lanes L, cresso_hyper h) {
+    double* __restrict__ part, unsigned long long* __restrict__ hist, Lanes L, cresso_hyper h, int one_round) {
     if (L.dv) grad = (const GT*)lane_desc(L).grad;
     ctrl = lane_at(ctrl, L); lt = lane_at(lt, L); rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L);
     colfac = lane_at(colfac, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L); hist = lane_at(hist, L);
@@ -2460,7 +2460,7 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
     row_alpha(0);
     recon(0, lmA, prA);
     for (int tr = 0; tr < ntr; ++tr) {
-        progress_prio(4 * tr / ntr);
+        if (one_round) progress_prio(4 * tr / ntr);
         // the fields of tile (tr, tc + 1), or of (tr + 1, 0), go to the matrix
         // cores before tile (tr, tc)'s element math, which reads the fields
         // issued one tile earlier
@@ -2944,7 +2944,7 @@ template <int RM, int KC, int TT, bool C5C>
 __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void sweep4m_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
     const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
-    float* __restrict__ tbuf, double* __restrict__ part, int echo_on, Lanes L, cresso_hyper h) {
+    float* __restrict__ tbuf, double* __restrict__ part, int echo_on, Lanes L, cresso_hyper h, int one_round) {
     ctrl = lane_at(ctrl, L); imp_tab = lane_at(imp_tab, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L);
     static_assert(!C5C || TT == 2, "closed-form hash term with two tables");
     extern __shared__ __align__(16) unsigned char dyn[];
@@ -3054,7 +3054,7 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
         elem_fence();
     };
     auto row_tiles = [&](int tr, const float* x, const uint32_t* b) {
-        progress_prio(64 * tr / nr);   // rows of tiles done of nr / 16
+        if (one_round) progress_prio(64 * tr / nr);   // rows of tiles done of nr / 16
         // A operands of this row of tiles: alpha_{4 kc + lg}(row 16 tr + li)
         const float* __restrict__ alr = s_al + (16 * tr + li) * (2 * KP) + lg;
         float aP[KCH], aX[KCH];
@@ -3325,6 +3325,18 @@ size_t lds_sweep2(const Geom& g, int rw) {
 size_t lds_sweep3(const Geom& g, int kp, int rw) {
     return lds_al_off(g) + sizeof(float) * (2 * (size_t)kp + rw) * g.PR;
 }
+// Compute units of the current device (queried once per device).
+inline int resident_cus() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int cus = 0;
+        cache[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0 ? cus : 256;
+    }
+    return cache[dev];
+}
+
 template <int KC> size_t lds_sweep3m(const Geom& g, int rw) {
     return lds_sweep3(g, kcp<KC>(), rw) + sizeof(float) * ((bq_in_regs<KC>() ? 0 : (size_t)kcp<KC>() * SP_BQS) + SP_NT);
 }
@@ -3401,14 +3413,17 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     // the matrix-core sweeps write per-block histogram partials (hpart),
     // which part_reduce sums into hist; the general sweeps add into hist
     const bool m2 = mf;
+    // the matrix-core sweeps' wave priorities pay only when every block is
+    // resident at once (one round: the blocks of a CU then start together)
+    const int one_round = (int64_t)g.nblk * count <= (int64_t)resident_cus() * ((RM > 8 || kch<KC>() > 3) ? 2 : 4);
     const bool m3 = mf && lds_sweep3m<KC>(g, 2 * RM) <= SP_LDS_MAX_M;
     if (m2) {
         if (t4)
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 4>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h);
+                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round);
         else
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 2>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h);
+                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round);
     } else if (fast) {
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
@@ -3432,10 +3447,10 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
         const size_t l3m = lds_sweep3m<KC>(g, 2 * RM);
         if (t4)
             hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 4>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h);
+                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h, one_round);
         else
             hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 2>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h);
+                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h, one_round);
     } else if (fast) {
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 1>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, L, h);
@@ -3452,10 +3467,10 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
                        cooc, step, hash_on, hard, echo_on, c5c, L, h);
     if (c5c)
         hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
-                           tbuf, part, echo_on, L, h);
+                           tbuf, part, echo_on, L, h, one_round);
     else if (mf && t4)
         hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
-                           tbuf, part, echo_on, L, h);
+                           tbuf, part, echo_on, L, h, one_round);
     else if (fast)
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
                            hash_on, echo_on, L, h);
