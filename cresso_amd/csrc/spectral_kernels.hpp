@@ -737,28 +737,67 @@ __device__ __forceinline__ float reservoir_f(float old, float cur, double decay,
     return old * (float)decay + (float)(1.0 - decay) * cur;
 }
 
-// Cross-block merge of a sweep's partials spread over many CUs: block v sums
-// value v of every block's row part[block][VS] (thread j: blocks j, j + 256,
-// ... in order; then a fixed-order DPP wave tree and the four wave totals in
-// order) into sums[v].  Blocks VS.. reduce the matrix-core sweeps' per-block
-// histogram partials (hpart[block][bin], 64-bit fixed point: integer sums, in
-// any order the same) into hist[bin], one bin per block.
+// Histogram partials merged by part_reduce_kernel's blocks after the values:
+// small merges (64-bin groups x partial rows <= 4096, e.g. C2's 128 bins x
+// 1024 rows) take one bin per block over every row (pr_hist_rows = 0); larger
+// ones blocks of 64 bins x pr_hist_rows partial rows (each wave reads 512
+// contiguous bytes of a row), about 1024 such blocks (8 to 64 rows each:
+// C5's 1024 bins x 4096 rows take 1024 blocks of 64), whose bin strides
+// would otherwise make every load its own cache line.
+constexpr int PR_HB = 64;
+__host__ __device__ inline int pr_hist_rows(int TB, int nblk) {
+    const int ng = (TB + PR_HB - 1) / PR_HB;
+    if ((int64_t)ng * nblk <= 4096) return 0;
+    const int r = (int)(((int64_t)nblk * ng) / 1024);
+    return r < 8 ? 8 : (r > 64 ? 64 : r);
+}
+__host__ __device__ inline int pr_hist_blocks(int TB, int nblk) {
+    const int hr = pr_hist_rows(TB, nblk);
+    return hr == 0 ? TB : ((TB + PR_HB - 1) / PR_HB) * ((nblk + hr - 1) / hr);
+}
+
+// Cross-block merge of a sweep's partials spread over many CUs: block v < VS
+// sums value v of every block's row part[block][VS] (thread j: blocks j,
+// j + 256, ... in order; then a fixed-order DPP wave tree and the four wave
+// totals in order) into sums[v].  The pr_hist_blocks(TB, nblk) blocks after
+// them merge the matrix-core sweeps' per-block histogram partials
+// (hpart[block][bin], 64-bit fixed point): one bin over every row each, or
+// 64 bins of pr_hist_rows partial rows adding their integer sums into
+// hist[bin] with 64-bit atomics (integer
+// sums: the same in any order).  hist is zero on entry (the finish kernels
+// clear it after reading).
 __global__ __launch_bounds__(256) void part_reduce_kernel(
     const double* __restrict__ part, int nblk, int VS, double* __restrict__ sums,
-    const unsigned long long* __restrict__ hpart, unsigned long long* __restrict__ hist, Lanes L) {
+    const unsigned long long* __restrict__ hpart, unsigned long long* __restrict__ hist, int TB, Lanes L) {
     part = lane_at(part, L); sums = lane_at(sums, L); hpart = lane_at(hpart, L); hist = lane_at(hist, L);
     __shared__ double s_w[4];
-    __shared__ unsigned long long s_h[4];
+    __shared__ unsigned long long s_h[4][PR_HB];
     const int v = blockIdx.x;
-    if (v >= VS) {
+    const int hr = pr_hist_rows(TB, nblk);
+    if (v >= VS && hr == 0) {
+        // one bin, every block's row
         const int i = v - VS;
         unsigned long long a = 0ull;
-        const int TB = (int)gridDim.x - VS;
         for (int b = threadIdx.x; b < nblk; b += 256) a += hpart[(size_t)b * TB + i];
         for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
-        if ((threadIdx.x & 63) == 0) s_h[threadIdx.x >> 6] = a;
+        if ((threadIdx.x & 63) == 0) s_h[threadIdx.x >> 6][0] = a;
         __syncthreads();
-        if (threadIdx.x == 0) hist[i] = s_h[0] + s_h[1] + s_h[2] + s_h[3];
+        if (threadIdx.x == 0) hist[i] = s_h[0][0] + s_h[1][0] + s_h[2][0] + s_h[3][0];
+        return;
+    }
+    if (v >= VS) {
+        const int hb = v - VS, ng = (TB + PR_HB - 1) / PR_HB;
+        const int bin = (hb % ng) * PR_HB + (threadIdx.x & (PR_HB - 1));
+        const int b0 = (hb / ng) * hr, b1 = b0 + hr < nblk ? b0 + hr : nblk;
+        unsigned long long a = 0ull;
+        if (bin < TB)
+            for (int b = b0 + (int)(threadIdx.x >> 6); b < b1; b += 4) a += hpart[(size_t)b * TB + bin];
+        s_h[threadIdx.x >> 6][threadIdx.x & (PR_HB - 1)] = a;
+        __syncthreads();
+        if (threadIdx.x < PR_HB && bin < TB) {
+            const unsigned long long t = s_h[0][threadIdx.x] + s_h[1][threadIdx.x] + s_h[2][threadIdx.x] + s_h[3][threadIdx.x];
+            atomicAdd(&hist[bin], t);
+        }
         return;
     }
     double a = 0.0;
@@ -3431,8 +3470,8 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 0>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
     }
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2 + (m2 ? g.T * g.B : 0), ny), dim3(256), 0, s, part, g.nblk, NV2, sums,
-                       hpart, hist, L);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2 + (m2 ? pr_hist_blocks(g.T * g.B, g.nblk) : 0), ny), dim3(256), 0, s,
+                       part, g.nblk, NV2, sums, hpart, hist, g.T * g.B, L);
     hipLaunchKernelGGL(fin2_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st, ctrl,
                        step, hash_on, hard, L, h);
     if (axes_on && g.ntrail > 1) {
@@ -3461,8 +3500,8 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     // with two tables sweep4m writes the full drive: fin3 then forms the hash
     // term's RMS from the co-occurrence counts, and sweep 5 needs no bins
     const int c5c = (mf && cooc_closed(g)) ? 1 : 0;
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 ? g.T * g.B : 0), ny), dim3(256), 0, s, part, g.nblk, NV3, sums,
-                       hpart, hist, L);
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 ? pr_hist_blocks(g.T * g.B, g.nblk) : 0), ny), dim3(256), 0, s,
+                       part, g.nblk, NV3, sums, hpart, hist, g.T * g.B, L);
     hipLaunchKernelGGL(fin3_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
                        cooc, step, hash_on, hard, echo_on, c5c, L, h);
     if (c5c)

@@ -609,7 +609,7 @@ extern "C" int32_t cresso_spectral_workspace_project(const cresso_spectral_plan*
     hipLaunchKernelGGL(ws_project_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, at<ModeMeta>(ws, P->o.meta),
                        at<float>(ws, P->o.rowtab), at<float>(ws, P->o.coltab), at<double>(ws, P->o.stats), x, part);
     hipLaunchKernelGGL(part_reduce_kernel, dim3((unsigned)(2 * g.R)), dim3(256), 0, s, part, (int)blocks, 2 * g.R, sums,
-                       nullptr, nullptr, Lanes{nullptr, 0});
+                       nullptr, nullptr, 0, Lanes{nullptr, 0});
     hipLaunchKernelGGL(ws_mean_kernel, dim3(1), dim3(64), 0, s, sums, 2 * g.R, 1.0 / (double)g.n, out);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace project");
