@@ -80,6 +80,21 @@ def make_c3(device, pool=4, seed=0):
     return params, grads, kwargs, shapes, scales
 
 
+def make_forms(device, pool=1, seed=0):
+    """Profile-only group (not a bench line) for the scalar route's other launch
+    forms: 256 small thin tensors (scalar_stream_kernel), 4 large thin tensors
+    (the wide form's passes and finishes) and 64 micro-route tensors
+    (micro_kernel), one scalar plan."""
+    gen = torch.Generator().manual_seed(seed)
+    shapes = [(999, 7)] * 256 + [(262144, 32)] * 4 + [(64, 64)] * 64
+    params = [torch.nn.Parameter((0.02 * torch.randn(s, generator=gen)).to(device)) for s in shapes]
+    grads = []
+    for _ in range(pool):
+        grads.append([(1e-3 * torch.randn(s, generator=gen)).to(device) for s in shapes])
+    kwargs = dict(lr=2e-3, rank=4, hash_bins=64, hash_tables=2, micro_field_max_size=4096)
+    return params, grads, kwargs, shapes, None
+
+
 def make_c2(device, pool=4, seed=0):
     gen = torch.Generator().manual_seed(seed)
     shape = (4096, 4096)
@@ -299,6 +314,23 @@ def _counter_means(paths, by_grid=False):
     return {k: {cn: (sum(v) / len(v), len(v)) for cn, v in d.items()} for k, d in agg.items()}
 
 
+def _trace_means(paths):
+    """{"kernel @ workgroups": mean duration in us} of the library's kernels
+    over the given kernel-trace files."""
+    from collections import defaultdict
+    acc = defaultdict(lambda: [0, 0.0])
+    for path in paths:
+        for r in _read_csv(path):
+            if not _hot(r["Kernel_Name"]):
+                continue
+            wg = max(1, int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"]))
+            blocks = (int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])) // wg
+            a = acc[f"{_short_kernel(r['Kernel_Name'])} @ {blocks}"]
+            a[0] += 1
+            a[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    return {k: tot / n for k, (n, tot) in acc.items()}
+
+
 def _copy_reading(calib_dirs, counter):
     """Median reading of `counter` over the 256 MiB copies of `bench.py --workload copy`."""
     import glob
@@ -415,6 +447,29 @@ def rocprof_summary(dirs, calib=None, launches=None):
                 t_v = (iv - mf + 3.0 * tr) * 4 / 1024 / 2.4e9 * 1e6
                 t_m = mf * 32 / 1024 / 2.4e9 * 1e6
                 out.append(f"| {k} | {iv:.4g} | {100 * tr / max(iv, 1):.1f} | {t_v:.1f} | {mf:.4g} | {t_m:.1f} |")
+        # achieved HBM bandwidth of each library kernel of the step, per launch
+        # grid: the scaled FETCH_SIZE + WRITE_SIZE bytes per dispatch over the
+        # mean duration of that kernel at that grid in the kernel trace given
+        # with the counter directories
+        dur = _trace_means(found("*kernel_trace.csv"))
+        if dur and "FETCH_SIZE" in scale and "WRITE_SIZE" in scale:
+            gmb = _counter_means(cc, by_grid=True)
+            rows_bw = []
+            for k, d_ in gmb.items():
+                if not k.startswith("*") or "FETCH_SIZE" not in d_ or "WRITE_SIZE" not in d_:
+                    continue
+                key = k[1:]
+                if key not in dur:
+                    continue
+                b = d_["FETCH_SIZE"][0] * 1024.0 * scale["FETCH_SIZE"] + d_["WRITE_SIZE"][0] * 1024.0 * scale["WRITE_SIZE"]
+                us = dur[key]
+                rows_bw.append((key, b, us, b / (us * 1e3)))
+            if rows_bw:
+                out.append("\n### Achieved HBM bandwidth per kernel and launch grid (counter bytes / trace duration)\n")
+                out.append("| kernel @ workgroups | HBM bytes per dispatch | mean us | GB/s | of 8 TB/s |")
+                out.append("|---|---:|---:|---:|---:|")
+                for key, b, us, gbs in sorted(rows_bw, key=lambda r: -r[2]):
+                    out.append(f"| {key} | {b:.4g} | {us:.2f} | {gbs:.0f} | {gbs / HBM_PEAK_GBS:.3f} |")
         # workloads of several shapes: the same per launch grid of the library's kernels
         gm = {k: d_ for k, d_ in _counter_means(cc, by_grid=True).items() if k.startswith("*")}
         if len(gm) > len([k for k in means if k.startswith("*")]):
@@ -438,7 +493,7 @@ def rocprof_summary(dirs, calib=None, launches=None):
     print("\n".join(out))
 
 
-MAKERS = {"c1": make_c1, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5}
+MAKERS = {"c1": make_c1, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5, "forms": make_forms}
 # the timing leg of the full C4 set draws its inputs on the device
 # C3's 840 grads are set once: assigning p.grad for 840 tensors in Python costs
 # ~0.3 us each, more than the GPU step, and is input refresh, not optimizer work
@@ -564,7 +619,9 @@ WORKLOAD_NAMES = {"c1": "C1: (2048,2048) fp32 spectral/hash route, rank 8, F=5, 
                   "c4": "C4: 1.2 B fp32 params (embedding (32000,2048), 22 layers of q,k,v,o (2048,2048), gate/up "
                         "(5632,2048), down (2048,5632), two (2048,) norms), rank 8, F=5, B=64, T=2",
                   "c5": "C5: bf16 (8192,8192), fp32 (512,256,3,3), (256,256,3,3), (64,512,512), rank 16, F=7, "
-                        "B=256, T=4"}
+                        "B=256, T=4",
+                  "forms": "profile-only: 256 x (999,7) scalar stream form, 4 x (262144,32) wide form, 64 x (64,64) "
+                           "micro route, fp32"}
 
 
 def measure(workload, args):
@@ -598,7 +655,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "c5", "copy"], default=None)
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "c5", "forms", "copy"], default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--rocprof-summary", default=None, nargs="+", metavar="DIR")
     ap.add_argument("--calib", default=None, nargs="+", metavar="DIR")
