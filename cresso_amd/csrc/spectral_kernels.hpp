@@ -2450,48 +2450,116 @@ __global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void swee
             aQ[kc] = alr[KP + 4 * kc];
         }
     };
+    // With registers to spare (two waves per SIMD: rank 16, or carriers held in
+    // registers) the tile's LDS reads go first: LDS operations complete in
+    // order, so a read issued after histogram atomics waits for them.  The
+    // atomics then follow the element math that feeds them, and the moments
+    // (the tile's longest VALU stretch) come after the atomics, so the next
+    // tile's reads find the LDS queue drained.  At four waves per SIMD the
+    // extra live registers spill, and the reads stay beside their uses.
+    constexpr bool GATHER = RM > 8 || kch<KC>() > 3;
     auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const f32x4m& lm, const f32x4m& pred) {
-        const float ec = ecl[16 * tc];
-        float tvs[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
-            const float M = med3f(fexp2(kM * med3f(lm[r], -3.0f, 3.0f)), 0.06f, 16.0f);
-            float den = scale_s * M;
-            den = den * med3f(s_rf[16 * tr + 4 * lg + r] * ec, 0.08f, 12.0f);
-            // hash metric exp(mean over tables of lt) as the product of the tables' exp(lt / T)
-            float hm = s_lt[bin_byte<TT>(b[r], 0)];
-#pragma unroll
-            for (int tt = 1; tt < TT; ++tt) hm *= s_lt[tt * B + bin_byte<TT>(b[r], tt)];
-            den = den * med3f(hm, 0.08f, 12.0f);
-            const float tv = med3f(x[r] * frcp(den + eps_s), -1.0e4f, 1.0e4f);
-            bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
-            tvs[r] = tv;
-            const float err = tv - pred[r];
-            const float P = err + tm * tv;
-            m_ee += err * err;
-            m_t += tv;
-            m_tt += tv * tv;
-            const float at = fabsf(tv);
-            const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
-            m_rr = fmaf(z.rat, z.rat, m_rr); m_bb = fmaf(z.th, z.th, m_bb); m_oo = fmaf(z.root, z.root, m_oo);
-            m_rb = fmaf(z.rat, z.th, m_rb); m_ro = fmaf(z.rat, z.root, m_ro); m_bo = fmaf(z.th, z.root, m_bo);
-            m_tr = fmaf(at, z.rat, m_tr); m_tb = fmaf(at, z.th, m_tb); m_to = fmaf(at, z.root, m_to);
-            const unsigned long long v = to_fixed_s(P * hs);
-#pragma unroll
-            for (int tt = 0; tt < TT; ++tt) atomicAdd(&s_hist[(tt * B + bin_byte<TT>(b[r], tt)) * NH + hc], v);
-        }
-        // A of the projection: a_q(row 16 tr + 4 lg + r), q = 16 qt + li
-#pragma unroll
-        for (int qt = 0; qt < NQ; ++qt)
+        if constexpr (GATHER) {
+            const float ec = ecl[16 * tc];
+            float rfv[4], hmv[4], aJv[NQ][4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int q = 16 * qt + li;
-                const float aJ = q < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (q < RW ? q : 0)] : 0.f;
-                zacc[qt][tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJ, tvs[r], zacc[qt][tc], 0, 0, 0);
+                rfv[r] = s_rf[16 * tr + 4 * lg + r];
+                // hash metric exp(mean over tables of lt) as the product of the tables' exp(lt / T)
+                float hm = s_lt[bin_byte<TT>(b[r], 0)];
+#pragma unroll
+                for (int tt = 1; tt < TT; ++tt) hm *= s_lt[tt * B + bin_byte<TT>(b[r], tt)];
+                hmv[r] = hm;
             }
-        pin1(m_ee); pin1(m_t); pin1(m_tt); pin1(m_rr); pin1(m_bb); pin1(m_oo);
-        pin1(m_rb); pin1(m_ro); pin1(m_bo); pin1(m_tr); pin1(m_tb); pin1(m_to);
+            // A of the projection: a_q(row 16 tr + 4 lg + r), q = 16 qt + li
+#pragma unroll
+            for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int q = 16 * qt + li;
+                    aJv[qt][r] = q < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (q < RW ? q : 0)] : 0.f;
+                }
+            float tvs[4];
+            unsigned long long vfx[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
+                const float M = med3f(fexp2(kM * med3f(lm[r], -3.0f, 3.0f)), 0.06f, 16.0f);
+                float den = scale_s * M;
+                den = den * med3f(rfv[r] * ec, 0.08f, 12.0f);
+                den = den * med3f(hmv[r], 0.08f, 12.0f);
+                const float tv = med3f(x[r] * frcp(den + eps_s), -1.0e4f, 1.0e4f);
+                bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
+                tvs[r] = tv;
+                const float err = tv - pred[r];
+                const float P = err + tm * tv;
+                m_ee += err * err;
+                m_t += tv;
+                m_tt += tv * tv;
+                vfx[r] = to_fixed_s(P * hs);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int tt = 0; tt < TT; ++tt) atomicAdd(&s_hist[(tt * B + bin_byte<TT>(b[r], tt)) * NH + hc], vfx[r]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float at = fabsf(tvs[r]);
+                const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+                m_rr = fmaf(z.rat, z.rat, m_rr); m_bb = fmaf(z.th, z.th, m_bb); m_oo = fmaf(z.root, z.root, m_oo);
+                m_rb = fmaf(z.rat, z.th, m_rb); m_ro = fmaf(z.rat, z.root, m_ro); m_bo = fmaf(z.th, z.root, m_bo);
+                m_tr = fmaf(at, z.rat, m_tr); m_tb = fmaf(at, z.th, m_tb); m_to = fmaf(at, z.root, m_to);
+            }
+#pragma unroll
+            for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    zacc[qt][tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJv[qt][r], tvs[r], zacc[qt][tc], 0, 0, 0);
+            pin1(m_ee); pin1(m_t); pin1(m_tt); pin1(m_rr); pin1(m_bb); pin1(m_oo);
+            pin1(m_rb); pin1(m_ro); pin1(m_bo); pin1(m_tr); pin1(m_tb); pin1(m_to);
+        } else {
+            const float ec = ecl[16 * tc];
+            float tvs[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                // metric field exp(c * clamp(recon(metric), +-3)) clamped (cresso_v5.py:1090-1093)
+                const float M = med3f(fexp2(kM * med3f(lm[r], -3.0f, 3.0f)), 0.06f, 16.0f);
+                float den = scale_s * M;
+                den = den * med3f(s_rf[16 * tr + 4 * lg + r] * ec, 0.08f, 12.0f);
+                // hash metric exp(mean over tables of lt) as the product of the tables' exp(lt / T)
+                float hm = s_lt[bin_byte<TT>(b[r], 0)];
+#pragma unroll
+                for (int tt = 1; tt < TT; ++tt) hm *= s_lt[tt * B + bin_byte<TT>(b[r], tt)];
+                den = den * med3f(hm, 0.08f, 12.0f);
+                const float tv = med3f(x[r] * frcp(den + eps_s), -1.0e4f, 1.0e4f);
+                bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
+                tvs[r] = tv;
+                const float err = tv - pred[r];
+                const float P = err + tm * tv;
+                m_ee += err * err;
+                m_t += tv;
+                m_tt += tv * tv;
+                const float at = fabsf(tv);
+                const Shape3A z = shape3a(at, k2, iclip, clip2, eps);
+                m_rr = fmaf(z.rat, z.rat, m_rr); m_bb = fmaf(z.th, z.th, m_bb); m_oo = fmaf(z.root, z.root, m_oo);
+                m_rb = fmaf(z.rat, z.th, m_rb); m_ro = fmaf(z.rat, z.root, m_ro); m_bo = fmaf(z.th, z.root, m_bo);
+                m_tr = fmaf(at, z.rat, m_tr); m_tb = fmaf(at, z.th, m_tb); m_to = fmaf(at, z.root, m_to);
+                const unsigned long long v = to_fixed_s(P * hs);
+#pragma unroll
+                for (int tt = 0; tt < TT; ++tt) atomicAdd(&s_hist[(tt * B + bin_byte<TT>(b[r], tt)) * NH + hc], v);
+            }
+            // A of the projection: a_q(row 16 tr + 4 lg + r), q = 16 qt + li
+#pragma unroll
+            for (int qt = 0; qt < NQ; ++qt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int q = 16 * qt + li;
+                    const float aJ = q < RW ? s_ar[(16 * tr + 4 * lg + r) * RW + (q < RW ? q : 0)] : 0.f;
+                    zacc[qt][tc] = __builtin_amdgcn_mfma_f32_16x16x4f32(aJ, tvs[r], zacc[qt][tc], 0, 0, 0);
+                }
+            pin1(m_ee); pin1(m_t); pin1(m_tt); pin1(m_rr); pin1(m_bb); pin1(m_oo);
+            pin1(m_rb); pin1(m_ro); pin1(m_bo); pin1(m_tr); pin1(m_tb); pin1(m_to);
+        }
         elem_fence();
     };
     const int ntr = nr / 16;
