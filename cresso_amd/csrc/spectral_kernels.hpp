@@ -1536,6 +1536,7 @@ template <int TT> __device__ __forceinline__ uint32_t bin_byte(uint32_t b, int t
 // projection rows of rank RM in 16-row tiles; carriers in chunks of 4
 template <int RM> constexpr int nqt() { return (2 * RM + 15) / 16; }
 
+
 // Inputs of a matrix-core sweep's projection finish: lane group lg's modes
 // r = 8 qt + 2 lg + h (h = 0, 1) and their column carriers b1, b2 at the
 // lane's 4 columns.  Fetched in the prologue, so that the finish after the
@@ -1621,6 +1622,14 @@ struct ProjCols {
     }
 };
 template <int KC> constexpr int kch() { return (KC + 3) / 4; }
+// Waves per SIMD (blocks of 256 threads per CU) each matrix-core sweep is
+// compiled for: 4 at rank <= 8 with carriers in LDS; sweep 3m holds the
+// carriers in registers past three chunks and 256 VGPRs at rank 16 (two
+// waves); sweeps 2m and 4m fit in 168 VGPRs at rank 16 (three waves, their
+// LDS 44 and 31 KiB a block).
+template <int RM, int KC> constexpr int occ2m() { return RM > 8 ? 3 : 4; }
+template <int RM, int KC> constexpr int occ3m() { return (RM > 8 || kch<KC>() > 3) ? 2 : 4; }
+template <int RM, int KC> constexpr int occ4m() { return (RM > 8 || kch<KC>() > 3) ? 3 : 4; }
 
 // ---------------------------------------------------------------------------
 // S2 on the matrix cores (MODE 1 tiles, RM <= 16, TT = 2 or 4 tables of
@@ -1633,7 +1642,7 @@ template <int KC> constexpr int kch() { return (KC + 3) / 4; }
 // lane and tile column until the end.
 // ---------------------------------------------------------------------------
 template <int RM, int KC, typename GT, int TT>
-__global__ __launch_bounds__(SP_NT, RM > 8 ? 2 : 4) void sweep2m_kernel(
+__global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
     Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl,
     double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ rowfx,
@@ -2307,7 +2316,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep3_kernel(
 // ---------------------------------------------------------------------------
 template <int KC> constexpr bool bq_in_regs() { return kch<KC>() > 3; }
 template <int RM, int KC, typename GT, int TT>
-__global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void sweep3m_kernel(
+__global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
     Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
     const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx,
@@ -3048,7 +3057,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
 // and the sums of d^2, d hp and hp^2 go to sweep 5.
 // ---------------------------------------------------------------------------
 template <int RM, int KC, int TT, bool C5C>
-__global__ __launch_bounds__(SP_NT, (RM > 8 || kch<KC>() > 3) ? 2 : 4) void sweep4m_kernel(
+__global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
     const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
     float* __restrict__ tbuf, double* __restrict__ part, int echo_on, Lanes L, cresso_hyper h, int one_round) {
@@ -3522,15 +3531,17 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     const bool m2 = mf;
     // the matrix-core sweeps' wave priorities pay only when every block is
     // resident at once (one round: the blocks of a CU then start together)
-    const int one_round = (int64_t)g.nblk * count <= (int64_t)resident_cus() * ((RM > 8 || kch<KC>() > 3) ? 2 : 4);
+    const int64_t nb = (int64_t)g.nblk * count, cus = resident_cus();
+    const int one_round2 = nb <= cus * occ2m<RM, KC>(), one_round3 = nb <= cus * occ3m<RM, KC>();
+    const int one_round4 = nb <= cus * occ4m<RM, KC>();
     const bool m3 = mf && lds_sweep3m<KC>(g, 2 * RM) <= SP_LDS_MAX_M;
     if (m2) {
         if (t4)
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 4>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round);
+                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2);
         else
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 2>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round);
+                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2);
     } else if (fast) {
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
@@ -3554,10 +3565,10 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
         const size_t l3m = lds_sweep3m<KC>(g, 2 * RM);
         if (t4)
             hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 4>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h, one_round);
+                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h, one_round3);
         else
             hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 2>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h, one_round);
+                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h, one_round3);
     } else if (fast) {
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 1>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, L, h);
@@ -3574,10 +3585,10 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
                        cooc, step, hash_on, hard, echo_on, c5c, L, h);
     if (c5c)
         hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
-                           tbuf, part, echo_on, L, h, one_round);
+                           tbuf, part, echo_on, L, h, one_round4);
     else if (mf && t4)
         hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
-                           tbuf, part, echo_on, L, h, one_round);
+                           tbuf, part, echo_on, L, h, one_round4);
     else if (fast)
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
                            hash_on, echo_on, L, h);
