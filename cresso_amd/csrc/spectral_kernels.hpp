@@ -927,11 +927,34 @@ struct F1Values {
     float inv_s;
     double hs_ds;
 };
-__device__ F1Values fin1_values(const Geom& g, const double* __restrict__ part1, Ctrl* __restrict__ ctrl,
-                                float* __restrict__ fr_state, int step, const cresso_hyper& h) {
+// Sweep 1's block partials (sum, max) of one thread, blocks threadIdx.x +
+// i SP_NT: the first N loaded at once (indices clamped, so that no branch
+// separates the loads), summed later in block order.
+template <int N>
+struct F1Part {
+    double s[N > 0 ? N : 1], m[N > 0 ? N : 1];
+    __device__ __forceinline__ void load(const Geom& g, const double* __restrict__ part1) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            int b = (int)threadIdx.x + i * SP_NT;
+            b = b < g.nblk1 ? b : g.nblk1 - 1;
+            s[i] = part1[(size_t)b * 2];
+            m[i] = part1[(size_t)b * 2 + 1];
+        }
+    }
+};
+template <int N>
+__device__ F1Values fin1_values(const Geom& g, const F1Part<N>& fp, const double* __restrict__ part1,
+                                Ctrl* __restrict__ ctrl, float* __restrict__ fr_state, int step, const cresso_hyper& h) {
     __shared__ double s_w[SP_NT / 64], s_m[SP_NT / 64];
     double a = 0.0, mx = 0.0;
-    for (int b = threadIdx.x; b < g.nblk1; b += SP_NT) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if ((int)threadIdx.x + i * SP_NT < g.nblk1) {
+            a += fp.s[i];
+            mx = fmax(mx, fp.m[i]);
+        }
+    for (int b = threadIdx.x + N * SP_NT; b < g.nblk1; b += SP_NT) {
         a += part1[(size_t)b * 2];
         mx = fmax(mx, part1[(size_t)b * 2 + 1]);
     }
@@ -965,6 +988,10 @@ __device__ F1Values fin1_values(const Geom& g, const double* __restrict__ part1,
         ctrl->hs_ds = v.hs_ds;   // fin2 converts the histogram back with it
     }
     return v;
+}
+__device__ __forceinline__ F1Values fin1_values(const Geom& g, const double* __restrict__ part1, Ctrl* __restrict__ ctrl,
+                                                float* __restrict__ fr_state, int step, const cresso_hyper& h) {
+    return fin1_values<0>(g, F1Part<0>{}, part1, ctrl, fr_state, step, h);
 }
 
 // ---------------------------------------------------------------------------
@@ -1029,37 +1056,72 @@ __host__ __device__ inline size_t lds_al_off(const Geom& g) {
                         sizeof(float) * (size_t)g.PR;
     return (head + 15) & ~(size_t)15;
 }
+// The reconstruction coefficients alpha_rows builds from: every Cm entry a
+// thread writes has the same q = threadIdx.x mod 2 RM (blocks of SP_NT
+// threads, a multiple of 2 RM), so the thread needs one mode-table entry and
+// the weights of mode q / 2 in both sets.  Loaded first thing, with the
+// block's other set-up loads, so that they return in one round trip.
+struct CmSrc {
+    int on, add, k1, k2;
+    float wc[2], ws[2];
+};
+template <int RM>
+__device__ __forceinline__ CmSrc cm_src(const Geom& g, const ModeMeta* __restrict__ meta,
+                                        const float (*const rc0[2])[2], const float w0[2],
+                                        const float (*const rc1[2])[2], const float w1[2]) {
+    constexpr int RW = 2 * RM;
+    static_assert(SP_NT % RW == 0, "one projection row per thread residue");
+    const int r = (int)(threadIdx.x % RW) >> 1;
+    const int rr = r < g.R ? r : 0;
+    CmSrc c;
+    const ModeMeta m = meta[rr];
+    c.on = r < g.R;
+    c.add = m.type == M_ADD;
+    c.k1 = m.k1;
+    c.k2 = m.k2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        // the second set's loads are issued either way (from the first set,
+        // weighted 0, where it is absent: the coefficients are finite): a
+        // load inside a branch would wait at once for every load before it
+        const float (*const p1)[2] = rc1[j] ? rc1[j] : rc0[j];
+        const float v1 = rc1[j] ? w1[j] : 0.f;
+        c.wc[j] = fmaf(v1, p1[rr][0], w0[j] * rc0[j][rr][0]);
+        c.ws[j] = fmaf(v1, p1[rr][1], w0[j] * rc0[j][rr][1]);
+    }
+    return c;
+}
+
 template <int RM, int KC>
-__device__ void alpha_rows(const Geom& g, const ModeMeta* __restrict__ meta, const float* __restrict__ s_rows, int nr,
-                           const float (*const rc0[2])[2], const float w0[2], const float (*const rc1[2])[2],
-                           const float w1[2], float* __restrict__ s_al) {
+__device__ void alpha_rows(const Geom& g, const CmSrc& cs, const float* __restrict__ s_rows, int nr,
+                           float* __restrict__ s_al) {
     // alpha = rows x Cm^T: Cm[j][k][q] is the coefficient of the row factor
     // a_q (q = 2r + c: component c of mode r) in alpha_k of set j.  Every Cm
     // entry is built by its own thread from the mode table; each (row, set)
     // pair is then 2 RM x KP branch-free FMAs on values held in registers.
     constexpr int KP = kcp<KC>();
     constexpr int RW = 2 * RM;
+    constexpr int NE = 2 * KP * RW;
     __shared__ __align__(16) float s_cm[2][KP][RW];
-    for (int e = threadIdx.x; e < 2 * KP * RW; e += blockDim.x) {
-        const int j = e / (KP * RW), rem = e - j * (KP * RW), k = rem / RW, q = rem - k * RW;
-        const int r = q >> 1, c = q & 1;
-        float v = 0.f;
-        if (r < g.R && k < KC) {
-            const ModeMeta m = meta[r];
-            float wc = w0[j] * rc0[j][r][0], ws = w0[j] * rc0[j][r][1];
-            if (rc1[j]) {
-                wc += w1[j] * rc1[j][r][0];
-                ws += w1[j] * rc1[j][r][1];
+    const int q = (int)(threadIdx.x % RW), c = q & 1;
+#pragma unroll
+    for (int i = 0; i < (NE + SP_NT - 1) / SP_NT; ++i) {
+        const int e = (int)threadIdx.x + i * SP_NT;
+        if (e < NE) {
+            const int j = e / (KP * RW), k = (e - j * (KP * RW)) / RW;
+            const float wc = j ? cs.wc[1] : cs.wc[0], ws = j ? cs.ws[1] : cs.ws[0];
+            float v = 0.f;
+            if (cs.on && k < KC) {
+                if (cs.add) {   // alpha_k1 += wc a1 + ws a2, alpha_k2 += ws a1 - wc a2
+                    if (cs.k1 == k) v += c == 0 ? wc : ws;
+                    if (cs.k2 == k) v += c == 0 ? ws : -wc;
+                } else {        // alpha_k1 += wc a1, alpha_k2 += ws a2
+                    if (cs.k1 == k && c == 0) v += wc;
+                    if (cs.k2 == k && c == 1) v += ws;
+                }
             }
-            if (m.type == M_ADD) {   // alpha_k1 += wc a1 + ws a2, alpha_k2 += ws a1 - wc a2
-                if (m.k1 == k) v += c == 0 ? wc : ws;
-                if (m.k2 == k) v += c == 0 ? ws : -wc;
-            } else {                 // alpha_k1 += wc a1, alpha_k2 += ws a2
-                if (m.k1 == k && c == 0) v += wc;
-                if (m.k2 == k && c == 1) v += ws;
-            }
+            s_cm[j][k][q] = v;
         }
-        s_cm[j][k][q] = v;
     }
     __syncthreads();   // Cm and the caller's staged rows are complete
     // (row, set, half of the carriers) per thread: 4 nr items, all threads busy
@@ -1080,6 +1142,12 @@ __device__ void alpha_rows(const Geom& g, const ModeMeta* __restrict__ meta, con
     }
     __syncthreads();
 }
+template <int RM, int KC>
+__device__ void alpha_rows(const Geom& g, const ModeMeta* __restrict__ meta, const float* __restrict__ s_rows, int nr,
+                           const float (*const rc0[2])[2], const float w0[2], const float (*const rc1[2])[2],
+                           const float w1[2], float* __restrict__ s_al) {
+    alpha_rows<RM, KC>(g, cm_src<RM>(g, meta, rc0, w0, rc1, w1), s_rows, nr, s_al);
+}
 
 // The block's rows of the row-factor table into LDS: s_rows[lr][q], q < 2 RM
 // (the table's rows have g.RW >= 2 RM entries).  No barrier.
@@ -1088,6 +1156,62 @@ __device__ __forceinline__ void stage_rows(const Geom& g, const float* __restric
                                            float* __restrict__ s_rows) {
     constexpr int RW = 2 * RM;
     for (int e = threadIdx.x; e < nr * RW; e += blockDim.x) {
+        const int lr = e / RW, q = e - lr * RW;
+        s_rows[e] = rowtab[(r0 + lr) * g.RW + q];
+    }
+}
+
+// Set-up loads of the matrix-core sweeps, in two halves: load() issues every
+// global load of a staged table at once (addresses clamped into the table,
+// so that no branch separates them and one wait covers them all), store()
+// writes the values to LDS.  Up to N values per thread; a larger table takes
+// its remainder in a loop (never on the matrix-core path: panels of 32 or 64
+// rows, at most 4 tables of 256 bins).
+template <int N>
+struct Staged {
+    float v[N];
+    __device__ __forceinline__ void load(const float* __restrict__ src, int n) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int e = (int)threadIdx.x + i * SP_NT;
+            v[i] = src[e < n ? e : n - 1];
+        }
+    }
+    // row lr of the row-factor table: 2 RM entries of a row of g.RW
+    template <int RM>
+    __device__ __forceinline__ void load_rows(const Geom& g, const float* __restrict__ rowtab, int64_t r0, int nr) {
+        constexpr int RW = 2 * RM;
+        const int n = nr * RW;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            int e = (int)threadIdx.x + i * SP_NT;
+            e = e < n ? e : n - 1;
+            const int lr = e / RW, q = e - lr * RW;
+            v[i] = rowtab[(r0 + lr) * g.RW + q];
+        }
+    }
+    template <typename F>
+    __device__ __forceinline__ void store(float* __restrict__ dst, int n, F&& f) const {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int e = (int)threadIdx.x + i * SP_NT;
+            if (e < n) dst[e] = f(v[i]);
+        }
+    }
+    __device__ __forceinline__ void store(float* __restrict__ dst, int n) const {
+        store(dst, n, [](float x) { return x; });
+    }
+};
+// the remainder of a table longer than N values a thread
+template <int N, typename F>
+__device__ __forceinline__ void stage_rest(float* __restrict__ dst, const float* __restrict__ src, int n, F&& f) {
+    for (int e = (int)threadIdx.x + N * SP_NT; e < n; e += SP_NT) dst[e] = f(src[e]);
+}
+template <int RM, int N>
+__device__ __forceinline__ void stage_rows_rest(const Geom& g, const float* __restrict__ rowtab, int64_t r0, int nr,
+                                                float* __restrict__ s_rows) {
+    constexpr int RW = 2 * RM;
+    for (int e = (int)threadIdx.x + N * SP_NT; e < nr * RW; e += SP_NT) {
         const int lr = e / RW, q = e - lr * RW;
         s_rows[e] = rowtab[(r0 + lr) * g.RW + q];
     }
@@ -1568,9 +1692,12 @@ struct ProjCols {
             for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                 for (int tc = 0; tc < 4; ++tc) {
+                    // (row 0 for an absent carrier, then zeroed: no branch between the loads)
                     const int64_t c = colw + 16 * tc + li;
-                    b1[qt][hh][tc] = k1[qt][hh] >= 0 ? coltab[(size_t)k1[qt][hh] * g.cols + c] : 0.f;
-                    b2[qt][hh][tc] = k2[qt][hh] >= 0 ? coltab[(size_t)k2[qt][hh] * g.cols + c] : 0.f;
+                    const float v1 = coltab[(size_t)(k1[qt][hh] >= 0 ? k1[qt][hh] : 0) * g.cols + c];
+                    const float v2 = coltab[(size_t)(k2[qt][hh] >= 0 ? k2[qt][hh] : 0) * g.cols + c];
+                    b1[qt][hh][tc] = k1[qt][hh] >= 0 ? v1 : 0.f;
+                    b2[qt][hh][tc] = k2[qt][hh] >= 0 ? v2 : 0.f;
                 }
     }
     // the same carriers from an LDS copy of the block's column table rows (row stride ls)
@@ -1693,17 +1820,27 @@ __global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
     float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
     float* s_ar = s_wrow + 16 * g.PR;
+    // set-up loads, all issued behind the first tiles': the row factors and
+    // sweep 1's block partials
+    constexpr int NRW = (64 * RW + SP_NT - 1) / SP_NT;
+    Staged<NRW> srw;
+    srw.template load_rows<RM>(g, rowtab, t.r0, nr);
+    F1Part<4> f1p;
+    f1p.load(g, part1);
     for (int i = threadIdx.x; i < NH * TB; i += SP_NT) s_hist[i] = 0ull;
-    stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
+    srw.store(s_ar, nr * RW);
+    stage_rows_rest<RM, NRW>(g, rowtab, t.r0, nr, s_ar);
+    // the projection finish's carriers (their rows come from the mode table,
+    // in registers by now); first used after the loop
+    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
+    pc.load(g, coltab, colw, li);
     __syncthreads();
-    const F1Values f1 = fin1_values(g, part1, ctrl, fr_state, step, h);
+    const F1Values f1 = fin1_values<4>(g, f1p, part1, ctrl, fr_state, step, h);
     const float inv_s = f1.inv_s;
     const float eps = (float)h.eps;
     const float pw = (float)h.energy_power;
     const float sg = h.maximize ? -1.f : 1.f;
     const float hs = (float)f1.hs_ds;
-    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
-    pc.load(g, coltab, colw, li);
     // the lane's projection A operands, a_{16 qt + li}(row 16 tr + 4 lg + r),
     // held in registers: read from LDS inside the loop they would queue
     // behind the histogram atomics (LDS operations complete in order)
@@ -2375,49 +2512,68 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
     float* s_ar = s_al + 2 * KP * g.PR;
     const float eps = (float)h.eps;
     const float kappa = ctrl->kappa, gden = ctrl->gden;
+    // every set-up load goes out here, behind the first tiles' loads: the
+    // coefficient sources, exp(lt / T), the row factors and axis sums, the
+    // column carriers (B operands and the projection finish's) and axis sums
+    const float (*const rcm0[2])[2] = {ctrl->rc[0], ctrl->rc[1]};
+    const float (*const rcm1[2])[2] = {nullptr, nullptr};
+    const float wm0[2] = {1.f, 1.f}, wm1[2] = {0.f, 0.f};
+    const CmSrc cs = cm_src<RM>(g, meta, rcm0, wm0, rcm1, wm1);
+    constexpr int NLT = TT, NRW = (64 * RW + SP_NT - 1) / SP_NT;
+    Staged<NLT> slt;
+    slt.load(lt, TB);
+    Staged<NRW> srw;
+    srw.template load_rows<RM>(g, rowtab, t.r0, nr);
+    const unsigned long long rfx = rowfx[t.r0 + ((int)threadIdx.x < nr ? (int)threadIdx.x : nr - 1)];
+    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
+    const int64_t c_own = (int64_t)t.slab * SP_NT + threadIdx.x;
+    // the column's axis sum (2-D) or factor (more dims): both loads issued,
+    // the unused one through an empty buffer range (reads 0, no branch)
+    const bool two_d = g.ntrail == 1;
+    const u32x2 cfx2 = bload2u(make_rsrc(colfx + (int64_t)t.slab * SP_NT, two_d ? SP_NT * 8u : 0u), threadIdx.x * 8u, 0);
+    const float cfac = bload1(make_rsrc(colfac + (int64_t)t.slab * SP_NT, two_d ? 0u : SP_NT * 4u), threadIdx.x * 4u, 0);
+    const unsigned long long cfx = ((unsigned long long)cfx2[1] << 32) | cfx2[0];
+    float bqr[BQR ? 4 : 1][BQR ? KCH : 1];
+    if constexpr (BQR) {
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+            for (int kc = 0; kc < KCH; ++kc) {
+                const int k = 4 * kc + lg;
+                bqr[tc][kc] = coltab[(size_t)(k < KC ? k : 0) * g.cols + colw + 16 * tc + li];
+                if (k >= KC) bqr[tc][kc] = 0.f;
+            }
+    }
+    const float lts = 1.4426950408889634f / (float)TT;
+    auto exp_lt = [&](float v) { return fexp2(v * lts); };   // exp(lt / T)
+    slt.store(s_lt, TB, exp_lt);
+    stage_rest<NLT>(s_lt, lt, TB, exp_lt);
     for (int i = threadIdx.x; i < TB; i += SP_NT) {
-        s_lt[i] = fexp2(lt[i] * (1.4426950408889634f / (float)TT));   // exp(lt / T)
 #pragma unroll
         for (int c = 0; c < NH; ++c) s_hist[i * NH + c] = 0ull;
     }
-    for (int lr = threadIdx.x; lr < nr; lr += SP_NT)
-        s_rf[lr] = marg_factor(rowfx[t.r0 + lr], 1.0 / (g.hs_row * (double)g.cols), gden, kappa, eps);
-    stage_rows<RM>(g, rowtab, t.r0, nr, s_ar);
+    // the projection finish's carriers (their rows come from the mode table,
+    // in registers by now); first used after the loop
+    if constexpr (BQR) pc.load(g, coltab, colw, li);
+    const double irow = 1.0 / (g.hs_row * (double)g.cols);
+    if ((int)threadIdx.x < nr) s_rf[threadIdx.x] = marg_factor(rfx, irow, gden, kappa, eps);
+    for (int lr = threadIdx.x + SP_NT; lr < nr; lr += SP_NT) s_rf[lr] = marg_factor(rowfx[t.r0 + lr], irow, gden, kappa, eps);
+    srw.store(s_ar, nr * RW);
+    stage_rows_rest<RM, NRW>(g, rowtab, t.r0, nr, s_ar);
     // the block's column instant-metric factors in LDS [SP_NT], after the
     // column carriers (B operands of the reconstructions) when those are in
     // LDS too: [KP][SP_BQS] (rows padded so that the 4 lane groups of a wave
     // read distinct banks)
     float* s_bq = s_ar + RW * g.PR;
     float* s_ec = s_bq + (BQR ? 0 : KP * SP_BQS);
-    const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
-    float bqr[BQR ? 4 : 1][BQR ? KCH : 1];
-    {
-        const int64_t c = (int64_t)t.slab * SP_NT + threadIdx.x;
-        if constexpr (BQR) {
+    if constexpr (!BQR) {
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc)
-#pragma unroll
-                for (int kc = 0; kc < KCH; ++kc) {
-                    const int k = 4 * kc + lg;
-                    bqr[tc][kc] = k < KC ? coltab[(size_t)k * g.cols + colw + 16 * tc + li] : 0.f;
-                }
-        } else {
-#pragma unroll
-            for (int k = 0; k < KP; ++k) s_bq[k * SP_BQS + threadIdx.x] = k < KC ? coltab[(size_t)k * g.cols + c] : 0.f;
-        }
-        s_ec[threadIdx.x] = g.ntrail == 1 ? marg_factor(colfx[c], 1.0 / (g.hs_col * (double)g.rows), gden, kappa, eps) : colfac[c];
+        for (int k = 0; k < KP; ++k) s_bq[k * SP_BQS + threadIdx.x] = k < KC ? coltab[(size_t)k * g.cols + c_own] : 0.f;
     }
+    s_ec[threadIdx.x] = two_d ? marg_factor(cfx, 1.0 / (g.hs_col * (double)g.rows), gden, kappa, eps) : cfac;
     const float* __restrict__ bql = s_bq + lg * SP_BQS + 64 * wv + li;   // + 4 kc SP_BQS + 16 tc
     const float* __restrict__ ecl = s_ec + 64 * wv + li;                  // + 16 tc
-    {
-        const float (*const r0[2])[2] = {ctrl->rc[0], ctrl->rc[1]};
-        const float (*const r1[2])[2] = {nullptr, nullptr};
-        const float w0[2] = {1.f, 1.f}, w1[2] = {0.f, 0.f};
-        alpha_rows<RM, KC>(g, meta, s_ar, nr, r0, w0, r1, w1, s_al);   // ends with a barrier
-    }
-    // the projection finish's carriers: from the LDS table after the last
-    // tile, or (carriers held in registers) loaded now
-    if constexpr (BQR) pc.load(g, coltab, colw, li);
+    alpha_rows<RM, KC>(g, cs, s_ar, nr, s_al);   // ends with a barrier
     const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
     // the force's sign (maximize) rides on the denominator: f / den = grad / (sign den)
     const float sg = h.maximize ? -1.f : 1.f;
@@ -3101,8 +3257,20 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     float* s_imp = reinterpret_cast<float*>(dyn);
     float* s_al = reinterpret_cast<float*>(dyn + ((sizeof(float) * (size_t)g.T * g.B + 15) & ~(size_t)15));
     float* s_rows = s_al + 2 * KP * g.PR;   // the block's row factors [PR][2 RM]
-    stage_rows<RM>(g, rowtab, t.r0, nr, s_rows);
-    // B operands: carriers 4 kc + lg of the lane's column in each column tile
+    // set-up loads, all issued behind the first row's: the coefficient
+    // sources, the row factors, the impulse table and the B operands
+    // (carriers 4 kc + lg of the lane's column in each column tile)
+    const float kp = ctrl->k_pred, ke = ctrl->k_echo;
+    const float (*const rcm0[2])[2] = {ctrl->rc[2], ctrl->rc[2]};
+    const float (*const rcm1[2])[2] = {nullptr, echo_on ? ctrl->rc[3] : nullptr};
+    const float wm0[2] = {1.f, kp}, wm1[2] = {0.f, ke};
+    const CmSrc cs = cm_src<RM>(g, meta, rcm0, wm0, rcm1, wm1);
+    constexpr int RW = 2 * RM;
+    constexpr int NRW = (64 * RW + SP_NT - 1) / SP_NT;
+    Staged<NRW> srw;
+    srw.template load_rows<RM>(g, rowtab, t.r0, nr);
+    Staged<TT> simp;
+    simp.load(imp_tab, TB);
     const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
     float bq[4][KCH];
 #pragma unroll
@@ -3110,16 +3278,14 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
 #pragma unroll
         for (int kc = 0; kc < KCH; ++kc) {
             const int k = 4 * kc + lg;
-            bq[tc][kc] = k < KC ? coltab[(size_t)k * g.cols + colw + 16 * tc + li] : 0.f;
+            bq[tc][kc] = coltab[(size_t)(k < KC ? k : 0) * g.cols + colw + 16 * tc + li];
+            if (k >= KC) bq[tc][kc] = 0.f;
         }
-    for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
-    const float kp = ctrl->k_pred, ke = ctrl->k_echo;
-    {
-        const float (*const r0[2])[2] = {ctrl->rc[2], ctrl->rc[2]};
-        const float (*const r1[2])[2] = {nullptr, echo_on ? ctrl->rc[3] : nullptr};
-        const float w0[2] = {1.f, kp}, w1[2] = {0.f, ke};
-        alpha_rows<RM, KC>(g, meta, s_rows, nr, r0, w0, r1, w1, s_al);
-    }
+    srw.store(s_rows, nr * RW);
+    stage_rows_rest<RM, NRW>(g, rowtab, t.r0, nr, s_rows);
+    simp.store(s_imp, TB);
+    stage_rest<TT>(s_imp, imp_tab, TB, [](float x) { return x; });
+    alpha_rows<RM, KC>(g, cs, s_rows, nr, s_al);
     const float cQ = ctrl->rconst[2];
     const float cX = kp * ctrl->rconst[2] + (echo_on ? ke * ctrl->rconst[3] : 0.f);
     __syncthreads();
@@ -3209,9 +3375,24 @@ __device__ void fin4_values(const Geom& g, const double* __restrict__ part, cons
                             const cresso_hyper& h, float& gain, float& c5f) {
     __shared__ double s_w[SP_NT / 64][NV4];
     double acc[NV4] = {0.0, 0.0, 0.0};
-    for (int b = threadIdx.x; b < g.nblk; b += SP_NT)
+    // blocks threadIdx.x + i SP_NT in groups of NG: a group's loads go out
+    // together (indices clamped: no branch between them), then are summed in
+    // block order
+    constexpr int NG = 8;
+    for (int b0 = threadIdx.x; b0 < g.nblk; b0 += NG * SP_NT) {
+        double pv[NG][NV4];
 #pragma unroll
-        for (int v = 0; v < NV4; ++v) acc[v] += part[(size_t)b * NV4 + v];
+        for (int i = 0; i < NG; ++i) {
+            const int b = b0 + i * SP_NT < g.nblk ? b0 + i * SP_NT : g.nblk - 1;
+#pragma unroll
+            for (int v = 0; v < NV4; ++v) pv[i][v] = part[(size_t)b * NV4 + v];
+        }
+#pragma unroll
+        for (int i = 0; i < NG; ++i)
+            if (b0 + i * SP_NT < g.nblk)
+#pragma unroll
+                for (int v = 0; v < NV4; ++v) acc[v] += pv[i][v];
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int v = 0; v < NV4; ++v) {
@@ -3333,12 +3514,16 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
             b1 = ld_bins4(bins, e + st, binbytes);
         }
     }
-    float gain, c5;
-    fin4_values(g, part, ctrl, de_state, step, hash_on, hard, c5_closed, h, gain, c5);
+    // the impulse table's loads go out with the finish's (first 4 values a thread)
     const int TB = T * B;
     float* s_imp = reinterpret_cast<float*>(dyn);
+    Staged<4> simp;
+    if (HASH) simp.load(imp_tab, TB);
+    float gain, c5;
+    fin4_values(g, part, ctrl, de_state, step, hash_on, hard, c5_closed, h, gain, c5);
     if (HASH) {
-        for (int i = threadIdx.x; i < TB; i += SP_NT) s_imp[i] = imp_tab[i];
+        simp.store(s_imp, TB);
+        stage_rest<4>(s_imp, imp_tab, TB, [](float x) { return x; });
         __syncthreads();
     }
     const float kh = c5 * (1.0f / (float)T);
