@@ -1149,6 +1149,96 @@ __device__ void alpha_rows(const Geom& g, const ModeMeta* __restrict__ meta, con
     alpha_rows<RM, KC>(g, cm_src<RM>(g, meta, rc0, w0, rc1, w1), s_rows, nr, s_al);
 }
 
+// alpha on the matrix cores (the matrix-core sweeps):
+//   alpha[j][row][k] = sum_q rows[row][q] Cm[j][k][q]
+// as v_mfma_f32_16x16x4f32 over 16-row and 16-carrier tiles.  In step s of a
+// tile, lane (li, lg) holds q = QPL lg + s (QPL = 2 RM / 4 values of q a
+// lane): A[i][k] = rows[16 rt + li][q], B[k][j] = Cm[j][16 kt + li][q] built
+// in registers from the lane's modes q / 2 (CmLane, loaded with the block's
+// other set-up loads), so the Cm table needs no LDS and no barrier.
+typedef float f32x4m __attribute__((ext_vector_type(4)));
+template <int RM>
+struct CmLane {
+    static constexpr int QPL = RM / 2;
+    static constexpr int NM = QPL / 2;   // modes a lane (QPL is even: RM >= 4)
+    int on[NM], add[NM], k1[NM], k2[NM];
+    float wc[NM][2], ws[NM][2];
+};
+template <int RM>
+__device__ __forceinline__ CmLane<RM> cm_lane(const Geom& g, const ModeMeta* __restrict__ meta,
+                                              const float (*const rc0[2])[2], const float w0[2],
+                                              const float (*const rc1[2])[2], const float w1[2]) {
+    constexpr int QPL = CmLane<RM>::QPL, NM = CmLane<RM>::NM;
+    static_assert(RM >= 4 && RM % 4 == 0, "even q count a lane");
+    const int lg = (int)(threadIdx.x & 63) >> 4;
+    CmLane<RM> c;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        const int r = (QPL * lg) / 2 + m;
+        const int rr = r < g.R ? r : 0;
+        const ModeMeta mm = meta[rr];
+        c.on[m] = r < g.R;
+        c.add[m] = mm.type == M_ADD;
+        c.k1[m] = mm.k1;
+        c.k2[m] = mm.k2;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            // as cm_src: the second set's loads issued either way
+            const float (*const p1)[2] = rc1[j] ? rc1[j] : rc0[j];
+            const float v1 = rc1[j] ? w1[j] : 0.f;
+            c.wc[m][j] = fmaf(v1, p1[rr][0], w0[j] * rc0[j][rr][0]);
+            c.ws[m][j] = fmaf(v1, p1[rr][1], w0[j] * rc0[j][rr][1]);
+        }
+    }
+    return c;
+}
+template <int RM, int KC>
+__device__ void alpha_rows_m(const Geom& g, const CmLane<RM>& cl, const float* __restrict__ s_rows, int nr,
+                             float* __restrict__ s_al) {
+    constexpr int KP = kcp<KC>();
+    constexpr int RW = 2 * RM;
+    constexpr int QPL = CmLane<RM>::QPL;
+    constexpr int NKT = (KP + 15) / 16;
+    __syncthreads();   // the staged rows are complete
+    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int li = l & 15, lg = l >> 4;
+    const int ntr = nr / 16;
+    // (row tile, set) items over the block's waves (wave-uniform loop)
+    for (int it = wv; it < 2 * ntr; it += SP_NT / 64) {
+        const int rt = it >> 1, j = it & 1;
+        float a[QPL];
+#pragma unroll
+        for (int s = 0; s < QPL; ++s) a[s] = s_rows[(16 * rt + li) * RW + QPL * lg + s];
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+            const int k = 16 * kt + li;
+            f32x4m d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < QPL; ++s) {
+                const int m = s >> 1, c = s & 1;
+                const float wc = j ? cl.wc[m][1] : cl.wc[m][0], ws = j ? cl.ws[m][1] : cl.ws[m][0];
+                float v = 0.f;
+                if (cl.on[m] && k < KC) {
+                    if (cl.add[m]) {   // alpha_k1 += wc a1 + ws a2, alpha_k2 += ws a1 - wc a2
+                        if (cl.k1[m] == k) v += c == 0 ? wc : ws;
+                        if (cl.k2[m] == k) v += c == 0 ? ws : -wc;
+                    } else {           // alpha_k1 += wc a1, alpha_k2 += ws a2
+                        if (cl.k1[m] == k && c == 0) v += wc;
+                        if (cl.k2[m] == k && c == 1) v += ws;
+                    }
+                }
+                d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], v, d, 0, 0, 0);
+            }
+            // D[i][j'] in lane j' = li (carrier k), register r: row 16 rt + 4 lg + r
+            if (k < KP) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s_al[(16 * rt + 4 * lg + r) * (2 * KP) + j * KP + k] = d[r];
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // The block's rows of the row-factor table into LDS: s_rows[lr][q], q < 2 RM
 // (the table's rows have g.RW >= 2 RM entries).  No barrier.
 template <int RM>
@@ -1618,7 +1708,6 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
 
 
 // Helpers of the matrix-core sweeps.
-typedef float f32x4m __attribute__((ext_vector_type(4)));
 constexpr int SP_BQS = SP_NT + 16;   // row stride of sweep3m's LDS carrier table
 template <typename GT> __device__ __forceinline__ float ldg_el(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff);
 template <> __device__ __forceinline__ float ldg_el<float>(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -2518,7 +2607,7 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
     const float (*const rcm0[2])[2] = {ctrl->rc[0], ctrl->rc[1]};
     const float (*const rcm1[2])[2] = {nullptr, nullptr};
     const float wm0[2] = {1.f, 1.f}, wm1[2] = {0.f, 0.f};
-    const CmSrc cs = cm_src<RM>(g, meta, rcm0, wm0, rcm1, wm1);
+    const CmLane<RM> cs = cm_lane<RM>(g, meta, rcm0, wm0, rcm1, wm1);
     constexpr int NLT = TT, NRW = (64 * RW + SP_NT - 1) / SP_NT;
     Staged<NLT> slt;
     slt.load(lt, TB);
@@ -2573,7 +2662,7 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
     s_ec[threadIdx.x] = two_d ? marg_factor(cfx, 1.0 / (g.hs_col * (double)g.rows), gden, kappa, eps) : cfac;
     const float* __restrict__ bql = s_bq + lg * SP_BQS + 64 * wv + li;   // + 4 kc SP_BQS + 16 tc
     const float* __restrict__ ecl = s_ec + 64 * wv + li;                  // + 16 tc
-    alpha_rows<RM, KC>(g, cs, s_ar, nr, s_al);   // ends with a barrier
+    alpha_rows_m<RM, KC>(g, cs, s_ar, nr, s_al);   // ends with a barrier
     const float cM = ctrl->rconst[0], cP = ctrl->rconst[1];
     // the force's sign (maximize) rides on the denominator: f / den = grad / (sign den)
     const float sg = h.maximize ? -1.f : 1.f;
@@ -3264,7 +3353,7 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     const float (*const rcm0[2])[2] = {ctrl->rc[2], ctrl->rc[2]};
     const float (*const rcm1[2])[2] = {nullptr, echo_on ? ctrl->rc[3] : nullptr};
     const float wm0[2] = {1.f, kp}, wm1[2] = {0.f, ke};
-    const CmSrc cs = cm_src<RM>(g, meta, rcm0, wm0, rcm1, wm1);
+    const CmLane<RM> cs = cm_lane<RM>(g, meta, rcm0, wm0, rcm1, wm1);
     constexpr int RW = 2 * RM;
     constexpr int NRW = (64 * RW + SP_NT - 1) / SP_NT;
     Staged<NRW> srw;
@@ -3285,7 +3374,7 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     stage_rows_rest<RM, NRW>(g, rowtab, t.r0, nr, s_rows);
     simp.store(s_imp, TB);
     stage_rest<TT>(s_imp, imp_tab, TB, [](float x) { return x; });
-    alpha_rows<RM, KC>(g, cs, s_rows, nr, s_al);
+    alpha_rows_m<RM, KC>(g, cs, s_rows, nr, s_al);
     const float cQ = ctrl->rconst[2];
     const float cX = kp * ctrl->rconst[2] + (echo_on ? ke * ctrl->rconst[3] : 0.f);
     __syncthreads();
