@@ -70,6 +70,9 @@ constexpr int SP_FN_NT = 512;    // per-step finalize kernels (room for fp64 acc
 // bin and the copy match.  The copies are summed (integers: any order) before
 // the block's global atomics.  LDS is sized for the copies in every mode.
 constexpr int SP_NHIST = 4;
+// Copies of the global histogram (hist[copy][T*B]) that part_reduce's blocks
+// spread their atomics over; the finish kernels read their sum.
+constexpr int SP_HCOPIES = 8;
 
 enum ModeType : int32_t { M_ZERO = 0, M_ADD = 1, M_PROD = 2 };
 
@@ -108,6 +111,8 @@ struct Geom {
     double shrink;                     // 1/sqrt(max(1, 0.7 log2(R + 1))) (cresso_v5.py:362-376)
     double inv_n;                      // 1/n
     int32_t binbytes, bpb, one_d, nblkg;   // nblkg: blocks of the Gram pair-sum kernel
+    int32_t hcopies;                   // copies of the global histogram (SP_HCOPIES when part_reduce adds
+                                       // row groups with atomics, else 1)
 };
 
 struct Offs {
@@ -741,14 +746,18 @@ __device__ __forceinline__ float reservoir_f(float old, float cur, double decay,
 // small merges (64-bin groups x partial rows <= 4096, e.g. C2's 128 bins x
 // 1024 rows) take one bin per block over every row (pr_hist_rows = 0); larger
 // ones blocks of 64 bins x pr_hist_rows partial rows (each wave reads 512
-// contiguous bytes of a row), about 1024 such blocks (8 to 64 rows each:
-// C5's 1024 bins x 4096 rows take 1024 blocks of 64), whose bin strides
-// would otherwise make every load its own cache line.
+// contiguous bytes of a row), whose bin strides would otherwise make every
+// load its own cache line.  A block covers at least 1/64 of the rows (8 to
+// 64 rows: C5's 1024 bins x 4096 rows take 1024 blocks of 64, C4's 128 bins
+// x 4000 rows 128 blocks of 63), so a bin receives at most 64 of the blocks'
+// 64-bit atomic adds, spread over SP_HCOPIES copies of the histogram (same-
+// address atomics from many CUs serialize; the finish kernels add the copies).
 constexpr int PR_HB = 64;
+constexpr int PR_U = 8;   // rows whose loads one part_reduce thread has in flight together
 __host__ __device__ inline int pr_hist_rows(int TB, int nblk) {
     const int ng = (TB + PR_HB - 1) / PR_HB;
     if ((int64_t)ng * nblk <= 4096) return 0;
-    const int r = (int)(((int64_t)nblk * ng) / 1024);
+    const int r = (nblk + 63) / 64;
     return r < 8 ? 8 : (r > 64 ? 64 : r);
 }
 __host__ __device__ inline int pr_hist_blocks(int TB, int nblk) {
@@ -763,9 +772,9 @@ __host__ __device__ inline int pr_hist_blocks(int TB, int nblk) {
 // them merge the matrix-core sweeps' per-block histogram partials
 // (hpart[block][bin], 64-bit fixed point): one bin over every row each, or
 // 64 bins of pr_hist_rows partial rows adding their integer sums into
-// hist[bin] with 64-bit atomics (integer
-// sums: the same in any order).  hist is zero on entry (the finish kernels
-// clear it after reading).
+// copy (row group mod SP_HCOPIES) of hist[bin] with 64-bit atomics (integer
+// sums: the same in any order).  Every copy is zero on entry (the finish
+// kernels clear them after reading).
 __global__ __launch_bounds__(256) void part_reduce_kernel(
     const double* __restrict__ part, int nblk, int VS, double* __restrict__ sums,
     const unsigned long long* __restrict__ hpart, unsigned long long* __restrict__ hist, int TB, Lanes L) {
@@ -774,11 +783,21 @@ __global__ __launch_bounds__(256) void part_reduce_kernel(
     __shared__ unsigned long long s_h[4][PR_HB];
     const int v = blockIdx.x;
     const int hr = pr_hist_rows(TB, nblk);
+    // Each thread issues the loads of PR_U rows before adding any of them (a
+    // loop of one load and one add per row waits one memory latency per row:
+    // 34 us for 4096 rows), and adds them in row order, as one load per
+    // iteration would.
     if (v >= VS && hr == 0) {
         // one bin, every block's row
         const int i = v - VS;
         unsigned long long a = 0ull;
-        for (int b = threadIdx.x; b < nblk; b += 256) a += hpart[(size_t)b * TB + i];
+        for (int b = threadIdx.x; b < nblk; b += 256 * PR_U) {
+            unsigned long long x[PR_U];
+#pragma unroll
+            for (int u = 0; u < PR_U; ++u) x[u] = b + 256 * u < nblk ? hpart[(size_t)(b + 256 * u) * TB + i] : 0ull;
+#pragma unroll
+            for (int u = 0; u < PR_U; ++u) a += x[u];
+        }
         for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
         if ((threadIdx.x & 63) == 0) s_h[threadIdx.x >> 6][0] = a;
         __syncthreads();
@@ -791,17 +810,31 @@ __global__ __launch_bounds__(256) void part_reduce_kernel(
         const int b0 = (hb / ng) * hr, b1 = b0 + hr < nblk ? b0 + hr : nblk;
         unsigned long long a = 0ull;
         if (bin < TB)
-            for (int b = b0 + (int)(threadIdx.x >> 6); b < b1; b += 4) a += hpart[(size_t)b * TB + bin];
+            for (int b = b0 + (int)(threadIdx.x >> 6); b < b1; b += 4 * PR_U) {
+                unsigned long long x[PR_U];
+#pragma unroll
+                for (int u = 0; u < PR_U; ++u) x[u] = b + 4 * u < b1 ? hpart[(size_t)(b + 4 * u) * TB + bin] : 0ull;
+#pragma unroll
+                for (int u = 0; u < PR_U; ++u) a += x[u];
+            }
         s_h[threadIdx.x >> 6][threadIdx.x & (PR_HB - 1)] = a;
         __syncthreads();
         if (threadIdx.x < PR_HB && bin < TB) {
             const unsigned long long t = s_h[0][threadIdx.x] + s_h[1][threadIdx.x] + s_h[2][threadIdx.x] + s_h[3][threadIdx.x];
-            atomicAdd(&hist[bin], t);
+            atomicAdd(&hist[(size_t)((hb / ng) % SP_HCOPIES) * TB + bin], t);
         }
         return;
     }
+    // (+0.0 for the rows past nblk leaves the sum unchanged: a starts at +0.0,
+    // so it is never -0.0)
     double a = 0.0;
-    for (int b = threadIdx.x; b < nblk; b += 256) a += part[(size_t)b * VS + v];
+    for (int b = threadIdx.x; b < nblk; b += 256 * PR_U) {
+        double x[PR_U];
+#pragma unroll
+        for (int u = 0; u < PR_U; ++u) x[u] = b + 256 * u < nblk ? part[(size_t)(b + 256 * u) * VS + v] : 0.0;
+#pragma unroll
+        for (int u = 0; u < PR_U; ++u) a += x[u];
+    }
     a = wave_total_d(a);
     if ((threadIdx.x & 63) == 63) s_w[threadIdx.x >> 6] = a;
     __syncthreads();
@@ -2028,6 +2061,22 @@ __global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
 
 
 
+// Bin i of a merged histogram: the sum of its nc copies (loads issued
+// together), each cleared for the next sweep.
+__device__ __forceinline__ unsigned long long take_hist(unsigned long long* __restrict__ hist, int TB, int i, int nc) {
+    unsigned long long c[SP_HCOPIES];
+#pragma unroll
+    for (int k = 0; k < SP_HCOPIES; ++k) c[k] = k < nc ? hist[(size_t)k * TB + i] : 0ull;
+    unsigned long long v = 0ull;
+#pragma unroll
+    for (int k = 0; k < SP_HCOPIES; ++k) {
+        if (k >= nc) break;
+        v += c[k];
+        hist[(size_t)k * TB + i] = 0ull;
+    }
+    return v;
+}
+
 // ---------------------------------------------------------------------------
 // finalize helpers: one wave, one lane per mode
 // ---------------------------------------------------------------------------
@@ -2136,8 +2185,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
         constexpr unsigned nw1 = SP_FN_NT / 64 - 1;
         for (int i = t1; i < TB; i += n1) {
             const double cnt = (double)counts[i];
-            const float cell = (float)((double)(long long)hist[i] / ctrl->hs_ds / fmax(cnt, 1.0));
-            hist[i] = 0ull;
+            const float cell = (float)((double)(long long)take_hist(hist, TB, i, g.hcopies) / ctrl->hs_ds / fmax(cnt, 1.0));
             float e = st.hash_energy[i];
             e = step <= 1 ? cell : e * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * cell;
             st.hash_energy[i] = e;
@@ -3112,8 +3160,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             const int TB = g.T * g.B;
             for (int i = t1; i < TB; i += n1) {
                 const double cnt = fmax((double)counts[i], 1.0);
-                const float cp = (float)((double)(long long)hist[i] / ctrl->hs_P / cnt);
-                hist[i] = 0ull;
+                const float cp = (float)((double)(long long)take_hist(hist, TB, i, g.hcopies) / ctrl->hs_P / cnt);
                 const float ref = st.hash_refractory[i] * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * fabsf(cp);
                 const float gate = 1.0f / (1.0f + (float)h.refractory_gain * ref);
                 const float im =
