@@ -534,6 +534,8 @@ extern "C" int32_t cresso_drive_update(void* param, int32_t param_dtype, const f
     if (numel < 1) return fail(CRESSO_E_INVALID, "drive update: numel must be positive");
     if (step < 1) return fail(CRESSO_E_INVALID, "drive update: step must be >= 1 (after the increment)");
     if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "drive update: drive_clip must be positive");
+    if (param_dtype != CRESSO_F32 && param_dtype != CRESSO_BF16 && param_dtype != CRESSO_F16)
+        return fail(CRESSO_E_UNSUPPORTED, "drive update: param dtype %d not supported (f32, bf16, f16)", param_dtype);
     int32_t rc = check_ws(workspace, workspace_bytes, 1);
     if (rc != CRESSO_OK) return rc;
     const UnitOffs o = unit_offs(1);
@@ -558,8 +560,8 @@ extern "C" int32_t cresso_drive_update(void* param, int32_t param_dtype, const f
             hipLaunchKernelGGL(un_drive_apply_kernel<__half>, dim3(nb), dim3(UN_NT), 0, s, in, head, (__half*)param,
                                hyper->lr);
             break;
-        default:
-            return fail(CRESSO_E_UNSUPPORTED, "drive update: param dtype %d not supported (f32, bf16, f16)", param_dtype);
+        default:   // rejected above, before any launch
+            break;
     }
     return launched("drive update");
 }

@@ -175,6 +175,22 @@ def test_plan_creation_rejects_bad_descriptors_without_gpu():
     assert b"numel" in lib.cresso_hip_last_error()
 
 
+def test_unit_drive_update_rejects_dtype_before_any_launch():
+    # an unsupported param dtype is refused by the host checks, so the call
+    # returns before touching the (here fake) device pointers or any GPU
+    lib_path = ROOT / "cresso_amd" / "libcresso_hip.so"
+    if not lib_path.exists():
+        pytest.skip("library not built")
+    lib = _native.load()
+    fake = ctypes.c_void_p(1 << 20)
+    h = _native.Hyper()
+    h.drive_clip = 4.0
+    rc = lib.cresso_drive_update(fake, _native.DTYPE_CODE[torch.float64], fake, fake, fake, None, None, fake, fake,
+                                 16, 1, 1, ctypes.byref(h), fake, 1 << 20, None)
+    assert rc == _native.CRESSO_E_UNSUPPORTED
+    assert b"not supported" in lib.cresso_hip_last_error()
+
+
 def test_hash_c_oracle_matches_numpy_oracle():
     so = ROOT / "oracle" / "_build" / "libcresso_hash_oracle.so"
     if not so.exists():
