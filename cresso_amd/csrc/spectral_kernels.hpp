@@ -73,6 +73,9 @@ constexpr int SP_NHIST = 4;
 // Copies of the global histogram (hist[copy][T*B]) that part_reduce's blocks
 // spread their atomics over; the finish kernels read their sum.
 constexpr int SP_HCOPIES = 8;
+// Closed-form hash term with four tables: 6 table pairs x (B / 16) row chunks
+// of co-occurrence counts plus one block of the per-table terms (B <= 256).
+constexpr int SP_HHP_MAX = 6 * 16 + 1;
 
 enum ModeType : int32_t { M_ZERO = 0, M_ADD = 1, M_PROD = 2 };
 
@@ -136,6 +139,8 @@ struct Ctrl {
     float k_rat, k_ths, k_root, k_t, k_pred, k_echo, k_nov, k_hash, gain;
     float de_prev;            // drive_energy before this step (sweep 5 updates the state)
     float fr_prev;            // force_rms before this step (sweep 2 updates the state)
+    int32_t hard_hash, pad_;  // four-table closed form: the hard channel's hash term is on (set by fin3)
+    double hh_part[SP_HHP_MAX];   // four-table closed form: partial sums of sum_i hp_i^2 (hh4_kernel)
 };
 
 // state pointers of one tensor (kernel argument)
@@ -489,13 +494,25 @@ __global__ __launch_bounds__(256) void ws_bins_kernel(Geom g, unsigned char* __r
 
 #endif  // CRESSO_SPECTRAL_WS_KERNELS
 
-// Co-occurrence counts of the two tables' bins, cooc[b0][b1] = #{i : bin0(i) =
-// b0, bin1(i) = b1} (data independent, once per shape).  With them the hash
-// prediction's sum of squares is a closed form over the impulse tables:
-//   sum_i ((imp0[b0] + imp1[b1]) / 2)^2
-//     = (sum_b cnt0 imp0^2 + sum_b cnt1 imp1^2 + 2 sum_{b0,b1} cooc imp0 imp1) / 4.
-// Used when there are two tables of one-byte bins (the sweeps' fast path).
-__host__ __device__ inline bool cooc_closed(const Geom& g) { return g.T == 2 && g.bpb == 1 && g.binbytes == 2; }
+// Co-occurrence counts of the tables' bins, cooc[pair][b][b'] = #{i : bin_t(i)
+// = b, bin_t'(i) = b'} for each table pair t < t' (data independent, once per
+// shape).  With them the hash prediction's sum of squares is a closed form
+// over the impulse tables:
+//   sum_i ((1/T) sum_t imp_t[b_t(i)])^2
+//     = (sum_t sum_b cnt_t imp_t^2 + 2 sum_{t<t'} sum_{b,b'} cooc_tt' imp_t imp_t') / T^2.
+// Used with two or four tables of one-byte bins (the matrix-core sweeps):
+// one pair (fin3 evaluates the form) or six (hh4_kernel, many blocks).
+__host__ __device__ inline bool cooc_closed(const Geom& g) {
+    return (g.T == 2 || g.T == 4) && g.bpb == 1 && g.binbytes == g.T && g.B <= 256;
+}
+__host__ __device__ inline int cooc_pairs(const Geom& g) { return g.T * (g.T - 1) / 2; }
+// tables of pair p of four: (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+__host__ __device__ inline void cooc_pair(int p, int& t0, int& t1) {
+    t0 = p < 3 ? 0 : (p < 5 ? 1 : 2);
+    t1 = p < 3 ? p + 1 : (p < 5 ? p - 1 : 3);
+}
+__host__ __device__ inline int hh4_chunks(const Geom& g) { return (g.B + 15) / 16; }
+__host__ __device__ inline int hh4_blocks(const Geom& g) { return 6 * hh4_chunks(g) + 1; }
 #ifdef CRESSO_SPECTRAL_WS_KERNELS
 constexpr int WS_COOC_LDS = 16384;  // u32 counters privatised per block (B <= 128)
 __global__ __launch_bounds__(256) void ws_cooc_kernel(Geom g, const uint16_t* __restrict__ bins,
@@ -519,6 +536,24 @@ __global__ __launch_bounds__(256) void ws_cooc_kernel(Geom g, const uint16_t* __
     if (priv)
         for (int i = threadIdx.x; i < BB; i += blockDim.x)
             if (s_cnt[i]) atomicAdd(&cooc[i], (unsigned long long)s_cnt[i]);
+}
+
+// Four tables of one-byte bins (packed 32-bit): the six pairs' counts, with
+// 64-bit global atomics (6 x B^2 counters do not fit in LDS).
+__global__ __launch_bounds__(256) void ws_cooc4_kernel(Geom g, const uint32_t* __restrict__ bins,
+                                                       unsigned long long* __restrict__ cooc) {
+    const int64_t BB = (int64_t)g.B * g.B;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < g.n; i += stride) {
+        const uint32_t v = bins[i];
+#pragma unroll
+        for (int p = 0; p < 6; ++p) {
+            int t0, t1;
+            cooc_pair(p, t0, t1);
+            const int b0 = (int)((v >> (8 * t0)) & 0xffu), b1 = (int)((v >> (8 * t1)) & 0xffu);
+            atomicAdd(&cooc[p * BB + (int64_t)b0 * g.B + b1], 1ull);
+        }
+    }
 }
 
 #endif  // CRESSO_SPECTRAL_WS_KERNELS
@@ -3168,10 +3203,10 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
                 st.hash_refractory[i] = ref;
                 st.hash_impulse[i] = im;
                 imp_tab[i] = im;
-                if (c5_closed) s_impv[i] = im;
+                if (c5_closed == 1) s_impv[i] = im;
             }
         }
-        if (c5_closed) {
+        if (c5_closed == 1) {
             waves_sync(&s_sync, SP_FN_NT / 64 - 1);   // s_impv complete
             // the hash prediction's sum of squares over the field,
             // sum_i ((imp0[b0] + imp1[b1]) / 2)^2, in closed form from the bin
@@ -3185,7 +3220,8 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             if ((tid & 63) == 63) s_hhw[(tid >> 6) - 1] = w;
         }
     }
-    if (c5_closed) {
+    if (c5_closed == 2 && tid == 0) ctrl->hard_hash = hard;   // four tables: sweep 4m forms the coefficient
+    if (c5_closed == 1) {
         __syncthreads();
         if (tid == 0) {
             double hh = 0.0;
@@ -3199,6 +3235,45 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
 }
 
 
+
+// ---------------------------------------------------------------------------
+// F3b, four tables: the hash prediction's sum of squares in closed form over
+// the impulse tables fin3 wrote, spread over hh4_blocks(g) blocks: block
+// 16-row chunk c of pair p sums cooc_p[b][b'] * 2 imp_t[b] imp_t'[b'] over its
+// rows (thread b'), the last block sum_t sum_b cnt_t[b] imp_t[b]^2; each block
+// writes its fp64 total to ctrl->hh_part (fixed-order wave and block sums), and
+// every block of sweep 4m adds them in block order.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void hh4_kernel(Geom g, const unsigned long long* __restrict__ cooc,
+                                                  const unsigned long long* __restrict__ counts,
+                                                  const float* __restrict__ imp_tab, Ctrl* __restrict__ ctrl, Lanes L) {
+    imp_tab = lane_at(imp_tab, L); ctrl = lane_at(ctrl, L);
+    __shared__ double s_w[4];
+    const int B = g.B, nc = hh4_chunks(g), j = threadIdx.x;
+    const int b = blockIdx.x;
+    double a = 0.0;
+    if (b < 6 * nc) {
+        int t0, t1;
+        cooc_pair(b / nc, t0, t1);
+        const int r0 = 16 * (b % nc);
+        if (j < B) {
+            const unsigned long long* c = cooc + (size_t)(b / nc) * B * B + (size_t)r0 * B + j;
+            const double w1 = (double)imp_tab[t1 * B + j];
+            unsigned long long cv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) cv[r] = r0 + r < B ? c[(size_t)r * B] : 0ull;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (r0 + r < B) a += (double)cv[r] * (2.0 * (double)imp_tab[t0 * B + r0 + r] * w1);
+        }
+    } else {
+        for (int k = j; k < 4 * B; k += 256) a += (double)counts[k] * ((double)imp_tab[k] * (double)imp_tab[k]);
+    }
+    const double w = wave_total_d(a);
+    if ((j & 63) == 63) s_w[j >> 6] = w;
+    __syncthreads();
+    if (j == 0) ctrl->hh_part[b] = ((s_w[0] + s_w[1]) + s_w[2]) + s_w[3];
+}
 
 // ---------------------------------------------------------------------------
 // S4: drive without the hash term, written over t; sums for the drive energy
@@ -3343,18 +3418,20 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
 // so lane l processes rows 4 (l/16) + r of column l % 16 of each tile, and the
 // elementwise drive math is unchanged.  The loads of the next tile are in
 // flight while a tile is processed.  C5C: the hash term's coefficient c5 is
-// known here (fin3 forms the hash prediction's RMS from the co-occurrence
-// counts), so the full drive is written and sum drive^2 is summed directly;
-// otherwise (sweep4_kernel's form) the drive without the hash term is written
-// and the sums of d^2, d hp and hp^2 go to sweep 5.
+// known here (from the hash prediction's RMS in closed form over the
+// co-occurrence counts: fin3 forms it for two tables; for four, every block
+// adds hh4_kernel's partials and block 0 publishes c5 for sweep 5), so the
+// full drive is written and sum drive^2 is summed directly; otherwise
+// (sweep4_kernel's form) the drive without the hash term is written and the
+// sums of d^2, d hp and hp^2 go to sweep 5.
 // ---------------------------------------------------------------------------
 template <int RM, int KC, int TT, bool C5C>
 __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
-    const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
+    const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
     float* __restrict__ tbuf, double* __restrict__ part, int echo_on, Lanes L, cresso_hyper h, int one_round) {
     ctrl = lane_at(ctrl, L); imp_tab = lane_at(imp_tab, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L);
-    static_assert(!C5C || TT == 2, "closed-form hash term with two tables");
+    static_assert(TT == 2 || TT == 4, "two or four tables of one-byte bins");
     extern __shared__ __align__(16) unsigned char dyn[];
     __shared__ float red[4 * NV4];
     const Tile t = tile_of(g);
@@ -3407,6 +3484,8 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     srw.template load_rows<RM>(g, rowtab, t.r0, nr);
     Staged<TT> simp;
     simp.load(imp_tab, TB);
+    double hhv = 0.0;   // four tables, closed form: hh4_kernel's partial of this thread
+    if constexpr (C5C && TT == 4) hhv = (int)threadIdx.x < hh4_blocks(g) ? ctrl->hh_part[threadIdx.x] : 0.0;
     const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
     float bq[4][KCH];
 #pragma unroll
@@ -3430,7 +3509,20 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     const float k_rat = ctrl->k_rat, k_ths = ctrl->k_ths, k_root = ctrl->k_root, k_t = ctrl->k_t, k_nov = ctrl->k_nov;
     const float k2 = -2.8853900817779268f * iclip;
     const float k2n = -2.8853900817779268f * ctrl->nscale;
-    const float c5 = C5C ? ctrl->k_hash : 0.f;   // set by fin3 (closed-form hash-term RMS)
+    float c5 = 0.f;
+    if constexpr (C5C && TT == 2) c5 = ctrl->k_hash;   // set by fin3 (closed-form hash-term RMS)
+    if constexpr (C5C && TT == 4) {
+        // sum hp^2 = (hh4_kernel's partials, added in block order) / T^2, and
+        // the coefficient as fin3 forms it for two tables
+        __shared__ double s_hh[SP_NT / 64];
+        const double w = wave_total_d(hhv);
+        if (l == 63) s_hh[wv] = w;
+        __syncthreads();
+        const double hh = (((s_hh[0] + s_hh[1]) + s_hh[2]) + s_hh[3]) * (1.0 / 16.0);
+        const float khp = ctrl->srms / fmaxf(sqrtf((float)(hh * g.inv_n) + eps), eps);
+        c5 = (float)(ctrl->hard_hash ? h.hash_drive_mix * (double)khp : 0.0);
+        if (blockIdx.x == 0 && threadIdx.x == 0) ctrl->k_hash = c5;   // for sweep 5 (fin4_values)
+    }
     constexpr float invT = 1.0f / (float)TT;
     float a_dd = 0.f, a_dh = 0.f, a_hh = 0.f;
     auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const float* aP, const float* aX) {
@@ -3897,18 +3989,21 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 0>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, L, h);
     }
-    // with two tables sweep4m writes the full drive: fin3 then forms the hash
-    // term's RMS from the co-occurrence counts, and sweep 5 needs no bins
-    const int c5c = (mf && cooc_closed(g)) ? 1 : 0;
+    // the matrix-core sweep 4 writes the full drive: the hash term's RMS comes
+    // from the co-occurrence counts (two tables: in fin3, c5c = 1; four: in
+    // hh4_kernel's blocks and sweep 4m, c5c = 2), and sweep 5 needs no bins
+    const int c5c = (mf && cooc_closed(g)) ? (g.T == 2 ? 1 : 2) : 0;
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 ? pr_hist_blocks(g.T * g.B, g.nblk) : 0), ny), dim3(256), 0, s,
                        part, g.nblk, NV3, sums, hpart, hist, g.T * g.B, L);
     hipLaunchKernelGGL(fin3_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
                        cooc, step, hash_on, hard, echo_on, c5c, L, h);
-    if (c5c)
+    if (c5c == 2)
+        hipLaunchKernelGGL(hh4_kernel, dim3((unsigned)hh4_blocks(g), ny), dim3(256), 0, s, g, cooc, counts, imp, ctrl, L);
+    if (c5c == 1)
         hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
                            tbuf, part, echo_on, L, h, one_round4);
-    else if (mf && t4)
-        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
+    else if (c5c == 2)
+        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
                            tbuf, part, echo_on, L, h, one_round4);
     else if (fast)
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,

@@ -183,7 +183,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.gram = take(sizeof(double) * 4 * (size_t)g.R * g.R);
     o.gpart = take(sizeof(double) * (size_t)g.nblkg * (4 * (size_t)g.R * g.R + (size_t)g.K * g.K));
     o.counts = take(sizeof(unsigned long long) * (size_t)g.T * g.B);
-    o.cooc = take(cooc_closed(g) ? sizeof(unsigned long long) * (size_t)g.B * g.B : 0);
+    o.cooc = take(cooc_closed(g) ? sizeof(unsigned long long) * (size_t)cooc_pairs(g) * g.B * g.B : 0);
     o.bins = take((size_t)g.binbytes * (size_t)g.n);
     o.tbuf = take(sizeof(float) * (size_t)g.n);
     o.part = take(sizeof(double) * (size_t)NVMAX * std::max(g.nblk, g.nblk1));
@@ -294,11 +294,15 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
     hipLaunchKernelGGL(ws_cmax_kernel, dim3(1), dim3(256), 0, s, at<unsigned long long>(ws, o.counts), TB, g.n,
                        P->bins_off, at<Ctrl>(ws, o.ctrl));
     if (cooc_closed(g)) {
-        const int64_t BB = (int64_t)g.B * g.B;
+        const int64_t BB = (int64_t)cooc_pairs(g) * g.B * g.B;
         hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((BB + 255) / 256)), dim3(256), 0, s,
                            at<unsigned long long>(ws, o.cooc), BB);
-        hipLaunchKernelGGL(ws_cooc_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g,
-                           at<const uint16_t>(ws, o.bins), at<unsigned long long>(ws, o.cooc));
+        if (g.T == 2)
+            hipLaunchKernelGGL(ws_cooc_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g,
+                               at<const uint16_t>(ws, o.bins), at<unsigned long long>(ws, o.cooc));
+        else
+            hipLaunchKernelGGL(ws_cooc4_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g,
+                               at<const uint32_t>(ws, o.bins), at<unsigned long long>(ws, o.cooc));
     }
     e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(s);
