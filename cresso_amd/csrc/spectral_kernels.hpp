@@ -3417,15 +3417,15 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
 //   D[i][j]                          lane l, register r: i = 4 (l / 16) + r, j = l % 16
 // so lane l processes rows 4 (l/16) + r of column l % 16 of each tile, and the
 // elementwise drive math is unchanged.  The loads of the next tile are in
-// flight while a tile is processed.  C5C: the hash term's coefficient c5 is
-// known here (from the hash prediction's RMS in closed form over the
-// co-occurrence counts: fin3 forms it for two tables; for four, every block
-// adds hh4_kernel's partials and block 0 publishes c5 for sweep 5), so the
-// full drive is written and sum drive^2 is summed directly; otherwise
-// (sweep4_kernel's form) the drive without the hash term is written and the
-// sums of d^2, d hp and hp^2 go to sweep 5.
+// flight while a tile is processed.  The hash term's coefficient c5 is known
+// here (from the hash prediction's RMS in closed form over the co-occurrence
+// counts: fin3 forms it for two tables; for four, every block adds
+// hh4_kernel's partials and block 0 publishes c5 for sweep 5), so the full
+// drive is written and sum drive^2 is summed directly (sweep4_kernel instead
+// writes the drive without the hash term and sums d^2, d hp and hp^2 for
+// sweep 5).
 // ---------------------------------------------------------------------------
-template <int RM, int KC, int TT, bool C5C>
+template <int RM, int KC, int TT>
 __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
     const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
@@ -3485,7 +3485,7 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     Staged<TT> simp;
     simp.load(imp_tab, TB);
     double hhv = 0.0;   // four tables, closed form: hh4_kernel's partial of this thread
-    if constexpr (C5C && TT == 4) hhv = (int)threadIdx.x < hh4_blocks(g) ? ctrl->hh_part[threadIdx.x] : 0.0;
+    if constexpr (TT == 4) hhv = (int)threadIdx.x < hh4_blocks(g) ? ctrl->hh_part[threadIdx.x] : 0.0;
     const int64_t colw = (int64_t)t.slab * SP_NT + 64 * wv;
     float bq[4][KCH];
 #pragma unroll
@@ -3510,8 +3510,8 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     const float k2 = -2.8853900817779268f * iclip;
     const float k2n = -2.8853900817779268f * ctrl->nscale;
     float c5 = 0.f;
-    if constexpr (C5C && TT == 2) c5 = ctrl->k_hash;   // set by fin3 (closed-form hash-term RMS)
-    if constexpr (C5C && TT == 4) {
+    if constexpr (TT == 2) c5 = ctrl->k_hash;   // set by fin3 (closed-form hash-term RMS)
+    if constexpr (TT == 4) {
         // sum hp^2 = (hh4_kernel's partials, added in block order) / T^2, and
         // the coefficient as fin3 forms it for two tables
         __shared__ double s_hh[SP_NT / 64];
@@ -3524,7 +3524,7 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
         if (blockIdx.x == 0 && threadIdx.x == 0) ctrl->k_hash = c5;   // for sweep 5 (fin4_values)
     }
     constexpr float invT = 1.0f / (float)TT;
-    float a_dd = 0.f, a_dh = 0.f, a_hh = 0.f;
+    float a_dd = 0.f;
     auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const float* aP, const float* aX) {
         f32x4m pred = {cQ, cQ, cQ, cQ}, mixed = {cX, cX, cX, cX};
 #pragma unroll
@@ -3544,23 +3544,11 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
 #pragma unroll
             for (int tt = 1; tt < TT; ++tt) hp += s_imp[tt * B + bin_byte<TT>(b[r], tt)];
             hp = hp * invT;
-            if constexpr (C5C) {
-                const float d = fmaf(c5, hp, fmaf(k_nov, nov, core + mixed[r]));
-                bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
-                a_dd = fmaf(d, d, a_dd);
-            } else {
-                const float d = fmaf(k_nov, nov, core + mixed[r]);
-                bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
-                a_dd = fmaf(d, d, a_dd);
-                a_dh = fmaf(d, hp, a_dh);
-                a_hh = fmaf(hp, hp, a_hh);
-            }
+            const float d = fmaf(c5, hp, fmaf(k_nov, nov, core + mixed[r]));
+            bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
+            a_dd = fmaf(d, d, a_dd);
         }
         pin1(a_dd);
-        if constexpr (!C5C) {
-            pin1(a_dh);
-            pin1(a_hh);
-        }
         elem_fence();
     };
     auto row_tiles = [&](int tr, const float* x, const uint32_t* b) {
@@ -3583,10 +3571,8 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
         if (tr + 2 < ntr) load_row(tr + 2, xa, ba);
         row_tiles(tr + 1, xb, bb);
     }
-    Partials P{red, 3, NV4};
+    Partials P{red, 1, NV4};   // sum drive^2 (the d hp and hp^2 slots of sweep4_kernel's layout are zero)
     P.add(0, a_dd);
-    P.add(1, a_dh);
-    P.add(2, a_hh);
     P.flush(part);
 }
 
@@ -4000,10 +3986,10 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     if (c5c == 2)
         hipLaunchKernelGGL(hh4_kernel, dim3((unsigned)hh4_blocks(g), ny), dim3(256), 0, s, g, cooc, counts, imp, ctrl, L);
     if (c5c == 1)
-        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
+        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
                            tbuf, part, echo_on, L, h, one_round4);
     else if (c5c == 2)
-        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
+        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
                            tbuf, part, echo_on, L, h, one_round4);
     else if (fast)
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
