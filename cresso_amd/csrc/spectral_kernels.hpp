@@ -3571,7 +3571,7 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
         if (tr + 2 < ntr) load_row(tr + 2, xa, ba);
         row_tiles(tr + 1, xb, bb);
     }
-    Partials P{red, 1, NV4};   // sum drive^2 (the d hp and hp^2 slots of sweep4_kernel's layout are zero)
+    Partials P{red, 1, 1};   // sum drive^2 only: rows of one value (sweep4_kernel's rows hold NV4)
     P.add(0, a_dd);
     P.flush(part);
 }
@@ -3591,15 +3591,17 @@ __device__ void fin4_values(const Geom& g, const double* __restrict__ part, cons
     double acc[NV4] = {0.0, 0.0, 0.0};
     // blocks threadIdx.x + i SP_NT in groups of NG: a group's loads go out
     // together (indices clamped: no branch between them), then are summed in
-    // block order
+    // block order.  With the closed-form hash term sweep 4m writes rows of one
+    // value (sum drive^2), sweep4_kernel rows of NV4.
     constexpr int NG = 8;
+    const int nv = c5_closed ? 1 : NV4;
     for (int b0 = threadIdx.x; b0 < g.nblk; b0 += NG * SP_NT) {
         double pv[NG][NV4];
 #pragma unroll
         for (int i = 0; i < NG; ++i) {
             const int b = b0 + i * SP_NT < g.nblk ? b0 + i * SP_NT : g.nblk - 1;
 #pragma unroll
-            for (int v = 0; v < NV4; ++v) pv[i][v] = part[(size_t)b * NV4 + v];
+            for (int v = 0; v < NV4; ++v) pv[i][v] = v < nv ? part[(size_t)b * nv + v] : 0.0;
         }
 #pragma unroll
         for (int i = 0; i < NG; ++i)
