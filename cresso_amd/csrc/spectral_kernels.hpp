@@ -919,8 +919,8 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(
     float a = 0.f, m = 0.f;   // sum of f^2, max |f|
     const int64_t vend = beg + ((end - beg) & ~(int64_t)3);
     if (V4) {
-        // eight float4 loads per thread in flight per iteration, then the rest one by one
-        constexpr int UN = 8;
+        // sixteen float4 loads per thread in flight per iteration, then the rest one by one
+        constexpr int UN = 16;
         const int64_t st = 4 * (int64_t)SP_NT;
         int64_t e = beg + 4 * (int64_t)threadIdx.x;
         for (; e + (UN - 1) * st < vend; e += UN * st) {
