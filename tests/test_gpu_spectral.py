@@ -211,13 +211,15 @@ def test_spectral_deterministic():
 # the C2 case: rank 4 with 128 bins (co-occurrence counts at the LDS limit),
 # rank 8 with 256 bins (co-occurrence counts by global atomics) and maximize,
 # rank 16 with two tables (closed-form hash term, nine carrier chunks), and
-# four tables at rank 8 and at C5's rank 16 / 256 bins (hash term summed in
-# sweep 4 and added in sweep 5).
+# four tables at rank 8, at 100 bins (not a power of two: a partial last
+# chunk of co-occurrence rows) and at C5's rank 16 / 256 bins (closed-form
+# hash term over the six table pairs).
 FAST_CASES = [
     ("r4_b128", (2048, 4096), dict(lr=2e-3, rank=4, max_frequency=3, hash_bins=128, hash_tables=2)),
     ("r8_b256_max", (2048, 4096), dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=256, hash_tables=2, maximize=True)),
     ("r16_t2_b64", (2048, 4096), dict(lr=2e-3, rank=16, max_frequency=7, hash_bins=64, hash_tables=2)),
     ("r8_t4_b64", (2048, 4096), dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=4)),
+    ("r8_t4_b100", (2048, 4096), dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=100, hash_tables=4)),
     ("r16_t4_b256", (2048, 4096), dict(lr=2e-3, rank=16, max_frequency=7, hash_bins=256, hash_tables=4)),
 ]
 
