@@ -146,8 +146,11 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     // the matrix-core sweeps take panels of 32 or 64 rows that tile the rows
     // exactly: prefer those when the rows allow it, 64 rows from 512 blocks on
     // (measured: (5632,2048) 0.174 -> 0.166 ms a step; (2048,2048), 256 blocks
-    // of 64 rows, 0.098 -> 0.107 ms, so it keeps 32)
-    if (pr >= 16 && g.rows >= 1024 && g.rows % 32 == 0) pr = (pr >= 32 && g.rows % 64 == 0) ? 64 : 32;
+    // of 64 rows, 0.098 -> 0.107 ms, so it keeps 32), and from 256 rows on
+    // (C5's (512,256,3,3) and (256,256,3,3) conv tensors then take the
+    // matrix-core sweeps instead of the general kernels' 16-row panels: C5
+    // 1.32 -> 1.28 ms)
+    if (pr >= 16 && g.rows >= 256 && g.rows % 32 == 0) pr = (pr >= 32 && g.rows % 64 == 0) ? 64 : 32;
     // 32-bit element offsets inside a panel: PR * cols < 2^29
     if (g.cols >= ((int64_t)1 << 29))
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: %lld elements per row exceed this build's panel limit",
