@@ -144,13 +144,14 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     int64_t pr = std::max<int64_t>(16, (g.rows * g.slabs) / 1024);
     pr = std::min<int64_t>(std::min<int64_t>(pr, 64), g.rows);
     // the matrix-core sweeps take panels of 32 or 64 rows that tile the rows
-    // exactly: prefer those when the rows allow it, 64 rows from 512 blocks on
-    // (measured: (5632,2048) 0.174 -> 0.166 ms a step; (2048,2048), 256 blocks
-    // of 64 rows, 0.098 -> 0.107 ms, so it keeps 32), and from 256 rows on
-    // (C5's (512,256,3,3) and (256,256,3,3) conv tensors then take the
-    // matrix-core sweeps instead of the general kernels' 16-row panels: C5
-    // 1.32 -> 1.28 ms)
-    if (pr >= 16 && g.rows >= 256 && g.rows % 32 == 0) pr = (pr >= 32 && g.rows % 64 == 0) ? 64 : 32;
+    // exactly: prefer those from 256 rows on (C5's (512,256,3,3) and
+    // (256,256,3,3) conv tensors then take the matrix-core sweeps instead of
+    // the general kernels' 16-row panels: C5 1.32 -> 1.28 ms), 64 rows when
+    // they tile the rows (measured: (5632,2048) 0.174 -> 0.166 ms a step; a
+    // lone (2048,2048) tensor, 256 blocks of 64 rows, is slower, 0.098 ->
+    // 0.107 ms, but C4's batches of them fill the GPU and gain: 12.2-12.3 ->
+    // 12.0-12.1 ms)
+    if (pr >= 16 && g.rows >= 256 && g.rows % 32 == 0) pr = (g.rows % 64 == 0) ? 64 : 32;
     // 32-bit element offsets inside a panel: PR * cols < 2^29
     if (g.cols >= ((int64_t)1 << 29))
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: %lld elements per row exceed this build's panel limit",
