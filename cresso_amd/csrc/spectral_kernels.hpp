@@ -1931,7 +1931,7 @@ __global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl,
     double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ rowfx,
     unsigned long long* __restrict__ colfx, const double* __restrict__ part1, float* __restrict__ fr_state, int step,
-    Lanes L, cresso_hyper h, int one_round) {
+    Lanes L, cresso_hyper h, int one_round, int hdirect) {
     if (L.dv) {
         const cresso_spectral_desc& d = lane_desc(L);
         grad = (const GT*)d.grad; fr_state = (float*)d.force_rms; step = d.step;
@@ -2085,7 +2085,13 @@ __global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
         unsigned long long v = 0ull;
 #pragma unroll
         for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-        hist[(size_t)blockIdx.x * TB + i] = v;   // this block's partial (hpart[block][bin])
+        if (hdirect) {
+            // multi-round launch: blocks end at different times, so they add
+            // into the SP_HCOPIES histogram copies directly (integer sums)
+            if (v) atomicAdd(&hist[(size_t)(blockIdx.x % SP_HCOPIES) * TB + i], v);
+        } else {
+            hist[(size_t)blockIdx.x * TB + i] = v;   // this block's partial (hpart[block][bin])
+        }
     }
     Partials P{red, 2 + 2 * g.R, NV2};
     P.add(0, aL);
@@ -2630,7 +2636,8 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, const Ctrl* __restrict__ ctrl,
     const float* __restrict__ lt, const unsigned long long* __restrict__ rowfx,
     const unsigned long long* __restrict__ colfx, const float* __restrict__ colfac, float* __restrict__ tbuf,
-    double* __restrict__ part, unsigned long long* __restrict__ hist, Lanes L, cresso_hyper h, int one_round) {
+    double* __restrict__ part, unsigned long long* __restrict__ hist, Lanes L, cresso_hyper h, int one_round,
+    int hdirect) {
     if (L.dv) grad = (const GT*)lane_desc(L).grad;
     ctrl = lane_at(ctrl, L); lt = lane_at(lt, L); rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L);
     colfac = lane_at(colfac, L); tbuf = lane_at(tbuf, L); part = lane_at(part, L); hist = lane_at(hist, L);
@@ -2927,7 +2934,13 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
         unsigned long long v = 0ull;
 #pragma unroll
         for (int c = 0; c < NH; ++c) v += s_hist[i * NH + c];
-        hist[(size_t)blockIdx.x * TB + i] = v;   // this block's partial (hpart[block][bin])
+        if (hdirect) {
+            // multi-round launch: blocks end at different times, so they add
+            // into the SP_HCOPIES histogram copies directly (integer sums)
+            if (v) atomicAdd(&hist[(size_t)(blockIdx.x % SP_HCOPIES) * TB + i], v);
+        } else {
+            hist[(size_t)blockIdx.x * TB + i] = v;   // this block's partial (hpart[block][bin])
+        }
     }
     Partials P{red, 15 + 2 * g.R, NV3};
     const float mm[13] = {m_ee, 0.f, m_t, m_tt, m_rr, m_bb, m_oo, m_rb, m_ro, m_bo, m_tr, m_tb, m_to};
@@ -3936,13 +3949,19 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     const int one_round2 = nb <= cus * occ2m<RM, KC>(), one_round3 = nb <= cus * occ3m<RM, KC>();
     const int one_round4 = nb <= cus * occ4m<RM, KC>();
     const bool m3 = mf && lds_sweep3m<KC>(g, 2 * RM) <= SP_LDS_MAX_M;
+    // histogram merges: per-block partial rows summed by part_reduce, or, in
+    // multi-round launches of plans with histogram copies, atomics of every
+    // block straight into the copies (blocks end at different times; one-round
+    // launches end together and would contend)
+    const int hd2 = (m2 && !one_round2 && g.hcopies == SP_HCOPIES) ? 1 : 0;
+    const int hd3 = (m3 && !one_round3 && g.hcopies == SP_HCOPIES) ? 1 : 0;
     if (m2) {
         if (t4)
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 4>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2);
+                               part, hd2 ? hist : hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2, hd2);
         else
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 2>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2);
+                               part, hd2 ? hist : hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2, hd2);
     } else if (fast) {
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
@@ -3950,7 +3969,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 0>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
     }
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2 + (m2 ? pr_hist_blocks(g.T * g.B, g.nblk) : 0), ny), dim3(256), 0, s,
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2 + (m2 && !hd2 ? pr_hist_blocks(g.T * g.B, g.nblk) : 0), ny), dim3(256), 0, s,
                        part, g.nblk, NV2, sums, hpart, hist, g.T * g.B, L);
     hipLaunchKernelGGL(fin2_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st, ctrl,
                        step, hash_on, hard, L, h);
@@ -3966,10 +3985,10 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
         const size_t l3m = lds_sweep3m<KC>(g, 2 * RM);
         if (t4)
             hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 4>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h, one_round3);
+                               lt, rowfx, colfx, colfac, tbuf, part, hd3 ? hist : hpart, L, h, one_round3, hd3);
         else
             hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 2>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               lt, rowfx, colfx, colfac, tbuf, part, hpart, L, h, one_round3);
+                               lt, rowfx, colfx, colfac, tbuf, part, hd3 ? hist : hpart, L, h, one_round3, hd3);
     } else if (fast) {
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 1>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, L, h);
@@ -3981,7 +4000,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     // from the co-occurrence counts (two tables: in fin3, c5c = 1; four: in
     // hh4_kernel's blocks and sweep 4m, c5c = 2), and sweep 5 needs no bins
     const int c5c = (mf && cooc_closed(g)) ? (g.T == 2 ? 1 : 2) : 0;
-    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 ? pr_hist_blocks(g.T * g.B, g.nblk) : 0), ny), dim3(256), 0, s,
+    hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 && !hd3 ? pr_hist_blocks(g.T * g.B, g.nblk) : 0), ny), dim3(256), 0, s,
                        part, g.nblk, NV3, sums, hpart, hist, g.T * g.B, L);
     hipLaunchKernelGGL(fin3_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
                        cooc, step, hash_on, hard, echo_on, c5c, L, h);
