@@ -114,8 +114,8 @@ struct Geom {
     double shrink;                     // 1/sqrt(max(1, 0.7 log2(R + 1))) (cresso_v5.py:362-376)
     double inv_n;                      // 1/n
     int32_t binbytes, bpb, one_d, nblkg;   // nblkg: blocks of the Gram pair-sum kernel
-    int32_t hcopies;                   // copies of the global histogram (SP_HCOPIES when part_reduce adds
-                                       // row groups with atomics, else 1)
+    int32_t hcopies;                   // copies of the global histogram (SP_HCOPIES for the matrix-core
+                                       // sweeps' atomic merges, else 1)
 };
 
 struct Offs {
@@ -2189,7 +2189,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
     Geom g, const ModeMeta* __restrict__ meta, const double* __restrict__ stats, const double* __restrict__ bounds,
     const double* __restrict__ part, unsigned long long* __restrict__ hist,
     const unsigned long long* __restrict__ counts, float* __restrict__ lt, SpecState st, Ctrl* __restrict__ ctrl,
-    int step, int hash_on, int hard, Lanes L, cresso_hyper h) {
+    int step, int hash_on, int hard, int nc, Lanes L, cresso_hyper h) {
     if (L.dv) {
         st = spec_state(lane_desc(L));
         step = lane_desc(L).step;
@@ -2226,7 +2226,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
         constexpr unsigned nw1 = SP_FN_NT / 64 - 1;
         for (int i = t1; i < TB; i += n1) {
             const double cnt = (double)counts[i];
-            const float cell = (float)((double)(long long)take_hist(hist, TB, i, g.hcopies) / ctrl->hs_ds / fmax(cnt, 1.0));
+            const float cell = (float)((double)(long long)take_hist(hist, TB, i, nc) / ctrl->hs_ds / fmax(cnt, 1.0));
             float e = st.hash_energy[i];
             e = step <= 1 ? cell : e * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * cell;
             st.hash_energy[i] = e;
@@ -3015,7 +3015,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
     Geom g, const ModeMeta* __restrict__ meta, const double* __restrict__ stats, const double* __restrict__ gram,
     const double* __restrict__ part, unsigned long long* __restrict__ hist,
     const unsigned long long* __restrict__ counts, float* __restrict__ imp_tab, SpecState st, Ctrl* __restrict__ ctrl,
-    const unsigned long long* __restrict__ cooc, int step, int hash_on, int hard, int echo_on, int c5_closed, Lanes L,
+    const unsigned long long* __restrict__ cooc, int step, int hash_on, int hard, int echo_on, int c5_closed, int nc, Lanes L,
     cresso_hyper h) {
     if (L.dv) {
         st = spec_state(lane_desc(L));
@@ -3208,7 +3208,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             const int TB = g.T * g.B;
             for (int i = t1; i < TB; i += n1) {
                 const double cnt = fmax((double)counts[i], 1.0);
-                const float cp = (float)((double)(long long)take_hist(hist, TB, i, g.hcopies) / ctrl->hs_P / cnt);
+                const float cp = (float)((double)(long long)take_hist(hist, TB, i, nc) / ctrl->hs_P / cnt);
                 const float ref = st.hash_refractory[i] * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * fabsf(cp);
                 const float gate = 1.0f / (1.0f + (float)h.refractory_gain * ref);
                 const float im =
@@ -3955,6 +3955,10 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     // launches end together and would contend)
     const int hd2 = (m2 && !one_round2 && g.hcopies == SP_HCOPIES) ? 1 : 0;
     const int hd3 = (m3 && !one_round3 && g.hcopies == SP_HCOPIES) ? 1 : 0;
+    // histogram copies the finishes read: all of them after atomic merges
+    // (direct, or part_reduce's row groups), else copy 0 only
+    const int prh = pr_hist_rows(g.T * g.B, g.nblk) > 0;
+    const int nc2 = (hd2 || (m2 && prh)) ? g.hcopies : 1, nc3 = (hd3 || (m3 && prh)) ? g.hcopies : 1;
     if (m2) {
         if (t4)
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 4>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
@@ -3972,7 +3976,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV2 + (m2 && !hd2 ? pr_hist_blocks(g.T * g.B, g.nblk) : 0), ny), dim3(256), 0, s,
                        part, g.nblk, NV2, sums, hpart, hist, g.T * g.B, L);
     hipLaunchKernelGGL(fin2_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, bounds, sums, hist, counts, lt, st, ctrl,
-                       step, hash_on, hard, L, h);
+                       step, hash_on, hard, nc2, L, h);
     if (axes_on && g.ntrail > 1) {
         int64_t nterms = 0;
         for (int a = 0; a < g.ntrail; ++a) nterms += g.tdim[a];
@@ -4003,7 +4007,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     hipLaunchKernelGGL(part_reduce_kernel, dim3(NV3 + (m3 && !hd3 ? pr_hist_blocks(g.T * g.B, g.nblk) : 0), ny), dim3(256), 0, s,
                        part, g.nblk, NV3, sums, hpart, hist, g.T * g.B, L);
     hipLaunchKernelGGL(fin3_kernel, fin, dim3(SP_FN_NT), 0, s, g, meta, stats, gram, sums, hist, counts, imp, st, ctrl,
-                       cooc, step, hash_on, hard, echo_on, c5c, L, h);
+                       cooc, step, hash_on, hard, echo_on, c5c, nc3, L, h);
     if (c5c == 2)
         hipLaunchKernelGGL(hh4_kernel, dim3((unsigned)hh4_blocks(g), ny), dim3(256), 0, s, g, cooc, counts, imp, ctrl, L);
     if (c5c == 1)

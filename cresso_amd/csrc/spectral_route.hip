@@ -160,8 +160,9 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     g.PR = (int32_t)std::max<int64_t>(1, pr);
     g.panels = (int32_t)((g.rows + g.PR - 1) / g.PR);
     g.nblk = g.slabs * g.panels;
-    // part_reduce merges many partial rows of a histogram with atomics spread over copies
-    g.hcopies = pr_hist_rows(g.T * g.B, g.nblk) > 0 ? SP_HCOPIES : 1;
+    // the matrix-core sweeps' histograms: atomic merges (part_reduce's row
+    // groups, or every block of a multi-round launch) spread over copies
+    g.hcopies = mtables(g) ? SP_HCOPIES : 1;
     // Gram pair sums: one block per ~1024 rows/columns of the longer axis, at most 256
     g.nblkg = (int32_t)std::max<int64_t>(1, std::min<int64_t>(256, std::max(g.rows, g.cols) / 1024));
     // flat force-RMS sweep and parameter update: contiguous chunks (multiple of 4 elements) per block
