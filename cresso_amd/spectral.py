@@ -117,7 +117,7 @@ class SpectralEngine:
     READY = True
     LANES = 4                 # side streams of a multi-tensor step
     BATCH = True              # batch same-plan tensors into one launch per kernel
-    BATCH_BYTES = 256 << 20   # per-tensor scratch held by one batch
+    BATCH_BYTES = 512 << 20   # per-tensor scratch held by one batch (C4: 3 % faster than 256 MiB, as fast as 1 GiB)
 
     def __init__(self):
         self.lib = _native.load()
