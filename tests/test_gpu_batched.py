@@ -33,6 +33,11 @@ CASES = [
     ("no_hash", (512, 256), torch.float32, torch.float32, dict(rank=8, max_frequency=5, hash_bins=0, hash_tables=2)),
     ("soft_only", (256, 256), torch.float32, torch.float32,
      dict(rank=8, max_frequency=5, hash_bins=64, hash_tables=2, hard_channel_min_size=1 << 30)),
+    # rank 8, two tables: 32 tensors of C4's (2048,2048) shape are 8192 blocks,
+    # a multi-round batch whose histograms merge with atomics into the eight
+    # copies, while each single step is one round (partial-row merge)
+    ("multiround_r8_t2", (2048, 2048), torch.float32, torch.float32,
+     dict(rank=8, max_frequency=5, hash_bins=64, hash_tables=2), 32),
 ]
 
 COUNT = 5
@@ -105,28 +110,30 @@ def _grad(shape, dtype, gen, scale):
 def test_batched_matches_single(case):
     from cresso_amd.spectral import SpectralEngine
 
-    name, shape, pdt, gdt, kw = case
+    name, shape, pdt, gdt, kw = case[:5]
+    count = case[5] if len(case) > 5 else COUNT
     engine = SpectralEngine()
-    gen = torch.Generator().manual_seed(hash(name) % 1000)
-    p0 = [0.02 * torch.randn(shape, generator=gen) for _ in range(COUNT)]
+    gen = torch.Generator().manual_seed(sum(map(ord, name)) % 1000)
+    p0 = [0.02 * torch.randn(shape, generator=gen) for _ in range(count)]
     ref = [_Side(p, pdt, kw) for p in p0]
     bat = [_Side(p, pdt, kw) for p in p0]
-    scales = [10.0 ** (-4 + 0.5 * i) for i in range(COUNT)]
-    # tensor i starts i steps ahead: the batch holds tensors at different steps
-    for i in range(COUNT):
-        for _ in range(i):
+    scales = [10.0 ** (-4 + 0.5 * (i % COUNT)) for i in range(count)]
+    # tensor i starts i % COUNT steps ahead: the batch holds tensors at different steps
+    for i in range(count):
+        for _ in range(i % COUNT):
             g = _grad(shape, gdt, gen, scales[i])
             _single(engine, ref[i], g)
             _single(engine, bat[i], g)
-    plan = [list(range(COUNT)), list(range(COUNT)), [3, 0, 4], list(range(COUNT))]   # full, full, subset, full
+    full = list(range(count))
+    plan = [full, full, [3, 0, 4], full]   # full, full, subset, full
     for it, sel in enumerate(plan):
-        announce(f"batched {name} {shape} call {it} tensors {sel}")
+        announce(f"batched {name} {shape} x {count} call {it} tensors {len(sel)}")
         gs = [_grad(shape, gdt, gen, scales[i]) for i in sel]
         for i, g in zip(sel, gs):
             _single(engine, ref[i], g)
-        _batched(engine, [bat[i] for i in sel], gs, COUNT)
+        _batched(engine, [bat[i] for i in sel], gs, count)
         torch.cuda.synchronize()
-        for i in range(COUNT):
+        for i in range(count):
             _assert_same(ref[i].snapshot(), bat[i].snapshot(), f"{name} call {it} tensor {i}")
 
 

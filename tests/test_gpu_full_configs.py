@@ -232,3 +232,63 @@ def test_c5_rank16_t4_b256():
 
     announce("C5 bf16 (8192,8192), (512,256,3,3), (256,256,3,3), (64,512,512) x 2 steps, rank 16, T=4, B=256")
     _run_oracle_vectors("c5", bench.make_c5)
+
+
+def _c4_run(params0, grads, kwargs, batch: bool, lanes: int, steps: int):
+    """Step a copy of the C4 params `steps` times with the spectral engine set to
+    (BATCH, LANES); -> (params, optimizer) after the last step."""
+    import cresso_amd
+    from cresso_amd import spectral
+
+    old = (spectral.SpectralEngine.BATCH, spectral.SpectralEngine.LANES)
+    try:
+        spectral.SpectralEngine.BATCH, spectral.SpectralEngine.LANES = batch, lanes
+        ps = [torch.nn.Parameter(p.detach().clone()) for p in params0]
+        opt = cresso_amd.CRESSO5(ps, cuda_ops="required", **kwargs)
+        for k in range(steps):
+            for p, g in zip(ps, grads[k % len(grads)]):
+                p.grad = g
+            opt.step()
+        torch.cuda.synchronize()
+        eng = opt._spectral_engine
+        units = eng._units([eng._prepare(p, p.grad, opt.state[p], opt.param_groups[0]) for p in ps],
+                           [opt.state[p] for p in ps])
+    finally:
+        spectral.SpectralEngine.BATCH, spectral.SpectralEngine.LANES = old
+    return ps, opt, units
+
+
+def test_c4_full_set_as_benched_batched_matches_per_tensor():
+    """C4's 199 tensors (1.2 B fp32 elements) stepped the way bench.py times
+    them -- same-plan tensors in batches of at most BATCH_BYTES of per-tensor
+    scratch over LANES side streams, so the 88 (2048,2048) tensors go out as
+    multi-round batches of about 30 that merge their histograms with atomics --
+    against every tensor stepped on its own on one stream (one-round launches
+    merge with partial rows).  Two steps; params and every state tensor must
+    be bit-identical.  Parity of the per-tensor step itself against the oracle
+    is test_c4_each_shape; the reference steps these tensors one by one
+    (cresso_v5.py:828-844)."""
+    import bench
+    from cresso_amd import spectral
+
+    announce("C4 full 199-tensor set: default batched engine (4 lanes) vs per-tensor steps on one stream, 2 steps")
+    dev = torch.device("cuda:0")
+    params, grads, kwargs, shapes, _ = bench.make_c4(dev, pool=2, on_device=True)
+    a_ps, a_opt, a_units = _c4_run(params, grads, kwargs, True, spectral.SpectralEngine.LANES, 2)
+    biggest = max(len(u[3]) for u in a_units)
+    sq = [len(u[3]) for u in a_units if u[1][1] == (2048, 2048)]
+    announce(f"batched engine: {len(a_units)} units, largest batch {biggest} tensors, (2048,2048) batches {sq}")
+    assert biggest >= 20 and len(sq) >= 2, "the default engine no longer forms multi-round batches"
+    b_ps, b_opt, b_units = _c4_run(params, grads, kwargs, False, 1, 2)
+    assert max(len(u[3]) for u in b_units) == 1
+    del params, grads
+    for i, (a, b) in enumerate(zip(a_ps, b_ps)):
+        what = f"C4 tensor {i} {tuple(a.shape)}"
+        assert torch.equal(a.detach(), b.detach()), f"{what}: param differs"
+        sa, sb = a_opt.state[a], b_opt.state[b]
+        assert set(sa) == set(sb), what
+        for k, v in sa.items():
+            if torch.is_tensor(v):
+                assert torch.equal(v, sb[k]), f"{what}: state {k} differs"
+            else:
+                assert v == sb[k], (what, k)
