@@ -153,6 +153,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     vp, i32, i64, f64 = c.c_void_p, c.c_int32, c.c_int64, c.c_double
     lib.cresso_unit_workspace_bytes.restype = c.c_size_t
     lib.cresso_unit_workspace_bytes.argtypes = [i32]
+    lib.cresso_hash_reduce_mean.restype = i32
+    lib.cresso_hash_reduce_mean.argtypes = [vp, i64, i32, i32, vp, vp, c.c_size_t, vp]
+    lib.cresso_hash_gather.restype = i32
+    lib.cresso_hash_gather.argtypes = [vp, i32, i64, i32, vp, vp]
+    lib.cresso_instant_axis_metric_2d_workspace_bytes.restype = c.c_size_t
+    lib.cresso_instant_axis_metric_2d_workspace_bytes.argtypes = [i64, i64]
+    lib.cresso_instant_axis_metric_2d.restype = i32
+    lib.cresso_instant_axis_metric_2d.argtypes = [vp, i64, i64, f64, f64, f64, vp, vp, c.c_size_t, vp]
     lib.cresso_hash_metric_update_log.restype = i32
     lib.cresso_hash_metric_update_log.argtypes = [vp, i64, vp, i32, i32, i32, f64, f64, f64, f64, vp, vp, c.c_size_t, vp]
     lib.cresso_hash_impulse_update_gather.restype = i32

@@ -1042,13 +1042,27 @@ __device__ F1Values fin1_values(const Geom& g, const F1Part<N>& fp, const double
     const float sc = fmaxf(fr, eps);
     F1Values v;
     v.inv_s = 1.0f / sc;
-    // density histogram scale from this step's largest density: ds = rel^p with
-    // rel = min(|f|/s + eps, 1e4) (margin for the hardware exp2/log2), times
-    // the largest bin count, below 2^62
-    // (fp32 hardware log2 with margins: every block computes the same bound)
+    // Density histogram scale: every bin's sum of ds = rel^p, rel = min(|f|/s
+    // + eps, 1e4), times the scale stays below 2^61 (rounding adds at most
+    // half a unit per element).  A bin's sum is at most the smaller of
+    //   cmax rmax^p                                 (cmax elements, each <= rmax^p)
+    //   sum_i rel_i^p <= rmax^(p-2) S2              (p >= 2)
+    //                 <= n^(1-p/2) S2^(p/2)         (p < 2, power means)
+    // with S2 = sum_i rel_i^2 <= sum f^2/s^2 + 2 eps sqrt(n sum f^2)/s + n eps^2
+    // from sweep 1's sums.  The second bound keeps the resolution of ordinary
+    // bins when a few elements reach rel near 1e4 at a large energy power.
+    // (fp32 hardware log2 with margins for it and for the sweep's exp2/log2 of
+    // rel^p; every block computes the same bound)
     const float rmax = fminf(fmaf((float)mx, v.inv_s, eps), 1.0e4f);
-    const float l2ds = fmaxf((float)h.energy_power * flog2(rmax) + 0.0144f, 0.0f) + 1.01f;  // >= log2(rmax^p 1.01 + 1)
-    v.hs_ds = ldexp(1.0, (int)floorf(62.0f - l2ds - flog2((float)ctrl->cmax) - 0.01f));
+    const float pw = (float)h.energy_power;
+    const float lr = flog2(rmax);
+    const double is = (double)v.inv_s, dn = (double)g.n;
+    const double s2 = (sum * is * is + 2.0 * (double)eps * is * sqrt(dn * sum) + dn * (double)eps * (double)eps) * 1.001;
+    const float l2s = flog2((float)s2 + 1.0e-30f);
+    const float l2tot = pw >= 2.0f ? (pw - 2.0f) * lr + l2s : (1.0f - 0.5f * pw) * flog2((float)dn) + 0.5f * pw * l2s;
+    const float l2bin = pw * lr + flog2((float)ctrl->cmax);
+    const int ex = (int)floorf(61.0f - fminf(l2bin, l2tot) - 0.05f);
+    v.hs_ds = ldexp(1.0, ex < 120 ? ex : 120);   // the scale itself stays a finite fp32 value
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         *fr_state = fr;
         ctrl->scale = sc;

@@ -565,6 +565,15 @@ extern "C" int32_t cresso_spectral_step_noalloc(const cresso_spectral_plan* P, c
     }
     void* ws = g_noalloc_ptr[dev];
     if (g_noalloc_plan[dev] != P->serial) {
+        // the rebuild copies from host memory and synchronizes the stream,
+        // which a stream under graph capture cannot do: refuse before any work
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(reinterpret_cast<hipStream_t>(stream), &cap);
+        if (e != hipSuccess) return hip_fail(e, "spectral route (no-alloc): hipStreamIsCapturing");
+        if (cap != hipStreamCaptureStatusNone)
+            return fail(CRESSO_E_INVALID,
+                        "spectral route (no-alloc): the stream is capturing a graph and this plan's tables are not "
+                        "resident in the device's static scratch; make one uncaptured call with this plan first");
         g_noalloc_plan[dev] = 0;   // tables unknown until the rebuild below succeeds
         const int32_t rc = cresso_spectral_workspace_init(P, ws, need, hyper, stream);
         if (rc != CRESSO_OK) return rc;

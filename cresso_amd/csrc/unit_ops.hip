@@ -1,6 +1,9 @@
 // Unit operations of the spectral route, one entry point each: the pieces that
 // the reference's fused CUDA path exposes as separate ops
 // (cresso_cuda/cresso_cuda.cpp:44-125, kernels in cresso_cuda_kernel.cu):
+//   hash bin mean                     hash_reduce_mean_cuda (cu:1222-1253)
+//   hash gather                       hash_gather_cuda (cu:1255-1276)
+//   2-D instant axis metric           instant_axis_metric_2d_cuda (cu:1766-1827)
 //   hash metric update + log gather   hash_metric_update_log_cuda (cu:1515-1591)
 //   hash impulse update + gather      hash_impulse_update_gather_cuda (cu:1593-1661)
 //   metric oscillator                 metric_update_cuda (cu:1829-1867)
@@ -87,7 +90,10 @@ __global__ __launch_bounds__(UN_NT) void un_absmax_kernel(const float* __restric
 // fixed-point scale: every |x| * scale * n stays below 2^62
 __device__ __forceinline__ double un_scale(const UnitHead* head, int64_t n) {
     const double amax = (double)__uint_as_float(head->maxbits);
-    return ldexp(1.0, (int)floor(62.0 - log2((amax * 1.000001 + 1e-30) * (double)n)) );
+    // at most 2^100: x * scale stays finite in fp32 (and zero for exact zeros)
+    // when every input is zero or tiny
+    const int e = (int)floor(62.0 - log2((amax * 1.000001 + 1e-30) * (double)n));
+    return ldexp(1.0, e < 100 ? e : 100);
 }
 
 // bin sums (fixed point) and counts: LDS per block, then global atomics
@@ -181,6 +187,120 @@ __global__ __launch_bounds__(UN_NT) void un_gather_kernel(const float* __restric
     const int64_t mask = bin_mask(bins);
     for (int64_t i = (int64_t)blockIdx.x * UN_NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * UN_NT)
         out[i] = s_tab[hash_bin((uint64_t)i, hs, bins, mask)];
+}
+
+// bin means of one table (cresso_v5.py:519-526)
+__global__ __launch_bounds__(UN_NT) void un_mean_fin_kernel(const UnitHead* head, int64_t n, int bins,
+                                                            const unsigned long long* __restrict__ hist,
+                                                            const unsigned long long* __restrict__ cnt,
+                                                            float* __restrict__ out) {
+    const double scale = un_scale(head, n);
+    for (int b = blockIdx.x * UN_NT + threadIdx.x; b < bins; b += gridDim.x * UN_NT) out[b] = un_cell(hist, cnt, b, scale);
+}
+
+// out[i] = values[bin(i)] for tables too large for LDS
+__global__ __launch_bounds__(UN_NT) void un_gather_global_kernel(const float* __restrict__ tab, int bins, int salt,
+                                                                 int64_t n, float* __restrict__ out) {
+    const HashSalt hs = hash_salt(salt);
+    const int64_t mask = bin_mask(bins);
+    for (int64_t i = (int64_t)blockIdx.x * UN_NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * UN_NT)
+        out[i] = tab[hash_bin((uint64_t)i, hs, bins, mask)];
+}
+
+// ---------------------------------------------------------------------------
+// 2-D instant axis metric (cresso_v5.py:243-262 for ndim = 2): density
+// min(max(rel, eps)^p, 1e6), its row and column means, each normalized by the
+// mean of its marginal, exp(coupling / (2 p) * (log row term + log col term))
+// clamped to [0.08, 12].  Sums are fp64 in a fixed order (no atomics).
+// ---------------------------------------------------------------------------
+struct AxisOffs {
+    size_t rows, cols, part, glob, total;
+    int chunks;
+};
+inline AxisOffs axis_offs(int64_t rows, int64_t cols) {
+    AxisOffs o;
+    // row chunks of the column pass: about 256 Ki threads in all, at most one per row
+    o.chunks = (int)std::max<int64_t>(1, std::min<int64_t>({rows, 1024, (262144 + cols - 1) / std::max<int64_t>(cols, 1)}));
+    size_t off = 0;
+    auto take = [&](size_t b) { size_t at = off; off = al256u(off + b); return at; };
+    o.rows = take(sizeof(double) * (size_t)std::max<int64_t>(rows, 1));
+    o.cols = take(sizeof(double) * (size_t)std::max<int64_t>(cols, 1));
+    o.part = take(sizeof(double) * (size_t)o.chunks * (size_t)std::max<int64_t>(cols, 1));
+    o.glob = take(sizeof(double) * 2);
+    o.total = off;
+    return o;
+}
+
+__device__ __forceinline__ float am_density(float rel, float p, float eps) {
+    return fminf(powf(fmaxf(rel, eps), p), 1.0e6f);
+}
+
+// one wave per row: the row's density sum in fp64 (lane partials, then the wave total)
+__global__ __launch_bounds__(UN_NT) void am_rows_kernel(const float* __restrict__ rel, int64_t rows, int64_t cols,
+                                                        float p, float eps, double* __restrict__ rsum) {
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = (int64_t)gridDim.x * (UN_NT / 64);
+    for (int64_t r = (int64_t)blockIdx.x * (UN_NT / 64) + (threadIdx.x >> 6); r < rows; r += waves) {
+        const float* x = rel + r * cols;
+        double a = 0.0;
+        for (int64_t j = lane; j < cols; j += 64) a += (double)am_density(x[j], p, eps);
+        a = wave_total_d(a);   // the total lands in lane 63
+        if (lane == 63) rsum[r] = a;
+    }
+}
+
+// column partial sums over row chunks: part[chunk][col]
+__global__ __launch_bounds__(UN_NT) void am_cols_kernel(const float* __restrict__ rel, int64_t rows, int64_t cols,
+                                                        int chunks, float p, float eps, double* __restrict__ part) {
+    const int64_t j = (int64_t)blockIdx.x * UN_NT + threadIdx.x;
+    if (j >= cols) return;
+    const int c = blockIdx.y;
+    const int64_t per = (rows + chunks - 1) / chunks;
+    const int64_t r0 = (int64_t)c * per, r1 = r0 + per < rows ? r0 + per : rows;
+    double a = 0.0;
+    for (int64_t r = r0; r < r1; ++r) a += (double)am_density(rel[r * cols + j], p, eps);
+    part[(size_t)c * cols + j] = a;
+}
+
+__global__ __launch_bounds__(UN_NT) void am_colfin_kernel(const double* __restrict__ part, int64_t cols, int chunks,
+                                                          double* __restrict__ csum) {
+    const int64_t j = (int64_t)blockIdx.x * UN_NT + threadIdx.x;
+    if (j >= cols) return;
+    double a = 0.0;
+    for (int c = 0; c < chunks; ++c) a += part[(size_t)c * cols + j];
+    csum[j] = a;
+}
+
+// means of the row means and of the column means (one block, fixed order)
+__global__ __launch_bounds__(UN_NT) void am_glob_kernel(const double* __restrict__ rsum, const double* __restrict__ csum,
+                                                        int64_t rows, int64_t cols, double* __restrict__ glob) {
+    __shared__ double red[2 * (UN_NT / 64)];
+    double v[2] = {0.0, 0.0};
+    for (int64_t i = threadIdx.x; i < rows; i += UN_NT) v[0] += (double)(float)(rsum[i] / (double)cols);
+    for (int64_t i = threadIdx.x; i < cols; i += UN_NT) v[1] += (double)(float)(csum[i] / (double)rows);
+    block_sum<2>(v, red);
+    if (threadIdx.x == 0) {
+        glob[0] = v[0] / (double)rows;
+        glob[1] = v[1] / (double)cols;
+    }
+}
+
+__global__ __launch_bounds__(UN_NT) void am_apply_kernel(const double* __restrict__ rsum,
+                                                         const double* __restrict__ csum,
+                                                         const double* __restrict__ glob, int64_t rows, int64_t cols,
+                                                         float k, float eps, float* __restrict__ out) {
+    const int64_t n = rows * cols;
+    const float gr = fmaxf((float)glob[0], eps), gc = fmaxf((float)glob[1], eps);
+    for (int64_t i = (int64_t)blockIdx.x * UN_NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * UN_NT) {
+        const int64_t r = i / cols, j = i - r * cols;
+        const float rm = (float)(rsum[r] / (double)cols), cm = (float)(csum[j] / (double)rows);
+        const float lg = logf(fmaxf(rm / gr, eps)) + logf(fmaxf(cm / gc, eps));
+        out[i] = fminf(fmaxf(expf(k * lg), 0.08f), 12.0f);
+    }
+}
+
+__global__ __launch_bounds__(UN_NT) void am_ones_kernel(int64_t n, float* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * UN_NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * UN_NT) out[i] = 1.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -429,6 +549,87 @@ int32_t launched(const char* what) {
 using namespace cresso;
 
 extern "C" size_t cresso_unit_workspace_bytes(int32_t bins) { return unit_offs(bins).total; }
+
+extern "C" int32_t cresso_hash_reduce_mean(const float* x, int64_t numel, int32_t bins, int32_t salt, float* mean_out,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+    if (!x || !mean_out) return fail(CRESSO_E_INVALID, "hash reduce mean: null argument");
+    if (numel < 1) return fail(CRESSO_E_INVALID, "hash reduce mean: numel must be positive");
+    if (bins < 1 || bins > UN_MAXB) return fail(CRESSO_E_INVALID, "hash reduce mean: bins %d outside 1..%d", bins, UN_MAXB);
+    if (salt < 0) return fail(CRESSO_E_INVALID, "hash reduce mean: salt must be >= 0");
+    int32_t rc = check_ws(workspace, workspace_bytes, bins);
+    if (rc != CRESSO_OK) return rc;
+    const UnitOffs o = unit_offs(bins);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    UnitHead* head = wat<UnitHead>(workspace, o.head);
+    unsigned long long* hist = wat<unsigned long long>(workspace, o.hist);
+    unsigned long long* cnt = wat<unsigned long long>(workspace, o.cnt);
+    const int nb = nblocks(numel);
+    hipLaunchKernelGGL(un_clear_kernel, dim3(1), dim3(UN_NT), 0, s, head, hist, cnt, bins);
+    hipLaunchKernelGGL(un_absmax_kernel, dim3(nb), dim3(UN_NT), 0, s, x, numel, head);
+    hipLaunchKernelGGL(un_hist_kernel, dim3(nb), dim3(UN_NT), 0, s, x, numel, bins, salt, head, hist, cnt);
+    hipLaunchKernelGGL(un_mean_fin_kernel, dim3((bins + UN_NT - 1) / UN_NT), dim3(UN_NT), 0, s, head, numel, bins, hist,
+                       cnt, mean_out);
+    return launched("hash reduce mean");
+}
+
+extern "C" int32_t cresso_hash_gather(const float* values, int32_t bins, int64_t numel, int32_t salt, float* out,
+                                      void* stream) {
+    if (!values || !out) return fail(CRESSO_E_INVALID, "hash gather: null argument");
+    if (numel < 1) return fail(CRESSO_E_INVALID, "hash gather: numel must be positive");
+    if (bins < 1) return fail(CRESSO_E_INVALID, "hash gather: values must be non-empty");
+    if (salt < 0) return fail(CRESSO_E_INVALID, "hash gather: salt must be >= 0");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int nb = nblocks(numel);
+    if (bins <= UN_MAXB)
+        hipLaunchKernelGGL(un_gather_kernel, dim3(nb), dim3(UN_NT), 0, s, values, bins, salt, numel, out);
+    else
+        hipLaunchKernelGGL(un_gather_global_kernel, dim3(nb), dim3(UN_NT), 0, s, values, bins, salt, numel, out);
+    return launched("hash gather");
+}
+
+extern "C" size_t cresso_instant_axis_metric_2d_workspace_bytes(int64_t rows, int64_t cols) {
+    return rows > 0 && cols > 0 ? axis_offs(rows, cols).total : 0;
+}
+
+extern "C" int32_t cresso_instant_axis_metric_2d(const float* rel, int64_t rows, int64_t cols, double power,
+                                                 double coupling, double eps, float* out, void* workspace,
+                                                 size_t workspace_bytes, void* stream) {
+    if (!rel || !out) return fail(CRESSO_E_INVALID, "instant axis metric: null argument");
+    if (rows < 1 || cols < 1) return fail(CRESSO_E_INVALID, "instant axis metric: requires a non-empty 2D tensor");
+    if (cols > ((int64_t)1 << 31) || rows > (((int64_t)1 << 46) / cols))
+        return fail(CRESSO_E_INVALID, "instant axis metric: %lld x %lld elements is too large", (long long)rows,
+                    (long long)cols);
+    if (!std::isfinite(power) || !std::isfinite(coupling)) return fail(CRESSO_E_INVALID, "instant axis metric: power and coupling must be finite");
+    if (!(eps > 0.0) || !std::isfinite(eps)) return fail(CRESSO_E_INVALID, "instant axis metric: eps must be positive and finite");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t n = rows * cols;
+    const int nb = nblocks(n);
+    if (coupling == 0.0 || n <= 1) {   // cresso_v5.py:249-250
+        hipLaunchKernelGGL(am_ones_kernel, dim3(nb), dim3(UN_NT), 0, s, n, out);
+        return launched("instant axis metric");
+    }
+    if (!workspace) return fail(CRESSO_E_INVALID, "instant axis metric: null workspace");
+    if ((uintptr_t)workspace % 256 != 0) return fail(CRESSO_E_INVALID, "instant axis metric: workspace must be 256-byte aligned");
+    const AxisOffs o = axis_offs(rows, cols);
+    if (workspace_bytes < o.total)
+        return fail(CRESSO_E_INVALID, "instant axis metric: workspace of %zu bytes is smaller than %zu", workspace_bytes, o.total);
+    const double p = std::max(power, 0.25);
+    double* rsum = wat<double>(workspace, o.rows);
+    double* csum = wat<double>(workspace, o.cols);
+    double* part = wat<double>(workspace, o.part);
+    double* glob = wat<double>(workspace, o.glob);
+    const float fe = (float)eps;
+    const int rb = (int)std::min<int64_t>(4096, (rows + UN_NT / 64 - 1) / (UN_NT / 64));
+    const int cb = (int)((cols + UN_NT - 1) / UN_NT);
+    hipLaunchKernelGGL(am_rows_kernel, dim3(rb), dim3(UN_NT), 0, s, rel, rows, cols, (float)p, fe, rsum);
+    hipLaunchKernelGGL(am_cols_kernel, dim3(cb, o.chunks), dim3(UN_NT), 0, s, rel, rows, cols, o.chunks, (float)p, fe,
+                       part);
+    hipLaunchKernelGGL(am_colfin_kernel, dim3(cb), dim3(UN_NT), 0, s, part, cols, o.chunks, csum);
+    hipLaunchKernelGGL(am_glob_kernel, dim3(1), dim3(UN_NT), 0, s, rsum, csum, rows, cols, glob);
+    hipLaunchKernelGGL(am_apply_kernel, dim3(nb), dim3(UN_NT), 0, s, rsum, csum, glob, rows, cols,
+                       (float)(coupling / (2.0 * p)), fe, out);
+    return launched("instant axis metric");
+}
 
 extern "C" int32_t cresso_hash_metric_update_log(const float* density_source, int64_t numel, float* hash_energy,
                                                  int32_t bins, int32_t salt, int32_t step, double hash_decay,

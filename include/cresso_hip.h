@@ -218,7 +218,15 @@ int32_t cresso_spectral_step_batched(const cresso_spectral_plan* plan, const cre
  * cresso_spectral_workspace_init does, including its one synchronization of
  * `stream`).  All calls on one GPU share the array: calls that overlap (two
  * streams or two host threads) race.  Results are identical to
- * cresso_spectral_step's. */
+ * cresso_spectral_step's.
+ *
+ * Graph capture: a call whose plan's tables are already resident launches
+ * kernels only and may be captured.  A call that would rebuild the tables
+ * returns CRESSO_E_INVALID when `stream` is capturing (the rebuild copies from
+ * host memory and synchronizes).  A captured graph reads the tables of the
+ * plan it was captured with: it is valid only while no no-alloc call with
+ * another plan has run on that GPU since; after one, make an uncaptured call
+ * with the graph's plan before replaying it. */
 #define CRESSO_SPECTRAL_NOALLOC_MAX_BYTES (32u << 20)
 int32_t cresso_spectral_step_noalloc(const cresso_spectral_plan* plan, const cresso_spectral_desc* desc,
                                      const cresso_hyper* hyper, void* stream);
@@ -285,6 +293,33 @@ int32_t cresso_spectral_workspace_reconstruct(const cresso_spectral_plan* plan, 
  * _hash_index_tensor (cresso_v5.py:495-516) bit for bit.
  * ------------------------------------------------------------------------- */
 size_t cresso_unit_workspace_bytes(int32_t bins);
+
+/* Bin means of x [numel] for one hash table (table salt `salt`): the sum of
+ * the elements of each bin divided by max(count, 1), into mean_out [bins]
+ * (cresso_v5.py:519-526).  Replaces hash_reduce_mean_cuda
+ * (cresso_cuda_kernel.cu:1222-1253; binding cresso_cuda.cpp:42).
+ * bins <= 4096, as the reference's op. */
+int32_t cresso_hash_reduce_mean(const float* x, int64_t numel, int32_t bins, int32_t salt, float* mean_out,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* out[i] = values[bin(i)] for i < numel, bin of table salt `salt` over
+ * `bins` = the length of values (cresso_v5.py:1024, 1158).  Replaces
+ * hash_gather_cuda (cresso_cuda_kernel.cu:1255-1276; binding
+ * cresso_cuda.cpp:43).  Needs no workspace. */
+int32_t cresso_hash_gather(const float* values, int32_t bins, int64_t numel, int32_t salt, float* out, void* stream);
+
+/* Instant axis metric of a 2-D field rel [rows][cols] (cresso_v5.py:243-262):
+ * density d = min(max(rel, eps)^p, 1e6) with p = max(power, 0.25); row and
+ * column means of d, each divided by max(mean of its marginal, eps); out =
+ * clamp(exp(coupling / (2 p) * (log max(row term, eps) + log max(col term,
+ * eps))), 0.08, 12); all ones when coupling = 0 or rows * cols = 1.  Replaces
+ * instant_axis_metric_2d_cuda (cresso_cuda_kernel.cu:1766-1827; binding
+ * cresso_cuda.cpp:63).  Sums are fp64 in a fixed order.  The workspace
+ * (256-byte aligned) holds cresso_instant_axis_metric_2d_workspace_bytes(rows,
+ * cols) bytes. */
+size_t cresso_instant_axis_metric_2d_workspace_bytes(int64_t rows, int64_t cols);
+int32_t cresso_instant_axis_metric_2d(const float* rel, int64_t rows, int64_t cols, double power, double coupling,
+                                      double eps, float* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* One hash table's metric (cresso_v5.py:1014-1026): bin means of
  * density_source [numel] (row-major linear index, table salt `salt`), EMA into

@@ -80,6 +80,40 @@ def test_spectral_c2_shape_large_energy_power(power):
     compare([hp], hopt, [op], oopt)
 
 
+def test_spectral_energy_power_4_spike_after_quiet_steps():
+    """energy_power 4 at 4096^2: three quiet steps, then one element at about
+    2000 times the lagging force-RMS reservoir (rel^4 ~ 1.6e13 against ~0.5
+    for ordinary elements).  The density histogram's fixed-point scale takes
+    the tighter of the per-bin bound (cmax rmax^p) and the whole-histogram
+    bound from sweep 1's sum of squares, so the ordinary bins keep their
+    resolution next to the spike's bin (the per-bin bound alone left a quantum
+    of 4 here).  Oracle bin sums in fp64."""
+    import cresso_amd
+    from gpu_util import _PREV
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    announce("spectral 4096x4096 energy_power 4, spike after quiet steps")
+    gen = torch.Generator().manual_seed(23)
+    shape = (4096, 4096)
+    p0 = 0.02 * torch.randn(shape, generator=gen)
+    kw = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2, energy_power=4.0)
+    hp = torch.nn.Parameter(p0.clone().cuda())
+    hopt = cresso_amd.CRESSO5([hp], cuda_ops="required", **kw)
+    op = p0.clone()
+    oopt = OracleCRESSO5([op], hash_accum="fp64", **kw)
+    for k in range(4):
+        g = 1e-3 * torch.randn(shape, generator=gen)
+        if k == 3:
+            g[1234, 567] = 3.0   # ~2000x the reservoir's rms after three quiet steps
+            torch.cuda.synchronize()
+            _PREV[hopt] = ([hp.detach().clone()], [op.clone()])
+        hp.grad = g.cuda()
+        hopt.step()
+        oopt.step([g])
+    torch.cuda.synchronize()
+    compare([hp], hopt, [op], oopt)
+
+
 def test_spectral_bf16_params():
     announce("spectral bf16")
     kw = dict(OPS_KW, lr=1e-3)

@@ -214,3 +214,98 @@ def test_unit_ops_reject_bad_arguments():
     assert b"workspace" in lib.cresso_hip_last_error()
     assert lib.cresso_metric_update(*([_ptr(x)] * 7), 0, 0.1, 0.2, _stream()) == -1
     assert b"rank" in lib.cresso_hip_last_error()
+
+
+@pytest.mark.parametrize("shape,bins,salt,scale", [((250, 200), 64, 0, 1.0), ((129, 77), 37, 3, 1.0),
+                                                   ((50000,), 4096, 1, 1.0), ((3000,), 64, 0, 1e-25),
+                                                   ((3000,), 64, 1, 0.0)])
+def test_hash_reduce_mean(shape, bins, salt, scale):
+    """Bin means (hash_reduce_mean_cuda, cu:1222-1253) against the oracle's fp64
+    scatter-add; also all-zero and ~1e-25 inputs (the fixed-point scale is
+    capped so x * scale stays finite and exact zeros stay zero)."""
+    native, lib = _lib()
+    announce(f"unit hash reduce mean {shape} bins {bins} salt {salt} scale {scale}")
+    gen = torch.Generator().manual_seed(44)
+    n = int(np.prod(shape))
+    x = (torch.randn(shape, generator=gen) * 0.7 + 0.05) * scale
+    idx = O.hash_index(shape, bins, salt)
+    ref = O.hash_reduce_mean(x.reshape(-1), idx.reshape(-1), bins, accum="fp64")
+    out = torch.full((bins,), float("nan"), device="cuda")
+    buf, ws, nb = _ws(lib, bins)
+    native.check(lib.cresso_hash_reduce_mean(_ptr(_dev(x)), n, bins, salt, _ptr(out), ws, nb, _stream()),
+                 "hash reduce mean")
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    assert np.isfinite(got).all()
+    # relative tolerance only: the values may be ~1e-25
+    np.testing.assert_allclose(got, ref.double().numpy(), rtol=1e-5, atol=1e-6 * scale, err_msg="bin means")
+
+
+@pytest.mark.parametrize("scale", [0.0, 1e-25])
+def test_hash_impulse_zero_and_tiny_sources(scale):
+    native, lib = _lib()
+    announce(f"unit hash impulse with port source scale {scale}")
+    gen = torch.Generator().manual_seed(45)
+    shape, bins, salt = (4000,), 64, 1
+    n = shape[0]
+    psrc = torch.randn(shape, generator=gen) * scale
+    ref0 = torch.rand(bins, generator=gen) * 0.3 * max(scale, 1e-30)
+    imp0 = torch.randn(bins, generator=gen) * 0.1 * max(scale, 1e-30)
+    r_ref, i_ref = ref0.clone(), imp0.clone()
+    idx = O.hash_index(shape, bins, salt)
+    got_ref = O.hash_impulse_update_gather(psrc, r_ref, i_ref, idx, bins, H, torch.float32, accum="fp64")
+    r_gpu, i_gpu = ref0.cuda(), imp0.cuda()
+    out = torch.empty(n, device="cuda")
+    buf, ws, nb = _ws(lib, bins)
+    native.check(lib.cresso_hash_impulse_update_gather(_ptr(_dev(psrc)), n, _ptr(r_gpu), _ptr(i_gpu), bins, salt,
+                                                       H["hash_decay"], H["hash_impulse_decay"],
+                                                       H["refractory_gain"], _ptr(out), ws, nb, _stream()),
+                 "hash impulse")
+    torch.cuda.synchronize()
+    tol = dict(rtol=1e-5, atol=1e-6 * scale)
+    for got, exp, what in ((r_gpu, r_ref, "hash_refractory"), (i_gpu, i_ref, "hash_impulse"),
+                           (out, got_ref.reshape(-1), "retrieved")):
+        g = got.double().cpu().numpy()
+        assert np.isfinite(g).all(), what
+        np.testing.assert_allclose(g, exp.double().numpy(), **tol, err_msg=what)
+
+
+@pytest.mark.parametrize("bins,salt", [(64, 0), (37, 2), (5000, 1)])
+def test_hash_gather(bins, salt):
+    """hash_gather_cuda (cu:1255-1276): out[i] = values[bin(i)], exact."""
+    native, lib = _lib()
+    announce(f"unit hash gather bins {bins} salt {salt}")
+    gen = torch.Generator().manual_seed(46)
+    shape = (123, 457)
+    n = int(np.prod(shape))
+    vals = torch.randn(bins, generator=gen)
+    idx = O.hash_index(shape, bins, salt).reshape(-1)
+    out = torch.empty(n, device="cuda")
+    native.check(lib.cresso_hash_gather(_ptr(_dev(vals)), bins, n, salt, _ptr(out), _stream()), "hash gather")
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), vals[idx])
+
+
+@pytest.mark.parametrize("shape,power,coupling,lo,hi", [((300, 257), 1.0, 0.55, 1e-3, 5.0),
+                                                        ((64, 4096), 1.7, 0.55, 1e-9, 2e4),
+                                                        ((5000, 3), 0.1, 1.3, 0.0, 3.0),
+                                                        ((17, 19), 1.0, 0.0, 0.0, 1.0),
+                                                        ((1, 1), 1.0, 0.55, 0.5, 0.5)])
+def test_instant_axis_metric_2d(shape, power, coupling, lo, hi):
+    """instant_axis_metric_2d_cuda (cu:1766-1827) against the oracle's
+    instant_axis_metric (cresso_v5.py:243-262), fp32 tolerance; densities
+    clamped at 1e6 and power below the 0.25 floor included."""
+    native, lib = _lib()
+    announce(f"unit instant axis metric 2d {shape} power {power} coupling {coupling}")
+    gen = torch.Generator().manual_seed(47)
+    rel = lo + (hi - lo) * torch.rand(shape, generator=gen) ** 3
+    ref = O.instant_axis_metric(rel, power, coupling, H["eps"])
+    rows, cols = shape
+    nbytes = int(lib.cresso_instant_axis_metric_2d_workspace_bytes(rows, cols))
+    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device="cuda")
+    ws = ctypes.c_void_p(buf.data_ptr() + (-buf.data_ptr()) % 256)
+    out = torch.full(shape, float("nan"), device="cuda")
+    native.check(lib.cresso_instant_axis_metric_2d(_ptr(_dev(rel)), rows, cols, power, coupling, H["eps"], _ptr(out),
+                                                   ws, nbytes, _stream()), "instant axis metric")
+    torch.cuda.synchronize()
+    _close(out, ref, "instant axis metric")

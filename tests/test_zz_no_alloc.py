@@ -112,3 +112,66 @@ def test_spectral_noalloc_rejects_oversized_plan():
         assert b"static scratch" in lib.cresso_hip_last_error()
     finally:
         lib.cresso_spectral_plan_destroy(ctypes.c_void_p(plan))
+
+
+def _noalloc_call(engine, side: _Side, d, stream: int) -> int:
+    from cresso_amd import _native
+
+    key, rank, _ = engine._prepare(side.p, side.p.grad, side.st, side.group)
+    ws = engine._workspace(key, 0, rank, side.group)
+    hyper = _native.hyper_from_group(side.group)
+    return engine.lib.cresso_spectral_step_noalloc(ws.plan, ctypes.byref(d), ctypes.byref(hyper),
+                                                   ctypes.c_void_p(stream))
+
+
+def test_spectral_noalloc_graph_capture_and_plan_switch():
+    """With its plan's tables resident, a no-alloc call launches kernels only:
+    captured into a graph and replayed three times (eager work and a
+    synchronization between the replays), it matches three eager calls with
+    the same descriptor bit for bit.  After a call with another plan, a call
+    that would rebuild the tables is refused while the stream captures."""
+    from cresso_amd import _native
+    from cresso_amd.spectral import SpectralEngine
+
+    engine = SpectralEngine()
+    gen = torch.Generator().manual_seed(22)
+    shape, other = (512, 384), (256, 320)
+    p0 = 0.02 * torch.randn(shape, generator=gen)
+    eager, graph = _Side(p0), _Side(p0)
+    g = (1e-3 * torch.randn(shape, generator=gen)).cuda()
+    eager.p.grad = g
+    graph.p.grad = g
+    # one uncaptured call per side makes the plan's tables resident
+    for side in (eager, graph):
+        _step(engine, side, g, noalloc=True)
+    torch.cuda.synchronize()
+    de = engine._prepare(eager.p, g, eager.st, eager.group)[2]
+    dg = engine._prepare(graph.p, g, graph.st, graph.group)[2]
+    announce("noalloc spectral: capture a resident-plan call")
+    cap = torch.cuda.Stream()
+    hg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(hg, stream=cap):
+        rc = _noalloc_call(engine, graph, dg, int(cap.cuda_stream))
+    assert rc == 0, _native.load().cresso_hip_last_error()
+    for k in range(3):
+        announce(f"noalloc spectral: replay {k}")
+        _native.check(_noalloc_call(engine, eager, de, _native.stream_handle(eager.p.device)), "eager no-alloc")
+        hg.replay()
+        torch.cuda.synchronize()
+        x = torch.randn(1000, device="cuda").sum()   # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.isfinite(x)
+        _assert_same(eager.snapshot(), graph.snapshot(), f"replay {k}")
+    # another plan's call rebuilds the static tables; a capture with the first plan is then refused
+    announce("noalloc spectral: plan switch, then a capture that would rebuild")
+    q0 = 0.02 * torch.randn(other, generator=gen)
+    side_b = _Side(q0)
+    _step(engine, side_b, (1e-3 * torch.randn(other, generator=gen)).cuda(), noalloc=True)
+    torch.cuda.synchronize()
+    hg2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(hg2, stream=cap):
+        rc = _noalloc_call(engine, graph, dg, int(cap.cuda_stream))
+    assert rc == _native.CRESSO_E_INVALID
+    assert b"capturing" in _native.load().cresso_hip_last_error()
+    del hg2
+    torch.cuda.synchronize()
