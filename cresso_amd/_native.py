@@ -120,6 +120,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cresso_spectral_plan_create.restype = c.c_void_p
     lib.cresso_spectral_plan_create.argtypes = [c.POINTER(c.c_int64), c.c_int32, c.POINTER(c.c_int64), c.c_int32,
                                                 c.c_int32, c.c_int32]
+    lib.cresso_spectral_plan_create_ex.restype = c.c_void_p
+    lib.cresso_spectral_plan_create_ex.argtypes = [c.POINTER(c.c_int64), c.c_int32, c.POINTER(c.c_int64), c.c_int32,
+                                                   c.c_int32, c.c_int32, c.c_int32]
     lib.cresso_spectral_plan_destroy.restype = None
     lib.cresso_spectral_plan_destroy.argtypes = [c.c_void_p]
     lib.cresso_spectral_workspace_bytes.restype = c.c_size_t

@@ -120,8 +120,26 @@ struct Geom {
 
 struct Offs {
     size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins;   // shape tables
-    size_t tbuf, part, part1, sums, hist, hpart, lt, imp, rowfx, colfx, colfac, terms, ctrl, desc, shadow;   // per-step scratch
+    size_t tbuf, part, part1, sums, hist, hpart, lt, imp, rowfx, colfx, colfac, terms, ctrl, desc;   // per-step scratch
     size_t total;
+};
+
+// fp64 constants of one (mode, axis) of the carrier, as the reference's fp64
+// work dtype evaluates its Python scalars (cresso_v5.py:272-348)
+struct AxisConst64 {
+    double pf;    // pi * f
+    double pcm;   // (pi * c) * max(1, f) (chirp kinds)
+    double mu;    // center (kind 3)
+    double sig;   // width  (kind 3)
+    int32_t f, kind;
+};
+
+// Workspace regions of a plan with the fp64 work dtype (spectral_f64.hip),
+// after the fp32 layout (whose bins, counts and bin-count maximum it shares).
+struct Offs64 {
+    size_t axc, tab, nst, sums, part, hist, lt, marg, terms, ctrl, tbuf;
+    int32_t nblk;   // blocks of the element sweeps
+    int64_t sumd;   // sum of the dims (axis-table length per mode)
 };
 
 // per-step device scalars (written by finalize kernels)
@@ -3856,6 +3874,9 @@ struct cresso_spectral_plan {
     int32_t rmax;
     int32_t bins_off;   // hash_bins == 0: no bin tables (bins/counts hold a dummy single bin)
     uint64_t serial;    // unique per created plan (never reused): names the tables a workspace holds
+    int32_t work;       // CRESSO_F32: the fp32 work dtype (fp32/bf16/fp16 params); CRESSO_F64: fp64 params
+    cresso::Offs64 o64; // work == CRESSO_F64: the fp64 regions
+    std::vector<cresso::AxisConst64> axc64;
 };
 
 namespace cresso {
@@ -4074,6 +4095,13 @@ int32_t spectral_run(const cresso_spectral_plan& P, const cresso_spectral_desc* 
 // its own translation unit (spectral_step_<pt>_<gt>.hip) so they compile in
 // parallel.  The carrier-count variant (rank and distinct column carriers
 // fixed at compile time) is chosen inside.
+// fp64 work dtype (spectral_f64.hip): the plan's fp64 regions after `off`
+// (-> the new end), their set-up, and one step of an fp64 tensor
+size_t plan_f64_layout(cresso_spectral_plan& P, size_t off);
+int32_t workspace_init_f64(const cresso_spectral_plan& P, void* ws, hipStream_t s);
+int32_t spectral_run_f64(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws, const cresso_hyper& h,
+                         hipStream_t s);
+
 typedef int32_t (*SpectralRunFn)(const cresso_spectral_plan&, const cresso_spectral_desc*, int,
                                  const cresso_spectral_desc*, size_t, void*, const cresso_hyper&, hipStream_t);
 #define CRESSO_SP_DECL(NAME)                                                                                      \
@@ -4084,7 +4112,6 @@ CRESSO_SP_DECL(spectral_run_bf16_bf16)
 CRESSO_SP_DECL(spectral_run_f16_f16)
 CRESSO_SP_DECL(spectral_run_f32_bf16)
 CRESSO_SP_DECL(spectral_run_f32_f16)
-CRESSO_SP_DECL(spectral_run_f64_f64)
 #undef CRESSO_SP_DECL
 
 }  // namespace cresso

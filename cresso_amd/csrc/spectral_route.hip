@@ -29,8 +29,11 @@ double hash_unit_host(int64_t n, int64_t salt) {
 size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, int32_t rank, int32_t bins,
-                      int32_t tables, cresso_spectral_plan& P) {
+                      int32_t tables, int32_t work, cresso_spectral_plan& P) {
     if (ndim < 1 || ndim > 8) return fail(CRESSO_E_INVALID, "spectral route: ndim %d outside 1..8", ndim);
+    if (work != CRESSO_F32 && work != CRESSO_F64)
+        return fail(CRESSO_E_INVALID, "spectral route: work dtype %d is neither CRESSO_F32 nor CRESSO_F64", work);
+    P.work = work;
     if (rank < 1 || rank > SP_MAXR)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: rank %d outside 1..%d supported by this build", rank, SP_MAXR);
     if (bins < 0 || tables < 1 || tables > SP_MAXT)
@@ -80,6 +83,21 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
             c.sig = (float)(0.18 + 0.20 * hash_unit_host(r, 151 + a));
         }
     }
+    // the same constants in fp64 for the fp64 work dtype (math.pi * f, (math.pi * c) * max(1, f))
+    P.axc64.clear();
+    if (work == CRESSO_F64)
+        for (int r = 0; r < rank; ++r)
+            for (int a = 0; a < ndim; ++a) {
+                const int64_t f = freqs[(size_t)r * ndim + a];
+                AxisConst64 c;
+                c.pf = M_PI * (double)f;
+                c.pcm = (M_PI * (0.25 + 1.75 * hash_unit_host(r, 17 + a))) * (double)std::max<int64_t>(1, f);
+                c.mu = 0.15 + 0.70 * hash_unit_host(r, 101 + a);
+                c.sig = 0.18 + 0.20 * hash_unit_host(r, 151 + a);
+                c.f = (int32_t)f;
+                c.kind = r % 4;
+                P.axc64.push_back(c);
+            }
     // distinct column carriers: k = 0 is the constant 1; a mode's column pair
     // is identified symbolically by its column-group parameters
     P.csrc.clear();
@@ -207,9 +225,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.terms = take(sizeof(float) * (size_t)std::max<int64_t>(1, sum_trail));
     o.ctrl = take(sizeof(Ctrl));
     o.desc = take(sizeof(cresso_spectral_desc));   // the tensor's descriptor in a batched step
-    // fp32 copy of an fp64 param's state (4 scalars, 12 rank vectors, 3 hash tables)
-    o.shadow = take(sizeof(float) * (4 + 12 * (size_t)g.R + 3 * (size_t)g.T * g.B));
-    o.total = off;
+    o.total = work == CRESSO_F64 ? plan_f64_layout(P, off) : off;
     return CRESSO_OK;
 }
 
@@ -240,20 +256,26 @@ __global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
 
 using namespace cresso;
 
-extern "C" cresso_spectral_plan* cresso_spectral_plan_create(const int64_t* shape, int32_t ndim, const int64_t* freqs,
-                                                             int32_t rank, int32_t hash_bins, int32_t hash_tables) {
+extern "C" cresso_spectral_plan* cresso_spectral_plan_create_ex(const int64_t* shape, int32_t ndim,
+                                                                const int64_t* freqs, int32_t rank, int32_t hash_bins,
+                                                                int32_t hash_tables, int32_t work_dtype) {
     if (!shape || !freqs) {
         fail(CRESSO_E_INVALID, "spectral route: null shape or freqs");
         return nullptr;
     }
     static std::atomic<uint64_t> next_serial{1};
     cresso_spectral_plan* P = new cresso_spectral_plan();
-    if (plan_spectral(shape, ndim, freqs, rank, hash_bins, hash_tables, *P) != CRESSO_OK) {
+    if (plan_spectral(shape, ndim, freqs, rank, hash_bins, hash_tables, work_dtype, *P) != CRESSO_OK) {
         delete P;
         return nullptr;
     }
     P->serial = next_serial.fetch_add(1);
     return P;
+}
+
+extern "C" cresso_spectral_plan* cresso_spectral_plan_create(const int64_t* shape, int32_t ndim, const int64_t* freqs,
+                                                             int32_t rank, int32_t hash_bins, int32_t hash_tables) {
+    return cresso_spectral_plan_create_ex(shape, ndim, freqs, rank, hash_bins, hash_tables, CRESSO_F32);
 }
 
 extern "C" void cresso_spectral_plan_destroy(cresso_spectral_plan* P) { delete P; }
@@ -310,7 +332,12 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
                                at<const uint32_t>(ws, o.bins), at<unsigned long long>(ws, o.cooc));
     }
     e = hipGetLastError();
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "spectral route: workspace init");
+    if (P->work == CRESSO_F64) {
+        const int32_t rc = workspace_init_f64(*P, ws, s);
+        if (rc != CRESSO_OK) return rc;
+    }
+    e = hipStreamSynchronize(s);
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: workspace init");
 }
 
@@ -338,7 +365,6 @@ SpectralRunFn find_run(int pt, int gt) {
         {CRESSO_F16, CRESSO_F16, spectral_run_f16_f16},
         {CRESSO_F32, CRESSO_BF16, spectral_run_f32_bf16},
         {CRESSO_F32, CRESSO_F16, spectral_run_f32_f16},
-        {CRESSO_F64, CRESSO_F64, spectral_run_f64_f64},
     };
     for (const auto& e : table)
         if (e.pt == pt && e.gt == gt) return e.fn;
@@ -380,67 +406,6 @@ __global__ __launch_bounds__(256) void ws_lanes_kernel(unsigned char* __restrict
 }
 static_assert(sizeof(Ctrl) % 8 == 0, "control block copied as 64-bit words");
 
-// fp64 params keep fp64 state (the reference's state dtype follows the work
-// dtype, cresso_v5.py:119-124).  The step's finishes read and write fp32
-// state: the state goes through an fp32 copy in the workspace, converted
-// before and after the step's kernels on the same stream.
-constexpr int XFER_MAX = 19;
-struct StateXfer {
-    const void* src[XFER_MAX];
-    void* dst[XFER_MAX];
-    int32_t n[XFER_MAX];
-    int32_t count, to_f32;
-};
-__global__ __launch_bounds__(256) void state_xfer_kernel(StateXfer x) {
-    for (int a = 0; a < x.count; ++a)
-        for (int i = threadIdx.x; i < x.n[a]; i += blockDim.x) {
-            if (x.to_f32)
-                reinterpret_cast<float*>(x.dst[a])[i] = (float)reinterpret_cast<const double*>(x.src[a])[i];
-            else
-                reinterpret_cast<double*>(x.dst[a])[i] = (double)reinterpret_cast<const float*>(x.src[a])[i];
-        }
-}
-
-// The descriptor of the step on the fp32 copy (state pointers into the
-// workspace's shadow) and the two transfers (in: every state array; out:
-// every array but the constant omega).
-void shadow_state(const cresso_spectral_plan* P, const cresso_spectral_desc& d, void* ws, cresso_spectral_desc& sd,
-                  StateXfer& in, StateXfer& out) {
-    const Geom& g = P->g;
-    sd = d;
-    float* sh = at<float>(ws, P->o.shadow);
-    std::memset(&in, 0, sizeof(in));
-    std::memset(&out, 0, sizeof(out));
-    in.to_f32 = 1;
-    out.to_f32 = 0;
-    auto add = [&](void*& field, int n, bool writes) {
-        if (!field) return;
-        in.src[in.count] = field;
-        in.dst[in.count] = sh;
-        in.n[in.count++] = n;
-        if (writes) {
-            out.src[out.count] = sh;
-            out.dst[out.count] = field;
-            out.n[out.count++] = n;
-        }
-        field = sh;
-        sh += n;
-    };
-    const int R = g.R, TB = g.T * g.B;
-    add(sd.force_rms, 1, true);
-    add(sd.drive_energy, 1, true);
-    add(sd.surprise, 1, true);
-    add(sd.action, 1, true);
-    void* om = const_cast<void*>(sd.omega);
-    add(om, R, false);
-    sd.omega = om;
-    void** vecs[] = {&sd.q_cos, &sd.q_sin, &sd.p_cos, &sd.p_sin, &sd.metric_cos, &sd.metric_sin, &sd.metric_p_cos,
-                     &sd.metric_p_sin, &sd.calcium_cos, &sd.calcium_sin, &sd.mode_confidence};
-    for (void** v : vecs) add(*v, R, true);
-    add(sd.hash_energy, TB, true);
-    add(sd.hash_impulse, TB, true);
-    add(sd.hash_refractory, TB, true);
-}
 }  // namespace
 
 extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cresso_spectral_desc* d, void* ws,
@@ -450,29 +415,28 @@ extern "C" int32_t cresso_spectral_step(const cresso_spectral_plan* P, const cre
     const int32_t rc = check_desc(P, d);
     if (rc != CRESSO_OK) return rc;
     if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "spectral route: drive_clip must be positive");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (d->param_dtype == CRESSO_F64 || P->work == CRESSO_F64) {
+        if (d->param_dtype != CRESSO_F64 || d->grad_dtype != CRESSO_F64 || P->work != CRESSO_F64)
+            return fail(CRESSO_E_INVALID, "spectral route: fp64 params and grads need a plan with the fp64 work dtype "
+                        "(cresso_spectral_plan_create_ex(..., CRESSO_F64)), and such a plan steps fp64 tensors only");
+        return spectral_run_f64(*P, *d, ws, *hyper, s);
+    }
     const SpectralRunFn fn = find_run(d->param_dtype, d->grad_dtype);
     if (!fn) return CRESSO_E_UNSUPPORTED;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (d->param_dtype != CRESSO_F64) return fn(*P, d, 1, nullptr, 0, ws, *hyper, s);
-    cresso_spectral_desc sd;
-    StateXfer in, out;
-    shadow_state(P, *d, ws, sd, in, out);
-    hipLaunchKernelGGL(state_xfer_kernel, dim3(1), dim3(256), 0, s, in);
-    const int32_t r = fn(*P, &sd, 1, nullptr, 0, ws, *hyper, s);
-    if (r != CRESSO_OK) return r;
-    hipLaunchKernelGGL(state_xfer_kernel, dim3(1), dim3(256), 0, s, out);
-    const hipError_t e = hipGetLastError();
-    return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: fp64 state transfer");
+    return fn(*P, d, 1, nullptr, 0, ws, *hyper, s);
 }
 
 extern "C" size_t cresso_spectral_batched_workspace_bytes(const cresso_spectral_plan* P, int32_t count) {
-    return P && count >= 1 ? batched_bytes(P, count) : 0;
+    return P && count >= 1 && P->work == CRESSO_F32 ? batched_bytes(P, count) : 0;
 }
 
 extern "C" int32_t cresso_spectral_batched_workspace_init(const cresso_spectral_plan* P, int32_t count, void* ws,
                                                           size_t ws_bytes, const cresso_hyper* hyper, void* stream) {
     if (!P || !ws || !hyper) return fail(CRESSO_E_INVALID, "spectral route: null argument");
     if (count < 1) return fail(CRESSO_E_INVALID, "spectral route: batch of %d tensors", count);
+    if (P->work != CRESSO_F32)
+        return fail(CRESSO_E_UNSUPPORTED, "spectral route: fp64 plans step one tensor at a time (cresso_spectral_step)");
     if (ws_bytes < batched_bytes(P, count))
         return fail(CRESSO_E_INVALID, "spectral route: batched workspace of %zu bytes is smaller than %zu", ws_bytes,
                     batched_bytes(P, count));
@@ -496,7 +460,7 @@ extern "C" int32_t cresso_spectral_step_batched(const cresso_spectral_plan* P, c
         return fail(CRESSO_E_INVALID, "spectral route: batched workspace too small for %d tensors", count);
     if (!(hyper->drive_clip > 0.0)) return fail(CRESSO_E_INVALID, "spectral route: drive_clip must be positive");
     const cresso_spectral_desc& d0 = descs[0];
-    if (d0.param_dtype == CRESSO_F64)
+    if (d0.param_dtype == CRESSO_F64 || P->work != CRESSO_F32)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: fp64 params step one tensor at a time (cresso_spectral_step)");
     for (int i = 0; i < count; ++i) {
         const cresso_spectral_desc& d = descs[i];

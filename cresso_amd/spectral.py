@@ -35,9 +35,9 @@ import torch
 from . import _native
 
 # (param dtype, grad dtype) pairs of the library's spectral step; the force is
-# the grad converted to the work dtype (fp32), as in cresso_v5.py:907-912.
-# fp64 params keep fp64 state (cresso_v5.py:119-124); the library steps them
-# in fp32 with the update added in fp64.
+# the grad converted to the work dtype, as in cresso_v5.py:907-912: fp32 for
+# fp32/bf16/fp16 params, fp64 for fp64 params, whose state is fp64 too and
+# whose plans carry the fp64 work dtype (cresso_v5.py:119-124).
 _DTYPE_PAIRS = {(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
                 (torch.float32, torch.bfloat16), (torch.float32, torch.float16), (torch.float64, torch.float64)}
 
@@ -73,13 +73,13 @@ class _Workspace:
     batches of up to `count` tensors."""
 
     def __init__(self, lib, shape, freqs_host: Tuple[int, ...], rank: int, bins: int, tables: int, group: dict,
-                 device: torch.device, count=None):
+                 device: torch.device, count=None, work: int = _native.F32):
         self.lib = lib
         self.count = count
         nd = len(shape)
         shp = (ctypes.c_int64 * 8)(*shape)
         fr = (ctypes.c_int64 * max(1, len(freqs_host)))(*freqs_host)
-        plan = lib.cresso_spectral_plan_create(shp, nd, fr, rank, bins, tables)
+        plan = lib.cresso_spectral_plan_create_ex(shp, nd, fr, rank, bins, tables, work)
         if not plan:
             _native.check(-1, "spectral route plan")
         self.plan = ctypes.c_void_p(plan)
@@ -144,10 +144,10 @@ class SpectralEngine:
         wkey = (key, count is not None, lane)
         ws = self.ws.get(wkey)
         if ws is None or (count is not None and ws.count < count):
-            device, shape, freqs, bins, tables = key
+            device, shape, freqs, bins, tables, work = key
             ws = None
             self.ws.pop(wkey, None)
-            ws = _Workspace(self.lib, shape, freqs, rank, bins, tables, group, device, count)
+            ws = _Workspace(self.lib, shape, freqs, rank, bins, tables, group, device, count, work)
             self.ws[wkey] = ws
         return ws
 
@@ -164,7 +164,8 @@ class SpectralEngine:
         freqs = self._freqs(st)
         bins, tables = int(group["hash_bins"]), int(group["hash_tables"])
         shape = tuple(int(d) for d in param.shape)
-        key = (param.device, shape, freqs, bins, tables)
+        work = _native.F64 if param.dtype == torch.float64 else _native.F32
+        key = (param.device, shape, freqs, bins, tables, work)
         cut = int(group["thin_matrix_hard_cutoff"])
         thin = param.ndim == 2 and cut > 0 and min(shape) <= cut
         hard = param.numel() >= int(group["hard_channel_min_size"]) and not thin
@@ -220,8 +221,7 @@ class SpectralEngine:
     def _units(self, prepared: list, sts: list) -> list:
         """Cut a step's tensors into units: (unit key, plan key, rank, [desc], [state]).
         Tensors batch when they share the plan, dtypes, hard channel and hash
-        state; fp64 tensors step one at a time (the library's fp64 state
-        transfer is per tensor)."""
+        state; fp64 tensors step one at a time (fp64 plans are not batched)."""
         groups: Dict[tuple, list] = {}
         for i, (key, rank, d) in enumerate(prepared):
             bkey = (key, d.param_dtype, d.grad_dtype, d.hard, bool(d.hash_energy))

@@ -141,6 +141,16 @@ int32_t cresso_scalar_plan_step(cresso_scalar_plan* plan, void* dev_table, const
 typedef struct cresso_spectral_plan cresso_spectral_plan;
 cresso_spectral_plan* cresso_spectral_plan_create(const int64_t* shape, int32_t ndim, const int64_t* freqs,
                                                   int32_t rank, int32_t hash_bins, int32_t hash_tables);
+/* The same with the work dtype of the tensors the plan steps: CRESSO_F32
+ * (fp32, bf16 and fp16 params; what cresso_spectral_plan_create makes) or
+ * CRESSO_F64 (fp64 params: every carrier, field, sum and state update in
+ * fp64, the reference's work dtype for them, cresso_v5.py:119-124).  An F64
+ * plan's workspace also holds per-axis fp64 carrier tables (rank x sum of the
+ * dims x 32 bytes) and an fp64 field (8 bytes per element); it steps fp64
+ * params with fp64 grads only, one tensor per call. */
+cresso_spectral_plan* cresso_spectral_plan_create_ex(const int64_t* shape, int32_t ndim, const int64_t* freqs,
+                                                     int32_t rank, int32_t hash_bins, int32_t hash_tables,
+                                                     int32_t work_dtype);
 void cresso_spectral_plan_destroy(cresso_spectral_plan* plan);
 
 /* Device bytes of the plan's workspace: per-axis carrier tables, basis stats,
@@ -161,8 +171,7 @@ typedef struct cresso_spectral_desc {
     int64_t numel;
     /* state of cresso_v5.py:857-883, updated in place: fp32, or fp64 when
      * param_dtype is F64 (the reference's state follows the work dtype,
-     * v5.py:119-124; an F64 step computes in fp32 through an fp32 copy of the
-     * state in the workspace and adds the update to the param in fp64) */
+     * v5.py:119-124; an F64 step computes in fp64 on an F64 plan) */
     void *force_rms, *drive_energy, *surprise, *action;       /* 0-dim       */
     const void* omega;                                         /* [rank]      */
     void *q_cos, *q_sin, *p_cos, *p_sin;                       /* [rank]      */
@@ -174,8 +183,8 @@ typedef struct cresso_spectral_desc {
 } cresso_spectral_desc;
 
 /* One optimizer step of one tensor on the spectral route.  (param, grad)
- * dtype pairs: (F32,F32), (BF16,BF16), (F16,F16), (F32,BF16), (F32,F16),
- * (F64,F64). */
+ * dtype pairs: (F32,F32), (BF16,BF16), (F16,F16), (F32,BF16), (F32,F16) on
+ * an F32 plan; (F64,F64) on an F64 plan (cresso_spectral_plan_create_ex). */
 int32_t cresso_spectral_step(const cresso_spectral_plan* plan, const cresso_spectral_desc* desc, void* workspace,
                              size_t workspace_bytes, const cresso_hyper* hyper, void* stream);
 

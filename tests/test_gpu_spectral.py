@@ -415,22 +415,35 @@ def test_spectral_loads_float_cast_checkpoint():
     compare([hp2], hopt2, [op], oopt, param_tol=BF16_PARAM_TOL)
 
 
-# fp64 params on the spectral route: fp64 param and grad I/O with the update
-# added in fp64 (cresso_v5.py:1353) and fp64 state (v5.py:119-124), the
-# step's arithmetic in fp32 -- so the fp64 oracle is matched to the fp32
-# tolerances (params, states, and the update at DP_RTOL[float32]).
-FP64_CASES = [("general", (300, 257), 3), ("fast_tiles", (2048, 4096), 2)]
+# fp64 params on the spectral route compute in fp64 (the reference's work
+# dtype for them, cresso_v5.py:119-124): params, every fp64 state tensor and
+# the per-step update dp against the fp64 oracle at rtol 1e-9.  Cases: 1-D,
+# 2-D, 3-D at rank 16 with four tables, a 4-D conv shape (degenerate
+# carriers), tables too large for the per-block LDS histograms (global
+# two-word atomics), and the options weight_decay / maximize /
+# local_sharpness.
+F64_TOL = dict(rtol=1e-9, atol=1e-12)
+FP64_CASES = [
+    ("2d", (300, 257), 3, {}),
+    ("2d_large", (2048, 4096), 2, {}),
+    ("1d", (5000,), 3, {}),
+    ("3d_r16_t4", (24, 20, 36), 3, dict(rank=16, max_frequency=7, hash_bins=256, hash_tables=4)),
+    ("conv_r16", (16, 8, 3, 3), 3, dict(rank=16, max_frequency=7, hash_bins=256, hash_tables=4)),
+    ("global_bins", (512, 300), 2, dict(hash_bins=1024)),
+    ("options", (300, 257), 3, dict(weight_decay=0.01, maximize=True, local_sharpness=0.3)),
+]
 
 
 @pytest.mark.parametrize("case", FP64_CASES, ids=[c[0] for c in FP64_CASES])
 def test_spectral_fp64_params(case):
-    name, shape, steps = case
+    name, shape, steps, extra = case
     announce(f"spectral fp64 {name} {shape}")
     import cresso_amd
     from gpu_util import DP_RTOL
     from oracle.cresso_oracle import OracleCRESSO5
 
     kw = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2)
+    kw.update(extra)
     gen = torch.Generator().manual_seed(23)
     p0 = 0.02 * torch.randn(shape, generator=gen, dtype=torch.float64)
     hp = torch.nn.Parameter(p0.clone().cuda())
@@ -449,4 +462,5 @@ def test_spectral_fp64_params(case):
         oopt.step([g])
     torch.cuda.synchronize()
     assert hp.dtype == torch.float64 and hopt.state[hp]["q_cos"].dtype == torch.float64
-    compare([hp], hopt, [op], oopt, dp_rtol=DP_RTOL[torch.float32])
+    assert oopt.route(op) == "spectral"
+    compare([hp], hopt, [op], oopt, param_tol=F64_TOL, state_tol=F64_TOL, dp_rtol=DP_RTOL[torch.float64])
