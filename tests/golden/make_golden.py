@@ -2,7 +2,8 @@
 
 Runs in the build container only (the reference is never shipped):
 
-    python tests/golden/make_golden.py [/root/reference]
+    python tests/golden/make_golden.py [/root/reference]          # every fixture
+    python tests/golden/make_golden.py [/root/reference] --dtypes  # only trajectories_f16_f64.npz
 
 It loads ``cresso_v5.py`` by path exactly as the reference's own tests do and
 records, as plain arrays in ``tests/golden/*.npz``:
@@ -11,7 +12,8 @@ records, as plain arrays in ``tests/golden/*.npz``:
   * dense normalized basis pairs (2D, 1D, 3D and the degenerate 3-wide 4D case);
   * project / reconstruct outputs;
   * multi-step optimizer trajectories (params + every state tensor per step)
-    for the spectral, scalar and micro routes, fp32 and bf16.
+    for the spectral, scalar and micro routes, fp32 and bf16
+    (trajectories.npz), fp16 and fp64 (trajectories_f16_f64.npz).
 Nothing but arrays and JSON-encoded hyperparameters is written.
 """
 
@@ -26,7 +28,8 @@ import numpy as np
 import torch
 
 HERE = Path(__file__).resolve().parent
-REF = Path(sys.argv[1]) if len(sys.argv) > 1 else Path("/root/reference")
+ARGS = [a for a in sys.argv[1:] if not a.startswith("--")]
+REF = Path(ARGS[0]) if ARGS else Path("/root/reference")
 
 
 def load_reference():
@@ -84,7 +87,9 @@ def run_trajectory(ref, name, shape, dtype, kwargs, steps, seed, grad_std=1.0, p
         out[f"grad{k}_sum"] = np.array(float(g.double().sum()))
         param.grad = g.clone()
         opt.step()
-        pflat = param.detach().float().reshape(-1)
+        pflat = param.detach().reshape(-1)
+        if pflat.dtype in (torch.bfloat16, torch.float16):
+            pflat = pflat.float()
         if store_dense:
             out[f"step{k}/param"] = to_np(param)
         out[f"step{k}/param_sample"] = to_np(pflat[torch.from_numpy(idx)])
@@ -98,9 +103,55 @@ def run_trajectory(ref, name, shape, dtype, kwargs, steps, seed, grad_std=1.0, p
     return out
 
 
+# fp16 and fp64 params: the fp16 update step (alpha rounded to the param
+# dtype by torch's add_) and every fp64 state and field (the fp64 work dtype,
+# cresso_v5.py:119-124) on the spectral, scalar and micro routes
+OPS_KWARGS = dict(lr=2.0e-3, rank=8, max_frequency=5, min_spectral_size=1, hard_channel_min_size=1,
+                  thin_matrix_hard_cutoff=0, hash_bins=37, hash_tables=2, basis_cache_limit_elements=0)
+DTYPE_CASES = [
+    ("spectral_31x37_f16", (31, 37), torch.float16, dict(OPS_KWARGS, lr=1e-3), 3, 8643, 0.05, 0.05, False),
+    ("spectral_64x48_f16", (64, 48), torch.float16,
+     dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2), 4, 31, 1e-2, 0.02, True),
+    ("spectral_31x37_f64", (31, 37), torch.float64, OPS_KWARGS, 5, 9013, 1.0, 1.0, False),
+    ("spectral_64x48_f64", (64, 48), torch.float64,
+     dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2), 6, 32, 1e-3, 0.02, True),
+    ("spectral_1d_2048_f64", (2048,), torch.float64,
+     dict(rank=8, max_frequency=5, hash_bins=64, hash_tables=2), 4, 33, 1e-2, 0.02, False),
+    ("spectral_3d_6x10x12_f64", (6, 10, 12), torch.float64,
+     dict(rank=16, max_frequency=7, hash_bins=256, hash_tables=4, min_spectral_size=1), 4, 34, 1e-3, 0.02, False),
+    ("spectral_4d_8x6x3x3_f64", (8, 6, 3, 3), torch.float64,
+     dict(rank=16, max_frequency=7, hash_bins=256, hash_tables=4, min_spectral_size=1), 3, 35, 1e-3, 0.02, False),
+    ("spectral_40x30_variants_f64", (40, 30), torch.float64,
+     dict(rank=8, max_frequency=5, hash_bins=64, hash_tables=3, weight_decay=0.01, maximize=True,
+          local_sharpness=0.3, min_spectral_size=1, warmup_steps=0), 4, 36, 1e-2, 0.05, False),
+    ("scalar_128x16_f64", (128, 16), torch.float64,
+     dict(lr=2e-3, rank=4, thin_matrix_route="scalar", thin_matrix_max_width=64, min_spectral_size=1), 8, 2469,
+     1.0, 1.0, False),
+    ("scalar_4096x16_f64", (4096, 16), torch.float64, dict(rank=4, hash_bins=64, hash_tables=2), 4, 37, 1e-4, 0.02,
+     False),
+    ("scalar_64x16_f16", (64, 16), torch.float16,
+     dict(lr=1e-3, rank=4, thin_matrix_route="scalar", thin_matrix_max_width=64, min_spectral_size=1), 3, 3580,
+     0.05, 0.05, False),
+    ("micro_12x10_f64", (12, 10), torch.float64, dict(micro_field_max_size=256, rank=4), 4, 38, 1e-2, 0.1, False),
+]
+
+
+def write_trajectories(ref, cases, fname):
+    tz = {}
+    for name, shape, dtype, kwargs, steps, seed, gstd, pstd, spike in cases:
+        tr = run_trajectory(ref, name, shape, dtype, kwargs, steps, seed, gstd, pstd, spike)
+        for k, v in tr.items():
+            tz[f"{name}/{k}"] = v
+        print("trajectory", name, flush=True)
+    np.savez_compressed(HERE / fname, **tz)
+
+
 def main() -> None:
     torch.set_num_threads(max(1, torch.get_num_threads()))
     ref = load_reference()
+    write_trajectories(ref, DTYPE_CASES, "trajectories_f16_f64.npz")
+    if "--dtypes" in sys.argv:
+        return
 
     # ---------------- frequencies / omega / hash_unit ----------------
     fz = {}
@@ -193,13 +244,7 @@ def main() -> None:
         ("scalar_tiny_eps_f32", (4096, 16), torch.float32, dict(rank=4), 3, 26, 1e-7, 0.02, False),
         ("micro_12x10_f32", (12, 10), torch.float32, dict(micro_field_max_size=256, rank=4), 4, 27, 1e-2, 0.1, False),
     ]
-    tz = {}
-    for name, shape, dtype, kwargs, steps, seed, gstd, pstd, spike in cases:
-        tr = run_trajectory(ref, name, shape, dtype, kwargs, steps, seed, gstd, pstd, spike)
-        for k, v in tr.items():
-            tz[f"{name}/{k}"] = v
-        print("trajectory", name, flush=True)
-    np.savez_compressed(HERE / "trajectories.npz", **tz)
+    write_trajectories(ref, cases, "trajectories.npz")
 
     # C1 of BASELINE.json: (2048,2048) fp32, grad N(0,1e-3) from seed 0, 10 steps.
     c1 = run_c1(ref)

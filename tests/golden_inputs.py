@@ -39,14 +39,14 @@ def _same(a: float, b: float) -> bool:
     return abs(a - b) <= 1e-12 * max(1.0, abs(a), abs(b))
 
 
-def trajectory_names() -> List[str]:
-    z = load("trajectories")
+def trajectory_names(file: str = "trajectories") -> List[str]:
+    z = load(file)
     return sorted({k.split("/")[0] for k in z})
 
 
-def trajectory(name: str):
+def trajectory(name: str, file: str = "trajectories"):
     """-> (meta, p0, grads, per-step expected dict) with inputs checked against stored sums."""
-    z = load("trajectories")
+    z = load(file)
     pre = name + "/"
     sub = {k[len(pre):]: v for k, v in z.items() if k.startswith(pre)}
     meta = json.loads(str(sub["meta"]))

@@ -194,6 +194,43 @@ def test_trajectory_matches_reference(name):
                 assert got == int(v)
 
 
+def _dtype_tol(dtype: str):
+    # fp64 runs the reference's own fp64 ops: agreement to fp64 rounding;
+    # fp16 params: the same fp32 work and the same rounded update as the reference
+    return dict(rtol=1e-11, atol=1e-14) if dtype == "float64" else dict(rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("name", trajectory_names("trajectories_f16_f64"))
+def test_f16_f64_trajectory_matches_reference(name):
+    """The oracle's fp16 and fp64 legs (the update step's rounding for fp16
+    params, every fp64 state and field for fp64 params) against the
+    reference's own output (tests/golden/trajectories_f16_f64.npz)."""
+    meta, p0, grads, steps, sidx = trajectory(name, "trajectories_f16_f64")
+    opt = O.OracleCRESSO5([p0.clone()], **meta["kwargs"])
+    p = opt.params[0]
+    tol = _dtype_tol(meta["dtype"])
+    for k, g in enumerate(grads):
+        opt.step([g])
+        exp = steps[k]
+        pf = p.detach().reshape(-1)
+        pf = pf if pf.dtype == torch.float64 else pf.float()
+        if "param" in exp:
+            np.testing.assert_allclose(p.double().numpy(), exp["param"], **tol, err_msg=f"{name} step {k} param")
+        np.testing.assert_allclose(pf[torch.from_numpy(sidx)].double().numpy(), exp["param_sample"], **tol)
+        st = opt.state[0]
+        for key, v in exp.items():
+            if not key.startswith("state/"):
+                continue
+            sk = key[len("state/"):]
+            got = st[sk]
+            if torch.is_tensor(got):
+                if got.is_floating_point() and meta["dtype"] == "float64":
+                    assert got.dtype == torch.float64, (name, sk)
+                np.testing.assert_allclose(got.double().numpy(), v, **tol, err_msg=f"{name} step {k} {sk}")
+            else:
+                assert got == int(v)
+
+
 def test_c1_2048_trajectory_matches_reference():
     z = load("c1_2048")
     meta = json.loads(str(z["meta"]))
