@@ -574,6 +574,58 @@ __global__ __launch_bounds__(256) void ws_cooc4_kernel(Geom g, const uint32_t* _
     }
 }
 
+// The same counts without global atomics per element: each block counts a
+// contiguous chunk of elements into LDS, one table pair and one half of the
+// B x B cells (32768 u32 counters, 128 KiB of dynamic LDS) at a time, and
+// writes the chunk's whole table part[block][pair][cell]; ws_cooc4_sum_kernel
+// adds the blocks' tables in block order (integers: exact).  The chunk is read
+// once per (pair, half), from the cache after the first.
+constexpr int WS_COOC4_NT = 1024;
+constexpr int WS_COOC4_HALF = 32768;
+__global__ __launch_bounds__(WS_COOC4_NT) void ws_cooc4_part_kernel(Geom g, const uint32_t* __restrict__ bins,
+                                                                    unsigned int* __restrict__ part) {
+    extern __shared__ unsigned int s_cnt[];
+    const int BB = g.B * g.B;
+    const int halves = (BB + WS_COOC4_HALF - 1) / WS_COOC4_HALF;
+    const int64_t per = (g.n + gridDim.x - 1) / gridDim.x;
+    const int64_t i0 = (int64_t)blockIdx.x * per, i1 = i0 + per < g.n ? i0 + per : g.n;
+    for (int c = 0; c < 6 * halves; ++c) {
+        const int p = c / halves, h = c % halves;
+        int t0, t1;
+        cooc_pair(p, t0, t1);
+        const int lo = h * WS_COOC4_HALF, len = BB - lo < WS_COOC4_HALF ? BB - lo : WS_COOC4_HALF;
+        for (int i = threadIdx.x; i < len; i += WS_COOC4_NT) s_cnt[i] = 0u;
+        __syncthreads();
+        // sixteen loads in flight per thread before their counts
+        constexpr int U = 16;
+        for (int64_t base = i0 + threadIdx.x; base < i1; base += (int64_t)U * WS_COOC4_NT) {
+            uint32_t v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t i = base + (int64_t)u * WS_COOC4_NT;
+                v[u] = bins[i < i1 ? i : i0];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k = (int)((v[u] >> (8 * t0)) & 0xffu) * g.B + (int)((v[u] >> (8 * t1)) & 0xffu) - lo;
+                if (base + (int64_t)u * WS_COOC4_NT < i1 && (unsigned)k < (unsigned)len) atomicAdd(&s_cnt[k], 1u);
+            }
+        }
+        __syncthreads();
+        unsigned int* dst = part + ((size_t)blockIdx.x * 6 + p) * (size_t)BB + lo;
+        for (int i = threadIdx.x; i < len; i += WS_COOC4_NT) dst[i] = s_cnt[i];
+        __syncthreads();
+    }
+}
+__global__ __launch_bounds__(256) void ws_cooc4_sum_kernel(const unsigned int* __restrict__ part, int nblk, int64_t cells,
+                                                           unsigned long long* __restrict__ cooc) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= cells) return;
+    unsigned long long a = 0ull;
+    for (int b = 0; b < nblk; ++b) a += part[(size_t)b * cells + i];
+    cooc[i] = a;
+}
+
 #endif  // CRESSO_SPECTRAL_WS_KERNELS
 
 __device__ __forceinline__ uint64_t load_bins(const unsigned char* __restrict__ bins, int64_t e, int binbytes) {

@@ -327,9 +327,26 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
         if (g.T == 2)
             hipLaunchKernelGGL(ws_cooc_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g,
                                at<const uint16_t>(ws, o.bins), at<unsigned long long>(ws, o.cooc));
-        else
-            hipLaunchKernelGGL(ws_cooc4_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g,
-                               at<const uint32_t>(ws, o.bins), at<unsigned long long>(ws, o.cooc));
+        else {
+            // per-block tables in the (not yet used) tangent-field region: as
+            // many blocks as fit, at most 256; few elements take the atomics
+            const int64_t cells = 6 * (int64_t)g.B * g.B;
+            const int64_t nb = std::min<int64_t>(256, (int64_t)(sizeof(float) * (size_t)g.n) / (cells * 4));
+            static const hipError_t lds_ok = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&ws_cooc4_part_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                (int)(sizeof(unsigned int) * WS_COOC4_HALF));
+            if (nb >= 16 && lds_ok == hipSuccess) {
+                unsigned int* part = at<unsigned int>(ws, o.tbuf);
+                const size_t lds = sizeof(unsigned int) * (size_t)std::min<int64_t>(WS_COOC4_HALF, (int64_t)g.B * g.B);
+                hipLaunchKernelGGL(ws_cooc4_part_kernel, dim3((unsigned)nb), dim3(WS_COOC4_NT), lds, s, g,
+                                   at<const uint32_t>(ws, o.bins), part);
+                hipLaunchKernelGGL(ws_cooc4_sum_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, s, part,
+                                   (int)nb, cells, at<unsigned long long>(ws, o.cooc));
+            } else {
+                hipLaunchKernelGGL(ws_cooc4_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g,
+                                   at<const uint32_t>(ws, o.bins), at<unsigned long long>(ws, o.cooc));
+            }
+        }
     }
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "spectral route: workspace init");

@@ -455,7 +455,18 @@ class CRESSO5(Optimizer):
                         st[k] = v.to(device=p.device, dtype=_state_dtype(p.dtype)).clone()
         self._batches.clear()
         if self._spectral_engine is not None:
-            self._spectral_engine.reset()
+            # workspaces are derived from (shape, freqs, hash_bins, hash_tables,
+            # work dtype) only: keep those the loaded state still uses
+            self._spectral_engine.retain(self._spectral_plan_keys())
+
+    def _spectral_plan_keys(self) -> set:
+        keys = set()
+        for group in self.param_groups:
+            for p in group["params"]:
+                st = self.state.get(p)
+                if st and "freqs" in st and "omega" in st:
+                    keys.add(self._spectral_engine.plan_key(p, st, group))
+        return keys
 
 
 CRESSO = CRESSO5

@@ -22,7 +22,8 @@ directly.
 
 Device memory held: per (plan, lane) a workspace of the plan's tables (about
 (2 + 4) bytes per element at two tables of <= 256 bins) and its scratch;
-`reset()` (called by the optimizer's load_state_dict) frees them all.
+the optimizer's load_state_dict keeps those whose plan the loaded state still
+uses (`retain`) and frees the others; `reset()` frees them all.
 """
 
 from __future__ import annotations
@@ -130,6 +131,19 @@ class SpectralEngine:
         self.freq_cache.clear()
         self.ws.clear()
 
+    def retain(self, keys) -> None:
+        """Forget cached frequency lists; free the workspaces whose plan key is
+        not in `keys` (a workspace depends on its plan key only)."""
+        self.freq_cache.clear()
+        for wkey in [k for k in self.ws if k[0] not in keys]:
+            del self.ws[wkey]
+
+    def plan_key(self, param: torch.Tensor, st: dict, group: dict) -> tuple:
+        """The plan key of a spectral tensor: (device, shape, freqs, hash_bins, hash_tables, work dtype)."""
+        work = _native.F64 if param.dtype == torch.float64 else _native.F32
+        return (param.device, tuple(int(d) for d in param.shape), self._freqs(st), int(group["hash_bins"]),
+                int(group["hash_tables"]), work)
+
     def _freqs(self, st: dict) -> Tuple[int, ...]:
         fr = st["freqs"]
         key = id(fr)
@@ -161,11 +175,9 @@ class SpectralEngine:
             if st[k].dtype != sdt:
                 raise RuntimeError(f"CRESSO5 spectral state {k} has dtype {st[k].dtype}, expected {sdt}")
         rank = int(st["omega"].numel())
-        freqs = self._freqs(st)
         bins, tables = int(group["hash_bins"]), int(group["hash_tables"])
-        shape = tuple(int(d) for d in param.shape)
-        work = _native.F64 if param.dtype == torch.float64 else _native.F32
-        key = (param.device, shape, freqs, bins, tables, work)
+        key = self.plan_key(param, st, group)
+        shape = key[1]
         cut = int(group["thin_matrix_hard_cutoff"])
         thin = param.ndim == 2 and cut > 0 and min(shape) <= cut
         hard = param.numel() >= int(group["hard_channel_min_size"]) and not thin

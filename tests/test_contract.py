@@ -323,3 +323,36 @@ def test_spectral_batch_units_and_chunks():
     assert all(not u[0][1] for u in units[3:])
     eng.BATCH = False
     assert [len(u[4]) for u in eng._units(prepared, sts)] == [1] * len(prepared)
+
+
+def test_load_state_dict_keeps_same_plan_workspaces():
+    """A spectral workspace depends only on its plan key (shape, freqs,
+    hash_bins, hash_tables, work dtype): load_state_dict keeps those the
+    loaded state still uses and frees the rest (no GPU needed: the workspaces
+    here are stand-in objects in the engine's table)."""
+    lib_path = ROOT / "cresso_amd" / "libcresso_hip.so"
+    if not lib_path.exists():
+        pytest.skip("library not built")
+    from cresso_amd.spectral import SpectralEngine
+
+    p = torch.nn.Parameter(torch.zeros(64, 48))
+    q = torch.nn.Parameter(torch.zeros(32, 40))
+    opt = CRESSO5([p, q], cuda_ops="required", rank=8, hash_bins=64, hash_tables=2)
+    group = opt.param_groups[0]
+    for t in (p, q):
+        opt.state[t] = opt._init_spectral(t, group)
+    eng = SpectralEngine()
+    opt._spectral_engine = eng
+    kp = eng.plan_key(p, opt.state[p], group)
+    kq = eng.plan_key(q, opt.state[q], group)
+    stale = (kp[0], (7, 7)) + kp[2:]
+    keep_p, keep_q, drop = object(), object(), object()
+    eng.ws = {(kp, False, 0): keep_p, (kq, True, 2): keep_q, (stale, False, 1): drop}
+    sd = opt.state_dict()
+    opt.load_state_dict(sd)
+    assert eng.ws == {(kp, False, 0): keep_p, (kq, True, 2): keep_q}
+    # a loaded state with other freqs for p no longer uses p's plan
+    sd2 = opt.state_dict()
+    sd2["state"][0]["freqs"] = sd2["state"][0]["freqs"].flip(0).clone()
+    opt.load_state_dict(sd2)
+    assert set(eng.ws) == {(kq, True, 2)}
