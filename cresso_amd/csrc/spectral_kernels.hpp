@@ -1509,6 +1509,20 @@ __device__ __forceinline__ void elem_fence() { __builtin_amdgcn_sched_barrier(0)
 // is addressed as (uniform base pointer) + (32-bit lane offset lr * cols +
 // lane); the planner keeps PR * cols below 2^29.
 __device__ __forceinline__ int64_t panel_base(const Geom& g, const Tile& t) { return t.r0 * g.cols + (int64_t)t.slab * SP_NT; }
+// The tangent / drive field after the matrix-core sweeps, 4-row interleaved:
+// element (R, C) at 4 ((R / 4) cols + C) + R % 4 (rows are a multiple of 4 on
+// that path).  A block's elements (r0 + i, c0 + j) then sit at
+// q4_base + 4 ((i / 4) cols + j) + i % 4, and the four rows 4 lg + r of a
+// lane's tile column are one float4.
+__device__ __forceinline__ int64_t q4_base(const Geom& g, const Tile& t) {
+    return t.r0 * g.cols + 4 * (int64_t)t.slab * SP_NT;
+}
+__device__ __forceinline__ uint32_t q4_lane_bytes(uint32_t cols, int lg, int wv, int li) {
+    return 16u * ((uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li);
+}
+__device__ __forceinline__ uint32_t q4_tile_bytes(uint32_t cols, int tr, int tc) {
+    return 16u * (4u * (uint32_t)tr * cols + 16u * (uint32_t)tc);
+}
 __device__ __forceinline__ uint32_t panel_off(const Geom& g, int lr) { return (uint32_t)lr * (uint32_t)g.cols + threadIdx.x; }
 __device__ __forceinline__ uint64_t load_bins_at(const unsigned char* __restrict__ bins, int64_t base, uint32_t off,
                                                  int binbytes) {
@@ -2744,10 +2758,13 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
     const int64_t base = panel_base(g, t);
     const uint32_t cols = (uint32_t)g.cols;
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(grad + base, (uint32_t)((int64_t)nr * g.cols * (int64_t)sizeof(GT)));
-    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tbuf + base, (uint32_t)((int64_t)nr * g.cols * 4));
+    // t goes to the field in the 4-row interleaved layout (q4_base): a lane's
+    // four rows of a tile are one float4, and a wave's store writes whole lines
+    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tbuf + q4_base(g, t), (uint32_t)((int64_t)nr * g.cols * 4));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(bins + (size_t)TT * base, (uint32_t)((int64_t)nr * g.cols * TT));
     const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
-    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vt = lane_el * 4u, vb = lane_el * (uint32_t)TT;
+    const uint32_t vg = lane_el * (uint32_t)sizeof(GT), vb = lane_el * (uint32_t)TT;
+    const uint32_t vt = q4_lane_bytes(cols, lg, wv, li);
     // tile (tr, tc), lane element r: panel element (16 tr + 4 lg + r, 64 wv + 16 tc + li)
     auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
     // one register set, refilled tile by tile: the loads of tile (tr + 1, tc)
@@ -2917,7 +2934,6 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
                 den = den * med3f(rfv[r] * ec, 0.08f, 12.0f);
                 den = den * med3f(hmv[r], 0.08f, 12.0f);
                 const float tv = med3f(x[r] * frcp(den + eps_s), -1.0e4f, 1.0e4f);
-                bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
                 tvs[r] = tv;
                 const float err = tv - pred[r];
                 const float P = err + tm * tv;
@@ -2926,6 +2942,7 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
                 m_tt += tv * tv;
                 vfx[r] = to_fixed_s(P * hs);
             }
+            bstore4(rt, vt, q4_tile_bytes(cols, tr, tc), f32x4{tvs[0], tvs[1], tvs[2], tvs[3]});
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -2960,7 +2977,6 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
                 for (int tt = 1; tt < TT; ++tt) hm *= s_lt[tt * B + bin_byte<TT>(b[r], tt)];
                 den = den * med3f(hm, 0.08f, 12.0f);
                 const float tv = med3f(x[r] * frcp(den + eps_s), -1.0e4f, 1.0e4f);
-                bstore1(rt, vt, tile_off(tr, tc, r) * 4u, tv);
                 tvs[r] = tv;
                 const float err = tv - pred[r];
                 const float P = err + tm * tv;
@@ -2976,6 +2992,7 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
 #pragma unroll
                 for (int tt = 0; tt < TT; ++tt) atomicAdd(&s_hist[(tt * B + bin_byte<TT>(b[r], tt)) * NH + hc], v);
             }
+            bstore4(rt, vt, q4_tile_bytes(cols, tr, tc), f32x4{tvs[0], tvs[1], tvs[2], tvs[3]});
             // A of the projection: a_q(row 16 tr + 4 lg + r), q = 16 qt + li
 #pragma unroll
             for (int qt = 0; qt < NQ; ++qt)
@@ -3522,7 +3539,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep4_kernel(
 // writes the drive without the hash term and sums d^2, d hp and hp^2 for
 // sweep 5).
 // ---------------------------------------------------------------------------
-template <int RM, int KC, int TT>
+template <int RM, int KC, int TT, bool Q4>
 __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     Geom g, const float* __restrict__ rowtab, const float* __restrict__ coltab, const ModeMeta* __restrict__ meta,
     const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl, const float* __restrict__ imp_tab,
@@ -3540,12 +3557,13 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int li = l & 15, lg = l >> 4;
     const int64_t base = panel_base(g, t);
-    float* __restrict__ tb = tbuf + base;
+    // the field: 4-row interleaved after sweep 3m (Q4), row-major after the general sweep 3
+    float* __restrict__ tb = tbuf + (Q4 ? q4_base(g, t) : base);
     const uint32_t cols = (uint32_t)g.cols;
     const __amdgpu_buffer_rsrc_t rt = make_rsrc(tb, (uint32_t)((int64_t)nr * g.cols * 4));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(bins + (size_t)TT * base, (uint32_t)((int64_t)nr * g.cols * TT));
     const uint32_t lane_el = 4u * (uint32_t)lg * cols + 64u * (uint32_t)wv + (uint32_t)li;  // element offset
-    const uint32_t vt = lane_el * 4u, vb = lane_el * (uint32_t)TT;
+    const uint32_t vt = Q4 ? q4_lane_bytes(cols, lg, wv, li) : lane_el * 4u, vb = lane_el * (uint32_t)TT;
     // tile (tr, tc), lane element r: panel element (16 tr + 4 lg + r, 64 wv + 16 tc + li)
     auto tile_off = [&](int tr, int tc, int r) -> uint32_t { return (uint32_t)(16 * tr + r) * cols + 16u * tc; };
     // A row of tiles (4 tiles x 4 elements) is in flight while the previous row
@@ -3555,13 +3573,19 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     uint32_t ba[16], bb[16];
     auto load_row = [&](int tr, float* x, uint32_t* b) {
 #pragma unroll
-        for (int tc = 0; tc < 4; ++tc)
+        for (int tc = 0; tc < 4; ++tc) {
+            if constexpr (Q4) {
+                const f32x4 v = bload4(rt, vt, q4_tile_bytes(cols, tr, tc));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x[4 * tc + r] = v[r];
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t o = tile_off(tr, tc, r);
-                x[4 * tc + r] = bload1(rt, vt, o * 4u);
+                if constexpr (!Q4) x[4 * tc + r] = bload1(rt, vt, o * 4u);
                 b[4 * tc + r] = ldg_bins<TT>(rb, vb, o * (uint32_t)TT);
             }
+        }
     };
     load_row(0, xa, ba);
     float* s_imp = reinterpret_cast<float*>(dyn);
@@ -3624,6 +3648,7 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
     float a_dd = 0.f;
     auto tile = [&](int tr, int tc, const float* x, const uint32_t* b, const float* aP, const float* aX) {
         f32x4m pred = {cQ, cQ, cQ, cQ}, mixed = {cX, cX, cX, cX};
+        float dv[4];
 #pragma unroll
         for (int kc = 0; kc < KCH; ++kc) {
             pred = __builtin_amdgcn_mfma_f32_16x16x4f32(aP[kc], bq[tc][kc], pred, 0, 0, 0);
@@ -3642,9 +3667,13 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
             for (int tt = 1; tt < TT; ++tt) hp += s_imp[tt * B + bin_byte<TT>(b[r], tt)];
             hp = hp * invT;
             const float d = fmaf(c5, hp, fmaf(k_nov, nov, core + mixed[r]));
-            bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
+            if constexpr (Q4)
+                dv[r] = d;
+            else
+                bstore1(rt, vt, tile_off(tr, tc, r) * 4u, d);
             a_dd = fmaf(d, d, a_dd);
         }
+        if constexpr (Q4) bstore4(rt, vt, q4_tile_bytes(cols, tr, tc), f32x4{dv[0], dv[1], dv[2], dv[3]});
         pin1(a_dd);
         elem_fence();
     };
@@ -3674,6 +3703,17 @@ __global__ __launch_bounds__(SP_NT, (occ4m<RM, KC>())) void sweep4m_kernel(
 }
 
 
+
+// Sweep 5 after the matrix-core sweeps, whose drive field is 4-row
+// interleaved (q4_base): a thread takes four rows by four columns at a time,
+// the drive as four float4 (one per column) and the param as four vectors of
+// four (one per row), transposed in registers; params not aligned for vector
+// access take one column of four rows at a time.  Same grid as sweep 5.
+template <typename PT, bool VEC>
+__global__ __launch_bounds__(SP_NT) void sweep5q_kernel(Geom g, PT* __restrict__ param, const float* __restrict__ dbuf,
+                                                        const Ctrl* __restrict__ ctrl, const double* __restrict__ part,
+                                                        float* __restrict__ de_state, int step, int hash_on, int hard,
+                                                        int c5_closed, Lanes L, cresso_hyper h);
 
 // F4, in every block of sweep 5: sweep 4's block partials summed in a fixed
 // order (so every block gets the same values), then the hash-term
@@ -3912,6 +3952,95 @@ __global__ __launch_bounds__(SP_NT) void sweep5_kernel(
 
 
 
+template <typename PT, bool VEC>
+__global__ __launch_bounds__(SP_NT) void sweep5q_kernel(Geom g, PT* __restrict__ param, const float* __restrict__ dbuf,
+                                                        const Ctrl* __restrict__ ctrl, const double* __restrict__ part,
+                                                        float* __restrict__ de_state, int step, int hash_on, int hard,
+                                                        int c5_closed, Lanes L, cresso_hyper h) {
+    if (L.dv) {
+        const cresso_spectral_desc& d = lane_desc(L);
+        param = (PT*)d.param; de_state = (float*)d.drive_energy; step = d.step;
+    }
+    dbuf = lane_at(dbuf, L); ctrl = lane_at(ctrl, L); part = lane_at(part, L);
+    if constexpr (!VEC) {
+        // params not aligned for vector access: one column of four rows per
+        // item, element loads and stores (coalesced across the wave)
+        const int64_t nq = g.n / 4;
+        const int64_t per = (nq + gridDim.x - 1) / gridDim.x;
+        const int64_t w0 = (int64_t)blockIdx.x * per, w1 = w0 + per < nq ? w0 + per : nq;
+        const int32_t cols = (int32_t)g.cols;
+        int64_t w = w0 + threadIdx.x;
+        int64_t q = w / cols;
+        int32_t c = (int32_t)(w - q * cols);
+        float gain, c5;
+        fin4_values(g, part, ctrl, de_state, step, hash_on, hard, c5_closed, h, gain, c5);
+        const float nlr = (float)update_alpha<PT>(-h.lr);
+        while (w < w1) {
+            const f32x4 d4 = gload4(dbuf + 4 * w);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t e = (4 * q + r) * g.cols + c;
+                const float u = to_f(from_w<PT>(d4[r] * gain));
+                param[e] = from_w<PT>(to_f(param[e]) + nlr * u);
+            }
+            w += SP_NT;
+            c += SP_NT;
+            while (c >= cols) {
+                c -= cols;
+                ++q;
+            }
+        }
+        return;
+    }
+    // item w = q (cols / 4) + k: rows 4q .. 4q + 3, columns 4k .. 4k + 3: four
+    // float4 of drive (one per column, 64 contiguous bytes) and four of param
+    // (one per row); the items of a block are a contiguous range
+    const int32_t c4 = (int32_t)(g.cols / 4);   // a multiple of SP_NT / 4 on this path
+    const int64_t ni = g.n / 16;
+    const int64_t per = (ni + gridDim.x - 1) / gridDim.x;
+    const int64_t w0 = (int64_t)blockIdx.x * per, w1 = w0 + per < ni ? w0 + per : ni;
+    int64_t w = w0 + threadIdx.x;
+    int64_t q = w / c4;
+    int32_t k = (int32_t)(w - q * c4);
+    auto next = [&]() {
+        w += SP_NT;
+        k += SP_NT;
+        while (k >= c4) {
+            k -= c4;
+            ++q;
+        }
+    };
+    f32x4 dd[4];
+    float pp[4][4];
+    auto load = [&]() {
+        const float* dq = dbuf + 4 * (q * g.cols + 4 * (int64_t)k);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dd[j] = gload4(dq + 4 * j);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pre4<PT>(param, (4 * q + r) * g.cols + 4 * (int64_t)k, pp[r]);
+    };
+    // the first item's loads go out before the gain is known
+    const bool pre = w < w1;
+    if (pre) load();
+    float gain, c5;
+    fin4_values(g, part, ctrl, de_state, step, hash_on, hard, c5_closed, h, gain, c5);
+    const float nlr = (float)update_alpha<PT>(-h.lr);
+    while (w < w1) {
+        if (w != w0 + threadIdx.x) load();
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float u = to_f(from_w<PT>(dd[j][r] * gain));
+                o[j] = pp[r][j] + nlr * u;
+            }
+            St4<PT>::go(param, (4 * q + r) * g.cols + 4 * (int64_t)k, o);
+        }
+        next();
+    }
+}
+
 }  // namespace
 }  // namespace cresso
 
@@ -4097,11 +4226,20 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
                        cooc, step, hash_on, hard, echo_on, c5c, nc3, L, h);
     if (c5c == 2)
         hipLaunchKernelGGL(hh4_kernel, dim3((unsigned)hh4_blocks(g), ny), dim3(256), 0, s, g, cooc, counts, imp, ctrl, L);
-    if (c5c == 1)
-        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
+    // the field is 4-row interleaved when sweep 3m wrote it (then sweep 4m
+    // runs too, in place, and sweep 5q applies it)
+    const bool q4 = m3 && c5c != 0;
+    if (c5c == 1 && q4)
+        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
+                           tbuf, part, echo_on, L, h, one_round4);
+    else if (c5c == 1)
+        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
+                           tbuf, part, echo_on, L, h, one_round4);
+    else if (c5c == 2 && q4)
+        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
                            tbuf, part, echo_on, L, h, one_round4);
     else if (c5c == 2)
-        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
+        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
                            tbuf, part, echo_on, L, h, one_round4);
     else if (fast)
         hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
@@ -4111,7 +4249,13 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
                            hash_on, echo_on, L, h);
     const bool hash5 = hash_on && !c5c;   // sweep 5 adds the hash term itself
     const size_t l5 = hash5 ? sizeof(float) * (size_t)g.T * g.B : 0;
-    if (hash5 && pv4)
+    if (q4 && pv4)
+        hipLaunchKernelGGL((sweep5q_kernel<PT, true>), grid1, blk, 0, s, g, param, tbuf, ctrl, part, st.drive_energy, step,
+                           hash_on, hard, c5c, L, h);
+    else if (q4)
+        hipLaunchKernelGGL((sweep5q_kernel<PT, false>), grid1, blk, 0, s, g, param, tbuf, ctrl, part, st.drive_energy,
+                           step, hash_on, hard, c5c, L, h);
+    else if (hash5 && pv4)
         hipLaunchKernelGGL((sweep5_kernel<PT, true, true>), grid1, blk, l5, s, g, param, tbuf, bins, ctrl, imp, part,
                            st.drive_energy, step, hash_on, hard, c5c, L, h);
     else if (hash5)

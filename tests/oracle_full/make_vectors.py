@@ -10,8 +10,11 @@ same seeded inputs with bench.py's recipes and compare against them.
 
 Each <name>.npz holds, per step k and tensor i: every state tensor
 (``s{k}/t{i}/<key>``), the param at fixed sampled indices (``s{k}/t{i}/sample``,
-indices in ``t{i}/index``), and the fp64 sum and sum of squares of the whole
-param and of its update dp = p_after - p_before (``dsum``, ``dsumsq``);
+indices in ``t{i}/index``), the fp64 sum and sum of squares of the whole
+param and of its update dp = p_after - p_before (``dsum``, ``dsumsq``), and,
+for fp32 params outside C3, the fp64 marginal sums of dp along every axis
+(``dm{a}``: for each coordinate of axis a, the sum of dp over the other axes;
+rows and columns of a matrix);
 ``t{i}/p0_sum`` and ``s{k}/t{i}/grad_sum`` are checksums of the
 regenerated inputs.  Entries of one shape across all tensors are stored
 stacked (``pack``).  Hash bin sums are accumulated in fp64 (the oracle's
@@ -41,7 +44,7 @@ CASES = {
     "c1_fp64": ("c1", dict(pool=10), 10, 10, 4096),
     # name: (recipe, recipe kwargs, steps, grad pool, samples per tensor)
     "c2_bench": ("c2", dict(pool=4), 25, 4, 2048),
-    "c3_840": ("c3", dict(pool=4), 4, 4, 16),
+    "c3_840": ("c3", dict(pool=4), 4, 4, 256),
     "c4_shapes": ("c4", dict(pool=2, shapes=bench.C4_SHAPES), 2, 2, 4096),
     "c5": ("c5", dict(pool=2), 2, 2, 4096),
 }
@@ -123,6 +126,11 @@ def run(name: str) -> None:
             dp = flat.double() - before[i]
             out[pre + "dsum"] = np.float64(dp.sum())
             out[pre + "dsumsq"] = np.float64((dp * dp).sum())
+            if recipe != "c3" and p.dtype == torch.float32:
+                full = dp.view(tuple(p.shape))
+                for a in range(p.ndim):
+                    others = tuple(d for d in range(p.ndim) if d != a)
+                    out[pre + f"dm{a}"] = (full.sum(dim=others) if others else full).numpy().copy()
             for key, v in opt.state[i].items():
                 # copies: the oracle updates its state tensors in place
                 out[pre + key] = v.numpy().copy() if torch.is_tensor(v) else np.int64(v)

@@ -10,10 +10,12 @@
   reference's golden vectors by tests/test_oracle_golden.py).
 
 At every step: every state tensor (fp32 tolerance), the param at sampled
-indices (fp32: rtol 1e-5 / atol 1e-6; bf16: within one ulp), the update
-dp = p_after - p_before at those indices against the oracle's, and, over the
-whole tensor, sum(dp) and sum(dp^2) in fp64 (an error in a few elements that
-the samples miss moves sum(dp) beyond its tolerance).
+indices (fp32: rtol 1e-5 / atol 1e-6; bf16: within one ulp; 256 per tensor at
+C3), the update dp = p_after - p_before at those indices against the
+oracle's, over the whole tensor sum(dp) and sum(dp^2) in fp64, and for fp32
+params of C1, C2, C4 and C5 the fp64 sums of dp along every axis (every row
+and column of a matrix), so an O(rms) error in a single element of any row
+or column that the samples miss exceeds its tolerance.
 """
 
 from __future__ import annotations
@@ -53,7 +55,7 @@ def _states_close(got: dict, z: dict, pre: str, what: str, tol=F32_TOL) -> None:
     keys = [k[len(pre):] for k in z if k.startswith(pre) and "/" not in k[len(pre):]]
     skip = {"sample", "sum", "sumsq", "dsum", "dsumsq", "grad_sum"}
     for k in keys:
-        if k in skip:
+        if k in skip or k.startswith("dm"):   # dm{a}: marginal sums of dp, checked in _check_param
             continue
         assert k in got, f"{what}: state {k} missing"
         v = got[k]
@@ -118,6 +120,24 @@ def _check_param(i, p, before, z, pre, idx, prev_sample, what, worst):
     np.testing.assert_allclose(dsq_g, dsq_e, rtol=1e-5, err_msg=f"{what}: sum(dp^2)")
     np.testing.assert_allclose(float(flat.double().pow(2).sum()), float(z[pre + "sumsq"]), rtol=1e-6,
                                err_msg=f"{what}: sum(p^2)")
+    # marginal sums of dp along every axis (each row and each column of a
+    # matrix), same tolerance per marginal of m elements: an O(rms) error in
+    # one element of a row or column exceeds it
+    full = dp.view(tuple(p.shape))
+    a = 0
+    while pre + f"dm{a}" in z:
+        exp_m = z[pre + f"dm{a}"].astype(np.float64)
+        others = tuple(d for d in range(p.ndim) if d != a)
+        got_m = (full.sum(dim=others) if others else full).cpu().numpy()
+        m = n // int(p.shape[a])
+        tol_m = 2e-7 * m * rms + 1e-4 * rms * m ** 0.5 + 1e-12
+        err = np.abs(got_m - exp_m) / tol_m
+        worst["dm"] = max(worst.get("dm", 0.0), float(err.max()))
+        bad = np.flatnonzero(err > 1.0)
+        assert bad.size == 0, (f"{what}: sums of dp along axis {a} differ at coordinates {bad[:8].tolist()} "
+                               f"(worst {err.max():.2f} x the tolerance)")
+        worst["marginals"] = worst.get("marginals", 0) + exp_m.size
+        a += 1
 
 
 def _run_oracle_vectors(name: str, maker, state_tol=F32_TOL, on_step=None):
@@ -150,7 +170,8 @@ def _run_oracle_vectors(name: str, maker, state_tol=F32_TOL, on_step=None):
         if on_step is not None:
             on_step(k, run, z)
     announce(f"{name}: worst update error {worst['dp']:.2e} of its scale, sum(dp) {worst['dsum']:.2e} of "
-             f"rms*sqrt(n), low-precision params: {100 * worst['frac']:.2f}% of samples differ")
+             f"rms*sqrt(n), {worst.get('marginals', 0)} marginal sums of dp (worst {worst.get('dm', 0.0):.2f} of the "
+             f"tolerance), low-precision params: {100 * worst['frac']:.2f}% of samples differ")
 
 
 def test_c1_against_reference_golden_and_fp64_oracle_10_steps():

@@ -464,3 +464,38 @@ def test_spectral_fp64_params(case):
     assert hp.dtype == torch.float64 and hopt.state[hp]["q_cos"].dtype == torch.float64
     assert oopt.route(op) == "spectral"
     compare([hp], hopt, [op], oopt, param_tol=F64_TOL, state_tol=F64_TOL, dp_rtol=DP_RTOL[torch.float64])
+
+
+def test_spectral_unaligned_param_and_grad():
+    """A param and grad that start one element past a 16-byte boundary (views
+    into larger buffers) on the matrix-core path: the element-wise form of the
+    update (no vector access) against the oracle."""
+    import cresso_amd
+    from gpu_util import _PREV
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    announce("spectral (512,512) param and grad at a 4-byte offset")
+    shape = (512, 512)
+    n = shape[0] * shape[1]
+    gen = torch.Generator().manual_seed(29)
+    p0 = 0.02 * torch.randn(shape, generator=gen)
+    kw = dict(rank=8, max_frequency=5, hash_bins=64, hash_tables=2)
+    pbuf = torch.zeros(n + 1, device="cuda")
+    pbuf[1:] = p0.reshape(-1).cuda()
+    hp = torch.nn.Parameter(pbuf[1:].view(shape))
+    assert hp.data_ptr() % 16 == 4
+    hopt = cresso_amd.CRESSO5([hp], cuda_ops="required", **kw)
+    op = p0.clone()
+    oopt = OracleCRESSO5([op], **kw)
+    gbuf = torch.zeros(n + 1, device="cuda")
+    for k in range(3):
+        g = 1e-3 * torch.randn(shape, generator=gen)
+        if k == 2:
+            torch.cuda.synchronize()
+            _PREV[hopt] = ([hp.detach().clone()], [op.clone()])
+        gbuf[1:] = g.reshape(-1).cuda()
+        hp.grad = gbuf[1:].view(shape)
+        hopt.step()
+        oopt.step([g])
+    torch.cuda.synchronize()
+    compare([hp], hopt, [op], oopt)
