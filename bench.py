@@ -208,11 +208,11 @@ def algorithmic_bytes(params):
     return sum(3 * p.element_size() * p.numel() for p in params), n
 
 
-def time_gpu(workload, steps, warmup):
+def time_gpu(workload, steps, warmup, maker=None):
     import cresso_amd
 
     device = torch.device("cuda:0")
-    params, grads, kwargs, shapes, _ = TIMING_MAKERS.get(workload, MAKERS[workload])(device)
+    params, grads, kwargs, shapes, _ = (maker or TIMING_MAKERS.get(workload, MAKERS[workload]))(device)
     nbytes, n = algorithmic_bytes(params)
     opt = cresso_amd.CRESSO5(params, cuda_ops="required", **kwargs)
     pool = len(grads)
@@ -242,8 +242,15 @@ def time_gpu(workload, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     total_ms = start.elapsed_time(end)
+    # host cost of the grad assignments alone (no optimizer work): what a
+    # caller that swaps grad sets every step pays on top of the step
+    t1 = time.perf_counter()
+    for k in range(steps):
+        for p, g in zip(params, grads[k % pool]):
+            p.grad = g
+    assign_ms = 1e3 * (time.perf_counter() - t1) / steps
     return dict(ms_per_step=total_ms / steps, wall_ms_per_step=1e3 * wall / steps, shapes=shapes, kwargs=kwargs,
-                nbytes=nbytes, n=n)
+                nbytes=nbytes, n=n, pool=pool, assign_ms=assign_ms)
 
 
 def copy_calibration(steps, warmup, nbytes=256 << 20):
@@ -642,8 +649,21 @@ def measure(workload, args):
                      "launch": "one optimizer step (the library's kernel sequence); mean over the timed region, "
                                "HIP events on the launch stream"},
     }
+    if workload == "c3":
+        # the same step with two grad sets alternating (840 p.grad assignments
+        # a step inside the timed region); the assignments' host cost alone
+        # is reported beside it
+        alt = time_gpu(workload, args.steps, args.warmup, maker=lambda device: make_c3(device, pool=2))
+        rec["alternating_grads"] = {"grad_sets": 2, "ms_per_step": round(alt["ms_per_step"], 4),
+                                    "host_grad_assignment_ms_per_step": round(alt["assign_ms"], 4),
+                                    "note": "840 p.grad assignments a step inside the timed region; the line's "
+                                            "value is timed with one grad set assigned before the first step"}
     if not args.no_cpu and workload in CPU_LEG:
         rec["cpu_baseline"], rec["parity"] = cpu_and_parity(workload)
+        if workload == "c2":
+            rec["cpu_baseline"]["note"] = ("the oracle sums the hash bins in fp64 (hash_accum='fp64'); the "
+                                           "reference's cuda_ops='off' path sums them sequentially in fp32, "
+                                           "the same torch ops otherwise")
     elif workload not in CPU_LEG:
         rec["parity"] = {"in_run": False, "covered_by": "tests/test_gpu_full_configs.py (oracle trajectories at "
                          "this config's shapes)"}
@@ -693,6 +713,8 @@ def main():
     if "cpu_baseline" in first:
         out["cpu_baseline"] = first["cpu_baseline"]
         out["parity"] = first["parity"]
+    if "alternating_grads" in first:
+        out["alternating_grads"] = first["alternating_grads"]
     if len(recs) > 1:
         # the metric names both headline configs: the second rides along with
         # the same fields (value = algorithmic GB/s, ms_per_step, roofline, CPU)
