@@ -118,6 +118,10 @@ struct Geom {
                                        // sweeps' atomic merges, else 1)
 };
 
+// 64-bit words of a plan's global density histogram: hcopies copies of the
+// [T][B] low words, then one [T][B] table of high words.
+__host__ __device__ inline int64_t hist_words(const Geom& g) { return (int64_t)(g.hcopies + 1) * g.T * g.B; }
+
 struct Offs {
     size_t axc, meta, csrc, rowtab, coltab, stats, bounds, gram, gpart, counts, cooc, bins;   // shape tables
     size_t tbuf, part, part1, sums, hist, hpart, lt, imp, rowfx, colfx, colfac, terms, ctrl, desc;   // per-step scratch
@@ -150,6 +154,7 @@ struct Ctrl {
     float rconst[4];
     float wpred[2 * SP_MAXR]; // weights of the pre-contact prediction on the normalized carriers
     double hs_ds, hs_P;       // fixed-point scales of the histograms
+    double hs_hi;             // weight of one unit of the density histogram's high words
     double cmax;              // largest bin count of any table (data independent, set at workspace init)
     float nscale, srms;
     // drive = k_rat rat + k_ths tanh(t/clip) + k_root root + k_t t + k_pred pred' + k_echo echo
@@ -157,7 +162,8 @@ struct Ctrl {
     float k_rat, k_ths, k_root, k_t, k_pred, k_echo, k_nov, k_hash, gain;
     float de_prev;            // drive_energy before this step (sweep 5 updates the state)
     float fr_prev;            // force_rms before this step (sweep 2 updates the state)
-    int32_t hard_hash, pad_;  // four-table closed form: the hard channel's hash term is on (set by fin3)
+    int32_t hard_hash;        // four-table closed form: the hard channel's hash term is on (set by fin3)
+    int32_t kq;               // 62 - ceil(log2 cmax): limit exponent of the density histogram's low words
     double hh_part[SP_HHP_MAX];   // four-table closed form: partial sums of sum_i hp_i^2 (hh4_kernel)
 };
 
@@ -1059,11 +1065,31 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(
 // and the scale.  Block 0 stores the new force RMS and the values later
 // kernels read from ctrl; the reservoir starts from ctrl->fr_prev (stashed by
 // sweep 1), so no block reads a value another block of this launch writes.
-// The density histogram's fixed-point scale comes from sweep 1's block maxima
-// of |f| (each block's row of part1 holds its sum, then its maximum).
+// The density histogram's fixed-point scales come from sweep 1's block sums
+// and maxima of f^2, |f| (each block's row of part1 holds its sum, then its
+// maximum).
+//
+// Density histogram: every bin holds a low and a high 64-bit word, value =
+// (low + high 2^k) / 2^F, each element adding y = rel^p 2^F.  Elements with
+// y < 2^k add rint(y) to the low word (one LDS atomic per table, the common
+// case); larger ones add floor(rel^p 2^-j) (j = k - F) to the high word and
+// the exact remainder to the low word.  F, k, j are chosen so that
+//   - the low words cannot overflow: either every element's y stays below
+//     2^k <= 2^(62 - ceil log2 cmax) (cmax elements per bin at most), or F
+//     is the single-word scale F0 for which a bin's whole sum stays below
+//     2^61 (bounds below);
+//   - the high words cannot overflow: sum rel^p 2^-j <= 2^60;
+//   - ordinary elements stay in the low word: 2^j >= 2^16 times a typical
+//     rel^p, from the mean of f^2 without each sweep-1 block's largest
+//     element (so that a few spikes near the rel clamp, at a large energy
+//     power, do not set the resolution of every other bin, as they do F0).
+// F is never below F0, so the resolution is never coarser than one word's.
 struct F1Values {
     float inv_s;
-    double hs_ds;
+    double hs_ds;   // 2^F
+    float yk, hq;   // 2^k, 2^-j
+    float kmf;      // k - F
+    bool hi_on;     // some element may reach the high words (rmax^p >= 2^(k - F))
 };
 // Sweep 1's block partials (sum, max) of one thread, blocks threadIdx.x +
 // i SP_NT: the first N loaded at once (indices clamped, so that no branch
@@ -1084,26 +1110,33 @@ struct F1Part {
 template <int N>
 __device__ F1Values fin1_values(const Geom& g, const F1Part<N>& fp, const double* __restrict__ part1,
                                 Ctrl* __restrict__ ctrl, float* __restrict__ fr_state, int step, const cresso_hyper& h) {
-    __shared__ double s_w[SP_NT / 64], s_m[SP_NT / 64];
-    double a = 0.0, mx = 0.0;
+    __shared__ double s_w[SP_NT / 64], s_x[SP_NT / 64], s_m[SP_NT / 64];
+    double a = 0.0, ax = 0.0, mx = 0.0;
 #pragma unroll
     for (int i = 0; i < N; ++i)
         if ((int)threadIdx.x + i * SP_NT < g.nblk1) {
             a += fp.s[i];
+            ax += fmax(fp.s[i] - fp.m[i] * fp.m[i], 0.0);
             mx = fmax(mx, fp.m[i]);
         }
     for (int b = threadIdx.x + N * SP_NT; b < g.nblk1; b += SP_NT) {
-        a += part1[(size_t)b * 2];
-        mx = fmax(mx, part1[(size_t)b * 2 + 1]);
+        const double sb = part1[(size_t)b * 2], mb = part1[(size_t)b * 2 + 1];
+        a += sb;
+        ax += fmax(sb - mb * mb, 0.0);
+        mx = fmax(mx, mb);
     }
-    const double w = wave_total_d(a);
+    const double w = wave_total_d(a), wx = wave_total_d(ax);
     for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
-    if ((threadIdx.x & 63) == 63) s_w[threadIdx.x >> 6] = w;
+    if ((threadIdx.x & 63) == 63) {
+        s_w[threadIdx.x >> 6] = w;
+        s_x[threadIdx.x >> 6] = wx;
+    }
     if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = mx;
     __syncthreads();
-    double sum = 0.0;
+    double sum = 0.0, sumx = 0.0;
     for (int i = 0; i < SP_NT / 64; ++i) {
         sum += s_w[i];
+        sumx += s_x[i];
         mx = fmax(mx, s_m[i]);
     }
     const float eps = (float)h.eps;
@@ -1112,17 +1145,17 @@ __device__ F1Values fin1_values(const Geom& g, const F1Part<N>& fp, const double
     const float sc = fmaxf(fr, eps);
     F1Values v;
     v.inv_s = 1.0f / sc;
-    // Density histogram scale: every bin's sum of ds = rel^p, rel = min(|f|/s
-    // + eps, 1e4), times the scale stays below 2^61 (rounding adds at most
-    // half a unit per element).  A bin's sum is at most the smaller of
+    // Single-word scale F0: every bin's sum of ds = rel^p, rel = min(|f|/s +
+    // eps, 1e4), times 2^F0 stays below 2^61 (rounding adds at most half a
+    // unit per element).  A bin's sum is at most the smaller of
     //   cmax rmax^p                                 (cmax elements, each <= rmax^p)
     //   sum_i rel_i^p <= rmax^(p-2) S2              (p >= 2)
     //                 <= n^(1-p/2) S2^(p/2)         (p < 2, power means)
     // with S2 = sum_i rel_i^2 <= sum f^2/s^2 + 2 eps sqrt(n sum f^2)/s + n eps^2
-    // from sweep 1's sums.  The second bound keeps the resolution of ordinary
-    // bins when a few elements reach rel near 1e4 at a large energy power.
+    // from sweep 1's sums; the smaller bound (l2b, log2) also bounds the
+    // whole histogram's sum, which sizes the high words.
     // (fp32 hardware log2 with margins for it and for the sweep's exp2/log2 of
-    // rel^p; every block computes the same bound)
+    // rel^p; every block computes the same values)
     const float rmax = fminf(fmaf((float)mx, v.inv_s, eps), 1.0e4f);
     const float pw = (float)h.energy_power;
     const float lr = flog2(rmax);
@@ -1131,13 +1164,29 @@ __device__ F1Values fin1_values(const Geom& g, const F1Part<N>& fp, const double
     const float l2s = flog2((float)s2 + 1.0e-30f);
     const float l2tot = pw >= 2.0f ? (pw - 2.0f) * lr + l2s : (1.0f - 0.5f * pw) * flog2((float)dn) + 0.5f * pw * l2s;
     const float l2bin = pw * lr + flog2((float)ctrl->cmax);
-    const int ex = (int)floorf(61.0f - fminf(l2bin, l2tot) - 0.05f);
-    v.hs_ds = ldexp(1.0, ex < 120 ? ex : 120);   // the scale itself stays a finite fp32 value
+    const float l2b = fminf(l2bin, l2tot);
+    // (exponents clamped as floats, so that infinite or NaN bounds convert)
+    const int f0 = (int)fminf(fmaxf(floorf(61.0f - l2b - 0.05f), -120.0f), 120.0f);
+    // two-word scale: the low words' limit 2^kq, the high words' weight 2^j
+    const int kq = ctrl->kq;
+    const float rtyp = sqrtf((float)(sumx * g.inv_n)) * v.inv_s + eps;   // typical rel
+    const int j = (int)fminf(fmaxf(ceilf(fmaxf(pw * flog2(rtyp) + 16.0f, l2b - 60.0f + 0.05f)), -100.0f), 100.0f);
+    int F = kq - j > f0 ? kq - j : f0;
+    F = F < 120 ? F : 120;   // 2^F stays a finite fp32 value
+    const int k = F + j < 62 ? F + j : 62;
+    v.hs_ds = ldexp(1.0, F);
+    v.yk = ldexpf(1.0f, k);
+    v.hq = ldexpf(1.0f, -j);
+    // the sweeps test elements against 2^k only when the largest one can
+    // reach it (margin 0.05 in log2 units for the hardware log2/exp2 of rel^p)
+    v.kmf = (float)(k - F);
+    v.hi_on = pw * lr + 0.05f >= v.kmf;
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         *fr_state = fr;
         ctrl->scale = sc;
         ctrl->inv_s = v.inv_s;
-        ctrl->hs_ds = v.hs_ds;   // fin2 converts the histogram back with it
+        ctrl->hs_ds = v.hs_ds;   // fin2 converts the histogram back with these
+        ctrl->hs_hi = ldexp(1.0, j);
     }
     return v;
 }
@@ -1534,6 +1583,52 @@ __device__ __forceinline__ uint64_t load_bins_at(const unsigned char* __restrict
     }
 }
 
+// A value every thread of the wave holds, moved to a scalar register.
+__device__ __forceinline__ float uniform_f(float x) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+// Density of one element: rel = min(|f|/s + eps, 1e4), f = sign grad (+
+// weight decay param), and ds = rel^p.  The full-tile form (no weight decay,
+// instant-metric power 1) writes rel with one fma.  A sweep computes an
+// element's density with the same helpers in its loop and again in its
+// high-word pass, which must reproduce the loop's values exactly.
+__device__ __forceinline__ float force_of(float gv, float pv, float sg, float wd, bool wd_on) {
+    float f = sg * gv;
+    if (wd_on) f = f + wd * pv;
+    return f;
+}
+__device__ __forceinline__ float rel_gen(float f, float inv_s, float eps) { return fminf(fabsf(f) * inv_s + eps, 1.0e4f); }
+__device__ __forceinline__ float rel_full(float x, float inv_s, float eps) { return fminf(fmaf(fabsf(x), inv_s, eps), 1.0e4f); }
+// An element whose y = ds 2^F reached 2^k: the sweep's loop added 2^k
+// (lo_k, y clamped) to its low word; the high-word pass adds the high word
+// floor(q), q = ds 2^-j, and (q - floor q) 2^k - 2^k to the low word (mod
+// 2^64: the bin's final low sum is in range, so the wrapped partial sums
+// come out exact).  Both parts are exact in fp32 (scalings by powers of two,
+// the fraction of q).
+struct HiSplit {
+    unsigned long long hi, lo;
+};
+__device__ __forceinline__ HiSplit hi_split(float ds, float hq, float yk, unsigned long long lo_k) {
+    const float q = ds * hq, qi = floorf(q);
+    return HiSplit{to_fixed_u(qi), to_fixed_u((q - qi) * yk) - lo_k};
+}
+
+// Whether a block's elements may include one whose y reached 2^k: sweep 1's
+// maxima of |f| over the chunks that the block's flat index range [base,
+// base + (nr - 1) cols + SP_NT) touches, with hi_on's margin.  A spike thus
+// sends the blocks of its panel rows (not every block) through the
+// high-word pass.  Every thread of the block calls it (a barrier).
+__device__ __forceinline__ bool hi_block(const Geom& g, const double* __restrict__ part1, int64_t base, int nr,
+                                         float inv_s, float eps, float pw, float kmf) {
+    const int64_t c0 = base / g.chunk1;
+    int64_t c1 = (base + (int64_t)(nr - 1) * g.cols + SP_NT - 1) / g.chunk1;
+    c1 = c1 < g.nblk1 - 1 ? c1 : g.nblk1 - 1;
+    int hit = 0;
+    for (int64_t c = c0 + threadIdx.x; c <= c1; c += SP_NT)
+        hit |= pw * flog2(rel_full((float)part1[c * 2 + 1], inv_s, eps)) + 0.05f >= kmf ? 1 : 0;
+    return __syncthreads_or(hit) != 0;
+}
+
 // Panel arrays of a full tile as buffer views: one descriptor per array (the
 // panel's first element as base), the lane's column as the VGPR offset and the
 // row as a uniform SGPR offset, so the row loop needs no address arithmetic.
@@ -1727,8 +1822,9 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
             b0[u] = ldb_bins16(bnv, u);
         }
     }
-    // LDS: histogram [T][B] u64 | row-sum partials [16][PR] (MODE 0: [4 waves][PR];
-    // MODE 1: [4 waves][4 DPP rows][PR]) | MODE 1 row factors [PR][RW]
+    // LDS: histogram [T][B] u64 (low words; MODE 1: [T][B][SP_NHIST] copies) |
+    // row-sum partials [16][PR] (MODE 0: [4 waves][PR]; MODE 1: [4 waves][4
+    // DPP rows][PR]) | MODE 1 row factors [PR][RW]
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
     float* s_wrow = reinterpret_cast<float*>(dyn + sizeof(unsigned long long) * SP_NHIST * (size_t)TB);
     constexpr int NH = MODE == 1 ? SP_NHIST : 1;   // histogram copies in use
@@ -1747,7 +1843,9 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
     const bool ip_one = ipw == 1.0f;
     const float wd = (float)h.weight_decay;
     const float sg = h.maximize ? -1.f : 1.f;
-    const float hs = (float)f1.hs_ds;
+    // (every thread holds the same values: scalar registers)
+    const float hs = (float)f1.hs_ds, yk = uniform_f(f1.yk), hq = uniform_f(f1.hq), kmf = uniform_f(f1.kmf);
+    const bool hi_on = __builtin_amdgcn_readfirstlane((int)f1.hi_on) != 0;   // uniform: a scalar branch
     float Z[RW];
 #pragma unroll
     for (int q = 0; q < RW; ++q) Z[q] = 0.f;
@@ -1771,7 +1869,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
 #pragma unroll
                     for (int v8 = 0; v8 < 8; ++v8) {
                         const int u = 8 * h8 + v8;
-                        const float rel = fminf(fmaf(fabsf(x[u]), inv_s, eps), 1.0e4f);
+                        const float rel = rel_full(x[u], inv_s, eps);
                         const float ds = fexp2(pw * flog2(rel));
                         const float L = flog2(1.0f + ds);
                         dn[v8] = rel;
@@ -1780,7 +1878,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
                         const float* __restrict__ ar = s_ar + (i0 + u) * RW;
 #pragma unroll
                         for (int q = 0; q < RW; ++q) Z[q] = fmaf(ar[q], L, Z[q]);
-                        const unsigned long long v = to_fixed_u(ds * hs);
+                        const unsigned long long v = to_fixed_u(fminf(ds * hs, yk));   // high words: hi_pass
                         atomicAdd(&s_hist[bin_of(bv[u], 0, 1) * NH + hc], v);
                         atomicAdd(&s_hist[(B + bin_of(bv[u], 1, 1)) * NH + hc], v);
 #pragma unroll
@@ -1817,9 +1915,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
             if (lr >= nr) break;
             float dens = 0.f;
             if (t.colok) {
-                float f = sg * gv[u];
-                if (F.wd_on) f = f + wd * pv[u];
-                const float rel = fminf(fabsf(f) * inv_s + eps, 1.0e4f);
+                const float rel = rel_gen(force_of(gv[u], pv[u], sg, wd, F.wd_on), inv_s, eps);
                 const float ds = fpow(rel, pw);
                 const float L = flog2(1.0f + ds);
                 const float rl = fmaxf(rel, eps);
@@ -1830,7 +1926,7 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
 #pragma unroll
                 for (int q = 0; q < RW; ++q) Z[q] += ar[q] * L;
                 if (F.hash_on) {
-                    const unsigned long long v = to_fixed_u(ds * hs);
+                    const unsigned long long v = to_fixed_u(fminf(ds * hs, yk));   // high words: hi_pass
 #pragma unroll
                     for (int tt = 0; tt < SP_MAXT; ++tt) {
                         if (tt >= F.T) break;
@@ -1843,6 +1939,33 @@ __global__ __launch_bounds__(SP_NT, RM >= 16 ? 2 : 4) void sweep2_kernel(
                 if (lane == 63) s_wrow[wave * g.PR + lr] = ws;
             }
             if (MODE == 0) elem_fence();
+        }
+    }
+    if (F.hash_on && hi_on && hi_block(g, part1, base, nr, inv_s, eps, pw, kmf) && t.colok) {
+        // high-word pass: the thread's elements again
+        const unsigned long long lo_k = to_fixed_u(yk);   // what the loop added for y >= 2^k
+        for (int lr = 0; lr < nr; ++lr) {
+            const uint32_t o = panel_off(g, lr);
+            float ds;
+            if constexpr (MODE == 1) {
+                ds = fexp2(pw * flog2(rel_full(to_f(gb[o]), inv_s, eps)));
+            } else {
+                const float pvv = F.wd_on ? to_f(pb[o]) : 0.f;
+                ds = fpow(rel_gen(force_of(to_f(gb[o]), pvv, sg, wd, F.wd_on), inv_s, eps), pw);
+            }
+            if (ds * hs >= yk) {
+                // MODE 1: two tables of one-byte bins, histogram copy threadIdx.x mod SP_NHIST
+                const uint64_t bb = MODE == 1 ? (uint64_t)(reinterpret_cast<const uint16_t*>(bins) + base)[o]
+                                              : load_bins_at(bins, base, o, F.binbytes);
+                const int nt = MODE == 1 ? 2 : F.T, bpb = MODE == 1 ? 1 : F.bpb;
+                const int hcm = MODE == 1 ? (int)(threadIdx.x & (SP_NHIST - 1)) : 0;
+                const HiSplit sp = hi_split(ds, hq, yk, lo_k);
+                for (int tt = 0; tt < nt; ++tt) {
+                    const int bin = tt * B + bin_of(bb, tt, bpb);
+                    atomicAdd(&hist[(size_t)g.hcopies * TB + bin], sp.hi);   // the high-word table
+                    atomicAdd(&s_hist[bin * NH + hcm], sp.lo);
+                }
+            }
         }
     }
     __syncthreads();
@@ -2027,14 +2150,14 @@ template <int RM, int KC, typename GT, int TT>
 __global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
     Geom g, const GT* __restrict__ grad, const float* __restrict__ rowtab, const float* __restrict__ coltab,
     const ModeMeta* __restrict__ meta, const unsigned char* __restrict__ bins, Ctrl* __restrict__ ctrl,
-    double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ rowfx,
-    unsigned long long* __restrict__ colfx, const double* __restrict__ part1, float* __restrict__ fr_state, int step,
-    Lanes L, cresso_hyper h, int one_round, int hdirect) {
+    double* __restrict__ part, unsigned long long* __restrict__ hist, unsigned long long* __restrict__ hhi,
+    unsigned long long* __restrict__ rowfx, unsigned long long* __restrict__ colfx, const double* __restrict__ part1,
+    float* __restrict__ fr_state, int step, Lanes L, cresso_hyper h, int one_round, int hdirect) {
     if (L.dv) {
         const cresso_spectral_desc& d = lane_desc(L);
         grad = (const GT*)d.grad; fr_state = (float*)d.force_rms; step = d.step;
     }
-    ctrl = lane_at(ctrl, L); part = lane_at(part, L); hist = lane_at(hist, L);
+    ctrl = lane_at(ctrl, L); part = lane_at(part, L); hist = lane_at(hist, L); hhi = lane_at(hhi, L);
     rowfx = lane_at(rowfx, L); colfx = lane_at(colfx, L); part1 = lane_at(part1, L);
     static_assert(RM <= 16, "two 16-row tiles of projection rows at most");
     constexpr int RW = 2 * RM;
@@ -2069,7 +2192,7 @@ __global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
     };
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc) load_tile(0, tc);
-    // LDS: histogram copies [TB][NH] u64 | row-sum partials [4 waves][PR] | row factors [PR][RW]
+    // LDS: histogram copies [TB][NH] u64 (low words) | row-sum partials [4 waves][PR] | row factors [PR][RW]
     constexpr int NH = SP_NHIST;
     const int hc = (int)(threadIdx.x & (SP_NHIST - 1));
     unsigned long long* s_hist = reinterpret_cast<unsigned long long*>(dyn);
@@ -2094,8 +2217,9 @@ __global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
     const float inv_s = f1.inv_s;
     const float eps = (float)h.eps;
     const float pw = (float)h.energy_power;
-    const float sg = h.maximize ? -1.f : 1.f;
-    const float hs = (float)f1.hs_ds;
+    // (every thread holds the same values: scalar registers)
+    const float hs = (float)f1.hs_ds, yk = uniform_f(f1.yk), hq = uniform_f(f1.hq), kmf = uniform_f(f1.kmf);
+    const bool hi_on = __builtin_amdgcn_readfirstlane((int)f1.hi_on) != 0;   // uniform: a scalar branch
     // the lane's projection A operands, a_{16 qt + li}(row 16 tr + 4 lg + r),
     // held in registers: read from LDS inside the loop they would queue
     // behind the histogram atomics (LDS operations complete in order)
@@ -2131,14 +2255,15 @@ __global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 // full tile: rel >= eps and instant-metric power 1, so the density is rel
-                const float rel = fminf(fmaf(fabsf(sg * x[r]), inv_s, eps), 1.0e4f);
+                // (|sign x| = |x|)
+                const float rel = rel_full(x[r], inv_s, eps);
                 const float ds = fexp2(pw * flog2(rel));
                 const float L = flog2(1.0f + ds);
                 Ls[r] = L;
                 aL += L;
                 rs[r] += rel;
                 cD[tc] += rel;
-                const unsigned long long v = to_fixed_u(ds * hs);
+                const unsigned long long v = to_fixed_u(fminf(ds * hs, yk));   // high words: hi_pass
 #pragma unroll
                 for (int tt = 0; tt < TT; ++tt) atomicAdd(&s_hist[(tt * B + bin_byte<TT>(b[r], tt)) * NH + hc], v);
             }
@@ -2161,6 +2286,27 @@ __global__ __launch_bounds__(SP_NT, (occ2m<RM, KC>())) void sweep2m_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) rt[r] = row16_total(rs[r]);
         if (li < 4) s_wrow[wv * g.PR + 16 * tr + 4 * lg + li] = li == 0 ? rt[0] : (li == 1 ? rt[1] : (li == 2 ? rt[2] : rt[3]));
+    }
+    if (hi_on && hi_block(g, part1, base, nr, inv_s, eps, pw, kmf)) {
+        // high-word pass: the lane's elements again
+        const unsigned long long lo_k = to_fixed_u(yk);   // what the loop added for y >= 2^k
+        for (int tr = 0; tr < ntr; ++tr)
+            for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t o = tile_off(tr, tc, r);
+                    const float ds = fexp2(pw * flog2(rel_full(ldg_el<GT>(rg, vg, o * (uint32_t)sizeof(GT)), inv_s, eps)));
+                    if (ds * hs >= yk) {
+                        const uint32_t bb = ldg_bins<TT>(rb, vb, o * (uint32_t)TT);
+                        const HiSplit sp = hi_split(ds, hq, yk, lo_k);
+#pragma unroll
+                        for (int tt = 0; tt < TT; ++tt) {
+                            const int bin = tt * B + (int)bin_byte<TT>(bb, tt);
+                            atomicAdd(&hhi[bin], sp.hi);   // the high-word table (global)
+                            atomicAdd(&s_hist[bin * NH + hc], sp.lo);
+                        }
+                    }
+                }
     }
     __syncthreads();
     // axis density sums: one fixed-point atomic per row of this slab and per column of this panel
@@ -2324,7 +2470,12 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
         constexpr unsigned nw1 = SP_FN_NT / 64 - 1;
         for (int i = t1; i < TB; i += n1) {
             const double cnt = (double)counts[i];
-            const float cell = (float)((double)(long long)take_hist(hist, TB, i, nc) / ctrl->hs_ds / fmax(cnt, 1.0));
+            // low words (every copy) plus the high word, each cleared for the next step
+            unsigned long long* hhi = hist + (size_t)g.hcopies * TB + i;
+            const unsigned long long hv = *hhi;
+            *hhi = 0ull;
+            const double lo = (double)(long long)take_hist(hist, TB, i, nc) / ctrl->hs_ds;
+            const float cell = (float)(fma((double)hv, ctrl->hs_hi, lo) / fmax(cnt, 1.0));
             float e = st.hash_energy[i];
             e = step <= 1 ? cell : e * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * cell;
             st.hash_energy[i] = e;
@@ -4119,6 +4270,7 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     double* part = at<double>(ws, o.part);
     double* sums = at<double>(ws, o.sums);
     unsigned long long* hist = at<unsigned long long>(ws, o.hist);
+    unsigned long long* hhi = hist + (size_t)g.hcopies * g.T * g.B;   // the density histogram's high words
     unsigned long long* hpart = at<unsigned long long>(ws, o.hpart);
     const unsigned long long* cooc = at<unsigned long long>(ws, o.cooc);
     float* lt = at<float>(ws, o.lt);
@@ -4178,10 +4330,10 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     if (m2) {
         if (t4)
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 4>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hd2 ? hist : hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2, hd2);
+                               part, hd2 ? hist : hpart, hhi, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2, hd2);
         else
             hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 2>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hd2 ? hist : hpart, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2, hd2);
+                               part, hd2 ? hist : hpart, hhi, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2, hd2);
     } else if (fast) {
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);

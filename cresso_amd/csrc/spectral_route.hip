@@ -212,7 +212,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     o.part = take(sizeof(double) * (size_t)NVMAX * std::max(g.nblk, g.nblk1));
     o.part1 = take(sizeof(double) * 2 * (size_t)g.nblk1);   // sweep 1's sums and maxima, read by every block of sweep 2
     o.sums = take(sizeof(double) * (size_t)NVMAX);
-    o.hist = take(sizeof(unsigned long long) * (size_t)g.hcopies * g.T * g.B);
+    o.hist = take(sizeof(unsigned long long) * (size_t)hist_words(g));   // low-word copies, then the high words
     // per-block histogram partials of the matrix-core sweeps (two or four tables of one-byte bins)
     o.hpart = take(mtables(g) ? sizeof(unsigned long long) * (size_t)g.T * g.B * g.nblk : 0);
     o.lt = take(sizeof(float) * (size_t)g.T * g.B);
@@ -242,7 +242,11 @@ __global__ void ws_cmax_kernel(const unsigned long long* __restrict__ counts, in
         if ((int)threadIdx.x < w && s[threadIdx.x + w] > s[threadIdx.x]) s[threadIdx.x] = s[threadIdx.x + w];
         __syncthreads();
     }
-    if (threadIdx.x == 0) ctrl->cmax = bins_off ? (double)n : (double)s[0];
+    if (threadIdx.x == 0) {
+        const unsigned long long c = bins_off ? (unsigned long long)n : s[0];
+        ctrl->cmax = (double)c;
+        ctrl->kq = 62 - (c > 1 ? 64 - __clzll((long long)(c - 1)) : 0);   // 62 - ceil(log2 cmax)
+    }
 }
 
 __global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
@@ -313,8 +317,8 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
                        at<double>(ws, o.gpart), at<double>(ws, o.gram));
     const int64_t TB = (int64_t)g.T * g.B;
     hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((TB + 255) / 256)), dim3(256), 0, s, at<unsigned long long>(ws, o.counts), TB);
-    hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((g.hcopies * TB + 255) / 256)), dim3(256), 0, s,
-                       at<unsigned long long>(ws, o.hist), g.hcopies * TB);
+    hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)((hist_words(g) + 255) / 256)), dim3(256), 0, s,
+                       at<unsigned long long>(ws, o.hist), hist_words(g));
     const int64_t bins_blocks = std::max<int64_t>(1, std::min<int64_t>(2048, (g.n + 255) / 256));
     hipLaunchKernelGGL(ws_bins_kernel, dim3((unsigned)bins_blocks), dim3(256), 0, s, g, at<unsigned char>(ws, o.bins),
                        at<unsigned long long>(ws, o.counts));
@@ -462,7 +466,7 @@ extern "C" int32_t cresso_spectral_batched_workspace_init(const cresso_spectral_
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const Offs& o = P->o;
     hipLaunchKernelGGL(ws_lanes_kernel, dim3((unsigned)(count - 1)), dim3(256), 0, s, at<unsigned char>(ws, o.tbuf),
-                       lane_stride(P), o.ctrl - o.tbuf, o.hist - o.tbuf, (int64_t)P->g.hcopies * P->g.T * P->g.B);
+                       lane_stride(P), o.ctrl - o.tbuf, o.hist - o.tbuf, hist_words(P->g));
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route: batched workspace init");

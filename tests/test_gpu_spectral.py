@@ -80,23 +80,40 @@ def test_spectral_c2_shape_large_energy_power(power):
     compare([hp], hopt, [op], oopt)
 
 
-def test_spectral_energy_power_4_spike_after_quiet_steps():
-    """energy_power 4 at 4096^2: three quiet steps, then one element at about
-    2000 times the lagging force-RMS reservoir (rel^4 ~ 1.6e13 against ~0.5
-    for ordinary elements).  The density histogram's fixed-point scale takes
-    the tighter of the per-bin bound (cmax rmax^p) and the whole-histogram
-    bound from sweep 1's sum of squares, so the ordinary bins keep their
-    resolution next to the spike's bin (the per-bin bound alone left a quantum
-    of 4 here).  Oracle bin sums in fp64."""
+SPIKE_CASES = [
+    # name, shape, energy_power, spike elements and values
+    # about 2000 times the lagging force-RMS reservoir (rel^4 ~ 1.6e13)
+    ("p4_4096sq_x2000", (4096, 4096), 4.0, [((1234, 567), 3.0)]),
+    # at the rel clamp 1e4 (rel^4 = 1e16): one spike, then five in five sweep-1
+    # blocks (16384 elements, four rows of 4096, each)
+    ("p4_4096sq_clamp", (4096, 4096), 4.0, [((1234, 567), 30.0)]),
+    ("p4_4096sq_clamp_x5", (4096, 4096), 4.0, [((100 + 700 * i, 37 * i + 5), 30.0) for i in range(5)]),
+    # the general sweeps (odd column count) and the matrix-core sweeps with
+    # 32-row panels, energy power 6
+    ("p4_300x257_clamp", (300, 257), 4.0, [((17, 200), 30.0)]),
+    ("p6_1024x768_spike", (1024, 768), 6.0, [((700, 3), 10.0)]),
+]
+
+
+@pytest.mark.parametrize("case", SPIKE_CASES, ids=[c[0] for c in SPIKE_CASES])
+def test_spectral_large_energy_power_spike_after_quiet_steps(case):
+    """Three quiet steps (grad std 1e-3), then a step with spikes far above the
+    lagging force-RMS reservoir at a large energy power.  The density
+    histogram keeps two words per bin: ordinary elements add to the low word
+    at a scale set from the step's typical density, the spikes' rel^p splits
+    into a high word and an exact remainder.  A single word sized for the
+    spikes' sum leaves the ordinary bins a quantum near 2^-7 (relative errors
+    of 1e-5 to 1e-4 in the hash energy at p = 4 and rel = 1e4).  Oracle bin
+    sums in fp64, state within the fp32 tolerance."""
     import cresso_amd
     from gpu_util import _PREV
     from oracle.cresso_oracle import OracleCRESSO5
 
-    announce("spectral 4096x4096 energy_power 4, spike after quiet steps")
+    name, shape, power, spikes = case
+    announce(f"spectral {name} {shape} energy_power {power}, spikes after quiet steps")
     gen = torch.Generator().manual_seed(23)
-    shape = (4096, 4096)
     p0 = 0.02 * torch.randn(shape, generator=gen)
-    kw = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2, energy_power=4.0)
+    kw = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2, energy_power=power)
     hp = torch.nn.Parameter(p0.clone().cuda())
     hopt = cresso_amd.CRESSO5([hp], cuda_ops="required", **kw)
     op = p0.clone()
@@ -104,7 +121,8 @@ def test_spectral_energy_power_4_spike_after_quiet_steps():
     for k in range(4):
         g = 1e-3 * torch.randn(shape, generator=gen)
         if k == 3:
-            g[1234, 567] = 3.0   # ~2000x the reservoir's rms after three quiet steps
+            for idx, val in spikes:
+                g[idx] = val
             torch.cuda.synchronize()
             _PREV[hopt] = ([hp.detach().clone()], [op.clone()])
         hp.grad = g.cuda()
