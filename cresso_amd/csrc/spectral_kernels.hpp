@@ -61,7 +61,7 @@ namespace cresso {
 namespace {
 
 constexpr int SP_NT = 256;
-constexpr int SP_MAXR = 16;
+constexpr int SP_MAXR = 32;
 constexpr int SP_MAXT = 8;
 constexpr int SP_FIN_NT = 1024;  // workspace set-up kernels
 constexpr int SP_FN_NT = 512;    // per-step finalize kernels (room for fp64 accumulators)
@@ -4306,7 +4306,9 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
         hipLaunchKernelGGL((sweep1_kernel<PT, GT, false>), grid1, blk, 0, s, g, grad, param, part1, rowfx, colfx, ctrl,
                            st.force_rms, L, h);
     const bool fast = fast_mode(g, hash_on, axes_on, h);    // MODE 1 tiles of the general sweeps (two tables)
-    const bool mf = mfast_mode(g, hash_on, axes_on, h);     // the matrix-core sweeps (two or four tables)
+    // the matrix-core sweeps (two or four tables; ranks up to 16: two 16-row projection tiles)
+    constexpr bool MX = RM <= 16;
+    const bool mf = MX && mfast_mode(g, hash_on, axes_on, h);
     const bool t4 = g.T == 4;
     // the matrix-core sweeps write per-block histogram partials (hpart),
     // which part_reduce sums into hist; the general sweeps add into hist
@@ -4328,12 +4330,16 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     const int prh = pr_hist_rows(g.T * g.B, g.nblk) > 0;
     const int nc2 = (hd2 || (m2 && prh)) ? g.hcopies : 1, nc3 = (hd3 || (m3 && prh)) ? g.hcopies : 1;
     if (m2) {
-        if (t4)
-            hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 4>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hd2 ? hist : hpart, hhi, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2, hd2);
-        else
-            hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 2>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               part, hd2 ? hist : hpart, hhi, rowfx, colfx, part1, st.force_rms, step, L, h, one_round2, hd2);
+        if constexpr (MX) {
+            if (t4)
+                hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 4>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins,
+                                   ctrl, part, hd2 ? hist : hpart, hhi, rowfx, colfx, part1, st.force_rms, step, L, h,
+                                   one_round2, hd2);
+            else
+                hipLaunchKernelGGL((sweep2m_kernel<RM, KC, GT, 2>), grid, blk, l2, s, g, grad, rowtab, coltab, meta, bins,
+                                   ctrl, part, hd2 ? hist : hpart, hhi, rowfx, colfx, part1, st.force_rms, step, L, h,
+                                   one_round2, hd2);
+        }
     } else if (fast) {
         hipLaunchKernelGGL((sweep2_kernel<RM, KC, PT, GT, 1>), grid, blk, l2, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, part, hist, rowfx, colfx, hash_on, axes_on, part1, st.force_rms, step, L, h);
@@ -4354,13 +4360,15 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
                            0, s, g, terms, colfac, L);
     }
     if (m3) {
-        const size_t l3m = lds_sweep3m<KC>(g, 2 * RM);
-        if (t4)
-            hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 4>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               lt, rowfx, colfx, colfac, tbuf, part, hd3 ? hist : hpart, L, h, one_round3, hd3);
-        else
-            hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 2>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins, ctrl,
-                               lt, rowfx, colfx, colfac, tbuf, part, hd3 ? hist : hpart, L, h, one_round3, hd3);
+        if constexpr (MX) {
+            const size_t l3m = lds_sweep3m<KC>(g, 2 * RM);
+            if (t4)
+                hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 4>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins,
+                                   ctrl, lt, rowfx, colfx, colfac, tbuf, part, hd3 ? hist : hpart, L, h, one_round3, hd3);
+            else
+                hipLaunchKernelGGL((sweep3m_kernel<RM, KC, GT, 2>), grid, blk, l3m, s, g, grad, rowtab, coltab, meta, bins,
+                                   ctrl, lt, rowfx, colfx, colfac, tbuf, part, hd3 ? hist : hpart, L, h, one_round3, hd3);
+        }
     } else if (fast) {
         hipLaunchKernelGGL((sweep3_kernel<RM, KC, PT, GT, 1>), grid, blk, l3, s, g, grad, param, rowtab, coltab, meta, bins,
                            ctrl, lt, rowfx, colfx, colfac, tbuf, part, hist, hash_on, L, h);
@@ -4381,24 +4389,27 @@ int32_t run_step(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, 
     // the field is 4-row interleaved when sweep 3m wrote it (then sweep 4m
     // runs too, in place, and sweep 5q applies it)
     const bool q4 = m3 && c5c != 0;
-    if (c5c == 1 && q4)
-        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
-                           tbuf, part, echo_on, L, h, one_round4);
-    else if (c5c == 1)
-        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
-                           tbuf, part, echo_on, L, h, one_round4);
-    else if (c5c == 2 && q4)
-        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
-                           tbuf, part, echo_on, L, h, one_round4);
-    else if (c5c == 2)
-        hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp,
-                           tbuf, part, echo_on, L, h, one_round4);
-    else if (fast)
-        hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
-                           hash_on, echo_on, L, h);
-    else
-        hipLaunchKernelGGL((sweep4_kernel<RM, KC, 0>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf, part,
-                           hash_on, echo_on, L, h);
+    if (!MX || c5c == 0) {
+        if (fast)
+            hipLaunchKernelGGL((sweep4_kernel<RM, KC, 1>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf,
+                               part, hash_on, echo_on, L, h);
+        else
+            hipLaunchKernelGGL((sweep4_kernel<RM, KC, 0>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl, imp, tbuf,
+                               part, hash_on, echo_on, L, h);
+    } else if constexpr (MX) {
+        if (c5c == 1 && q4)
+            hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl,
+                               imp, tbuf, part, echo_on, L, h, one_round4);
+        else if (c5c == 1)
+            hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 2, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl,
+                               imp, tbuf, part, echo_on, L, h, one_round4);
+        else if (q4)
+            hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, true>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl,
+                               imp, tbuf, part, echo_on, L, h, one_round4);
+        else
+            hipLaunchKernelGGL((sweep4m_kernel<RM, KC, 4, false>), grid, blk, l4, s, g, rowtab, coltab, meta, bins, ctrl,
+                               imp, tbuf, part, echo_on, L, h, one_round4);
+    }
     const bool hash5 = hash_on && !c5c;   // sweep 5 adds the hash term itself
     const size_t l5 = hash5 ? sizeof(float) * (size_t)g.T * g.B : 0;
     if (q4 && pv4)
@@ -4428,12 +4439,13 @@ template <typename PT, typename GT>
 int32_t spectral_run(const cresso_spectral_plan& P, const cresso_spectral_desc* hd, int count,
                      const cresso_spectral_desc* dv, size_t ls, void* ws, const cresso_hyper& h, hipStream_t s) {
     const int R = P.g.R, K = P.g.K;
-    const int var = (R <= 4 && K <= 9) ? 0 : (R <= 8 && K <= 11) ? 1 : (R <= 8) ? 2 : 3;
+    const int var = (R <= 4 && K <= 9) ? 0 : (R <= 8 && K <= 11) ? 1 : (R <= 8) ? 2 : (R <= 16) ? 3 : 4;
     switch (var) {
         case 0: return run_step<4, 9, PT, GT>(P, hd, count, dv, ls, ws, h, s);
         case 1: return run_step<8, 11, PT, GT>(P, hd, count, dv, ls, ws, h, s);
         case 2: return run_step<8, 17, PT, GT>(P, hd, count, dv, ls, ws, h, s);
-        default: return run_step<16, 33, PT, GT>(P, hd, count, dv, ls, ws, h, s);
+        case 3: return run_step<16, 33, PT, GT>(P, hd, count, dv, ls, ws, h, s);
+        default: return run_step<32, 65, PT, GT>(P, hd, count, dv, ls, ws, h, s);   // general sweeps only
     }
 }
 

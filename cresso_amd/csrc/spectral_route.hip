@@ -36,6 +36,8 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     P.work = work;
     if (rank < 1 || rank > SP_MAXR)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: rank %d outside 1..%d supported by this build", rank, SP_MAXR);
+    if (work == CRESSO_F64 && rank > 16)
+        return fail(CRESSO_E_UNSUPPORTED, "spectral route: fp64 params support rank 1..16 in this build (rank %d)", rank);
     if (bins < 0 || tables < 1 || tables > SP_MAXT)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_tables %d outside 1..%d", tables, SP_MAXT);
     if (bins > 65535) return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_bins %d above 65535", bins);
@@ -150,7 +152,7 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
         m.k2 = k + 1;
     }
     g.K = (int32_t)P.csrc.size();
-    P.rmax = rank <= 8 ? 8 : 16;
+    P.rmax = rank <= 8 ? 8 : (rank <= 16 ? 16 : 32);
     const int KM = 2 * P.rmax + 1;
     if (g.K > KM) return fail(CRESSO_E_INVALID, "spectral route: %d column carriers exceed %d", g.K, KM);
     if ((double)g.K * (double)g.cols * 4.0 > 2.0e9)
@@ -170,6 +172,9 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     // 0.107 ms, but C4's batches of them fill the GPU and gain: 12.2-12.3 ->
     // 12.0-12.1 ms)
     if (pr >= 16 && g.rows >= 256 && g.rows % 32 == 0) pr = (g.rows % 64 == 0) ? 64 : 32;
+    // ranks above 16 run the general sweeps, whose per-block LDS (row
+    // coefficients of 2 * 68 + 64 floats per panel row) fits with 32-row panels
+    if (rank > 16) pr = std::min<int64_t>(pr, 32);
     // 32-bit element offsets inside a panel: PR * cols < 2^29
     if (g.cols >= ((int64_t)1 << 29))
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: %lld elements per row exceed this build's panel limit",
@@ -313,6 +318,11 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
     hipLaunchKernelGGL(ws_pairsum_kernel, dim3((unsigned)g.nblkg), dim3(256), 0, s, g, at<float>(ws, o.rowtab),
                        at<float>(ws, o.coltab), at<double>(ws, o.gpart));
     const size_t gram_lds = sizeof(double) * (4 * (size_t)g.R * g.R + (size_t)g.K * g.K);
+    if (gram_lds > 64 * 1024) {   // ranks above 16: up to 66.5 KB of pair sums (gfx950: 160 KB per workgroup)
+        const hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(&ws_gram_kernel),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)gram_lds);
+        if (ea != hipSuccess) return hip_fail(ea, "spectral route: Gram kernel LDS");
+    }
     hipLaunchKernelGGL(ws_gram_kernel, dim3(1), dim3(SP_FIN_NT), gram_lds, s, g, meta, at<double>(ws, o.stats),
                        at<double>(ws, o.gpart), at<double>(ws, o.gram));
     const int64_t TB = (int64_t)g.T * g.B;

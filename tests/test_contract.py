@@ -356,3 +356,31 @@ def test_load_state_dict_keeps_same_plan_workspaces():
     sd2["state"][0]["freqs"] = sd2["state"][0]["freqs"].flip(0).clone()
     opt.load_state_dict(sd2)
     assert set(eng.ws) == {(kq, True, 2)}
+
+
+def test_spectral_plan_rank_limits_without_gpu():
+    # plan creation is host work: ranks up to 32 plan on the fp32 work dtype
+    # (ranks above 16 take the general sweeps); fp64 params stop at 16; the
+    # refusals carry the library's message instead of a fallback
+    lib_path = ROOT / "cresso_amd" / "libcresso_hip.so"
+    if not lib_path.exists():
+        pytest.skip("library not built")
+    from cresso_amd.modes import mode_list
+
+    lib = _native.load()
+    shape = (1024, 512)
+
+    def create(rank, work):
+        freqs = [f for m in mode_list(rank, 2, 7) for f in m]
+        return lib.cresso_spectral_plan_create_ex((ctypes.c_int64 * 8)(*shape), 2,
+                                                  (ctypes.c_int64 * len(freqs))(*freqs), rank, 64, 2, work)
+
+    for rank in (17, 24, 32):
+        plan = create(rank, _native.F32)
+        assert plan, lib.cresso_hip_last_error()
+        assert lib.cresso_spectral_workspace_bytes(ctypes.c_void_p(plan)) > 0
+        lib.cresso_spectral_plan_destroy(ctypes.c_void_p(plan))
+    assert not create(33, _native.F32)
+    assert b"rank 33" in lib.cresso_hip_last_error()
+    assert not create(24, _native.F64)
+    assert b"fp64 params support rank 1..16" in lib.cresso_hip_last_error()

@@ -30,6 +30,12 @@ CASES = [
     ("mixed_group", [(256, 300), (4096, 16), (64, 65), (1500,)], dict(rank=8, hash_bins=64, hash_tables=2), 3,
      1e-3, 0.02),
     ("no_hash_b0", [(96, 80)], dict(rank=8, hash_bins=0), 3, 1e-3, 0.02),
+    # ranks above 16: the general sweeps with 32 projection slots (2 x 32
+    # carriers per element), MODE 0 and MODE 1 tiles, 2-D and 3-D
+    ("r24_300x257", [(300, 257)], dict(rank=24, max_frequency=6, hash_bins=64, hash_tables=2), 3, 1e-3, 0.02),
+    ("r32_1024x512_fast", [(1024, 512)], dict(rank=32, max_frequency=7, hash_bins=64, hash_tables=2), 3, 1e-3, 0.02),
+    ("r20_3d_t4", [(6, 10, 12)], dict(rank=20, max_frequency=7, hash_bins=256, hash_tables=4, min_spectral_size=1),
+     3, 1e-3, 0.02),
     # the matrix-core fast path with 32-row panels and few blocks (1024 rows)
     ("fast_1024x768", [(1024, 768)], dict(rank=8, hash_bins=64, hash_tables=2), 3, 1e-3, 0.02),
     ("fast_1024x512_r4_b32", [(1024, 512)], dict(rank=4, max_frequency=3, hash_bins=32, hash_tables=2), 3, 1e-3,
