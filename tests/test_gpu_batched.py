@@ -23,6 +23,9 @@ CASES = [
      dict(rank=4, max_frequency=3, hash_bins=128, hash_tables=2)),
     ("general_r16_t4", (300, 260), torch.float32, torch.float32,
      dict(rank=16, max_frequency=5, hash_bins=256, hash_tables=4)),
+    # rank above 16: the general sweeps instantiated for 32 modes (MODE 1 tiles)
+    ("general_r24", (512, 512), torch.float32, torch.float32,
+     dict(rank=24, max_frequency=6, hash_bins=64, hash_tables=2)),
     # matrix-core route whose histogram merge adds row groups with atomics into
     # eight histogram copies per lane (1024 bins x 512 or more block partials)
     ("merge_r16_t4", (4096, 2048), torch.float32, torch.float32,
