@@ -333,14 +333,16 @@ __device__ void block_max2(double (&v)[2], double* lds) {
 
 // Closed-form normalization stats (cresso_v5.py:138-142 over the separable
 // carriers): per mode (mu_c, 1/max(sqrt(var_c+1e-12),1e-6), mu_s, ...) and a
-// bound of max|C_n|, max|S_n| used to size fixed-point histograms.
+// bound of max|C_n|, max|S_n| used to size fixed-point histograms.  One
+// block per mode.
 __global__ __launch_bounds__(SP_FIN_NT) void ws_stats_kernel(Geom g, const ModeMeta* __restrict__ meta,
                                                              const float* __restrict__ rowtab,
                                                              const float* __restrict__ coltab, double* __restrict__ stats,
                                                              double* __restrict__ bounds) {
     __shared__ double red[16 * 8];
     const int tid = threadIdx.x;
-    for (int r = 0; r < g.R; ++r) {
+    {
+        const int r = blockIdx.x;   // one block per mode
         // row sums of this mode
         double v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         for (int64_t i = tid; i < g.rows; i += SP_FIN_NT) {
@@ -395,7 +397,6 @@ __global__ __launch_bounds__(SP_FIN_NT) void ws_stats_kernel(Geom g, const ModeM
                 bounds[2 * r + 1] = (ms + fabs(mus)) * is;
             }
         }
-        __syncthreads();
     }
 }
 

@@ -186,8 +186,8 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     // the matrix-core sweeps' histograms: atomic merges (part_reduce's row
     // groups, or every block of a multi-round launch) spread over copies
     g.hcopies = mtables(g) ? SP_HCOPIES : 1;
-    // Gram pair sums: one block per ~1024 rows/columns of the longer axis, at most 256
-    g.nblkg = (int32_t)std::max<int64_t>(1, std::min<int64_t>(256, std::max(g.rows, g.cols) / 1024));
+    // Gram pair sums: one block per ~128 rows/columns of the longer axis, at most 256
+    g.nblkg = (int32_t)std::max<int64_t>(1, std::min<int64_t>(256, std::max(g.rows, g.cols) / 128));
     // flat force-RMS sweep and parameter update: contiguous chunks (multiple of 4 elements) per block
     g.nblk1 = (int32_t)std::max<int64_t>(1, std::min<int64_t>(1024, (g.n + 16383) / 16384));
     g.chunk1 = (((g.n + g.nblk1 - 1) / g.nblk1) + 3) & ~(int64_t)3;
@@ -313,7 +313,7 @@ extern "C" int32_t cresso_spectral_workspace_init(const cresso_spectral_plan* P,
                        at<float>(ws, o.rowtab));
     hipLaunchKernelGGL(ws_coltab_kernel, dim3((unsigned)((g.cols + 255) / 256)), dim3(256), 0, s, g, axc, meta,
                        at<CarrierSrc>(ws, o.csrc), at<float>(ws, o.coltab));
-    hipLaunchKernelGGL(ws_stats_kernel, dim3(1), dim3(SP_FIN_NT), 0, s, g, meta, at<float>(ws, o.rowtab),
+    hipLaunchKernelGGL(ws_stats_kernel, dim3((unsigned)g.R), dim3(SP_FIN_NT), 0, s, g, meta, at<float>(ws, o.rowtab),
                        at<float>(ws, o.coltab), at<double>(ws, o.stats), at<double>(ws, o.bounds));
     hipLaunchKernelGGL(ws_pairsum_kernel, dim3((unsigned)g.nblkg), dim3(256), 0, s, g, at<float>(ws, o.rowtab),
                        at<float>(ws, o.coltab), at<double>(ws, o.gpart));
