@@ -51,6 +51,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -788,6 +789,24 @@ template <> struct Ld4<double> {
     }
 };
 
+// VW = 4 or 8 consecutive elements from e (8: 16-byte loads of 2-byte types,
+// two float4 loads of 4-byte ones)
+template <typename T, int VW> struct LdV;
+template <typename T> struct LdV<T, 4> : Ld4<T> {};
+template <typename T> struct LdV<T, 8> {
+    __device__ static void go(const T* p, int64_t e, float* o) {
+        if constexpr (sizeof(T) == 2) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(p + e);
+            const T* h = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) o[c] = to_f(h[c]);
+        } else {
+            Ld4<T>::go(p, e, o);
+            Ld4<T>::go(p, e + 4, o + 4);
+        }
+    }
+};
+
 // 4 consecutive elements stored at e, rounded to the storage dtype
 template <typename T> struct St4;
 template <> struct St4<float> {
@@ -994,51 +1013,63 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(
     const int64_t end = beg + g.chunk1 < g.n ? beg + g.chunk1 : g.n;
     const float sg = h.maximize ? -1.f : 1.f;
     float a = 0.f, m = 0.f;   // sum of f^2, max |f|
-    const int64_t vend = beg + ((end - beg) & ~(int64_t)3);
-    if (V4) {
-        // sixteen float4 loads per thread in flight per iteration, then the rest one by one
-        constexpr int UN = 16;
-        const int64_t st = 4 * (int64_t)SP_NT;
-        int64_t e = beg + 4 * (int64_t)threadIdx.x;
+    // 64 elements per thread per iteration in flight: 16 float4 loads, or, for
+    // 2-byte grads on a 16-byte aligned base, 8 16-byte loads (8 elements each)
+    auto vec_loop = [&](auto vw) -> int64_t {
+        constexpr int VW = decltype(vw)::value;
+        constexpr int UN = 64 / VW;
+        const int64_t vend = beg + ((end - beg) & ~(int64_t)(VW - 1));
+        const int64_t st = VW * (int64_t)SP_NT;
+        int64_t e = beg + VW * (int64_t)threadIdx.x;
         for (; e + (UN - 1) * st < vend; e += UN * st) {
-            float f[UN][4];
+            float f[UN][VW];
 #pragma unroll
-            for (int u = 0; u < UN; ++u) Ld4<GT>::go(grad, e + u * st, f[u]);
+            for (int u = 0; u < UN; ++u) LdV<GT, VW>::go(grad, e + u * st, f[u]);
             if (wd_on) {
-                float pv[UN][4];
+                float pv[UN][VW];
 #pragma unroll
-                for (int u = 0; u < UN; ++u) Ld4<PT>::go(param, e + u * st, pv[u]);
+                for (int u = 0; u < UN; ++u) LdV<PT, VW>::go(param, e + u * st, pv[u]);
 #pragma unroll
                 for (int u = 0; u < UN; ++u)
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) f[u][c] = sg * f[u][c] + wd * pv[u][c];
+                    for (int c = 0; c < VW; ++c) f[u][c] = sg * f[u][c] + wd * pv[u][c];
             }
 #pragma unroll
             for (int u = 0; u < UN; ++u)
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
+                for (int c = 0; c < VW; ++c) {
                     a += f[u][c] * f[u][c];
                     m = fmaxf(m, fabsf(f[u][c]));
                 }
         }
         for (; e < vend; e += st) {
-            float f[4];
-            Ld4<GT>::go(grad, e, f);
+            float f[VW];
+            LdV<GT, VW>::go(grad, e, f);
             if (wd_on) {
-                float pv[4];
-                Ld4<PT>::go(param, e, pv);
+                float pv[VW];
+                LdV<PT, VW>::go(param, e, pv);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) f[c] = sg * f[c] + wd * pv[c];
+                for (int c = 0; c < VW; ++c) f[c] = sg * f[c] + wd * pv[c];
             }
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
+            for (int c = 0; c < VW; ++c) {
                 a += f[c] * f[c];
                 m = fmaxf(m, fabsf(f[c]));
             }
         }
+        return vend;
+    };
+    int64_t vend = beg;
+    if constexpr (V4) {
+        // (chunks start at multiples of 8 elements)
+        if (sizeof(GT) == 2 && ((uintptr_t)grad & 15) == 0 &&
+            (!wd_on || sizeof(PT) != 2 || ((uintptr_t)param & 15) == 0))
+            vend = vec_loop(std::integral_constant<int, 8>{});
+        else
+            vend = vec_loop(std::integral_constant<int, 4>{});
     }
-    // scalar elements: the < 4 tail of a vectorized chunk, or the whole chunk
-    for (int64_t i = (V4 ? vend : beg) + threadIdx.x; i < end; i += SP_NT) {
+    // scalar elements: the tail of a vectorized chunk, or the whole chunk
+    for (int64_t i = vend + threadIdx.x; i < end; i += SP_NT) {
         float f = sg * ld(grad, i);
         if (wd_on) f = f + wd * ld(param, i);
         a += f * f;
@@ -1074,7 +1105,9 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(
 // (low + high 2^k) / 2^F, each element adding y = rel^p 2^F.  Elements with
 // y < 2^k add rint(y) to the low word (one LDS atomic per table, the common
 // case); larger ones add floor(rel^p 2^-j) (j = k - F) to the high word and
-// the exact remainder to the low word.  F, k, j are chosen so that
+// the exact remainder to the low word.  (The sweeps' loops add min(y, 2^k);
+// a high-word pass, in the blocks hi_block finds can hold such an element,
+// adds the rest: HiSplit.)  F, k, j are chosen so that
 //   - the low words cannot overflow: either every element's y stays below
 //     2^k <= 2^(62 - ceil log2 cmax) (cmax elements per bin at most), or F
 //     is the single-word scale F0 for which a bin's whole sum stays below

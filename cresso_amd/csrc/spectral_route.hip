@@ -188,9 +188,9 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     g.hcopies = mtables(g) ? SP_HCOPIES : 1;
     // Gram pair sums: one block per ~128 rows/columns of the longer axis, at most 256
     g.nblkg = (int32_t)std::max<int64_t>(1, std::min<int64_t>(256, std::max(g.rows, g.cols) / 128));
-    // flat force-RMS sweep and parameter update: contiguous chunks (multiple of 4 elements) per block
+    // flat force-RMS sweep and parameter update: contiguous chunks (multiple of 8 elements) per block
     g.nblk1 = (int32_t)std::max<int64_t>(1, std::min<int64_t>(1024, (g.n + 16383) / 16384));
-    g.chunk1 = (((g.n + g.nblk1 - 1) / g.nblk1) + 3) & ~(int64_t)3;
+    g.chunk1 = (((g.n + g.nblk1 - 1) / g.nblk1) + 7) & ~(int64_t)7;   // multiples of 8 elements (16-byte loads)
     g.nblk1 = (int32_t)((g.n + g.chunk1 - 1) / g.chunk1);
     // axis density sums: density <= 1e6 per element, sums below 2^62
     g.shrink = 1.0 / std::sqrt(std::fmax(1.0, 0.7 * std::log2((double)g.R + 1.0)));

@@ -146,6 +146,17 @@ def test_spectral_bf16_params():
     compare(*res, param_tol=BF16_PARAM_TOL, state_tol=F32_TOL)
 
 
+@pytest.mark.parametrize("shape", [(256, 320), (31, 37)], ids=["256x320", "31x37"])
+def test_spectral_bf16_params_weight_decay_first_step(shape):
+    # sweep 1 with weight decay on 2-byte params and grads: 16-byte loads of
+    # both (chunks of multiples of 8 elements, a 3-element tail at 31x37).
+    # One step: the force then depends on identical params on both sides.
+    announce(f"spectral bf16 weight decay {shape}")
+    kw = dict(OPS_KW, lr=1e-3, weight_decay=0.01)
+    res = run_pair([shape], torch.bfloat16, kw, steps=1, seed=13, grad_std=0.05, param_std=0.05)
+    compare(*res, param_tol=BF16_PARAM_TOL, state_tol=F32_TOL)
+
+
 @pytest.mark.parametrize("pdt,gdt", [(torch.float32, torch.bfloat16), (torch.float32, torch.float16),
                                      (torch.float16, torch.float16)],
                          ids=["f32_param_bf16_grad", "f32_param_f16_grad", "f16_param_f16_grad"])
