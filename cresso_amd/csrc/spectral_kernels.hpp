@@ -1118,6 +1118,8 @@ __global__ __launch_bounds__(SP_NT) void sweep1_kernel(
 //     element (so that a few spikes near the rel clamp, at a large energy
 //     power, do not set the resolution of every other bin, as they do F0).
 // F is never below F0, so the resolution is never coarser than one word's.
+// When F0 alone resolves densities near 1 to 2^-36 (no large element set
+// it), the high words stay off and the step pays nothing for them.
 struct F1Values {
     float inv_s;
     double hs_ds;   // 2^F
@@ -1144,33 +1146,26 @@ struct F1Part {
 template <int N>
 __device__ F1Values fin1_values(const Geom& g, const F1Part<N>& fp, const double* __restrict__ part1,
                                 Ctrl* __restrict__ ctrl, float* __restrict__ fr_state, int step, const cresso_hyper& h) {
-    __shared__ double s_w[SP_NT / 64], s_x[SP_NT / 64], s_m[SP_NT / 64];
-    double a = 0.0, ax = 0.0, mx = 0.0;
+    __shared__ double s_w[SP_NT / 64], s_m[SP_NT / 64];
+    double a = 0.0, mx = 0.0;
 #pragma unroll
     for (int i = 0; i < N; ++i)
         if ((int)threadIdx.x + i * SP_NT < g.nblk1) {
             a += fp.s[i];
-            ax += fmax(fp.s[i] - fp.m[i] * fp.m[i], 0.0);
             mx = fmax(mx, fp.m[i]);
         }
     for (int b = threadIdx.x + N * SP_NT; b < g.nblk1; b += SP_NT) {
-        const double sb = part1[(size_t)b * 2], mb = part1[(size_t)b * 2 + 1];
-        a += sb;
-        ax += fmax(sb - mb * mb, 0.0);
-        mx = fmax(mx, mb);
+        a += part1[(size_t)b * 2];
+        mx = fmax(mx, part1[(size_t)b * 2 + 1]);
     }
-    const double w = wave_total_d(a), wx = wave_total_d(ax);
+    const double w = wave_total_d(a);
     for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
-    if ((threadIdx.x & 63) == 63) {
-        s_w[threadIdx.x >> 6] = w;
-        s_x[threadIdx.x >> 6] = wx;
-    }
+    if ((threadIdx.x & 63) == 63) s_w[threadIdx.x >> 6] = w;
     if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = mx;
     __syncthreads();
-    double sum = 0.0, sumx = 0.0;
+    double sum = 0.0;
     for (int i = 0; i < SP_NT / 64; ++i) {
         sum += s_w[i];
-        sumx += s_x[i];
         mx = fmax(mx, s_m[i]);
     }
     const float eps = (float)h.eps;
@@ -1201,13 +1196,36 @@ __device__ F1Values fin1_values(const Geom& g, const F1Part<N>& fp, const double
     const float l2b = fminf(l2bin, l2tot);
     // (exponents clamped as floats, so that infinite or NaN bounds convert)
     const int f0 = (int)fminf(fmaxf(floorf(61.0f - l2b - 0.05f), -120.0f), 120.0f);
-    // two-word scale: the low words' limit 2^kq, the high words' weight 2^j
-    const int kq = ctrl->kq;
-    const float rtyp = sqrtf((float)(sumx * g.inv_n)) * v.inv_s + eps;   // typical rel
-    const int j = (int)fminf(fmaxf(ceilf(fmaxf(pw * flog2(rtyp) + 16.0f, l2b - 60.0f + 0.05f)), -100.0f), 100.0f);
-    int F = kq - j > f0 ? kq - j : f0;
-    F = F < 120 ? F : 120;   // 2^F stays a finite fp32 value
-    const int k = F + j < 62 ? F + j : 62;
+    // The single word keeps 2^-36 resolution at ds = 1 or finer (rel is
+    // normalized by the force RMS, so ordinary densities are near 1): high
+    // words off (k = 62, which no element reaches under F0).  A coarser F0
+    // means a large element set it: the two-word scale, with the low words'
+    // limit 2^kq and the high words' weight 2^j.  (f0 is the same in every
+    // block, so every block takes the same branch.)
+    int F = f0, k = 62, j = 62 - f0;
+    if (f0 < 36) {
+        // sum f^2 without each sweep-1 block's largest element, in block order
+        __shared__ double s_x[SP_NT / 64];
+        double ax = 0.0;
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if ((int)threadIdx.x + i * SP_NT < g.nblk1) ax += fmax(fp.s[i] - fp.m[i] * fp.m[i], 0.0);
+        for (int b = threadIdx.x + N * SP_NT; b < g.nblk1; b += SP_NT) {
+            const double mb = part1[(size_t)b * 2 + 1];
+            ax += fmax(part1[(size_t)b * 2] - mb * mb, 0.0);
+        }
+        const double wx = wave_total_d(ax);
+        if ((threadIdx.x & 63) == 63) s_x[threadIdx.x >> 6] = wx;
+        __syncthreads();
+        double sumx = 0.0;
+        for (int i = 0; i < SP_NT / 64; ++i) sumx += s_x[i];
+        const int kq = ctrl->kq;
+        const float rtyp = sqrtf((float)(sumx * g.inv_n)) * v.inv_s + eps;   // typical rel
+        j = (int)fminf(fmaxf(ceilf(fmaxf(pw * flog2(rtyp) + 16.0f, l2b - 60.0f + 0.05f)), -100.0f), 100.0f);
+        F = kq - j > f0 ? kq - j : f0;
+        F = F < 120 ? F : 120;   // 2^F stays a finite fp32 value
+        k = F + j < 62 ? F + j : 62;
+    }
     v.hs_ds = ldexp(1.0, F);
     v.yk = ldexpf(1.0f, k);
     v.hq = ldexpf(1.0f, -j);
