@@ -36,6 +36,10 @@ CASES = [
     ("r32_1024x512_fast", [(1024, 512)], dict(rank=32, max_frequency=7, hash_bins=64, hash_tables=2), 3, 1e-3, 0.02),
     ("r20_3d_t4", [(6, 10, 12)], dict(rank=20, max_frequency=7, hash_bins=256, hash_tables=4, min_spectral_size=1),
      3, 1e-3, 0.02),
+    ("r20_1d_4096", [(4096,)], dict(rank=20, max_frequency=7, hash_bins=64, hash_tables=2), 3, 1e-2, 0.02),
+    ("r24_variants_40x30", [(40, 30)], dict(rank=24, max_frequency=6, hash_bins=64, hash_tables=3, weight_decay=0.01,
+                                            maximize=True, local_sharpness=0.3, min_spectral_size=1, warmup_steps=0),
+     4, 1e-2, 0.05),
     # the matrix-core fast path with 32-row panels and few blocks (1024 rows)
     ("fast_1024x768", [(1024, 768)], dict(rank=8, hash_bins=64, hash_tables=2), 3, 1e-3, 0.02),
     ("fast_1024x512_r4_b32", [(1024, 512)], dict(rank=4, max_frequency=3, hash_bins=32, hash_tables=2), 3, 1e-3,
