@@ -538,3 +538,43 @@ def test_spectral_unaligned_param_and_grad():
         oopt.step([g])
     torch.cuda.synchronize()
     compare([hp], hopt, [op], oopt)
+
+
+def test_spectral_group_changes_between_steps():
+    """Hyperparameters are read from the param group at every step: a torch
+    learning-rate scheduler halves lr after step 2, hash_decay and
+    energy_power change at step 4, and one parameter gets new storage (same
+    values) at step 5; the HIP path follows the oracle given the same changes."""
+    import cresso_amd
+    from gpu_util import F32_TOL
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    announce("spectral param-group changes between steps")
+    gen = torch.Generator().manual_seed(29)
+    shapes = [(256, 192), (96, 80)]
+    kw = dict(lr=2e-3, rank=8, max_frequency=5, hash_bins=64, hash_tables=2)
+    p0 = [0.02 * torch.randn(s, generator=gen) for s in shapes]
+    hp = [torch.nn.Parameter(p.clone().cuda()) for p in p0]
+    op = [p.clone() for p in p0]
+    hopt = cresso_amd.CRESSO5(hp, cuda_ops="required", **kw)
+    oopt = OracleCRESSO5(op, **kw)
+    sched = torch.optim.lr_scheduler.StepLR(hopt, step_size=2, gamma=0.5)
+    for k in range(6):
+        gs = [1e-3 * torch.randn(s, generator=gen) for s in shapes]
+        if k == 4:
+            for grp in hopt.param_groups:
+                grp["hash_decay"] = 0.8
+                grp["energy_power"] = 1.5
+            oopt.h["hash_decay"] = 0.8
+            oopt.h["energy_power"] = 1.5
+        if k == 5:
+            hp[0].data = hp[0].data.clone()
+        oopt.h["lr"] = hopt.param_groups[0]["lr"]
+        for p, g in zip(hp, gs):
+            p.grad = g.cuda()
+        hopt.step()
+        oopt.step(gs)
+        sched.step()
+    torch.cuda.synchronize()
+    assert abs(hopt.param_groups[0]["lr"] - 2e-3 * 0.5 ** 3) < 1e-12
+    compare(hp, hopt, op, oopt, state_tol=F32_TOL)
