@@ -578,3 +578,38 @@ def test_spectral_group_changes_between_steps():
     torch.cuda.synchronize()
     assert abs(hopt.param_groups[0]["lr"] - 2e-3 * 0.5 ** 3) < 1e-12
     compare(hp, hopt, op, oopt, state_tol=F32_TOL)
+
+
+def test_spectral_param_groups_with_different_ranks():
+    """Two param groups with their own rank, tables and bins (a rank-8 spectral
+    tensor; a rank-24 spectral tensor and a LoRA-thin scalar-route tensor),
+    each against its own oracle; a third group is added after two steps."""
+    import cresso_amd
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    announce("spectral param groups with different ranks")
+    gen = torch.Generator().manual_seed(31)
+    ka = dict(rank=8, max_frequency=5, hash_bins=64, hash_tables=2)
+    kb = dict(rank=24, max_frequency=6, hash_bins=128, hash_tables=3)
+    kc = dict(rank=4, max_frequency=3, hash_bins=32, hash_tables=2, min_spectral_size=1)
+    shapes = {"a": [(128, 96)], "b": [(200, 150), (4096, 16)], "c": [(48, 40)]}
+    p0 = {k: [0.02 * torch.randn(s, generator=gen) for s in v] for k, v in shapes.items()}
+    hp = {k: [torch.nn.Parameter(p.clone().cuda()) for p in v] for k, v in p0.items()}
+    op = {k: [p.clone() for p in v] for k, v in p0.items()}
+    hopt = cresso_amd.CRESSO5([dict(params=hp["a"], **ka), dict(params=hp["b"], **kb)], cuda_ops="required",
+                              lr=2e-3)
+    oo = {"a": OracleCRESSO5(op["a"], lr=2e-3, **ka), "b": OracleCRESSO5(op["b"], lr=2e-3, **kb)}
+    for k in range(4):
+        if k == 2:
+            hopt.add_param_group(dict(params=hp["c"], **kc))
+            oo["c"] = OracleCRESSO5(op["c"], lr=2e-3, **kc)
+        gs = {key: [1e-3 * torch.randn(s, generator=gen) for s in shapes[key]] for key in oo}
+        for key in oo:
+            for p, g in zip(hp[key], gs[key]):
+                p.grad = g.cuda()
+        hopt.step()
+        for key in oo:
+            oo[key].step(gs[key])
+    torch.cuda.synchronize()
+    for key in oo:
+        compare(hp[key], hopt, op[key], oo[key])
