@@ -284,6 +284,23 @@ class CRESSO5(Optimizer):
         state["surprise"] = torch.zeros((), device=device, dtype=dtype)
         state["action"] = torch.zeros((), device=device, dtype=dtype)
 
+    def _step_empty(self, param: Tensor, group: dict) -> None:
+        """A parameter with no elements (the scalar or micro route: the
+        spectral route needs min_spectral_size >= 1 elements): nothing to
+        update.  The reference's step takes its means over no elements, so the
+        state entries computed from them become NaN: every floating scalar of
+        the scalar route; the three reservoirs of the micro route, whose
+        action the micro step does not touch (cresso_v5.py:1355-1432, 1434-1585)."""
+        micro = self._route(param, group) == "micro"
+        st = self.state[param]
+        if len(st) == 0:
+            st = self._init_micro(param) if micro else self._init_scalar(param)
+        st["step"] = int(st["step"]) + 1
+        keep = {"action"} if micro else set()
+        for k, v in st.items():
+            if torch.is_tensor(v) and v.is_floating_point() and v.numel() > 0 and k not in keep:
+                v.fill_(float("nan"))
+
     def _init_scalar(self, param: Tensor) -> dict:
         st = self.state[param]
         dtype = _state_dtype(param.dtype)
@@ -373,6 +390,10 @@ class CRESSO5(Optimizer):
                                    "cuda_ops='auto'); the reference's CPU PyTorch path is not part of this build")
             if grad.shape != p.shape or not grad.is_contiguous() or not p.is_contiguous():
                 raise RuntimeError("CRESSO5 needs contiguous parameters and gradients of the parameter's shape")
+            if p.numel() == 0:
+                other = True
+                self._step_empty(p, group)
+                continue
             route = self._route(p, group)
             if route == "micro":
                 st = self.state[p]

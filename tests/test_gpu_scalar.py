@@ -306,3 +306,32 @@ def test_scalar_plan_step_null_grads_reuse_the_previous_pointers():
     oopt.step(g2)
     torch.cuda.synchronize()
     compare(hp, hopt, op, oopt)
+
+
+@pytest.mark.parametrize("extra", [{}, dict(micro_field_max_size=64)], ids=["scalar_route", "micro_route"])
+def test_empty_parameters_follow_the_reference(extra):
+    """Parameters with no elements beside ordinary ones: nothing to update, and
+    the state entries the reference computes as means over no elements are
+    NaN (compare treats NaN as equal to NaN); the ordinary tensors step as
+    usual.  (min_spectral_size >= 1, so an empty parameter never takes the
+    spectral route.)"""
+    import cresso_amd
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    announce(f"empty parameters {extra}")
+    gen = torch.Generator().manual_seed(37)
+    shapes = [(0, 8), (128, 96), (0,), (4096, 16)]
+    kw = dict(rank=8, hash_bins=64, hash_tables=2, **extra)
+    p0 = [0.02 * torch.randn(s, generator=gen) for s in shapes]
+    hp = [torch.nn.Parameter(p.clone().cuda()) for p in p0]
+    op = [p.clone() for p in p0]
+    hopt = cresso_amd.CRESSO5(hp, cuda_ops="required", **kw)
+    oopt = OracleCRESSO5(op, **kw)
+    for k in range(3):
+        gs = [1e-3 * torch.randn(s, generator=gen) for s in shapes]
+        for p, g in zip(hp, gs):
+            p.grad = g.cuda()
+        hopt.step()
+        oopt.step(gs)
+    torch.cuda.synchronize()
+    compare(hp, hopt, op, oopt)
