@@ -163,6 +163,13 @@ class _ScalarBatch:
                 and [p.data_ptr() for p in params] == self.pptrs and self.key_of(group) == self.hyper_key
                 and [p.grad.dtype for p in params] == self.gdtypes)
 
+    @staticmethod
+    def grads_ready(params: List[Tensor]) -> bool:
+        """Every grad can be passed by pointer as it is (dense, contiguous, the
+        parameter's shape and device)."""
+        return all(not p.grad.is_sparse and p.grad.is_contiguous() and p.grad.shape == p.shape
+                   and p.grad.device == p.device for p in params)
+
     def run(self, group: dict, gptrs: Optional[List[int]]) -> None:
         """One step; gptrs None: the grad pointers are already in self.gbuf."""
         hyper = _native.hyper_from_group(group)
@@ -361,7 +368,7 @@ class CRESSO5(Optimizer):
             gptrs = [p.grad.data_ptr() for p in batch.params]
         except (AttributeError, RuntimeError):
             return False
-        if not batch.matches(group["params"], group):
+        if not batch.matches(group["params"], group) or not batch.grads_ready(batch.params):
             return False
         batch.run(group, gptrs)
         return True
@@ -371,6 +378,7 @@ class CRESSO5(Optimizer):
             return
         mode = str(group.get("cuda_ops", "auto"))
         scalar_ps: List[Tensor] = []
+        scalar_gs: List[Tensor] = []   # their grads (contiguous)
         spectral_items = []
         other = False
         for p in group["params"]:
@@ -388,8 +396,13 @@ class CRESSO5(Optimizer):
             if not p.is_cuda:
                 raise RuntimeError("CRESSO5 on MI355X optimizes GPU parameters only (got a CPU parameter with "
                                    "cuda_ops='auto'); the reference's CPU PyTorch path is not part of this build")
-            if grad.shape != p.shape or not grad.is_contiguous() or not p.is_contiguous():
+            if grad.shape != p.shape or not p.is_contiguous():
                 raise RuntimeError("CRESSO5 needs contiguous parameters and gradients of the parameter's shape")
+            if not grad.is_contiguous():
+                # the kernels read elements in the parameter's (row-major)
+                # order; a contiguous copy, on the current stream, outlives the
+                # launches that read it (the side streams join back first)
+                grad = grad.contiguous()
             if p.numel() == 0:
                 other = True
                 self._step_empty(p, group)
@@ -402,6 +415,7 @@ class CRESSO5(Optimizer):
                 else:
                     self._check_micro_state(p, st)
                 scalar_ps.append(p)
+                scalar_gs.append(grad)
                 continue
             if route == "spectral":
                 other = True
@@ -418,6 +432,7 @@ class CRESSO5(Optimizer):
             elif st["q"].dtype != _state_dtype(p.dtype):
                 raise RuntimeError("CRESSO5 scalar state has dtype %s, expected %s" % (st["q"].dtype, _state_dtype(p.dtype)))
             scalar_ps.append(p)
+            scalar_gs.append(grad)
         if spectral_items:
             self._spectral_step(spectral_items, group)
         self._group_other[gi] = other
@@ -432,7 +447,7 @@ class CRESSO5(Optimizer):
             self._batches[(gi, "scalar")] = None  # drop the old plan first
             batch = _ScalarBatch(scalar_ps, [self.state[p] for p in scalar_ps], group, scalar_ps[0].device)
             self._batches[(gi, "scalar")] = batch
-        batch.run(group, [p.grad.data_ptr() for p in scalar_ps])
+        batch.run(group, [g.data_ptr() for g in scalar_gs])
 
     @staticmethod
     def _check_micro_state(p: Tensor, st: dict) -> None:

@@ -335,3 +335,34 @@ def test_empty_parameters_follow_the_reference(extra):
         oopt.step(gs)
     torch.cuda.synchronize()
     compare(hp, hopt, op, oopt)
+
+
+def test_non_contiguous_grads_follow_the_reference():
+    """Grads in a transposed layout (the parameter's shape, other strides) on
+    the scalar and spectral routes are read in the parameter's element order
+    (through a contiguous copy); contiguous grads before and after take the
+    steady-state path."""
+    import cresso_amd
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    announce("non-contiguous grads")
+    gen = torch.Generator().manual_seed(41)
+    shapes = [(4096, 16), (16, 4096), (128, 96)]
+    kw = dict(rank=8, hash_bins=64, hash_tables=2)
+    p0 = [0.02 * torch.randn(s, generator=gen) for s in shapes]
+    hp = [torch.nn.Parameter(p.clone().cuda()) for p in p0]
+    op = [p.clone() for p in p0]
+    hopt = cresso_amd.CRESSO5(hp, cuda_ops="required", **kw)
+    oopt = OracleCRESSO5(op, **kw)
+    for k in range(5):
+        gs = [1e-3 * torch.randn(s, generator=gen) for s in shapes]
+        for p, g in zip(hp, gs):
+            gd = g.cuda()
+            if k in (1, 2):
+                gd = gd.t().contiguous().t()   # same values, column-major strides
+                assert not gd.is_contiguous()
+            p.grad = gd
+        hopt.step()
+        oopt.step(gs)
+    torch.cuda.synchronize()
+    compare(hp, hopt, op, oopt)
