@@ -105,19 +105,19 @@ class _ScalarBatch:
     """Cached plan of the scalar-route and micro-route tensors of one param
     group on one device (one library plan; micro tensors carry route 1)."""
 
-    def __init__(self, params: List[Tensor], states: List[dict], group: dict, device: torch.device):
+    def __init__(self, params: List[Tensor], grads: List[Tensor], states: List[dict], group: dict,
+                 device: torch.device):
         lib = _native.load()
         self.lib = lib
         self.params = params
         self.states = states
         self.device = device
         self.pptrs = [p.data_ptr() for p in params]
-        self.gdtypes = [p.grad.dtype for p in params]   # the plan's descriptors fix the grad dtype
+        self.gdtypes = [g.dtype for g in grads]   # the plan's descriptors fix the grad dtype
         self.hyper_key = self.key_of(group)
         descs = (_native.ScalarDesc * len(params))()
-        for i, (p, st) in enumerate(zip(params, states)):
+        for i, (p, g, st) in enumerate(zip(params, grads, states)):
             d = descs[i]
-            g = p.grad
             d.param = p.data_ptr()
             d.grad = g.data_ptr()
             micro = "micro_energy" in st
@@ -148,7 +148,7 @@ class _ScalarBatch:
         self.gbuf = self.gptr_type()
         self.guard = None
         hb = _native.host_batch()
-        if hb is not None:
+        if hb is not None and all(p.grad is not None for p in params):   # (not for contiguous copies)
             try:
                 self.guard = hb.BatchGuard(list(params))
             except (ValueError, RuntimeError):
@@ -158,10 +158,10 @@ class _ScalarBatch:
     def key_of(group: dict):
         return tuple(group[k] for k in _native.HYPER_DOUBLES if k != "lr") + (group["warmup_steps"], group["maximize"])
 
-    def matches(self, params: List[Tensor], group: dict) -> bool:
+    def matches(self, params: List[Tensor], gdtypes: List[torch.dtype], group: dict) -> bool:
         return (len(params) == len(self.params) and all(a is b for a, b in zip(params, self.params))
                 and [p.data_ptr() for p in params] == self.pptrs and self.key_of(group) == self.hyper_key
-                and [p.grad.dtype for p in params] == self.gdtypes)
+                and gdtypes == self.gdtypes)
 
     @staticmethod
     def grads_ready(params: List[Tensor]) -> bool:
@@ -368,7 +368,8 @@ class CRESSO5(Optimizer):
             gptrs = [p.grad.data_ptr() for p in batch.params]
         except (AttributeError, RuntimeError):
             return False
-        if not batch.matches(group["params"], group) or not batch.grads_ready(batch.params):
+        if (not batch.matches(group["params"], [p.grad.dtype for p in batch.params], group)
+                or not batch.grads_ready(batch.params)):
             return False
         batch.run(group, gptrs)
         return True
@@ -377,9 +378,11 @@ class CRESSO5(Optimizer):
         if self._fast_scalar(gi, group):
             return
         mode = str(group.get("cuda_ops", "auto"))
-        scalar_ps: List[Tensor] = []
+        scalar_ps: List[Tensor] = []   # the scalar/micro tensors stepped (contiguous)
         scalar_gs: List[Tensor] = []   # their grads (contiguous)
+        scalar_st: List[dict] = []     # their states (keyed by the parameter)
         spectral_items = []
+        copies = []                    # (parameter, contiguous copy) of non-contiguous parameters
         other = False
         for p in group["params"]:
             if p.grad is None or not torch.is_floating_point(p):
@@ -396,13 +399,21 @@ class CRESSO5(Optimizer):
             if not p.is_cuda:
                 raise RuntimeError("CRESSO5 on MI355X optimizes GPU parameters only (got a CPU parameter with "
                                    "cuda_ops='auto'); the reference's CPU PyTorch path is not part of this build")
-            if grad.shape != p.shape or not p.is_contiguous():
-                raise RuntimeError("CRESSO5 needs contiguous parameters and gradients of the parameter's shape")
+            if grad.shape != p.shape:
+                raise RuntimeError("CRESSO5 needs gradients of the parameter's shape")
+            # The kernels read elements in the parameter's (row-major) order:
+            # other layouts (channels-last convolution weights, transposed
+            # views) step through contiguous copies on the current stream,
+            # which outlive the launches that read them (the side streams join
+            # back first), and the parameter takes the result back in its own
+            # layout.
             if not grad.is_contiguous():
-                # the kernels read elements in the parameter's (row-major)
-                # order; a contiguous copy, on the current stream, outlives the
-                # launches that read it (the side streams join back first)
                 grad = grad.contiguous()
+            data = p
+            if not p.is_contiguous():
+                data = p.detach().contiguous()
+                copies.append((p, data))
+                other = True
             if p.numel() == 0:
                 other = True
                 self._step_empty(p, group)
@@ -414,15 +425,16 @@ class CRESSO5(Optimizer):
                     st = self._init_micro(p)
                 else:
                     self._check_micro_state(p, st)
-                scalar_ps.append(p)
+                scalar_ps.append(data)
                 scalar_gs.append(grad)
+                scalar_st.append(st)
                 continue
             if route == "spectral":
                 other = True
                 st = self.state[p]
                 if len(st) == 0:
                     st = self._init_spectral(p, group)
-                spectral_items.append((p, grad, st))
+                spectral_items.append((data, grad, st))
                 continue
             st = self.state[p]
             if len(st) == 0:
@@ -431,21 +443,28 @@ class CRESSO5(Optimizer):
                 raise RuntimeError("CRESSO5 scalar route: the parameter's state belongs to another route")
             elif st["q"].dtype != _state_dtype(p.dtype):
                 raise RuntimeError("CRESSO5 scalar state has dtype %s, expected %s" % (st["q"].dtype, _state_dtype(p.dtype)))
-            scalar_ps.append(p)
+            scalar_ps.append(data)
             scalar_gs.append(grad)
+            scalar_st.append(st)
         if spectral_items:
             self._spectral_step(spectral_items, group)
         self._group_other[gi] = other
-        if not scalar_ps:
+        if scalar_ps:
+            self._step_scalar_batch(gi, group, scalar_ps, scalar_gs, scalar_st)
+        else:
             self._batches.pop((gi, "scalar"), None)
-            return
+        for p, data in copies:
+            p.detach().copy_(data)
+
+    def _step_scalar_batch(self, gi: int, group: dict, scalar_ps: List[Tensor], scalar_gs: List[Tensor],
+                           scalar_st: List[dict]) -> None:
         devices = {p.device for p in scalar_ps}
         if len(devices) != 1:
             raise RuntimeError("CRESSO5 scalar route: all parameters of a group must be on one device")
         batch = self._batches.get((gi, "scalar"))
-        if batch is None or not batch.matches(scalar_ps, group):
+        if batch is None or not batch.matches(scalar_ps, [g.dtype for g in scalar_gs], group):
             self._batches[(gi, "scalar")] = None  # drop the old plan first
-            batch = _ScalarBatch(scalar_ps, [self.state[p] for p in scalar_ps], group, scalar_ps[0].device)
+            batch = _ScalarBatch(scalar_ps, scalar_gs, scalar_st, group, scalar_ps[0].device)
             self._batches[(gi, "scalar")] = batch
         batch.run(group, [g.data_ptr() for g in scalar_gs])
 

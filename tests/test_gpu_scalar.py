@@ -366,3 +366,36 @@ def test_non_contiguous_grads_follow_the_reference():
         oopt.step(gs)
     torch.cuda.synchronize()
     compare(hp, hopt, op, oopt)
+
+
+def test_non_contiguous_params_follow_the_reference():
+    """Parameters in other layouts (a channels-last convolution weight and a
+    transposed matrix on the spectral route, a transposed LoRA-thin matrix on
+    the scalar route) step in their logical element order and keep their
+    layout; values and state follow the oracle on contiguous copies."""
+    import cresso_amd
+    from oracle.cresso_oracle import OracleCRESSO5
+
+    announce("non-contiguous params")
+    gen = torch.Generator().manual_seed(43)
+    shapes = [(64, 32, 3, 3), (96, 128), (4096, 16)]
+    kw = dict(rank=8, hash_bins=64, hash_tables=2)
+    p0 = [0.02 * torch.randn(s, generator=gen) for s in shapes]
+    dev = [p0[0].cuda().contiguous(memory_format=torch.channels_last),
+           p0[1].t().contiguous().cuda().t(),
+           p0[2].t().contiguous().cuda().t()]
+    hp = [torch.nn.Parameter(d) for d in dev]
+    assert not any(p.is_contiguous() for p in hp)
+    strides = [p.stride() for p in hp]
+    op = [p.clone() for p in p0]
+    hopt = cresso_amd.CRESSO5(hp, cuda_ops="required", **kw)
+    oopt = OracleCRESSO5(op, **kw)
+    for k in range(3):
+        gs = [1e-3 * torch.randn(s, generator=gen) for s in shapes]
+        for p, g in zip(hp, gs):
+            p.grad = g.cuda()
+        hopt.step()
+        oopt.step(gs)
+    torch.cuda.synchronize()
+    assert [p.stride() for p in hp] == strides
+    compare(hp, hopt, op, oopt)
