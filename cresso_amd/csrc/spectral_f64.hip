@@ -1056,15 +1056,20 @@ int32_t workspace_init_f64(const cresso_spectral_plan& P, void* ws, hipStream_t 
     if (e != hipSuccess) return hip_fail(e, "spectral route (fp64): workspace upload");
     if (P.g.R <= 8)
         init_f64_tables<8>(P, ws, s);
-    else
+    else if (P.g.R <= 16)
         init_f64_tables<16>(P, ws, s);
+    else
+        init_f64_tables<32>(P, ws, s);
     e = hipGetLastError();
     return e == hipSuccess ? CRESSO_OK : hip_fail(e, "spectral route (fp64): workspace init");
 }
 
 int32_t spectral_run_f64(const cresso_spectral_plan& P, const cresso_spectral_desc& d, void* ws, const cresso_hyper& h,
                          hipStream_t s) {
-    return P.g.R <= 8 ? run_f64<8>(P, d, ws, h, s) : run_f64<16>(P, d, ws, h, s);
+    // ranks 17-32: correct, not tuned (the per-thread carrier arrays spill to scratch)
+    if (P.g.R <= 8) return run_f64<8>(P, d, ws, h, s);
+    if (P.g.R <= 16) return run_f64<16>(P, d, ws, h, s);
+    return run_f64<32>(P, d, ws, h, s);
 }
 
 }  // namespace cresso

@@ -36,8 +36,6 @@ int32_t plan_spectral(const int64_t* shape, int32_t ndim, const int64_t* freqs, 
     P.work = work;
     if (rank < 1 || rank > SP_MAXR)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: rank %d outside 1..%d supported by this build", rank, SP_MAXR);
-    if (work == CRESSO_F64 && rank > 16)
-        return fail(CRESSO_E_UNSUPPORTED, "spectral route: fp64 params support rank 1..16 in this build (rank %d)", rank);
     if (bins < 0 || tables < 1 || tables > SP_MAXT)
         return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_tables %d outside 1..%d", tables, SP_MAXT);
     if (bins > 65535) return fail(CRESSO_E_UNSUPPORTED, "spectral route: hash_bins %d above 65535", bins);

@@ -95,8 +95,15 @@ def freqs_tensor(rank: int, ndim: int, max_frequency: int, device) -> torch.Tens
 
 
 def omega_tensor(freqs: torch.Tensor) -> torch.Tensor:
-    """omega_r = sqrt(1 + sum_a f_ra^2), fp32."""
+    """omega_r = sqrt(1 + sum_a f_ra^2), fp32 (cresso_v5.py:230-234).
+
+    Evaluated on the host, where the fp32 square root is correctly rounded
+    (as CUDA's default sqrtf is); the device square root torch uses on ROCm
+    can be one ulp off (sqrt(37) was), and an fp64 plan widens omega
+    from this fp32 value, so that ulp would show at fp64 precision. The
+    result is returned on the device of ``freqs``.
+    """
     if freqs.numel() == 0:
         return torch.empty((0,), dtype=torch.float32, device=freqs.device)
-    f = freqs.to(torch.float32)
-    return torch.sqrt(1.0 + (f * f).sum(dim=1))
+    f = freqs.detach().to("cpu", torch.float32)
+    return torch.sqrt(1.0 + (f * f).sum(dim=1)).to(freqs.device)

@@ -137,8 +137,8 @@ int32_t cresso_scalar_plan_step(cresso_scalar_plan* plan, void* dev_table, const
 
 /* Opaque plan for one (shape, freqs, hash_bins, hash_tables): geometry,
  * carrier bookkeeping and workspace layout.  freqs is the host copy of
- * state["freqs"] (int64 [rank][ndim], cresso_v5.py:864-868).  rank 1..32
- * (1..16 for CRESSO_F64 plans), hash_tables 1..8 with tables x bin bytes
+ * state["freqs"] (int64 [rank][ndim], cresso_v5.py:864-868).  rank 1..32,
+ * hash_tables 1..8 with tables x bin bytes
  * <= 8, hash_bins <= 65535.  NULL on error (cresso_hip_last_error says why). */
 typedef struct cresso_spectral_plan cresso_spectral_plan;
 cresso_spectral_plan* cresso_spectral_plan_create(const int64_t* shape, int32_t ndim, const int64_t* freqs,

@@ -5,6 +5,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
@@ -23,6 +24,11 @@ def test_modes_match_oracle_restatement():
         fr = freqs_tensor(*args, device="cpu")
         assert torch.equal(fr, O.make_freqs(*args))
         assert torch.equal(omega_tensor(fr), O.omega_from_freqs(fr))
+    # omega is the correctly rounded fp32 square root (numpy's is IEEE): the
+    # fp64 route widens this value, so one ulp would show at fp64 precision.
+    fr = freqs_tensor(32, 2, 6, device="cpu").numpy().astype(np.float64)
+    exact = np.sqrt(1.0 + (fr * fr).sum(axis=1)).astype(np.float32)
+    assert np.array_equal(omega_tensor(torch.from_numpy(fr)).numpy(), exact)
     for n in range(20):
         for s in (0, 17, 101, 151, 170):
             assert hash_unit(n, s) == O.hash_unit(n, s)
@@ -359,9 +365,9 @@ def test_load_state_dict_keeps_same_plan_workspaces():
 
 
 def test_spectral_plan_rank_limits_without_gpu():
-    # plan creation is host work: ranks up to 32 plan on the fp32 work dtype
-    # (ranks above 16 take the general sweeps); fp64 params stop at 16; the
-    # refusals carry the library's message instead of a fallback
+    # plan creation is host work: ranks up to 32 plan on the fp32 and fp64
+    # work dtypes (ranks above 16 take the general sweeps); a refusal carries
+    # the library's message instead of a fallback
     lib_path = ROOT / "cresso_amd" / "libcresso_hip.so"
     if not lib_path.exists():
         pytest.skip("library not built")
@@ -380,7 +386,8 @@ def test_spectral_plan_rank_limits_without_gpu():
         assert plan, lib.cresso_hip_last_error()
         assert lib.cresso_spectral_workspace_bytes(ctypes.c_void_p(plan)) > 0
         lib.cresso_spectral_plan_destroy(ctypes.c_void_p(plan))
+    plan = create(24, _native.F64)
+    assert plan, lib.cresso_hip_last_error()
+    lib.cresso_spectral_plan_destroy(ctypes.c_void_p(plan))
     assert not create(33, _native.F32)
     assert b"rank 33" in lib.cresso_hip_last_error()
-    assert not create(24, _native.F64)
-    assert b"fp64 params support rank 1..16" in lib.cresso_hip_last_error()
