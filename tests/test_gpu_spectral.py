@@ -470,6 +470,7 @@ FP64_CASES = [
     ("conv_r16", (16, 8, 3, 3), 3, dict(rank=16, max_frequency=7, hash_bins=256, hash_tables=4)),
     ("global_bins", (512, 300), 2, dict(hash_bins=1024)),
     ("r24", (200, 150), 2, dict(rank=24, max_frequency=6)),
+    ("r32_3d_t4", (12, 20, 18), 2, dict(rank=32, max_frequency=4, hash_bins=128, hash_tables=4)),
     ("options", (300, 257), 3, dict(weight_decay=0.01, maximize=True, local_sharpness=0.3)),
 ]
 
