@@ -66,6 +66,7 @@ constexpr int SP_MAXR = 32;
 constexpr int SP_MAXT = 8;
 constexpr int SP_FIN_NT = 1024;  // workspace set-up kernels
 constexpr int SP_FN_NT = 512;    // per-step finalize kernels (room for fp64 accumulators)
+constexpr int SP_FN_E = 2048;    // fin2 keeps the new hash energies in LDS up to this many bins (T B)
 // Fast-path histograms keep SP_NHIST interleaved copies ([bin][copy], copy =
 // lane & 3): lanes of one wave then collide on an address only when both the
 // bin and the copy match.  The copies are summed (integers: any order) before
@@ -973,12 +974,6 @@ __global__ __launch_bounds__(256) void part_reduce_kernel(
 }
 
 
-
-// The merged sums of a sweep into LDS (all loads in flight).
-__device__ void load_sums(const double* __restrict__ sums, int V, double* out) {
-    for (int v = threadIdx.x; v < V; v += blockDim.x) out[v] = sums[v];
-    __syncthreads();
-}
 
 // ---------------------------------------------------------------------------
 // S1: sum f^2 over contiguous chunks (float4 loads when aligned)
@@ -2494,32 +2489,45 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
     __shared__ double s_v[NV2];
     __shared__ double s_wsum[SP_MAXT][SP_FN_NT / 64];
     __shared__ float s_emean[SP_MAXT];
+    __shared__ float s_e[SP_FN_E];   // this step's hash energy when T B <= SP_FN_E
     __shared__ float s_tmpf[64];
     __shared__ unsigned int s_sync;
     const int tid = threadIdx.x;
-    if (tid == 0) s_sync = 0u;   // published by load_sums' barrier
+    if (tid == 0) s_sync = 0u;   // published by the staging barrier
     const float eps = (float)h.eps;
     __shared__ double s_stats[4 * SP_MAXR], s_bounds[2 * SP_MAXR];
     __shared__ float s_mode[SP_MAXR][9];
     __shared__ int s_zero[SP_MAXR];
-    for (int i = tid; i < 4 * g.R; i += SP_FN_NT) s_stats[i] = stats[i];
-    for (int i = tid; i < 2 * g.R; i += SP_FN_NT) s_bounds[i] = bounds[i];
-    for (int i = tid; i < 9 * g.R; i += SP_FN_NT) {
-        const int r = i / 9, j = i - 9 * r;
-        const float* src[8] = {st.omega, st.metric_cos, st.metric_p_cos, st.metric_sin, st.metric_p_sin, st.q_cos,
-                               st.q_sin, st.conf};
-        if (j < 8) s_mode[r][j] = src[j][r];
-        else s_zero[r] = meta[r].type == M_ZERO;
+    // everything the block reads is loaded first, one value per thread at
+    // clamped (in-bounds) indices, so the loads are in flight together; then
+    // stored to LDS
+    static_assert(9 * SP_MAXR <= SP_FN_NT && NV2 <= SP_FN_NT, "one staged value per thread");
+    const int R = g.R, NS = 2 + 2 * R;
+    const double v_st = stats[tid < 4 * R ? tid : 0];
+    const double v_bd = bounds[tid < 2 * R ? tid : 0];
+    const int mi = tid < 9 * R ? tid : 0, mr = mi / 9, mj = mi - 9 * mr;
+    const float* src[8] = {st.omega, st.metric_cos, st.metric_p_cos, st.metric_sin, st.metric_p_sin, st.q_cos,
+                           st.q_sin, st.conf};
+    const float v_md = src[mj < 8 ? mj : 0][mr];
+    const int v_zero = meta[mr].type == M_ZERO;
+    const double v_sum = part[tid < NS ? tid : 0];
+    if (tid < 4 * R) s_stats[tid] = v_st;
+    if (tid < 2 * R) s_bounds[tid] = v_bd;
+    if (tid < 9 * R) {
+        if (mj < 8) s_mode[mr][mj] = v_md;
+        else s_zero[mr] = v_zero;
     }
-    load_sums(part, 2 + 2 * g.R, s_v);
     // sweep 2 sums log(1 + ds) in log2 units
-    if (tid < 2 + 2 * g.R && tid != 1) s_v[tid] *= 0.6931471805599453;
+    if (tid < NS) s_v[tid] = tid != 1 ? v_sum * 0.6931471805599453 : v_sum;
     __syncthreads();
     // hash energy per table (cresso_v5.py:1012-1056), on waves 1.. while wave 0
     // runs the mode lanes (which read none of it)
     if (hash_on && tid >= 64) {
         const int TB = g.T * g.B, t1 = tid - 64, n1 = SP_FN_NT - 64;
         constexpr unsigned nw1 = SP_FN_NT / 64 - 1;
+        // the means and the log table read the new energies back from LDS
+        // (from the state in global memory when the tables are larger)
+        const bool el = TB <= SP_FN_E;
         for (int i = t1; i < TB; i += n1) {
             const double cnt = (double)counts[i];
             // low words (every copy) plus the high word, each cleared for the next step
@@ -2531,12 +2539,13 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
             float e = st.hash_energy[i];
             e = step <= 1 ? cell : e * (float)h.hash_decay + (float)(1.0 - h.hash_decay) * cell;
             st.hash_energy[i] = e;
+            if (el) s_e[i] = e;
         }
         waves_sync(&s_sync, nw1);
         // each table's mean: the waves' fp64 totals added in wave order
         for (int tt = 0; tt < g.T; ++tt) {
             double a = 0.0;
-            for (int b = t1; b < g.B; b += n1) a += (double)st.hash_energy[tt * g.B + b];
+            for (int b = t1; b < g.B; b += n1) a += (double)(el ? s_e[tt * g.B + b] : st.hash_energy[tt * g.B + b]);
             const double w = wave_total_d(a);
             if ((tid & 63) == 63) s_wsum[tt][(tid >> 6) - 1] = w;
         }
@@ -2550,7 +2559,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin2_kernel(
         const float ex = (float)(h.hash_metric_coupling / fmax(0.25, h.energy_power));
         for (int i = t1; i < TB; i += n1) {
             const int tt = i / g.B;
-            const float hm = fmaxf(st.hash_energy[i] / fmaxf(s_emean[tt], eps), eps);
+            const float hm = fmaxf((el ? s_e[i] : st.hash_energy[i]) / fmaxf(s_emean[tt], eps), eps);
             lt[i] = logf(fmaxf(clampf(powf(hm, ex), 0.08f, 12.0f), eps));
         }
     }
@@ -3344,20 +3353,40 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
     __shared__ double s_hhw[SP_FN_NT / 64];
     __shared__ float s_srms;
     __shared__ unsigned int s_sync;
-    if (tid == 0) s_sync = 0u;   // published by load_sums' barrier
-    for (int i = tid; i < V * V; i += SP_FN_NT) s_gram[i] = gram[i];
-    for (int i = tid; i < 4 * R; i += SP_FN_NT) s_stats[i] = stats[i];
-    for (int i = tid; i < 9 * R; i += SP_FN_NT) {
-        const int r = i / 9, j = i - 9 * r;
-        const float* src[8] = {st.omega, st.q_cos, st.q_sin, st.p_cos, st.p_sin, st.calcium_cos, st.calcium_sin, st.conf};
-        s_mode[r][j] = j < 8 ? src[j][r] : 0.f;
+    if (tid == 0) s_sync = 0u;   // published by the staging barrier
+    // every staged value is loaded first (clamped, in-bounds indices: the
+    // loads are in flight together), then stored to LDS
+    constexpr int NG = 4 * SP_MAXR * SP_MAXR / SP_FN_NT;   // Gram values per thread at most
+    static_assert(NG * SP_FN_NT == 4 * SP_MAXR * SP_MAXR && 9 * SP_MAXR <= SP_FN_NT && NV3 <= SP_FN_NT,
+                  "staged values per thread");
+    const int VV = V * V, NS = 15 + 2 * R;
+    double v_gr[NG];
+#pragma unroll
+    for (int u = 0; u < NG; ++u) {
+        const int i = tid + u * SP_FN_NT;
+        v_gr[u] = gram[i < VV ? i : 0];
     }
-    for (int i = tid; i < V; i += SP_FN_NT) s_u[0][i] = (double)ctrl->wpred[i];
+    const double v_st = stats[tid < 4 * R ? tid : 0];
+    const int mi = tid < 9 * R ? tid : 0, mr = mi / 9, mj = mi - 9 * mr;
+    const float* src[8] = {st.omega, st.q_cos, st.q_sin, st.p_cos, st.p_sin, st.calcium_cos, st.calcium_sin, st.conf};
+    const float v_md = src[mj < 8 ? mj : 0][mr];
+    const double v_wp = (double)ctrl->wpred[tid < V ? tid : 0];
+    const float v_sur = *st.surprise, v_act = *st.action;
+    const double v_sum = part[tid < NS ? tid : 0];
+#pragma unroll
+    for (int u = 0; u < NG; ++u) {
+        const int i = tid + u * SP_FN_NT;
+        if (i < VV) s_gram[i] = v_gr[u];
+    }
+    if (tid < 4 * R) s_stats[tid] = v_st;
+    if (tid < 9 * R) s_mode[mr][mj] = mj < 8 ? v_md : 0.f;
+    if (tid < V) s_u[0][tid] = v_wp;
     if (tid == 0) {
-        s_scal[0] = *st.surprise;
-        s_scal[1] = *st.action;
+        s_scal[0] = v_sur;
+        s_scal[1] = v_act;
     }
-    load_sums(part, 15 + 2 * R, s_m);
+    if (tid < NS) s_m[tid] = v_sum;
+    __syncthreads();
     const float eps = (float)h.eps;
     __shared__ double s_gu[2 * SP_MAXR];     // G u_pred: mean(pred Xn_v)
     if (tid < 64) {
@@ -3508,6 +3537,20 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
         // waves 1.. while wave 0 runs the mode lanes: hash refractory / impulse
         // (cresso_v5.py:1140-1184)
         const int t1 = tid - 64, n1 = SP_FN_NT - 64;
+        // the closed form's co-occurrence and bin counts (fixed per shape) are
+        // loaded before the bin work when they fit CPF values per thread
+        constexpr int CPF = 10;
+        const int BB = g.B * g.B;
+        const bool cpf = c5_closed == 1 && BB <= CPF * n1 && 2 * g.B <= n1;
+        unsigned long long cpre[CPF], npre = 0ull;
+        if (cpf) {
+#pragma unroll
+            for (int u = 0; u < CPF; ++u) {
+                const int k = t1 + u * n1;
+                cpre[u] = cooc[k < BB ? k : 0];
+            }
+            npre = counts[t1 < 2 * g.B ? t1 : 0];
+        }
         if (hash_on) {
             const int TB = g.T * g.B;
             for (int i = t1; i < TB; i += n1) {
@@ -3530,9 +3573,18 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             // and co-occurrence counts
             const int B = g.B;
             double a = 0.0;
-            for (int k = t1; k < B * B; k += n1)
-                a += (double)cooc[k] * (2.0 * (double)s_impv[k / B] * (double)s_impv[B + k % B]);
-            for (int k = t1; k < 2 * B; k += n1) a += (double)counts[k] * ((double)s_impv[k] * (double)s_impv[k]);
+            if (cpf) {
+#pragma unroll
+                for (int u = 0; u < CPF; ++u) {
+                    const int k = t1 + u * n1;
+                    if (k < BB) a += (double)cpre[u] * (2.0 * (double)s_impv[k / B] * (double)s_impv[B + k % B]);
+                }
+                if (t1 < 2 * B) a += (double)npre * ((double)s_impv[t1] * (double)s_impv[t1]);
+            } else {
+                for (int k = t1; k < B * B; k += n1)
+                    a += (double)cooc[k] * (2.0 * (double)s_impv[k / B] * (double)s_impv[B + k % B]);
+                for (int k = t1; k < 2 * B; k += n1) a += (double)counts[k] * ((double)s_impv[k] * (double)s_impv[k]);
+            }
             const double w = wave_total_d(a);
             if ((tid & 63) == 63) s_hhw[(tid >> 6) - 1] = w;
         }
