@@ -3626,17 +3626,37 @@ __global__ __launch_bounds__(256) void hh4_kernel(Geom g, const unsigned long lo
         cooc_pair(b / nc, t0, t1);
         const int r0 = 16 * (b % nc);
         if (j < B) {
-            const unsigned long long* c = cooc + (size_t)(b / nc) * B * B + (size_t)r0 * B + j;
+            // every load first (rows past B clamped to row r0, not added), then the sums in row order
+            const unsigned long long* c = cooc + (size_t)(b / nc) * B * B + j;
             const double w1 = (double)imp_tab[t1 * B + j];
             unsigned long long cv[16];
+            float iv[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) cv[r] = r0 + r < B ? c[(size_t)r * B] : 0ull;
+            for (int r = 0; r < 16; ++r) {
+                const int rr = r0 + r < B ? r0 + r : r0;
+                cv[r] = c[(size_t)rr * B];
+                iv[r] = imp_tab[t0 * B + rr];
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-                if (r0 + r < B) a += (double)cv[r] * (2.0 * (double)imp_tab[t0 * B + r0 + r] * w1);
+                if (r0 + r < B) a += (double)cv[r] * (2.0 * (double)iv[r] * w1);
         }
     } else {
-        for (int k = j; k < 4 * B; k += 256) a += (double)counts[k] * ((double)imp_tab[k] * (double)imp_tab[k]);
+        // four rows of loads in flight per thread, added in the order k = j, j + 256, ...
+        constexpr int U = 4;
+        for (int k0 = j; k0 < 4 * B; k0 += 256 * U) {
+            unsigned long long cn[U];
+            float im[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k = k0 + 256 * u < 4 * B ? k0 + 256 * u : k0;
+                cn[u] = counts[k];
+                im[u] = imp_tab[k];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (k0 + 256 * u < 4 * B) a += (double)cn[u] * ((double)im[u] * (double)im[u]);
+        }
     }
     const double w = wave_total_d(a);
     if ((j & 63) == 63) s_w[j >> 6] = w;
