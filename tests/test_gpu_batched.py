@@ -140,6 +140,36 @@ def test_batched_matches_single(case):
             _assert_same(ref[i].snapshot(), bat[i].snapshot(), f"{name} call {it} tensor {i}")
 
 
+@pytest.mark.parametrize("shape", [(1024, 768), (300, 257)], ids=["matrix_cores", "general"])
+def test_batched_matches_single_with_density_spikes(shape):
+    """Energy power 4 and grads at the rel clamp after quiet steps: the density
+    histograms take their high words (kept per tensor after its low-word
+    copies).  A batch of four, two of them spiking at different positions,
+    against single steps, bit for bit, on the spike step and the next."""
+    from cresso_amd.spectral import SpectralEngine
+
+    kw = dict(rank=8, max_frequency=5, hash_bins=64, hash_tables=2, energy_power=4.0)
+    count = 4
+    engine = SpectralEngine()
+    gen = torch.Generator().manual_seed(71)
+    p0 = [0.02 * torch.randn(shape, generator=gen) for _ in range(count)]
+    ref = [_Side(p, torch.float32, kw) for p in p0]
+    bat = [_Side(p, torch.float32, kw) for p in p0]
+    full = list(range(count))
+    for it in range(5):
+        announce(f"batched spikes {shape} x {count} call {it}")
+        gs = [(1e-3 * torch.randn(shape, generator=gen)).cuda() for _ in full]
+        if it == 3:
+            gs[1][17, 200] = 30.0
+            gs[3][shape[0] - 5, 3] = -30.0
+        for i in full:
+            _single(engine, ref[i], gs[i])
+        _batched(engine, [bat[i] for i in full], gs, count)
+        torch.cuda.synchronize()
+        for i in full:
+            _assert_same(ref[i].snapshot(), bat[i].snapshot(), f"spikes {shape} call {it} tensor {i}")
+
+
 def test_batched_rejects_mixed_batches():
     from cresso_amd import _native
     from cresso_amd.spectral import SpectralEngine
