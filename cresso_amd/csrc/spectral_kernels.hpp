@@ -3272,42 +3272,58 @@ __global__ __launch_bounds__(SP_NT, (occ3m<RM, KC>())) void sweep3m_kernel(
 // F3: surprise, hash impulse, confidence, contact, and every drive-shaping
 // coefficient that does not need the hash prediction's rms
 // ---------------------------------------------------------------------------
-// Contact oscillator of one bank (cresso_v5.py:914-943), lane r = mode r; the
-// energy and power sums over modes are summed in mode order.
-__device__ void contact_bank_lanes(float& q, float& p, float port, float omega, float& calcium, float& action, float S,
-                                   int R, const cresso_hyper& h) {
+// Contact oscillator (cresso_v5.py:914-943) on bank 0 (cos) then bank 1 (sin)
+// with the shared action, lane r = mode r; the energy and power sums over
+// modes are summed in mode order.  A bank's sums use its own pre-update p and
+// q, so both banks' sums are formed first (the six wave reductions in flight
+// together); the action, the friction it sets and each bank's update then run
+// in bank order.
+__device__ void contact_banks_lanes(float (&q)[2], float (&p)[2], const float (&port)[2], float omega,
+                                    float (&calcium)[2], float& action, float S, int R, const cresso_hyper& h) {
     const int r = threadIdx.x & 63;
     const bool on = r < R;
     const float dt = (float)h.dt;
     const float rd = (float)h.refractory_decay;
     const float plast = 1.0f + (float)h.surprise_gain * S / (1.0f + S);
     const float brake = 1.0f / (1.0f + (float)h.surprise_brake * S);
-    float gp = 0.f;
-    double e1 = 0.0, e2 = 0.0, pw = 0.0;
-    if (on) {
-        calcium = calcium * rd + (float)(1.0 - h.refractory_decay) * fabsf(port);
-        const float gate = 1.0f / (1.0f + (float)h.refractory_gain * calcium);
-        gp = port * gate * plast * brake;
-        e1 = (double)(p * p);
-        const float oq = omega * q;
-        e2 = (double)(oq * oq);
-        pw = (double)(gp * p);
+    float gp[2] = {0.f, 0.f};
+    double e1[2] = {0.0, 0.0}, e2[2] = {0.0, 0.0}, pw[2] = {0.0, 0.0};
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        if (on) {
+            calcium[b] = calcium[b] * rd + (float)(1.0 - h.refractory_decay) * fabsf(port[b]);
+            const float gate = 1.0f / (1.0f + (float)h.refractory_gain * calcium[b]);
+            gp[b] = port[b] * gate * plast * brake;
+            e1[b] = (double)(p[b] * p[b]);
+            const float oq = omega * q[b];
+            e2[b] = (double)(oq * oq);
+            pw[b] = (double)(gp[b] * p[b]);
+        }
     }
-    const double E1 = lanes_sum(e1, R), E2 = lanes_sum(e2, R), PW = lanes_sum(pw, R);
-    if (R > 0) {
-        const double iR = 1.0 / (double)R;
-        const float energy = 0.5f * ((float)(E1 * iR) + (float)(E2 * iR));
-        const float power = (float)(PW * iR);
-        action = action * 0.985f + dt * (power - energy);
+    double E1[2], E2[2], PW[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        E1[b] = lanes_sum(e1[b], R);
+        E2[b] = lanes_sum(e2[b], R);
+        PW[b] = lanes_sum(pw[b], R);
     }
-    const float fric = (float)h.impulse_friction + (float)h.contact_gain * tanhf(fabsf(action));
-    const float damp = fmaxf(1.0f - dt * fric, 0.0f);
-    if (on) {
-        float pr = p * damp;
-        const float qq = q;
-        pr = pr + dt * (gp - (float)h.restoring * (omega * omega) * qq - (float)h.cubic * (qq * qq * qq));
-        p = pr;
-        q = clampf(qq + dt * pr, -8.0f, 8.0f);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        if (R > 0) {
+            const double iR = 1.0 / (double)R;
+            const float energy = 0.5f * ((float)(E1[b] * iR) + (float)(E2[b] * iR));
+            const float power = (float)(PW[b] * iR);
+            action = action * 0.985f + dt * (power - energy);
+        }
+        const float fric = (float)h.impulse_friction + (float)h.contact_gain * tanhf(fabsf(action));
+        const float damp = fmaxf(1.0f - dt * fric, 0.0f);
+        if (on) {
+            float pr = p[b] * damp;
+            const float qq = q[b];
+            pr = pr + dt * (gp[b] - (float)h.restoring * (omega * omega) * qq - (float)h.cubic * (qq * qq * qq));
+            p[b] = pr;
+            q[b] = clampf(qq + dt * pr, -8.0f, 8.0f);
+        }
     }
 }
 
@@ -3409,6 +3425,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
         // mean(pred Xn_v) = (G u_pred)_v, lane v = carrier v
         if (r < V) {
             double gu = 0.0;
+#pragma unroll 8
             for (int w = 0; w < V; ++w) gu += s_gram[r * V + w] * s_u[0][w];
             s_gu[r] = gu;
         }
@@ -3437,8 +3454,12 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
         }
         // contact on the cos bank then the sin bank with the shared action
         float action = s_scal[1];
-        contact_bank_lanes(qc, pcv, pc, om, cac, action, sur, R, h);
-        contact_bank_lanes(qs, psv, ps, om, cas, action, sur, R, h);
+        {
+            float qb[2] = {qc, qs}, pb[2] = {pcv, psv}, cb[2] = {cac, cas};
+            const float portb[2] = {pc, ps};
+            contact_banks_lanes(qb, pb, portb, om, cb, action, sur, R, h);
+            qc = qb[0]; qs = qb[1]; pcv = pb[0]; psv = pb[1]; cac = cb[0]; cas = cb[1];
+        }
         set_recon_lanes(g, s_stats, ctrl->rc[2], &ctrl->rconst[2], qc, qs, gt, s_tmpf, s_wp);
         if (echo_on) set_recon_lanes(g, s_stats, ctrl->rc[3], &ctrl->rconst[3], ecs, ess, 1.0f, s_tmpf, s_we);
         if (on) {
@@ -3461,6 +3482,7 @@ __global__ __launch_bounds__(SP_FN_NT) void fin3_kernel(
             const int v = r;
             const double gu = s_gu[v];
             double gup = 0.0, gue = 0.0;
+#pragma unroll 8
             for (int w = 0; w < V; ++w) {
                 const double gvw = s_gram[v * V + w];
                 gup += gvw * s_u[1][w];
